@@ -1,0 +1,338 @@
+#!/usr/bin/env python3
+"""Benchmark of the decode-step operator path on one MI355X.
+
+Default workload (the headline metric): paged decode attention at the Qwen3-8B
+shape, batch 64 (C3): q [64, 32, 128] bf16, 8 kv heads, 256-token pages from a
+4096-block pool, context lengths ~ U[512, 8192].  One step = one
+FlashAttnDecode-equivalent call (split-context partials kernel + merge kernel)
+over the batch, with all inputs resident in HBM.
+
+Prints ONE JSON line: value = whole-call throughput in algorithmic GB/s
+(K+V bytes attended + q + out + block-table entries + ctx, per call, divided by
+the mean step time), the per-call time, the roofline of the dominant kernel
+(the partials kernel, timed live with HIP events on its stream) against the
+8 TB/s HBM peak, and the CPU oracle timed on a bounded sample.
+
+  python bench.py [--steps K] [--warmup W] [--num-splits S] [--no-cpu]
+  python bench.py --table          # per-op table for C1-C5 to stderr (+ --table-json PATH)
+  python bench.py --calib-copy     # plain 1 GiB device copy, for rocprof counter scaling
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "paged decode attn µs/call + achieved HBM GB/s (% of 8 TB/s), Qwen3-8B bs64"
+
+
+def _parse():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--num-splits", type=int, default=0, help="0 = automatic partitioning")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline time budget")
+    ap.add_argument("--table", action="store_true", help="per-op table for C1-C5")
+    ap.add_argument("--table-json", type=str, default=None)
+    ap.add_argument("--calib-copy", action="store_true")
+    ap.add_argument("--seed", type=int, default=200)
+    return ap.parse_args()
+
+
+def _events(n):
+    import torch
+
+    return [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+
+
+def _flush_buffer(device):
+    import torch
+
+    # Twice the 256 MB MALL (Infinity Cache): evicts L2 and MALL between timed calls.
+    return torch.empty(512 * 1024 * 1024, dtype=torch.uint8, device=device)
+
+
+def time_call(fn, iters=50, warmup=10, flush=None):
+    """Median and mean of fn's GPU time (events bracket only fn; an optional cache
+    flush is enqueued before each start event)."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    starts, ends = _events(iters), _events(iters)
+    for i in range(iters):
+        if flush is not None:
+            flush.fill_(i & 0xFF)
+        starts[i].record()
+        fn()
+        ends[i].record()
+    torch.cuda.synchronize()
+    ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    return statistics.median(ms), statistics.fmean(ms)
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline: the oracle (numpy restatement of the reference's torch path)
+# ---------------------------------------------------------------------------
+def cpu_baseline_decode(case, budget_s: float):
+    import numpy as np
+    import torch
+
+    import oracle
+
+    try:
+        from threadpoolctl import threadpool_limits
+    except ImportError:  # pragma: no cover
+        threadpool_limits = None
+    cores = min(len(os.sched_getaffinity(0)), 16)
+    ctx = case.ctx_lens.cpu().numpy().astype(np.int64)
+    bt = case.block_tables.cpu().numpy()
+    bs = case.k_cache.shape[1]
+    order = np.argsort(ctx)
+    sample = [int(order[len(order) // 2]), int(order[-1]), int(order[0]), int(order[len(order) // 4])]
+    q = case.q.float().cpu().numpy()
+    data = []
+    for i in sample:
+        n = int(ctx[i])
+        pages = (n + bs - 1) // bs
+        ids = torch.from_numpy(bt[i, :pages].astype(np.int64)).to(case.k_cache.device)
+        data.append((i, n, case.k_cache[ids].float().cpu().numpy(),
+                     case.v_cache[ids].float().cpu().numpy()))
+    hk, d = case.k_cache.shape[2], case.k_cache.shape[3]
+    per_tok = 2 * hk * d * case.k_cache.element_size()
+
+    def run_once():
+        for i, n, kp, vp in data:
+            oracle.paged_decode(q[i:i + 1], kp, vp, np.arange(kp.shape[0])[None], np.array([n]),
+                                case.scale)
+
+    ctx_mgr = threadpool_limits(limits=cores) if threadpool_limits else None
+    try:
+        run_once()  # warmup
+        t0 = time.perf_counter()
+        reps = 0
+        while True:
+            run_once()
+            reps += 1
+            if time.perf_counter() - t0 >= budget_s:
+                break
+        el = (time.perf_counter() - t0) / reps
+    finally:
+        if ctx_mgr is not None:
+            ctx_mgr.__exit__(None, None, None)
+    toks = sum(n for _, n, _, _ in data)
+    gbs = toks * per_tok / el / 1e9
+    total_toks = int(ctx.sum())
+    return {
+        "value": round(gbs, 3),
+        "unit": "GB/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": (f"oracle.paged_decode (numpy float64, gather + softmax attention as "
+                   f"attention_impl.py:592-664) on {len(sample)} of {len(ctx)} C3 sequences "
+                   f"({toks} of {total_toks} cached tokens), {reps} reps in {budget_s:.0f}s; "
+                   f"whole-batch estimate {el * total_toks / toks * 1e6:.0f} us/call"),
+        "us_per_call_estimate": round(el * total_toks / toks * 1e6, 1),
+    }
+
+
+# ---------------------------------------------------------------------------
+# Headline: paged decode C3
+# ---------------------------------------------------------------------------
+def bench_decode(args):
+    import torch
+
+    from fastkernels_amd import ops, workloads
+
+    dev = torch.device("cuda:0")
+    case = workloads.c3_decode(dev, seed=args.seed)
+    b, hq, d = case.q.shape
+    hk = case.k_cache.shape[2]
+    part, nparts = ops.paged_decode_plan(b, hk, case.max_seq_len, args.num_splits)
+    ws = torch.empty(max(1, ops.paged_decode_workspace_bytes(b, hq, hk, d, nparts)),
+                     dtype=torch.uint8, device=dev)
+    out = torch.empty_like(case.q)
+    partials, reduce = ops.paged_decode_phases(out, case.q, case.k_cache, case.v_cache,
+                                               case.block_tables, case.ctx_lens, case.scale,
+                                               part, nparts, ws)
+    total_bytes = case.algorithmic_bytes()
+    out_bytes = out.numel() * out.element_size()
+    partial_bytes = total_bytes - out_bytes  # the partials kernel's algorithmic bytes
+    for _ in range(args.warmup):
+        partials()
+        reduce()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    ev = _events(2 * args.steps)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        ev[2 * i].record(stream)
+        partials()
+        ev[2 * i + 1].record(stream)
+        reduce()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    kern_ms = [ev[2 * i].elapsed_time(ev[2 * i + 1]) for i in range(args.steps)]
+    ms_per_step = wall * 1e3 / args.steps
+    kavg = statistics.fmean(kern_ms)
+    achieved = partial_bytes / (kavg * 1e-3) / 1e9
+    result = {
+        "metric": METRIC,
+        "value": round(total_bytes / (ms_per_step * 1e-3) / 1e9, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "us_per_call": round(ms_per_step * 1e3, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) q/KV, ctx ~ U[512,8192], random-permutation block tables)",
+        "config": {
+            "workload": "C3 paged decode attention, Qwen3-8B shape, batch 64",
+            "batch": b, "num_heads": hq, "num_kv_heads": hk, "head_dim": d,
+            "block_size": case.k_cache.shape[1], "pool_blocks": case.k_cache.shape[0],
+            "sum_ctx": int(case.ctx_lens.to(torch.int64).sum().item()),
+            "part_tokens": part, "max_parts": nparts, "seed": args.seed,
+            "algorithmic_bytes_per_call": total_bytes,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "paged_decode_partials_kernel",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "avg_kernel_us": round(kavg * 1e3, 2),
+            "algorithmic_bytes_per_launch": partial_bytes,
+        },
+    }
+    return result, case
+
+
+def bench_table(args):
+    """Per-op µs/call and GB/s for C1-C5 (L2 + MALL flushed before each timed call)."""
+    import torch
+
+    from fastkernels_amd import ops, workloads
+
+    dev = torch.device("cuda:0")
+    flush = _flush_buffer(dev)
+    rows = []
+
+    def add(cfg, op, fn, nbytes, iters=50):
+        med, mean = time_call(fn, iters=iters, warmup=5, flush=flush)
+        rows.append({"config": cfg, "op": op, "us_median": round(med * 1e3, 2),
+                     "us_mean": round(mean * 1e3, 2), "bytes": nbytes,
+                     "GBs": round(nbytes / (med * 1e-3) / 1e9, 1),
+                     "frac_of_8TBs": round(nbytes / (med * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
+        print(json.dumps(rows[-1]), file=sys.stderr, flush=True)
+
+    c1 = workloads.c1_norm(dev)
+    x, r = c1.x.clone(), c1.residual.clone()
+    add("C1", "fused_add_rmsnorm bf16 [256,1024]",
+        lambda: ops.fused_add_rms_norm(x, r, c1.weight, c1.eps), (4 * 256 * 1024 + 1024) * 2)
+    c2 = workloads.c2_store(dev)
+    nvalid = int((c2.slot_mapping >= 0).sum().item())
+    add("C2", "store_kvcache [4096,8,128]",
+        lambda: ops.store_kvcache(c2.key, c2.value, c2.k_cache, c2.v_cache, c2.slot_mapping),
+        8 * 4096 + nvalid * 4 * 8 * 128 * 2)
+    del c2
+    c4 = workloads.c4_chain(dev)
+    h, rr = c4.hidden.clone(), c4.residual.clone()
+    add("C4", "fused_add_rmsnorm bf16 [256,4096]",
+        lambda: ops.fused_add_rms_norm(h, rr, c4.norm_weight, 1e-6), (4 * 256 * 4096 + 4096) * 2)
+    from fastkernels_amd.candidate.L1.rotary_emb import RotaryEmbedding
+
+    rope = RotaryEmbedding(128, c4.max_position, c4.rope_theta).to(dev)
+    qkv = c4.qkv.clone()
+    q, k = qkv[:, :4096], qkv[:, 4096:5120]
+    add("C4", "rotary q[256,32x128] k[256,8x128]",
+        lambda: ops.rotary_embedding(c4.positions, q, k, 128, rope.cos_sin_cache, True),
+        2 * 256 * 5120 * 2 + 256 * 8 + 256 * 128 * 4)
+    v = qkv[:, 5120:]
+    dec = c4.decode
+    add("C4", "store_kvcache [256,8,128]",
+        lambda: ops.store_kvcache(k.view(256, 8, 128), v.view(256, 8, 128), dec.k_cache,
+                                  dec.v_cache, c4.slot_mapping), 8 * 256 + 256 * 4 * 1024 * 2)
+    c3 = workloads.c3_decode(dev)
+    c5 = workloads.c5_fp8_decode(dev)
+    for name, case, splits in (("C4", dec, 0), ("C3", c3, 0), ("C5", c5, 16), ("C5", c5, 32),
+                               ("C5", c5, 64)):
+        b, hq, d = case.q.shape
+        hk = case.k_cache.shape[2]
+        part, nparts = ops.paged_decode_plan(b, hk, case.max_seq_len, splits)
+        ws = torch.empty(max(1, ops.paged_decode_workspace_bytes(b, hq, hk, d, nparts)),
+                         dtype=torch.uint8, device=dev)
+        out = torch.empty_like(case.q)
+        add(name, f"paged_decode {case.k_cache.dtype} B={b} Hq={hq} part={part} x{nparts}",
+            lambda: ops.paged_decode(out, case.q, case.k_cache, case.v_cache, case.block_tables,
+                                     case.ctx_lens, case.scale, part, nparts, ws, case.k_scale,
+                                     case.v_scale), case.algorithmic_bytes(), iters=30)
+    gu = c4.gate_up
+    act = torch.empty(256, 12288, dtype=torch.bfloat16, device=dev)
+    add("C4", "silu_and_mul [256,2x12288]", lambda: ops.silu_and_mul(act, gu),
+        256 * 3 * 12288 * 2)
+    if args.table_json:
+        Path(args.table_json).parent.mkdir(parents=True, exist_ok=True)
+        Path(args.table_json).write_text(json.dumps(rows, indent=1))
+    return rows
+
+
+def calib_copy():
+    import torch
+
+    dev = torch.device("cuda:0")
+    src = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calib_copy_bytes": src.numel(), "launches": 5}), flush=True)
+
+
+def main():
+    args = _parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build measures one GPU only (the decode path has no cross-GPU "
+              "exchange in this tier); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    from fastkernels_amd import _native
+
+    _native.lib()
+    if args.calib_copy:
+        calib_copy()
+        return
+    if args.table:
+        bench_table(args)
+        return
+    result, case = bench_decode(args)
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline_decode(case, args.cpu_seconds)
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,137 @@
+"""Candidate ``FlashAttnDecode`` for fastkernels/tasks/baseline/L1/flash_attn_decode.py:22-181.
+
+Same constructor ``(num_heads, num_kv_heads, head_dim, page_size=None)`` and
+``forward(q, k_cache, v_cache, cache_seqlens=None, **kwargs)`` with the kwargs
+the reference forwards to ``flash_attn_varlen_func`` (flash_attn_decode.py:
+113-181): ``block_table``, ``max_seq_len``, ``softmax_scale``, ``causal``
+(decode: every cached key is visible), ``num_splits``, ``out``.  Returns
+``[B, num_heads, head_dim]`` in q's dtype.
+
+The gfx950 kernel is split-context flash-decoding: work-groups of
+``part_tokens`` tokens per (sequence, kv head) write partials into a
+per-module workspace that a second kernel merges with the log-sum-exp rule.
+The workspace is allocated outside graph capture (like the reference's
+persistent FA3 scheduler buffer, flash_attn_decode.py:87-111) and only grows;
+inside a capture it must already be large enough.
+
+fp8 KV: caches of dtype ``torch.float8_e4m3fn`` are dequantised per kv head
+with ``k_scale`` / ``v_scale`` (float32 [num_kv_heads]; per-tensor scales may be
+given as a single value and are broadcast), i.e. K = float(K8) * k_scale as in
+``_cast_kv_tile`` (triton_unified_attention.py:51-67).  FA-style
+``k_descale`` / ``v_descale`` are accepted as aliases.
+
+No host synchronisation: when ``max_seq_len`` is absent the bound is taken from
+the block table width (``block_table.shape[1] * page_size``) instead of
+``cache_seqlens.max().item()`` (flash_attn_decode.py:122-125).
+"""
+from __future__ import annotations
+
+import sys
+from pathlib import Path
+
+import torch
+import torch.nn as nn
+
+try:
+    import fastkernels_amd  # noqa: F401
+except ImportError:  # loaded by file path from the reference harness
+    sys.path.insert(0, str(Path(__file__).resolve().parents[3]))
+from fastkernels_amd import ops
+
+
+class FlashAttnDecode(nn.Module):
+    def __init__(self, num_heads: int, num_kv_heads: int, head_dim: int,
+                 page_size: int | None = None):
+        super().__init__()
+        self.num_heads = num_heads
+        self.num_kv_heads = num_kv_heads
+        self.head_dim = head_dim
+        self.page_size = page_size
+        self._workspace: torch.Tensor | None = None
+
+    def _get_workspace(self, nbytes: int, device: torch.device) -> torch.Tensor | None:
+        if nbytes <= 0:
+            return None
+        ws = self._workspace
+        if ws is None or ws.device != device or ws.numel() < nbytes:
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError(
+                    "FlashAttnDecode: split-context workspace must be allocated before graph "
+                    f"capture ({nbytes} bytes needed); call preallocate() or run eagerly once")
+            ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+            self._workspace = ws
+        return ws
+
+    def preallocate(self, max_batch_size: int, max_seq_len: int, device: torch.device,
+                    num_splits: int = 0) -> None:
+        """Allocate the workspace for batches up to max_batch_size (outside capture)."""
+        _, max_parts = ops.paged_decode_plan(max_batch_size, self.num_kv_heads, max_seq_len,
+                                             num_splits)
+        nbytes = ops.paged_decode_workspace_bytes(max_batch_size, self.num_heads,
+                                                  self.num_kv_heads, self.head_dim, max_parts)
+        self._get_workspace(nbytes, torch.device(device))
+
+    @staticmethod
+    def _scale_vec(s, hk: int, device) -> torch.Tensor | None:
+        if s is None:
+            return None
+        if not isinstance(s, torch.Tensor):
+            s = torch.tensor([float(s)], dtype=torch.float32)
+        s = s.to(device=device, dtype=torch.float32).reshape(-1)
+        if s.numel() == 1:
+            s = s.expand(hk)
+        if s.numel() != hk:
+            raise ValueError(f"FlashAttnDecode: fp8 scale must have 1 or {hk} entries")
+        return s.contiguous()
+
+    def forward(self, q, k_cache, v_cache, cache_seqlens=None, **kwargs):
+        max_seq_len = kwargs.pop("max_seq_len", None)
+        block_table = kwargs.pop("block_table", None)
+        softmax_scale = kwargs.pop("softmax_scale", None)
+        kwargs.pop("causal", None)
+        num_splits = int(kwargs.pop("num_splits", 0) or 0)
+        out = kwargs.pop("out", None)
+        k_scale = kwargs.pop("k_scale", kwargs.pop("k_descale", None))
+        v_scale = kwargs.pop("v_scale", kwargs.pop("v_descale", None))
+        window = kwargs.pop("window_size", (-1, -1))
+        s_aux = kwargs.pop("s_aux", None)
+        kwargs.pop("scheduler_metadata", None)
+        if window is not None and tuple(window) != (-1, -1):
+            raise NotImplementedError("FlashAttnDecode (gfx950): sliding window is not supported")
+        if s_aux is not None:
+            raise NotImplementedError("FlashAttnDecode (gfx950): attention sinks are not supported")
+        if kwargs:
+            raise TypeError(f"FlashAttnDecode: unexpected arguments {sorted(kwargs)}")
+        if block_table is None or cache_seqlens is None:
+            raise ValueError("FlashAttnDecode: block_table and cache_seqlens are required")
+
+        b = q.shape[0]
+        q3 = q.view(b, self.num_heads, self.head_dim)
+        block_size = k_cache.shape[1]
+        if block_table.dtype != torch.int32:
+            block_table = block_table.to(torch.int32)
+        if cache_seqlens.dtype != torch.int32:
+            cache_seqlens = cache_seqlens.to(torch.int32)
+        if max_seq_len is None:
+            max_seq_len = block_table.shape[1] * block_size
+        if softmax_scale is None:
+            softmax_scale = ops.default_softmax_scale(self.head_dim)
+        hk = k_cache.shape[2]
+        k_scale = self._scale_vec(k_scale, hk, q.device)
+        v_scale = self._scale_vec(v_scale, hk, q.device)
+
+        part_tokens, max_parts = ops.paged_decode_plan(b, hk, int(max_seq_len), num_splits)
+        ws = self._get_workspace(
+            ops.paged_decode_workspace_bytes(b, self.num_heads, hk, self.head_dim, max_parts)
+            if max_parts > 1 else 0, q.device)
+        if out is None:
+            out = torch.empty((b, self.num_heads, self.head_dim), dtype=q.dtype, device=q.device)
+        out3 = out.view(b, self.num_heads, self.head_dim)
+        if torch.compiler.is_compiling():
+            torch.ops.fastkernels_amd.paged_decode(out3, q3, k_cache, v_cache, block_table,
+                                                   cache_seqlens, float(softmax_scale),
+                                                   part_tokens, max_parts, ws, k_scale, v_scale)
+        else:
+            ops.paged_decode(out3, q3, k_cache, v_cache, block_table, cache_seqlens,
+                             float(softmax_scale), part_tokens, max_parts, ws, k_scale, v_scale)
+        return out

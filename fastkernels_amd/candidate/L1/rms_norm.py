@@ -1,0 +1,58 @@
+"""Candidate ``RMSNorm`` for fastkernels/tasks/baseline/L1/rms_norm.py:76-164.
+
+Same constructor, parameter names and ``forward(x, residual=None)`` contract:
+without a residual it returns a new normalised tensor; with one it updates
+``x`` and ``residual`` in place (as the reference's CUDA path does,
+rms_norm.py:141-146) and returns ``(x, residual)``.  Both paths run the
+gfx950 kernels of libfk_amd (one wave64 per row, row held in registers); under
+torch.compile they are the opaque ``fastkernels_amd::rmsnorm`` /
+``fastkernels_amd::fused_add_rmsnorm`` custom ops.
+"""
+from __future__ import annotations
+
+import sys
+from pathlib import Path
+
+import torch
+import torch.nn as nn
+
+try:
+    import fastkernels_amd  # noqa: F401
+except ImportError:  # loaded by file path from the reference harness
+    sys.path.insert(0, str(Path(__file__).resolve().parents[3]))
+from fastkernels_amd import ops
+
+
+class RMSNorm(nn.Module):
+    def __init__(self, hidden_size: int, eps: float = 1e-6, elementwise_affine: bool = True):
+        super().__init__()
+        self.hidden_size = hidden_size
+        self.eps = eps
+        self.elementwise_affine = elementwise_affine
+        if elementwise_affine:
+            self.weight = nn.Parameter(torch.ones(hidden_size))
+        else:
+            self.register_buffer("_unit_weight", torch.ones(hidden_size), persistent=False)
+
+    def forward(self, x: torch.Tensor, residual: torch.Tensor | None = None):
+        weight = self.weight if self.elementwise_affine else self._unit_weight
+        if weight.dtype != x.dtype or weight.device != x.device:
+            weight = weight.to(device=x.device, dtype=x.dtype)
+        weight = weight.detach()
+        if x.stride(-1) != 1:
+            x = x.contiguous()
+        compiling = torch.compiler.is_compiling()
+        if residual is None:
+            out = torch.empty_like(x, memory_format=torch.contiguous_format)
+            if compiling:
+                torch.ops.fastkernels_amd.rmsnorm(out, x, weight, self.eps)
+            else:
+                ops.rms_norm(out, x, weight, self.eps)
+            return out
+        if residual.stride(-1) != 1:
+            residual = residual.contiguous()
+        if compiling:
+            torch.ops.fastkernels_amd.fused_add_rmsnorm(x, residual, weight, self.eps)
+        else:
+            ops.fused_add_rms_norm(x, residual, weight, self.eps)
+        return x, residual

@@ -1,0 +1,77 @@
+"""Candidate ``RotaryEmbedding`` for fastkernels/tasks/baseline/L1/rotary_emb.py:71-191.
+
+Same constructor (including the Llama-3.1 frequency scaling of
+rotary_emb.py:44-68,95-102), the same ``cos_sin_cache`` buffer
+([max_position, rot_dim] float32, cos then sin, rotary_emb.py:104-107), and
+``forward(positions, query, key)`` rotating query/key in place and returning
+them (rotary_emb.py:179-191).  The kernel reads the float32 cache directly and
+rounds cos/sin to the query dtype itself, so no per-call cache cast is made
+(the reference casts the whole cache on every call when it is float32,
+rotary_emb.py:171-173).
+"""
+from __future__ import annotations
+
+import math
+import sys
+from pathlib import Path
+
+import torch
+import torch.nn as nn
+
+try:
+    import fastkernels_amd  # noqa: F401
+except ImportError:  # loaded by file path from the reference harness
+    sys.path.insert(0, str(Path(__file__).resolve().parents[3]))
+from fastkernels_amd import ops
+
+
+def _llama31_inv_freq(inv_freq: torch.Tensor, factor: float, low_freq_factor: float,
+                      high_freq_factor: float, original_max_pos: int) -> torch.Tensor:
+    """Llama-3.1 piecewise frequency scaling (rotary_emb.py:44-68)."""
+    wavelen = 2 * math.pi / inv_freq
+    low_wavelen = original_max_pos / low_freq_factor
+    high_wavelen = original_max_pos / high_freq_factor
+    if low_freq_factor != high_freq_factor:
+        smooth = (original_max_pos / wavelen - low_freq_factor) / (high_freq_factor - low_freq_factor)
+    else:
+        smooth = torch.zeros_like(inv_freq)
+    blended = (1 - smooth) * inv_freq / factor + smooth * inv_freq
+    scaled = torch.where(wavelen > low_wavelen, inv_freq / factor, blended)
+    return torch.where(wavelen < high_wavelen, inv_freq, scaled)
+
+
+class RotaryEmbedding(nn.Module):
+    def __init__(self, head_dim: int, max_position_embeddings: int, rope_theta: float,
+                 rope_scaling_factor: float = 1.0, rope_low_freq_factor: float = 1.0,
+                 rope_high_freq_factor: float = 1.0,
+                 rope_original_max_position_embeddings: int | None = None,
+                 is_neox_style: bool = True):
+        super().__init__()
+        self.head_dim = head_dim
+        self.is_neox_style = is_neox_style
+        exponents = torch.arange(0, head_dim, 2, dtype=torch.float) / head_dim
+        inv_freq = 1.0 / (rope_theta ** exponents)
+        if rope_scaling_factor != 1.0 and rope_original_max_position_embeddings is not None:
+            inv_freq = _llama31_inv_freq(inv_freq, rope_scaling_factor, rope_low_freq_factor,
+                                         rope_high_freq_factor,
+                                         rope_original_max_position_embeddings)
+        angles = torch.outer(torch.arange(max_position_embeddings, dtype=torch.float), inv_freq)
+        cache = torch.cat((angles.cos(), angles.sin()), dim=-1).float()
+        self.register_buffer("cos_sin_cache", cache, persistent=False)
+
+    def forward(self, positions: torch.Tensor, query: torch.Tensor, key: torch.Tensor | None):
+        cache = self.cos_sin_cache
+        if cache.device != query.device:
+            cache = cache.to(query.device)
+        if cache.dtype not in (torch.float32, query.dtype):
+            cache = cache.to(query.dtype)
+        if positions.dtype != torch.int64:
+            positions = positions.to(torch.int64)
+        if not positions.is_contiguous():
+            positions = positions.contiguous()
+        if torch.compiler.is_compiling():
+            torch.ops.fastkernels_amd.rotary_embedding(positions, query, key, self.head_dim, cache,
+                                                       self.is_neox_style)
+        else:
+            ops.rotary_embedding(positions, query, key, self.head_dim, cache, self.is_neox_style)
+        return query, key

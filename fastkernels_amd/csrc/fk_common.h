@@ -1,0 +1,103 @@
+// Device and host helpers shared by the gfx950 decode-step kernels.
+//
+// Numeric conversions are written out explicitly (round-to-nearest-even for
+// fp32 -> bf16/f16, exact widening for bf16/f16/fp8 -> fp32) so that every
+// kernel rounds exactly where the reference's PyTorch formulas round.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/fastkernels_amd.h"
+
+namespace fk {
+
+// ---------------------------------------------------------------------------
+// Error reporting (thread-local message behind fk_last_error()).
+// ---------------------------------------------------------------------------
+int set_error(int code, const char* fmt, ...);
+int check_launch(const char* what);
+
+#define FK_REQUIRE(cond, ...)                                  \
+  do {                                                         \
+    if (!(cond)) return ::fk::set_error(FK_ERR_INVALID_ARG, __VA_ARGS__); \
+  } while (0)
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// ---------------------------------------------------------------------------
+// Scalar conversions.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16; NaN maps to the canonical quiet NaN.
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+
+__device__ __forceinline__ uint16_t f32_to_f16(float f) {
+  // The hardware conversion rounds to nearest even.
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+// Element-type traits: storage type + widening / narrowing.
+struct BF16 {
+  using storage = uint16_t;
+  static constexpr int kDtype = FK_DTYPE_BF16;
+  __device__ __forceinline__ static float to_f32(storage v) { return bf16_to_f32(v); }
+  __device__ __forceinline__ static storage from_f32(float f) { return f32_to_bf16(f); }
+  // Round an fp32 value to this type and back (models a tensor op's rounding).
+  __device__ __forceinline__ static float round(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+};
+struct F16 {
+  using storage = uint16_t;
+  static constexpr int kDtype = FK_DTYPE_F16;
+  __device__ __forceinline__ static float to_f32(storage v) { return f16_to_f32(v); }
+  __device__ __forceinline__ static storage from_f32(float f) { return f32_to_f16(f); }
+  __device__ __forceinline__ static float round(float f) { return f16_to_f32(f32_to_f16(f)); }
+};
+struct F32 {
+  using storage = float;
+  static constexpr int kDtype = FK_DTYPE_F32;
+  __device__ __forceinline__ static float to_f32(storage v) { return v; }
+  __device__ __forceinline__ static storage from_f32(float f) { return f; }
+  __device__ __forceinline__ static float round(float f) { return f; }
+};
+
+// 16-byte vector of storage elements.
+template <typename T>
+struct Vec16 {
+  static constexpr int N = 16 / sizeof(typename T::storage);
+  union {
+    uint4 raw;
+    typename T::storage e[N];
+  };
+};
+
+// ---------------------------------------------------------------------------
+// Wave64 reductions (butterfly over all 64 lanes; every lane gets the result).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+}  // namespace fk

@@ -1,0 +1,603 @@
+// Paged decode attention for MI355X (gfx950): split-context ("flash-decoding")
+// with GQA-packed MFMA tiles.
+//
+// Semantics (one query token per sequence, all cached keys visible):
+//   out[b, hq] = sum_t softmax_t(scale * q[b,hq] . K[b,t]) V[b,t],  t < ctx_lens[b]
+// K/V rows of sequence b are gathered through block_tables[b, t / block_size]
+// from NHD pages [num_blocks, block_size, Hk, D]; kv head = hq / (Hq/Hk).  This is
+// FlashAttnDecode.forward (fastkernels/tasks/baseline/L1/flash_attn_decode.py:
+// 113-181) and the reference's torch fallback Attention._decode_torch
+// (fastkernels/tasks/baseline/L2/attention_impl.py:592-664).  Partitions are
+// merged with the log-sum-exp rule of reduce_segments
+// (triton_unified_attention.py:741-776): M = max m_p, L = sum l_p e^(m_p - M),
+// O = sum o_p e^(m_p - M) / L, and O = 0 when L = 0.  fp8 KV pages are
+// dequantised per (kv head) as float(x) * scale, the per-tensor rule of
+// _cast_kv_tile (triton_unified_attention.py:51-67): k_scale is folded into the
+// score scale and v_scale into the output, which is algebraically the same.
+//
+// Work decomposition.  Work-group = (partition p, kv head h, sequence b) with
+// NW wave64s.  A partition is part_tokens consecutive tokens; the waves take
+// 16-token tiles round-robin, so the NW waves of a group stream NW adjacent
+// tiles at once.  Each wave keeps an online-softmax state for the G query heads
+// of its kv head; the waves are merged through LDS and the group writes one
+// partial (or the final row when the sequence has a single partition).  A
+// second kernel merges partials per (b, hq).
+//
+// MFMA mapping (per 16-token tile, per wave).  Let r = lane % 16, g = lane / 16.
+//   S[t, j] = K[t, :] . Q[j, :]   4 x v_mfma_f32_16x16x32_bf16 over D = 128:
+//     A = K tile (row t = r, 8 dims per lane), B = Q^T (column j = r), both
+//     with the same dim permutation, so lane (r, g) receives S[4g + i, r].
+//   O[j, d] += P[j, t] V[t, d]    8 x v_mfma_f32_16x16x16bf16_1k (one per
+//     16-dim slice): A = P, whose layout (row j = r, tokens 4g..4g+3) is exactly
+//     the S layout above, so the probabilities never leave their lane; B = V
+//     (column = dim 8r + slice, tokens 4g..4g+3).  A lane loads 16 contiguous
+//     bytes (dims 8r..8r+7) of each of its 4 V rows and regroups the halves with
+//     byte permutes.
+// Rows j >= G of the 16-row MFMA tiles are padding (zero Q, zero P): the matrix
+// cores have ~80x the throughput this HBM-bound loop needs, so the padding is
+// free, while the VALU work per token stays at a few instructions (no
+// cross-lane dot-product reductions, two wave shuffles per tile for the max).
+#include "fk_common.h"
+
+namespace fk {
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef short short4_t __attribute__((ext_vector_type(4)));
+typedef float floatx4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kHead = 128;
+constexpr int kTile = 16;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kNegInf = -__builtin_huge_valf();
+
+struct DecodeParams {
+  uint16_t* out;
+  int64_t out_row_stride;
+  const uint16_t* q;
+  int64_t q_row_stride;
+  const uint8_t* k_cache;  // byte pointers; element size from the template
+  const uint8_t* v_cache;
+  const float* k_scale;
+  const float* v_scale;
+  const int32_t* block_tables;
+  int64_t bt_row_stride;
+  const int32_t* ctx_lens;
+  int num_kv_heads;
+  int gqa;
+  int block_size_log2;
+  int part_tokens;
+  int max_parts;
+  int64_t num_blocks;
+  float scale_log2;  // softmax scale * log2(e)
+  float* part_o;     // [B][Hk][max_parts][gqa][128] unnormalised partial outputs
+  float* part_ml;    // [B][Hk][max_parts][gqa][2]   (max, sum) in the log2 domain
+};
+
+__device__ __forceinline__ uint32_t lo_pair(uint32_t a, uint32_t b) {
+  return (a & 0xffffu) | (b << 16);
+}
+__device__ __forceinline__ uint32_t hi_pair(uint32_t a, uint32_t b) {
+  return (a >> 16) | (b & 0xffff0000u);
+}
+__device__ __forceinline__ uint32_t word(const uint4& v, int i) {
+  return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+
+// 4 OCP e4m3fn bytes -> 4 bf16 (exact: every e4m3fn value is a bf16 value).
+__device__ __forceinline__ uint2 fp8x4_to_bf16x4(uint32_t w) {
+  const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8(w, false);
+  const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8(w, true);
+  return make_uint2(hi_pair(__float_as_uint(lo[0]), __float_as_uint(lo[1])),
+                    hi_pair(__float_as_uint(hi[0]), __float_as_uint(hi[1])));
+}
+
+// Raw registers one wave loads for one 16-token tile.  load_tile only issues
+// the loads; conversion and masking happen in the consumer, after the
+// prefetch of the following tile has been issued.
+template <bool kFp8>
+struct TileRegs;
+template <>
+struct TileRegs<false> {
+  uint4 k[4];  // dims 32c + 8g .. +8 of row r
+  uint4 v[4];  // rows 4g+i, dims 8r .. 8r+7
+};
+template <>
+struct TileRegs<true> {
+  uint4 k[2];  // 32 fp8 bytes of row r: dims 32g .. 32g+31
+  uint2 v[4];  // rows 4g+i, dims 8r .. 8r+7 (fp8 bytes)
+};
+
+// Page id of token `tok` of sequence b, or -1 when the block-table entry is
+// negative, >= num_blocks, or past the row (index >= bt_row_stride): such a
+// page is masked and never read.
+__device__ __forceinline__ int64_t page_of(const DecodeParams& P, int b, int tok) {
+  const int idx = tok >> P.block_size_log2;
+  if (idx >= P.bt_row_stride) return -1;
+  const int64_t page = P.block_tables[b * P.bt_row_stride + idx];
+  return (page >= 0 && page < P.num_blocks) ? page : -1;
+}
+
+template <bool kFp8>
+__device__ __forceinline__ void load_tile(const DecodeParams& P, int b, int h, int tok0, int r,
+                                          int g, TileRegs<kFp8>& t) {
+  const int64_t page = page_of(P, b, tok0);
+  if (page < 0) {  // masked page: nothing is read
+    t = TileRegs<kFp8>{};
+    return;
+  }
+  const int bs_mask = (1 << P.block_size_log2) - 1;
+  const int64_t slot0 = (page << P.block_size_log2) + (tok0 & bs_mask);
+  constexpr int kElem = kFp8 ? 1 : 2;
+  const int64_t row_bytes = static_cast<int64_t>(P.num_kv_heads) * kHead * kElem;
+  const int64_t head_off = static_cast<int64_t>(h) * kHead * kElem;
+  const uint8_t* krow = P.k_cache + (slot0 + r) * row_bytes + head_off;
+  if constexpr (!kFp8) {
+    // Per instruction: 16 rows x 64 contiguous bytes.
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      t.k[c] = *reinterpret_cast<const uint4*>(krow + (32 * c + 8 * g) * 2);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      t.v[i] = *reinterpret_cast<const uint4*>(P.v_cache + (slot0 + 4 * g + i) * row_bytes +
+                                               head_off + 8 * r * 2);
+  } else {
+    t.k[0] = *reinterpret_cast<const uint4*>(krow + 32 * g);
+    t.k[1] = *reinterpret_cast<const uint4*>(krow + 32 * g + 16);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      t.v[i] = *reinterpret_cast<const uint2*>(P.v_cache + (slot0 + 4 * g + i) * row_bytes +
+                                               head_off + 8 * r);
+  }
+}
+
+// K operand chunks (bf16) of a loaded tile.
+__device__ __forceinline__ void k_chunks(const TileRegs<false>& t, uint4 (&k)[4]) {
+#pragma unroll
+  for (int c = 0; c < 4; ++c) k[c] = t.k[c];
+}
+__device__ __forceinline__ void k_chunks(const TileRegs<true>& t, uint4 (&k)[4]) {
+  // chunk c = dims 32g + 8c .. +8 = bytes 8c .. 8c+7 of the lane's 32.
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const uint4& src = t.k[c >> 1];
+    const uint32_t w0 = (c & 1) ? src.z : src.x;
+    const uint32_t w1 = (c & 1) ? src.w : src.y;
+    const uint2 lo = fp8x4_to_bf16x4(w0), hi = fp8x4_to_bf16x4(w1);
+    k[c] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+  }
+}
+// V rows (bf16, dims 8r .. 8r+7) of a loaded tile.
+__device__ __forceinline__ uint4 v_row(const TileRegs<false>& t, int i) { return t.v[i]; }
+__device__ __forceinline__ uint4 v_row(const TileRegs<true>& t, int i) {
+  const uint2 lo = fp8x4_to_bf16x4(t.v[i].x), hi = fp8x4_to_bf16x4(t.v[i].y);
+  return make_uint4(lo.x, lo.y, hi.x, hi.y);
+}
+
+template <int NW, int kG, bool kFp8>
+__global__ __launch_bounds__(NW * 64) void paged_decode_partials_kernel(DecodeParams P) {
+  const int p = blockIdx.x;
+  const int h = blockIdx.y;
+  const int b = blockIdx.z;
+  const int ctx = P.ctx_lens[b];
+  const int tok_begin = p * P.part_tokens;
+  if (tok_begin >= ctx) return;  // uniform over the work-group
+  const int tok_end = min(ctx, tok_begin + P.part_tokens);
+  // Tokens past part_tokens * max_parts are outside the launch (the plan's
+  // max_seq_len bounds every context); clamp so the partition count matches
+  // the grid and the reduce kernel.
+  const int nparts = min((ctx + P.part_tokens - 1) / P.part_tokens, P.max_parts);
+
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int r = lane & 15;
+  const int g = lane >> 4;
+  const int gqa = P.gqa;
+  const bool head_ok = r < gqa;
+
+  // Q^T operand: column r = query head h*G + r; dims permuted as the K loads.
+  bf16x8_t qb[4];
+  {
+    const uint16_t* qp = P.q + b * P.q_row_stride + static_cast<int64_t>(h * gqa + r) * kHead;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int d0 = kFp8 ? 32 * g + 8 * c : 32 * c + 8 * g;
+      uint4 v = head_ok ? *reinterpret_cast<const uint4*>(qp + d0) : make_uint4(0, 0, 0, 0);
+      qb[c] = __builtin_bit_cast(bf16x8_t, v);
+    }
+  }
+  float s2 = P.scale_log2;
+  if (kFp8 && P.k_scale) s2 *= P.k_scale[h];
+
+  float m_run = kNegInf;  // running max for head r (same in the 4 lanes of a column)
+  float l_run = 0.f;      // this lane's share of the running sum for head r
+  floatx4_t o[8];
+#pragma unroll
+  for (int d = 0; d < 8; ++d) o[d] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+
+  const int ntiles = (tok_end - tok_begin + kTile - 1) / kTile;
+  TileRegs<kFp8> cur{}, nxt{};
+  int t = wave;
+  if (t < ntiles) load_tile<kFp8>(P, b, h, tok_begin + kTile * t, r, g, cur);
+  for (; t < ntiles; t += NW) {
+    const int tok0 = tok_begin + kTile * t;
+    if (t + NW < ntiles) load_tile<kFp8>(P, b, h, tok_begin + kTile * (t + NW), r, g, nxt);
+    const bool page_ok = page_of(P, b, tok0) >= 0;
+
+    // S[4g+i, r] for the 16 tokens of the tile.
+    uint4 kc[4];
+    k_chunks(cur, kc);
+    floatx4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kc[c]), qb[c],
+                                                   acc, 0, 0, 0);
+    float s[4];
+    float mt = kNegInf;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const bool ok = head_ok && page_ok && (tok0 + 4 * g + i < tok_end);
+      s[i] = ok ? acc[i] * s2 : kNegInf;
+      mt = fmaxf(mt, s[i]);
+    }
+    mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+    const float m_new = fmaxf(m_run, mt);
+    const float m_use = m_new == kNegInf ? 0.f : m_new;
+    // alpha = 1 for columns that have seen no valid score (their O and l are 0).
+    const float alpha = m_new == kNegInf ? 1.f : exp2f(m_run - m_use);
+    float p[4];
+    float psum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      p[i] = exp2f(s[i] - m_use);
+      psum += p[i];
+    }
+    l_run = l_run * alpha + psum;
+    m_run = m_new;
+    // Rescale O rows (head 4g+i lives in lanes whose column r == 4g+i).
+    if (__ballot(alpha != 1.f) != 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float a = __shfl(alpha, 4 * g + i, 64);
+#pragma unroll
+        for (int d = 0; d < 8; ++d) o[d][i] *= a;
+      }
+    }
+    // P as the A operand: row r (head), k = tokens 4g..4g+3.
+    const uint32_t p01 = (static_cast<uint32_t>(f32_to_bf16(p[1])) << 16) | f32_to_bf16(p[0]);
+    const uint32_t p23 = (static_cast<uint32_t>(f32_to_bf16(p[3])) << 16) | f32_to_bf16(p[2]);
+    const short4_t pa = __builtin_bit_cast(short4_t, make_uint2(p01, p23));
+    // V rows past the context (inside a valid page) may hold anything: zero
+    // them so that P = 0 never meets a NaN.
+    uint4 vr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      vr[i] = (tok0 + 4 * g + i < tok_end) ? v_row(cur, i) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+      const int wi = d >> 1;
+      uint32_t b01, b23;
+      if (d & 1) {
+        b01 = hi_pair(word(vr[0], wi), word(vr[1], wi));
+        b23 = hi_pair(word(vr[2], wi), word(vr[3], wi));
+      } else {
+        b01 = lo_pair(word(vr[0], wi), word(vr[1], wi));
+        b23 = lo_pair(word(vr[2], wi), word(vr[3], wi));
+      }
+      const short4_t vb = __builtin_bit_cast(short4_t, make_uint2(b01, b23));
+      o[d] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, vb, o[d], 0, 0, 0);
+    }
+    cur = nxt;
+  }
+
+  // Column sums of l over the 4 lane groups.
+  l_run += __shfl_xor(l_run, 16, 64);
+  l_run += __shfl_xor(l_run, 32, 64);
+
+  // Merge the NW waves through LDS.
+  __shared__ float sm_m[NW][16];
+  __shared__ float sm_l[NW][16];
+  __shared__ float sm_o[NW][kG][kHead];
+  if (lane < 16) {
+    sm_m[wave][lane] = m_run;
+    sm_l[wave][lane] = l_run;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int j = 4 * g + i;
+    if (j < kG && j < gqa) {
+#pragma unroll
+      for (int d = 0; d < 8; ++d) sm_o[wave][j][8 * r + d] = o[d][i];
+    }
+  }
+  __syncthreads();
+
+  const float vs = (kFp8 && P.v_scale) ? P.v_scale[h] : 1.f;
+  const int64_t part_row = (static_cast<int64_t>(b) * P.num_kv_heads + h) * P.max_parts + p;
+  for (int e = threadIdx.x; e < gqa * kHead; e += NW * 64) {
+    const int j = e / kHead;
+    const int d = e - j * kHead;
+    float M = kNegInf;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, sm_m[w][j]);
+    float L = 0.f, O = 0.f;
+    if (M != kNegInf) {
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        const float f = exp2f(sm_m[w][j] - M);
+        L += f * sm_l[w][j];
+        O += f * sm_o[w][j][d];
+      }
+    }
+    if (nparts == 1) {
+      const float v = L > 0.f ? O / L * vs : 0.f;
+      P.out[b * P.out_row_stride + static_cast<int64_t>(h * gqa + j) * kHead + d] = f32_to_bf16(v);
+    } else {
+      P.part_o[(part_row * gqa + j) * kHead + d] = O * vs;
+      if (d == 0) {
+        P.part_ml[(part_row * gqa + j) * 2 + 0] = M;
+        P.part_ml[(part_row * gqa + j) * 2 + 1] = L;
+      }
+    }
+  }
+}
+
+// Merge the partitions of each (sequence, query head) with more than one
+// partition; write zeros for empty sequences.  One wave per (hq, b); each lane
+// owns two output dims.
+__global__ __launch_bounds__(64) void paged_decode_reduce_kernel(
+    uint16_t* __restrict__ out, int64_t out_row_stride, const int32_t* __restrict__ ctx_lens,
+    int num_kv_heads, int gqa, int part_tokens, int max_parts,
+    const float* __restrict__ part_o, const float* __restrict__ part_ml) {
+  const int hq = blockIdx.x;
+  const int b = blockIdx.y;
+  const int lane = threadIdx.x;
+  const int ctx = ctx_lens[b];
+  uint16_t* orow = out + b * out_row_stride + static_cast<int64_t>(hq) * kHead;
+  if (ctx <= 0) {
+    reinterpret_cast<uint32_t*>(orow)[lane] = 0u;
+    return;
+  }
+  const int nparts = min((ctx + part_tokens - 1) / part_tokens, max_parts);
+  if (nparts <= 1) return;  // written by the partials kernel
+  const int h = hq / gqa;
+  const int j = hq - h * gqa;
+  const int64_t base = (static_cast<int64_t>(b) * num_kv_heads + h) * max_parts;
+  float M = kNegInf;
+  for (int p = lane; p < nparts; p += 64) M = fmaxf(M, part_ml[((base + p) * gqa + j) * 2]);
+  M = wave_max(M);
+  float L = 0.f, o0 = 0.f, o1 = 0.f;
+  if (M != kNegInf) {
+    for (int p = 0; p < nparts; ++p) {
+      const int64_t row = (base + p) * gqa + j;
+      const float f = exp2f(part_ml[row * 2] - M);
+      L += f * part_ml[row * 2 + 1];
+      const float2 ov = reinterpret_cast<const float2*>(part_o + row * kHead)[lane];
+      o0 += f * ov.x;
+      o1 += f * ov.y;
+    }
+  }
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  reinterpret_cast<uint32_t*>(orow)[lane] =
+      (static_cast<uint32_t>(f32_to_bf16(o1 * inv)) << 16) | f32_to_bf16(o0 * inv);
+}
+
+constexpr int kNW = 4;  // waves per work-group
+
+struct Shape {
+  int64_t batch;
+  int hq, hk, gqa, head;
+  int64_t part_tokens, max_parts;
+};
+
+int64_t workspace_bytes(int64_t batch, int hq, int hk, int64_t max_parts) {
+  const int64_t rows = batch * hq * max_parts;  // = B * Hk * max_parts * gqa
+  const int64_t o_bytes = (rows * kHead * 4 + 255) / 256 * 256;
+  return o_bytes + rows * 2 * 4;
+}
+
+int validate(const char* name, int64_t batch, int num_heads, int num_kv_heads, int head_size,
+             int64_t part_tokens, int64_t max_parts) {
+  FK_REQUIRE(batch >= 0 && batch <= 65535, "%s: batch %lld out of range [0, 65535]", name,
+             (long long)batch);
+  FK_REQUIRE(num_heads > 0 && num_kv_heads > 0 && num_heads % num_kv_heads == 0,
+             "%s: num_heads %d must be a positive multiple of num_kv_heads %d", name, num_heads,
+             num_kv_heads);
+  if (head_size != kHead)
+    return set_error(FK_ERR_UNSUPPORTED, "%s: head_size %d unsupported (128 only)", name,
+                     head_size);
+  if (num_heads / num_kv_heads > 16)
+    return set_error(FK_ERR_UNSUPPORTED, "%s: GQA group %d > 16 unsupported", name,
+                     num_heads / num_kv_heads);
+  FK_REQUIRE(part_tokens > 0 && part_tokens % (kNW * kTile) == 0 && part_tokens <= (1 << 30),
+             "%s: part_tokens %lld must be a positive multiple of %d", name,
+             (long long)part_tokens, kNW * kTile);
+  FK_REQUIRE(max_parts > 0 && max_parts <= 65535, "%s: max_parts %lld out of range", name,
+             (long long)max_parts);
+  return FK_OK;
+}
+
+}  // namespace
+}  // namespace fk
+
+using namespace fk;
+
+extern "C" int64_t fk_paged_decode_workspace_bytes(int64_t batch, int num_heads,
+                                                   int num_kv_heads, int head_size,
+                                                   int64_t max_parts) {
+  (void)num_kv_heads;
+  (void)head_size;
+  if (batch <= 0 || num_heads <= 0 || max_parts <= 0) return 0;
+  return workspace_bytes(batch, num_heads, num_kv_heads, max_parts);
+}
+
+extern "C" int fk_paged_decode_plan(int64_t batch, int num_kv_heads, int64_t max_seq_len,
+                                    int num_splits, int64_t* part_tokens, int64_t* max_parts) {
+  FK_REQUIRE(part_tokens && max_parts, "fk_paged_decode_plan: null output pointer");
+  FK_REQUIRE(batch >= 0 && num_kv_heads > 0 && max_seq_len >= 0 && num_splits >= 0,
+             "fk_paged_decode_plan: negative argument");
+  constexpr int64_t kQuant = kNW * kTile;  // partition granularity (64 tokens)
+  const int64_t L = max_seq_len > 0 ? max_seq_len : 1;
+  int64_t part;
+  if (num_splits > 0) {
+    part = (L + num_splits - 1) / num_splits;
+  } else {
+    // Enough work-groups to fill 256 CUs several times over, but at least
+    // 256 tokens (64 KiB of bf16 K+V per kv head) per partition.
+    const int64_t units = (batch > 0 ? batch : 1) * num_kv_heads;
+    part = (L * units + 4095) / 4096;
+    if (part < 256) part = 256;
+  }
+  part = (part + kQuant - 1) / kQuant * kQuant;
+  *part_tokens = part;
+  *max_parts = (L + part - 1) / part;
+  return FK_OK;
+}
+
+static int launch_partials(void* out, int64_t out_row_stride, const void* q,
+                           int64_t q_row_stride, const void* k_cache, const void* v_cache,
+                           int kv_dtype, const float* k_scale, const float* v_scale,
+                           const int32_t* block_tables, int64_t bt_row_stride,
+                           const int32_t* ctx_lens, int64_t batch, int num_heads,
+                           int num_kv_heads, int head_size, int block_size, int64_t num_blocks,
+                           float scale, int64_t part_tokens, int64_t max_parts, void* workspace,
+                           int64_t ws_bytes, hipStream_t stream) {
+  const char* name = "fk_paged_decode";
+  int rc = validate(name, batch, num_heads, num_kv_heads, head_size, part_tokens, max_parts);
+  if (rc != FK_OK) return rc;
+  FK_REQUIRE(block_size >= kTile && (block_size & (block_size - 1)) == 0,
+             "%s: block_size %d must be a power of two >= 16", name, block_size);
+  FK_REQUIRE(kv_dtype == FK_DTYPE_BF16 || kv_dtype == FK_DTYPE_FP8_E4M3FN,
+             "%s: kv dtype %d unsupported (bf16 or fp8 e4m3fn)", name, kv_dtype);
+  FK_REQUIRE(q_row_stride >= static_cast<int64_t>(num_heads) * head_size &&
+                 out_row_stride >= static_cast<int64_t>(num_heads) * head_size,
+             "%s: row stride shorter than num_heads * head_size", name);
+  if (batch == 0) return FK_OK;
+  FK_REQUIRE(out && q && k_cache && v_cache && block_tables && ctx_lens, "%s: null pointer",
+             name);
+  FK_REQUIRE(aligned16(q) && aligned16(k_cache) && aligned16(v_cache) && aligned16(out) &&
+                 q_row_stride % 8 == 0 && out_row_stride % 2 == 0,
+             "%s: q/out/cache must be 16-byte aligned with q rows a multiple of 8 elements",
+             name);
+  const int64_t need = workspace_bytes(batch, num_heads, num_kv_heads, max_parts);
+  if (max_parts > 1 && (workspace == nullptr || ws_bytes < need))
+    return set_error(FK_ERR_WORKSPACE, "%s: workspace of %lld bytes < %lld required", name,
+                     (long long)ws_bytes, (long long)need);
+  FK_REQUIRE(max_parts == 1 || aligned16(workspace), "%s: workspace must be 16-byte aligned",
+             name);
+
+  DecodeParams P;
+  P.out = static_cast<uint16_t*>(out);
+  P.out_row_stride = out_row_stride;
+  P.q = static_cast<const uint16_t*>(q);
+  P.q_row_stride = q_row_stride;
+  P.k_cache = static_cast<const uint8_t*>(k_cache);
+  P.v_cache = static_cast<const uint8_t*>(v_cache);
+  P.k_scale = k_scale;
+  P.v_scale = v_scale;
+  P.block_tables = block_tables;
+  P.bt_row_stride = bt_row_stride;
+  P.ctx_lens = ctx_lens;
+  P.num_kv_heads = num_kv_heads;
+  P.gqa = num_heads / num_kv_heads;
+  P.block_size_log2 = __builtin_ctz(static_cast<unsigned>(block_size));
+  P.part_tokens = static_cast<int>(part_tokens);
+  P.max_parts = static_cast<int>(max_parts);
+  P.num_blocks = num_blocks;
+  P.scale_log2 = scale * kLog2e;
+  const int64_t rows = batch * num_heads * max_parts;
+  P.part_o = static_cast<float*>(workspace);
+  P.part_ml = workspace ? reinterpret_cast<float*>(static_cast<char*>(workspace) +
+                                                   (rows * kHead * 4 + 255) / 256 * 256)
+                        : nullptr;
+
+  const dim3 grid(static_cast<unsigned>(max_parts), static_cast<unsigned>(num_kv_heads),
+                  static_cast<unsigned>(batch));
+  const dim3 block(kNW * 64);
+  const bool fp8 = kv_dtype == FK_DTYPE_FP8_E4M3FN;
+#define FK_PD(G)                                                                          \
+  do {                                                                                    \
+    if (fp8)                                                                              \
+      hipLaunchKernelGGL((paged_decode_partials_kernel<kNW, G, true>), grid, block, 0,    \
+                         stream, P);                                                      \
+    else                                                                                  \
+      hipLaunchKernelGGL((paged_decode_partials_kernel<kNW, G, false>), grid, block, 0,   \
+                         stream, P);                                                      \
+  } while (0)
+  if (P.gqa <= 4)
+    FK_PD(4);
+  else if (P.gqa <= 8)
+    FK_PD(8);
+  else
+    FK_PD(16);
+#undef FK_PD
+  return check_launch(name);
+}
+
+static int launch_reduce(void* out, int64_t out_row_stride, const int32_t* ctx_lens,
+                         int64_t batch, int num_heads, int num_kv_heads, int head_size,
+                         int64_t part_tokens, int64_t max_parts, void* workspace,
+                         int64_t ws_bytes, hipStream_t stream) {
+  const char* name = "fk_paged_decode_reduce";
+  int rc = validate(name, batch, num_heads, num_kv_heads, head_size, part_tokens, max_parts);
+  if (rc != FK_OK) return rc;
+  if (batch == 0) return FK_OK;
+  FK_REQUIRE(out && ctx_lens, "%s: null pointer", name);
+  const int64_t need = workspace_bytes(batch, num_heads, num_kv_heads, max_parts);
+  if (max_parts > 1 && (workspace == nullptr || ws_bytes < need))
+    return set_error(FK_ERR_WORKSPACE, "%s: workspace of %lld bytes < %lld required", name,
+                     (long long)ws_bytes, (long long)need);
+  const int64_t rows = batch * num_heads * max_parts;
+  const float* part_o = static_cast<const float*>(workspace);
+  const float* part_ml =
+      workspace ? reinterpret_cast<const float*>(static_cast<const char*>(workspace) +
+                                                 (rows * kHead * 4 + 255) / 256 * 256)
+                : nullptr;
+  hipLaunchKernelGGL(paged_decode_reduce_kernel,
+                     dim3(static_cast<unsigned>(num_heads), static_cast<unsigned>(batch)),
+                     dim3(64), 0, stream, static_cast<uint16_t*>(out), out_row_stride, ctx_lens,
+                     num_kv_heads, num_heads / num_kv_heads, static_cast<int>(part_tokens),
+                     static_cast<int>(max_parts), part_o, part_ml);
+  return check_launch(name);
+}
+
+extern "C" int fk_paged_decode_partials(
+    void* out, int64_t out_row_stride, const void* q, int64_t q_row_stride, const void* k_cache,
+    const void* v_cache, int kv_dtype, const float* k_scale, const float* v_scale,
+    const int32_t* block_tables, int64_t bt_row_stride, const int32_t* ctx_lens, int64_t batch,
+    int num_heads, int num_kv_heads, int head_size, int block_size, int64_t num_blocks,
+    float scale, int64_t part_tokens, int64_t max_parts, void* workspace,
+    int64_t workspace_bytes_, void* stream) {
+  return launch_partials(out, out_row_stride, q, q_row_stride, k_cache, v_cache, kv_dtype,
+                         k_scale, v_scale, block_tables, bt_row_stride, ctx_lens, batch,
+                         num_heads, num_kv_heads, head_size, block_size, num_blocks, scale,
+                         part_tokens, max_parts, workspace, workspace_bytes_, as_stream(stream));
+}
+
+extern "C" int fk_paged_decode_reduce(void* out, int64_t out_row_stride, const int32_t* ctx_lens,
+                                      int64_t batch, int num_heads, int num_kv_heads,
+                                      int head_size, int64_t part_tokens, int64_t max_parts,
+                                      void* workspace, int64_t workspace_bytes_, void* stream) {
+  return launch_reduce(out, out_row_stride, ctx_lens, batch, num_heads, num_kv_heads, head_size,
+                       part_tokens, max_parts, workspace, workspace_bytes_, as_stream(stream));
+}
+
+extern "C" int fk_paged_decode(void* out, int64_t out_row_stride, const void* q,
+                               int64_t q_row_stride, const void* k_cache, const void* v_cache,
+                               int kv_dtype, const float* k_scale, const float* v_scale,
+                               const int32_t* block_tables, int64_t bt_row_stride,
+                               const int32_t* ctx_lens, int64_t batch, int num_heads,
+                               int num_kv_heads, int head_size, int block_size,
+                               int64_t num_blocks, float scale, int64_t part_tokens,
+                               int64_t max_parts, void* workspace, int64_t workspace_bytes_,
+                               void* stream) {
+  int rc = launch_partials(out, out_row_stride, q, q_row_stride, k_cache, v_cache, kv_dtype,
+                           k_scale, v_scale, block_tables, bt_row_stride, ctx_lens, batch,
+                           num_heads, num_kv_heads, head_size, block_size, num_blocks, scale,
+                           part_tokens, max_parts, workspace, workspace_bytes_,
+                           as_stream(stream));
+  if (rc != FK_OK) return rc;
+  return launch_reduce(out, out_row_stride, ctx_lens, batch, num_heads, num_kv_heads, head_size,
+                       part_tokens, max_parts, workspace, workspace_bytes_, as_stream(stream));
+}

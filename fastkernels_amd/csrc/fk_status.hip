@@ -1,0 +1,34 @@
+// Library-wide status reporting and version for the fastkernels_amd C ABI.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "fk_common.h"
+
+namespace fk {
+
+namespace {
+thread_local char g_last_error[512] = "";
+}
+
+int set_error(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+// Reports a failed launch (bad configuration, no device, ...) as its hipError_t.
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    return set_error(static_cast<int>(e), "%s: launch failed: %s", what, hipGetErrorString(e));
+  }
+  return FK_OK;
+}
+
+}  // namespace fk
+
+extern "C" int fk_version(void) { return 100; }  // 0.1.0
+
+extern "C" const char* fk_last_error(void) { return fk::g_last_error; }

@@ -1,0 +1,163 @@
+// store_kvcache: bit-exact scatter of each token's K and V row into the NHD
+// paged cache at slot_mapping[token] (fastkernels/tasks/baseline/L1/
+// store_kvcache.py:16-35 computes the same mapping, one Triton program per token).
+//
+// MI355X layout: a token row is num_kv_heads*head_size contiguous elements
+// (2 KiB for 8x128 bf16), and slot s owns bytes [s*row, (s+1)*row) of each cache.
+// Each lane moves 16-byte chunks (global_load/store_dwordx4); a 256-lane
+// work-group covers 256/chunks_per_row tokens, so one wave writes a contiguous
+// 1 KiB run of a destination row and every access is a full 64-byte segment.
+#include "fk_common.h"
+
+namespace fk {
+namespace {
+
+template <typename IdxT>
+__device__ __forceinline__ int64_t load_slot(const void* slot_mapping, int64_t i) {
+  return static_cast<int64_t>(static_cast<const IdxT*>(slot_mapping)[i]);
+}
+
+// Vector path: row bytes, row strides and base pointers are multiples of 16 B.
+template <typename IdxT>
+__global__ __launch_bounds__(256) void store_kvcache_vec16(
+    const uint4* __restrict__ key, int64_t key_row_chunks, const uint4* __restrict__ value,
+    int64_t value_row_chunks, uint4* __restrict__ k_cache, uint4* __restrict__ v_cache,
+    const void* __restrict__ slot_mapping, int64_t tokens, int chunks_per_row,
+    int tokens_per_block, int64_t num_slots) {
+  const int lane_tok = threadIdx.x / chunks_per_row;  // chunks_per_row <= 256 here
+  const int chunk0 = threadIdx.x % chunks_per_row;
+  if (lane_tok >= tokens_per_block) return;
+  const int64_t tok = static_cast<int64_t>(blockIdx.x) * tokens_per_block + lane_tok;
+  if (tok >= tokens) return;
+  const int64_t slot = load_slot<IdxT>(slot_mapping, tok);
+  if (slot < 0 || slot >= num_slots) return;
+  const uint4* ksrc = key + tok * key_row_chunks;
+  const uint4* vsrc = value + tok * value_row_chunks;
+  uint4* kdst = k_cache + slot * chunks_per_row;
+  uint4* vdst = v_cache + slot * chunks_per_row;
+  const uint4 kv = ksrc[chunk0];
+  const uint4 vv = vsrc[chunk0];
+  kdst[chunk0] = kv;
+  vdst[chunk0] = vv;
+}
+
+// Wide rows (> 256 chunks): one work-group per token, lanes stride the row.
+template <typename IdxT>
+__global__ __launch_bounds__(256) void store_kvcache_vec16_wide(
+    const uint4* __restrict__ key, int64_t key_row_chunks, const uint4* __restrict__ value,
+    int64_t value_row_chunks, uint4* __restrict__ k_cache, uint4* __restrict__ v_cache,
+    const void* __restrict__ slot_mapping, int64_t tokens, int64_t chunks_per_row,
+    int64_t num_slots) {
+  const int64_t tok = blockIdx.x;
+  const int64_t slot = load_slot<IdxT>(slot_mapping, tok);
+  if (slot < 0 || slot >= num_slots) return;
+  const uint4* ksrc = key + tok * key_row_chunks;
+  const uint4* vsrc = value + tok * value_row_chunks;
+  uint4* kdst = k_cache + slot * chunks_per_row;
+  uint4* vdst = v_cache + slot * chunks_per_row;
+  for (int64_t c = threadIdx.x; c < chunks_per_row; c += 256) {
+    const uint4 kv = ksrc[c];
+    const uint4 vv = vsrc[c];
+    kdst[c] = kv;
+    vdst[c] = vv;
+  }
+}
+
+// Scalar path for any alignment: elements of ElemT (1, 2 or 4 bytes).
+template <typename IdxT, typename ElemT>
+__global__ __launch_bounds__(256) void store_kvcache_scalar(
+    const ElemT* __restrict__ key, int64_t key_row_stride, const ElemT* __restrict__ value,
+    int64_t value_row_stride, ElemT* __restrict__ k_cache, ElemT* __restrict__ v_cache,
+    const void* __restrict__ slot_mapping, int64_t row_elems, int64_t num_slots) {
+  const int64_t tok = blockIdx.x;
+  const int64_t slot = load_slot<IdxT>(slot_mapping, tok);
+  if (slot < 0 || slot >= num_slots) return;
+  for (int64_t c = threadIdx.x; c < row_elems; c += 256) {
+    k_cache[slot * row_elems + c] = key[tok * key_row_stride + c];
+    v_cache[slot * row_elems + c] = value[tok * value_row_stride + c];
+  }
+}
+
+template <typename IdxT>
+int launch(const void* key, int64_t key_row_stride, const void* value, int64_t value_row_stride,
+           void* k_cache, void* v_cache, const void* slot_mapping, int64_t tokens,
+           int64_t row_elems, int elem_bytes, int64_t num_slots, hipStream_t stream) {
+  const int64_t row_bytes = row_elems * elem_bytes;
+  const bool vec = (row_bytes % 16 == 0) && ((key_row_stride * elem_bytes) % 16 == 0) &&
+                   ((value_row_stride * elem_bytes) % 16 == 0) && aligned16(key) &&
+                   aligned16(value) && aligned16(k_cache) && aligned16(v_cache);
+  if (vec) {
+    const int64_t cpr = row_bytes / 16;
+    const int64_t krc = key_row_stride * elem_bytes / 16;
+    const int64_t vrc = value_row_stride * elem_bytes / 16;
+    if (cpr <= 256) {
+      const int tpb = static_cast<int>(256 / cpr);
+      const int64_t blocks = (tokens + tpb - 1) / tpb;
+      hipLaunchKernelGGL(store_kvcache_vec16<IdxT>, dim3(static_cast<unsigned>(blocks)), dim3(256),
+                         0, stream, static_cast<const uint4*>(key), krc,
+                         static_cast<const uint4*>(value), vrc, static_cast<uint4*>(k_cache),
+                         static_cast<uint4*>(v_cache), slot_mapping, tokens,
+                         static_cast<int>(cpr), tpb, num_slots);
+    } else {
+      hipLaunchKernelGGL(store_kvcache_vec16_wide<IdxT>, dim3(static_cast<unsigned>(tokens)),
+                         dim3(256), 0, stream, static_cast<const uint4*>(key), krc,
+                         static_cast<const uint4*>(value), vrc, static_cast<uint4*>(k_cache),
+                         static_cast<uint4*>(v_cache), slot_mapping, tokens, cpr, num_slots);
+    }
+    return check_launch("fk_store_kvcache");
+  }
+  const dim3 grid(static_cast<unsigned>(tokens));
+  switch (elem_bytes) {
+    case 1:
+      hipLaunchKernelGGL((store_kvcache_scalar<IdxT, uint8_t>), grid, dim3(256), 0, stream,
+                         static_cast<const uint8_t*>(key), key_row_stride,
+                         static_cast<const uint8_t*>(value), value_row_stride,
+                         static_cast<uint8_t*>(k_cache), static_cast<uint8_t*>(v_cache),
+                         slot_mapping, row_elems, num_slots);
+      break;
+    case 2:
+      hipLaunchKernelGGL((store_kvcache_scalar<IdxT, uint16_t>), grid, dim3(256), 0, stream,
+                         static_cast<const uint16_t*>(key), key_row_stride,
+                         static_cast<const uint16_t*>(value), value_row_stride,
+                         static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache),
+                         slot_mapping, row_elems, num_slots);
+      break;
+    default:
+      hipLaunchKernelGGL((store_kvcache_scalar<IdxT, uint32_t>), grid, dim3(256), 0, stream,
+                         static_cast<const uint32_t*>(key), key_row_stride,
+                         static_cast<const uint32_t*>(value), value_row_stride,
+                         static_cast<uint32_t*>(k_cache), static_cast<uint32_t*>(v_cache),
+                         slot_mapping, row_elems, num_slots);
+      break;
+  }
+  return check_launch("fk_store_kvcache");
+}
+
+}  // namespace
+}  // namespace fk
+
+extern "C" int fk_store_kvcache(const void* key, int64_t key_row_stride, const void* value,
+                                int64_t value_row_stride, void* k_cache, void* v_cache,
+                                const void* slot_mapping, int slot_is_i64, int64_t tokens,
+                                int64_t row_elems, int elem_bytes, int64_t num_slots,
+                                void* stream) {
+  FK_REQUIRE(tokens >= 0 && row_elems >= 0 && num_slots >= 0,
+             "fk_store_kvcache: negative size (tokens=%lld row_elems=%lld num_slots=%lld)",
+             (long long)tokens, (long long)row_elems, (long long)num_slots);
+  FK_REQUIRE(elem_bytes == 1 || elem_bytes == 2 || elem_bytes == 4,
+             "fk_store_kvcache: elem_bytes must be 1, 2 or 4 (got %d)", elem_bytes);
+  FK_REQUIRE(tokens <= 0x7fffffffLL, "fk_store_kvcache: too many tokens (%lld)",
+             (long long)tokens);
+  FK_REQUIRE(key_row_stride >= row_elems && value_row_stride >= row_elems,
+             "fk_store_kvcache: row stride shorter than the row (%lld/%lld < %lld)",
+             (long long)key_row_stride, (long long)value_row_stride, (long long)row_elems);
+  if (tokens == 0 || row_elems == 0) return FK_OK;
+  FK_REQUIRE(key && value && k_cache && v_cache && slot_mapping,
+             "fk_store_kvcache: null pointer");
+  hipStream_t s = fk::as_stream(stream);
+  if (slot_is_i64)
+    return fk::launch<int64_t>(key, key_row_stride, value, value_row_stride, k_cache, v_cache,
+                               slot_mapping, tokens, row_elems, elem_bytes, num_slots, s);
+  return fk::launch<int32_t>(key, key_row_stride, value, value_row_stride, k_cache, v_cache,
+                             slot_mapping, tokens, row_elems, elem_bytes, num_slots, s);
+}

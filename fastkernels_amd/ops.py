@@ -1,0 +1,326 @@
+"""Torch-facing entry points of the gfx950 decode-step kernels.
+
+Each function validates its tensors, then calls the C ABI (``_native``) with raw
+device pointers and the current HIP stream.  Nothing here computes on the host:
+every op is one or two kernel launches, enqueued asynchronously.
+
+The same functions are registered as ``torch.library`` custom ops in the
+``fastkernels_amd`` namespace with in-place mutation annotations and no-op
+fake (Meta) implementations, mirroring the reference's
+``fastkernels_norm::*`` (fastkernels/tasks/baseline/L1/rms_norm.py:44-69) and
+``fastkernels_rope::rotary_embedding`` (rotary_emb.py:24-39) schemas, so they
+stay opaque under torch.compile and are capturable in HIP graphs.
+"""
+from __future__ import annotations
+
+import math
+from ctypes import c_void_p
+
+import torch
+
+from . import _native
+
+_DTYPE_TAG = {
+    torch.float32: _native.FK_DTYPE_F32,
+    torch.float16: _native.FK_DTYPE_F16,
+    torch.bfloat16: _native.FK_DTYPE_BF16,
+}
+_FP8 = getattr(torch, "float8_e4m3fn", None)
+
+
+def _tag(t: torch.Tensor, what: str) -> int:
+    try:
+        return _DTYPE_TAG[t.dtype]
+    except KeyError:
+        raise TypeError(f"{what}: unsupported dtype {t.dtype}") from None
+
+
+def _stream(t: torch.Tensor) -> c_void_p:
+    if t.device.type != "cuda":
+        raise RuntimeError(f"fastkernels_amd ops run on the GPU only (got a {t.device} tensor)")
+    return c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _ptr(t: torch.Tensor | None) -> c_void_p:
+    return c_void_p(t.data_ptr() if t is not None else 0)
+
+
+def _rows(t: torch.Tensor, width: int, what: str) -> tuple[int, int]:
+    """(rows, row_stride) of a tensor viewed as [rows, width] with unit inner stride."""
+    if t.dim() == 0:
+        raise ValueError(f"{what}: expected at least one dimension")
+    if t.numel() == 0:
+        return 0, width
+    if t.dim() == 1:
+        if t.shape[0] != width or t.stride(0) != 1:
+            raise ValueError(f"{what}: expected a contiguous row of {width}")
+        return 1, width
+    try:
+        v = t.view(-1, t.shape[-1])
+    except RuntimeError as e:
+        raise ValueError(f"{what}: leading dimensions must be collapsible ({e})") from None
+    if v.shape[-1] != width or v.stride(-1) != 1:
+        raise ValueError(f"{what}: last dimension must be contiguous with size {width}")
+    return v.shape[0], v.stride(0)
+
+
+def _same_device(*ts: torch.Tensor) -> None:
+    dev = ts[0].device
+    for t in ts[1:]:
+        if t is not None and t.device != dev:
+            raise ValueError(f"tensors on different devices: {dev} vs {t.device}")
+
+
+# ---------------------------------------------------------------------------
+# RMSNorm
+# ---------------------------------------------------------------------------
+def rms_norm(out: torch.Tensor, x: torch.Tensor, weight: torch.Tensor, eps: float) -> None:
+    """out = rmsnorm(x) * weight (vLLM ``rms_norm(out, input, weight, eps)`` contract)."""
+    hidden = x.shape[-1]
+    _same_device(out, x, weight)
+    if out.dtype != x.dtype or weight.dtype != x.dtype:
+        raise TypeError("rms_norm: out, x and weight must share a dtype")
+    if out.shape != x.shape or weight.shape != (hidden,) or not weight.is_contiguous():
+        raise ValueError("rms_norm: shape mismatch")
+    rows, xs = _rows(x, hidden, "rms_norm x")
+    _, os_ = _rows(out, hidden, "rms_norm out")
+    if rows == 0:
+        return
+    _native.call("fk_rmsnorm", _ptr(out), os_, _ptr(x), xs, _ptr(weight), rows, hidden,
+                 float(eps), _tag(x, "rms_norm"), _stream(x))
+
+
+def fused_add_rms_norm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor,
+                       eps: float) -> None:
+    """In place: residual <- x + residual; x <- rmsnorm(residual) * weight."""
+    hidden = x.shape[-1]
+    _same_device(x, residual, weight)
+    if residual.dtype != x.dtype or weight.dtype != x.dtype:
+        raise TypeError("fused_add_rms_norm: x, residual and weight must share a dtype")
+    if residual.shape != x.shape or weight.shape != (hidden,) or not weight.is_contiguous():
+        raise ValueError("fused_add_rms_norm: shape mismatch")
+    rows, xs = _rows(x, hidden, "fused_add_rms_norm x")
+    _, rs = _rows(residual, hidden, "fused_add_rms_norm residual")
+    if rows == 0:
+        return
+    _native.call("fk_fused_add_rmsnorm", _ptr(x), xs, _ptr(residual), rs, _ptr(weight), rows,
+                 hidden, float(eps), _tag(x, "fused_add_rms_norm"), _stream(x))
+
+
+# ---------------------------------------------------------------------------
+# Rotary embedding
+# ---------------------------------------------------------------------------
+def rotary_embedding(positions: torch.Tensor, query: torch.Tensor, key: torch.Tensor | None,
+                     head_size: int, cos_sin_cache: torch.Tensor, is_neox: bool) -> None:
+    """In-place rotary embedding of query (and key) rows at ``positions``."""
+    if positions.dtype != torch.int64:
+        raise TypeError("rotary_embedding: positions must be int64")
+    tokens = positions.numel()
+    if not positions.is_contiguous():
+        raise ValueError("rotary_embedding: positions must be contiguous")
+    _same_device(positions, query, cos_sin_cache, *([key] if key is not None else []))
+    if cos_sin_cache.dim() != 2 or not cos_sin_cache.is_contiguous():
+        raise ValueError("rotary_embedding: cos_sin_cache must be a contiguous [max_pos, rot_dim]")
+    if cos_sin_cache.dtype not in (torch.float32, query.dtype):
+        raise TypeError("rotary_embedding: cos_sin_cache must be float32 or the query dtype")
+    if key is not None and key.dtype != query.dtype:
+        raise TypeError("rotary_embedding: query and key must share a dtype")
+    if tokens == 0:
+        return
+    qw = query.numel() // tokens
+    if qw % head_size:
+        raise ValueError("rotary_embedding: query width is not a multiple of head_size")
+    try:
+        q2 = query.view(tokens, qw)
+    except RuntimeError as e:
+        raise ValueError(f"rotary_embedding: query rows must be [heads*head_size] ({e})") from None
+    if q2.stride(1) != 1:
+        raise ValueError("rotary_embedding: query rows must be contiguous")
+    num_heads = qw // head_size
+    k_stride, num_kv = 0, 0
+    if key is not None:
+        kw = key.numel() // tokens
+        if kw % head_size:
+            raise ValueError("rotary_embedding: key width is not a multiple of head_size")
+        try:
+            k2 = key.view(tokens, kw)
+        except RuntimeError as e:
+            raise ValueError(f"rotary_embedding: key rows must be [heads*head_size] ({e})") from None
+        if k2.stride(1) != 1:
+            raise ValueError("rotary_embedding: key rows must be contiguous")
+        k_stride, num_kv = k2.stride(0), kw // head_size
+    _native.call("fk_rotary_embedding", _ptr(positions), _ptr(query), q2.stride(0), _ptr(key),
+                 k_stride, _ptr(cos_sin_cache), _tag(cos_sin_cache, "rotary cache"),
+                 cos_sin_cache.shape[0], tokens, num_heads, num_kv, head_size,
+                 cos_sin_cache.shape[1], int(bool(is_neox)), _tag(query, "rotary_embedding"),
+                 _stream(query))
+
+
+# ---------------------------------------------------------------------------
+# store_kvcache
+# ---------------------------------------------------------------------------
+def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
+                  v_cache: torch.Tensor, slot_mapping: torch.Tensor) -> None:
+    """Scatter key/value [N, Hk, D] rows into NHD caches at slot_mapping (-1 skips)."""
+    if key.dim() != 3 or value.shape != key.shape:
+        raise ValueError("store_kvcache: key/value must be [N, num_kv_heads, head_dim]")
+    n, hk, hd = key.shape
+    if k_cache.dim() != 4 or v_cache.shape != k_cache.shape or tuple(k_cache.shape[2:]) != (hk, hd):
+        raise ValueError("store_kvcache: caches must be [num_blocks, block_size, Hk, D]")
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("store_kvcache: caches must be contiguous")
+    if key.dtype != k_cache.dtype or value.dtype != v_cache.dtype:
+        raise TypeError("store_kvcache: key/value dtype must equal the cache dtype")
+    for t, nm in ((key, "key"), (value, "value")):
+        if t.stride(2) != 1 or (hk > 1 and t.stride(1) != hd):
+            raise ValueError(f"store_kvcache: {nm} rows must be [Hk, D] contiguous")
+    if slot_mapping.dtype not in (torch.int32, torch.int64) or not slot_mapping.is_contiguous():
+        raise TypeError("store_kvcache: slot_mapping must be contiguous int32 or int64")
+    if slot_mapping.numel() < n:
+        raise ValueError("store_kvcache: slot_mapping shorter than the token count")
+    _same_device(key, value, k_cache, v_cache, slot_mapping)
+    if n == 0:
+        return
+    num_slots = k_cache.shape[0] * k_cache.shape[1]
+    _native.call("fk_store_kvcache", _ptr(key), key.stride(0), _ptr(value), value.stride(0),
+                 _ptr(k_cache), _ptr(v_cache), _ptr(slot_mapping),
+                 int(slot_mapping.dtype == torch.int64), n, hk * hd, key.element_size(),
+                 num_slots, _stream(key))
+
+
+# ---------------------------------------------------------------------------
+# Paged decode attention
+# ---------------------------------------------------------------------------
+def paged_decode_plan(batch: int, num_kv_heads: int, max_seq_len: int,
+                      num_splits: int = 0) -> tuple[int, int]:
+    """(part_tokens, max_parts) for a launch over contexts of at most max_seq_len."""
+    return _native.plan(batch, num_kv_heads, max_seq_len, num_splits)
+
+
+def paged_decode_workspace_bytes(batch: int, num_heads: int, num_kv_heads: int, head_size: int,
+                                 max_parts: int) -> int:
+    return _native.workspace_bytes(batch, num_heads, num_kv_heads, head_size, max_parts)
+
+
+def _check_decode(out, q, k_cache, v_cache, block_table, cache_seqlens, k_scale, v_scale):
+    if q.dim() != 3 or q.dtype != torch.bfloat16 or q.stride(2) != 1 or q.stride(1) != q.shape[2]:
+        raise ValueError("paged_decode: q must be bf16 [B, Hq, D] with contiguous heads")
+    b, hq, d = q.shape
+    if out.shape != q.shape or out.dtype != q.dtype or out.stride(2) != 1 or out.stride(1) != d:
+        raise ValueError("paged_decode: out must be bf16 [B, Hq, D] with contiguous heads")
+    if k_cache.dim() != 4 or v_cache.shape != k_cache.shape or k_cache.shape[3] != d:
+        raise ValueError("paged_decode: caches must be [num_blocks, block_size, Hk, D]")
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("paged_decode: caches must be contiguous")
+    if k_cache.dtype != v_cache.dtype or k_cache.dtype not in (torch.bfloat16, _FP8):
+        raise TypeError("paged_decode: caches must both be bf16 or float8_e4m3fn")
+    if block_table.dtype != torch.int32 or block_table.dim() != 2 or block_table.stride(1) != 1:
+        raise TypeError("paged_decode: block_table must be int32 [B, max_blocks], rows contiguous")
+    if block_table.shape[0] < b:
+        raise ValueError("paged_decode: block_table has fewer rows than the batch")
+    if cache_seqlens.dtype != torch.int32 or not cache_seqlens.is_contiguous() or \
+            cache_seqlens.numel() < b:
+        raise TypeError("paged_decode: cache_seqlens must be contiguous int32 [B]")
+    hk = k_cache.shape[2]
+    for s, nm in ((k_scale, "k_scale"), (v_scale, "v_scale")):
+        if s is not None and (s.dtype != torch.float32 or s.numel() != hk or
+                              not s.is_contiguous()):
+            raise ValueError(f"paged_decode: {nm} must be float32 [num_kv_heads]")
+    _same_device(out, q, k_cache, v_cache, block_table, cache_seqlens)
+
+
+def paged_decode(out: torch.Tensor, q: torch.Tensor, k_cache: torch.Tensor,
+                 v_cache: torch.Tensor, block_table: torch.Tensor, cache_seqlens: torch.Tensor,
+                 softmax_scale: float, part_tokens: int, max_parts: int,
+                 workspace: torch.Tensor | None, k_scale: torch.Tensor | None = None,
+                 v_scale: torch.Tensor | None = None) -> None:
+    """Paged decode attention into ``out`` ([B, Hq, D] bf16)."""
+    _check_decode(out, q, k_cache, v_cache, block_table, cache_seqlens, k_scale, v_scale)
+    b, hq, d = q.shape
+    if b == 0:
+        return
+    nb, bs, hk, _ = k_cache.shape
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    _native.call("fk_paged_decode", _ptr(out), out.stride(0), _ptr(q), q.stride(0),
+                 _ptr(k_cache), _ptr(v_cache),
+                 _native.FK_DTYPE_FP8_E4M3FN if k_cache.dtype == _FP8 else _native.FK_DTYPE_BF16,
+                 _ptr(k_scale), _ptr(v_scale), _ptr(block_table), block_table.stride(0),
+                 _ptr(cache_seqlens), b, hq, hk, d, bs, nb, float(softmax_scale), part_tokens,
+                 max_parts, _ptr(workspace), ws_bytes, _stream(q))
+
+
+def paged_decode_phases(out, q, k_cache, v_cache, block_table, cache_seqlens, softmax_scale,
+                        part_tokens, max_parts, workspace, k_scale=None, v_scale=None):
+    """The two launches of :func:`paged_decode` as separate callables (for timing)."""
+    _check_decode(out, q, k_cache, v_cache, block_table, cache_seqlens, k_scale, v_scale)
+    b, hq, d = q.shape
+    nb, bs, hk, _ = k_cache.shape
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    kvd = _native.FK_DTYPE_FP8_E4M3FN if k_cache.dtype == _FP8 else _native.FK_DTYPE_BF16
+    stream = _stream(q)
+    lib = _native.lib()
+    part_args = (_ptr(out), out.stride(0), _ptr(q), q.stride(0), _ptr(k_cache), _ptr(v_cache),
+                 kvd, _ptr(k_scale), _ptr(v_scale), _ptr(block_table), block_table.stride(0),
+                 _ptr(cache_seqlens), b, hq, hk, d, bs, nb, float(softmax_scale), part_tokens,
+                 max_parts, _ptr(workspace), ws_bytes, stream)
+    red_args = (_ptr(out), out.stride(0), _ptr(cache_seqlens), b, hq, hk, d, part_tokens,
+                max_parts, _ptr(workspace), ws_bytes, stream)
+    fp, fr = lib.fk_paged_decode_partials, lib.fk_paged_decode_reduce
+
+    def partials():
+        _native.check("fk_paged_decode_partials", fp(*part_args))
+
+    def reduce():
+        _native.check("fk_paged_decode_reduce", fr(*red_args))
+
+    return partials, reduce
+
+
+# ---------------------------------------------------------------------------
+# SiLU-and-mul
+# ---------------------------------------------------------------------------
+def silu_and_mul(out: torch.Tensor, x: torch.Tensor) -> None:
+    """out = silu(x[..., :d]) * x[..., d:] (``_C.silu_and_mul(out, x)`` contract)."""
+    d = x.shape[-1] // 2
+    if x.shape[-1] != 2 * d or out.shape != x.shape[:-1] + (d,) or out.dtype != x.dtype:
+        raise ValueError("silu_and_mul: out must be x.shape[:-1] + (d,) with x's dtype")
+    _same_device(out, x)
+    rows, xs = _rows(x, 2 * d, "silu_and_mul x")
+    _, os_ = _rows(out, d, "silu_and_mul out")
+    if rows == 0 or d == 0:
+        return
+    _native.call("fk_silu_and_mul", _ptr(out), os_, _ptr(x), xs, rows, d, _tag(x, "silu_and_mul"),
+                 _stream(x))
+
+
+# ---------------------------------------------------------------------------
+# torch.library registration (opaque custom ops with mutation annotations).
+# ---------------------------------------------------------------------------
+_LIB = torch.library.Library("fastkernels_amd", "DEF")
+_LIB.define("rmsnorm(Tensor! result, Tensor input, Tensor weight, float eps) -> ()")
+_LIB.define("fused_add_rmsnorm(Tensor(a!) input, Tensor(b!) residual, Tensor weight, "
+            "float eps) -> ()")
+_LIB.define("rotary_embedding(Tensor positions, Tensor(a!) query, Tensor(b!)? key, "
+            "int head_size, Tensor cos_sin_cache, bool is_neox) -> ()")
+_LIB.define("store_kvcache(Tensor key, Tensor value, Tensor(a!) k_cache, Tensor(b!) v_cache, "
+            "Tensor slot_mapping) -> ()")
+_LIB.define("paged_decode(Tensor(a!) out, Tensor q, Tensor k_cache, Tensor v_cache, "
+            "Tensor block_table, Tensor cache_seqlens, float softmax_scale, int part_tokens, "
+            "int max_parts, Tensor(b!)? workspace, Tensor? k_scale, Tensor? v_scale) -> ()")
+_LIB.define("silu_and_mul(Tensor! result, Tensor input) -> ()")
+
+_IMPLS = {
+    "rmsnorm": lambda result, input, weight, eps: rms_norm(result, input, weight, eps),
+    "fused_add_rmsnorm": fused_add_rms_norm,
+    "rotary_embedding": rotary_embedding,
+    "store_kvcache": store_kvcache,
+    "paged_decode": paged_decode,
+    "silu_and_mul": lambda result, input: silu_and_mul(result, input),
+}
+for _name, _fn in _IMPLS.items():
+    _LIB.impl(_name, _fn, "CUDA")
+    _LIB.impl(_name, lambda *a, **k: None, "Meta")
+
+
+def default_softmax_scale(head_dim: int) -> float:
+    return 1.0 / math.sqrt(head_dim)

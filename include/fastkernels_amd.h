@@ -1,0 +1,177 @@
+/*
+ * fastkernels_amd.h — C ABI of the MI355X (gfx950) decode-step operator library.
+ *
+ * One shared library, libfk_amd.so, exports one entry point per operator of the
+ * serving-engine decode step.  Every entry point:
+ *   - takes raw device pointers, element counts, row strides (in elements) and a
+ *     hipStream_t passed as void* (NULL = the null stream);
+ *   - enqueues its kernels on that stream and returns without synchronising;
+ *   - allocates nothing (the paged-decode split-context workspace is caller-owned);
+ *   - returns FK_OK (0), a negative FK_ERR_* code for a rejected argument, or a
+ *     positive hipError_t from the launch.  fk_last_error() returns a message for
+ *     the last failing call on the calling thread.
+ * No torch types appear here: the Python layer (fastkernels_amd/_native.py)
+ * binds these symbols with ctypes.
+ *
+ * Reference interfaces replaced (paths relative to the Snowflake-AI-Research/
+ * fastkernels checkout):
+ *   fk_rmsnorm / fk_fused_add_rmsnorm
+ *       fastkernels/tasks/baseline/L1/rms_norm.py:44-69 (ops fastkernels_norm::rmsnorm,
+ *       fastkernels_norm::fused_add_rmsnorm) and the vLLM kernels they bind,
+ *       rms_norm.cu:1456 (rms_norm) and rms_norm.cu:1546 (fused_add_rms_norm).
+ *   fk_rotary_embedding
+ *       fastkernels/tasks/baseline/L1/rotary_emb.py:24-39 (op fastkernels_rope::rotary_embedding),
+ *       host function rotary_emb.cu:427-533.
+ *   fk_store_kvcache
+ *       fastkernels/tasks/baseline/L1/store_kvcache.py:16-35,71-82 (Triton _store_kvcache_kernel,
+ *       StoreKVCache.forward, NHD layout).
+ *   fk_paged_decode_workspace_bytes / fk_paged_decode
+ *       fastkernels/tasks/baseline/L1/flash_attn_decode.py:113-181 (FlashAttnDecode.forward ->
+ *       vllm.vllm_flash_attn.flash_attn_varlen_func with block_table, seqused_k, num_splits);
+ *       split-context merge semantics of triton_unified_attention.py:697-784 (reduce_segments);
+ *       fp8 per-tensor KV dequant semantics of triton_unified_attention.py:51-67 (_cast_kv_tile).
+ *   fk_silu_and_mul
+ *       fastkernels/tasks/baseline/L1/silu_and_mul.py:24-30 (_C.silu_and_mul(out, x)),
+ *       kernel silu_and_mul.cu:951-956.
+ */
+#ifndef FASTKERNELS_AMD_H_
+#define FASTKERNELS_AMD_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes (negative = argument rejected before any launch). */
+#define FK_OK 0
+#define FK_ERR_INVALID_ARG (-1)
+#define FK_ERR_UNSUPPORTED (-2)
+#define FK_ERR_WORKSPACE (-3)
+
+/* Element type tags. */
+#define FK_DTYPE_F32 0
+#define FK_DTYPE_F16 1
+#define FK_DTYPE_BF16 2
+#define FK_DTYPE_FP8_E4M3FN 3 /* OCP float8 e4m3fn (torch.float8_e4m3fn) */
+
+/* Library version as 10000*major + 100*minor + patch. */
+int fk_version(void);
+
+/* Message describing the last failing call on this thread ("" if none). */
+const char* fk_last_error(void);
+
+/* RMSNorm without residual: out[r,:] = cast(x[r,:] * rsqrt(mean(x[r,:]^2) + eps)) * weight.
+ * x rows are `x_row_stride` elements apart, out rows `out_row_stride`; the
+ * hidden dimension is contiguous.  dtype is F32, F16 or BF16 for x/out/weight.
+ * Replaces fastkernels_norm::rmsnorm (rms_norm.py:51) / vLLM rms_norm (rms_norm.cu:1456). */
+int fk_rmsnorm(void* out, int64_t out_row_stride, const void* x, int64_t x_row_stride,
+               const void* weight, int64_t rows, int64_t hidden, float eps, int dtype,
+               void* stream);
+
+/* Fused residual add + RMSNorm, in place on both tensors:
+ *   residual[r,:] <- cast(x[r,:] + residual[r,:])            (sum formed in fp32)
+ *   x[r,:]        <- cast(cast(s * rsqrt(mean(s^2) + eps)) * weight),  s = fp32 sum
+ * Replaces fastkernels_norm::fused_add_rmsnorm (rms_norm.py:57-65) and vLLM
+ * fused_add_rms_norm (rms_norm.cu:1546-1598); numerics follow forward_native
+ * (rms_norm.py:97-118). */
+int fk_fused_add_rmsnorm(void* x, int64_t x_row_stride, void* residual,
+                         int64_t residual_row_stride, const void* weight, int64_t rows,
+                         int64_t hidden, float eps, int dtype, void* stream);
+
+/* Rotary embedding, in place on query and (optional, may be NULL) key.
+ * positions: int64 [tokens].  query rows `q_row_stride` elements apart, each row
+ * num_heads*head_size contiguous; same for key with num_kv_heads.
+ * cos_sin: [max_position, rot_dim] rows (first rot_dim/2 = cos, rest = sin) of
+ * dtype `cache_dtype` (F32 or the query dtype).  cos/sin are rounded to the query
+ * dtype before use, as the reference casts the cache (rotary_emb.py:171-173).
+ * is_neox != 0: pairs (i, i + rot_dim/2); else pairs (2i, 2i+1).
+ * Positions outside [0, max_position) leave that token unchanged.
+ * Replaces fastkernels_rope::rotary_embedding (rotary_emb.py:26-37). */
+int fk_rotary_embedding(const int64_t* positions, void* query, int64_t q_row_stride,
+                        void* key, int64_t k_row_stride, const void* cos_sin,
+                        int cache_dtype, int64_t max_position, int64_t tokens,
+                        int num_heads, int num_kv_heads, int head_size, int rot_dim,
+                        int is_neox, int dtype, void* stream);
+
+/* store_kvcache (NHD paged layout), a bit-exact scatter:
+ *   for i < tokens with s = slot_mapping[i] >= 0:
+ *     k_cache[s*row_elems : (s+1)*row_elems] = key[i*key_row_stride : +row_elems]
+ *     v_cache[...]                           = value[i*value_row_stride : +row_elems]
+ * row_elems = num_kv_heads*head_size, elem_bytes = bytes per element (1, 2 or 4).
+ * slot_mapping is int64 when slot_is_i64 != 0, else int32.  Slots >= num_slots
+ * (= num_blocks*block_size) are skipped like negative ones, so no write leaves
+ * the cache.  Replaces StoreKVCache.forward (store_kvcache.py:71-82). */
+int fk_store_kvcache(const void* key, int64_t key_row_stride, const void* value,
+                     int64_t value_row_stride, void* k_cache, void* v_cache,
+                     const void* slot_mapping, int slot_is_i64, int64_t tokens,
+                     int64_t row_elems, int elem_bytes, int64_t num_slots, void* stream);
+
+/* Bytes of split-context workspace fk_paged_decode needs for this launch shape.
+ * part_tokens: tokens per partition as returned by fk_paged_decode_plan. */
+int64_t fk_paged_decode_workspace_bytes(int64_t batch, int num_heads, int num_kv_heads,
+                                        int head_size, int64_t max_parts);
+
+/* Chooses the partition size (tokens per split-context work-group) for a
+ * launch: num_splits > 0 asks for that many partitions over max_seq_len;
+ * num_splits == 0 picks a size that fills the GPU.  Writes the partition size
+ * and the partition count per sequence.  Host-only arithmetic (no device call). */
+int fk_paged_decode_plan(int64_t batch, int num_kv_heads, int64_t max_seq_len,
+                         int num_splits, int64_t* part_tokens, int64_t* max_parts);
+
+/* Paged decode attention (one query token per sequence):
+ *   out[b,h,:] = softmax(scale * q[b,h,:] . K_b^T) V_b  over the first ctx_lens[b]
+ * tokens of sequence b, gathered through block_tables[b, :]; kv head = h / (Hq/Hk).
+ * q: [batch, num_heads, head_size] rows `q_row_stride` elements apart (head_size
+ *    contiguous, heads head_size apart); dtype BF16.
+ * k_cache, v_cache: [num_blocks, block_size, num_kv_heads, head_size] of kv_dtype
+ *    (BF16, or FP8_E4M3FN dequantised as float(x) * k_scale[kv_head] /
+ *    v_scale[kv_head]; scale pointers are device fp32 [num_kv_heads] or NULL = 1).
+ * block_tables: int32 [batch, bt_row_stride]; entries outside [0, num_blocks),
+ *    and pages past the row (index >= bt_row_stride), are masked (never read).  ctx_lens: int32 [batch]; 0 gives a zero output row.
+ * out: [batch, num_heads, head_size] BF16 rows `out_row_stride` elements apart.
+ * part_tokens / max_parts: from fk_paged_decode_plan with the same max_seq_len,
+ *    which must be >= every ctx_lens[b] (tokens past part_tokens*max_parts are
+ *    not attended).  workspace: device memory of
+ *    fk_paged_decode_workspace_bytes(...) bytes.
+ * Supported: head_size 128; Hq/Hk in 1..16; block_size a power of two >= 16.
+ * Replaces FlashAttnDecode.forward (flash_attn_decode.py:113-181). */
+int fk_paged_decode(void* out, int64_t out_row_stride, const void* q, int64_t q_row_stride,
+                    const void* k_cache, const void* v_cache, int kv_dtype,
+                    const float* k_scale, const float* v_scale, const int32_t* block_tables,
+                    int64_t bt_row_stride, const int32_t* ctx_lens, int64_t batch,
+                    int num_heads, int num_kv_heads, int head_size, int block_size,
+                    int64_t num_blocks, float scale, int64_t part_tokens, int64_t max_parts,
+                    void* workspace, int64_t workspace_bytes, void* stream);
+
+/* The two launches fk_paged_decode makes, exposed so a profiler or benchmark can
+ * time them separately.  Same arguments as fk_paged_decode; the reduce merges
+ * the partitions of every sequence with more than one (the partials launch
+ * writes single-partition sequences straight to `out`). */
+int fk_paged_decode_partials(void* out, int64_t out_row_stride, const void* q,
+                             int64_t q_row_stride, const void* k_cache, const void* v_cache,
+                             int kv_dtype, const float* k_scale, const float* v_scale,
+                             const int32_t* block_tables, int64_t bt_row_stride,
+                             const int32_t* ctx_lens, int64_t batch, int num_heads,
+                             int num_kv_heads, int head_size, int block_size,
+                             int64_t num_blocks, float scale, int64_t part_tokens,
+                             int64_t max_parts, void* workspace, int64_t workspace_bytes,
+                             void* stream);
+int fk_paged_decode_reduce(void* out, int64_t out_row_stride, const int32_t* ctx_lens, int64_t batch, int num_heads,
+                           int num_kv_heads, int head_size, int64_t part_tokens,
+                           int64_t max_parts, void* workspace, int64_t workspace_bytes,
+                           void* stream);
+
+/* SiLU-and-mul: out[r, j] = cast(cast(silu(x[r, j])) * x[r, d + j]) for j < d.
+ * x: [rows, 2d] rows `x_row_stride` elements apart; out: [rows, d] rows
+ * `out_row_stride` apart.  dtype F32, F16 or BF16.
+ * Replaces _C.silu_and_mul(out, x) (silu_and_mul.py:24-30, silu_and_mul.cu:951-956);
+ * the bf16-rounded activation matches forward_native (silu_and_mul.py:19-22). */
+int fk_silu_and_mul(void* out, int64_t out_row_stride, const void* x, int64_t x_row_stride,
+                    int64_t rows, int64_t d, int dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FASTKERNELS_AMD_H_ */

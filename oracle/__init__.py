@@ -1,0 +1,300 @@
+"""CPU oracle for the decode-step operator path (numpy restatement of the reference).
+
+TEST INFRASTRUCTURE ONLY.  Nothing in the product (``fastkernels_amd``) imports,
+links or calls this package.  Only ``tests/``, ``__graft_entry__.smoke()`` and
+``bench.py``'s ``cpu_baseline`` leg use it, and only as the checker (or as the
+CPU baseline being timed), never as an implementation of an op.
+
+Conventions: tensors are numpy arrays holding the *values* of the reference's
+tensors as float32 (every bf16 / fp16 value is exactly a float32), plus a dtype
+tag ("bf16", "f16", "f32") saying where the reference rounds.  ``round_to``
+performs that rounding (round-to-nearest-even, as torch does).  fp8 KV caches
+are uint8 arrays of OCP e4m3fn codes.
+
+Each function names the reference code it restates (paths relative to the
+Snowflake-AI-Research/fastkernels checkout).  How each is pinned (golden
+vectors, library routines, closed forms, invariants, brute force) is listed in
+tests/test_oracle.py; a function none of those pin would be marked
+"parity unpinned" here — none is.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+# ---------------------------------------------------------------------------
+# Number formats
+# ---------------------------------------------------------------------------
+
+
+def bf16_bits_to_f32(bits: np.ndarray) -> np.ndarray:
+    """bf16 bit patterns (uint16) -> float32 values (exact)."""
+    return (np.asarray(bits, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """float32 -> bf16 bit patterns, round-to-nearest-even; NaN -> 0x7fc0."""
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = (u + np.uint32(0x7FFF) + ((u >> 16) & np.uint32(1))) >> 16
+    r = np.where(nan, np.uint32(0x7FC0), r)
+    return r.astype(np.uint16)
+
+
+def round_to(x: np.ndarray, dtype: str) -> np.ndarray:
+    """Round float values to ``dtype`` and return them as float32."""
+    x = np.asarray(x, np.float32)
+    if dtype == "bf16":
+        return bf16_bits_to_f32(f32_to_bf16_bits(x))
+    if dtype == "f16":
+        return x.astype(np.float16).astype(np.float32)
+    if dtype == "f32":
+        return x
+    raise ValueError(f"unknown dtype {dtype}")
+
+
+def _e4m3fn_table() -> np.ndarray:
+    """Value of every OCP float8 e4m3fn code: 1 sign, 4 exponent (bias 7), 3 mantissa
+    bits; exponent 0 is subnormal (m/8 * 2^-6); code S.1111.111 is NaN; no infinities."""
+    t = np.empty(256, np.float32)
+    for c in range(256):
+        s = -1.0 if c & 0x80 else 1.0
+        e = (c >> 3) & 0xF
+        m = c & 0x7
+        if e == 0xF and m == 0x7:
+            t[c] = np.nan
+        elif e == 0:
+            t[c] = s * (m / 8.0) * 2.0 ** -6
+        else:
+            t[c] = s * (1.0 + m / 8.0) * 2.0 ** (e - 7)
+    return t
+
+
+E4M3FN_TABLE = _e4m3fn_table()
+E4M3FN_MAX = 448.0
+
+
+def fp8_e4m3fn_decode(codes: np.ndarray) -> np.ndarray:
+    return E4M3FN_TABLE[np.asarray(codes, np.uint8)]
+
+
+def fp8_e4m3fn_encode(x: np.ndarray) -> np.ndarray:
+    """Saturating round-to-nearest-even float -> e4m3fn code (|x| clamped to 448)."""
+    x = np.clip(np.asarray(x, np.float64), -E4M3FN_MAX, E4M3FN_MAX)
+    finite = E4M3FN_TABLE.astype(np.float64)
+    pos_codes = np.arange(0, 0x7F, dtype=np.int64)  # 0 .. 0x7E are the finite non-negatives
+    pos_vals = finite[pos_codes]
+    a = np.abs(x).ravel()
+    idx = np.searchsorted(pos_vals, a)  # pos_vals is increasing
+    idx = np.clip(idx, 1, len(pos_vals) - 1)
+    lo, hi = pos_vals[idx - 1], pos_vals[idx]
+    pick_hi = (a - lo > hi - a) | ((a - lo == hi - a) & ((pos_codes[idx] & 1) == 0))
+    code = np.where(pick_hi, pos_codes[idx], pos_codes[idx - 1])
+    code = np.where(a == 0, 0, code)
+    sign = (np.signbit(x).ravel()) & (code != 0)
+    return (code | (sign.astype(np.int64) << 7)).astype(np.uint8).reshape(np.shape(x))
+
+
+# ---------------------------------------------------------------------------
+# RMSNorm — RMSNorm.forward_native, fastkernels/tasks/baseline/L1/rms_norm.py:97-118
+# ---------------------------------------------------------------------------
+
+
+def rms_norm(x: np.ndarray, weight: np.ndarray, eps: float, dtype: str,
+             residual: np.ndarray | None = None):
+    """Returns ``out`` (no residual) or ``(out, new_residual)``.
+
+    xf = float(x) [+ float(residual)]; new_residual = cast(xf);
+    var = mean(xf^2); out = cast(cast(xf * rsqrt(var + eps)) * weight)."""
+    xf = np.asarray(x, np.float32)
+    if residual is not None:
+        xf = xf + np.asarray(residual, np.float32)
+        new_res = round_to(xf, dtype)
+    var = np.mean(xf.astype(np.float64) ** 2, axis=-1, keepdims=True)
+    inv = (1.0 / np.sqrt(var + eps)).astype(np.float32)
+    xh = round_to(xf * inv, dtype)
+    out = round_to(xh * np.asarray(weight, np.float32), dtype)
+    return out if residual is None else (out, new_res)
+
+
+# ---------------------------------------------------------------------------
+# Rotary — RotaryEmbedding, fastkernels/tasks/baseline/L1/rotary_emb.py:79-191
+# ---------------------------------------------------------------------------
+
+
+def rope_inv_freq(head_dim: int, theta: float) -> np.ndarray:
+    """inv_freq_i = 1 / theta^(2i/D) (rotary_emb.py:93), in float32 as torch forms it."""
+    exps = (np.arange(0, head_dim, 2, dtype=np.float32) / np.float32(head_dim)).astype(np.float32)
+    return (np.float32(1.0) / np.power(np.float32(theta), exps, dtype=np.float32)).astype(np.float32)
+
+
+def rope_cos_sin_cache(head_dim: int, max_pos: int, theta: float) -> np.ndarray:
+    """[max_pos, head_dim] float32: cos(t * inv_freq) then sin(t * inv_freq) (:104-107)."""
+    inv = rope_inv_freq(head_dim, theta)
+    ang = np.outer(np.arange(max_pos, dtype=np.float32), inv).astype(np.float32)
+    return np.concatenate([np.cos(ang), np.sin(ang)], axis=-1).astype(np.float32)
+
+
+def rotary(positions: np.ndarray, query: np.ndarray, key: np.ndarray | None, head_size: int,
+           cos_sin: np.ndarray, is_neox: bool, dtype: str):
+    """Rotated copies of query/key ([T, H*D] values).  cos/sin are cast to the query
+    dtype (rotary_emb.py:171-173); products and sums in fp32, one rounding."""
+    pos = np.asarray(positions, np.int64)
+    cs = round_to(np.asarray(cos_sin, np.float32)[pos], dtype)  # [T, rot]
+    rot = cs.shape[-1]
+    half = rot // 2
+    cos, sin = cs[:, None, :half], cs[:, None, half:]
+
+    def apply(x):
+        t = x.shape[0]
+        xh = np.asarray(x, np.float32).reshape(t, -1, head_size).copy()
+        if is_neox:
+            a, b = xh[..., :half].copy(), xh[..., half:rot].copy()
+            xh[..., :half] = a * cos - b * sin
+            xh[..., half:rot] = b * cos + a * sin
+        else:
+            a, b = xh[..., 0:rot:2].copy(), xh[..., 1:rot:2].copy()
+            xh[..., 0:rot:2] = a * cos - b * sin
+            xh[..., 1:rot:2] = b * cos + a * sin
+        return round_to(xh, dtype).reshape(x.shape)
+
+    return apply(query), (apply(key) if key is not None else None)
+
+
+# ---------------------------------------------------------------------------
+# store_kvcache — _store_kvcache_kernel, fastkernels/tasks/baseline/L1/store_kvcache.py:16-35
+# ---------------------------------------------------------------------------
+
+
+def store_kvcache(key: np.ndarray, value: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray,
+                  slot_mapping: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """Copies of the caches after the scatter.  Arrays may be any dtype (bit copy):
+    key/value [N, Hk, D]; caches [num_blocks, block_size, Hk, D]; slot < 0 skips."""
+    kc, vc = k_cache.copy(), v_cache.copy()
+    nb, bs = kc.shape[:2]
+    kflat = kc.reshape(nb * bs, -1)
+    vflat = vc.reshape(nb * bs, -1)
+    slots = np.asarray(slot_mapping, np.int64)
+    n = key.shape[0]
+    keep = slots[:n] >= 0
+    idx = slots[:n][keep]
+    kflat[idx] = key.reshape(n, -1)[keep]
+    vflat[idx] = value.reshape(n, -1)[keep]
+    return kc, vc
+
+
+# ---------------------------------------------------------------------------
+# Paged decode attention — Attention._decode_torch / _cache_seq / _sdpa_one /
+# _repeat_kv_for_heads, fastkernels/tasks/baseline/L2/attention_impl.py:592-664
+# ---------------------------------------------------------------------------
+
+
+def gather_seq(cache: np.ndarray, block_row: np.ndarray, length: int) -> np.ndarray:
+    """_cache_seq (attention_impl.py:598-604): the first `length` token rows of a sequence."""
+    bs = cache.shape[1]
+    pages = (length + bs - 1) // bs
+    ids = np.asarray(block_row[:pages], np.int64)
+    return cache[ids].reshape(-1, cache.shape[2], cache.shape[3])[:length]
+
+
+def dequant_kv(cache: np.ndarray, scale: np.ndarray | None, q_dtype: str) -> np.ndarray:
+    """fp8 per-(kv head) dequant: cast(float(x) * scale) to the query dtype
+    (_cast_kv_tile, triton_unified_attention.py:64-67).  Non-fp8 caches pass through."""
+    if cache.dtype != np.uint8:
+        return np.asarray(cache, np.float32)
+    v = fp8_e4m3fn_decode(cache)
+    if scale is not None:
+        v = v * np.asarray(scale, np.float32).reshape(1, 1, -1, 1)
+    return round_to(v, q_dtype)
+
+
+def attend_one(q: np.ndarray, k_seq: np.ndarray, v_seq: np.ndarray, scale: float) -> np.ndarray:
+    """softmax(scale * q k^T) v for one query token; GQA by head // (Hq/Hk)
+    (repeat_interleave, attention_impl.py:592-596).  float64; 0 rows when empty."""
+    hq, d = q.shape
+    n, hk, _ = k_seq.shape
+    if n == 0:
+        return np.zeros((hq, d), np.float64)
+    grp = hq // hk
+    qh = q.astype(np.float64).reshape(hk, grp, d)
+    k = k_seq.astype(np.float64).transpose(1, 2, 0)  # [Hk, D, n]
+    v = v_seq.astype(np.float64).transpose(1, 0, 2)  # [Hk, n, D]
+    s = np.matmul(qh, k) * scale  # [Hk, grp, n]
+    s -= s.max(axis=-1, keepdims=True)
+    p = np.exp(s)
+    p /= p.sum(axis=-1, keepdims=True)
+    return np.matmul(p, v).reshape(hq, d)
+
+
+def paged_decode(q: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray,
+                 block_tables: np.ndarray, ctx_lens: np.ndarray, scale: float,
+                 k_scale: np.ndarray | None = None, v_scale: np.ndarray | None = None,
+                 q_dtype: str = "bf16", seqs=None) -> np.ndarray:
+    """Decode attention output [B, Hq, D] (float64, unrounded) — `_decode_torch`.
+
+    q: [B, Hq, D] values; caches [num_blocks, block_size, Hk, D] values, or uint8
+    e4m3fn codes with per-kv-head scales.  ``seqs`` restricts the sequences
+    computed (others stay 0), for bounded CPU-baseline samples."""
+    b, hq, d = q.shape
+    out = np.zeros((b, hq, d), np.float64)
+    fp8 = k_cache.dtype == np.uint8
+    for i in (range(b) if seqs is None else seqs):
+        n = int(ctx_lens[i])
+        k_seq = gather_seq(k_cache, block_tables[i], n)
+        v_seq = gather_seq(v_cache, block_tables[i], n)
+        if fp8:
+            k_seq = dequant_kv(k_seq[None], k_scale, q_dtype)[0]
+            v_seq = dequant_kv(v_seq[None], v_scale, q_dtype)[0]
+        out[i] = attend_one(q[i], k_seq, v_seq, scale)
+    return out
+
+
+def attend_partials(q: np.ndarray, k_seq: np.ndarray, v_seq: np.ndarray, scale: float,
+                    part_tokens: int):
+    """Split-context partials of one sequence: per partition p the max m_p, the sum
+    l_p = sum exp(s - m_p), and the unnormalised o_p = sum exp(s - m_p) v
+    (the segment state of triton_unified_attention.py:815-1066)."""
+    hq, d = q.shape
+    n, hk, _ = k_seq.shape
+    grp = hq // hk
+    parts = []
+    for t0 in range(0, n, part_tokens):
+        ks, vs = k_seq[t0:t0 + part_tokens], v_seq[t0:t0 + part_tokens]
+        qh = q.astype(np.float64).reshape(hk, grp, d)
+        s = np.matmul(qh, ks.astype(np.float64).transpose(1, 2, 0)) * scale
+        m = s.max(axis=-1)
+        e = np.exp(s - m[..., None])
+        parts.append((m.reshape(hq), e.sum(-1).reshape(hq),
+                      np.matmul(e, vs.astype(np.float64).transpose(1, 0, 2)).reshape(hq, d)))
+    return parts
+
+
+def merge_partials(parts) -> np.ndarray:
+    """Log-sum-exp merge of reduce_segments (triton_unified_attention.py:741-776):
+    M = max m_p; L = sum l_p e^(m_p - M); O = sum o_p e^(m_p - M) / L; 0 if L == 0."""
+    if not parts:
+        return None
+    m = np.stack([p[0] for p in parts])
+    l = np.stack([p[1] for p in parts])
+    o = np.stack([p[2] for p in parts])
+    big_m = m.max(axis=0)
+    f = np.exp(m - big_m)
+    big_l = (l * f).sum(axis=0)
+    acc = (o * f[..., None]).sum(axis=0)
+    with np.errstate(invalid="ignore", divide="ignore"):
+        res = np.where(big_l[..., None] == 0, 0.0, acc / big_l[..., None])
+    return res
+
+
+# ---------------------------------------------------------------------------
+# SiLU-and-mul — SiluAndMul.forward_native, fastkernels/tasks/baseline/L1/silu_and_mul.py:19-22
+# ---------------------------------------------------------------------------
+
+
+def silu_and_mul(x: np.ndarray, dtype: str) -> np.ndarray:
+    """cast(cast(silu(g)) * u) with g = x[..., :d], u = x[..., d:] (F.silu in the tensor
+    dtype, then the product in the tensor dtype)."""
+    x = np.asarray(x, np.float32)
+    d = x.shape[-1] // 2
+    g = x[..., :d].astype(np.float64)
+    act = round_to((g / (1.0 + np.exp(-g))).astype(np.float32), dtype)
+    return round_to(act * x[..., d:], dtype)

@@ -1,0 +1,402 @@
+"""GPU parity: the gfx950 kernels (through the C ABI) against the CPU oracle.
+
+Bars: store_kvcache bit-exact; bf16 ops within atol=rtol=1e-2 of the oracle's
+fp32-upcast result (every element, stricter than the reference harness's 99%
+rule, fastkernels/bench.py:142-155); fp8-KV attention within atol=rtol=3e-2.
+Sizes are the benchmark configurations (C1-C5) where the oracle finishes in
+seconds, and small edge cases otherwise.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from fastkernels_amd import ops, workloads
+
+pytestmark = pytest.mark.gpu
+
+BF16_TOL = 1e-2
+FP8_TOL = 3e-2
+
+
+def f32(t: torch.Tensor) -> np.ndarray:
+    return t.detach().float().cpu().numpy()
+
+
+def assert_close(got, ref, atol, rtol, what=""):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    assert got.shape == ref.shape, f"{what}: shape {got.shape} != {ref.shape}"
+    assert np.isfinite(got).all(), f"{what}: non-finite output"
+    err = np.abs(got - ref)
+    bad = err > atol + rtol * np.abs(ref)
+    if bad.any():
+        i = np.unravel_index(np.argmax(err - (atol + rtol * np.abs(ref))), err.shape)
+        raise AssertionError(f"{what}: {int(bad.sum())}/{bad.size} outside atol={atol} rtol={rtol};"
+                             f" worst at {i}: got {got[i]} ref {ref[i]}; max abs {err.max():.3g}")
+
+
+def _flush(msg):
+    print(msg, flush=True)
+
+
+# ---------------------------------------------------------------------------
+# store_kvcache (bit-exact)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("slot_dtype", [torch.int64, torch.int32])
+def test_store_kvcache_c2_bitexact(cuda, slot_dtype):
+    _flush(f"store_kvcache C2 slot_dtype={slot_dtype}")
+    c = workloads.c2_store(cuda, slot_dtype=slot_dtype)
+    ops.store_kvcache(c.key, c.value, c.k_cache, c.v_cache, c.slot_mapping)
+    torch.cuda.synchronize()
+    as_u16 = lambda t: t.view(torch.int16).cpu().numpy()
+    kc0 = np.zeros(c.k_cache.shape, np.int16)
+    ek, ev = oracle.store_kvcache(as_u16(c.key), as_u16(c.value), kc0, kc0,
+                                  c.slot_mapping.cpu().numpy())
+    assert np.array_equal(as_u16(c.k_cache), ek)
+    assert np.array_equal(as_u16(c.v_cache), ev)
+
+
+def test_store_kvcache_strided_views_and_edges(cuda):
+    """key/value as strided views of a fused qkv row (attention_impl.py:319-325),
+    slots -1 and past the cache end skipped, empty input, int32 slots."""
+    g = torch.Generator().manual_seed(7)
+    n, hq, hk, d, nb, bs = 37, 4, 2, 128, 8, 16
+    qkv = torch.randn(n, (hq + 2 * hk) * d, generator=g).to(torch.bfloat16).to(cuda)
+    k = qkv[:, hq * d:(hq + hk) * d].view(n, hk, d)
+    v = qkv[:, (hq + hk) * d:].view(n, hk, d)
+    slots = torch.randperm(nb * bs, generator=g)[:n]
+    slots[::5] = -1
+    slots[3] = nb * bs + 11  # past the end: must be skipped, not written
+    kc = torch.zeros(nb, bs, hk, d, dtype=torch.bfloat16, device=cuda)
+    vc = torch.zeros_like(kc)
+    ops.store_kvcache(k, v, kc, vc, slots.to(torch.int32).to(cuda))
+    ops.store_kvcache(k[:0], v[:0], kc, vc, slots[:0].to(cuda))
+    torch.cuda.synchronize()
+    u16 = lambda t: t.contiguous().view(torch.int16).cpu().numpy()
+    sl = slots.numpy().copy()
+    sl[sl >= nb * bs] = -1
+    ek, ev = oracle.store_kvcache(u16(k), u16(v), np.zeros(kc.shape, np.int16),
+                                  np.zeros(kc.shape, np.int16), sl)
+    assert np.array_equal(u16(kc), ek) and np.array_equal(u16(vc), ev)
+
+
+@pytest.mark.parametrize("dtype,hk,d", [(torch.float8_e4m3fn, 8, 128), (torch.float32, 2, 64),
+                                        (torch.bfloat16, 3, 5)])
+def test_store_kvcache_dtypes(cuda, dtype, hk, d):
+    g = torch.Generator().manual_seed(11)
+    n, nb, bs = 50, 4, 32
+    key = torch.randn(n, hk, d, generator=g).to(dtype).to(cuda)
+    val = torch.randn(n, hk, d, generator=g).to(dtype).to(cuda)
+    slots = torch.randperm(nb * bs, generator=g)[:n].to(cuda)
+    kc = torch.zeros(nb, bs, hk, d, dtype=dtype, device=cuda)
+    vc = torch.zeros_like(kc)
+    ops.store_kvcache(key, val, kc, vc, slots)
+    torch.cuda.synchronize()
+    iv = torch.int8 if dtype.itemsize == 1 else (torch.int16 if dtype.itemsize == 2 else torch.int32)
+    raw = lambda t: t.view(iv).cpu().numpy()
+    ek, ev = oracle.store_kvcache(raw(key), raw(val), np.zeros(kc.shape, raw(kc).dtype),
+                                  np.zeros(kc.shape, raw(kc).dtype), slots.cpu().numpy())
+    assert np.array_equal(raw(kc), ek) and np.array_equal(raw(vc), ev)
+
+
+# ---------------------------------------------------------------------------
+# RMSNorm
+# ---------------------------------------------------------------------------
+_DT = {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: "f32"}
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("hidden", [1024, 4096])
+def test_fused_add_rmsnorm(cuda, dtype, hidden):
+    _flush(f"fused_add_rmsnorm {dtype} H={hidden}")
+    c = workloads.c1_norm(cuda, dtype=dtype, hidden=hidden)
+    x0, r0 = f32(c.x), f32(c.residual)
+    ref_out, ref_res = oracle.rms_norm(x0, f32(c.weight), c.eps, _DT[dtype], residual=r0)
+    x, r = c.x.clone(), c.residual.clone()
+    ops.fused_add_rms_norm(x, r, c.weight, c.eps)
+    torch.cuda.synchronize()
+    assert np.array_equal(f32(r), ref_res), "new residual must be bit-exact cast(x + r)"
+    tol = BF16_TOL if dtype != torch.float32 else 1e-5
+    assert_close(f32(x), ref_out, tol, tol if dtype != torch.float32 else 1e-3, "out")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("hidden", [64, 1024, 5120, 1001, 16384])
+def test_rmsnorm_plain(cuda, dtype, hidden):
+    c = workloads.c1_norm(cuda, dtype=dtype, tokens=33, hidden=hidden)
+    out = torch.empty_like(c.x)
+    ops.rms_norm(out, c.x, c.weight, c.eps)
+    torch.cuda.synchronize()
+    ref = oracle.rms_norm(f32(c.x), f32(c.weight), c.eps, _DT[dtype])
+    tol = (BF16_TOL, BF16_TOL) if dtype != torch.float32 else (1e-5, 1e-3)
+    assert_close(f32(out), ref, *tol, f"rmsnorm H={hidden}")
+
+
+def test_rmsnorm_strided_rows(cuda):
+    g = torch.Generator().manual_seed(3)
+    big = torch.randn(40, 3 * 512, generator=g).to(torch.bfloat16).to(cuda)
+    x = big[:, 512:1024]  # row stride 1536
+    res = torch.randn(40, 512, generator=g).to(torch.bfloat16).to(cuda)
+    w = (1 + 0.1 * torch.randn(512, generator=g)).to(torch.bfloat16).to(cuda)
+    ref_out, ref_res = oracle.rms_norm(f32(x), f32(w), 1e-6, "bf16", residual=f32(res))
+    before = big.clone()
+    ops.fused_add_rms_norm(x, res, w, 1e-6)
+    torch.cuda.synchronize()
+    assert np.array_equal(f32(res), ref_res)
+    assert_close(f32(x), ref_out, BF16_TOL, BF16_TOL)
+    assert torch.equal(big[:, :512], before[:, :512]) and torch.equal(big[:, 1024:], before[:, 1024:])
+
+
+# ---------------------------------------------------------------------------
+# Rotary
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("is_neox", [True, False])
+@pytest.mark.parametrize("cache_dtype", [torch.float32, torch.bfloat16])
+def test_rotary_c4(cuda, is_neox, cache_dtype):
+    """C4 dims: q [256, 32*128], k [256, 8*128] as strided views of qkv, theta 1e6."""
+    _flush(f"rotary neox={is_neox} cache={cache_dtype}")
+    t, hq, hk, d = 256, 32, 8, 128
+    g = torch.Generator().manual_seed(5)
+    qkv = torch.randn(t, (hq + 2 * hk) * d, generator=g).to(torch.bfloat16).to(cuda)
+    pos = torch.randint(0, 8192, (t,), generator=g).to(cuda)
+    cs_np = oracle.rope_cos_sin_cache(d, 8192, 1e6)
+    cache = torch.from_numpy(cs_np).to(cuda).to(cache_dtype)
+    q = qkv[:, :hq * d]
+    k = qkv[:, hq * d:(hq + hk) * d]
+    q0, k0, v0 = f32(q), f32(k), qkv[:, (hq + hk) * d:].clone()
+    ref_q, ref_k = oracle.rotary(pos.cpu().numpy(), q0, k0, d, f32(cache), is_neox, "bf16")
+    ops.rotary_embedding(pos, q, k, d, cache, is_neox)
+    torch.cuda.synchronize()
+    assert_close(f32(q), ref_q, BF16_TOL, BF16_TOL, "q")
+    assert_close(f32(k), ref_k, BF16_TOL, BF16_TOL, "k")
+    assert torch.equal(qkv[:, (hq + hk) * d:], v0), "v slice must be untouched"
+
+
+def test_rotary_partial_and_f32(cuda):
+    """rot_dim < head_size (scalar path), fp32 tensors, key=None, out-of-range position."""
+    t, h, d, rot = 9, 3, 64, 32
+    g = torch.Generator().manual_seed(9)
+    q = torch.randn(t, h * d, generator=g).to(cuda)
+    pos = torch.randint(0, 100, (t,), generator=g)
+    pos[4] = 100  # out of range: token left unchanged
+    cs = oracle.rope_cos_sin_cache(rot, 100, 1e4)
+    q0 = f32(q)
+    ref_q, _ = oracle.rotary(np.clip(pos.numpy(), 0, 99), q0, None, d, cs, True, "f32")
+    ref_q[4] = q0[4]
+    ops.rotary_embedding(pos.to(cuda), q, None, d, torch.from_numpy(cs).to(cuda), True)
+    torch.cuda.synchronize()
+    assert_close(f32(q), ref_q, 1e-5, 1e-4)
+
+
+# ---------------------------------------------------------------------------
+# SiLU-and-mul
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype,shape", [(torch.bfloat16, (256, 2 * 12288)),
+                                         (torch.bfloat16, (7, 2 * 1003)),
+                                         (torch.float16, (16, 2 * 4096)),
+                                         (torch.float32, (5, 2 * 512))])
+def test_silu_and_mul(cuda, dtype, shape):
+    g = torch.Generator().manual_seed(13)
+    x = (3 * torch.randn(*shape, generator=g)).to(dtype).to(cuda)
+    out = torch.empty(shape[0], shape[1] // 2, dtype=dtype, device=cuda)
+    ops.silu_and_mul(out, x)
+    torch.cuda.synchronize()
+    ref = oracle.silu_and_mul(f32(x), _DT[dtype])
+    tol = (BF16_TOL, BF16_TOL) if dtype != torch.float32 else (1e-5, 1e-4)
+    assert_close(f32(out), ref, *tol)
+
+
+# ---------------------------------------------------------------------------
+# Paged decode attention
+# ---------------------------------------------------------------------------
+def run_decode(case, num_splits=0, max_seq_len=None):
+    b, hq, d = case.q.shape
+    hk = case.k_cache.shape[2]
+    msl = case.max_seq_len if max_seq_len is None else max_seq_len
+    part, nparts = ops.paged_decode_plan(b, hk, msl, num_splits)
+    nbytes = ops.paged_decode_workspace_bytes(b, hq, hk, d, nparts)
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=case.q.device)
+    out = torch.full_like(case.q, float("nan"))
+    ops.paged_decode(out, case.q, case.k_cache, case.v_cache, case.block_tables, case.ctx_lens,
+                     case.scale, part, nparts, ws, case.k_scale, case.v_scale)
+    torch.cuda.synchronize()
+    return out
+
+
+def oracle_decode(case, seqs=None):
+    """Oracle on the pages the selected sequences use (host copies of those pages only)."""
+    b = case.q.shape[0]
+    seqs = list(range(b)) if seqs is None else list(seqs)
+    bs = case.k_cache.shape[1]
+    ctx = case.ctx_lens.cpu().numpy()
+    bt = case.block_tables.cpu().numpy()
+    fp8 = case.k_cache.dtype == torch.float8_e4m3fn
+    out = np.zeros(tuple(case.q.shape), np.float64)
+    q = f32(case.q)
+    for i in seqs:
+        n = int(ctx[i])
+        pages = (n + bs - 1) // bs
+        ids = torch.from_numpy(bt[i, :pages].astype(np.int64)).to(case.k_cache.device)
+        if fp8:
+            kp = case.k_cache[ids].view(torch.uint8).cpu().numpy()
+            vp = case.v_cache[ids].view(torch.uint8).cpu().numpy()
+        else:
+            kp = f32(case.k_cache[ids])
+            vp = f32(case.v_cache[ids])
+        local_bt = np.arange(pages)[None]
+        ks = None if case.k_scale is None else case.k_scale.cpu().numpy()
+        vs = None if case.v_scale is None else case.v_scale.cpu().numpy()
+        out[i] = oracle.paged_decode(q[i:i + 1], kp, vp, local_bt, np.array([n]), case.scale,
+                                     ks, vs)[0]
+    return out
+
+
+def test_paged_decode_c3_north_star(cuda):
+    """Full C3 launch (64 seqs, ctx U[512, 8192]); 16 sequences checked against the oracle
+    (shortest, longest and a spread), all 64 checked for finiteness."""
+    _flush("paged_decode C3")
+    case = workloads.c3_decode(cuda)
+    out = run_decode(case)
+    ctx = case.ctx_lens.cpu().numpy()
+    order = np.argsort(ctx)
+    seqs = sorted(set(order[np.linspace(0, len(ctx) - 1, 16).astype(int)].tolist()))
+    ref = oracle_decode(case, seqs)
+    got = f32(out)
+    assert np.isfinite(got).all()
+    assert_close(got[seqs], ref[seqs], BF16_TOL, BF16_TOL, "C3")
+
+
+@pytest.mark.parametrize("num_splits", [1, 3, 16, 64])
+def test_paged_decode_split_invariance(cuda, num_splits):
+    """Any partition count gives the unsplit result (the LSE merge is exact)."""
+    case = workloads.c3_decode(cuda, batch=6, num_heads=8, kv_heads=2, pool_blocks=64,
+                               ctx_lo=1, ctx_hi=2000, seed=21)
+    ref = oracle_decode(case)
+    assert_close(f32(run_decode(case, num_splits)), ref, BF16_TOL, BF16_TOL, f"splits={num_splits}")
+
+
+@pytest.mark.parametrize("hq,hk", [(8, 8), (16, 8), (32, 8), (64, 8), (16, 1), (32, 2)])
+@pytest.mark.parametrize("block_size", [16, 64, 256])
+def test_paged_decode_gqa_blocks(cuda, hq, hk, block_size):
+    ctx = [1, 15, 16, 17, 255, 256, 257, 1000]
+    pool = sum((n + block_size - 1) // block_size for n in ctx) + 5
+    case = workloads.c3_decode(cuda, num_heads=hq, kv_heads=hk, block_size=block_size,
+                               pool_blocks=pool, ctx_lens=ctx, seed=31 + hq + block_size)
+    assert_close(f32(run_decode(case)), oracle_decode(case), BF16_TOL, BF16_TOL,
+                 f"hq={hq} hk={hk} bs={block_size}")
+
+
+def test_paged_decode_padded_rows_and_masked_pages(cuda):
+    """ctx 0 rows (engine padding, engine.py:5405-5407) give zeros; a -1 page inside
+    the context is masked instead of read."""
+    ctx = [0, 300, 0, 70]
+    case = workloads.c3_decode(cuda, num_heads=8, kv_heads=2, block_size=64, pool_blocks=32,
+                               ctx_lens=ctx, seed=41)
+    out = f32(run_decode(case))
+    ref = oracle_decode(case)
+    assert np.array_equal(out[0], np.zeros_like(out[0])) and np.array_equal(out[2], 0 * out[2])
+    assert_close(out, ref, BF16_TOL, BF16_TOL)
+    # Mask page 1 of sequence 1: tokens 64..127 drop out of its softmax.
+    bt = case.block_tables.clone()
+    bt[1, 1] = -1
+    case.block_tables = bt
+    out2 = f32(run_decode(case))
+    q = f32(case.q)[1]
+    keep = np.r_[0:64, 128:300]
+    ids = case.block_tables[1, :5].cpu().numpy()
+    ids[1] = 0
+    kp = f32(case.k_cache[torch.from_numpy(ids.astype(np.int64)).to(cuda)]).reshape(-1, 2, 128)
+    vp = f32(case.v_cache[torch.from_numpy(ids.astype(np.int64)).to(cuda)]).reshape(-1, 2, 128)
+    ref1 = oracle.attend_one(q, kp[keep], vp[keep], case.scale)
+    assert_close(out2[1], ref1, BF16_TOL, BF16_TOL, "masked page")
+
+
+def test_paged_decode_fp8_small(cuda):
+    _flush("paged_decode fp8 small")
+    case = workloads.c5_fp8_decode(cuda, batch=3, ctx_lens=[5000, 8192, 333], seed=51)
+    ref = oracle_decode(case)
+    for splits in (0, 16):
+        assert_close(f32(run_decode(case, splits)), ref, FP8_TOL, FP8_TOL, f"fp8 splits={splits}")
+
+
+def test_paged_decode_fp8_c5(cuda):
+    """Full C5 launch (8 x 131072, fp8 KV): two sequences against the oracle; 16 vs 64
+    partitions agree on all eight."""
+    _flush("paged_decode C5 fp8")
+    case = workloads.c5_fp8_decode(cuda)
+    out16 = run_decode(case, 16)
+    out64 = run_decode(case, 64)
+    ref = oracle_decode(case, seqs=[0, 7])
+    got = f32(out64)
+    assert_close(got[[0, 7]], ref[[0, 7]], FP8_TOL, FP8_TOL, "C5 vs oracle")
+    assert_close(f32(out16), got, FP8_TOL, FP8_TOL, "C5 16 vs 64 partitions")
+
+
+# ---------------------------------------------------------------------------
+# Candidate classes (drop-in surface) and the C4 chain
+# ---------------------------------------------------------------------------
+def test_candidates_chain_c4(cuda):
+    """C4: add+RMSNorm -> rotary -> store_kvcache -> paged decode -> SiLU-and-mul through
+    the candidate classes, each against the oracle on the same inputs."""
+    _flush("chain C4")
+    from fastkernels_amd.candidate.L1.flash_attn_decode import FlashAttnDecode
+    from fastkernels_amd.candidate.L1.rms_norm import RMSNorm
+    from fastkernels_amd.candidate.L1.rotary_emb import RotaryEmbedding
+    from fastkernels_amd.candidate.L1.silu_and_mul import SiluAndMul
+    from fastkernels_amd.candidate.L1.store_kvcache import StoreKVCache
+
+    c = workloads.c4_chain(cuda)
+    t, hq, hk, d = 256, 32, 8, 128
+    norm = RMSNorm(4096).to(cuda)
+    norm.weight.data.copy_(c.norm_weight.float())
+    h0, r0 = f32(c.hidden), f32(c.residual)
+    hn, rn = norm(c.hidden.clone(), c.residual.clone())
+    ref_h, ref_r = oracle.rms_norm(h0, f32(c.norm_weight), 1e-6, "bf16", residual=r0)
+    assert np.array_equal(f32(rn), ref_r)
+    assert_close(f32(hn), ref_h, BF16_TOL, BF16_TOL, "norm")
+
+    rope = RotaryEmbedding(d, c.max_position, c.rope_theta).to(cuda)
+    qkv = c.qkv.clone()
+    q, k, v = qkv[:, :hq * d], qkv[:, hq * d:(hq + hk) * d], qkv[:, (hq + hk) * d:]
+    ref_q, ref_k = oracle.rotary(c.positions.cpu().numpy(), f32(q), f32(k), d,
+                                 f32(rope.cos_sin_cache), True, "bf16")
+    rope(c.positions, q, k)
+    assert_close(f32(q), ref_q, BF16_TOL, BF16_TOL, "rope q")
+    assert_close(f32(k), ref_k, BF16_TOL, BF16_TOL, "rope k")
+
+    dec = c.decode
+    StoreKVCache()(k.view(t, hk, d), v.view(t, hk, d), dec.k_cache, dec.v_cache, c.slot_mapping)
+    torch.cuda.synchronize()
+    rows = c.slot_mapping.cpu()
+    kflat = dec.k_cache.view(-1, hk * d)
+    assert torch.equal(kflat[rows.to(cuda)].view(torch.int16), k.contiguous().view(torch.int16))
+
+    attn = FlashAttnDecode(hq, hk, d, page_size=256)
+    o = attn(q.view(t, hq, d), dec.k_cache, dec.v_cache, cache_seqlens=dec.ctx_lens,
+             block_table=dec.block_tables, softmax_scale=dec.scale, causal=True,
+             max_seq_len=dec.max_seq_len)
+    dec.q = q.view(t, hq, d)
+    seqs = list(range(0, t, 17))
+    ref_o = oracle_decode(dec, seqs)
+    assert_close(f32(o)[seqs], ref_o[seqs], BF16_TOL, BF16_TOL, "decode")
+
+    act = SiluAndMul()(c.gate_up)
+    assert_close(f32(act), oracle.silu_and_mul(f32(c.gate_up), "bf16"), BF16_TOL, BF16_TOL, "silu")
+
+
+def test_flash_attn_decode_defaults_no_sync(cuda):
+    """max_seq_len omitted: bound from the block table width, no host sync needed."""
+    from fastkernels_amd.candidate.L1.flash_attn_decode import FlashAttnDecode
+
+    case = workloads.c3_decode(cuda, batch=5, num_heads=16, kv_heads=4, pool_blocks=64,
+                               ctx_lo=10, ctx_hi=3000, seed=61)
+    attn = FlashAttnDecode(16, 4, 128)
+    o = attn(case.q, case.k_cache, case.v_cache, cache_seqlens=case.ctx_lens,
+             block_table=case.block_tables)
+    assert_close(f32(o), oracle_decode(case), BF16_TOL, BF16_TOL)
+    assert math.isclose(case.scale, 1 / math.sqrt(128))
