@@ -90,7 +90,7 @@ def fp8_e4m3fn_encode(x: np.ndarray) -> np.ndarray:
     pick_hi = (a - lo > hi - a) | ((a - lo == hi - a) & ((pos_codes[idx] & 1) == 0))
     code = np.where(pick_hi, pos_codes[idx], pos_codes[idx - 1])
     code = np.where(a == 0, 0, code)
-    sign = (np.signbit(x).ravel()) & (code != 0)
+    sign = np.signbit(x).ravel()  # negative values that round to 0 give -0 (0x80)
     return (code | (sign.astype(np.int64) << 7)).astype(np.uint8).reshape(np.shape(x))
 
 

@@ -1,0 +1,334 @@
+"""Pins the CPU oracle (``oracle/``) before it is trusted as the checker.
+
+The reference holds no golden vectors for this path (its tests pin harness
+behaviour only), so each oracle function is pinned by checks independent of
+its own formula:
+  number formats   exhaustive / randomized agreement with torch's bf16, fp16 and
+                   float8_e4m3fn conversions (library routines);
+  rms_norm         torch.nn.functional.rms_norm (library), a closed-form scale
+                   invariance, the bit-exact residual rule, eps-dominated rows;
+  rotary           hand-computed known-answer vectors for both pairings, the
+                   cos/sin cache against float64 math, norm preservation, the
+                   relative-position property, position 0 = identity;
+  store_kvcache    a brute-force per-slot loop and the untouched-slot invariant;
+  paged decode     torch scaled_dot_product_attention in float64 (library) with
+                   repeat_interleave GQA, closed forms (uniform scores -> mean of V,
+                   one dominant key -> its V row, empty -> 0), page-permutation
+                   invariance, split-context merge == unsplit;
+  silu_and_mul     torch.nn.functional.silu (library) with the reference's
+                   rounding points.
+Planted-mistake tests show the checks reject plausible slips (wrong GQA head
+mapping, dropped eps, swapped rotary pairing, a wrong sign).
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle
+
+RNG = np.random.default_rng(1234)
+
+
+# ---------------------------------------------------------------------------
+# Number formats
+# ---------------------------------------------------------------------------
+def test_bf16_decode_exhaustive():
+    bits = np.arange(65536, dtype=np.uint16)
+    ours = oracle.bf16_bits_to_f32(bits)
+    theirs = torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).float().numpy()
+    same = (ours.view(np.uint32) == theirs.view(np.uint32)) | (np.isnan(ours) & np.isnan(theirs))
+    assert same.all()
+
+
+def test_bf16_round_matches_torch():
+    x = np.concatenate([
+        RNG.standard_normal(200_000).astype(np.float32) * 10.0 ** RNG.integers(-30, 30, 200_000),
+        np.array([0.0, -0.0, np.inf, -np.inf, 1e-40, -1e-40, 3.4e38, 1.0 + 2 ** -8,
+                  1.0 + 3 * 2 ** -8, 1.0 + 2 ** -9], np.float32),
+        # exact ties at several exponents
+        (np.arange(1, 2000, dtype=np.float32) * 2.0 ** -8 + 1.0).astype(np.float32),
+    ]).astype(np.float32)
+    ours = oracle.f32_to_bf16_bits(x)
+    theirs = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(ours, theirs)
+    assert oracle.f32_to_bf16_bits(np.array([np.nan], np.float32))[0] == 0x7FC0
+
+
+def test_f16_round_matches_torch():
+    x = (RNG.standard_normal(100_000) * 100).astype(np.float32)
+    theirs = torch.from_numpy(x).half().float().numpy()
+    assert np.array_equal(oracle.round_to(x, "f16"), theirs)
+
+
+def test_e4m3fn_table_matches_torch_all_codes():
+    codes = np.arange(256, dtype=np.uint8)
+    theirs = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy()
+    ours = oracle.fp8_e4m3fn_decode(codes)
+    assert np.array_equal(np.isnan(ours), np.isnan(theirs))
+    ok = ~np.isnan(ours)
+    assert np.array_equal(ours[ok], theirs[ok])
+    assert np.nanmax(ours) == 448.0 and np.isnan(ours[0x7F]) and np.isnan(ours[0xFF])
+    assert ours[0x01] == 2.0 ** -9 and ours[0x08] == 2.0 ** -6  # smallest subnormal / normal
+
+
+def test_e4m3fn_encode_matches_torch():
+    x = np.concatenate([RNG.standard_normal(100_000) * 30, RNG.standard_normal(1000) * 1e-3,
+                        [0.0, 447.0, 448.0, 464.0, 1e6, -1e6, 2.0 ** -10, 2.0 ** -9 * 1.5]])
+    xc = np.clip(x, -448, 448).astype(np.float32)
+    theirs = torch.from_numpy(xc).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    ours = oracle.fp8_e4m3fn_encode(x)
+    assert np.array_equal(ours, theirs)
+
+
+# ---------------------------------------------------------------------------
+# RMSNorm
+# ---------------------------------------------------------------------------
+def _norm_inputs(t=16, h=256, scale=1.0):
+    x = (RNG.standard_normal((t, h)) * scale).astype(np.float32)
+    r = (RNG.standard_normal((t, h)) * scale).astype(np.float32)
+    w = (1 + 0.1 * RNG.standard_normal(h)).astype(np.float32)
+    return x, r, w
+
+
+def test_rms_norm_f32_matches_torch_rms_norm():
+    x, r, w = _norm_inputs()
+    ours = oracle.rms_norm(x, w, 1e-6, "f32")
+    theirs = F.rms_norm(torch.from_numpy(x), (x.shape[-1],), torch.from_numpy(w), eps=1e-6)
+    np.testing.assert_allclose(ours, theirs.numpy(), rtol=2e-6, atol=2e-6)
+    # Fused form: the norm of the fp32 sum.
+    ours_f, res = oracle.rms_norm(x, w, 1e-6, "f32", residual=r)
+    theirs_f = F.rms_norm(torch.from_numpy(x + r), (x.shape[-1],), torch.from_numpy(w), eps=1e-6)
+    np.testing.assert_allclose(ours_f, theirs_f.numpy(), rtol=2e-6, atol=2e-6)
+    assert np.array_equal(res, x + r)
+
+
+def test_rms_norm_eps_dominated_rows():
+    """Tiny rows where eps dominates the variance: catches a dropped or misplaced eps."""
+    x, _, w = _norm_inputs(scale=1e-4)
+    ours = oracle.rms_norm(x, w, 1e-6, "f32")
+    theirs = F.rms_norm(torch.from_numpy(x), (x.shape[-1],), torch.from_numpy(w), eps=1e-6).numpy()
+    np.testing.assert_allclose(ours, theirs, rtol=1e-5, atol=1e-9)
+    no_eps = oracle.rms_norm(x, w, 0.0, "f32")
+    assert not np.allclose(no_eps, theirs, rtol=1e-3), "planted mistake (eps dropped) not caught"
+
+
+def test_rms_norm_bf16_residual_and_scale_invariance():
+    x, r, w = _norm_inputs()
+    xb, rb, wb = (oracle.round_to(a, "bf16") for a in (x, r, w))
+    out, res = oracle.rms_norm(xb, wb, 1e-6, "bf16", residual=rb)
+    # new residual == bf16(x + r): torch's bf16 add (fp32 sum, one rounding).
+    t = (torch.from_numpy(xb).bfloat16() + torch.from_numpy(rb).bfloat16()).float().numpy()
+    assert np.array_equal(res, t)
+    # Closed form: with eps = 0, scaling x by 4 (exact in fp32, sqrt(16 v) = 4 sqrt(v))
+    # leaves the output bit-identical.
+    a = oracle.rms_norm(xb, wb, 0.0, "bf16")
+    b = oracle.rms_norm(xb * 4, wb, 0.0, "bf16")
+    assert np.array_equal(a, b)
+    # Output matches torch's forward_native op sequence in bf16 to one bf16 ulp.
+    xt = torch.from_numpy(xb).bfloat16().float()
+    ref = (xt * torch.rsqrt(xt.pow(2).mean(-1, keepdim=True) + 1e-6)).bfloat16() * \
+        torch.from_numpy(wb).bfloat16()
+    np.testing.assert_allclose(oracle.rms_norm(xb, wb, 1e-6, "bf16"), ref.float().numpy(),
+                               rtol=8e-3, atol=1e-6)
+
+
+# ---------------------------------------------------------------------------
+# Rotary
+# ---------------------------------------------------------------------------
+def test_rotary_known_answers():
+    """head_dim 4, theta 10000: inv_freq = [1, 0.01].  x = e0 at position 1:
+    NeoX pairs (0,2),(1,3) -> [cos 1, 0, sin 1, 0]; GPT-J pairs (0,1),(2,3) -> [cos 1, sin 1, 0, 0]."""
+    cs = oracle.rope_cos_sin_cache(4, 2, 10000.0)
+    np.testing.assert_allclose(cs[1], [math.cos(1), math.cos(0.01), math.sin(1), math.sin(0.01)],
+                               rtol=1e-6)
+    x = np.array([[1.0, 0.0, 0.0, 0.0]], np.float32)
+    neox, _ = oracle.rotary(np.array([1]), x, None, 4, cs, True, "f32")
+    gptj, _ = oracle.rotary(np.array([1]), x, None, 4, cs, False, "f32")
+    np.testing.assert_allclose(neox[0], [math.cos(1), 0, math.sin(1), 0], atol=1e-6)
+    np.testing.assert_allclose(gptj[0], [math.cos(1), math.sin(1), 0, 0], atol=1e-6)
+    y = np.array([[0.0, 0.0, 1.0, 0.0]], np.float32)  # second half: -sin lands in slot 0
+    neox_y, _ = oracle.rotary(np.array([1]), y, None, 4, cs, True, "f32")
+    np.testing.assert_allclose(neox_y[0], [-math.sin(1), 0, math.cos(1), 0], atol=1e-6)
+
+
+def test_rotary_cache_vs_float64_math():
+    d, theta = 128, 1e6
+    cs = oracle.rope_cos_sin_cache(d, 4097, theta)
+    inv = 1.0 / theta ** (np.arange(0, d, 2) / d)
+    ang = np.outer(np.arange(4097), inv)
+    # float32 angles: error grows with |angle| ~ position * 1e-7 relative.
+    np.testing.assert_allclose(cs[:, :d // 2], np.cos(ang), atol=2e-3)
+    np.testing.assert_allclose(cs[:, d // 2:], np.sin(ang), atol=2e-3)
+    np.testing.assert_allclose(cs[:64, :d // 2], np.cos(ang[:64]), atol=1e-5)
+
+
+@pytest.mark.parametrize("neox", [True, False])
+def test_rotary_invariants(neox):
+    d, t = 64, 32
+    cs = oracle.rope_cos_sin_cache(d, 512, 10000.0)
+    q = RNG.standard_normal((t, 2 * d)).astype(np.float32)
+    k = RNG.standard_normal((t, d)).astype(np.float32)
+    pos = RNG.integers(0, 400, t)
+    rq, rk = oracle.rotary(pos, q, k, d, cs, neox, "f32")
+    # norm preservation per head
+    np.testing.assert_allclose(np.linalg.norm(rq.reshape(t, 2, d), axis=-1),
+                               np.linalg.norm(q.reshape(t, 2, d), axis=-1), rtol=1e-5)
+    # position 0 is the identity
+    r0, _ = oracle.rotary(np.zeros(t, np.int64), q, None, d, cs, neox, "f32")
+    assert np.array_equal(r0, q)
+    # relative position: <rot(q, p), rot(k, p')> depends on p - p' only
+    qa, ka = oracle.rotary(pos, q[:, :d], k, d, cs, neox, "f32")
+    qb, kb = oracle.rotary(pos + 50, q[:, :d], k, d, cs, neox, "f32")
+    sa = np.einsum("td,sd->ts", qa, ka)
+    sb = np.einsum("td,sd->ts", qb, kb)
+    np.testing.assert_allclose(sa, sb, atol=2e-4)
+    # planted mistake: "x*c + y*s" in the first output is not a rotation; the
+    # norm-preservation check above rejects it.
+    half = d // 2
+    c_, s_ = cs[pos][:, None, :half], cs[pos][:, None, half:]
+    x1, x2 = q.reshape(t, 2, d)[..., :half], q.reshape(t, 2, d)[..., half:]
+    mutant = np.concatenate([x1 * c_ + x2 * s_, x2 * c_ + x1 * s_], -1)
+    assert not np.allclose(np.linalg.norm(mutant, axis=-1),
+                           np.linalg.norm(q.reshape(t, 2, d), axis=-1), rtol=1e-3)
+
+
+# ---------------------------------------------------------------------------
+# store_kvcache
+# ---------------------------------------------------------------------------
+def test_store_kvcache_vs_loop():
+    nb, bs, hk, d, n = 6, 8, 2, 4, 20
+    key = RNG.integers(-30000, 30000, (n, hk, d)).astype(np.int16)
+    val = RNG.integers(-30000, 30000, (n, hk, d)).astype(np.int16)
+    kc = RNG.integers(-5, 5, (nb, bs, hk, d)).astype(np.int16)
+    vc = kc.copy()
+    slots = RNG.permutation(nb * bs)[:n]
+    slots[[1, 7, 11]] = -1
+    ek, ev = oracle.store_kvcache(key, val, kc, vc, slots)
+    bk, bv = kc.copy(), vc.copy()
+    for i, s in enumerate(slots):
+        if s < 0:
+            continue
+        bk[s // bs, s % bs] = key[i]
+        bv[s // bs, s % bs] = val[i]
+    assert np.array_equal(ek, bk) and np.array_equal(ev, bv)
+    untouched = np.setdiff1d(np.arange(nb * bs), slots[slots >= 0])
+    assert np.array_equal(ek.reshape(nb * bs, -1)[untouched], kc.reshape(nb * bs, -1)[untouched])
+
+
+# ---------------------------------------------------------------------------
+# Paged decode attention
+# ---------------------------------------------------------------------------
+def _decode_case(b=4, hq=8, hk=2, d=16, bs=4, nb=64, seed=0, lens=None):
+    r = np.random.default_rng(seed)
+    lens = np.array(lens if lens is not None else r.integers(1, 40, b))
+    b = len(lens)
+    q = r.standard_normal((b, hq, d)).astype(np.float32)
+    kc = r.standard_normal((nb, bs, hk, d)).astype(np.float32)
+    vc = r.standard_normal((nb, bs, hk, d)).astype(np.float32)
+    perm = r.permutation(nb)
+    width = int(max(1, max((n + bs - 1) // bs for n in lens)))
+    bt = -np.ones((b, width), np.int32)
+    off = 0
+    for i, n in enumerate(lens):
+        p = (n + bs - 1) // bs
+        bt[i, :p] = perm[off:off + p]
+        off += p
+    return q, kc, vc, bt, lens.astype(np.int32)
+
+
+def _sdpa_ref(q, kc, vc, bt, lens, scale, head_of):
+    out = np.zeros(q.shape, np.float64)
+    for i in range(q.shape[0]):
+        n = int(lens[i])
+        ks = torch.from_numpy(oracle.gather_seq(kc, bt[i], n)).double()
+        vs = torch.from_numpy(oracle.gather_seq(vc, bt[i], n)).double()
+        hq = q.shape[1]
+        idx = torch.tensor([head_of(h) for h in range(hq)])
+        kh = ks[:, idx].transpose(0, 1).contiguous()  # [Hq, n, D]
+        vh = vs[:, idx].transpose(0, 1).contiguous()
+        qh = torch.from_numpy(q[i]).double()[:, None, :]
+        out[i] = F.scaled_dot_product_attention(qh, kh, vh, scale=scale)[:, 0].numpy()
+    return out
+
+
+def test_paged_decode_vs_torch_sdpa():
+    q, kc, vc, bt, lens = _decode_case()
+    scale = 1 / math.sqrt(16)
+    grp = q.shape[1] // kc.shape[2]
+    ours = oracle.paged_decode(q, kc, vc, bt, lens, scale)
+    ref = _sdpa_ref(q, kc, vc, bt, lens, scale, lambda h: h // grp)  # repeat_interleave
+    np.testing.assert_allclose(ours, ref, rtol=1e-10, atol=1e-12)
+    # planted mistake: GQA head h -> kv head h % Hk is caught by the same check
+    wrong = _sdpa_ref(q, kc, vc, bt, lens, scale, lambda h: h % kc.shape[2])
+    assert not np.allclose(ours, wrong, atol=1e-3), "planted mistake (GQA mapping) not caught"
+
+
+def test_paged_decode_closed_forms():
+    q, kc, vc, bt, lens = _decode_case(lens=[0, 5, 13])
+    out = oracle.paged_decode(q, kc, vc, bt, lens, 0.25)
+    assert np.array_equal(out[0], np.zeros_like(out[0]))  # empty context -> 0
+    # uniform scores (q = 0) -> the mean of the visible V rows
+    q0 = np.zeros_like(q)
+    out0 = oracle.paged_decode(q0, kc, vc, bt, lens, 0.25)
+    for i in (1, 2):
+        vs = oracle.gather_seq(vc, bt[i], int(lens[i])).astype(np.float64)
+        np.testing.assert_allclose(out0[i], np.repeat(vs.mean(0), 4, axis=0), atol=1e-12)
+    # one dominant key -> its V row: q of every head points at token 3's key of its kv head
+    i, tgt, bs, grp = 2, 3, kc.shape[1], q.shape[1] // kc.shape[2]
+    page, slot = bt[i, tgt // bs], tgt % bs
+    qd = q.copy()
+    for h in range(q.shape[1]):
+        kt = kc[page, slot, h // grp].astype(np.float64)
+        qd[i, h] = 200.0 * kt / (kt @ kt)
+    outd = oracle.paged_decode(qd, kc, vc, bt, lens, 1.0)
+    np.testing.assert_allclose(outd[i], np.repeat(vc[page, slot], grp, axis=0), atol=1e-6)
+
+
+def test_paged_decode_page_permutation_invariance():
+    q, kc, vc, bt, lens = _decode_case(seed=3)
+    base = oracle.paged_decode(q, kc, vc, bt, lens, 0.3)
+    perm = np.random.default_rng(9).permutation(kc.shape[0])  # page p moves to perm[p]
+    kc2, vc2 = np.empty_like(kc), np.empty_like(vc)
+    kc2[perm], vc2[perm] = kc, vc
+    bt2 = np.where(bt >= 0, perm[np.maximum(bt, 0)], -1).astype(np.int32)
+    np.testing.assert_allclose(oracle.paged_decode(q, kc2, vc2, bt2, lens, 0.3), base, atol=0)
+
+
+@pytest.mark.parametrize("part", [1, 3, 4, 16, 1000])
+def test_split_merge_equals_unsplit(part):
+    q, kc, vc, bt, lens = _decode_case(seed=4, lens=[37])
+    k = oracle.gather_seq(kc, bt[0], 37)
+    v = oracle.gather_seq(vc, bt[0], 37)
+    whole = oracle.attend_one(q[0], k, v, 0.3)
+    merged = oracle.merge_partials(oracle.attend_partials(q[0], k, v, 0.3, part))
+    np.testing.assert_allclose(merged, whole, rtol=1e-12, atol=1e-13)
+
+
+def test_fp8_dequant_matches_torch():
+    codes = RNG.integers(0, 256, (3, 4, 2, 8)).astype(np.uint8)
+    codes[(codes & 0x7F) == 0x7F] = 0  # no NaN codes
+    scale = np.array([0.05, 0.02], np.float32)
+    ours = oracle.dequant_kv(codes, scale, "bf16")
+    t = torch.from_numpy(codes).view(torch.float8_e4m3fn).float() * torch.from_numpy(scale).view(1, 1, 2, 1)
+    assert np.array_equal(ours, t.bfloat16().float().numpy())
+
+
+# ---------------------------------------------------------------------------
+# SiLU-and-mul
+# ---------------------------------------------------------------------------
+def test_silu_and_mul_matches_torch():
+    x = oracle.round_to((RNG.standard_normal((64, 2 * 96)) * 4).astype(np.float32), "bf16")
+    xt = torch.from_numpy(x).bfloat16()
+    ref = (F.silu(xt[:, :96]) * xt[:, 96:]).float().numpy()  # forward_native in bf16
+    ours = oracle.silu_and_mul(x, "bf16")
+    diff = np.abs(ours - ref)
+    assert (diff <= 1e-2 * np.abs(ref) + 1e-6).all()
+    assert (ours == ref).mean() > 0.99  # same rounding points: nearly all bit-identical
+    np.testing.assert_allclose(oracle.silu_and_mul(np.array([[0.0, 3.0]], np.float32), "f32"), [[0.0]])
+    big = oracle.silu_and_mul(np.array([[30.0, 2.0]], np.float32), "f32")
+    np.testing.assert_allclose(big, [[60.0]], rtol=1e-6)  # silu(x) -> x for large x
