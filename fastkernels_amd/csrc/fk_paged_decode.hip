@@ -45,6 +45,7 @@ namespace {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef short short4_t __attribute__((ext_vector_type(4)));
 typedef float floatx4_t __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kHead = 128;
 constexpr int kTile = 16;
@@ -73,6 +74,23 @@ struct DecodeParams {
   float* part_o;     // [B][Hk][max_parts][gqa][128] unnormalised partial outputs
   float* part_ml;    // [B][Hk][max_parts][gqa][2]   (max, sum) in the log2 domain
 };
+
+// Reductions over the four 16-lane rows of a wave (lanes r, r+16, r+32, r+48)
+// with the gfx950 row-swap permutes (VALU, no LDS traffic): each swap returns
+// a lane's own value and its partner row's value in some order, so combining
+// the two outputs symmetrically reduces each row pair.
+__device__ __forceinline__ float pair_max(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto c = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(c[0]), __uint_as_float(c[1]));
+}
+__device__ __forceinline__ float pair_sum(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto c = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(c[0]) + __uint_as_float(c[1]);
+}
 
 __device__ __forceinline__ uint32_t lo_pair(uint32_t a, uint32_t b) {
   return (a & 0xffffu) | (b << 16);
@@ -118,14 +136,14 @@ __device__ __forceinline__ int64_t page_of(const DecodeParams& P, int b, int tok
   return (page >= 0 && page < P.num_blocks) ? page : -1;
 }
 
+// Issues the loads of one tile from page `page` (>= 0, < num_blocks).  Loads
+// are unconditional so that every pipeline stage has the same number of loads
+// in flight and the compiler can wait for one stage with vmcnt(N) instead of
+// draining the queue; masked pages and tiles past the end load a safe page and
+// are discarded by the consumer.
 template <bool kFp8>
-__device__ __forceinline__ void load_tile(const DecodeParams& P, int b, int h, int tok0, int r,
-                                          int g, TileRegs<kFp8>& t) {
-  const int64_t page = page_of(P, b, tok0);
-  if (page < 0) {  // masked page: nothing is read
-    t = TileRegs<kFp8>{};
-    return;
-  }
+__device__ __forceinline__ void load_tile(const DecodeParams& P, int64_t page, int h, int tok0,
+                                          int r, int g, TileRegs<kFp8>& t) {
   const int bs_mask = (1 << P.block_size_log2) - 1;
   const int64_t slot0 = (page << P.block_size_log2) + (tok0 & bs_mask);
   constexpr int kElem = kFp8 ? 1 : 2;
@@ -174,10 +192,32 @@ __device__ __forceinline__ uint4 v_row(const TileRegs<true>& t, int i) {
   return make_uint4(lo.x, lo.y, hi.x, hi.y);
 }
 
-template <int NW, int kG, bool kFp8>
-__global__ __launch_bounds__(NW * 64) void paged_decode_partials_kernel(DecodeParams P) {
+// Value of `x` held by lane 4g + i (g = this lane's row group), for the O
+// row 4g + i this lane accumulates.  Rows >= kG are padding and get lane i's.
+template <int kG>
+__device__ __forceinline__ float row_value(float x, int g, int i) {
+  float a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__float_as_int(x), i));
+  if constexpr (kG > 4) {
+    const float a1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__float_as_int(x), 4 + i));
+    if constexpr (kG > 8) {
+      const float a2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__float_as_int(x), 8 + i));
+      const float a3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__float_as_int(x), 12 + i));
+      a = g == 0 ? a : g == 1 ? a1 : g == 2 ? a2 : a3;
+    } else {
+      a = g == 1 ? a1 : a;
+    }
+  }
+  return a;
+}
+
+// One work-group per (partition p, kv-head group, sequence b); wave w owns kv
+// head h = blockIdx.y * NH + w and streams every tile of the partition.  The
+// NH waves of a group walk the same token rows together, so the NHD rows
+// (Hk * 256 contiguous bytes per token) are read whole within a short window.
+// Each wave loads U tiles (U * 8 KiB for bf16) before consuming them in order.
+template <int NH, int kG, bool kFp8, int U>
+__global__ __launch_bounds__(NH * 64) void paged_decode_partials_kernel(DecodeParams P) {
   const int p = blockIdx.x;
-  const int h = blockIdx.y;
   const int b = blockIdx.z;
   const int ctx = P.ctx_lens[b];
   const int tok_begin = p * P.part_tokens;
@@ -188,7 +228,10 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_partials_kernel(DecodePa
   // the grid and the reduce kernel.
   const int nparts = min((ctx + P.part_tokens - 1) / P.part_tokens, P.max_parts);
 
-  const int wave = threadIdx.x >> 6;
+  // Wave index made provably uniform so that page lookups are scalar loads.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int h = blockIdx.y * NH + wave;
+  if (h >= P.num_kv_heads) return;  // uniform over the wave; no barriers follow
   const int lane = threadIdx.x & 63;
   const int r = lane & 15;
   const int g = lane >> 4;
@@ -215,16 +258,8 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_partials_kernel(DecodePa
 #pragma unroll
   for (int d = 0; d < 8; ++d) o[d] = floatx4_t{0.f, 0.f, 0.f, 0.f};
 
-  const int ntiles = (tok_end - tok_begin + kTile - 1) / kTile;
-  TileRegs<kFp8> cur{}, nxt{};
-  int t = wave;
-  if (t < ntiles) load_tile<kFp8>(P, b, h, tok_begin + kTile * t, r, g, cur);
-  for (; t < ntiles; t += NW) {
-    const int tok0 = tok_begin + kTile * t;
-    if (t + NW < ntiles) load_tile<kFp8>(P, b, h, tok_begin + kTile * (t + NW), r, g, nxt);
-    const bool page_ok = page_of(P, b, tok0) >= 0;
-
-    // S[4g+i, r] for the 16 tokens of the tile.
+  // One 16-token tile: scores, online softmax update, P.V accumulation.
+  auto process = [&](int tok0, int64_t page, const TileRegs<kFp8>& cur) {
     uint4 kc[4];
     k_chunks(cur, kc);
     floatx4_t acc = {0.f, 0.f, 0.f, 0.f};
@@ -236,44 +271,44 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_partials_kernel(DecodePa
     float mt = kNegInf;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const bool ok = head_ok && page_ok && (tok0 + 4 * g + i < tok_end);
+      const bool ok = head_ok && page >= 0 && (tok0 + 4 * g + i < tok_end);
       s[i] = ok ? acc[i] * s2 : kNegInf;
       mt = fmaxf(mt, s[i]);
     }
-    mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
-    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+    mt = pair_max(mt);  // max over the column's 4 lane groups (16 tokens)
     const float m_new = fmaxf(m_run, mt);
     const float m_use = m_new == kNegInf ? 0.f : m_new;
     // alpha = 1 for columns that have seen no valid score (their O and l are 0).
-    const float alpha = m_new == kNegInf ? 1.f : exp2f(m_run - m_use);
-    float p[4];
+    const float alpha = m_new == kNegInf ? 1.f : __builtin_amdgcn_exp2f(m_run - m_use);
+    float pr[4];
     float psum = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      p[i] = exp2f(s[i] - m_use);
-      psum += p[i];
+      pr[i] = __builtin_amdgcn_exp2f(s[i] - m_use);
+      psum += pr[i];
     }
     l_run = l_run * alpha + psum;
     m_run = m_new;
-    // Rescale O rows (head 4g+i lives in lanes whose column r == 4g+i).
+    // Rescale O rows when some column max moved (rare after the first tiles).
     if (__ballot(alpha != 1.f) != 0) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float a = __shfl(alpha, 4 * g + i, 64);
+        const float a = row_value<kG>(alpha, g, i);
 #pragma unroll
         for (int d = 0; d < 8; ++d) o[d][i] *= a;
       }
     }
-    // P as the A operand: row r (head), k = tokens 4g..4g+3.
-    const uint32_t p01 = (static_cast<uint32_t>(f32_to_bf16(p[1])) << 16) | f32_to_bf16(p[0]);
-    const uint32_t p23 = (static_cast<uint32_t>(f32_to_bf16(p[3])) << 16) | f32_to_bf16(p[2]);
-    const short4_t pa = __builtin_bit_cast(short4_t, make_uint2(p01, p23));
+    // P as the A operand: row r (head), k = tokens 4g..4g+3 (RNE bf16 pack).
+    const bf16x2_t p01 = {static_cast<__bf16>(pr[0]), static_cast<__bf16>(pr[1])};
+    const bf16x2_t p23 = {static_cast<__bf16>(pr[2]), static_cast<__bf16>(pr[3])};
+    const short4_t pa = __builtin_bit_cast(
+        short4_t, make_uint2(__builtin_bit_cast(uint32_t, p01), __builtin_bit_cast(uint32_t, p23)));
     // V rows past the context (inside a valid page) may hold anything: zero
     // them so that P = 0 never meets a NaN.
     uint4 vr[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      vr[i] = (tok0 + 4 * g + i < tok_end) ? v_row(cur, i) : make_uint4(0, 0, 0, 0);
+      vr[i] = (page >= 0 && tok0 + 4 * g + i < tok_end) ? v_row(cur, i) : make_uint4(0, 0, 0, 0);
 #pragma unroll
     for (int d = 0; d < 8; ++d) {
       const int wi = d >> 1;
@@ -288,58 +323,60 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_partials_kernel(DecodePa
       const short4_t vb = __builtin_bit_cast(short4_t, make_uint2(b01, b23));
       o[d] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, vb, o[d], 0, 0, 0);
     }
-    cur = nxt;
+  };
+
+  // Chunks of U tiles: issue all U tiles' loads, then consume them in order
+  // (the compiler waits for tile u with vmcnt = loads issued after it).  Loads
+  // are unconditional; tiles past the end re-read the last tile (cache hits).
+  const int ntiles = (tok_end - tok_begin + kTile - 1) / kTile;
+  for (int t0 = 0; t0 < ntiles; t0 += U) {
+    TileRegs<kFp8> buf[U];
+    int64_t pg[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int tok0 = tok_begin + kTile * min(t0 + u, ntiles - 1);
+      pg[u] = page_of(P, b, tok0);
+      load_tile<kFp8>(P, pg[u] < 0 ? 0 : pg[u], h, tok0, r, g, buf[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (t0 + u < ntiles) process(tok_begin + kTile * (t0 + u), pg[u], buf[u]);
   }
 
-  // Column sums of l over the 4 lane groups.
-  l_run += __shfl_xor(l_run, 16, 64);
-  l_run += __shfl_xor(l_run, 32, 64);
+  // Column sums of l over the 4 lane groups: every lane of column j holds l_j.
+  l_run = pair_sum(l_run);
 
-  // Merge the NW waves through LDS.
-  __shared__ float sm_m[NW][16];
-  __shared__ float sm_l[NW][16];
-  __shared__ float sm_o[NW][kG][kHead];
-  if (lane < 16) {
-    sm_m[wave][lane] = m_run;
-    sm_l[wave][lane] = l_run;
-  }
+  // Epilogue: lane (r, g) holds O[head 4g+i][dims 8r .. 8r+7] for i < 4.
+  const float vs = (kFp8 && P.v_scale) ? P.v_scale[h] : 1.f;
+  const int64_t part_row = (static_cast<int64_t>(b) * P.num_kv_heads + h) * P.max_parts + p;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int j = 4 * g + i;
-    if (j < kG && j < gqa) {
+    if (j >= kG || j >= gqa) continue;
+    if (nparts == 1) {
+      const float l = row_value<kG>(l_run, g, i);
+      const float f = l > 0.f ? vs / l : 0.f;
+      uint32_t w[4];
 #pragma unroll
-      for (int d = 0; d < 8; ++d) sm_o[wave][j][8 * r + d] = o[d][i];
+      for (int d = 0; d < 4; ++d) {
+        const bf16x2_t pk = {static_cast<__bf16>(o[2 * d][i] * f),
+                             static_cast<__bf16>(o[2 * d + 1][i] * f)};
+        w[d] = __builtin_bit_cast(uint32_t, pk);
+      }
+      *reinterpret_cast<uint4*>(P.out + b * P.out_row_stride +
+                                static_cast<int64_t>(h * gqa + j) * kHead + 8 * r) =
+          make_uint4(w[0], w[1], w[2], w[3]);
+    } else {
+      float* dst = P.part_o + (part_row * gqa + j) * kHead + 8 * r;
+      *reinterpret_cast<float4*>(dst) =
+          make_float4(o[0][i] * vs, o[1][i] * vs, o[2][i] * vs, o[3][i] * vs);
+      *reinterpret_cast<float4*>(dst + 4) =
+          make_float4(o[4][i] * vs, o[5][i] * vs, o[6][i] * vs, o[7][i] * vs);
     }
   }
-  __syncthreads();
-
-  const float vs = (kFp8 && P.v_scale) ? P.v_scale[h] : 1.f;
-  const int64_t part_row = (static_cast<int64_t>(b) * P.num_kv_heads + h) * P.max_parts + p;
-  for (int e = threadIdx.x; e < gqa * kHead; e += NW * 64) {
-    const int j = e / kHead;
-    const int d = e - j * kHead;
-    float M = kNegInf;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) M = fmaxf(M, sm_m[w][j]);
-    float L = 0.f, O = 0.f;
-    if (M != kNegInf) {
-#pragma unroll
-      for (int w = 0; w < NW; ++w) {
-        const float f = exp2f(sm_m[w][j] - M);
-        L += f * sm_l[w][j];
-        O += f * sm_o[w][j][d];
-      }
-    }
-    if (nparts == 1) {
-      const float v = L > 0.f ? O / L * vs : 0.f;
-      P.out[b * P.out_row_stride + static_cast<int64_t>(h * gqa + j) * kHead + d] = f32_to_bf16(v);
-    } else {
-      P.part_o[(part_row * gqa + j) * kHead + d] = O * vs;
-      if (d == 0) {
-        P.part_ml[(part_row * gqa + j) * 2 + 0] = M;
-        P.part_ml[(part_row * gqa + j) * 2 + 1] = L;
-      }
-    }
+  if (nparts > 1 && g == 0 && head_ok) {
+    P.part_ml[(part_row * gqa + r) * 2 + 0] = m_run;
+    P.part_ml[(part_row * gqa + r) * 2 + 1] = l_run;
   }
 }
 
@@ -383,7 +420,9 @@ __global__ __launch_bounds__(64) void paged_decode_reduce_kernel(
       (static_cast<uint32_t>(f32_to_bf16(o1 * inv)) << 16) | f32_to_bf16(o0 * inv);
 }
 
-constexpr int kNW = 4;  // waves per work-group
+constexpr int kMaxWavesPerGroup = 8;  // kv heads (waves) per work-group
+constexpr int kChunk = 4;             // tiles loaded per wave before consuming them
+constexpr int kPartQuant = 64;        // partition granularity in tokens
 
 struct Shape {
   int64_t batch;
@@ -410,9 +449,9 @@ int validate(const char* name, int64_t batch, int num_heads, int num_kv_heads, i
   if (num_heads / num_kv_heads > 16)
     return set_error(FK_ERR_UNSUPPORTED, "%s: GQA group %d > 16 unsupported", name,
                      num_heads / num_kv_heads);
-  FK_REQUIRE(part_tokens > 0 && part_tokens % (kNW * kTile) == 0 && part_tokens <= (1 << 30),
+  FK_REQUIRE(part_tokens > 0 && part_tokens % kPartQuant == 0 && part_tokens <= (1 << 30),
              "%s: part_tokens %lld must be a positive multiple of %d", name,
-             (long long)part_tokens, kNW * kTile);
+             (long long)part_tokens, kPartQuant);
   FK_REQUIRE(max_parts > 0 && max_parts <= 65535, "%s: max_parts %lld out of range", name,
              (long long)max_parts);
   return FK_OK;
@@ -437,16 +476,16 @@ extern "C" int fk_paged_decode_plan(int64_t batch, int num_kv_heads, int64_t max
   FK_REQUIRE(part_tokens && max_parts, "fk_paged_decode_plan: null output pointer");
   FK_REQUIRE(batch >= 0 && num_kv_heads > 0 && max_seq_len >= 0 && num_splits >= 0,
              "fk_paged_decode_plan: negative argument");
-  constexpr int64_t kQuant = kNW * kTile;  // partition granularity (64 tokens)
+  constexpr int64_t kQuant = kPartQuant;
   const int64_t L = max_seq_len > 0 ? max_seq_len : 1;
   int64_t part;
   if (num_splits > 0) {
     part = (L + num_splits - 1) / num_splits;
   } else {
-    // Enough work-groups to fill 256 CUs several times over, but at least
-    // 256 tokens (64 KiB of bf16 K+V per kv head) per partition.
+    // One wave streams one (sequence, kv head, partition): aim for ~8192 waves
+    // (256 CUs x 8 resident waves x ~4 rounds) with at least 256 tokens each.
     const int64_t units = (batch > 0 ? batch : 1) * num_kv_heads;
-    part = (L * units + 4095) / 4096;
+    part = (L * units + 8191) / 8192;
     if (part < 256) part = 256;
   }
   part = (part + kQuant - 1) / kQuant * kQuant;
@@ -476,6 +515,7 @@ static int launch_partials(void* out, int64_t out_row_stride, const void* q,
   if (batch == 0) return FK_OK;
   FK_REQUIRE(out && q && k_cache && v_cache && block_tables && ctx_lens, "%s: null pointer",
              name);
+  FK_REQUIRE(num_blocks >= 1, "%s: the cache must hold at least one block", name);
   FK_REQUIRE(aligned16(q) && aligned16(k_cache) && aligned16(v_cache) && aligned16(out) &&
                  q_row_stride % 8 == 0 && out_row_stride % 2 == 0,
              "%s: q/out/cache must be 16-byte aligned with q rows a multiple of 8 elements",
@@ -512,18 +552,28 @@ static int launch_partials(void* out, int64_t out_row_stride, const void* q,
                                                    (rows * kHead * 4 + 255) / 256 * 256)
                         : nullptr;
 
-  const dim3 grid(static_cast<unsigned>(max_parts), static_cast<unsigned>(num_kv_heads),
+  const int nh = num_kv_heads < kMaxWavesPerGroup ? num_kv_heads : kMaxWavesPerGroup;
+  const dim3 grid(static_cast<unsigned>(max_parts),
+                  static_cast<unsigned>((num_kv_heads + nh - 1) / nh),
                   static_cast<unsigned>(batch));
-  const dim3 block(kNW * 64);
   const bool fp8 = kv_dtype == FK_DTYPE_FP8_E4M3FN;
-#define FK_PD(G)                                                                          \
+#define FK_PD_NH(NH, G)                                                                   \
   do {                                                                                    \
     if (fp8)                                                                              \
-      hipLaunchKernelGGL((paged_decode_partials_kernel<kNW, G, true>), grid, block, 0,    \
-                         stream, P);                                                      \
+      hipLaunchKernelGGL((paged_decode_partials_kernel<NH, G, true, kChunk>), grid,       \
+                         dim3(NH * 64), 0, stream, P);                                    \
     else                                                                                  \
-      hipLaunchKernelGGL((paged_decode_partials_kernel<kNW, G, false>), grid, block, 0,   \
-                         stream, P);                                                      \
+      hipLaunchKernelGGL((paged_decode_partials_kernel<NH, G, false, kChunk>), grid,      \
+                         dim3(NH * 64), 0, stream, P);                                    \
+  } while (0)
+#define FK_PD(G)                            \
+  do {                                      \
+    switch (nh) {                           \
+      case 1: FK_PD_NH(1, G); break;        \
+      case 2: FK_PD_NH(2, G); break;        \
+      case 4: FK_PD_NH(4, G); break;        \
+      default: FK_PD_NH(8, G); break;       \
+    }                                       \
   } while (0)
   if (P.gqa <= 4)
     FK_PD(4);
@@ -532,6 +582,7 @@ static int launch_partials(void* out, int64_t out_row_stride, const void* q,
   else
     FK_PD(16);
 #undef FK_PD
+#undef FK_PD_NH
   return check_launch(name);
 }
 
