@@ -159,8 +159,8 @@ def bench_decode(args):
     case = workloads.c3_decode(dev, seed=args.seed)
     b, hq, d = case.q.shape
     hk = case.k_cache.shape[2]
-    part, nparts = ops.paged_decode_plan(b, hk, case.max_seq_len, args.num_splits)
-    ws = torch.empty(max(1, ops.paged_decode_workspace_bytes(b, hq, hk, d, nparts)),
+    part, nparts, wsb = ops.paged_decode_plan(b, hq, hk, d, case.max_seq_len, args.num_splits)
+    ws = torch.empty(max(1, wsb),
                      dtype=torch.uint8, device=dev)
     out = torch.empty_like(case.q)
     partials, reduce = ops.paged_decode_phases(out, case.q, case.k_cache, case.v_cache,
@@ -276,8 +276,8 @@ def bench_table(args):
                                ("C5", c5, 64)):
         b, hq, d = case.q.shape
         hk = case.k_cache.shape[2]
-        part, nparts = ops.paged_decode_plan(b, hk, case.max_seq_len, splits)
-        ws = torch.empty(max(1, ops.paged_decode_workspace_bytes(b, hq, hk, d, nparts)),
+        part, nparts, wsb = ops.paged_decode_plan(b, hq, hk, d, case.max_seq_len, splits)
+        ws = torch.empty(max(1, wsb),
                          dtype=torch.uint8, device=dev)
         out = torch.empty_like(case.q)
         add(name, f"paged_decode {case.k_cache.dtype} B={b} Hq={hq} part={part} x{nparts}",

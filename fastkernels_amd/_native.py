@@ -37,9 +37,9 @@ _SIGNATURES = {
                                     c_int, c_void_p]),
     "fk_store_kvcache": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p,
                                  c_void_p, c_int, c_int64, c_int64, c_int, c_int64, c_void_p]),
-    "fk_paged_decode_workspace_bytes": (c_int64, [c_int64, c_int, c_int, c_int, c_int64]),
-    "fk_paged_decode_plan": (c_int, [c_int64, c_int, c_int64, c_int,
-                                     ctypes.POINTER(c_int64), ctypes.POINTER(c_int64)]),
+    "fk_paged_decode_plan": (c_int, [c_int64, c_int, c_int, c_int, c_int64, c_int,
+                                     ctypes.POINTER(c_int64), ctypes.POINTER(c_int64),
+                                     ctypes.POINTER(c_int64)]),
     "fk_paged_decode": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_int,
                                 c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_int,
                                 c_int, c_int, c_int, c_int64, c_float, c_int64, c_int64,
@@ -49,8 +49,11 @@ _SIGNATURES = {
                                          c_void_p, c_int64, c_int, c_int, c_int, c_int, c_int64,
                                          c_float, c_int64, c_int64, c_void_p, c_int64,
                                          c_void_p]),
-    "fk_paged_decode_reduce": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_int, c_int,
-                                       c_int, c_int64, c_int64, c_void_p, c_int64, c_void_p]),
+    "fk_paged_decode_reduce": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p,
+                                       c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_int64,
+                                       c_void_p, c_int64, c_int, c_int, c_int, c_int, c_int64,
+                                       c_float, c_int64, c_int64, c_void_p, c_int64,
+                                       c_void_p]),
     "fk_silu_and_mul": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_int64, c_int64, c_int,
                                 c_void_p]),
 }
@@ -98,17 +101,15 @@ def call(fn: str, *args) -> None:
     check(fn, getattr(lib(), fn)(*args))
 
 
-def plan(batch: int, num_kv_heads: int, max_seq_len: int, num_splits: int) -> tuple[int, int]:
-    """fk_paged_decode_plan: (part_tokens, max_parts) for a decode launch."""
+def plan(batch: int, num_heads: int, num_kv_heads: int, head_size: int, max_seq_len: int,
+         num_splits: int) -> tuple[int, int, int]:
+    """fk_paged_decode_plan: (part_tokens, max_parts, workspace_bytes); part_tokens 0 is
+    the length-balanced schedule."""
     part = c_int64(0)
     nparts = c_int64(0)
+    ws = c_int64(0)
     check("fk_paged_decode_plan",
-          lib().fk_paged_decode_plan(batch, num_kv_heads, max_seq_len, num_splits,
-                                     ctypes.byref(part), ctypes.byref(nparts)))
-    return part.value, nparts.value
-
-
-def workspace_bytes(batch: int, num_heads: int, num_kv_heads: int, head_size: int,
-                    max_parts: int) -> int:
-    return int(lib().fk_paged_decode_workspace_bytes(batch, num_heads, num_kv_heads, head_size,
-                                                     max_parts))
+          lib().fk_paged_decode_plan(batch, num_heads, num_kv_heads, head_size, max_seq_len,
+                                     num_splits, ctypes.byref(part), ctypes.byref(nparts),
+                                     ctypes.byref(ws)))
+    return part.value, nparts.value, ws.value

@@ -7,9 +7,12 @@ the reference forwards to ``flash_attn_varlen_func`` (flash_attn_decode.py:
 (decode: every cached key is visible), ``num_splits``, ``out``.  Returns
 ``[B, num_heads, head_dim]`` in q's dtype.
 
-The gfx950 kernel is split-context flash-decoding: work-groups of
-``part_tokens`` tokens per (sequence, kv head) write partials into a
-per-module workspace that a second kernel merges with the log-sum-exp rule.
+The gfx950 kernel is split-context flash-decoding.  By default
+(``num_splits`` 0) the 16-token tiles of all sequences are cut into equal
+ranges, one work-group per CU, so mixed lengths leave no idle tail; an explicit
+``num_splits`` uses that many fixed partitions per sequence instead.  Sequences
+cut across work-groups leave partials in a per-module workspace that a second
+kernel merges with the log-sum-exp rule.
 The workspace is allocated outside graph capture (like the reference's
 persistent FA3 scheduler buffer, flash_attn_decode.py:87-111) and only grows;
 inside a capture it must already be large enough.
@@ -20,9 +23,10 @@ given as a single value and are broadcast), i.e. K = float(K8) * k_scale as in
 ``_cast_kv_tile`` (triton_unified_attention.py:51-67).  FA-style
 ``k_descale`` / ``v_descale`` are accepted as aliases.
 
-No host synchronisation: when ``max_seq_len`` is absent the bound is taken from
-the block table width (``block_table.shape[1] * page_size``) instead of
-``cache_seqlens.max().item()`` (flash_attn_decode.py:122-125).
+No host synchronisation: the default length-balanced schedule reads the context
+lengths on the device, and when ``max_seq_len`` is absent the bound used for
+fixed partitions is the block table width (``block_table.shape[1] * page_size``)
+instead of ``cache_seqlens.max().item()`` (flash_attn_decode.py:122-125).
 """
 from __future__ import annotations
 
@@ -65,11 +69,9 @@ class FlashAttnDecode(nn.Module):
     def preallocate(self, max_batch_size: int, max_seq_len: int, device: torch.device,
                     num_splits: int = 0) -> None:
         """Allocate the workspace for batches up to max_batch_size (outside capture)."""
-        _, max_parts = ops.paged_decode_plan(max_batch_size, self.num_kv_heads, max_seq_len,
-                                             num_splits)
-        nbytes = ops.paged_decode_workspace_bytes(max_batch_size, self.num_heads,
-                                                  self.num_kv_heads, self.head_dim, max_parts)
-        self._get_workspace(nbytes, torch.device(device))
+        plan = ops.paged_decode_plan(max_batch_size, self.num_heads, self.num_kv_heads,
+                                     self.head_dim, max_seq_len, num_splits)
+        self._get_workspace(plan.workspace_bytes, torch.device(device))
 
     @staticmethod
     def _scale_vec(s, hk: int, device) -> torch.Tensor | None:
@@ -120,10 +122,10 @@ class FlashAttnDecode(nn.Module):
         k_scale = self._scale_vec(k_scale, hk, q.device)
         v_scale = self._scale_vec(v_scale, hk, q.device)
 
-        part_tokens, max_parts = ops.paged_decode_plan(b, hk, int(max_seq_len), num_splits)
-        ws = self._get_workspace(
-            ops.paged_decode_workspace_bytes(b, self.num_heads, hk, self.head_dim, max_parts)
-            if max_parts > 1 else 0, q.device)
+        plan = ops.paged_decode_plan(b, self.num_heads, hk, self.head_dim, int(max_seq_len),
+                                     num_splits)
+        ws = self._get_workspace(plan.workspace_bytes, q.device)
+        part_tokens, max_parts = plan.part_tokens, plan.max_parts
         if out is None:
             out = torch.empty((b, self.num_heads, self.head_dim), dtype=q.dtype, device=q.device)
         out3 = out.view(b, self.num_heads, self.head_dim)

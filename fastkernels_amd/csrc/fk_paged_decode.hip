@@ -1,5 +1,5 @@
 // Paged decode attention for MI355X (gfx950): split-context ("flash-decoding")
-// with GQA-packed MFMA tiles.
+// with GQA-packed MFMA tiles and a length-balanced schedule.
 //
 // Semantics (one query token per sequence, all cached keys visible):
 //   out[b, hq] = sum_t softmax_t(scale * q[b,hq] . K[b,t]) V[b,t],  t < ctx_lens[b]
@@ -7,21 +7,26 @@
 // from NHD pages [num_blocks, block_size, Hk, D]; kv head = hq / (Hq/Hk).  This is
 // FlashAttnDecode.forward (fastkernels/tasks/baseline/L1/flash_attn_decode.py:
 // 113-181) and the reference's torch fallback Attention._decode_torch
-// (fastkernels/tasks/baseline/L2/attention_impl.py:592-664).  Partitions are
-// merged with the log-sum-exp rule of reduce_segments
-// (triton_unified_attention.py:741-776): M = max m_p, L = sum l_p e^(m_p - M),
-// O = sum o_p e^(m_p - M) / L, and O = 0 when L = 0.  fp8 KV pages are
-// dequantised per (kv head) as float(x) * scale, the per-tensor rule of
+// (fastkernels/tasks/baseline/L2/attention_impl.py:592-664).  Segments of a
+// sequence are merged with the log-sum-exp rule of reduce_segments
+// (triton_unified_attention.py:741-776): M = max m_s, L = sum l_s e^(m_s - M),
+// O = sum o_s e^(m_s - M) / L, and O = 0 when L = 0.  fp8 KV pages are
+// dequantised per kv head as float(x) * scale, the per-tensor rule of
 // _cast_kv_tile (triton_unified_attention.py:51-67): k_scale is folded into the
 // score scale and v_scale into the output, which is algebraically the same.
 //
-// Work decomposition.  Work-group = (partition p, kv head h, sequence b) with
-// NW wave64s.  A partition is part_tokens consecutive tokens; the waves take
-// 16-token tiles round-robin, so the NW waves of a group stream NW adjacent
-// tiles at once.  Each wave keeps an online-softmax state for the G query heads
-// of its kv head; the waves are merged through LDS and the group writes one
-// partial (or the final row when the sequence has a single partition).  A
-// second kernel merges partials per (b, hq).
+// Work decomposition.  A work-group has one wave64 per kv head (up to 8); the
+// waves of a group stream the same token rows of the NHD cache, so each
+// token's Hk * 256-byte row is read whole within a short window.  Two
+// schedules share the per-wave tile loop:
+//   balanced (default): the 16-token tiles of all sequences are concatenated
+//     and cut into one equal range per work-group, with one work-group per
+//     CU.  A sequence wholly inside a range is finished in place; a sequence
+//     cut by range boundaries leaves one partial per range, merged by a
+//     second kernel.  Every group streams the same number of bytes, so
+//     sequences of 512 and 8192 tokens leave no idle tail.
+//   fixed partitions (explicit num_splits): work-group = (partition p of
+//     part_tokens tokens, sequence b), the classic flash-decoding split.
 //
 // MFMA mapping (per 16-token tile, per wave).  Let r = lane % 16, g = lane / 16.
 //   S[t, j] = K[t, :] . Q[j, :]   4 x v_mfma_f32_16x16x32_bf16 over D = 128:
@@ -36,8 +41,12 @@
 // Rows j >= G of the 16-row MFMA tiles are padding (zero Q, zero P): the matrix
 // cores have ~80x the throughput this HBM-bound loop needs, so the padding is
 // free, while the VALU work per token stays at a few instructions (no
-// cross-lane dot-product reductions, two wave shuffles per tile for the max).
+// cross-lane dot-product reductions, two row-swap permutes per tile for the max).
 #include "fk_common.h"
+
+#ifndef FK_DECODE_PIPE
+#define FK_DECODE_PIPE 0
+#endif
 
 namespace fk {
 namespace {
@@ -71,8 +80,11 @@ struct DecodeParams {
   int max_parts;
   int64_t num_blocks;
   float scale_log2;  // softmax scale * log2(e)
-  float* part_o;     // [B][Hk][max_parts][gqa][128] unnormalised partial outputs
-  float* part_ml;    // [B][Hk][max_parts][gqa][2]   (max, sum) in the log2 domain
+  float* part_o;     // partial outputs (unnormalised), rows of 128 floats
+  float* part_ml;    // per partial row: (max, sum) in the log2 domain
+  int32_t* tile_off; // balanced schedule: [batch + 1] tile prefix sums, then range size
+  int batch;
+  int num_groups;    // balanced schedule: work-groups per kv-head group
 };
 
 // Reductions over the four 16-lane rows of a wave (lanes r, r+16, r+32, r+48)
@@ -109,6 +121,10 @@ __device__ __forceinline__ uint2 fp8x4_to_bf16x4(uint32_t w) {
   return make_uint2(hi_pair(__float_as_uint(lo[0]), __float_as_uint(lo[1])),
                     hi_pair(__float_as_uint(hi[0]), __float_as_uint(hi[1])));
 }
+
+// KV loads (plain cached loads: marking them non-temporal measured slower).
+__device__ __forceinline__ uint4 ld16(const uint8_t* p) { return *reinterpret_cast<const uint4*>(p); }
+__device__ __forceinline__ uint2 ld8(const uint8_t* p) { return *reinterpret_cast<const uint2*>(p); }
 
 // Raw registers one wave loads for one 16-token tile.  load_tile only issues
 // the loads; conversion and masking happen in the consumer, after the
@@ -154,17 +170,17 @@ __device__ __forceinline__ void load_tile(const DecodeParams& P, int64_t page, i
     // Per instruction: 16 rows x 64 contiguous bytes.
 #pragma unroll
     for (int c = 0; c < 4; ++c)
-      t.k[c] = *reinterpret_cast<const uint4*>(krow + (32 * c + 8 * g) * 2);
+      t.k[c] = ld16(krow + (32 * c + 8 * g) * 2);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      t.v[i] = *reinterpret_cast<const uint4*>(P.v_cache + (slot0 + 4 * g + i) * row_bytes +
+      t.v[i] = ld16(P.v_cache + (slot0 + 4 * g + i) * row_bytes +
                                                head_off + 8 * r * 2);
   } else {
-    t.k[0] = *reinterpret_cast<const uint4*>(krow + 32 * g);
-    t.k[1] = *reinterpret_cast<const uint4*>(krow + 32 * g + 16);
+    t.k[0] = ld16(krow + 32 * g);
+    t.k[1] = ld16(krow + 32 * g + 16);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      t.v[i] = *reinterpret_cast<const uint2*>(P.v_cache + (slot0 + 4 * g + i) * row_bytes +
+      t.v[i] = ld8(P.v_cache + (slot0 + 4 * g + i) * row_bytes +
                                                head_off + 8 * r);
   }
 }
@@ -210,13 +226,198 @@ __device__ __forceinline__ float row_value(float x, int g, int i) {
   return a;
 }
 
-// One work-group per (partition p, kv-head group, sequence b); wave w owns kv
-// head h = blockIdx.y * NH + w and streams every tile of the partition.  The
-// NH waves of a group walk the same token rows together, so the NHD rows
-// (Hk * 256 contiguous bytes per token) are read whole within a short window.
-// Each wave loads U tiles (U * 8 KiB for bf16) before consuming them in order.
+// Online-softmax state of one wave over the G query heads of one kv head, and
+// the tile loop that streams a token range [tok_begin, tok_end) of a sequence
+// through it (tok_begin a multiple of 16).
+template <int kG, bool kFp8, int U>
+struct WaveState {
+  float m_run;  // running max of column r (same in the 4 lanes of a column)
+  float l_run;  // this lane's share of the running sum of column r
+  floatx4_t o[8];
+
+  __device__ __forceinline__ void run(const DecodeParams& P, int b, int h, int tok_begin,
+                                      int tok_end, int r, int g) {
+    const int gqa = P.gqa;
+    const bool head_ok = r < gqa;
+    // Q^T operand: column r = query head h*G + r; dims permuted as the K loads.
+    bf16x8_t qb[4];
+    {
+      const uint16_t* qp = P.q + b * P.q_row_stride + static_cast<int64_t>(h * gqa + r) * kHead;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int d0 = kFp8 ? 32 * g + 8 * c : 32 * c + 8 * g;
+        uint4 v = head_ok ? *reinterpret_cast<const uint4*>(qp + d0) : make_uint4(0, 0, 0, 0);
+        qb[c] = __builtin_bit_cast(bf16x8_t, v);
+      }
+    }
+    float s2 = P.scale_log2;
+    if (kFp8 && P.k_scale) s2 *= P.k_scale[h];
+
+    m_run = kNegInf;
+    l_run = 0.f;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) o[d] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+
+    // One 16-token tile: scores, online softmax update, P.V accumulation.
+    auto process = [&](int tok0, int64_t page, const TileRegs<kFp8>& cur) {
+      uint4 kc[4];
+      k_chunks(cur, kc);
+      floatx4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kc[c]), qb[c],
+                                                     acc, 0, 0, 0);
+      float s[4];
+      float mt = kNegInf;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const bool ok = head_ok && page >= 0 && (tok0 + 4 * g + i < tok_end);
+        s[i] = ok ? acc[i] * s2 : kNegInf;
+        mt = fmaxf(mt, s[i]);
+      }
+      mt = pair_max(mt);  // max over the column's 4 lane groups (16 tokens)
+      const float m_new = fmaxf(m_run, mt);
+      const float m_use = m_new == kNegInf ? 0.f : m_new;
+      // alpha = 1 for columns that have seen no valid score (their O and l are 0).
+      const float alpha = m_new == kNegInf ? 1.f : __builtin_amdgcn_exp2f(m_run - m_use);
+      float pr[4];
+      float psum = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        pr[i] = __builtin_amdgcn_exp2f(s[i] - m_use);
+        psum += pr[i];
+      }
+      l_run = l_run * alpha + psum;
+      m_run = m_new;
+      // Rescale O rows when some column max moved (rare after the first tiles).
+      if (__ballot(alpha != 1.f) != 0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float a = row_value<kG>(alpha, g, i);
+#pragma unroll
+          for (int d = 0; d < 8; ++d) o[d][i] *= a;
+        }
+      }
+      // P as the A operand: row r (head), k = tokens 4g..4g+3 (RNE bf16 pack).
+      const bf16x2_t p01 = {static_cast<__bf16>(pr[0]), static_cast<__bf16>(pr[1])};
+      const bf16x2_t p23 = {static_cast<__bf16>(pr[2]), static_cast<__bf16>(pr[3])};
+      const short4_t pa = __builtin_bit_cast(
+          short4_t,
+          make_uint2(__builtin_bit_cast(uint32_t, p01), __builtin_bit_cast(uint32_t, p23)));
+      // V rows past the context (inside a valid page) may hold anything: zero
+      // them so that P = 0 never meets a NaN.
+      uint4 vr[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        vr[i] = (page >= 0 && tok0 + 4 * g + i < tok_end) ? v_row(cur, i) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+      for (int d = 0; d < 8; ++d) {
+        const int wi = d >> 1;
+        uint32_t b01, b23;
+        if (d & 1) {
+          b01 = hi_pair(word(vr[0], wi), word(vr[1], wi));
+          b23 = hi_pair(word(vr[2], wi), word(vr[3], wi));
+        } else {
+          b01 = lo_pair(word(vr[0], wi), word(vr[1], wi));
+          b23 = lo_pair(word(vr[2], wi), word(vr[3], wi));
+        }
+        const short4_t vb = __builtin_bit_cast(short4_t, make_uint2(b01, b23));
+        o[d] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, vb, o[d], 0, 0, 0);
+      }
+    };
+
+    const int ntiles = (tok_end - tok_begin + kTile - 1) / kTile;
+    // Issues the loads of tiles t0 .. t0+U-1 into `buf` (unconditional; tiles
+    // past the end re-read the last tile, which hits in cache).
+    auto fetch = [&](int t0, TileRegs<kFp8>(&buf)[U], int64_t(&pg)[U]) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int tok0 = tok_begin + kTile * min(t0 + u, ntiles - 1);
+        pg[u] = page_of(P, b, tok0);
+        load_tile<kFp8>(P, pg[u] < 0 ? 0 : pg[u], h, tok0, r, g, buf[u]);
+      }
+    };
+    auto consume = [&](int t0, const TileRegs<kFp8>(&buf)[U], const int64_t(&pg)[U]) {
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (t0 + u < ntiles) process(tok_begin + kTile * (t0 + u), pg[u], buf[u]);
+    };
+#if FK_DECODE_PIPE
+    // Two register sets of U tiles: one is consumed while the other is in flight.
+    TileRegs<kFp8> bufA[U], bufB[U];
+    int64_t pgA[U], pgB[U];
+    fetch(0, bufA, pgA);
+    for (int t0 = 0; t0 < ntiles; t0 += 2 * U) {
+      fetch(t0 + U, bufB, pgB);
+      consume(t0, bufA, pgA);
+      fetch(t0 + 2 * U, bufA, pgA);
+      consume(t0 + U, bufB, pgB);
+    }
+#else
+    // Chunks of U tiles: issue all U tiles' loads, then consume them in order
+    // (the compiler waits for tile u with vmcnt = loads issued after it).
+    for (int t0 = 0; t0 < ntiles; t0 += U) {
+      TileRegs<kFp8> buf[U];
+      int64_t pg[U];
+      fetch(t0, buf, pg);
+      consume(t0, buf, pg);
+    }
+#endif
+    // Column sums of l over the 4 lane groups: every lane of column j holds l_j.
+    l_run = pair_sum(l_run);
+  }
+
+  // Normalised output row(s) of kv head h for a sequence finished in place.
+  // Lane (r, g) holds O[head 4g+i][dims 8r .. 8r+7].
+  __device__ __forceinline__ void write_final(const DecodeParams& P, int b, int h, int r,
+                                              int g) const {
+    const float vs = (kFp8 && P.v_scale) ? P.v_scale[h] : 1.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int j = 4 * g + i;
+      const float l = row_value<kG>(l_run, g, i);
+      if (j >= kG || j >= P.gqa) continue;
+      const float f = l > 0.f ? vs / l : 0.f;
+      uint32_t w[4];
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const bf16x2_t pk = {static_cast<__bf16>(o[2 * d][i] * f),
+                             static_cast<__bf16>(o[2 * d + 1][i] * f)};
+        w[d] = __builtin_bit_cast(uint32_t, pk);
+      }
+      *reinterpret_cast<uint4*>(P.out + b * P.out_row_stride +
+                                static_cast<int64_t>(h * P.gqa + j) * kHead + 8 * r) =
+          make_uint4(w[0], w[1], w[2], w[3]);
+    }
+  }
+
+  // Unnormalised partial (O scaled by v_scale, and (max, sum)) into partial
+  // rows row0 + j, j < G.
+  __device__ __forceinline__ void write_partial(const DecodeParams& P, int64_t row0, int h, int r,
+                                                int g) const {
+    const float vs = (kFp8 && P.v_scale) ? P.v_scale[h] : 1.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int j = 4 * g + i;
+      if (j >= kG || j >= P.gqa) continue;
+      float* dst = P.part_o + (row0 + j) * kHead + 8 * r;
+      *reinterpret_cast<float4*>(dst) =
+          make_float4(o[0][i] * vs, o[1][i] * vs, o[2][i] * vs, o[3][i] * vs);
+      *reinterpret_cast<float4*>(dst + 4) =
+          make_float4(o[4][i] * vs, o[5][i] * vs, o[6][i] * vs, o[7][i] * vs);
+    }
+    if (g == 0 && r < P.gqa) {
+      P.part_ml[(row0 + r) * 2 + 0] = m_run;
+      P.part_ml[(row0 + r) * 2 + 1] = l_run;
+    }
+  }
+};
+
+// Fixed partitions: work-group = (partition p, kv-head group, sequence b);
+// wave w owns kv head h = blockIdx.y * NH + w and streams the partition.
+// Partial rows: ((b * Hk + h) * max_parts + p) * G + j.
 template <int NH, int kG, bool kFp8, int U>
-__global__ __launch_bounds__(NH * 64) void paged_decode_partials_kernel(DecodeParams P) {
+__global__ __launch_bounds__(NH * 64) void paged_decode_partition_kernel(DecodeParams P) {
   const int p = blockIdx.x;
   const int b = blockIdx.z;
   const int ctx = P.ctx_lens[b];
@@ -227,7 +428,6 @@ __global__ __launch_bounds__(NH * 64) void paged_decode_partials_kernel(DecodePa
   // max_seq_len bounds every context); clamp so the partition count matches
   // the grid and the reduce kernel.
   const int nparts = min((ctx + P.part_tokens - 1) / P.part_tokens, P.max_parts);
-
   // Wave index made provably uniform so that page lookups are scalar loads.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int h = blockIdx.y * NH + wave;
@@ -235,180 +435,99 @@ __global__ __launch_bounds__(NH * 64) void paged_decode_partials_kernel(DecodePa
   const int lane = threadIdx.x & 63;
   const int r = lane & 15;
   const int g = lane >> 4;
-  const int gqa = P.gqa;
-  const bool head_ok = r < gqa;
-
-  // Q^T operand: column r = query head h*G + r; dims permuted as the K loads.
-  bf16x8_t qb[4];
-  {
-    const uint16_t* qp = P.q + b * P.q_row_stride + static_cast<int64_t>(h * gqa + r) * kHead;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int d0 = kFp8 ? 32 * g + 8 * c : 32 * c + 8 * g;
-      uint4 v = head_ok ? *reinterpret_cast<const uint4*>(qp + d0) : make_uint4(0, 0, 0, 0);
-      qb[c] = __builtin_bit_cast(bf16x8_t, v);
-    }
-  }
-  float s2 = P.scale_log2;
-  if (kFp8 && P.k_scale) s2 *= P.k_scale[h];
-
-  float m_run = kNegInf;  // running max for head r (same in the 4 lanes of a column)
-  float l_run = 0.f;      // this lane's share of the running sum for head r
-  floatx4_t o[8];
-#pragma unroll
-  for (int d = 0; d < 8; ++d) o[d] = floatx4_t{0.f, 0.f, 0.f, 0.f};
-
-  // One 16-token tile: scores, online softmax update, P.V accumulation.
-  auto process = [&](int tok0, int64_t page, const TileRegs<kFp8>& cur) {
-    uint4 kc[4];
-    k_chunks(cur, kc);
-    floatx4_t acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kc[c]), qb[c],
-                                                   acc, 0, 0, 0);
-    float s[4];
-    float mt = kNegInf;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const bool ok = head_ok && page >= 0 && (tok0 + 4 * g + i < tok_end);
-      s[i] = ok ? acc[i] * s2 : kNegInf;
-      mt = fmaxf(mt, s[i]);
-    }
-    mt = pair_max(mt);  // max over the column's 4 lane groups (16 tokens)
-    const float m_new = fmaxf(m_run, mt);
-    const float m_use = m_new == kNegInf ? 0.f : m_new;
-    // alpha = 1 for columns that have seen no valid score (their O and l are 0).
-    const float alpha = m_new == kNegInf ? 1.f : __builtin_amdgcn_exp2f(m_run - m_use);
-    float pr[4];
-    float psum = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      pr[i] = __builtin_amdgcn_exp2f(s[i] - m_use);
-      psum += pr[i];
-    }
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-    // Rescale O rows when some column max moved (rare after the first tiles).
-    if (__ballot(alpha != 1.f) != 0) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float a = row_value<kG>(alpha, g, i);
-#pragma unroll
-        for (int d = 0; d < 8; ++d) o[d][i] *= a;
-      }
-    }
-    // P as the A operand: row r (head), k = tokens 4g..4g+3 (RNE bf16 pack).
-    const bf16x2_t p01 = {static_cast<__bf16>(pr[0]), static_cast<__bf16>(pr[1])};
-    const bf16x2_t p23 = {static_cast<__bf16>(pr[2]), static_cast<__bf16>(pr[3])};
-    const short4_t pa = __builtin_bit_cast(
-        short4_t, make_uint2(__builtin_bit_cast(uint32_t, p01), __builtin_bit_cast(uint32_t, p23)));
-    // V rows past the context (inside a valid page) may hold anything: zero
-    // them so that P = 0 never meets a NaN.
-    uint4 vr[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      vr[i] = (page >= 0 && tok0 + 4 * g + i < tok_end) ? v_row(cur, i) : make_uint4(0, 0, 0, 0);
-#pragma unroll
-    for (int d = 0; d < 8; ++d) {
-      const int wi = d >> 1;
-      uint32_t b01, b23;
-      if (d & 1) {
-        b01 = hi_pair(word(vr[0], wi), word(vr[1], wi));
-        b23 = hi_pair(word(vr[2], wi), word(vr[3], wi));
-      } else {
-        b01 = lo_pair(word(vr[0], wi), word(vr[1], wi));
-        b23 = lo_pair(word(vr[2], wi), word(vr[3], wi));
-      }
-      const short4_t vb = __builtin_bit_cast(short4_t, make_uint2(b01, b23));
-      o[d] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, vb, o[d], 0, 0, 0);
-    }
-  };
-
-  // Chunks of U tiles: issue all U tiles' loads, then consume them in order
-  // (the compiler waits for tile u with vmcnt = loads issued after it).  Loads
-  // are unconditional; tiles past the end re-read the last tile (cache hits).
-  const int ntiles = (tok_end - tok_begin + kTile - 1) / kTile;
-  for (int t0 = 0; t0 < ntiles; t0 += U) {
-    TileRegs<kFp8> buf[U];
-    int64_t pg[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int tok0 = tok_begin + kTile * min(t0 + u, ntiles - 1);
-      pg[u] = page_of(P, b, tok0);
-      load_tile<kFp8>(P, pg[u] < 0 ? 0 : pg[u], h, tok0, r, g, buf[u]);
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-      if (t0 + u < ntiles) process(tok_begin + kTile * (t0 + u), pg[u], buf[u]);
-  }
-
-  // Column sums of l over the 4 lane groups: every lane of column j holds l_j.
-  l_run = pair_sum(l_run);
-
-  // Epilogue: lane (r, g) holds O[head 4g+i][dims 8r .. 8r+7] for i < 4.
-  const float vs = (kFp8 && P.v_scale) ? P.v_scale[h] : 1.f;
-  const int64_t part_row = (static_cast<int64_t>(b) * P.num_kv_heads + h) * P.max_parts + p;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int j = 4 * g + i;
-    if (j >= kG || j >= gqa) continue;
-    if (nparts == 1) {
-      const float l = row_value<kG>(l_run, g, i);
-      const float f = l > 0.f ? vs / l : 0.f;
-      uint32_t w[4];
-#pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        const bf16x2_t pk = {static_cast<__bf16>(o[2 * d][i] * f),
-                             static_cast<__bf16>(o[2 * d + 1][i] * f)};
-        w[d] = __builtin_bit_cast(uint32_t, pk);
-      }
-      *reinterpret_cast<uint4*>(P.out + b * P.out_row_stride +
-                                static_cast<int64_t>(h * gqa + j) * kHead + 8 * r) =
-          make_uint4(w[0], w[1], w[2], w[3]);
-    } else {
-      float* dst = P.part_o + (part_row * gqa + j) * kHead + 8 * r;
-      *reinterpret_cast<float4*>(dst) =
-          make_float4(o[0][i] * vs, o[1][i] * vs, o[2][i] * vs, o[3][i] * vs);
-      *reinterpret_cast<float4*>(dst + 4) =
-          make_float4(o[4][i] * vs, o[5][i] * vs, o[6][i] * vs, o[7][i] * vs);
-    }
-  }
-  if (nparts > 1 && g == 0 && head_ok) {
-    P.part_ml[(part_row * gqa + r) * 2 + 0] = m_run;
-    P.part_ml[(part_row * gqa + r) * 2 + 1] = l_run;
+  WaveState<kG, kFp8, U> st;
+  st.run(P, b, h, tok_begin, tok_end, r, g);
+  if (nparts == 1) {
+    st.write_final(P, b, h, r, g);
+  } else {
+    const int64_t row0 = ((static_cast<int64_t>(b) * P.num_kv_heads + h) * P.max_parts + p) * P.gqa;
+    st.write_partial(P, row0, h, r, g);
   }
 }
 
-// Merge the partitions of each (sequence, query head) with more than one
-// partition; write zeros for empty sequences.  One wave per (hq, b); each lane
-// owns two output dims.
-__global__ __launch_bounds__(64) void paged_decode_reduce_kernel(
-    uint16_t* __restrict__ out, int64_t out_row_stride, const int32_t* __restrict__ ctx_lens,
-    int num_kv_heads, int gqa, int part_tokens, int max_parts,
-    const float* __restrict__ part_o, const float* __restrict__ part_ml) {
-  const int hq = blockIdx.x;
-  const int b = blockIdx.y;
-  const int lane = threadIdx.x;
-  const int ctx = ctx_lens[b];
-  uint16_t* orow = out + b * out_row_stride + static_cast<int64_t>(hq) * kHead;
-  if (ctx <= 0) {
-    reinterpret_cast<uint32_t*>(orow)[lane] = 0u;
-    return;
+__device__ __forceinline__ int tiles_of(int ctx) { return ctx > 0 ? (ctx + kTile - 1) / kTile : 0; }
+
+// Balanced schedule: work-group w (of num_groups per kv-head group) takes
+// tiles [w * S, (w+1) * S) of the concatenation of all sequences' tiles,
+// S = ceil(total / num_groups).  Partial rows of a cut sequence:
+// ((w * 2 + slot) * Hk + h) * G + j, slot 0 = the group's first segment,
+// slot 1 = its last (a group holds at most one cut sequence at each end).
+template <int NH, int kG, bool kFp8, int U>
+__global__ __launch_bounds__(NH * 64) void paged_decode_balanced_kernel(DecodeParams P) {
+  extern __shared__ int32_t toff[];  // [batch + 1] tile prefix sums
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int batch = P.batch;
+  if (wave == 0) {
+    int carry = 0;
+    for (int base = 0; base < batch; base += 64) {
+      const int i = base + lane;
+      int v = i < batch ? tiles_of(P.ctx_lens[i]) : 0;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_up(v, off, 64);
+        if (lane >= off) v += y;
+      }
+      if (i < batch) toff[i + 1] = carry + v;
+      carry += __shfl(v, 63, 64);
+    }
+    if (lane == 0) toff[0] = 0;
   }
-  const int nparts = min((ctx + part_tokens - 1) / part_tokens, max_parts);
-  if (nparts <= 1) return;  // written by the partials kernel
-  const int h = hq / gqa;
-  const int j = hq - h * gqa;
-  const int64_t base = (static_cast<int64_t>(b) * num_kv_heads + h) * max_parts;
+  __syncthreads();
+  const int total = toff[batch];
+  const int S = max(1, (total + P.num_groups - 1) / P.num_groups);
+  const int w = blockIdx.x;
+  if (w == 0 && blockIdx.y == 0) {  // publish the schedule for the merge kernel
+    for (int i = threadIdx.x; i <= batch; i += blockDim.x) P.tile_off[i] = toff[i];
+    if (threadIdx.x == 0) P.tile_off[batch + 1] = S;
+  }
+  const int t_lo = w * S;
+  const int t_hi = min(total, t_lo + S);
+  if (t_lo >= total) return;
+  const int h = blockIdx.y * NH + wave;
+  if (h >= P.num_kv_heads) return;  // uniform over the wave; no barriers follow
+  const int r = lane & 15;
+  const int g = lane >> 4;
+  // First sequence with tiles at t_lo: largest b with toff[b] <= t_lo.
+  int lo = 0, hi = batch;  // invariant: toff[lo] <= t_lo < toff[hi]
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (toff[mid] <= t_lo) lo = mid; else hi = mid;
+  }
+  WaveState<kG, kFp8, U> st;
+  for (int b = lo; b < batch && toff[b] < t_hi; ++b) {
+    const int s_lo = max(t_lo, toff[b]) - toff[b];
+    const int s_hi = min(t_hi, toff[b + 1]) - toff[b];
+    if (s_hi <= s_lo) continue;  // empty sequence
+    const int ctx = P.ctx_lens[b];
+    st.run(P, b, h, kTile * s_lo, min(ctx, kTile * s_hi), r, g);
+    if (toff[b] >= t_lo && toff[b + 1] <= t_hi) {
+      st.write_final(P, b, h, r, g);
+    } else {
+      const int slot = toff[b] <= t_lo ? 0 : 1;
+      const int64_t row0 = ((static_cast<int64_t>(w) * 2 + slot) * P.num_kv_heads + h) * P.gqa;
+      st.write_partial(P, row0, h, r, g);
+    }
+  }
+}
+
+// Merge of one (query head hq, sequence b): one wave, each lane owns two dims.
+// `rows` lists the partial rows of the sequence (index into part_o / part_ml).
+__device__ __forceinline__ void merge_rows(uint16_t* orow, const float* part_o,
+                                           const float* part_ml, int64_t first_row,
+                                           int64_t row_stride, int nrows, int lane,
+                                           int64_t alt_first_row) {
   float M = kNegInf;
-  for (int p = lane; p < nparts; p += 64) M = fmaxf(M, part_ml[((base + p) * gqa + j) * 2]);
+  for (int k = lane; k < nrows; k += 64) {
+    const int64_t row = (k == 0 ? alt_first_row : first_row + k * row_stride);
+    M = fmaxf(M, part_ml[row * 2]);
+  }
   M = wave_max(M);
   float L = 0.f, o0 = 0.f, o1 = 0.f;
   if (M != kNegInf) {
-    for (int p = 0; p < nparts; ++p) {
-      const int64_t row = (base + p) * gqa + j;
-      const float f = exp2f(part_ml[row * 2] - M);
+    for (int k = 0; k < nrows; ++k) {
+      const int64_t row = (k == 0 ? alt_first_row : first_row + k * row_stride);
+      const float f = __builtin_amdgcn_exp2f(part_ml[row * 2] - M);
       L += f * part_ml[row * 2 + 1];
       const float2 ov = reinterpret_cast<const float2*>(part_o + row * kHead)[lane];
       o0 += f * ov.x;
@@ -416,24 +535,98 @@ __global__ __launch_bounds__(64) void paged_decode_reduce_kernel(
     }
   }
   const float inv = L > 0.f ? 1.f / L : 0.f;
-  reinterpret_cast<uint32_t*>(orow)[lane] =
-      (static_cast<uint32_t>(f32_to_bf16(o1 * inv)) << 16) | f32_to_bf16(o0 * inv);
+  const bf16x2_t pk = {static_cast<__bf16>(o0 * inv), static_cast<__bf16>(o1 * inv)};
+  reinterpret_cast<uint32_t*>(orow)[lane] = __builtin_bit_cast(uint32_t, pk);
 }
 
-constexpr int kMaxWavesPerGroup = 8;  // kv heads (waves) per work-group
-constexpr int kChunk = 4;             // tiles loaded per wave before consuming them
-constexpr int kPartQuant = 64;        // partition granularity in tokens
+// Fixed partitions: merge sequences with more than one partition; zero empty ones.
+__global__ __launch_bounds__(64) void paged_decode_partition_reduce_kernel(DecodeParams P) {
+  const int hq = blockIdx.x;
+  const int b = blockIdx.y;
+  const int lane = threadIdx.x;
+  const int ctx = P.ctx_lens[b];
+  uint16_t* orow = P.out + b * P.out_row_stride + static_cast<int64_t>(hq) * kHead;
+  if (ctx <= 0) {
+    reinterpret_cast<uint32_t*>(orow)[lane] = 0u;
+    return;
+  }
+  const int nparts = min((ctx + P.part_tokens - 1) / P.part_tokens, P.max_parts);
+  if (nparts <= 1) return;  // written by the partition kernel
+  const int h = hq / P.gqa;
+  const int j = hq - h * P.gqa;
+  const int64_t first = (static_cast<int64_t>(b) * P.num_kv_heads + h) * P.max_parts * P.gqa + j;
+  merge_rows(orow, P.part_o, P.part_ml, first, P.gqa, nparts, lane, first);
+}
 
-struct Shape {
-  int64_t batch;
-  int hq, hk, gqa, head;
-  int64_t part_tokens, max_parts;
-};
+// Balanced schedule: merge sequences cut across work-groups; zero empty ones.
+__global__ __launch_bounds__(64) void paged_decode_balanced_reduce_kernel(DecodeParams P) {
+  const int hq = blockIdx.x;
+  const int b = blockIdx.y;
+  const int lane = threadIdx.x;
+  uint16_t* orow = P.out + b * P.out_row_stride + static_cast<int64_t>(hq) * kHead;
+  const int t0 = P.tile_off[b];
+  const int t1 = P.tile_off[b + 1];
+  const int S = P.tile_off[P.batch + 1];
+  if (t1 <= t0) {
+    reinterpret_cast<uint32_t*>(orow)[lane] = 0u;
+    return;
+  }
+  const int w0 = t0 / S;
+  const int w1 = (t1 - 1) / S;
+  if (w0 == w1) return;  // finished in place by work-group w0
+  const int h = hq / P.gqa;
+  const int j = hq - h * P.gqa;
+  const int64_t hk = P.num_kv_heads;
+  // Group w0 holds the sequence in slot 1 unless the sequence starts its range;
+  // groups w0+1 .. w1 hold it in slot 0.
+  const int slot0 = t0 > w0 * S ? 1 : 0;
+  const int64_t first_alt = ((static_cast<int64_t>(w0) * 2 + slot0) * hk + h) * P.gqa + j;
+  const int64_t first = ((static_cast<int64_t>(w0) * 2 + 0) * hk + h) * P.gqa + j;
+  merge_rows(orow, P.part_o, P.part_ml, first, 2 * hk * P.gqa, w1 - w0 + 1, lane, first_alt);
+}
 
-int64_t workspace_bytes(int64_t batch, int hq, int hk, int64_t max_parts) {
-  const int64_t rows = batch * hq * max_parts;  // = B * Hk * max_parts * gqa
-  const int64_t o_bytes = (rows * kHead * 4 + 255) / 256 * 256;
-  return o_bytes + rows * 2 * 4;
+// Tuning knobs (compile-time): tiles per load set, and whether two sets are
+// double-buffered (FK_DECODE_PIPE=1) or one set is loaded then consumed.
+#ifndef FK_DECODE_CHUNK
+#define FK_DECODE_CHUNK 4
+#endif
+constexpr int kChunk = FK_DECODE_CHUNK;  // tiles loaded per wave per set
+constexpr int kMaxWavesPerGroup = 8;     // kv heads (waves) per work-group
+constexpr int kPartQuant = 64;           // fixed-partition granularity in tokens
+constexpr int kMaxBalancedBatch = 8192;  // tile prefix sums live in LDS
+
+int num_cus() {
+  static int cached = -1;
+  if (cached < 0) {
+    int dev = 0;
+    hipDeviceProp_t prop;
+    if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&prop, dev) == hipSuccess &&
+        prop.multiProcessorCount > 0)
+      cached = prop.multiProcessorCount;
+    else
+      cached = 256;  // MI355X
+    (void)hipGetLastError();
+  }
+  return cached;
+}
+
+int waves_per_group(int num_kv_heads) {
+  return num_kv_heads < kMaxWavesPerGroup ? num_kv_heads : kMaxWavesPerGroup;
+}
+
+// Workspace layout: part_o rows, part_ml rows (256-byte aligned), then (balanced
+// only) batch + 2 int32 for the tile prefix sums and the range size.
+int64_t o_region(int64_t rows) { return (rows * kHead * 4 + 255) / 256 * 256; }
+int64_t ml_region(int64_t rows) { return (rows * 2 * 4 + 255) / 256 * 256; }
+
+int64_t partial_rows(bool balanced, int64_t batch, int num_heads, int64_t max_parts) {
+  // balanced: max_parts = work-groups per kv-head group, 2 slots each.
+  return balanced ? max_parts * 2 * num_heads : batch * num_heads * max_parts;
+}
+
+int64_t workspace_bytes(bool balanced, int64_t batch, int num_heads, int64_t max_parts) {
+  const int64_t rows = partial_rows(balanced, batch, num_heads, max_parts);
+  return o_region(rows) + ml_region(rows) + (balanced ? (batch + 2) * 4 : 0);
 }
 
 int validate(const char* name, int64_t batch, int num_heads, int num_kv_heads, int head_size,
@@ -449,60 +642,33 @@ int validate(const char* name, int64_t batch, int num_heads, int num_kv_heads, i
   if (num_heads / num_kv_heads > 16)
     return set_error(FK_ERR_UNSUPPORTED, "%s: GQA group %d > 16 unsupported", name,
                      num_heads / num_kv_heads);
-  FK_REQUIRE(part_tokens > 0 && part_tokens % kPartQuant == 0 && part_tokens <= (1 << 30),
-             "%s: part_tokens %lld must be a positive multiple of %d", name,
-             (long long)part_tokens, kPartQuant);
+  if (part_tokens == 0) {
+    FK_REQUIRE(batch <= kMaxBalancedBatch, "%s: balanced schedule supports batch <= %d", name,
+               kMaxBalancedBatch);
+  } else {
+    FK_REQUIRE(part_tokens > 0 && part_tokens % kPartQuant == 0 && part_tokens <= (1 << 30),
+               "%s: part_tokens %lld must be 0 (balanced) or a positive multiple of %d", name,
+               (long long)part_tokens, kPartQuant);
+  }
   FK_REQUIRE(max_parts > 0 && max_parts <= 65535, "%s: max_parts %lld out of range", name,
              (long long)max_parts);
   return FK_OK;
 }
 
-}  // namespace
-}  // namespace fk
+struct Launch {
+  DecodeParams P;
+  bool balanced;
+  bool fp8;
+  int nh;
+  dim3 grid;
+};
 
-using namespace fk;
-
-extern "C" int64_t fk_paged_decode_workspace_bytes(int64_t batch, int num_heads,
-                                                   int num_kv_heads, int head_size,
-                                                   int64_t max_parts) {
-  (void)num_kv_heads;
-  (void)head_size;
-  if (batch <= 0 || num_heads <= 0 || max_parts <= 0) return 0;
-  return workspace_bytes(batch, num_heads, num_kv_heads, max_parts);
-}
-
-extern "C" int fk_paged_decode_plan(int64_t batch, int num_kv_heads, int64_t max_seq_len,
-                                    int num_splits, int64_t* part_tokens, int64_t* max_parts) {
-  FK_REQUIRE(part_tokens && max_parts, "fk_paged_decode_plan: null output pointer");
-  FK_REQUIRE(batch >= 0 && num_kv_heads > 0 && max_seq_len >= 0 && num_splits >= 0,
-             "fk_paged_decode_plan: negative argument");
-  constexpr int64_t kQuant = kPartQuant;
-  const int64_t L = max_seq_len > 0 ? max_seq_len : 1;
-  int64_t part;
-  if (num_splits > 0) {
-    part = (L + num_splits - 1) / num_splits;
-  } else {
-    // One wave streams one (sequence, kv head, partition): aim for ~8192 waves
-    // (256 CUs x 8 resident waves x ~4 rounds) with at least 256 tokens each.
-    const int64_t units = (batch > 0 ? batch : 1) * num_kv_heads;
-    part = (L * units + 8191) / 8192;
-    if (part < 256) part = 256;
-  }
-  part = (part + kQuant - 1) / kQuant * kQuant;
-  *part_tokens = part;
-  *max_parts = (L + part - 1) / part;
-  return FK_OK;
-}
-
-static int launch_partials(void* out, int64_t out_row_stride, const void* q,
-                           int64_t q_row_stride, const void* k_cache, const void* v_cache,
-                           int kv_dtype, const float* k_scale, const float* v_scale,
-                           const int32_t* block_tables, int64_t bt_row_stride,
-                           const int32_t* ctx_lens, int64_t batch, int num_heads,
-                           int num_kv_heads, int head_size, int block_size, int64_t num_blocks,
-                           float scale, int64_t part_tokens, int64_t max_parts, void* workspace,
-                           int64_t ws_bytes, hipStream_t stream) {
-  const char* name = "fk_paged_decode";
+int prepare(const char* name, Launch& L, void* out, int64_t out_row_stride, const void* q,
+            int64_t q_row_stride, const void* k_cache, const void* v_cache, int kv_dtype,
+            const float* k_scale, const float* v_scale, const int32_t* block_tables,
+            int64_t bt_row_stride, const int32_t* ctx_lens, int64_t batch, int num_heads,
+            int num_kv_heads, int head_size, int block_size, int64_t num_blocks, float scale,
+            int64_t part_tokens, int64_t max_parts, void* workspace, int64_t ws_bytes) {
   int rc = validate(name, batch, num_heads, num_kv_heads, head_size, part_tokens, max_parts);
   if (rc != FK_OK) return rc;
   FK_REQUIRE(block_size >= kTile && (block_size & (block_size - 1)) == 0,
@@ -517,17 +683,17 @@ static int launch_partials(void* out, int64_t out_row_stride, const void* q,
              name);
   FK_REQUIRE(num_blocks >= 1, "%s: the cache must hold at least one block", name);
   FK_REQUIRE(aligned16(q) && aligned16(k_cache) && aligned16(v_cache) && aligned16(out) &&
-                 q_row_stride % 8 == 0 && out_row_stride % 2 == 0,
-             "%s: q/out/cache must be 16-byte aligned with q rows a multiple of 8 elements",
-             name);
-  const int64_t need = workspace_bytes(batch, num_heads, num_kv_heads, max_parts);
-  if (max_parts > 1 && (workspace == nullptr || ws_bytes < need))
+                 q_row_stride % 8 == 0 && out_row_stride % 8 == 0,
+             "%s: q/out/cache must be 16-byte aligned with rows a multiple of 8 elements", name);
+  const bool balanced = part_tokens == 0;
+  const bool needs_ws = balanced || max_parts > 1;
+  const int64_t need = workspace_bytes(balanced, batch, num_heads, max_parts);
+  if (needs_ws && (workspace == nullptr || ws_bytes < need))
     return set_error(FK_ERR_WORKSPACE, "%s: workspace of %lld bytes < %lld required", name,
                      (long long)ws_bytes, (long long)need);
-  FK_REQUIRE(max_parts == 1 || aligned16(workspace), "%s: workspace must be 16-byte aligned",
-             name);
+  FK_REQUIRE(!needs_ws || aligned16(workspace), "%s: workspace must be 16-byte aligned", name);
 
-  DecodeParams P;
+  DecodeParams& P = L.P;
   P.out = static_cast<uint16_t*>(out);
   P.out_row_stride = out_row_stride;
   P.q = static_cast<const uint16_t*>(q);
@@ -546,71 +712,91 @@ static int launch_partials(void* out, int64_t out_row_stride, const void* q,
   P.max_parts = static_cast<int>(max_parts);
   P.num_blocks = num_blocks;
   P.scale_log2 = scale * kLog2e;
-  const int64_t rows = batch * num_heads * max_parts;
-  P.part_o = static_cast<float*>(workspace);
-  P.part_ml = workspace ? reinterpret_cast<float*>(static_cast<char*>(workspace) +
-                                                   (rows * kHead * 4 + 255) / 256 * 256)
+  P.batch = static_cast<int>(batch);
+  P.num_groups = static_cast<int>(max_parts);
+  const int64_t rows = partial_rows(balanced, batch, num_heads, max_parts);
+  char* ws = static_cast<char*>(workspace);
+  P.part_o = needs_ws ? reinterpret_cast<float*>(ws) : nullptr;
+  P.part_ml = needs_ws ? reinterpret_cast<float*>(ws + o_region(rows)) : nullptr;
+  P.tile_off = balanced ? reinterpret_cast<int32_t*>(ws + o_region(rows) + ml_region(rows))
                         : nullptr;
-
-  const int nh = num_kv_heads < kMaxWavesPerGroup ? num_kv_heads : kMaxWavesPerGroup;
-  const dim3 grid(static_cast<unsigned>(max_parts),
-                  static_cast<unsigned>((num_kv_heads + nh - 1) / nh),
-                  static_cast<unsigned>(batch));
-  const bool fp8 = kv_dtype == FK_DTYPE_FP8_E4M3FN;
-#define FK_PD_NH(NH, G)                                                                   \
-  do {                                                                                    \
-    if (fp8)                                                                              \
-      hipLaunchKernelGGL((paged_decode_partials_kernel<NH, G, true, kChunk>), grid,       \
-                         dim3(NH * 64), 0, stream, P);                                    \
-    else                                                                                  \
-      hipLaunchKernelGGL((paged_decode_partials_kernel<NH, G, false, kChunk>), grid,      \
-                         dim3(NH * 64), 0, stream, P);                                    \
-  } while (0)
-#define FK_PD(G)                            \
-  do {                                      \
-    switch (nh) {                           \
-      case 1: FK_PD_NH(1, G); break;        \
-      case 2: FK_PD_NH(2, G); break;        \
-      case 4: FK_PD_NH(4, G); break;        \
-      default: FK_PD_NH(8, G); break;       \
-    }                                       \
-  } while (0)
-  if (P.gqa <= 4)
-    FK_PD(4);
-  else if (P.gqa <= 8)
-    FK_PD(8);
-  else
-    FK_PD(16);
-#undef FK_PD
-#undef FK_PD_NH
-  return check_launch(name);
+  L.balanced = balanced;
+  L.fp8 = kv_dtype == FK_DTYPE_FP8_E4M3FN;
+  L.nh = waves_per_group(num_kv_heads);
+  const unsigned hgroups = static_cast<unsigned>((num_kv_heads + L.nh - 1) / L.nh);
+  L.grid = balanced ? dim3(static_cast<unsigned>(max_parts), hgroups, 1)
+                    : dim3(static_cast<unsigned>(max_parts), hgroups, static_cast<unsigned>(batch));
+  return FK_OK;
 }
 
-static int launch_reduce(void* out, int64_t out_row_stride, const int32_t* ctx_lens,
-                         int64_t batch, int num_heads, int num_kv_heads, int head_size,
-                         int64_t part_tokens, int64_t max_parts, void* workspace,
-                         int64_t ws_bytes, hipStream_t stream) {
-  const char* name = "fk_paged_decode_reduce";
-  int rc = validate(name, batch, num_heads, num_kv_heads, head_size, part_tokens, max_parts);
-  if (rc != FK_OK) return rc;
-  if (batch == 0) return FK_OK;
-  FK_REQUIRE(out && ctx_lens, "%s: null pointer", name);
-  const int64_t need = workspace_bytes(batch, num_heads, num_kv_heads, max_parts);
-  if (max_parts > 1 && (workspace == nullptr || ws_bytes < need))
-    return set_error(FK_ERR_WORKSPACE, "%s: workspace of %lld bytes < %lld required", name,
-                     (long long)ws_bytes, (long long)need);
-  const int64_t rows = batch * num_heads * max_parts;
-  const float* part_o = static_cast<const float*>(workspace);
-  const float* part_ml =
-      workspace ? reinterpret_cast<const float*>(static_cast<const char*>(workspace) +
-                                                 (rows * kHead * 4 + 255) / 256 * 256)
-                : nullptr;
-  hipLaunchKernelGGL(paged_decode_reduce_kernel,
-                     dim3(static_cast<unsigned>(num_heads), static_cast<unsigned>(batch)),
-                     dim3(64), 0, stream, static_cast<uint16_t*>(out), out_row_stride, ctx_lens,
-                     num_kv_heads, num_heads / num_kv_heads, static_cast<int>(part_tokens),
-                     static_cast<int>(max_parts), part_o, part_ml);
-  return check_launch(name);
+template <int NH, int G, bool FP8>
+void launch_main(const Launch& L, hipStream_t stream) {
+  if (L.balanced) {
+    const size_t lds = static_cast<size_t>(L.P.batch + 1) * sizeof(int32_t);
+    hipLaunchKernelGGL((paged_decode_balanced_kernel<NH, G, FP8, kChunk>), L.grid, dim3(NH * 64),
+                       lds, stream, L.P);
+  } else {
+    hipLaunchKernelGGL((paged_decode_partition_kernel<NH, G, FP8, kChunk>), L.grid,
+                       dim3(NH * 64), 0, stream, L.P);
+  }
+}
+
+template <int G, bool FP8>
+void launch_main_nh(const Launch& L, hipStream_t stream) {
+  switch (L.nh) {
+    case 1: launch_main<1, G, FP8>(L, stream); break;
+    case 2: launch_main<2, G, FP8>(L, stream); break;
+    case 4: launch_main<4, G, FP8>(L, stream); break;
+    default: launch_main<8, G, FP8>(L, stream); break;
+  }
+}
+
+template <int G>
+void launch_main_g(const Launch& L, hipStream_t stream) {
+  if (L.fp8)
+    launch_main_nh<G, true>(L, stream);
+  else
+    launch_main_nh<G, false>(L, stream);
+}
+
+}  // namespace
+}  // namespace fk
+
+using namespace fk;
+
+extern "C" int fk_paged_decode_plan(int64_t batch, int num_heads, int num_kv_heads, int head_size,
+                                    int64_t max_seq_len, int num_splits, int64_t* part_tokens,
+                                    int64_t* max_parts, int64_t* workspace_bytes_out) {
+  FK_REQUIRE(part_tokens && max_parts && workspace_bytes_out,
+             "fk_paged_decode_plan: null output pointer");
+  FK_REQUIRE(batch >= 0 && num_heads > 0 && num_kv_heads > 0 && max_seq_len >= 0 &&
+                 num_splits >= 0,
+             "fk_paged_decode_plan: negative argument");
+  const int64_t L = max_seq_len > 0 ? max_seq_len : 1;
+  if (num_splits == 0 && batch <= kMaxBalancedBatch) {
+    // Balanced: one work-group per CU for each kv-head group when a group
+    // fills a CU (8 waves), proportionally more for fewer kv heads.
+    const int nh = waves_per_group(num_kv_heads);
+    *part_tokens = 0;
+    *max_parts = static_cast<int64_t>(num_cus()) * (kMaxWavesPerGroup / nh);
+  } else {
+    int64_t part;
+    if (num_splits > 0) {
+      part = (L + num_splits - 1) / num_splits;
+    } else {
+      // ~8192 waves (one per (sequence, kv head, partition)), >= 256 tokens each.
+      const int64_t units = (batch > 0 ? batch : 1) * num_kv_heads;
+      part = (L * units + 8191) / 8192;
+      if (part < 256) part = 256;
+    }
+    part = (part + kPartQuant - 1) / kPartQuant * kPartQuant;
+    *part_tokens = part;
+    *max_parts = (L + part - 1) / part;
+  }
+  (void)head_size;
+  *workspace_bytes_out =
+      batch > 0 ? workspace_bytes(*part_tokens == 0, batch, num_heads, *max_parts) : 0;
+  return FK_OK;
 }
 
 extern "C" int fk_paged_decode_partials(
@@ -618,20 +804,45 @@ extern "C" int fk_paged_decode_partials(
     const void* v_cache, int kv_dtype, const float* k_scale, const float* v_scale,
     const int32_t* block_tables, int64_t bt_row_stride, const int32_t* ctx_lens, int64_t batch,
     int num_heads, int num_kv_heads, int head_size, int block_size, int64_t num_blocks,
-    float scale, int64_t part_tokens, int64_t max_parts, void* workspace,
-    int64_t workspace_bytes_, void* stream) {
-  return launch_partials(out, out_row_stride, q, q_row_stride, k_cache, v_cache, kv_dtype,
-                         k_scale, v_scale, block_tables, bt_row_stride, ctx_lens, batch,
-                         num_heads, num_kv_heads, head_size, block_size, num_blocks, scale,
-                         part_tokens, max_parts, workspace, workspace_bytes_, as_stream(stream));
+    float scale, int64_t part_tokens, int64_t max_parts, void* workspace, int64_t ws_bytes,
+    void* stream) {
+  Launch L;
+  int rc = prepare("fk_paged_decode_partials", L, out, out_row_stride, q, q_row_stride, k_cache,
+                   v_cache, kv_dtype, k_scale, v_scale, block_tables, bt_row_stride, ctx_lens,
+                   batch, num_heads, num_kv_heads, head_size, block_size, num_blocks, scale,
+                   part_tokens, max_parts, workspace, ws_bytes);
+  if (rc != FK_OK || batch == 0) return rc;
+  hipStream_t s = as_stream(stream);
+  if (L.P.gqa <= 4)
+    launch_main_g<4>(L, s);
+  else if (L.P.gqa <= 8)
+    launch_main_g<8>(L, s);
+  else
+    launch_main_g<16>(L, s);
+  return check_launch("fk_paged_decode_partials");
 }
 
-extern "C" int fk_paged_decode_reduce(void* out, int64_t out_row_stride, const int32_t* ctx_lens,
-                                      int64_t batch, int num_heads, int num_kv_heads,
-                                      int head_size, int64_t part_tokens, int64_t max_parts,
-                                      void* workspace, int64_t workspace_bytes_, void* stream) {
-  return launch_reduce(out, out_row_stride, ctx_lens, batch, num_heads, num_kv_heads, head_size,
-                       part_tokens, max_parts, workspace, workspace_bytes_, as_stream(stream));
+extern "C" int fk_paged_decode_reduce(
+    void* out, int64_t out_row_stride, const void* q, int64_t q_row_stride, const void* k_cache,
+    const void* v_cache, int kv_dtype, const float* k_scale, const float* v_scale,
+    const int32_t* block_tables, int64_t bt_row_stride, const int32_t* ctx_lens, int64_t batch,
+    int num_heads, int num_kv_heads, int head_size, int block_size, int64_t num_blocks,
+    float scale, int64_t part_tokens, int64_t max_parts, void* workspace, int64_t ws_bytes,
+    void* stream) {
+  Launch L;
+  int rc = prepare("fk_paged_decode_reduce", L, out, out_row_stride, q, q_row_stride, k_cache,
+                   v_cache, kv_dtype, k_scale, v_scale, block_tables, bt_row_stride, ctx_lens,
+                   batch, num_heads, num_kv_heads, head_size, block_size, num_blocks, scale,
+                   part_tokens, max_parts, workspace, ws_bytes);
+  if (rc != FK_OK || batch == 0) return rc;
+  const dim3 grid(static_cast<unsigned>(num_heads), static_cast<unsigned>(batch));
+  if (L.balanced)
+    hipLaunchKernelGGL(paged_decode_balanced_reduce_kernel, grid, dim3(64), 0, as_stream(stream),
+                       L.P);
+  else
+    hipLaunchKernelGGL(paged_decode_partition_reduce_kernel, grid, dim3(64), 0, as_stream(stream),
+                       L.P);
+  return check_launch("fk_paged_decode_reduce");
 }
 
 extern "C" int fk_paged_decode(void* out, int64_t out_row_stride, const void* q,
@@ -641,14 +852,16 @@ extern "C" int fk_paged_decode(void* out, int64_t out_row_stride, const void* q,
                                const int32_t* ctx_lens, int64_t batch, int num_heads,
                                int num_kv_heads, int head_size, int block_size,
                                int64_t num_blocks, float scale, int64_t part_tokens,
-                               int64_t max_parts, void* workspace, int64_t workspace_bytes_,
+                               int64_t max_parts, void* workspace, int64_t ws_bytes,
                                void* stream) {
-  int rc = launch_partials(out, out_row_stride, q, q_row_stride, k_cache, v_cache, kv_dtype,
-                           k_scale, v_scale, block_tables, bt_row_stride, ctx_lens, batch,
-                           num_heads, num_kv_heads, head_size, block_size, num_blocks, scale,
-                           part_tokens, max_parts, workspace, workspace_bytes_,
-                           as_stream(stream));
+  int rc = fk_paged_decode_partials(out, out_row_stride, q, q_row_stride, k_cache, v_cache,
+                                    kv_dtype, k_scale, v_scale, block_tables, bt_row_stride,
+                                    ctx_lens, batch, num_heads, num_kv_heads, head_size,
+                                    block_size, num_blocks, scale, part_tokens, max_parts,
+                                    workspace, ws_bytes, stream);
   if (rc != FK_OK) return rc;
-  return launch_reduce(out, out_row_stride, ctx_lens, batch, num_heads, num_kv_heads, head_size,
-                       part_tokens, max_parts, workspace, workspace_bytes_, as_stream(stream));
+  return fk_paged_decode_reduce(out, out_row_stride, q, q_row_stride, k_cache, v_cache, kv_dtype,
+                                k_scale, v_scale, block_tables, bt_row_stride, ctx_lens, batch,
+                                num_heads, num_kv_heads, head_size, block_size, num_blocks, scale,
+                                part_tokens, max_parts, workspace, ws_bytes, stream);
 }

@@ -15,6 +15,7 @@ from __future__ import annotations
 
 import math
 from ctypes import c_void_p
+from typing import NamedTuple
 
 import torch
 
@@ -191,15 +192,19 @@ def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
 # ---------------------------------------------------------------------------
 # Paged decode attention
 # ---------------------------------------------------------------------------
-def paged_decode_plan(batch: int, num_kv_heads: int, max_seq_len: int,
-                      num_splits: int = 0) -> tuple[int, int]:
-    """(part_tokens, max_parts) for a launch over contexts of at most max_seq_len."""
-    return _native.plan(batch, num_kv_heads, max_seq_len, num_splits)
+class DecodePlan(NamedTuple):
+    """Schedule of a paged-decode launch (fk_paged_decode_plan)."""
+    part_tokens: int      # 0 = length-balanced schedule, else fixed partition size
+    max_parts: int        # work-groups per kv-head group (balanced) / partitions per sequence
+    workspace_bytes: int  # device workspace the launch needs
 
 
-def paged_decode_workspace_bytes(batch: int, num_heads: int, num_kv_heads: int, head_size: int,
-                                 max_parts: int) -> int:
-    return _native.workspace_bytes(batch, num_heads, num_kv_heads, head_size, max_parts)
+def paged_decode_plan(batch: int, num_heads: int, num_kv_heads: int, head_size: int,
+                      max_seq_len: int, num_splits: int = 0) -> DecodePlan:
+    """Plan a launch over contexts of at most max_seq_len.  num_splits = 0 picks the
+    length-balanced schedule; num_splits > 0 asks for that many fixed partitions."""
+    return DecodePlan(*_native.plan(batch, num_heads, num_kv_heads, head_size, max_seq_len,
+                                    num_splits))
 
 
 def _check_decode(out, q, k_cache, v_cache, block_table, cache_seqlens, k_scale, v_scale):
@@ -263,15 +268,13 @@ def paged_decode_phases(out, q, k_cache, v_cache, block_table, cache_seqlens, so
                  kvd, _ptr(k_scale), _ptr(v_scale), _ptr(block_table), block_table.stride(0),
                  _ptr(cache_seqlens), b, hq, hk, d, bs, nb, float(softmax_scale), part_tokens,
                  max_parts, _ptr(workspace), ws_bytes, stream)
-    red_args = (_ptr(out), out.stride(0), _ptr(cache_seqlens), b, hq, hk, d, part_tokens,
-                max_parts, _ptr(workspace), ws_bytes, stream)
     fp, fr = lib.fk_paged_decode_partials, lib.fk_paged_decode_reduce
 
     def partials():
         _native.check("fk_paged_decode_partials", fp(*part_args))
 
     def reduce():
-        _native.check("fk_paged_decode_reduce", fr(*red_args))
+        _native.check("fk_paged_decode_reduce", fr(*part_args))
 
     return partials, reduce
 

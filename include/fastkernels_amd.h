@@ -25,7 +25,7 @@
  *   fk_store_kvcache
  *       fastkernels/tasks/baseline/L1/store_kvcache.py:16-35,71-82 (Triton _store_kvcache_kernel,
  *       StoreKVCache.forward, NHD layout).
- *   fk_paged_decode_workspace_bytes / fk_paged_decode
+ *   fk_paged_decode_plan / fk_paged_decode (+ _partials / _reduce phases)
  *       fastkernels/tasks/baseline/L1/flash_attn_decode.py:113-181 (FlashAttnDecode.forward ->
  *       vllm.vllm_flash_attn.flash_attn_varlen_func with block_table, seqused_k, num_splits);
  *       split-context merge semantics of triton_unified_attention.py:697-784 (reduce_segments);
@@ -107,17 +107,20 @@ int fk_store_kvcache(const void* key, int64_t key_row_stride, const void* value,
                      const void* slot_mapping, int slot_is_i64, int64_t tokens,
                      int64_t row_elems, int elem_bytes, int64_t num_slots, void* stream);
 
-/* Bytes of split-context workspace fk_paged_decode needs for this launch shape.
- * part_tokens: tokens per partition as returned by fk_paged_decode_plan. */
-int64_t fk_paged_decode_workspace_bytes(int64_t batch, int num_heads, int num_kv_heads,
-                                        int head_size, int64_t max_parts);
-
-/* Chooses the partition size (tokens per split-context work-group) for a
- * launch: num_splits > 0 asks for that many partitions over max_seq_len;
- * num_splits == 0 picks a size that fills the GPU.  Writes the partition size
- * and the partition count per sequence.  Host-only arithmetic (no device call). */
-int fk_paged_decode_plan(int64_t batch, int num_kv_heads, int64_t max_seq_len,
-                         int num_splits, int64_t* part_tokens, int64_t* max_parts);
+/* Chooses the schedule of a paged-decode launch (host-only; may query the
+ * device's CU count once).  Outputs:
+ *   part_tokens: 0 = length-balanced schedule (the default, num_splits == 0):
+ *                the tiles of all sequences are cut into max_parts equal
+ *                ranges, one work-group each;
+ *                > 0 = fixed partitions of part_tokens tokens per sequence
+ *                (num_splits > 0 asks for that many over max_seq_len, as
+ *                flash_attn_varlen_func's num_splits).
+ *   max_parts:   work-groups per kv-head group (balanced) or partitions per
+ *                sequence (fixed).
+ *   workspace_bytes: device workspace fk_paged_decode needs for this plan. */
+int fk_paged_decode_plan(int64_t batch, int num_heads, int num_kv_heads, int head_size,
+                         int64_t max_seq_len, int num_splits, int64_t* part_tokens,
+                         int64_t* max_parts, int64_t* workspace_bytes);
 
 /* Paged decode attention (one query token per sequence):
  *   out[b,h,:] = softmax(scale * q[b,h,:] . K_b^T) V_b  over the first ctx_lens[b]
@@ -128,13 +131,16 @@ int fk_paged_decode_plan(int64_t batch, int num_kv_heads, int64_t max_seq_len,
  *    (BF16, or FP8_E4M3FN dequantised as float(x) * k_scale[kv_head] /
  *    v_scale[kv_head]; scale pointers are device fp32 [num_kv_heads] or NULL = 1).
  * block_tables: int32 [batch, bt_row_stride]; entries outside [0, num_blocks),
- *    and pages past the row (index >= bt_row_stride), are masked (never read).  ctx_lens: int32 [batch]; 0 gives a zero output row.
+ *    and pages past the row (index >= bt_row_stride), are masked (never read).
+ *    ctx_lens: int32 [batch]; 0 gives a zero output row.
  * out: [batch, num_heads, head_size] BF16 rows `out_row_stride` elements apart.
- * part_tokens / max_parts: from fk_paged_decode_plan with the same max_seq_len,
- *    which must be >= every ctx_lens[b] (tokens past part_tokens*max_parts are
- *    not attended).  workspace: device memory of
- *    fk_paged_decode_workspace_bytes(...) bytes.
- * Supported: head_size 128; Hq/Hk in 1..16; block_size a power of two >= 16.
+ * part_tokens / max_parts: from fk_paged_decode_plan.  With fixed partitions,
+ *    max_seq_len must be >= every ctx_lens[b] (tokens past part_tokens *
+ *    max_parts are not attended); the balanced schedule reads the lengths on
+ *    the device and has no such bound.
+ * workspace: device memory of the plan's workspace_bytes, 16-byte aligned.
+ * Supported: head_size 128; Hq/Hk in 1..16; block_size a power of two >= 16;
+ *    batch <= 65535 (<= 8192 for the balanced schedule).
  * Replaces FlashAttnDecode.forward (flash_attn_decode.py:113-181). */
 int fk_paged_decode(void* out, int64_t out_row_stride, const void* q, int64_t q_row_stride,
                     const void* k_cache, const void* v_cache, int kv_dtype,
@@ -145,9 +151,9 @@ int fk_paged_decode(void* out, int64_t out_row_stride, const void* q, int64_t q_
                     void* workspace, int64_t workspace_bytes, void* stream);
 
 /* The two launches fk_paged_decode makes, exposed so a profiler or benchmark can
- * time them separately.  Same arguments as fk_paged_decode; the reduce merges
- * the partitions of every sequence with more than one (the partials launch
- * writes single-partition sequences straight to `out`). */
+ * time them separately.  Same arguments as fk_paged_decode.  The partials launch
+ * finishes every sequence it holds whole and writes partials for the rest; the
+ * reduce launch merges those partials and writes zero rows for empty sequences. */
 int fk_paged_decode_partials(void* out, int64_t out_row_stride, const void* q,
                              int64_t q_row_stride, const void* k_cache, const void* v_cache,
                              int kv_dtype, const float* k_scale, const float* v_scale,
@@ -157,10 +163,14 @@ int fk_paged_decode_partials(void* out, int64_t out_row_stride, const void* q,
                              int64_t num_blocks, float scale, int64_t part_tokens,
                              int64_t max_parts, void* workspace, int64_t workspace_bytes,
                              void* stream);
-int fk_paged_decode_reduce(void* out, int64_t out_row_stride, const int32_t* ctx_lens, int64_t batch, int num_heads,
-                           int num_kv_heads, int head_size, int64_t part_tokens,
-                           int64_t max_parts, void* workspace, int64_t workspace_bytes,
-                           void* stream);
+int fk_paged_decode_reduce(void* out, int64_t out_row_stride, const void* q,
+                           int64_t q_row_stride, const void* k_cache, const void* v_cache,
+                           int kv_dtype, const float* k_scale, const float* v_scale,
+                           const int32_t* block_tables, int64_t bt_row_stride,
+                           const int32_t* ctx_lens, int64_t batch, int num_heads,
+                           int num_kv_heads, int head_size, int block_size, int64_t num_blocks,
+                           float scale, int64_t part_tokens, int64_t max_parts, void* workspace,
+                           int64_t workspace_bytes, void* stream);
 
 /* SiLU-and-mul: out[r, j] = cast(cast(silu(x[r, j])) * x[r, d + j]) for j < d.
  * x: [rows, 2d] rows `x_row_stride` elements apart; out: [rows, d] rows

@@ -218,8 +218,7 @@ def run_decode(case, num_splits=0, max_seq_len=None):
     b, hq, d = case.q.shape
     hk = case.k_cache.shape[2]
     msl = case.max_seq_len if max_seq_len is None else max_seq_len
-    part, nparts = ops.paged_decode_plan(b, hk, msl, num_splits)
-    nbytes = ops.paged_decode_workspace_bytes(b, hq, hk, d, nparts)
+    part, nparts, nbytes = ops.paged_decode_plan(b, hq, hk, d, msl, num_splits)
     ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=case.q.device)
     out = torch.full_like(case.q, float("nan"))
     ops.paged_decode(out, case.q, case.k_cache, case.v_cache, case.block_tables, case.ctx_lens,
@@ -271,7 +270,7 @@ def test_paged_decode_c3_north_star(cuda):
     assert_close(got[seqs], ref[seqs], BF16_TOL, BF16_TOL, "C3")
 
 
-@pytest.mark.parametrize("num_splits", [1, 3, 16, 64])
+@pytest.mark.parametrize("num_splits", [0, 1, 3, 16, 64])
 def test_paged_decode_split_invariance(cuda, num_splits):
     """Any partition count gives the unsplit result (the LSE merge is exact)."""
     case = workloads.c3_decode(cuda, batch=6, num_heads=8, kv_heads=2, pool_blocks=64,
@@ -289,6 +288,29 @@ def test_paged_decode_gqa_blocks(cuda, hq, hk, block_size):
                                pool_blocks=pool, ctx_lens=ctx, seed=31 + hq + block_size)
     assert_close(f32(run_decode(case)), oracle_decode(case), BF16_TOL, BF16_TOL,
                  f"hq={hq} hk={hk} bs={block_size}")
+
+
+@pytest.mark.parametrize("lens", [
+    [100_000],                                  # one sequence cut across every work-group
+    [0, 1, 17, 0, 33, 0, 0, 5, 4096, 0, 16],    # empties between cut and whole sequences
+    "many",                                     # 300 short sequences: more than work-groups
+])
+def test_paged_decode_balanced_schedule(cuda, lens):
+    """The length-balanced schedule: sequences finished in place, cut across ranges,
+    and empty, against the oracle; and equal to the fixed-partition schedule."""
+    if lens == "many":
+        lens = np.random.default_rng(71).integers(0, 100, 300).tolist()
+    bs = 16
+    pool = sum((n + bs - 1) // bs for n in lens) + 3
+    case = workloads.c3_decode(cuda, num_heads=8, kv_heads=2, block_size=bs, pool_blocks=pool,
+                               ctx_lens=lens, seed=81)
+    seqs = [i for i in range(len(lens))][:64]
+    got = f32(run_decode(case, 0))
+    assert_close(got[seqs], oracle_decode(case, seqs)[seqs], BF16_TOL, BF16_TOL, "balanced")
+    assert_close(got, f32(run_decode(case, 4)), BF16_TOL, BF16_TOL, "balanced vs fixed")
+    for i, n in enumerate(lens):
+        if n == 0:
+            assert not got[i].any()
 
 
 def test_paged_decode_padded_rows_and_masked_pages(cuda):
@@ -331,9 +353,11 @@ def test_paged_decode_fp8_c5(cuda):
     case = workloads.c5_fp8_decode(cuda)
     out16 = run_decode(case, 16)
     out64 = run_decode(case, 64)
+    outb = run_decode(case, 0)
     ref = oracle_decode(case, seqs=[0, 7])
     got = f32(out64)
     assert_close(got[[0, 7]], ref[[0, 7]], FP8_TOL, FP8_TOL, "C5 vs oracle")
+    assert_close(f32(outb)[[0, 7]], ref[[0, 7]], FP8_TOL, FP8_TOL, "C5 balanced vs oracle")
     assert_close(f32(out16), got, FP8_TOL, FP8_TOL, "C5 16 vs 64 partitions")
 
 
