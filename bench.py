@@ -160,7 +160,7 @@ def bench_decode(args):
     b, hq, d = case.q.shape
     hk = case.k_cache.shape[2]
     part, nparts, wsb = ops.paged_decode_plan(b, hq, hk, d, case.max_seq_len, args.num_splits)
-    ws = torch.empty(max(1, wsb),
+    ws = torch.zeros(max(1, wsb),
                      dtype=torch.uint8, device=dev)
     out = torch.empty_like(case.q)
     partials, reduce = ops.paged_decode_phases(out, case.q, case.k_cache, case.v_cache,
@@ -168,7 +168,7 @@ def bench_decode(args):
                                                part, nparts, ws)
     total_bytes = case.algorithmic_bytes()
     out_bytes = out.numel() * out.element_size()
-    partial_bytes = total_bytes - out_bytes  # the partials kernel's algorithmic bytes
+    partial_bytes = total_bytes - out_bytes  # the main kernel's algorithmic bytes (no output)
     for _ in range(args.warmup):
         partials()
         reduce()
@@ -212,7 +212,7 @@ def bench_decode(args):
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "paged_decode_partials_kernel",
+            "kernel": "paged_decode_balanced_kernel" if part == 0 else "paged_decode_partition_kernel",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
@@ -277,7 +277,7 @@ def bench_table(args):
         b, hq, d = case.q.shape
         hk = case.k_cache.shape[2]
         part, nparts, wsb = ops.paged_decode_plan(b, hq, hk, d, case.max_seq_len, splits)
-        ws = torch.empty(max(1, wsb),
+        ws = torch.zeros(max(1, wsb),
                          dtype=torch.uint8, device=dev)
         out = torch.empty_like(case.q)
         add(name, f"paged_decode {case.k_cache.dtype} B={b} Hq={hq} part={part} x{nparts}",

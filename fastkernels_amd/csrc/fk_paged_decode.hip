@@ -144,11 +144,15 @@ struct TileRegs<true> {
 
 // Page id of token `tok` of sequence b, or -1 when the block-table entry is
 // negative, >= num_blocks, or past the row (index >= bt_row_stride): such a
-// page is masked and never read.
-__device__ __forceinline__ int64_t page_of(const DecodeParams& P, int b, int tok) {
+// page is masked and never read.  `bt` comes straight from a __restrict__
+// kernel argument so that this wave-uniform read is a scalar load (lgkmcnt):
+// a vector load here would make the compiler drain every outstanding KV load
+// (vmcnt(0)) before the next tile's loads could issue.
+__device__ __forceinline__ int64_t page_of(const DecodeParams& P, const int32_t* __restrict__ bt,
+                                           int b, int tok) {
   const int idx = tok >> P.block_size_log2;
   if (idx >= P.bt_row_stride) return -1;
-  const int64_t page = P.block_tables[b * P.bt_row_stride + idx];
+  const int64_t page = bt[b * P.bt_row_stride + idx];
   return (page >= 0 && page < P.num_blocks) ? page : -1;
 }
 
@@ -235,8 +239,8 @@ struct WaveState {
   float l_run;  // this lane's share of the running sum of column r
   floatx4_t o[8];
 
-  __device__ __forceinline__ void run(const DecodeParams& P, int b, int h, int tok_begin,
-                                      int tok_end, int r, int g) {
+  __device__ __forceinline__ void run(const DecodeParams& P, const int32_t* __restrict__ bt, int b,
+                                      int h, int tok_begin, int tok_end, int r, int g) {
     const int gqa = P.gqa;
     const bool head_ok = r < gqa;
     // Q^T operand: column r = query head h*G + r; dims permuted as the K loads.
@@ -333,7 +337,7 @@ struct WaveState {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int tok0 = tok_begin + kTile * min(t0 + u, ntiles - 1);
-        pg[u] = page_of(P, b, tok0);
+        pg[u] = page_of(P, bt, b, tok0);
         load_tile<kFp8>(P, pg[u] < 0 ? 0 : pg[u], h, tok0, r, g, buf[u]);
       }
     };
@@ -417,10 +421,11 @@ struct WaveState {
 // wave w owns kv head h = blockIdx.y * NH + w and streams the partition.
 // Partial rows: ((b * Hk + h) * max_parts + p) * G + j.
 template <int NH, int kG, bool kFp8, int U>
-__global__ __launch_bounds__(NH * 64) void paged_decode_partition_kernel(DecodeParams P) {
+__global__ __launch_bounds__(NH * 64) void paged_decode_partition_kernel(
+    DecodeParams P, const int32_t* __restrict__ block_tables, const int32_t* __restrict__ ctx_lens) {
   const int p = blockIdx.x;
   const int b = blockIdx.z;
-  const int ctx = P.ctx_lens[b];
+  const int ctx = ctx_lens[b];
   const int tok_begin = p * P.part_tokens;
   if (tok_begin >= ctx) return;  // uniform over the work-group
   const int tok_end = min(ctx, tok_begin + P.part_tokens);
@@ -436,7 +441,7 @@ __global__ __launch_bounds__(NH * 64) void paged_decode_partition_kernel(DecodeP
   const int r = lane & 15;
   const int g = lane >> 4;
   WaveState<kG, kFp8, U> st;
-  st.run(P, b, h, tok_begin, tok_end, r, g);
+  st.run(P, block_tables, b, h, tok_begin, tok_end, r, g);
   if (nparts == 1) {
     st.write_final(P, b, h, r, g);
   } else {
@@ -453,7 +458,8 @@ __device__ __forceinline__ int tiles_of(int ctx) { return ctx > 0 ? (ctx + kTile
 // ((w * 2 + slot) * Hk + h) * G + j, slot 0 = the group's first segment,
 // slot 1 = its last (a group holds at most one cut sequence at each end).
 template <int NH, int kG, bool kFp8, int U>
-__global__ __launch_bounds__(NH * 64) void paged_decode_balanced_kernel(DecodeParams P) {
+__global__ __launch_bounds__(NH * 64) void paged_decode_balanced_kernel(
+    DecodeParams P, const int32_t* __restrict__ block_tables, const int32_t* __restrict__ ctx_lens) {
   extern __shared__ int32_t toff[];  // [batch + 1] tile prefix sums
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -462,7 +468,7 @@ __global__ __launch_bounds__(NH * 64) void paged_decode_balanced_kernel(DecodePa
     int carry = 0;
     for (int base = 0; base < batch; base += 64) {
       const int i = base + lane;
-      int v = i < batch ? tiles_of(P.ctx_lens[i]) : 0;
+      int v = i < batch ? tiles_of(ctx_lens[i]) : 0;
 #pragma unroll
       for (int off = 1; off < 64; off <<= 1) {
         const int y = __shfl_up(v, off, 64);
@@ -499,8 +505,8 @@ __global__ __launch_bounds__(NH * 64) void paged_decode_balanced_kernel(DecodePa
     const int s_lo = max(t_lo, toff[b]) - toff[b];
     const int s_hi = min(t_hi, toff[b + 1]) - toff[b];
     if (s_hi <= s_lo) continue;  // empty sequence
-    const int ctx = P.ctx_lens[b];
-    st.run(P, b, h, kTile * s_lo, min(ctx, kTile * s_hi), r, g);
+    const int ctx = ctx_lens[b];
+    st.run(P, block_tables, b, h, kTile * s_lo, min(ctx, kTile * s_hi), r, g);
     if (toff[b] >= t_lo && toff[b + 1] <= t_hi) {
       st.write_final(P, b, h, r, g);
     } else {
@@ -512,27 +518,28 @@ __global__ __launch_bounds__(NH * 64) void paged_decode_balanced_kernel(DecodePa
 }
 
 // Merge of one (query head hq, sequence b): one wave, each lane owns two dims.
-// `rows` lists the partial rows of the sequence (index into part_o / part_ml).
+// Partial rows: k = 0 is `alt_first_row`, k >= 1 is first_row + k * row_stride.
+// One online pass (running max with rescaling), so the loads of all partials
+// are independent and overlap instead of costing a latency per dependency.
 __device__ __forceinline__ void merge_rows(uint16_t* orow, const float* part_o,
                                            const float* part_ml, int64_t first_row,
                                            int64_t row_stride, int nrows, int lane,
                                            int64_t alt_first_row) {
-  float M = kNegInf;
-  for (int k = lane; k < nrows; k += 64) {
+  float M = kNegInf, L = 0.f, o0 = 0.f, o1 = 0.f;
+#pragma unroll 4
+  for (int k = 0; k < nrows; ++k) {
     const int64_t row = (k == 0 ? alt_first_row : first_row + k * row_stride);
-    M = fmaxf(M, part_ml[row * 2]);
-  }
-  M = wave_max(M);
-  float L = 0.f, o0 = 0.f, o1 = 0.f;
-  if (M != kNegInf) {
-    for (int k = 0; k < nrows; ++k) {
-      const int64_t row = (k == 0 ? alt_first_row : first_row + k * row_stride);
-      const float f = __builtin_amdgcn_exp2f(part_ml[row * 2] - M);
-      L += f * part_ml[row * 2 + 1];
-      const float2 ov = reinterpret_cast<const float2*>(part_o + row * kHead)[lane];
-      o0 += f * ov.x;
-      o1 += f * ov.y;
-    }
+    const float m = part_ml[row * 2];
+    const float l = part_ml[row * 2 + 1];
+    const float2 ov = reinterpret_cast<const float2*>(part_o + row * kHead)[lane];
+    const float mn = fmaxf(M, m);
+    if (mn == kNegInf) continue;  // nothing valid yet
+    const float a = __builtin_amdgcn_exp2f(M - mn);  // 0 when M = -inf
+    const float f = __builtin_amdgcn_exp2f(m - mn);  // 0 when m = -inf
+    L = L * a + l * f;
+    o0 = o0 * a + ov.x * f;
+    o1 = o1 * a + ov.y * f;
+    M = mn;
   }
   const float inv = L > 0.f ? 1.f / L : 0.f;
   const bf16x2_t pk = {static_cast<__bf16>(o0 * inv), static_cast<__bf16>(o1 * inv)};
@@ -559,6 +566,7 @@ __global__ __launch_bounds__(64) void paged_decode_partition_reduce_kernel(Decod
 }
 
 // Balanced schedule: merge sequences cut across work-groups; zero empty ones.
+// One wave per (query head hq, sequence b).
 __global__ __launch_bounds__(64) void paged_decode_balanced_reduce_kernel(DecodeParams P) {
   const int hq = blockIdx.x;
   const int b = blockIdx.y;
@@ -588,7 +596,7 @@ __global__ __launch_bounds__(64) void paged_decode_balanced_reduce_kernel(Decode
 // Tuning knobs (compile-time): tiles per load set, and whether two sets are
 // double-buffered (FK_DECODE_PIPE=1) or one set is loaded then consumed.
 #ifndef FK_DECODE_CHUNK
-#define FK_DECODE_CHUNK 4
+#define FK_DECODE_CHUNK 2
 #endif
 constexpr int kChunk = FK_DECODE_CHUNK;  // tiles loaded per wave per set
 constexpr int kMaxWavesPerGroup = 8;     // kv heads (waves) per work-group
@@ -734,10 +742,10 @@ void launch_main(const Launch& L, hipStream_t stream) {
   if (L.balanced) {
     const size_t lds = static_cast<size_t>(L.P.batch + 1) * sizeof(int32_t);
     hipLaunchKernelGGL((paged_decode_balanced_kernel<NH, G, FP8, kChunk>), L.grid, dim3(NH * 64),
-                       lds, stream, L.P);
+                       lds, stream, L.P, L.P.block_tables, L.P.ctx_lens);
   } else {
     hipLaunchKernelGGL((paged_decode_partition_kernel<NH, G, FP8, kChunk>), L.grid,
-                       dim3(NH * 64), 0, stream, L.P);
+                       dim3(NH * 64), 0, stream, L.P, L.P.block_tables, L.P.ctx_lens);
   }
 }
 

@@ -219,7 +219,7 @@ def run_decode(case, num_splits=0, max_seq_len=None):
     hk = case.k_cache.shape[2]
     msl = case.max_seq_len if max_seq_len is None else max_seq_len
     part, nparts, nbytes = ops.paged_decode_plan(b, hq, hk, d, msl, num_splits)
-    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=case.q.device)
+    ws = torch.zeros(max(nbytes, 1), dtype=torch.uint8, device=case.q.device)
     out = torch.full_like(case.q, float("nan"))
     ops.paged_decode(out, case.q, case.k_cache, case.v_cache, case.block_tables, case.ctx_lens,
                      case.scale, part, nparts, ws, case.k_scale, case.v_scale)
@@ -311,6 +311,25 @@ def test_paged_decode_balanced_schedule(cuda, lens):
     for i, n in enumerate(lens):
         if n == 0:
             assert not got[i].any()
+
+
+def test_paged_decode_workspace_reuse(cuda):
+    """One workspace across repeated balanced launches and interleaved fixed-partition
+    launches (stale partials from an earlier call never leak into a later one)."""
+    case = workloads.c3_decode(cuda, batch=9, num_heads=16, kv_heads=4, pool_blocks=256,
+                               ctx_lo=0, ctx_hi=6000, seed=91)
+    b, hq, d = case.q.shape
+    hk = case.k_cache.shape[2]
+    pb = ops.paged_decode_plan(b, hq, hk, d, case.max_seq_len, 0)
+    pf = ops.paged_decode_plan(b, hq, hk, d, case.max_seq_len, 5)
+    ws = torch.zeros(max(pb.workspace_bytes, pf.workspace_bytes), dtype=torch.uint8, device=cuda)
+    ref = oracle_decode(case)
+    for it, plan in enumerate([pb, pb, pf, pb, pf, pb]):
+        out = torch.full_like(case.q, float("nan"))
+        ops.paged_decode(out, case.q, case.k_cache, case.v_cache, case.block_tables,
+                         case.ctx_lens, case.scale, plan.part_tokens, plan.max_parts, ws)
+        torch.cuda.synchronize()
+        assert_close(f32(out), ref, BF16_TOL, BF16_TOL, f"call {it} part={plan.part_tokens}")
 
 
 def test_paged_decode_padded_rows_and_masked_pages(cuda):
