@@ -59,8 +59,10 @@ def _events(n):
 def _flush_buffer(device):
     import torch
 
-    # Twice the 256 MB MALL (Infinity Cache): evicts L2 and MALL between timed calls.
-    return torch.empty(512 * 1024 * 1024, dtype=torch.uint8, device=device)
+    # Twice the 256 MB MALL (Infinity Cache): reading it evicts L2 and MALL between
+    # timed calls.  A read (not a fill) leaves no dirty lines whose write-back
+    # would compete with the timed kernel.
+    return torch.ones(512 * 1024 * 1024 // 4, dtype=torch.float32, device=device)
 
 
 def time_call(fn, iters=50, warmup=10, flush=None):
@@ -71,13 +73,15 @@ def time_call(fn, iters=50, warmup=10, flush=None):
     for _ in range(warmup):
         fn()
     starts, ends = _events(iters), _events(iters)
+    sink = None
     for i in range(iters):
         if flush is not None:
-            flush.fill_(i & 0xFF)
+            sink = flush.sum()
         starts[i].record()
         fn()
         ends[i].record()
     torch.cuda.synchronize()
+    del sink
     ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
     return statistics.median(ms), statistics.fmean(ms)
 
@@ -217,12 +221,28 @@ def bench_decode(args):
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": _committed_traffic(
+                "paged_decode_balanced_kernel" if part == 0 else "paged_decode_partition_kernel",
+                part) if args.seed == 200 else None,
+            "traffic_source": "profiles/paged_decode_c3_traffic.json (rocprofv3 FETCH_SIZE/WRITE_SIZE, copy-calibrated)",
             "avg_kernel_us": round(kavg * 1e3, 2),
             "algorithmic_bytes_per_launch": partial_bytes,
         },
     }
     return result, case
+
+
+def _committed_traffic(kernel: str, part: int):
+    """HBM bytes per launch of the dominant kernel from the committed rocprof PMC
+    summary (profiles/paged_decode_c3_traffic.json), if it covers this kernel."""
+    path = ROOT / "profiles" / "paged_decode_c3_traffic.json"
+    try:
+        d = json.loads(path.read_text())
+    except (OSError, ValueError):
+        return None
+    if d.get("workload") != "C3" or d.get("part_tokens") != part or kernel not in d.get("kernel", ""):
+        return None
+    return d.get("traffic_bytes")
 
 
 def bench_table(args):
@@ -272,8 +292,8 @@ def bench_table(args):
                                   dec.v_cache, c4.slot_mapping), 8 * 256 + 256 * 4 * 1024 * 2)
     c3 = workloads.c3_decode(dev)
     c5 = workloads.c5_fp8_decode(dev)
-    for name, case, splits in (("C4", dec, 0), ("C3", c3, 0), ("C5", c5, 16), ("C5", c5, 32),
-                               ("C5", c5, 64)):
+    for name, case, splits in (("C4", dec, 0), ("C3", c3, 0), ("C5", c5, 0), ("C5", c5, 16),
+                               ("C5", c5, 32), ("C5", c5, 64)):
         b, hq, d = case.q.shape
         hk = case.k_cache.shape[2]
         part, nparts, wsb = ops.paged_decode_plan(b, hq, hk, d, case.max_seq_len, splits)

@@ -1,0 +1,147 @@
+"""The drop-in surface (no GPU): candidate files load the way the reference harness
+loads them, expose the baseline class names and signatures, carry the same
+parameters / buffers, and register opaque custom ops with fake impls.
+
+Reference contract: a candidate lives at tasks/candidate/L1/<stem>.py and defines
+the class named like the baseline (fastkernels/bench.py:239-271,
+fastkernels/list.py:443-467); bench.py loads baseline weights into it with
+load_state_dict(strict=False) (fastkernels/bench.py:2177).
+"""
+from __future__ import annotations
+
+import importlib.util
+import inspect
+import math
+import subprocess
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+
+ROOT = Path(__file__).resolve().parents[1]
+CAND = ROOT / "fastkernels_amd" / "candidate" / "L1"
+
+# stem -> (class name, __init__ parameters, forward parameters) of the reference baseline
+# (fastkernels/tasks/baseline/L1/<stem>.py); None = no __init__ of its own (nn.Module's).
+CONTRACT = {
+    "rms_norm": ("RMSNorm", ["hidden_size", "eps", "elementwise_affine"], ["x", "residual"]),
+    "rotary_emb": ("RotaryEmbedding",
+                   ["head_dim", "max_position_embeddings", "rope_theta", "rope_scaling_factor",
+                    "rope_low_freq_factor", "rope_high_freq_factor",
+                    "rope_original_max_position_embeddings", "is_neox_style"],
+                   ["positions", "query", "key"]),
+    "store_kvcache": ("StoreKVCache", None, ["key", "value", "k_cache", "v_cache", "slot_mapping"]),
+    "flash_attn_decode": ("FlashAttnDecode", ["num_heads", "num_kv_heads", "head_dim", "page_size"],
+                          ["q", "k_cache", "v_cache", "cache_seqlens", "kwargs"]),
+    "silu_and_mul": ("SiluAndMul", [], ["x"]),
+}
+
+
+def load_by_path(stem: str):
+    """As the reference harness does: spec_from_file_location on the bare file."""
+    spec = importlib.util.spec_from_file_location(f"_fk_candidate_L1_{stem}", CAND / f"{stem}.py")
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+@pytest.mark.parametrize("stem", sorted(CONTRACT))
+def test_candidate_class_and_signatures(stem):
+    cls_name, init_params, fwd_params = CONTRACT[stem]
+    cls = getattr(load_by_path(stem), cls_name)
+    assert issubclass(cls, torch.nn.Module)
+    fwd = [p for p in inspect.signature(cls.forward).parameters if p != "self"]
+    if init_params is None:
+        assert "__init__" not in cls.__dict__
+    else:
+        init = [p for p in inspect.signature(cls.__init__).parameters if p != "self"]
+        assert init == init_params
+    assert fwd == fwd_params
+
+
+def test_candidate_loads_in_a_fresh_interpreter_without_repo_on_path(tmp_path):
+    """A file-path import from another working directory still finds the package."""
+    code = ("import importlib.util, sys; "
+            f"spec = importlib.util.spec_from_file_location('c', r'{CAND / 'rms_norm.py'}'); "
+            "m = importlib.util.module_from_spec(spec); spec.loader.exec_module(m); "
+            "print(m.RMSNorm(64).weight.shape[0])")
+    out = subprocess.run([sys.executable, "-c", code], cwd=tmp_path, capture_output=True,
+                         text=True, timeout=240)
+    assert out.returncode == 0, out.stderr
+    assert out.stdout.strip().endswith("64")
+
+
+def test_rmsnorm_parameters_and_state_dict():
+    RMSNorm = load_by_path("rms_norm").RMSNorm
+    m = RMSNorm(4096)
+    assert list(m.state_dict()) == ["weight"] and torch.equal(m.weight.data, torch.ones(4096))
+    w = torch.randn(4096)
+    m.load_state_dict({"weight": w}, strict=False)
+    assert torch.equal(m.weight.data, w)
+    assert list(RMSNorm(64, elementwise_affine=False).state_dict()) == []
+
+
+def test_rotary_cache_matches_reference_construction():
+    RotaryEmbedding = load_by_path("rotary_emb").RotaryEmbedding
+    m = RotaryEmbedding(128, 4097, 1e6)
+    assert m.cos_sin_cache.dtype == torch.float32 and tuple(m.cos_sin_cache.shape) == (4097, 128)
+    # float32 angles t * inv_freq (as the reference forms them) carry up to half an ulp
+    # of 4096, 2.4e-4, so cos/sin agree to that; the first positions agree to 1e-6.
+    ref = oracle.rope_cos_sin_cache(128, 4097, 1e6)
+    np.testing.assert_allclose(m.cos_sin_cache.numpy(), ref, atol=5e-4)
+    np.testing.assert_allclose(m.cos_sin_cache.numpy()[:16], ref[:16], atol=1e-6)
+    assert "cos_sin_cache" not in m.state_dict()  # non-persistent, as the reference
+
+
+def test_rotary_llama31_scaling():
+    """Llama-3.1 frequency scaling (rotary_emb.py:44-68): high frequencies kept, low
+    frequencies divided by the factor, a smooth blend in between."""
+    RotaryEmbedding = load_by_path("rotary_emb").RotaryEmbedding
+    d, theta, factor, lo, hi, orig = 128, 5e5, 8.0, 1.0, 4.0, 8192
+    m = RotaryEmbedding(d, 16, theta, factor, lo, hi, orig)
+    inv = 1.0 / theta ** (np.arange(0, d, 2) / d)
+    wl = 2 * math.pi / inv
+    expect = np.where(wl < orig / hi, inv,
+                      np.where(wl > orig / lo, inv / factor,
+                               (1 - (orig / wl - lo) / (hi - lo)) * inv / factor
+                               + (orig / wl - lo) / (hi - lo) * inv))
+    got_inv = m.cos_sin_cache[1, d // 2:].numpy()  # sin(1 * inv_freq)
+    np.testing.assert_allclose(np.arcsin(got_inv), expect, rtol=1e-5, atol=1e-7)
+    assert (expect < inv).any() and (expect == inv).any()
+
+
+def test_custom_ops_registered_with_fake_impls():
+    from fastkernels_amd import ops  # noqa: F401  (registers the library)
+
+    for name in ("rmsnorm", "fused_add_rmsnorm", "rotary_embedding", "store_kvcache",
+                 "paged_decode", "silu_and_mul"):
+        assert hasattr(torch.ops.fastkernels_amd, name)
+    x = torch.empty(8, 2 * 64, device="meta", dtype=torch.bfloat16)
+    out = torch.empty(8, 64, device="meta", dtype=torch.bfloat16)
+    torch.ops.fastkernels_amd.silu_and_mul(out, x)  # Meta impl: no kernel, no error
+    q = torch.empty(4, 8, 128, device="meta", dtype=torch.bfloat16)
+    torch.ops.fastkernels_amd.fused_add_rmsnorm(q, q, torch.empty(128, device="meta",
+                                                                  dtype=torch.bfloat16), 1e-6)
+
+
+def test_flash_attn_decode_rejects_unsupported_features():
+    FlashAttnDecode = load_by_path("flash_attn_decode").FlashAttnDecode
+    m = FlashAttnDecode(32, 8, 128, page_size=256)
+    q = torch.zeros(2, 32, 128, dtype=torch.bfloat16)
+    kc = torch.zeros(4, 256, 8, 128, dtype=torch.bfloat16)
+    with pytest.raises(NotImplementedError):
+        m(q, kc, kc, torch.ones(2, dtype=torch.int32), block_table=torch.zeros(2, 1, dtype=torch.int32),
+          window_size=(128, 0))
+    with pytest.raises(TypeError):
+        m(q, kc, kc, torch.ones(2, dtype=torch.int32), block_table=torch.zeros(2, 1, dtype=torch.int32),
+          bogus=1)
+
+
+def test_bench_refuses_multi_gpu():
+    out = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"],
+                         capture_output=True, text=True, timeout=120)
+    assert out.returncode == 2 and "one GPU" in out.stderr
