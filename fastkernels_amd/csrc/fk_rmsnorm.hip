@@ -34,13 +34,24 @@ __global__ __launch_bounds__(64) void rmsnorm_wave_row(
   const int64_t nvec = hidden / N;
   const uint4* xr = reinterpret_cast<const uint4*>(x + row * x_row_stride);
 
+  // Loads are unconditional (lanes past the row re-read its last vector and are
+  // masked below): guarding each load with a branch makes the compiler wait for
+  // it before issuing the next, serialising VPT memory latencies.
   float s[VPT][N];
   float ss = 0.f;
   V xv[VPT];
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
     const int64_t vi = lane + 64 * j;
-    if (vi < nvec) xv[j].raw = xr[vi];
+    xv[j].raw = xr[vi < nvec ? vi : nvec - 1];
+  }
+  // The weight row is needed only after the reduction; issue it now.
+  const uint4* wr = reinterpret_cast<const uint4*>(weight);
+  V wv[VPT];
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const int64_t vi = lane + 64 * j;
+    wv[j].raw = wr[vi < nvec ? vi : nvec - 1];
   }
   if constexpr (kFused) {
     uint4* rr = reinterpret_cast<uint4*>(residual + row * residual_row_stride);
@@ -48,52 +59,45 @@ __global__ __launch_bounds__(64) void rmsnorm_wave_row(
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
       const int64_t vi = lane + 64 * j;
-      if (vi < nvec) rv[j].raw = rr[vi];
+      rv[j].raw = rr[vi < nvec ? vi : nvec - 1];
     }
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
       const int64_t vi = lane + 64 * j;
-      if (vi < nvec) {
-        V nr;
+      const bool in_row = vi < nvec;
+      V nr;
 #pragma unroll
-        for (int e = 0; e < N; ++e) {
-          s[j][e] = T::to_f32(xv[j].e[e]) + T::to_f32(rv[j].e[e]);
-          nr.e[e] = T::from_f32(s[j][e]);
-          ss += s[j][e] * s[j][e];
-        }
-        rr[vi] = nr.raw;
+      for (int e = 0; e < N; ++e) {
+        s[j][e] = T::to_f32(xv[j].e[e]) + T::to_f32(rv[j].e[e]);
+        nr.e[e] = T::from_f32(s[j][e]);
+        ss += in_row ? s[j][e] * s[j][e] : 0.f;
       }
+      if (in_row) rr[vi] = nr.raw;
     }
   } else {
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
-      const int64_t vi = lane + 64 * j;
-      if (vi < nvec) {
+      const bool in_row = lane + 64 * j < nvec;
 #pragma unroll
-        for (int e = 0; e < N; ++e) {
-          s[j][e] = T::to_f32(xv[j].e[e]);
-          ss += s[j][e] * s[j][e];
-        }
+      for (int e = 0; e < N; ++e) {
+        s[j][e] = T::to_f32(xv[j].e[e]);
+        ss += in_row ? s[j][e] * s[j][e] : 0.f;
       }
     }
   }
   ss = wave_sum(ss);
   const float inv = 1.0f / __builtin_sqrtf(ss / static_cast<float>(hidden) + eps);
-  const uint4* wr = reinterpret_cast<const uint4*>(weight);
   uint4* orow = reinterpret_cast<uint4*>(out + row * out_row_stride);
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
     const int64_t vi = lane + 64 * j;
-    if (vi < nvec) {
-      V wv, ov;
-      wv.raw = wr[vi];
+    V ov;
 #pragma unroll
-      for (int e = 0; e < N; ++e) {
-        const float xh = T::round(s[j][e] * inv);
-        ov.e[e] = T::from_f32(xh * T::to_f32(wv.e[e]));
-      }
-      orow[vi] = ov.raw;
+    for (int e = 0; e < N; ++e) {
+      const float xh = T::round(s[j][e] * inv);
+      ov.e[e] = T::from_f32(xh * T::to_f32(wv[j].e[e]));
     }
+    if (vi < nvec) orow[vi] = ov.raw;
   }
 }
 

@@ -1,0 +1,96 @@
+"""HIP-graph capture of a decode step built from the candidate classes.
+
+The reference engine replays each decode step as a captured graph
+(fastkernels/infra/engine.py:5386-5428, capture at :6702).  The kernels here
+allocate nothing and never synchronise, so the step (add+RMSNorm -> rotary ->
+store_kvcache -> paged decode -> SiLU-and-mul) must capture and replay.  New
+inputs are copied into the static buffers between replays (as the engine's
+graph_vars), with eager work in between, and every replay is checked against
+an eager run of the same step on the same inputs.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from fastkernels_amd import workloads
+
+pytestmark = pytest.mark.gpu
+
+
+def _step(mods, bufs):
+    norm, rope, store, attn, act = mods
+    h, r = norm(bufs["hidden"], bufs["residual"])
+    qkv = bufs["qkv"]
+    t, hq, hk, d = bufs["dims"]
+    q, k, v = qkv[:, :hq * d], qkv[:, hq * d:(hq + hk) * d], qkv[:, (hq + hk) * d:]
+    rope(bufs["positions"], q, k)
+    store(k.view(t, hk, d), v.view(t, hk, d), bufs["k_cache"], bufs["v_cache"], bufs["slots"])
+    o = attn(q.view(t, hq, d), bufs["k_cache"], bufs["v_cache"], cache_seqlens=bufs["ctx"],
+             block_table=bufs["bt"], softmax_scale=d ** -0.5, max_seq_len=bufs["max_seq_len"])
+    y = act(bufs["gate_up"])
+    return h, r, o, y
+
+
+def test_decode_step_graph_capture_and_replay(cuda):
+    from fastkernels_amd.candidate.L1.flash_attn_decode import FlashAttnDecode
+    from fastkernels_amd.candidate.L1.rms_norm import RMSNorm
+    from fastkernels_amd.candidate.L1.rotary_emb import RotaryEmbedding
+    from fastkernels_amd.candidate.L1.silu_and_mul import SiluAndMul
+    from fastkernels_amd.candidate.L1.store_kvcache import StoreKVCache
+
+    t, hq, hk, d, hidden, inter = 32, 32, 8, 128, 4096, 1024
+    cases = [workloads.c4_chain(cuda, tokens=t, inter=inter, pool_blocks=512, ctx_lo=16,
+                                ctx_hi=3000, seed=300 + i) for i in range(3)]
+    norm = RMSNorm(hidden).to(cuda)
+    norm.weight.data.copy_(cases[0].norm_weight.float())
+    norm = norm.to(torch.bfloat16)
+    mods = (norm, RotaryEmbedding(d, 4096, 1e6).to(cuda), StoreKVCache(),
+            FlashAttnDecode(hq, hk, d, page_size=256), SiluAndMul())
+    c0 = cases[0]
+    static = dict(hidden=c0.hidden.clone(), residual=c0.residual.clone(), qkv=c0.qkv.clone(),
+                  positions=c0.positions.clone(), gate_up=c0.gate_up.clone(),
+                  k_cache=c0.decode.k_cache.clone(), v_cache=c0.decode.v_cache.clone(),
+                  slots=c0.slot_mapping.clone(), ctx=c0.decode.ctx_lens.clone(),
+                  bt=torch.full((t, 16), -1, dtype=torch.int32, device=cuda),
+                  dims=(t, hq, hk, d), max_seq_len=4096)
+    mods[3].preallocate(t, 4096, cuda)
+
+    def load(case):
+        for key, src in (("hidden", case.hidden), ("residual", case.residual), ("qkv", case.qkv),
+                         ("positions", case.positions), ("gate_up", case.gate_up),
+                         ("k_cache", case.decode.k_cache), ("v_cache", case.decode.v_cache),
+                         ("slots", case.slot_mapping), ("ctx", case.decode.ctx_lens)):
+            static[key].copy_(src)
+        bt = case.decode.block_tables  # widths differ per case: pad with -1 to the static 16
+        static["bt"].fill_(-1)
+        static["bt"][:, :bt.shape[1]].copy_(bt)
+
+    # Warm up on a side stream, as torch requires before capture.
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        load(c0)
+        _step(mods, static)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+
+    load(c0)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = _step(mods, static)
+    torch.cuda.synchronize()
+
+    for i, case in enumerate(cases + cases[:1]):
+        # eager reference on a private copy of the same inputs
+        load(case)
+        eager_bufs = {k: (v.clone() if isinstance(v, torch.Tensor) else v) for k, v in static.items()}
+        eager = [o.clone() for o in _step(mods, eager_bufs)]
+        torch.cuda.synchronize()
+        load(case)
+        graph.replay()
+        torch.cuda.synchronize()
+        for name, got, ref in zip(("hidden", "residual", "attn", "act"), outs, eager):
+            assert torch.equal(got, ref), f"replay {i}: {name} differs from eager"
+        kflat = static["k_cache"].view(-1, hk * d)
+        assert torch.equal(kflat[static["slots"]], eager_bufs["k_cache"].view(-1, hk * d)[static["slots"]])
