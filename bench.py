@@ -245,69 +245,168 @@ def _committed_traffic(kernel: str, part: int):
     return d.get("traffic_bytes")
 
 
+def _cpu_time(fn, budget_s: float = 2.0) -> tuple[float, int]:
+    """Median seconds of fn over as many runs as fit in budget_s (after one warmup)."""
+    fn()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while not times or time.perf_counter() < t_end:
+        t0 = time.perf_counter_ns()
+        fn()
+        times.append((time.perf_counter_ns() - t0) * 1e-9)
+    return statistics.median(times), len(times)
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy()
+
+
 def bench_table(args):
-    """Per-op µs/call and GB/s for C1-C5 (L2 + MALL flushed before each timed call)."""
+    """Per-op µs/call and GB/s for C1-C5 on the GPU (L2 + MALL flushed before each
+    timed call), each beside the CPU oracle timed on a bounded sample of the same
+    inputs on this host's cores."""
+    import numpy as np
     import torch
 
+    import oracle
     from fastkernels_amd import ops, workloads
 
+    try:
+        from threadpoolctl import threadpool_limits
+    except ImportError:  # pragma: no cover
+        threadpool_limits = None
+    cores = min(len(os.sched_getaffinity(0)), 16)
+    limiter = threadpool_limits(limits=cores) if threadpool_limits else None
+    torch.set_num_threads(cores)
     dev = torch.device("cuda:0")
     flush = _flush_buffer(dev)
     rows = []
 
-    def add(cfg, op, fn, nbytes, iters=50):
+    def add(cfg, op, fn, nbytes, cpu=None, iters=50):
+        """cpu = (callable, fraction of the op's bytes it processes, sample text) or None."""
         med, mean = time_call(fn, iters=iters, warmup=5, flush=flush)
-        rows.append({"config": cfg, "op": op, "us_median": round(med * 1e3, 2),
-                     "us_mean": round(mean * 1e3, 2), "bytes": nbytes,
-                     "GBs": round(nbytes / (med * 1e-3) / 1e9, 1),
-                     "frac_of_8TBs": round(nbytes / (med * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
-        print(json.dumps(rows[-1]), file=sys.stderr, flush=True)
+        row = {"config": cfg, "op": op, "us_median": round(med * 1e3, 2),
+               "us_mean": round(mean * 1e3, 2), "bytes": nbytes,
+               "GBs": round(nbytes / (med * 1e-3) / 1e9, 1),
+               "frac_of_8TBs": round(nbytes / (med * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        if cpu is not None:
+            cfn, frac, sample = cpu
+            sec, reps = _cpu_time(cfn)
+            row["cpu"] = {"us_per_call": round(sec / frac * 1e6, 1),
+                          "GBs": round(nbytes * frac / sec / 1e9, 3), "cores": cores,
+                          "kind": "port", "sample": f"{sample}; median of {reps}"}
+        rows.append(row)
+        print(json.dumps(row), file=sys.stderr, flush=True)
 
+    # C1: fused add+RMSNorm; CPU path in fp32 (forward_native), GPU in bf16.
     c1 = workloads.c1_norm(dev)
+    c1f = workloads.c1_norm("cpu", dtype=torch.float32)
+    x1, r1, w1 = c1f.x.numpy(), c1f.residual.numpy(), c1f.weight.numpy()
     x, r = c1.x.clone(), c1.residual.clone()
     add("C1", "fused_add_rmsnorm bf16 [256,1024]",
-        lambda: ops.fused_add_rms_norm(x, r, c1.weight, c1.eps), (4 * 256 * 1024 + 1024) * 2)
+        lambda: ops.fused_add_rms_norm(x, r, c1.weight, c1.eps), (4 * 256 * 1024 + 1024) * 2,
+        (lambda: oracle.rms_norm(x1, w1, 1e-6, "f32", residual=r1), 2.0,
+         "oracle.rms_norm fp32 on the full [256,1024] (4,198,400 B; GB/s on the fp32 bytes)"))
+    # C2: store_kvcache (bit copy); CPU: in-place numpy scatter into full-size caches.
     c2 = workloads.c2_store(dev)
     nvalid = int((c2.slot_mapping >= 0).sum().item())
+    k2 = c2.key.view(torch.int16).cpu().numpy()
+    v2 = c2.value.view(torch.int16).cpu().numpy()
+    s2 = c2.slot_mapping.cpu().numpy()
+    kc2 = np.zeros(tuple(c2.k_cache.shape), np.int16)
+    vc2 = np.zeros_like(kc2)
     add("C2", "store_kvcache [4096,8,128]",
         lambda: ops.store_kvcache(c2.key, c2.value, c2.k_cache, c2.v_cache, c2.slot_mapping),
-        8 * 4096 + nvalid * 4 * 8 * 128 * 2)
-    del c2
+        8 * 4096 + nvalid * 4 * 8 * 128 * 2,
+        (lambda: oracle.store_kvcache_(k2, v2, kc2, vc2, s2), 1.0,
+         "oracle.store_kvcache_ (numpy scatter) on the full C2 inputs and caches"))
+    del c2, kc2, vc2
+    # C4 chain ops
     c4 = workloads.c4_chain(dev)
     h, rr = c4.hidden.clone(), c4.residual.clone()
+    hn, rn, wn = _np(c4.hidden), _np(c4.residual), _np(c4.norm_weight)
     add("C4", "fused_add_rmsnorm bf16 [256,4096]",
-        lambda: ops.fused_add_rms_norm(h, rr, c4.norm_weight, 1e-6), (4 * 256 * 4096 + 4096) * 2)
+        lambda: ops.fused_add_rms_norm(h, rr, c4.norm_weight, 1e-6), (4 * 256 * 4096 + 4096) * 2,
+        (lambda: oracle.rms_norm(hn, wn, 1e-6, "bf16", residual=rn), 1.0,
+         "oracle.rms_norm (bf16 rounding points) on the full [256,4096]"))
     from fastkernels_amd.candidate.L1.rotary_emb import RotaryEmbedding
 
     rope = RotaryEmbedding(128, c4.max_position, c4.rope_theta).to(dev)
     qkv = c4.qkv.clone()
     q, k = qkv[:, :4096], qkv[:, 4096:5120]
+    qn, kn, pn, csn = _np(q), _np(k), c4.positions.cpu().numpy(), _np(rope.cos_sin_cache)
     add("C4", "rotary q[256,32x128] k[256,8x128]",
         lambda: ops.rotary_embedding(c4.positions, q, k, 128, rope.cos_sin_cache, True),
-        2 * 256 * 5120 * 2 + 256 * 8 + 256 * 128 * 4)
+        2 * 256 * 5120 * 2 + 256 * 8 + 256 * 128 * 4,
+        (lambda: oracle.rotary(pn, qn, kn, 128, csn, True, "bf16"), 1.0,
+         "oracle.rotary NeoX on the full q/k"))
     v = qkv[:, 5120:]
     dec = c4.decode
+    kn16 = k.contiguous().view(torch.int16).view(256, 8, 128).cpu().numpy()
+    vn16 = v.contiguous().view(torch.int16).view(256, 8, 128).cpu().numpy()
+    sn = c4.slot_mapping.cpu().numpy()
+    cache_np = np.zeros((dec.k_cache.shape[0],) + tuple(dec.k_cache.shape[1:]), np.int16)
     add("C4", "store_kvcache [256,8,128]",
         lambda: ops.store_kvcache(k.view(256, 8, 128), v.view(256, 8, 128), dec.k_cache,
-                                  dec.v_cache, c4.slot_mapping), 8 * 256 + 256 * 4 * 1024 * 2)
+                                  dec.v_cache, c4.slot_mapping), 8 * 256 + 256 * 4 * 1024 * 2,
+        (lambda: oracle.store_kvcache_(kn16, vn16, cache_np, cache_np, sn), 1.0,
+         "oracle.store_kvcache_ on the full C4 tokens"))
+    del cache_np
+    gu = c4.gate_up
+    gun = _np(gu)
+    act = torch.empty(256, 12288, dtype=torch.bfloat16, device=dev)
+    add("C4", "silu_and_mul [256,2x12288]", lambda: ops.silu_and_mul(act, gu),
+        256 * 3 * 12288 * 2,
+        (lambda: oracle.silu_and_mul(gun, "bf16"), 1.0, "oracle.silu_and_mul on the full input"))
+
+    def decode_cpu(case, nseq):
+        """Oracle on nseq sequences (shortest..longest spread) with their pages on the host."""
+        ctx = case.ctx_lens.cpu().numpy().astype(np.int64)
+        bt = case.block_tables.cpu().numpy()
+        bs = case.k_cache.shape[1]
+        order = np.argsort(ctx)
+        pick = sorted(set(order[np.linspace(0, len(ctx) - 1, nseq).astype(int)].tolist()))
+        qh = _np(case.q)
+        fp8 = case.k_cache.dtype == torch.float8_e4m3fn
+        data = []
+        for i in pick:
+            n = int(ctx[i])
+            ids = torch.from_numpy(bt[i, :(n + bs - 1) // bs].astype(np.int64)).to(dev)
+            if fp8:
+                kp = case.k_cache[ids].view(torch.uint8).cpu().numpy()
+                vp = case.v_cache[ids].view(torch.uint8).cpu().numpy()
+            else:
+                kp, vp = _np(case.k_cache[ids]), _np(case.v_cache[ids])
+            data.append((i, n, kp, vp))
+        ks = None if case.k_scale is None else case.k_scale.cpu().numpy()
+        vs = None if case.v_scale is None else case.v_scale.cpu().numpy()
+
+        def run():
+            for i, n, kp, vp in data:
+                oracle.paged_decode(qh[i:i + 1], kp, vp, np.arange(kp.shape[0])[None],
+                                    np.array([n]), case.scale, ks, vs)
+
+        frac = sum(n for _, n, _, _ in data) / float(ctx.sum())
+        return (run, frac, f"oracle.paged_decode on {len(pick)} of {len(ctx)} sequences "
+                           f"({frac * 100:.1f}% of the cached tokens), scaled to the batch")
+
     c3 = workloads.c3_decode(dev)
     c5 = workloads.c5_fp8_decode(dev)
-    for name, case, splits in (("C4", dec, 0), ("C3", c3, 0), ("C5", c5, 0), ("C5", c5, 16),
-                               ("C5", c5, 32), ("C5", c5, 64)):
+    for name, case, splits, nseq in (("C4", dec, 0, 4), ("C3", c3, 0, 4), ("C5", c5, 0, 1),
+                                     ("C5", c5, 16, 0), ("C5", c5, 32, 0), ("C5", c5, 64, 0)):
         b, hq, d = case.q.shape
         hk = case.k_cache.shape[2]
         part, nparts, wsb = ops.paged_decode_plan(b, hq, hk, d, case.max_seq_len, splits)
-        ws = torch.zeros(max(1, wsb),
-                         dtype=torch.uint8, device=dev)
+        ws = torch.zeros(max(1, wsb), dtype=torch.uint8, device=dev)
         out = torch.empty_like(case.q)
-        add(name, f"paged_decode {case.k_cache.dtype} B={b} Hq={hq} part={part} x{nparts}",
+        add(name, f"paged_decode {str(case.k_cache.dtype).replace('torch.', '')} B={b} Hq={hq} "
+                  f"{'balanced' if part == 0 else f'{nparts} partitions'}",
             lambda: ops.paged_decode(out, case.q, case.k_cache, case.v_cache, case.block_tables,
                                      case.ctx_lens, case.scale, part, nparts, ws, case.k_scale,
-                                     case.v_scale), case.algorithmic_bytes(), iters=30)
-    gu = c4.gate_up
-    act = torch.empty(256, 12288, dtype=torch.bfloat16, device=dev)
-    add("C4", "silu_and_mul [256,2x12288]", lambda: ops.silu_and_mul(act, gu),
-        256 * 3 * 12288 * 2)
+                                     case.v_scale), case.algorithmic_bytes(),
+            decode_cpu(case, nseq) if nseq else None, iters=30)
+    if limiter is not None:
+        limiter.__exit__(None, None, None)
     if args.table_json:
         Path(args.table_json).parent.mkdir(parents=True, exist_ok=True)
         Path(args.table_json).write_text(json.dumps(rows, indent=1))

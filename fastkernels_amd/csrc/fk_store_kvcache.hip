@@ -29,16 +29,14 @@ __global__ __launch_bounds__(256) void store_kvcache_vec16(
   if (lane_tok >= tokens_per_block) return;
   const int64_t tok = static_cast<int64_t>(blockIdx.x) * tokens_per_block + lane_tok;
   if (tok >= tokens) return;
+  // The source rows do not depend on the slot: issue their loads together with
+  // the slot load so the kernel waits one memory round trip, not two.
+  const uint4 kv = key[tok * key_row_chunks + chunk0];
+  const uint4 vv = value[tok * value_row_chunks + chunk0];
   const int64_t slot = load_slot<IdxT>(slot_mapping, tok);
   if (slot < 0 || slot >= num_slots) return;
-  const uint4* ksrc = key + tok * key_row_chunks;
-  const uint4* vsrc = value + tok * value_row_chunks;
-  uint4* kdst = k_cache + slot * chunks_per_row;
-  uint4* vdst = v_cache + slot * chunks_per_row;
-  const uint4 kv = ksrc[chunk0];
-  const uint4 vv = vsrc[chunk0];
-  kdst[chunk0] = kv;
-  vdst[chunk0] = vv;
+  k_cache[slot * chunks_per_row + chunk0] = kv;
+  v_cache[slot * chunks_per_row + chunk0] = vv;
 }
 
 // Wide rows (> 256 chunks): one work-group per token, lanes stride the row.

@@ -165,20 +165,27 @@ def rotary(positions: np.ndarray, query: np.ndarray, key: np.ndarray | None, hea
 # ---------------------------------------------------------------------------
 
 
-def store_kvcache(key: np.ndarray, value: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray,
-                  slot_mapping: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
-    """Copies of the caches after the scatter.  Arrays may be any dtype (bit copy):
-    key/value [N, Hk, D]; caches [num_blocks, block_size, Hk, D]; slot < 0 skips."""
-    kc, vc = k_cache.copy(), v_cache.copy()
-    nb, bs = kc.shape[:2]
-    kflat = kc.reshape(nb * bs, -1)
-    vflat = vc.reshape(nb * bs, -1)
+def store_kvcache_(key: np.ndarray, value: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray,
+                   slot_mapping: np.ndarray) -> None:
+    """In-place scatter: for token i with s = slot_mapping[i] >= 0, cache row s = key[i]
+    (the row is Hk*D elements; the cache viewed as [num_blocks * block_size, Hk*D])."""
+    nb, bs = k_cache.shape[:2]
+    kflat = k_cache.reshape(nb * bs, -1)
+    vflat = v_cache.reshape(nb * bs, -1)
     slots = np.asarray(slot_mapping, np.int64)
     n = key.shape[0]
     keep = slots[:n] >= 0
     idx = slots[:n][keep]
     kflat[idx] = key.reshape(n, -1)[keep]
     vflat[idx] = value.reshape(n, -1)[keep]
+
+
+def store_kvcache(key: np.ndarray, value: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray,
+                  slot_mapping: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """Copies of the caches after the scatter.  Arrays may be any dtype (bit copy):
+    key/value [N, Hk, D]; caches [num_blocks, block_size, Hk, D]; slot < 0 skips."""
+    kc, vc = k_cache.copy(), v_cache.copy()
+    store_kvcache_(key, value, kc, vc, slot_mapping)
     return kc, vc
 
 
