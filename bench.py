@@ -390,6 +390,21 @@ def bench_table(args):
         return (run, frac, f"oracle.paged_decode on {len(pick)} of {len(ctx)} sequences "
                            f"({frac * 100:.1f}% of the cached tokens), scaled to the batch")
 
+    for t, hh in ((64, 32), (8192, 32)):
+        g = torch.Generator().manual_seed(workloads.SEED)
+        po = torch.randn(t, hh, 128, generator=g).to(torch.bfloat16).to(dev)
+        so = torch.randn(t, hh, 128, generator=g).to(torch.bfloat16).to(dev)
+        pl = (3 * torch.randn(hh, t, generator=g)).to(dev)
+        sl = (3 * torch.randn(hh, t, generator=g)).to(dev)
+        mo, ml = torch.empty_like(po), torch.empty_like(pl)
+        arrs = [_np(x) for x in (po, pl, so, sl)]
+        add("merge", f"merge_attn_states bf16 [{t},{hh},128] + lse",
+            lambda po=po, pl=pl, so=so, sl=sl, mo=mo, ml=ml:
+            ops.merge_attn_states(mo, po, pl, so, sl, ml),
+            3 * t * hh * 128 * 2 + 3 * hh * t * 4,
+            (lambda arrs=arrs: oracle.merge_attn_states(*arrs, "bf16"), 1.0,
+             "oracle.merge_attn_states on the full input"))
+
     c3 = workloads.c3_decode(dev)
     c5 = workloads.c5_fp8_decode(dev)
     for name, case, splits, nseq in (("C4", dec, 0, 4), ("C3", c3, 0, 4), ("C5", c5, 0, 1),

@@ -297,6 +297,43 @@ def silu_and_mul(out: torch.Tensor, x: torch.Tensor) -> None:
 
 
 # ---------------------------------------------------------------------------
+# merge_attn_states
+# ---------------------------------------------------------------------------
+def merge_attn_states(output: torch.Tensor, prefix_output: torch.Tensor, prefix_lse: torch.Tensor,
+                      suffix_output: torch.Tensor, suffix_lse: torch.Tensor,
+                      output_lse: torch.Tensor | None = None,
+                      prefill_tokens_with_context: int | None = None) -> None:
+    """LSE merge of two partial attention results into ``output`` (and ``output_lse``).
+
+    output / prefix_output / suffix_output: [T, H, D] (D contiguous; prefix and suffix
+    share strides); *_lse: float32 [H, T], natural log."""
+    if prefix_output.stride(1) != suffix_output.stride(1) or \
+            prefix_output.stride(0) != suffix_output.stride(0):
+        raise ValueError("merge_attn_states: prefix_output and suffix_output must share strides")
+    if output.dim() != 3 or prefix_output.shape != output.shape or suffix_output.shape != output.shape:
+        raise ValueError("merge_attn_states: outputs must be [tokens, heads, head_size]")
+    if output.dtype != prefix_output.dtype or suffix_output.dtype != output.dtype:
+        raise TypeError("merge_attn_states: fp8 output (output_scale) is not supported; "
+                        "output, prefix and suffix must share a dtype")
+    t, h, d = output.shape
+    for x in (output, prefix_output, suffix_output):
+        if x.stride(2) != 1:
+            raise ValueError("merge_attn_states: head_size must be contiguous")
+    for x, nm in ((prefix_lse, "prefix_lse"), (suffix_lse, "suffix_lse"), (output_lse, "output_lse")):
+        if x is not None and (x.dtype != torch.float32 or tuple(x.shape) != (h, t) or
+                              not x.is_contiguous()):
+            raise ValueError(f"merge_attn_states: {nm} must be contiguous float32 [heads, tokens]")
+    _same_device(output, prefix_output, suffix_output, prefix_lse, suffix_lse)
+    if t == 0 or h == 0:
+        return
+    _native.call("fk_merge_attn_states", _ptr(output), output.stride(0), output.stride(1),
+                 _ptr(output_lse), _ptr(prefix_output), _ptr(prefix_lse), _ptr(suffix_output),
+                 _ptr(suffix_lse), prefix_output.stride(0), prefix_output.stride(1), t, h, d,
+                 -1 if prefill_tokens_with_context is None else int(prefill_tokens_with_context),
+                 _tag(output, "merge_attn_states"), _stream(output))
+
+
+# ---------------------------------------------------------------------------
 # torch.library registration (opaque custom ops with mutation annotations).
 # ---------------------------------------------------------------------------
 _LIB = torch.library.Library("fastkernels_amd", "DEF")
@@ -311,6 +348,8 @@ _LIB.define("paged_decode(Tensor(a!) out, Tensor q, Tensor k_cache, Tensor v_cac
             "Tensor block_table, Tensor cache_seqlens, float softmax_scale, int part_tokens, "
             "int max_parts, Tensor(b!)? workspace, Tensor? k_scale, Tensor? v_scale) -> ()")
 _LIB.define("silu_and_mul(Tensor! result, Tensor input) -> ()")
+_LIB.define("merge_attn_states(Tensor(a!) output, Tensor prefix_output, Tensor prefix_lse, "
+            "Tensor suffix_output, Tensor suffix_lse, Tensor(b!)? output_lse) -> ()")
 
 _IMPLS = {
     "rmsnorm": lambda result, input, weight, eps: rms_norm(result, input, weight, eps),
@@ -319,6 +358,7 @@ _IMPLS = {
     "store_kvcache": store_kvcache,
     "paged_decode": paged_decode,
     "silu_and_mul": lambda result, input: silu_and_mul(result, input),
+    "merge_attn_states": merge_attn_states,
 }
 for _name, _fn in _IMPLS.items():
     _LIB.impl(_name, _fn, "CUDA")

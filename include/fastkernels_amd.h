@@ -33,6 +33,9 @@
  *   fk_silu_and_mul
  *       fastkernels/tasks/baseline/L1/silu_and_mul.py:24-30 (_C.silu_and_mul(out, x)),
  *       kernel silu_and_mul.cu:951-956.
+ *   fk_merge_attn_states
+ *       fastkernels/tasks/baseline/L1/merge_attn_states.py:30-122 (merge_attn_states,
+ *       MergeAttnStates.forward).
  */
 #ifndef FASTKERNELS_AMD_H_
 #define FASTKERNELS_AMD_H_
@@ -171,6 +174,23 @@ int fk_paged_decode_reduce(void* out, int64_t out_row_stride, const void* q,
                            int num_kv_heads, int head_size, int block_size, int64_t num_blocks,
                            float scale, int64_t part_tokens, int64_t max_parts, void* workspace,
                            int64_t workspace_bytes, void* stream);
+
+/* Log-sum-exp merge of two partial attention results (split-KV / prefix+suffix):
+ *   out[t,h,:] = (prefix[t,h,:] e^(p - M) + suffix[t,h,:] e^(s - M)) / (e^(p - M) + e^(s - M))
+ *   with p = prefix_lse[h,t], s = suffix_lse[h,t] (natural log, +inf read as -inf),
+ *   M = max(p, s), out_lse[h,t] = log(e^(p-M) + e^(s-M)) + M; when M = -inf the
+ *   prefix rows are copied and out_lse = -inf.  out_lse may be NULL.
+ * out/prefix/suffix: [tokens, heads, head_size] with the given token and head strides
+ * (prefix and suffix share theirs); lse tensors: fp32 [heads, tokens] contiguous.
+ * Tokens >= prefill_tokens_with_context (a negative value = all tokens) copy the
+ * suffix and its lse.  dtype: F32, F16 or BF16 (computed in fp32).
+ * Replaces merge_attn_states / MergeAttnStates.forward
+ * (fastkernels/tasks/baseline/L1/merge_attn_states.py:30-122). */
+int fk_merge_attn_states(void* out, int64_t out_token_stride, int64_t out_head_stride,
+                         float* out_lse, const void* prefix, const float* prefix_lse,
+                         const void* suffix, const float* suffix_lse, int64_t in_token_stride,
+                         int64_t in_head_stride, int64_t tokens, int heads, int head_size,
+                         int64_t prefill_tokens_with_context, int dtype, void* stream);
 
 /* SiLU-and-mul: out[r, j] = cast(cast(silu(x[r, j])) * x[r, d + j]) for j < d.
  * x: [rows, 2d] rows `x_row_stride` elements apart; out: [rows, d] rows

@@ -293,6 +293,47 @@ def merge_partials(parts) -> np.ndarray:
 
 
 # ---------------------------------------------------------------------------
+# merge_attn_states — fastkernels/tasks/baseline/L1/merge_attn_states.py:30-100,
+# kernel merge_attn_states.cu:2443-2571
+# ---------------------------------------------------------------------------
+
+
+def merge_attn_states(prefix: np.ndarray, prefix_lse: np.ndarray, suffix: np.ndarray,
+                      suffix_lse: np.ndarray, dtype: str,
+                      prefill_tokens_with_context: int | None = None):
+    """(out [T, H, D], out_lse [H, T]) of the two-partition LSE merge.
+
+    Tokens t < P (P = prefill_tokens_with_context, default T): infinite lse read as
+    -inf (cu:2476-2477); M = max(p, s); if M = -inf the prefix rows and -inf are
+    emitted (cu:2489-2517); else weights e^(p-M)/E, e^(s-M)/E with E their sum,
+    one rounding of the weighted sum to ``dtype`` (cu:2520-2565) and
+    out_lse = log(E) + M (cu:2567-2571).  Tokens t >= P copy the suffix and its lse
+    (cu:2443-2471)."""
+    prefix = np.asarray(prefix, np.float32)
+    suffix = np.asarray(suffix, np.float32)
+    t_all = prefix.shape[0]
+    n = t_all if prefill_tokens_with_context is None else min(int(prefill_tokens_with_context), t_all)
+    out = suffix.copy()
+    out_lse = np.asarray(suffix_lse, np.float32).copy()
+    p = np.asarray(prefix_lse, np.float64)[:, :n].T  # [n, H]
+    s = np.asarray(suffix_lse, np.float64)[:, :n].T
+    p = np.where(np.isinf(p), -np.inf, p)
+    s = np.where(np.isinf(s), -np.inf, s)
+    m = np.maximum(p, s)
+    empty = np.isneginf(m)
+    mz = np.where(empty, 0.0, m)
+    ep = np.where(empty, 0.0, np.exp(p - mz))
+    es = np.where(empty, 0.0, np.exp(s - mz))
+    e = np.where(empty, 1.0, ep + es)
+    merged = prefix[:n].astype(np.float64) * (ep / e)[..., None] + \
+        suffix[:n].astype(np.float64) * (es / e)[..., None]
+    merged = round_to(merged.astype(np.float32), dtype)
+    out[:n] = np.where(empty[..., None], prefix[:n], merged)
+    out_lse[:, :n] = np.where(empty, -np.inf, np.log(e) + mz).T.astype(np.float32)
+    return out, out_lse
+
+
+# ---------------------------------------------------------------------------
 # SiLU-and-mul — SiluAndMul.forward_native, fastkernels/tasks/baseline/L1/silu_and_mul.py:19-22
 # ---------------------------------------------------------------------------
 

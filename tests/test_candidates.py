@@ -38,6 +38,9 @@ CONTRACT = {
     "flash_attn_decode": ("FlashAttnDecode", ["num_heads", "num_kv_heads", "head_dim", "page_size"],
                           ["q", "k_cache", "v_cache", "cache_seqlens", "kwargs"]),
     "silu_and_mul": ("SiluAndMul", [], ["x"]),
+    "merge_attn_states": ("MergeAttnStates", None,
+                          ["output", "prefix_output", "prefix_lse", "suffix_output", "suffix_lse",
+                           "output_lse"]),
 }
 
 
@@ -61,6 +64,14 @@ def test_candidate_class_and_signatures(stem):
         init = [p for p in inspect.signature(cls.__init__).parameters if p != "self"]
         assert init == init_params
     assert fwd == fwd_params
+
+
+def test_merge_attn_states_function_signature():
+    """merge_attn_states.py:32-41: the module-level function keeps the reference's arguments."""
+    fn = load_by_path("merge_attn_states").merge_attn_states
+    assert list(inspect.signature(fn).parameters) == [
+        "output", "prefix_output", "prefix_lse", "suffix_output", "suffix_lse", "output_lse",
+        "prefill_tokens_with_context", "output_scale"]
 
 
 def test_candidate_loads_in_a_fresh_interpreter_without_repo_on_path(tmp_path):

@@ -2,7 +2,8 @@
 
 Bars: store_kvcache bit-exact; bf16 ops within atol=rtol=1e-2 of the oracle's
 fp32-upcast result (every element, stricter than the reference harness's 99%
-rule, fastkernels/bench.py:142-155); fp8-KV attention within atol=rtol=3e-2.
+rule, fastkernels/bench.py:142-155); fp8-KV attention within atol=rtol=3e-2;
+fp32 outputs within the harness's fp32 tolerance (atol 1e-5, rtol 1e-3).
 Sizes are the benchmark configurations (C1-C5) where the oracle finishes in
 seconds, and small edge cases otherwise.
 """
@@ -443,3 +444,111 @@ def test_flash_attn_decode_defaults_no_sync(cuda):
              block_table=case.block_tables)
     assert_close(f32(o), oracle_decode(case), BF16_TOL, BF16_TOL)
     assert math.isclose(case.scale, 1 / math.sqrt(128))
+
+
+# ---------------------------------------------------------------------------
+# merge_attn_states
+# ---------------------------------------------------------------------------
+def _merge_inputs(t, h, d, dtype, cuda, seed, specials=True):
+    g = torch.Generator().manual_seed(seed)
+    po = torch.randn(t, h, d, generator=g).to(dtype)
+    so = torch.randn(t, h, d, generator=g).to(dtype)
+    pl = (3 * torch.randn(h, t, generator=g)).float()
+    sl = (3 * torch.randn(h, t, generator=g)).float()
+    if specials and t >= 4:
+        pl[0, 0] = -math.inf                    # empty prefix
+        sl[0, 1] = -math.inf                    # empty suffix
+        pl[h - 1, 2] = sl[h - 1, 2] = -math.inf  # both empty: the prefix rows are copied
+        pl[h - 1, 3] = math.inf                 # +inf read as -inf
+        sl[0, 3] = 40.0                         # far apart: one weight underflows
+    return po.to(cuda), pl.to(cuda), so.to(cuda), sl.to(cuda)
+
+
+def _check_merge(out, out_lse, po, pl, so, sl, dtype, prefill=None):
+    ref, ref_lse = oracle.merge_attn_states(f32(po), f32(pl), f32(so), f32(sl), _DT[dtype], prefill)
+    tol = (BF16_TOL, BF16_TOL) if dtype != torch.float32 else (1e-5, 1e-3)
+    assert_close(f32(out), ref, *tol, what="merge out")
+    # copied rows are bit copies of the input rows
+    both = torch.isinf(pl) & torch.isinf(sl)
+    n = po.shape[0] if prefill is None else prefill
+    for hh, tt in both.nonzero().tolist():
+        if tt < n:
+            assert torch.equal(out[tt, hh], po[tt, hh])
+    if n < po.shape[0]:
+        assert torch.equal(out[n:], so[n:])
+    if out_lse is not None:
+        got = f32(out_lse)
+        assert np.array_equal(np.isneginf(got), np.isneginf(ref_lse))
+        fin = np.isfinite(ref_lse)
+        assert_close(got[fin], ref_lse[fin], 1e-5, 1e-5, what="merge lse")
+        if n < po.shape[0]:
+            assert torch.equal(out_lse[:, n:], sl[:, n:])
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("t,h,d", [(64, 32, 128), (5, 3, 100), (33, 8, 256), (1, 1, 8)])
+@pytest.mark.parametrize("with_lse", [True, False])
+def test_merge_attn_states(cuda, dtype, t, h, d, with_lse):
+    _flush(f"merge {dtype} t={t} h={h} d={d} lse={with_lse}")
+    po, pl, so, sl = _merge_inputs(t, h, d, dtype, cuda, seed=t * 7 + d)
+    out = torch.full_like(po, float("nan"))
+    out_lse = torch.full((h, t), float("nan"), device=cuda) if with_lse else None
+    ops.merge_attn_states(out, po, pl, so, sl, out_lse)
+    torch.cuda.synchronize()
+    _check_merge(out, out_lse, po, pl, so, sl, dtype)
+
+
+def test_merge_attn_states_prefill_tokens_and_strides(cuda):
+    """Suffix-only tail tokens, and strided [T, H, D] views (a slice of a wider
+    buffer for the inputs, a head-padded output)."""
+    t, h, d = 48, 16, 128
+    dtype = torch.bfloat16
+    _flush("merge strided + prefill_tokens_with_context=30")
+    g = torch.Generator().manual_seed(5)
+    wide = torch.randn(2, t, h, d + 64, generator=g).to(dtype).to(cuda)
+    po, so = wide[0, :, :, :d], wide[1, :, :, :d]
+    _, pl, _, sl = _merge_inputs(t, h, d, dtype, cuda, seed=6)
+    out_buf = torch.full((t, h, d + 32), float("nan"), dtype=dtype, device=cuda)
+    out = out_buf[:, :, :d]
+    out_lse = torch.full((h, t), float("nan"), device=cuda)
+    ops.merge_attn_states(out, po, pl, so, sl, out_lse, prefill_tokens_with_context=30)
+    torch.cuda.synchronize()
+    _check_merge(out, out_lse, po, pl, so, sl, dtype, prefill=30)
+    assert torch.isnan(out_buf[:, :, d:].float()).all(), "padding written"
+
+
+def test_merge_attn_states_two_halves_equal_whole(cuda):
+    """Attention over 2000 keys split at 700 and merged on the GPU equals attention
+    over all of them (torch fp32 on the device computes the halves and the whole)."""
+    t, h, d, n, cut = 32, 8, 128, 2000, 700
+    _flush("merge halves == whole")
+    g = torch.Generator().manual_seed(8)
+    q = torch.randn(t, h, 1, d, generator=g).to(cuda)
+    k = torch.randn(t, h, n, d, generator=g).to(cuda)
+    v = torch.randn(t, h, n, d, generator=g).to(cuda)
+    sc = d ** -0.5
+    s = (q @ k.transpose(-1, -2).contiguous())[:, :, 0] * sc  # [t, h, n]
+
+    def attend(lo, hi):
+        p = torch.softmax(s[..., lo:hi], dim=-1)
+        o = (p.unsqueeze(-2) @ v[:, :, lo:hi])[:, :, 0]
+        return o.bfloat16().contiguous(), torch.logsumexp(s[..., lo:hi], -1).T.contiguous()
+
+    (po, pl), (so, sl), (whole, whole_lse) = attend(0, cut), attend(cut, n), attend(0, n)
+    out = torch.empty_like(po)
+    out_lse = torch.empty_like(pl)
+    ops.merge_attn_states(out, po, pl, so, sl, out_lse)
+    torch.cuda.synchronize()
+    assert_close(f32(out), f32(whole), BF16_TOL, BF16_TOL, what="halves vs whole")
+    assert_close(f32(out_lse), f32(whole_lse), 1e-4, 1e-5, what="lse halves vs whole")
+
+
+def test_merge_attn_states_candidate(cuda):
+    from fastkernels_amd.candidate.L1.merge_attn_states import MergeAttnStates
+    t, h, d = 16, 8, 128
+    po, pl, so, sl = _merge_inputs(t, h, d, torch.bfloat16, cuda, seed=9)
+    out = torch.empty_like(po)
+    out_lse = torch.empty_like(pl)
+    MergeAttnStates()(out, po, pl, so, sl, out_lse)
+    torch.cuda.synchronize()
+    _check_merge(out, out_lse, po, pl, so, sl, torch.bfloat16)

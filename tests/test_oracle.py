@@ -16,7 +16,11 @@ its own formula:
                    one dominant key -> its V row, empty -> 0), page-permutation
                    invariance, split-context merge == unsplit;
   silu_and_mul     torch.nn.functional.silu (library) with the reference's
-                   rounding points.
+                   rounding points;
+  merge_attn_states  attention over a key set split in two and merged equals
+                   torch SDPA over the whole set, and out_lse equals
+                   torch.logsumexp of all scores (library); the special cases
+                   (one side empty, both empty, +inf lse, suffix-only tokens).
 Planted-mistake tests show the checks reject plausible slips (wrong GQA head
 mapping, dropped eps, swapped rotary pairing, a wrong sign).
 """
@@ -316,6 +320,63 @@ def test_fp8_dequant_matches_torch():
     ours = oracle.dequant_kv(codes, scale, "bf16")
     t = torch.from_numpy(codes).view(torch.float8_e4m3fn).float() * torch.from_numpy(scale).view(1, 1, 2, 1)
     assert np.array_equal(ours, t.bfloat16().float().numpy())
+
+
+# ---------------------------------------------------------------------------
+# merge_attn_states
+# ---------------------------------------------------------------------------
+def _halves(seed=11, t=5, h=3, d=16, n=40, cut=17):
+    """Per (token, head): attention of a query over n keys, and over the keys
+    [0, cut) and [cut, n) separately, with natural-log lse, from torch in float64."""
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(t, h, 1, d, generator=g, dtype=torch.float64)
+    k = torch.randn(t, h, n, d, generator=g, dtype=torch.float64)
+    v = torch.randn(t, h, n, d, generator=g, dtype=torch.float64)
+    sc = 0.4
+
+    def part(lo, hi):
+        o = F.scaled_dot_product_attention(q, k[:, :, lo:hi], v[:, :, lo:hi], scale=sc)[:, :, 0]
+        lse = torch.logsumexp((q @ k[:, :, lo:hi].transpose(-1, -2))[:, :, 0] * sc, dim=-1)
+        return o.numpy(), lse.T.contiguous().numpy()  # o [T, H, D], lse [H, T]
+
+    return part(0, cut), part(cut, n), part(0, n)
+
+
+def test_merge_attn_states_equals_attention_over_the_union():
+    (po, pl), (so, sl), (whole, whole_lse) = _halves()
+    out, out_lse = oracle.merge_attn_states(po, pl, so, sl, "f32")
+    np.testing.assert_allclose(out, whole, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(out_lse, whole_lse, rtol=1e-6)
+    # planted mistake: the prefix weight applied to the suffix is caught
+    m = np.maximum(pl, sl).T[..., None]
+    wp, ws = np.exp(pl.T[..., None] - m), np.exp(sl.T[..., None] - m)
+    wrong = (po * ws + so * wp) / (wp + ws)
+    assert not np.allclose(wrong, whole, atol=1e-3), "planted mistake (swapped weights) not caught"
+
+
+def test_merge_attn_states_special_cases():
+    (po, pl), (so, sl), _ = _halves(seed=12, t=6, h=2)
+    pl, sl = pl.astype(np.float32), sl.astype(np.float32)
+    pl[0, 0] = -np.inf            # empty prefix -> the suffix
+    sl[0, 1] = -np.inf            # empty suffix -> the prefix
+    pl[1, 2] = sl[1, 2] = -np.inf  # both empty -> prefix rows, lse -inf
+    pl[1, 3] = np.inf             # +inf is read as -inf (as empty)
+    out, out_lse = oracle.merge_attn_states(po, pl, so, sl, "f32", prefill_tokens_with_context=5)
+    np.testing.assert_allclose(out[0, 0], so[0, 0], rtol=1e-6)
+    np.testing.assert_allclose(out[1, 0], po[1, 0], rtol=1e-6)
+    assert np.array_equal(out[2, 1], po[2, 1].astype(np.float32)) and out_lse[1, 2] == -np.inf
+    np.testing.assert_allclose(out[3, 1], so[3, 1], rtol=1e-6)
+    assert out_lse[0, 0] == pytest.approx(sl[0, 0], rel=1e-6)
+    assert out_lse[1, 3] == pytest.approx(sl[1, 3], rel=1e-6)
+    # token 5 >= prefill_tokens_with_context: suffix copied, lse copied
+    assert np.array_equal(out[5], so[5].astype(np.float32)) and np.array_equal(out_lse[:, 5], sl[:, 5])
+    assert np.isfinite(out).all()
+    # bf16: one rounding of the fp32 value
+    b, _ = oracle.merge_attn_states(po, pl, so, sl, "bf16")
+    f, _ = oracle.merge_attn_states(po, pl, so, sl, "f32")
+    mask = np.ones(f.shape[:2], bool)
+    mask[2, 1] = False  # copied row, not rounded
+    assert np.array_equal(b[mask], oracle.round_to(f[mask], "bf16"))
 
 
 # ---------------------------------------------------------------------------
