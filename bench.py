@@ -420,6 +420,27 @@ def bench_table(args):
                                      case.ctx_lens, case.scale, part, nparts, ws, case.k_scale,
                                      case.v_scale), case.algorithmic_bytes(),
             decode_cpu(case, nseq) if nseq else None, iters=30)
+    # Decode step of Attention.forward_impl at C3: store + decode as two calls, and fused.
+    rows3 = workloads.decode_step_rows(c3)
+    b3, hq3, d3 = c3.q.shape
+    part3, np3, wsb3 = ops.paged_decode_plan(b3, hq3, c3.k_cache.shape[2], d3, c3.max_seq_len, 0)
+    ws3 = torch.zeros(max(1, wsb3), dtype=torch.uint8, device=dev)
+    out3 = torch.empty_like(c3.q)
+    step_bytes = c3.algorithmic_bytes() + b3 * (4 * rows3.key[0].numel() * 2 + 8)
+
+    def two_calls():
+        ops.store_kvcache(rows3.key, rows3.value, c3.k_cache, c3.v_cache, rows3.slot_mapping)
+        ops.paged_decode(out3, c3.q, c3.k_cache, c3.v_cache, c3.block_tables, c3.ctx_lens,
+                         c3.scale, part3, np3, ws3)
+
+    def fused():
+        ops.store_paged_decode(out3, c3.q, rows3.key, rows3.value, c3.k_cache, c3.v_cache,
+                               rows3.slot_mapping, c3.block_tables, c3.ctx_lens, c3.scale, part3,
+                               np3, ws3)
+
+    add("C3", "decode step: store_kvcache + paged_decode (two calls)", two_calls, step_bytes,
+        iters=30)
+    add("C3", "decode step: store_paged_decode (fused)", fused, step_bytes, iters=30)
     if limiter is not None:
         limiter.__exit__(None, None, None)
     if args.table_json:

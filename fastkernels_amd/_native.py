@@ -56,6 +56,11 @@ _SIGNATURES = {
                                        c_void_p]),
     "fk_silu_and_mul": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_int64, c_int64, c_int,
                                 c_void_p]),
+    "fk_store_paged_decode": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64,
+                                      c_void_p, c_int64, c_void_p, c_int, c_void_p, c_void_p,
+                                      c_int, c_void_p, c_void_p, c_void_p, c_int64, c_void_p,
+                                      c_int64, c_int, c_int, c_int, c_int, c_int64, c_float,
+                                      c_int64, c_int64, c_void_p, c_int64, c_void_p]),
     "fk_merge_attn_states": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p,
                                      c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int, c_int,
                                      c_int64, c_int, c_void_p]),

@@ -23,6 +23,10 @@ given as a single value and are broadcast), i.e. K = float(K8) * k_scale as in
 ``_cast_kv_tile`` (triton_unified_attention.py:51-67).  FA-style
 ``k_descale`` / ``v_descale`` are accepted as aliases.
 
+``forward_store(q, key, value, k_cache, v_cache, slot_mapping, cache_seqlens,
+**kwargs)`` is the decode step of ``Attention.forward_impl`` (store, then decode)
+in one launch.
+
 No host synchronisation: the default length-balanced schedule reads the context
 lengths on the device, and when ``max_seq_len`` is absent the bound used for
 fixed partitions is the block table width (``block_table.shape[1] * page_size``)
@@ -86,7 +90,8 @@ class FlashAttnDecode(nn.Module):
             raise ValueError(f"FlashAttnDecode: fp8 scale must have 1 or {hk} entries")
         return s.contiguous()
 
-    def forward(self, q, k_cache, v_cache, cache_seqlens=None, **kwargs):
+    def _launch_args(self, q, k_cache, cache_seqlens, kwargs):
+        """Parses the reference's decode kwargs; returns what both launch paths need."""
         max_seq_len = kwargs.pop("max_seq_len", None)
         block_table = kwargs.pop("block_table", None)
         softmax_scale = kwargs.pop("softmax_scale", None)
@@ -108,7 +113,6 @@ class FlashAttnDecode(nn.Module):
             raise ValueError("FlashAttnDecode: block_table and cache_seqlens are required")
 
         b = q.shape[0]
-        q3 = q.view(b, self.num_heads, self.head_dim)
         block_size = k_cache.shape[1]
         if block_table.dtype != torch.int32:
             block_table = block_table.to(torch.int32)
@@ -125,15 +129,43 @@ class FlashAttnDecode(nn.Module):
         plan = ops.paged_decode_plan(b, self.num_heads, hk, self.head_dim, int(max_seq_len),
                                      num_splits)
         ws = self._get_workspace(plan.workspace_bytes, q.device)
-        part_tokens, max_parts = plan.part_tokens, plan.max_parts
         if out is None:
             out = torch.empty((b, self.num_heads, self.head_dim), dtype=q.dtype, device=q.device)
-        out3 = out.view(b, self.num_heads, self.head_dim)
-        if torch.compiler.is_compiling():
-            torch.ops.fastkernels_amd.paged_decode(out3, q3, k_cache, v_cache, block_table,
-                                                   cache_seqlens, float(softmax_scale),
-                                                   part_tokens, max_parts, ws, k_scale, v_scale)
-        else:
-            ops.paged_decode(out3, q3, k_cache, v_cache, block_table, cache_seqlens,
-                             float(softmax_scale), part_tokens, max_parts, ws, k_scale, v_scale)
-        return out
+        return dict(out=out, block_table=block_table, cache_seqlens=cache_seqlens,
+                    softmax_scale=float(softmax_scale), part_tokens=plan.part_tokens,
+                    max_parts=plan.max_parts, ws=ws, k_scale=k_scale, v_scale=v_scale)
+
+    def forward(self, q, k_cache, v_cache, cache_seqlens=None, **kwargs):
+        a = self._launch_args(q, k_cache, cache_seqlens, kwargs)
+        b = q.shape[0]
+        q3 = q.view(b, self.num_heads, self.head_dim)
+        out3 = a["out"].view(b, self.num_heads, self.head_dim)
+        call = torch.ops.fastkernels_amd.paged_decode if torch.compiler.is_compiling() \
+            else ops.paged_decode
+        call(out3, q3, k_cache, v_cache, a["block_table"], a["cache_seqlens"], a["softmax_scale"],
+             a["part_tokens"], a["max_parts"], a["ws"], a["k_scale"], a["v_scale"])
+        return a["out"]
+
+    def forward_store(self, q, key, value, k_cache, v_cache, slot_mapping, cache_seqlens=None,
+                      **kwargs):
+        """``StoreKVCache()(key, value, k_cache, v_cache, slot_mapping)`` then
+        ``forward(q, k_cache, v_cache, cache_seqlens, **kwargs)`` in one launch: the
+        decode step of Attention.forward_impl (attention_impl.py:313-363, :436-450).
+
+        Token b must be sequence b's new token: slot_mapping[b] is -1 or the slot of
+        position cache_seqlens[b] - 1 in block_table[b], as the engine's decode step
+        builds it (engine.py:5020-5024).  The cache and the output then equal the
+        two separate calls bit for bit."""
+        a = self._launch_args(q, k_cache, cache_seqlens, kwargs)
+        b = q.shape[0]
+        hk = k_cache.shape[2]
+        q3 = q.view(b, self.num_heads, self.head_dim)
+        k3 = key.view(b, hk, self.head_dim)
+        v3 = value.view(b, hk, self.head_dim)
+        out3 = a["out"].view(b, self.num_heads, self.head_dim)
+        call = torch.ops.fastkernels_amd.store_paged_decode if torch.compiler.is_compiling() \
+            else ops.store_paged_decode
+        call(out3, q3, k3, v3, k_cache, v_cache, slot_mapping, a["block_table"],
+             a["cache_seqlens"], a["softmax_scale"], a["part_tokens"], a["max_parts"], a["ws"],
+             a["k_scale"], a["v_scale"])
+        return a["out"]

@@ -85,6 +85,14 @@ struct DecodeParams {
   int32_t* tile_off; // balanced schedule: [batch + 1] tile prefix sums, then range size
   int batch;
   int num_groups;    // balanced schedule: work-groups per kv-head group
+  // Fused store (fk_store_paged_decode); new_k == nullptr for a plain decode.
+  // Row b of new_k / new_v (cache element type, heads contiguous) is sequence
+  // b's new token, stored at slot slot_mapping[b] (skipped when out of range).
+  const uint8_t* new_k;
+  const uint8_t* new_v;
+  int64_t new_k_stride;  // bytes between the rows of new_k
+  int64_t new_v_stride;
+  int slot_is_i64;
 };
 
 // Reductions over the four 16-lane rows of a wave (lanes r, r+16, r+32, r+48)
@@ -160,33 +168,119 @@ __device__ __forceinline__ int64_t page_of(const DecodeParams& P, const int32_t*
 // are unconditional so that every pipeline stage has the same number of loads
 // in flight and the compiler can wait for one stage with vmcnt(N) instead of
 // draining the queue; masked pages and tiles past the end load a safe page and
-// are discarded by the consumer.
+// are discarded by the consumer.  Fused store: tile row j (-1: none) is read
+// from the new K/V row (nk / nv, this kv head's slice) instead of the cache,
+// by selecting each lane's address, so the loop has no extra control flow.
 template <bool kFp8>
 __device__ __forceinline__ void load_tile(const DecodeParams& P, int64_t page, int h, int tok0,
-                                          int r, int g, TileRegs<kFp8>& t) {
+                                          int r, int g, TileRegs<kFp8>& t, int j = -1,
+                                          const uint8_t* nk = nullptr,
+                                          const uint8_t* nv = nullptr) {
   const int bs_mask = (1 << P.block_size_log2) - 1;
   const int64_t slot0 = (page << P.block_size_log2) + (tok0 & bs_mask);
   constexpr int kElem = kFp8 ? 1 : 2;
   const int64_t row_bytes = static_cast<int64_t>(P.num_kv_heads) * kHead * kElem;
   const int64_t head_off = static_cast<int64_t>(h) * kHead * kElem;
   const uint8_t* krow = P.k_cache + (slot0 + r) * row_bytes + head_off;
+  if (r == j) krow = nk;
+  const uint8_t* vrow[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    vrow[i] = P.v_cache + (slot0 + 4 * g + i) * row_bytes + head_off;
+    if (4 * g + i == j) vrow[i] = nv;
+  }
   if constexpr (!kFp8) {
     // Per instruction: 16 rows x 64 contiguous bytes.
 #pragma unroll
     for (int c = 0; c < 4; ++c)
       t.k[c] = ld16(krow + (32 * c + 8 * g) * 2);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      t.v[i] = ld16(P.v_cache + (slot0 + 4 * g + i) * row_bytes +
-                                               head_off + 8 * r * 2);
+    for (int i = 0; i < 4; ++i) t.v[i] = ld16(vrow[i] + 8 * r * 2);
   } else {
     t.k[0] = ld16(krow + 32 * g);
     t.k[1] = ld16(krow + 32 * g + 16);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      t.v[i] = ld8(P.v_cache + (slot0 + 4 * g + i) * row_bytes +
-                                               head_off + 8 * r);
+    for (int i = 0; i < 4; ++i) t.v[i] = ld8(vrow[i] + 8 * r);
   }
+}
+
+// ---------------------------------------------------------------------------
+// Fused store.  Sequence b's new token is at position p = ctx - 1.  The wave
+// that streams p's tile (one per kv head) loads b's new K/V row up front and,
+// when slot_mapping[b] is the slot of p in b's block table (the decode step),
+// uses it in place of the cache row at p, then writes it to the cache after
+// its tile loop, so no load waits for the store.  A slot that is not p's
+// ("orphan") is written by that same wave, or, when no wave streams p (no
+// context, or p past the launch's partitions), by a designated work-group; the
+// order of an orphan write against other reads of its slot is unspecified.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int64_t slot_of(const DecodeParams& P, const void* __restrict__ sm,
+                                           int b) {
+  return P.slot_is_i64 ? static_cast<const int64_t*>(sm)[b]
+                       : static_cast<int64_t>(static_cast<const int32_t*>(sm)[b]);
+}
+
+// The raw 32-bit words of slot_mapping[b] (both halves of an int64 entry, or
+// the int32 entry twice), loaded at computed indices without a branch so that
+// they issue with the wave's first page lookups; slot_value() combines them
+// behind a compiler barrier, so the wait for them lands where the slot is used.
+struct SlotWords {
+  int32_t lo, hi;
+};
+__device__ __forceinline__ SlotWords slot_words(const DecodeParams& P,
+                                                const void* __restrict__ sm, int b) {
+  const int32_t* s32 = static_cast<const int32_t*>(sm);
+  const int w = P.slot_is_i64;  // 0 or 1
+  const int i = b << w;
+  return SlotWords{s32[i], s32[i + w]};
+}
+__device__ __forceinline__ int64_t slot_value(const DecodeParams& P, SlotWords s) {
+  asm volatile("" : "+s"(s.lo), "+s"(s.hi));
+  const int64_t wide = static_cast<int64_t>(
+      (static_cast<uint64_t>(static_cast<uint32_t>(s.hi)) << 32) | static_cast<uint32_t>(s.lo));
+  return P.slot_is_i64 ? wide : static_cast<int64_t>(s.lo);
+}
+
+// In-range slot of sequence b's new row, or -1.
+__device__ __forceinline__ int64_t valid_slot(const DecodeParams& P, const void* __restrict__ sm,
+                                              int b) {
+  const int64_t slot = slot_of(P, sm, b);
+  return (slot >= 0 && slot < (P.num_blocks << P.block_size_log2)) ? slot : -1;
+}
+
+// Writes kv head h of sequence b's new K and V rows to cache slot `slot`.
+template <bool kFp8>
+__device__ __forceinline__ void store_new_row(const DecodeParams& P, int b, int h, int64_t slot,
+                                              int lane) {
+  store_new_chunk<kFp8>(P, slot, h, lane, load_new_chunk<kFp8>(P, b, h, lane));
+}
+
+// One 16-byte chunk of sequence b's new K/V row for kv head h, in the layout
+// store_new_chunk writes: lanes 0..15 hold K chunk (lane & 15), lanes 16..31 V
+// chunk (lane & 15); chunk indices past the row (fp8) and lanes >= 32 re-read a
+// valid chunk and are not stored.
+template <bool kFp8>
+__device__ __forceinline__ uint4 load_new_chunk(const DecodeParams& P, int b, int h, int lane) {
+  constexpr int kElem = kFp8 ? 1 : 2;
+  constexpr int kChunks = kHead * kElem / 16;
+  const int c = min(lane & 15, kChunks - 1);
+  const int64_t head_off = static_cast<int64_t>(h) * kHead * kElem;
+  const bool is_v = (lane & 16) != 0;
+  const uint8_t* src = (is_v ? P.new_v + b * P.new_v_stride : P.new_k + b * P.new_k_stride) +
+                       head_off + 16 * c;
+  return ld16(src);
+}
+template <bool kFp8>
+__device__ __forceinline__ void store_new_chunk(const DecodeParams& P, int64_t slot, int h,
+                                                int lane, const uint4& v) {
+  constexpr int kElem = kFp8 ? 1 : 2;
+  constexpr int kChunks = kHead * kElem / 16;
+  const int c = lane & 15;
+  if (lane >= 32 || c >= kChunks) return;
+  const int64_t row_bytes = static_cast<int64_t>(P.num_kv_heads) * kHead * kElem;
+  uint8_t* dst = const_cast<uint8_t*>((lane & 16) ? P.v_cache : P.k_cache) + slot * row_bytes +
+                 static_cast<int64_t>(h) * kHead * kElem + 16 * c;
+  *reinterpret_cast<uint4*>(dst) = v;
 }
 
 // K operand chunks (bf16) of a loaded tile.
@@ -233,15 +327,36 @@ __device__ __forceinline__ float row_value(float x, int g, int i) {
 // Online-softmax state of one wave over the G query heads of one kv head, and
 // the tile loop that streams a token range [tok_begin, tok_end) of a sequence
 // through it (tok_begin a multiple of 16).
-template <int kG, bool kFp8, int U>
+template <int kG, bool kFp8, int U, bool kStore>
 struct WaveState {
   float m_run;  // running max of column r (same in the 4 lanes of a column)
   float l_run;  // this lane's share of the running sum of column r
   floatx4_t o[8];
 
-  __device__ __forceinline__ void run(const DecodeParams& P, const int32_t* __restrict__ bt, int b,
-                                      int h, int tok_begin, int tok_end, int r, int g) {
+  // kStore: when the segment ends at the context end (tok_end == ctx) and
+  // slot_mapping[b] is the slot of position ctx - 1, that position's K/V are
+  // read from sequence b's new row instead of the cache (load_tile's row j),
+  // and the row (one 16-byte chunk per lane, loaded up front) is written to the
+  // cache after the loop, so no load waits for the store.
+  __device__ __forceinline__ void run(const DecodeParams& P, const int32_t* __restrict__ bt,
+                                      const void* __restrict__ sm, int b, int h, int tok_begin,
+                                      int tok_end, int ctx, int r, int g) {
     const int gqa = P.gqa;
+    SlotWords sw{-1, -1};
+    uint4 new_chunk = make_uint4(0, 0, 0, 0);  // this lane's chunk of b's new row
+    const uint8_t* nk = nullptr;  // b's new K / V row, kv head h
+    const uint8_t* nv = nullptr;
+    int ftok0 = -1;  // first token of the tile holding ctx - 1, if this segment ends there
+    if constexpr (kStore) {
+      constexpr int kElem = kFp8 ? 1 : 2;
+      const int64_t head_off = static_cast<int64_t>(h) * kHead * kElem;
+      nk = P.new_k + b * P.new_k_stride + head_off;
+      nv = P.new_v + b * P.new_v_stride + head_off;
+      new_chunk = load_new_chunk<kFp8>(P, b, h, 16 * g + r);
+      sw = slot_words(P, sm, b);
+      if (tok_end == ctx && ctx > tok_begin)
+        ftok0 = tok_begin + kTile * ((ctx - 1 - tok_begin) / kTile);
+    }
     const bool head_ok = r < gqa;
     // Q^T operand: column r = query head h*G + r; dims permuted as the K loads.
     bf16x8_t qb[4];
@@ -338,13 +453,24 @@ struct WaveState {
       for (int u = 0; u < U; ++u) {
         const int tok0 = tok_begin + kTile * min(t0 + u, ntiles - 1);
         pg[u] = page_of(P, bt, b, tok0);
-        load_tile<kFp8>(P, pg[u] < 0 ? 0 : pg[u], h, tok0, r, g, buf[u]);
+        int j = -1;
+        if constexpr (kStore) {
+          // Fused when b's slot is that of position ctx - 1: in this tile's page
+          // (a tile never spans pages), at offset (ctx - 1) mod block_size.
+          // Branch-free (selects), so the load sequence stays one block.
+          const int64_t want = (pg[u] << P.block_size_log2) +
+                               ((ctx - 1) & ((1 << P.block_size_log2) - 1));
+          const bool hit = tok0 == ftok0 && pg[u] >= 0 && slot_value(P, sw) == want;
+          j = hit ? ctx - 1 - tok0 : -1;
+        }
+        load_tile<kFp8>(P, pg[u] < 0 ? 0 : pg[u], h, tok0, r, g, buf[u], j, nk, nv);
       }
     };
     auto consume = [&](int t0, const TileRegs<kFp8>(&buf)[U], const int64_t(&pg)[U]) {
 #pragma unroll
-      for (int u = 0; u < U; ++u)
+      for (int u = 0; u < U; ++u) {
         if (t0 + u < ntiles) process(tok_begin + kTile * (t0 + u), pg[u], buf[u]);
+      }
     };
 #if FK_DECODE_PIPE
     // Two register sets of U tiles: one is consumed while the other is in flight.
@@ -369,6 +495,13 @@ struct WaveState {
 #endif
     // Column sums of l over the 4 lane groups: every lane of column j holds l_j.
     l_run = pair_sum(l_run);
+    // The wave that streamed position ctx - 1 writes b's row: at that position
+    // (fused) or, for any other in-range slot, there (an orphan).
+    if (kStore && ftok0 >= 0) {
+      const int64_t slot = slot_value(P, sw);
+      if (slot >= 0 && slot < (P.num_blocks << P.block_size_log2))
+        store_new_chunk<kFp8>(P, slot, h, 16 * g + r, new_chunk);
+    }
   }
 
   // Normalised output row(s) of kv head h for a sequence finished in place.
@@ -420,33 +553,43 @@ struct WaveState {
 // Fixed partitions: work-group = (partition p, kv-head group, sequence b);
 // wave w owns kv head h = blockIdx.y * NH + w and streams the partition.
 // Partial rows: ((b * Hk + h) * max_parts + p) * G + j.
-template <int NH, int kG, bool kFp8, int U>
+template <int NH, int kG, bool kFp8, int U, bool kStore>
 __global__ __launch_bounds__(NH * 64) void paged_decode_partition_kernel(
-    DecodeParams P, const int32_t* __restrict__ block_tables, const int32_t* __restrict__ ctx_lens) {
+    DecodeParams P, const int32_t* __restrict__ block_tables, const int32_t* __restrict__ ctx_lens,
+    const void* __restrict__ slot_mapping) {
   const int p = blockIdx.x;
   const int b = blockIdx.z;
   const int ctx = ctx_lens[b];
   const int tok_begin = p * P.part_tokens;
-  if (tok_begin >= ctx) return;  // uniform over the work-group
-  const int tok_end = min(ctx, tok_begin + P.part_tokens);
-  // Tokens past part_tokens * max_parts are outside the launch (the plan's
-  // max_seq_len bounds every context); clamp so the partition count matches
-  // the grid and the reduce kernel.
-  const int nparts = min((ctx + P.part_tokens - 1) / P.part_tokens, P.max_parts);
   // Wave index made provably uniform so that page lookups are scalar loads.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int h = blockIdx.y * NH + wave;
   if (h >= P.num_kv_heads) return;  // uniform over the wave; no barriers follow
   const int lane = threadIdx.x & 63;
-  const int r = lane & 15;
-  const int g = lane >> 4;
-  WaveState<kG, kFp8, U> st;
-  st.run(P, block_tables, b, h, tok_begin, tok_end, r, g);
-  if (nparts == 1) {
-    st.write_final(P, b, h, r, g);
-  } else {
-    const int64_t row0 = ((static_cast<int64_t>(b) * P.num_kv_heads + h) * P.max_parts + p) * P.gqa;
-    st.write_partial(P, row0, h, r, g);
+  if (tok_begin < ctx) {  // uniform over the work-group
+    const int tok_end = min(ctx, tok_begin + P.part_tokens);
+    // Tokens past part_tokens * max_parts are outside the launch (the plan's
+    // max_seq_len bounds every context); clamp so the partition count matches
+    // the grid and the reduce kernel.
+    const int nparts = min((ctx + P.part_tokens - 1) / P.part_tokens, P.max_parts);
+    const int r = lane & 15;
+    const int g = lane >> 4;
+    WaveState<kG, kFp8, U, kStore> st;
+    st.run(P, block_tables, slot_mapping, b, h, tok_begin, tok_end, ctx, r, g);
+    if (nparts == 1) {
+      st.write_final(P, b, h, r, g);
+    } else {
+      const int64_t row0 =
+          ((static_cast<int64_t>(b) * P.num_kv_heads + h) * P.max_parts + p) * P.gqa;
+      st.write_partial(P, row0, h, r, g);
+    }
+  }
+  // No partition streams position ctx - 1 (no context, or past the launch's
+  // partitions): partition 0 writes b's row.
+  if (kStore && p == 0 &&
+      (ctx <= 0 || ctx - 1 >= static_cast<int64_t>(P.part_tokens) * P.max_parts)) {
+    const int64_t os = valid_slot(P, slot_mapping, b);
+    if (os >= 0) store_new_row<kFp8>(P, b, h, os, lane);
   }
 }
 
@@ -457,9 +600,10 @@ __device__ __forceinline__ int tiles_of(int ctx) { return ctx > 0 ? (ctx + kTile
 // S = ceil(total / num_groups).  Partial rows of a cut sequence:
 // ((w * 2 + slot) * Hk + h) * G + j, slot 0 = the group's first segment,
 // slot 1 = its last (a group holds at most one cut sequence at each end).
-template <int NH, int kG, bool kFp8, int U>
+template <int NH, int kG, bool kFp8, int U, bool kStore>
 __global__ __launch_bounds__(NH * 64) void paged_decode_balanced_kernel(
-    DecodeParams P, const int32_t* __restrict__ block_tables, const int32_t* __restrict__ ctx_lens) {
+    DecodeParams P, const int32_t* __restrict__ block_tables, const int32_t* __restrict__ ctx_lens,
+    const void* __restrict__ slot_mapping) {
   extern __shared__ int32_t toff[];  // [batch + 1] tile prefix sums
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -487,32 +631,43 @@ __global__ __launch_bounds__(NH * 64) void paged_decode_balanced_kernel(
     for (int i = threadIdx.x; i <= batch; i += blockDim.x) P.tile_off[i] = toff[i];
     if (threadIdx.x == 0) P.tile_off[batch + 1] = S;
   }
-  const int t_lo = w * S;
-  const int t_hi = min(total, t_lo + S);
-  if (t_lo >= total) return;
   const int h = blockIdx.y * NH + wave;
   if (h >= P.num_kv_heads) return;  // uniform over the wave; no barriers follow
-  const int r = lane & 15;
-  const int g = lane >> 4;
-  // First sequence with tiles at t_lo: largest b with toff[b] <= t_lo.
-  int lo = 0, hi = batch;  // invariant: toff[lo] <= t_lo < toff[hi]
-  while (hi - lo > 1) {
-    const int mid = (lo + hi) >> 1;
-    if (toff[mid] <= t_lo) lo = mid; else hi = mid;
+  const int t_lo = w * S;
+  const int t_hi = min(total, t_lo + S);
+  if (t_lo < total) {
+    const int r = lane & 15;
+    const int g = lane >> 4;
+    // First sequence with tiles at t_lo: largest b with toff[b] <= t_lo.
+    int lo = 0, hi = batch;  // invariant: toff[lo] <= t_lo < toff[hi]
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (toff[mid] <= t_lo) lo = mid; else hi = mid;
+    }
+    WaveState<kG, kFp8, U, kStore> st;
+    for (int b = lo; b < batch && toff[b] < t_hi; ++b) {
+      const int s_lo = max(t_lo, toff[b]) - toff[b];
+      const int s_hi = min(t_hi, toff[b + 1]) - toff[b];
+      if (s_hi <= s_lo) continue;  // empty sequence
+      const int ctx = ctx_lens[b];
+      st.run(P, block_tables, slot_mapping, b, h, kTile * s_lo, min(ctx, kTile * s_hi), ctx, r,
+             g);
+      if (toff[b] >= t_lo && toff[b + 1] <= t_hi) {
+        st.write_final(P, b, h, r, g);
+      } else {
+        const int slot = toff[b] <= t_lo ? 0 : 1;
+        const int64_t row0 = ((static_cast<int64_t>(w) * 2 + slot) * P.num_kv_heads + h) * P.gqa;
+        st.write_partial(P, row0, h, r, g);
+      }
+    }
   }
-  WaveState<kG, kFp8, U> st;
-  for (int b = lo; b < batch && toff[b] < t_hi; ++b) {
-    const int s_lo = max(t_lo, toff[b]) - toff[b];
-    const int s_hi = min(t_hi, toff[b + 1]) - toff[b];
-    if (s_hi <= s_lo) continue;  // empty sequence
-    const int ctx = ctx_lens[b];
-    st.run(P, block_tables, b, h, kTile * s_lo, min(ctx, kTile * s_hi), r, g);
-    if (toff[b] >= t_lo && toff[b + 1] <= t_hi) {
-      st.write_final(P, b, h, r, g);
-    } else {
-      const int slot = toff[b] <= t_lo ? 0 : 1;
-      const int64_t row0 = ((static_cast<int64_t>(w) * 2 + slot) * P.num_kv_heads + h) * P.gqa;
-      st.write_partial(P, row0, h, r, g);
+  // Sequences without tiles (no context) have no wave that streams their
+  // last position: group w writes the rows of those with b = w mod G.
+  if (kStore) {
+    for (int b = w; b < batch; b += P.num_groups) {
+      if (toff[b + 1] != toff[b]) continue;
+      const int64_t os = valid_slot(P, slot_mapping, b);
+      if (os >= 0) store_new_row<kFp8>(P, b, h, os, lane);
     }
   }
 }
@@ -665,6 +820,7 @@ int validate(const char* name, int64_t batch, int num_heads, int num_kv_heads, i
 
 struct Launch {
   DecodeParams P;
+  const void* slot_mapping = nullptr;
   bool balanced;
   bool fp8;
   int nh;
@@ -722,6 +878,10 @@ int prepare(const char* name, Launch& L, void* out, int64_t out_row_stride, cons
   P.scale_log2 = scale * kLog2e;
   P.batch = static_cast<int>(batch);
   P.num_groups = static_cast<int>(max_parts);
+  P.new_k = nullptr;
+  P.new_v = nullptr;
+  P.new_k_stride = P.new_v_stride = 0;
+  P.slot_is_i64 = 0;
   const int64_t rows = partial_rows(balanced, batch, num_heads, max_parts);
   char* ws = static_cast<char*>(workspace);
   P.part_o = needs_ws ? reinterpret_cast<float*>(ws) : nullptr;
@@ -737,16 +897,26 @@ int prepare(const char* name, Launch& L, void* out, int64_t out_row_stride, cons
   return FK_OK;
 }
 
-template <int NH, int G, bool FP8>
-void launch_main(const Launch& L, hipStream_t stream) {
+template <int NH, int G, bool FP8, bool ST>
+void launch_main_st(const Launch& L, hipStream_t stream) {
   if (L.balanced) {
     const size_t lds = static_cast<size_t>(L.P.batch + 1) * sizeof(int32_t);
-    hipLaunchKernelGGL((paged_decode_balanced_kernel<NH, G, FP8, kChunk>), L.grid, dim3(NH * 64),
-                       lds, stream, L.P, L.P.block_tables, L.P.ctx_lens);
+    hipLaunchKernelGGL((paged_decode_balanced_kernel<NH, G, FP8, kChunk, ST>), L.grid,
+                       dim3(NH * 64), lds, stream, L.P, L.P.block_tables, L.P.ctx_lens,
+                       L.slot_mapping);
   } else {
-    hipLaunchKernelGGL((paged_decode_partition_kernel<NH, G, FP8, kChunk>), L.grid,
-                       dim3(NH * 64), 0, stream, L.P, L.P.block_tables, L.P.ctx_lens);
+    hipLaunchKernelGGL((paged_decode_partition_kernel<NH, G, FP8, kChunk, ST>), L.grid,
+                       dim3(NH * 64), 0, stream, L.P, L.P.block_tables, L.P.ctx_lens,
+                       L.slot_mapping);
   }
+}
+
+template <int NH, int G, bool FP8>
+void launch_main(const Launch& L, hipStream_t stream) {
+  if (L.P.new_k != nullptr)
+    launch_main_st<NH, G, FP8, true>(L, stream);
+  else
+    launch_main_st<NH, G, FP8, false>(L, stream);
 }
 
 template <int G, bool FP8>
@@ -867,6 +1037,52 @@ extern "C" int fk_paged_decode(void* out, int64_t out_row_stride, const void* q,
                                     ctx_lens, batch, num_heads, num_kv_heads, head_size,
                                     block_size, num_blocks, scale, part_tokens, max_parts,
                                     workspace, ws_bytes, stream);
+  if (rc != FK_OK) return rc;
+  return fk_paged_decode_reduce(out, out_row_stride, q, q_row_stride, k_cache, v_cache, kv_dtype,
+                                k_scale, v_scale, block_tables, bt_row_stride, ctx_lens, batch,
+                                num_heads, num_kv_heads, head_size, block_size, num_blocks, scale,
+                                part_tokens, max_parts, workspace, ws_bytes, stream);
+}
+
+extern "C" int fk_store_paged_decode(
+    void* out, int64_t out_row_stride, const void* q, int64_t q_row_stride, const void* key,
+    int64_t key_row_stride, const void* value, int64_t value_row_stride, const void* slot_mapping,
+    int slot_is_i64, void* k_cache, void* v_cache, int kv_dtype, const float* k_scale,
+    const float* v_scale, const int32_t* block_tables, int64_t bt_row_stride,
+    const int32_t* ctx_lens, int64_t batch, int num_heads, int num_kv_heads, int head_size,
+    int block_size, int64_t num_blocks, float scale, int64_t part_tokens, int64_t max_parts,
+    void* workspace, int64_t ws_bytes, void* stream) {
+  const char* name = "fk_store_paged_decode";
+  Launch L;
+  int rc = prepare(name, L, out, out_row_stride, q, q_row_stride, k_cache, v_cache, kv_dtype,
+                   k_scale, v_scale, block_tables, bt_row_stride, ctx_lens, batch, num_heads,
+                   num_kv_heads, head_size, block_size, num_blocks, scale, part_tokens, max_parts,
+                   workspace, ws_bytes);
+  if (rc != FK_OK) return rc;
+  const int64_t elem = kv_dtype == FK_DTYPE_FP8_E4M3FN ? 1 : 2;
+  const int64_t row = static_cast<int64_t>(num_kv_heads) * kHead;
+  FK_REQUIRE(key_row_stride >= row && value_row_stride >= row,
+             "%s: key/value row stride shorter than num_kv_heads * head_size", name);
+  if (batch == 0) return FK_OK;
+  FK_REQUIRE(key && value && slot_mapping, "%s: null pointer", name);
+  FK_REQUIRE(aligned16(key) && aligned16(value) && (key_row_stride * elem) % 16 == 0 &&
+                 (value_row_stride * elem) % 16 == 0,
+             "%s: key/value must be 16-byte aligned with 16-byte row strides", name);
+  FK_REQUIRE(num_blocks <= (int64_t(1) << 40) / block_size, "%s: cache too large", name);
+  L.P.new_k = static_cast<const uint8_t*>(key);
+  L.P.new_v = static_cast<const uint8_t*>(value);
+  L.P.new_k_stride = key_row_stride * elem;
+  L.P.new_v_stride = value_row_stride * elem;
+  L.P.slot_is_i64 = slot_is_i64 ? 1 : 0;
+  L.slot_mapping = slot_mapping;
+  hipStream_t s = as_stream(stream);
+  if (L.P.gqa <= 4)
+    launch_main_g<4>(L, s);
+  else if (L.P.gqa <= 8)
+    launch_main_g<8>(L, s);
+  else
+    launch_main_g<16>(L, s);
+  rc = check_launch(name);
   if (rc != FK_OK) return rc;
   return fk_paged_decode_reduce(out, out_row_stride, q, q_row_stride, k_cache, v_cache, kv_dtype,
                                 k_scale, v_scale, block_tables, bt_row_stride, ctx_lens, batch,

@@ -254,6 +254,46 @@ def paged_decode(out: torch.Tensor, q: torch.Tensor, k_cache: torch.Tensor,
                  max_parts, _ptr(workspace), ws_bytes, _stream(q))
 
 
+def store_paged_decode(out: torch.Tensor, q: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                       k_cache: torch.Tensor, v_cache: torch.Tensor, slot_mapping: torch.Tensor,
+                       block_table: torch.Tensor, cache_seqlens: torch.Tensor,
+                       softmax_scale: float, part_tokens: int, max_parts: int,
+                       workspace: torch.Tensor | None, k_scale: torch.Tensor | None = None,
+                       v_scale: torch.Tensor | None = None) -> None:
+    """store_kvcache(key, value, k_cache, v_cache, slot_mapping) followed by
+    paged_decode(...) in one launch (plus the merge launch).
+
+    Decode step layout: token b is sequence b's new token, so key/value/slot_mapping
+    have B rows and slot_mapping[b] is -1 or the slot of position cache_seqlens[b] - 1
+    in block_table[b] (fastkernels/infra/engine.py:5020-5024).  The result then equals
+    the two separate calls bit for bit.  Other slots are still written, but the
+    attention output of a sequence that reads another token's slot is unspecified."""
+    _check_decode(out, q, k_cache, v_cache, block_table, cache_seqlens, k_scale, v_scale)
+    b, hq, d = q.shape
+    nb, bs, hk, _ = k_cache.shape
+    if key.shape != (b, hk, d) or value.shape != key.shape:
+        raise ValueError("store_paged_decode: key/value must be [B, num_kv_heads, head_dim]")
+    if key.dtype != k_cache.dtype or value.dtype != v_cache.dtype:
+        raise TypeError("store_paged_decode: key/value dtype must equal the cache dtype")
+    for t, nm in ((key, "key"), (value, "value")):
+        if t.stride(2) != 1 or (hk > 1 and t.stride(1) != d):
+            raise ValueError(f"store_paged_decode: {nm} rows must be [Hk, D] contiguous")
+    if slot_mapping.dtype not in (torch.int32, torch.int64) or not slot_mapping.is_contiguous() \
+            or slot_mapping.numel() < b:
+        raise TypeError("store_paged_decode: slot_mapping must be contiguous int32/int64 [B]")
+    _same_device(q, key, value, slot_mapping)
+    if b == 0:
+        return
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    _native.call("fk_store_paged_decode", _ptr(out), out.stride(0), _ptr(q), q.stride(0),
+                 _ptr(key), key.stride(0), _ptr(value), value.stride(0), _ptr(slot_mapping),
+                 int(slot_mapping.dtype == torch.int64), _ptr(k_cache), _ptr(v_cache),
+                 _native.FK_DTYPE_FP8_E4M3FN if k_cache.dtype == _FP8 else _native.FK_DTYPE_BF16,
+                 _ptr(k_scale), _ptr(v_scale), _ptr(block_table), block_table.stride(0),
+                 _ptr(cache_seqlens), b, hq, hk, d, bs, nb, float(softmax_scale), part_tokens,
+                 max_parts, _ptr(workspace), ws_bytes, _stream(q))
+
+
 def paged_decode_phases(out, q, k_cache, v_cache, block_table, cache_seqlens, softmax_scale,
                         part_tokens, max_parts, workspace, k_scale=None, v_scale=None):
     """The two launches of :func:`paged_decode` as separate callables (for timing)."""
@@ -347,6 +387,10 @@ _LIB.define("store_kvcache(Tensor key, Tensor value, Tensor(a!) k_cache, Tensor(
 _LIB.define("paged_decode(Tensor(a!) out, Tensor q, Tensor k_cache, Tensor v_cache, "
             "Tensor block_table, Tensor cache_seqlens, float softmax_scale, int part_tokens, "
             "int max_parts, Tensor(b!)? workspace, Tensor? k_scale, Tensor? v_scale) -> ()")
+_LIB.define("store_paged_decode(Tensor(a!) out, Tensor q, Tensor key, Tensor value, "
+            "Tensor(b!) k_cache, Tensor(c!) v_cache, Tensor slot_mapping, Tensor block_table, "
+            "Tensor cache_seqlens, float softmax_scale, int part_tokens, int max_parts, "
+            "Tensor? workspace, Tensor? k_scale=None, Tensor? v_scale=None) -> ()")
 _LIB.define("silu_and_mul(Tensor! result, Tensor input) -> ()")
 _LIB.define("merge_attn_states(Tensor(a!) output, Tensor prefix_output, Tensor prefix_lse, "
             "Tensor suffix_output, Tensor suffix_lse, Tensor(b!)? output_lse) -> ()")
@@ -359,6 +403,7 @@ _IMPLS = {
     "paged_decode": paged_decode,
     "silu_and_mul": lambda result, input: silu_and_mul(result, input),
     "merge_attn_states": merge_attn_states,
+    "store_paged_decode": store_paged_decode,
 }
 for _name, _fn in _IMPLS.items():
     _LIB.impl(_name, _fn, "CUDA")

@@ -185,6 +185,37 @@ def c5_fp8_decode(device="cpu", batch=8, num_heads=64, kv_heads=8, head_dim=128,
                       ctx_t.to(torch.int32).to(device), 1.0 / math.sqrt(head_dim), kd, vd)
 
 
+@dataclass
+class StepRows:
+    """The new token of each sequence in a decode step (Attention.forward_impl input)."""
+    key: torch.Tensor           # [B, Hk, D], the cache dtype
+    value: torch.Tensor
+    slot_mapping: torch.Tensor  # [B] int64: the slot of position ctx - 1
+
+
+def decode_step_rows(case: DecodeCase, seed: int = SEED + 20) -> StepRows:
+    """Random new K/V rows and the slots the engine's decode step gives them:
+    slot = block_table[b][(ctx-1) // bs] * bs + (ctx-1) % bs (engine.py:5020-5024),
+    -1 for sequences without context."""
+    b, _, d = case.q.shape
+    hk, bs = case.k_cache.shape[2], case.k_cache.shape[1]
+    g = _gen("cpu", seed)
+    key = torch.randn(b, hk, d, generator=g)
+    value = torch.randn(b, hk, d, generator=g)
+    dev = case.q.device
+    if case.k_cache.dtype == torch.float8_e4m3fn:
+        key = quantize_fp8(key.to(dev).view(b, 1, hk, d), case.k_scale).view(b, hk, d)
+        value = quantize_fp8(value.to(dev).view(b, 1, hk, d), case.v_scale).view(b, hk, d)
+    else:
+        key, value = key.to(case.k_cache.dtype).to(dev), value.to(case.v_cache.dtype).to(dev)
+    ctx = case.ctx_lens.to("cpu").to(torch.int64)
+    bt = case.block_tables.to("cpu").to(torch.int64)
+    last = (ctx - 1).clamp(min=0)
+    slots = bt[torch.arange(b), last // bs] * bs + last % bs
+    slots = torch.where(ctx > 0, slots, torch.full_like(slots, -1))
+    return StepRows(key, value, slots.to(dev))
+
+
 # ---------------------------------------------------------------------------
 # C4 (chain)
 # ---------------------------------------------------------------------------

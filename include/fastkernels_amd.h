@@ -36,6 +36,9 @@
  *   fk_merge_attn_states
  *       fastkernels/tasks/baseline/L1/merge_attn_states.py:30-122 (merge_attn_states,
  *       MergeAttnStates.forward).
+ *   fk_store_paged_decode
+ *       fastkernels/tasks/baseline/L2/attention_impl.py:313-363 (forward_impl: store,
+ *       then the decode branch of _forward_pure :436-450).
  */
 #ifndef FASTKERNELS_AMD_H_
 #define FASTKERNELS_AMD_H_
@@ -174,6 +177,30 @@ int fk_paged_decode_reduce(void* out, int64_t out_row_stride, const void* q,
                            int num_kv_heads, int head_size, int block_size, int64_t num_blocks,
                            float scale, int64_t part_tokens, int64_t max_parts, void* workspace,
                            int64_t workspace_bytes, void* stream);
+
+/* store_kvcache + paged decode in one launch (plus the merge launch): the
+ * decode step of Attention.forward_impl
+ * (fastkernels/tasks/baseline/L2/attention_impl.py:313-363, :436-450), which calls
+ * StoreKVCache (store_kvcache.py:16-35) and then FlashAttnDecode.forward
+ * (flash_attn_decode.py:113-181).
+ * key/value: [batch, Hk, 128] of the cache element type (bf16 or fp8 e4m3fn), row
+ * strides in elements, 16-byte aligned.  slot_mapping: int32 or int64 [batch].  All
+ * other arguments as fk_paged_decode (same plan and workspace).
+ * Decode-step layout: slot_mapping[b] is negative (not stored) or the slot of position
+ * ctx_lens[b] - 1 in block_tables[b] (engine.py:5020-5024).  Then the cache and the
+ * output equal fk_store_kvcache followed by fk_paged_decode, bit for bit: the wave
+ * that streams that position writes the row and takes it from registers.  Other
+ * in-range slots are written too, but the output of a sequence that reads such a
+ * slot in the same call is unspecified. */
+int fk_store_paged_decode(void* out, int64_t out_row_stride, const void* q, int64_t q_row_stride,
+                          const void* key, int64_t key_row_stride, const void* value,
+                          int64_t value_row_stride, const void* slot_mapping, int slot_is_i64,
+                          void* k_cache, void* v_cache, int kv_dtype, const float* k_scale,
+                          const float* v_scale, const int32_t* block_tables,
+                          int64_t bt_row_stride, const int32_t* ctx_lens, int64_t batch,
+                          int num_heads, int num_kv_heads, int head_size, int block_size,
+                          int64_t num_blocks, float scale, int64_t part_tokens, int64_t max_parts,
+                          void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Log-sum-exp merge of two partial attention results (split-KV / prefix+suffix):
  *   out[t,h,:] = (prefix[t,h,:] e^(p - M) + suffix[t,h,:] e^(s - M)) / (e^(p - M) + e^(s - M))

@@ -1,0 +1,162 @@
+"""GPU parity of the fused store + decode launch (fk_store_paged_decode).
+
+The reference's decode step stores the new token's K/V (StoreKVCache) and then
+runs the decode (FlashAttnDecode) (fastkernels/tasks/baseline/L2/
+attention_impl.py:313-363).  The fused launch must leave the caches and the
+output exactly as those two calls do (bit for bit: the kernel takes the new row
+from registers instead of re-reading the cache), and the output must meet the
+oracle's attention bar on the updated cache.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from fastkernels_amd import ops, workloads
+
+pytestmark = pytest.mark.gpu
+
+
+def _flush(msg):
+    print(msg, flush=True)
+
+
+def _plan(case, num_splits, max_seq_len=None):
+    b, hq, d = case.q.shape
+    hk = case.k_cache.shape[2]
+    msl = case.max_seq_len if max_seq_len is None else max_seq_len
+    part, nparts, nbytes = ops.paged_decode_plan(b, hq, hk, d, msl, num_splits)
+    ws = torch.zeros(max(nbytes, 1), dtype=torch.uint8, device=case.q.device)
+    return part, nparts, ws
+
+
+def _separate(case, rows, num_splits, max_seq_len=None):
+    """store_kvcache then paged_decode on private copies of the caches."""
+    kc, vc = case.k_cache.clone(), case.v_cache.clone()
+    ops.store_kvcache(rows.key, rows.value, kc, vc, rows.slot_mapping)
+    part, nparts, ws = _plan(case, num_splits, max_seq_len)
+    out = torch.full_like(case.q, float("nan"))
+    ops.paged_decode(out, case.q, kc, vc, case.block_tables, case.ctx_lens, case.scale, part,
+                     nparts, ws, case.k_scale, case.v_scale)
+    torch.cuda.synchronize()
+    return out, kc, vc
+
+
+def _fused(case, rows, num_splits, max_seq_len=None, slot_mapping=None):
+    kc, vc = case.k_cache.clone(), case.v_cache.clone()
+    part, nparts, ws = _plan(case, num_splits, max_seq_len)
+    out = torch.full_like(case.q, float("nan"))
+    sm = rows.slot_mapping if slot_mapping is None else slot_mapping
+    ops.store_paged_decode(out, case.q, rows.key, rows.value, kc, vc, sm, case.block_tables,
+                           case.ctx_lens, case.scale, part, nparts, ws, case.k_scale,
+                           case.v_scale)
+    torch.cuda.synchronize()
+    return out, kc, vc
+
+
+def _assert_same(fused, sep, what):
+    for name, a, b in zip(("out", "k_cache", "v_cache"), fused, sep):
+        if a.dtype == torch.float8_e4m3fn:
+            a, b = a.view(torch.uint8), b.view(torch.uint8)
+        assert torch.equal(a, b), f"{what}: {name} differs from store_kvcache + paged_decode"
+
+
+@pytest.mark.parametrize("num_splits", [0, 3, 64])
+@pytest.mark.parametrize("slot_dtype", [torch.int64, torch.int32])
+def test_fused_equals_store_then_decode_bf16(cuda, num_splits, slot_dtype):
+    _flush(f"fused bf16 num_splits={num_splits} slots={slot_dtype}")
+    case = workloads.c3_decode(cuda, batch=64, pool_blocks=1024, ctx_lo=1, ctx_hi=3000, seed=41)
+    rows = workloads.decode_step_rows(case)
+    rows.slot_mapping = rows.slot_mapping.to(slot_dtype)
+    _assert_same(_fused(case, rows, num_splits), _separate(case, rows, num_splits),
+                 f"bf16 splits={num_splits}")
+
+
+@pytest.mark.parametrize("num_splits", [0, 16])
+def test_fused_equals_store_then_decode_fp8(cuda, num_splits):
+    _flush(f"fused fp8 num_splits={num_splits}")
+    case = workloads.c5_fp8_decode(cuda, batch=8, ctx_lens=[5000, 1, 16, 17, 256, 257, 4096, 777],
+                                   pool_blocks=64, seed=43)
+    rows = workloads.decode_step_rows(case)
+    _assert_same(_fused(case, rows, num_splits), _separate(case, rows, num_splits),
+                 f"fp8 splits={num_splits}")
+
+
+@pytest.mark.parametrize("block_size", [16, 64, 256])
+def test_fused_edge_positions(cuda, block_size):
+    """New token at the first/last row of a tile and of a page, ctx 1, empty
+    sequences with slot -1, GQA 4/8."""
+    lens = [1, 15, 16, 17, block_size - 1, block_size, block_size + 1, 0, 2 * block_size, 33, 0]
+    for hq in (32, 64):
+        _flush(f"fused edges bs={block_size} hq={hq}")
+        case = workloads.c3_decode(cuda, num_heads=hq, block_size=block_size, pool_blocks=256,
+                                   ctx_lens=lens, seed=44 + hq)
+        rows = workloads.decode_step_rows(case)
+        assert (rows.slot_mapping[torch.tensor(lens, device=cuda) == 0] == -1).all()
+        for ns in (0, 2):
+            _assert_same(_fused(case, rows, ns), _separate(case, rows, ns),
+                         f"bs={block_size} hq={hq} splits={ns}")
+
+
+def test_fused_orphan_slots_and_uncovered_positions(cuda):
+    """Slots that are not position ctx-1 of their sequence (written by a designated
+    work-group) and, with fixed partitions planned for a shorter max_seq_len, new
+    tokens past the last partition: the caches still match store_kvcache, and so
+    does the output (no sequence reads those slots here)."""
+    case = workloads.c3_decode(cuda, batch=12, pool_blocks=200, ctx_lo=20, ctx_hi=2000, seed=46)
+    rows = workloads.decode_step_rows(case)
+    used = set(case.block_tables[case.block_tables >= 0].tolist())
+    free = [p for p in range(200) if p not in used]
+    sm = rows.slot_mapping.clone()
+    bs = case.k_cache.shape[1]
+    sm[3] = free[0] * bs + 5            # orphan in an unused page
+    sm[7] = free[1] * bs + bs - 1
+    sm[9] = 200 * bs + 3                 # out of range: skipped by both paths
+    rows.slot_mapping = sm
+    for ns, msl in ((0, None), (4, None), (2, 512)):
+        _flush(f"fused orphans splits={ns} max_seq_len={msl}")
+        _assert_same(_fused(case, rows, ns, msl), _separate(case, rows, ns, msl),
+                     f"orphans splits={ns} msl={msl}")
+
+
+def test_fused_against_oracle(cuda):
+    """Output of the fused launch vs the oracle on the updated cache (bf16 bar)."""
+    case = workloads.c3_decode(cuda, batch=16, pool_blocks=256, ctx_lo=1, ctx_hi=3000, seed=47)
+    rows = workloads.decode_step_rows(case)
+    out, kc, vc = _fused(case, rows, 0)
+    bs = case.k_cache.shape[1]
+    ctx = case.ctx_lens.cpu().numpy()
+    bt = case.block_tables.cpu().numpy()
+    q = case.q.float().cpu().numpy()
+    got = out.float().cpu().numpy()
+    for i in range(16):
+        n = int(ctx[i])
+        pages = (n + bs - 1) // bs
+        ids = torch.from_numpy(bt[i, :pages].astype(np.int64)).to(cuda)
+        kp, vp = kc[ids].float().cpu().numpy(), vc[ids].float().cpu().numpy()
+        # the new token's row is in the cache at position n-1
+        assert np.array_equal(kp.reshape(-1, *kp.shape[2:])[n - 1], rows.key[i].float().cpu().numpy())
+        ref = oracle.paged_decode(q[i:i + 1], kp, vp, np.arange(pages)[None], np.array([n]),
+                                  case.scale)[0]
+        err = np.abs(got[i] - ref)
+        assert (err <= 1e-2 + 1e-2 * np.abs(ref)).all(), f"seq {i}: max err {err.max()}"
+
+
+def test_fused_candidate_forward_store(cuda):
+    from fastkernels_amd.candidate.L1.flash_attn_decode import FlashAttnDecode
+    from fastkernels_amd.candidate.L1.store_kvcache import StoreKVCache
+    case = workloads.c3_decode(cuda, batch=24, pool_blocks=512, ctx_lo=1, ctx_hi=4000, seed=48)
+    rows = workloads.decode_step_rows(case)
+    attn = FlashAttnDecode(32, 8, 128, page_size=256)
+    kc1, vc1 = case.k_cache.clone(), case.v_cache.clone()
+    StoreKVCache()(rows.key, rows.value, kc1, vc1, rows.slot_mapping)
+    ref = attn(case.q, kc1, vc1, cache_seqlens=case.ctx_lens, block_table=case.block_tables,
+               softmax_scale=case.scale, causal=True, max_seq_len=4000)
+    kc2, vc2 = case.k_cache.clone(), case.v_cache.clone()
+    got = attn.forward_store(case.q, rows.key, rows.value, kc2, vc2, rows.slot_mapping,
+                             cache_seqlens=case.ctx_lens, block_table=case.block_tables,
+                             softmax_scale=case.scale, causal=True, max_seq_len=4000)
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref) and torch.equal(kc1, kc2) and torch.equal(vc1, vc2)

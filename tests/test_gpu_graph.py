@@ -94,3 +94,59 @@ def test_decode_step_graph_capture_and_replay(cuda):
             assert torch.equal(got, ref), f"replay {i}: {name} differs from eager"
         kflat = static["k_cache"].view(-1, hk * d)
         assert torch.equal(kflat[static["slots"]], eager_bufs["k_cache"].view(-1, hk * d)[static["slots"]])
+
+
+def test_fused_store_decode_graph_capture_and_replay(cuda):
+    """FlashAttnDecode.forward_store (store + decode in one launch) captured once and
+    replayed on new decode-step inputs; every replay equals an eager run."""
+    from fastkernels_amd.candidate.L1.flash_attn_decode import FlashAttnDecode
+
+    b, bw = 48, 16
+    cases = [workloads.c3_decode(cuda, batch=b, pool_blocks=768, ctx_lo=1, ctx_hi=4000,
+                                 seed=500 + i) for i in range(3)]
+    steps = [workloads.decode_step_rows(c, seed=600 + i) for i, c in enumerate(cases)]
+    attn = FlashAttnDecode(32, 8, 128, page_size=256)
+    attn.preallocate(b, 4096, cuda)
+    c0, s0 = cases[0], steps[0]
+    static = dict(q=c0.q.clone(), key=s0.key.clone(), value=s0.value.clone(),
+                  k_cache=c0.k_cache.clone(), v_cache=c0.v_cache.clone(),
+                  slots=s0.slot_mapping.clone(), ctx=c0.ctx_lens.clone(),
+                  bt=torch.full((b, bw), -1, dtype=torch.int32, device=cuda))
+
+    def load(case, step):
+        for key, src in (("q", case.q), ("key", step.key), ("value", step.value),
+                         ("k_cache", case.k_cache), ("v_cache", case.v_cache),
+                         ("slots", step.slot_mapping), ("ctx", case.ctx_lens)):
+            static[key].copy_(src)
+        static["bt"].fill_(-1)
+        static["bt"][:, :case.block_tables.shape[1]].copy_(case.block_tables)
+
+    def run(bufs):
+        return attn.forward_store(bufs["q"], bufs["key"], bufs["value"], bufs["k_cache"],
+                                  bufs["v_cache"], bufs["slots"], cache_seqlens=bufs["ctx"],
+                                  block_table=bufs["bt"], softmax_scale=128 ** -0.5,
+                                  max_seq_len=4096)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        load(c0, s0)
+        run(static)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    load(c0, s0)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = run(static)
+    torch.cuda.synchronize()
+    for i, (case, step) in enumerate(list(zip(cases, steps)) + [(c0, s0)]):
+        load(case, step)
+        eager_bufs = {k: v.clone() for k, v in static.items()}
+        eager = run(eager_bufs).clone()
+        torch.cuda.synchronize()
+        load(case, step)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i}: output differs from eager"
+        assert torch.equal(static["k_cache"], eager_bufs["k_cache"]), f"replay {i}: k_cache"
+        assert torch.equal(static["v_cache"], eager_bufs["v_cache"]), f"replay {i}: v_cache"
