@@ -342,6 +342,35 @@ def bench_table(args):
          "oracle.rotary NeoX on the full q/k"))
     v = qkv[:, 5120:]
     dec = c4.decode
+    # Qwen3 attention prologue at C4: per-head q/k RMSNorm + rotary + store_kvcache,
+    # as the separate ops (norm of each head row, then rotary, then store) and fused.
+    g = torch.Generator().manual_seed(workloads.SEED + 7)
+    qw = (1 + 0.1 * torch.randn(128, generator=g)).to(torch.bfloat16).to(dev)
+    kw = (1 + 0.1 * torch.randn(128, generator=g)).to(torch.bfloat16).to(dev)
+    qkv_a = c4.qkv.clone()
+    qa, ka, va = qkv_a[:, :4096], qkv_a[:, 4096:5120], qkv_a[:, 5120:]
+    qrows = torch.empty(256, 32, 128, dtype=torch.bfloat16, device=dev)
+    krows = torch.empty(256, 8, 128, dtype=torch.bfloat16, device=dev)
+
+    def qk_separate():
+        ops.rms_norm(qrows, qa.view(256, 32, 128).contiguous(), qw, 1e-6)
+        ops.rms_norm(krows, ka.view(256, 8, 128).contiguous(), kw, 1e-6)
+        qa.copy_(qrows.view(256, 4096))
+        ka.copy_(krows.view(256, 1024))
+        ops.rotary_embedding(c4.positions, qa, ka, 128, rope.cos_sin_cache, True)
+        ops.store_kvcache(ka.view(256, 8, 128), va.view(256, 8, 128), dec.k_cache, dec.v_cache,
+                          c4.slot_mapping)
+
+    def qk_fused():
+        ops.qk_norm_rope_store(c4.positions, qa, ka, va, dec.k_cache, dec.v_cache,
+                               c4.slot_mapping, 128, rope.cos_sin_cache, True, qw, kw, 1e-6)
+
+    qk_bytes = (256 * (4096 + 2 * 1024) * 2 + 256 * (4096 + 1024) * 2 + 256 * 2 * 1024 * 2
+                + 256 * 16 + 256 * 128 * 4 + 2 * 128 * 2)
+    add("C4", "q/k RMSNorm + rotary + store_kvcache, separate (the reference's op sequence)",
+        qk_separate, qk_bytes)
+    add("C4", "q/k RMSNorm + rotary + store_kvcache, fused (qk_norm_rope_store)", qk_fused,
+        qk_bytes)
     kn16 = k.contiguous().view(torch.int16).view(256, 8, 128).cpu().numpy()
     vn16 = v.contiguous().view(torch.int16).view(256, 8, 128).cpu().numpy()
     sn = c4.slot_mapping.cpu().numpy()

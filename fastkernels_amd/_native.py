@@ -61,6 +61,10 @@ _SIGNATURES = {
                                       c_int, c_void_p, c_void_p, c_void_p, c_int64, c_void_p,
                                       c_int64, c_int, c_int, c_int, c_int, c_int64, c_float,
                                       c_int64, c_int64, c_void_p, c_int64, c_void_p]),
+    "fk_qk_norm_rope_store": (c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_void_p,
+                                      c_int64, c_void_p, c_void_p, c_float, c_void_p, c_int,
+                                      c_int64, c_int, c_int, c_void_p, c_void_p, c_void_p, c_int,
+                                      c_int64, c_int64, c_int, c_int, c_int, c_int, c_void_p]),
     "fk_merge_attn_states": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p,
                                      c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int, c_int,
                                      c_int64, c_int, c_void_p]),

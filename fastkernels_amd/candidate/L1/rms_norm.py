@@ -34,12 +34,26 @@ class RMSNorm(nn.Module):
         else:
             self.register_buffer("_unit_weight", torch.ones(hidden_size), persistent=False)
 
+    @staticmethod
+    def _rows_view_ok(x: torch.Tensor) -> bool:
+        """Whether x can be viewed as [rows, hidden] with one row stride."""
+        if x.dim() <= 2:
+            return True
+        try:
+            x.view(-1, x.shape[-1])
+            return True
+        except RuntimeError:
+            return False
+
     def forward(self, x: torch.Tensor, residual: torch.Tensor | None = None):
         weight = self.weight if self.elementwise_affine else self._unit_weight
         if weight.dtype != x.dtype or weight.device != x.device:
             weight = weight.to(device=x.device, dtype=x.dtype)
         weight = weight.detach()
-        if x.stride(-1) != 1:
+        if x.stride(-1) != 1 or not self._rows_view_ok(x):
+            # e.g. the per-head q/k norm of Qwen3 on a [N, H, D] view of the fused
+            # qkv buffer: the reference makes such inputs contiguous too
+            # (rms_norm.py forward_cuda).
             x = x.contiguous()
         compiling = torch.compiler.is_compiling()
         if residual is None:

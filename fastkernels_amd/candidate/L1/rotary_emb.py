@@ -4,7 +4,10 @@ Same constructor (including the Llama-3.1 frequency scaling of
 rotary_emb.py:44-68,95-102), the same ``cos_sin_cache`` buffer
 ([max_position, rot_dim] float32, cos then sin, rotary_emb.py:104-107), and
 ``forward(positions, query, key)`` rotating query/key in place and returning
-them (rotary_emb.py:179-191).  The kernel reads the float32 cache directly and
+them (rotary_emb.py:179-191).  ``forward_store(positions, query, key, value,
+k_cache, v_cache, slot_mapping, q_norm=None, k_norm=None)`` additionally applies
+Qwen3's per-head q/k RMSNorm first and stores the rotated key and the value
+rows in the paged cache, in one launch.  The kernel reads the float32 cache directly and
 rounds cos/sin to the query dtype itself, so no per-call cache cast is made
 (the reference casts the whole cache on every call when it is float32,
 rotary_emb.py:171-173).
@@ -58,6 +61,48 @@ class RotaryEmbedding(nn.Module):
         angles = torch.outer(torch.arange(max_position_embeddings, dtype=torch.float), inv_freq)
         cache = torch.cat((angles.cos(), angles.sin()), dim=-1).float()
         self.register_buffer("cos_sin_cache", cache, persistent=False)
+
+    def _cache_for(self, query: torch.Tensor) -> torch.Tensor:
+        cache = self.cos_sin_cache
+        if cache.device != query.device:
+            cache = cache.to(query.device)
+        if cache.dtype not in (torch.float32, query.dtype):
+            cache = cache.to(query.dtype)
+        return cache
+
+    def forward_store(self, positions: torch.Tensor, query: torch.Tensor, key: torch.Tensor,
+                      value: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                      slot_mapping: torch.Tensor, q_norm: nn.Module | None = None,
+                      k_norm: nn.Module | None = None):
+        """The attention block's q/k path in one launch: ``q_norm`` / ``k_norm``
+        per head (Qwen3, attention.py:120-135; RMSNorm modules or None), this
+        rotation (:137-139), then ``StoreKVCache()(key, value, k_cache, v_cache,
+        slot_mapping)`` (attention_impl.py:323-325).  query / key ([T, H*D] views,
+        e.g. slices of the fused qkv output) are rewritten in place and returned."""
+        if (q_norm is None) != (k_norm is None):
+            raise ValueError("RotaryEmbedding.forward_store: pass both q_norm and k_norm, or neither")
+        qw = kw = None
+        eps = 1e-6
+        if q_norm is not None:
+            if q_norm.eps != k_norm.eps:
+                raise ValueError("RotaryEmbedding.forward_store: q_norm and k_norm eps differ")
+            eps = q_norm.eps
+            qw = (q_norm.weight if q_norm.elementwise_affine else q_norm._unit_weight).detach()
+            kw = (k_norm.weight if k_norm.elementwise_affine else k_norm._unit_weight).detach()
+            qw = qw.to(device=query.device, dtype=query.dtype).contiguous()
+            kw = kw.to(device=query.device, dtype=query.dtype).contiguous()
+        cache = self._cache_for(query)
+        if positions.dtype != torch.int64:
+            positions = positions.to(torch.int64)
+        if not positions.is_contiguous():
+            positions = positions.contiguous()
+        k3 = k_cache.view(k_cache.shape[0], k_cache.shape[1], -1, self.head_dim)
+        v3 = v_cache.view(v_cache.shape[0], v_cache.shape[1], -1, self.head_dim)
+        call = torch.ops.fastkernels_amd.qk_norm_rope_store if torch.compiler.is_compiling() \
+            else ops.qk_norm_rope_store
+        call(positions, query, key, value, k3, v3, slot_mapping, self.head_dim, cache,
+             self.is_neox_style, qw, kw, float(eps))
+        return query, key
 
     def forward(self, positions: torch.Tensor, query: torch.Tensor, key: torch.Tensor | None):
         cache = self.cos_sin_cache

@@ -47,7 +47,12 @@ __device__ __forceinline__ float f16_to_f32(uint16_t h) {
 }
 
 __device__ __forceinline__ uint16_t f32_to_f16(float f) {
-  // The hardware conversion rounds to nearest even.
+  // The hardware conversion rounds to nearest even.  The empty asm pins f as an
+  // fp32 value first: otherwise the compiler may fold the producing fma into a
+  // mixed-precision fma that rounds to fp16 directly, which differs (rarely, by
+  // one ulp) from rounding the fp32 result, as torch does, and differs between
+  // kernels that inline the same arithmetic.
+  asm volatile("" : "+v"(f));
   return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
 }
 
@@ -84,6 +89,29 @@ struct Vec16 {
     typename T::storage e[N];
   };
 };
+
+// ---------------------------------------------------------------------------
+// Arithmetic shared by the separate row ops and the fused ones, written with
+// explicit fused multiply-adds so that every kernel that inlines them rounds
+// identically, whatever contraction the compiler would choose at each site.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float sumsq_add(float acc, float v) { return __builtin_fmaf(v, v, acc); }
+// 1 / sqrt(mean + eps) for a row of n elements whose squares sum to ss.
+__device__ __forceinline__ float rms_inv(float ss, float n, float eps) {
+  return 1.0f / __builtin_sqrtf(ss / n + eps);
+}
+// cast(cast(v * inv) * w): forward_native's two rounding points.
+template <typename T>
+__device__ __forceinline__ typename T::storage rms_apply(float v, float inv, float w) {
+  return T::from_f32(T::round(v * inv) * w);
+}
+// Rotation of the pair (x, y) by (c, s): x c - y s and y c + x s, one rounding.
+__device__ __forceinline__ float rope_x(float x, float y, float c, float s) {
+  return __builtin_fmaf(x, c, -(y * s));
+}
+__device__ __forceinline__ float rope_y(float x, float y, float c, float s) {
+  return __builtin_fmaf(y, c, x * s);
+}
 
 // ---------------------------------------------------------------------------
 // Wave64 reductions (butterfly over all 64 lanes; every lane gets the result).

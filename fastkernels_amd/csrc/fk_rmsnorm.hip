@@ -70,7 +70,7 @@ __global__ __launch_bounds__(64) void rmsnorm_wave_row(
       for (int e = 0; e < N; ++e) {
         s[j][e] = T::to_f32(xv[j].e[e]) + T::to_f32(rv[j].e[e]);
         nr.e[e] = T::from_f32(s[j][e]);
-        ss += in_row ? s[j][e] * s[j][e] : 0.f;
+        ss = in_row ? sumsq_add(ss, s[j][e]) : ss;
       }
       if (in_row) rr[vi] = nr.raw;
     }
@@ -81,22 +81,19 @@ __global__ __launch_bounds__(64) void rmsnorm_wave_row(
 #pragma unroll
       for (int e = 0; e < N; ++e) {
         s[j][e] = T::to_f32(xv[j].e[e]);
-        ss += in_row ? s[j][e] * s[j][e] : 0.f;
+        ss = in_row ? sumsq_add(ss, s[j][e]) : ss;
       }
     }
   }
   ss = wave_sum(ss);
-  const float inv = 1.0f / __builtin_sqrtf(ss / static_cast<float>(hidden) + eps);
+  const float inv = rms_inv(ss, static_cast<float>(hidden), eps);
   uint4* orow = reinterpret_cast<uint4*>(out + row * out_row_stride);
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
     const int64_t vi = lane + 64 * j;
     V ov;
 #pragma unroll
-    for (int e = 0; e < N; ++e) {
-      const float xh = T::round(s[j][e] * inv);
-      ov.e[e] = T::from_f32(xh * T::to_f32(wv[j].e[e]));
-    }
+    for (int e = 0; e < N; ++e) ov.e[e] = rms_apply<T>(s[j][e], inv, T::to_f32(wv[j].e[e]));
     if (vi < nvec) orow[vi] = ov.raw;
   }
 }
@@ -119,14 +116,14 @@ __global__ __launch_bounds__(256) void rmsnorm_block_row(
   for (int64_t i = threadIdx.x; i < hidden; i += 256) {
     float v = T::to_f32(xr[i]);
     if constexpr (kFused) v += T::to_f32(rr[i]);
-    ss += v * v;
+    ss = sumsq_add(ss, v);
   }
   __shared__ float red[4];
   ss = wave_sum(ss);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
   __syncthreads();
   ss = red[0] + red[1] + red[2] + red[3];
-  const float inv = 1.0f / __builtin_sqrtf(ss / static_cast<float>(hidden) + eps);
+  const float inv = rms_inv(ss, static_cast<float>(hidden), eps);
   typename T::storage* orow = out + row * out_row_stride;
   // Same element ownership as pass 1: lane i only touches elements i (mod 256).
   for (int64_t i = threadIdx.x; i < hidden; i += 256) {
@@ -135,8 +132,7 @@ __global__ __launch_bounds__(256) void rmsnorm_block_row(
       v += T::to_f32(rr[i]);
       rr[i] = T::from_f32(v);
     }
-    const float xh = T::round(v * inv);
-    orow[i] = T::from_f32(xh * T::to_f32(weight[i]));
+    orow[i] = rms_apply<T>(v, inv, T::to_f32(weight[i]));
   }
 }
 

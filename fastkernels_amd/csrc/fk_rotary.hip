@@ -53,8 +53,8 @@ __global__ __launch_bounds__(256) void rotary_vec(
         const float s = T::round(CT::to_f32(cs[half + i0 + e]));
         const float x = T::to_f32(xv.e[e]);
         const float y = T::to_f32(yv.e[e]);
-        xv.e[e] = T::from_f32(x * c - y * s);
-        yv.e[e] = T::from_f32(y * c + x * s);
+        xv.e[e] = T::from_f32(rope_x(x, y, c, s));
+        yv.e[e] = T::from_f32(rope_y(x, y, c, s));
       }
       *reinterpret_cast<uint4*>(base + i0) = xv.raw;
       *reinterpret_cast<uint4*>(base + half + i0) = yv.raw;
@@ -69,8 +69,8 @@ __global__ __launch_bounds__(256) void rotary_vec(
         const float s = T::round(CT::to_f32(cs[half + i]));
         const float x = T::to_f32(v.e[2 * j]);
         const float y = T::to_f32(v.e[2 * j + 1]);
-        v.e[2 * j] = T::from_f32(x * c - y * s);
-        v.e[2 * j + 1] = T::from_f32(y * c + x * s);
+        v.e[2 * j] = T::from_f32(rope_x(x, y, c, s));
+        v.e[2 * j + 1] = T::from_f32(rope_y(x, y, c, s));
       }
       *reinterpret_cast<uint4*>(base + e0) = v.raw;
     }
@@ -103,8 +103,8 @@ __global__ __launch_bounds__(256) void rotary_scalar(
     const float s = T::round(CT::to_f32(cs[half + i]));
     const float x = T::to_f32(base[xi]);
     const float y = T::to_f32(base[yi]);
-    base[xi] = T::from_f32(x * c - y * s);
-    base[yi] = T::from_f32(y * c + x * s);
+    base[xi] = T::from_f32(rope_x(x, y, c, s));
+    base[yi] = T::from_f32(rope_y(x, y, c, s));
   }
 }
 

@@ -190,6 +190,75 @@ def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
 
 
 # ---------------------------------------------------------------------------
+# Fused per-head q/k RMSNorm + rotary + store_kvcache
+# ---------------------------------------------------------------------------
+def _token_rows(t: torch.Tensor, tokens: int, head_size: int, what: str) -> tuple[int, int]:
+    """(row_stride, heads) of a [tokens, heads*head_size] (or [tokens, heads, head_size])
+    view whose rows are contiguous."""
+    w = t.numel() // tokens
+    if w % head_size:
+        raise ValueError(f"{what}: width {w} is not a multiple of head_size {head_size}")
+    try:
+        t2 = t.view(tokens, w)
+    except RuntimeError as e:
+        raise ValueError(f"{what}: rows must be [heads*head_size] ({e})") from None
+    if t2.stride(1) != 1:
+        raise ValueError(f"{what}: rows must be contiguous")
+    return t2.stride(0), w // head_size
+
+
+def qk_norm_rope_store(positions: torch.Tensor, query: torch.Tensor, key: torch.Tensor,
+                       value: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                       slot_mapping: torch.Tensor, head_size: int, cos_sin_cache: torch.Tensor,
+                       is_neox: bool, q_weight: torch.Tensor | None = None,
+                       k_weight: torch.Tensor | None = None, eps: float = 1e-6) -> None:
+    """One launch for: q = q_norm(q per head), k = k_norm(k per head) (when weights are
+    given, Qwen3), rotary(positions, q, k), store_kvcache(k, v, caches, slot_mapping).
+
+    query / key are rewritten in place (normed and rotated); the caches receive the
+    rotated k rows and the v rows.  Bit-identical to rms_norm on each head row,
+    rotary_embedding and store_kvcache run one after another."""
+    if positions.dtype != torch.int64 or not positions.is_contiguous():
+        raise TypeError("qk_norm_rope_store: positions must be contiguous int64")
+    tokens = positions.numel()
+    for t, nm in ((key, "key"), (value, "value"), (k_cache, "k_cache"), (v_cache, "v_cache")):
+        if t.dtype != query.dtype:
+            raise TypeError(f"qk_norm_rope_store: {nm} dtype must equal the query dtype")
+    if cos_sin_cache.dim() != 2 or not cos_sin_cache.is_contiguous() or \
+            cos_sin_cache.dtype not in (torch.float32, query.dtype):
+        raise ValueError("qk_norm_rope_store: cos_sin_cache must be contiguous float32 or "
+                         "query-dtype [max_pos, rot_dim]")
+    if (q_weight is None) != (k_weight is None):
+        raise ValueError("qk_norm_rope_store: pass both q_weight and k_weight, or neither")
+    for w, nm in ((q_weight, "q_weight"), (k_weight, "k_weight")):
+        if w is not None and (w.dtype != query.dtype or w.numel() != head_size or
+                              not w.is_contiguous()):
+            raise ValueError(f"qk_norm_rope_store: {nm} must be contiguous [head_size] of the "
+                             "query dtype")
+    if slot_mapping.dtype not in (torch.int32, torch.int64) or not slot_mapping.is_contiguous() \
+            or slot_mapping.numel() < tokens:
+        raise TypeError("qk_norm_rope_store: slot_mapping must be contiguous int32/int64 [T]")
+    if k_cache.dim() != 4 or v_cache.shape != k_cache.shape or k_cache.shape[3] != head_size \
+            or not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("qk_norm_rope_store: caches must be contiguous [blocks, bs, Hk, D]")
+    _same_device(positions, query, key, value, k_cache, v_cache, slot_mapping, cos_sin_cache)
+    if tokens == 0:
+        return
+    qs, hq = _token_rows(query, tokens, head_size, "qk_norm_rope_store query")
+    ks, hk = _token_rows(key, tokens, head_size, "qk_norm_rope_store key")
+    vs, hv = _token_rows(value, tokens, head_size, "qk_norm_rope_store value")
+    if hv != hk or k_cache.shape[2] != hk:
+        raise ValueError("qk_norm_rope_store: key, value and caches must have the same kv heads")
+    _native.call("fk_qk_norm_rope_store", _ptr(positions), _ptr(query), qs, _ptr(key), ks,
+                 _ptr(value), vs, _ptr(q_weight), _ptr(k_weight), float(eps),
+                 _ptr(cos_sin_cache), _tag(cos_sin_cache, "rotary cache"),
+                 cos_sin_cache.shape[0], cos_sin_cache.shape[1], int(bool(is_neox)),
+                 _ptr(k_cache), _ptr(v_cache), _ptr(slot_mapping),
+                 int(slot_mapping.dtype == torch.int64), k_cache.shape[0] * k_cache.shape[1],
+                 tokens, hq, hk, head_size, _tag(query, "qk_norm_rope_store"), _stream(query))
+
+
+# ---------------------------------------------------------------------------
 # Paged decode attention
 # ---------------------------------------------------------------------------
 class DecodePlan(NamedTuple):
@@ -391,6 +460,10 @@ _LIB.define("store_paged_decode(Tensor(a!) out, Tensor q, Tensor key, Tensor val
             "Tensor(b!) k_cache, Tensor(c!) v_cache, Tensor slot_mapping, Tensor block_table, "
             "Tensor cache_seqlens, float softmax_scale, int part_tokens, int max_parts, "
             "Tensor? workspace, Tensor? k_scale=None, Tensor? v_scale=None) -> ()")
+_LIB.define("qk_norm_rope_store(Tensor positions, Tensor(a!) query, Tensor(b!) key, "
+            "Tensor value, Tensor(c!) k_cache, Tensor(d!) v_cache, Tensor slot_mapping, "
+            "int head_size, Tensor cos_sin_cache, bool is_neox, Tensor? q_weight=None, "
+            "Tensor? k_weight=None, float eps=1e-6) -> ()")
 _LIB.define("silu_and_mul(Tensor! result, Tensor input) -> ()")
 _LIB.define("merge_attn_states(Tensor(a!) output, Tensor prefix_output, Tensor prefix_lse, "
             "Tensor suffix_output, Tensor suffix_lse, Tensor(b!)? output_lse) -> ()")
@@ -404,6 +477,7 @@ _IMPLS = {
     "silu_and_mul": lambda result, input: silu_and_mul(result, input),
     "merge_attn_states": merge_attn_states,
     "store_paged_decode": store_paged_decode,
+    "qk_norm_rope_store": qk_norm_rope_store,
 }
 for _name, _fn in _IMPLS.items():
     _LIB.impl(_name, _fn, "CUDA")

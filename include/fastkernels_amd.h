@@ -39,6 +39,9 @@
  *   fk_store_paged_decode
  *       fastkernels/tasks/baseline/L2/attention_impl.py:313-363 (forward_impl: store,
  *       then the decode branch of _forward_pure :436-450).
+ *   fk_qk_norm_rope_store
+ *       fastkernels/tasks/baseline/L2/attention.py:120-140 (q_norm/k_norm, rotary_emb)
+ *       followed by attention_impl.py:323-325 (store_kvcache).
  */
 #ifndef FASTKERNELS_AMD_H_
 #define FASTKERNELS_AMD_H_
@@ -177,6 +180,27 @@ int fk_paged_decode_reduce(void* out, int64_t out_row_stride, const void* q,
                            int num_kv_heads, int head_size, int block_size, int64_t num_blocks,
                            float scale, int64_t part_tokens, int64_t max_parts, void* workspace,
                            int64_t workspace_bytes, void* stream);
+
+/* Per-head q/k RMSNorm (optional) + rotary embedding + store_kvcache in one launch:
+ * the attention block between the qkv projection and the decode
+ * (fastkernels/tasks/baseline/L2/attention.py:120-140: q_norm / k_norm on [N, H, D]
+ * views, then rotary_emb; then attention_impl.py:323-325 store_kvcache).
+ * query [tokens, Hq*D], key / value [tokens, Hk*D]: rows with the given strides (views
+ * of the fused qkv buffer), heads contiguous.  query and key are rewritten in place
+ * (normed when q_weight / k_weight are given, both or neither, [D] of the dtype; then
+ * rotated as fk_rotary_embedding); the rotated key rows and the value rows go to
+ * cache slot slot_mapping[t] (skipped outside [0, num_slots)).  Caches:
+ * [num_slots, Hk, D] of the dtype.  Vector path only: 16-byte aligned rows, caches and
+ * weights, D / (16 / elem) a power of two <= 64; otherwise FK_ERR_UNSUPPORTED.  The
+ * results are bit-identical to fk_rmsnorm per head row, fk_rotary_embedding and
+ * fk_store_kvcache in sequence. */
+int fk_qk_norm_rope_store(const int64_t* positions, void* query, int64_t q_row_stride, void* key,
+                          int64_t k_row_stride, const void* value, int64_t v_row_stride,
+                          const void* q_weight, const void* k_weight, float eps,
+                          const void* cos_sin, int cache_dtype, int64_t max_position, int rot_dim,
+                          int is_neox, void* k_cache, void* v_cache, const void* slot_mapping,
+                          int slot_is_i64, int64_t num_slots, int64_t tokens, int num_heads,
+                          int num_kv_heads, int head_size, int dtype, void* stream);
 
 /* store_kvcache + paged decode in one launch (plus the merge launch): the
  * decode step of Attention.forward_impl

@@ -160,3 +160,142 @@ def test_fused_candidate_forward_store(cuda):
                              softmax_scale=case.scale, causal=True, max_seq_len=4000)
     torch.cuda.synchronize()
     assert torch.equal(got, ref) and torch.equal(kc1, kc2) and torch.equal(vc1, vc2)
+
+
+# ---------------------------------------------------------------------------
+# Fused per-head q/k RMSNorm + rotary + store_kvcache (fk_qk_norm_rope_store)
+# ---------------------------------------------------------------------------
+def _qkv_case(cuda, dtype, t, hq, hk, d, seed, pool_blocks=64, bs=16, max_pos=4096):
+    g = torch.Generator().manual_seed(seed)
+    qkv = (2 * torch.randn(t, (hq + 2 * hk) * d, generator=g)).to(dtype).to(cuda)
+    positions = torch.randint(0, max_pos, (t,), generator=g).to(cuda)
+    perm = torch.randperm(pool_blocks * bs, generator=g)[:t]
+    slots = perm.to(torch.int64).to(cuda)
+    kc = torch.randn(pool_blocks, bs, hk, d, generator=g).to(dtype).to(cuda)
+    vc = torch.randn(pool_blocks, bs, hk, d, generator=g).to(dtype).to(cuda)
+    qw = (1 + 0.2 * torch.randn(d, generator=g)).to(dtype).to(cuda)
+    kw = (1 + 0.2 * torch.randn(d, generator=g)).to(dtype).to(cuda)
+    return qkv, positions, slots, kc, vc, qw, kw
+
+
+def _split(qkv, hq, hk, d):
+    return qkv[:, :hq * d], qkv[:, hq * d:(hq + hk) * d], qkv[:, (hq + hk) * d:]
+
+
+def _chain(qkv, positions, slots, kc, vc, qw, kw, eps, hq, hk, d, cache, neox):
+    """rms_norm per head row, rotary_embedding, store_kvcache: the separate ops."""
+    t = qkv.shape[0]
+    q, k, v = _split(qkv, hq, hk, d)
+    if qw is not None:
+        for x, w, h in ((q, qw, hq), (k, kw, hk)):
+            rows = x.reshape(t, h, d).contiguous()
+            out = torch.empty_like(rows)
+            ops.rms_norm(out, rows, w, eps)
+            x.copy_(out.view(t, h * d))
+    ops.rotary_embedding(positions, q, k, d, cache, neox)
+    ops.store_kvcache(k.view(t, hk, d), v.view(t, hk, d), kc, vc, slots)
+
+
+@pytest.mark.parametrize("neox", [True, False])
+@pytest.mark.parametrize("norm", [True, False])
+@pytest.mark.parametrize("cache_f32", [True, False])
+def test_qk_norm_rope_store_equals_chain(cuda, neox, norm, cache_f32):
+    """Qwen3-8B attention shapes (Hq 32, Hk 8, D 128), 256 tokens: bit-identical q, k
+    and caches; tokens with slot -1 or an out-of-range position included."""
+    from fastkernels_amd.candidate.L1.rotary_emb import RotaryEmbedding
+    _flush(f"qk_norm_rope_store neox={neox} norm={norm} cache_f32={cache_f32}")
+    t, hq, hk, d = 256, 32, 8, 128
+    qkv, pos, slots, kc, vc, qw, kw = _qkv_case(cuda, torch.bfloat16, t, hq, hk, d, seed=61)
+    pos[3] = -1
+    pos[10] = 4096  # == max_position: not rotated
+    slots[5] = -1
+    slots[6] = kc.shape[0] * kc.shape[1]  # out of range: not stored
+    rope = RotaryEmbedding(d, 4096, 1e6, is_neox_style=neox).to(cuda)
+    cache = rope.cos_sin_cache if cache_f32 else rope.cos_sin_cache.bfloat16()
+    eps = 1e-6
+    a = (qkv.clone(), kc.clone(), vc.clone())
+    _chain(a[0], pos, slots, a[1], a[2], qw if norm else None, kw, eps, hq, hk, d, cache, neox)
+    b = (qkv.clone(), kc.clone(), vc.clone())
+    q, k, v = _split(b[0], hq, hk, d)
+    ops.qk_norm_rope_store(pos, q, k, v, b[1], b[2], slots, d, cache, neox,
+                           qw if norm else None, kw if norm else None, eps)
+    torch.cuda.synchronize()
+    for name, x, y in zip(("qkv", "k_cache", "v_cache"), a, b):
+        assert torch.equal(x, y), f"{name} differs from rms_norm + rotary + store_kvcache"
+
+
+def test_qk_norm_rope_store_against_oracle(cuda):
+    """The fused result against the oracle's rms_norm -> rotary -> store on the same
+    inputs (bf16 bar), and v copied bit-exactly."""
+    t, hq, hk, d = 64, 16, 4, 128
+    qkv, pos, slots, kc, vc, qw, kw = _qkv_case(cuda, torch.bfloat16, t, hq, hk, d, seed=62)
+    cs = oracle.rope_cos_sin_cache(d, 4096, 1e6)
+    cache = torch.from_numpy(cs).to(cuda)
+    x = qkv.float().cpu().numpy()
+    q0, k0, v0 = x[:, :hq * d], x[:, hq * d:(hq + hk) * d], x[:, (hq + hk) * d:]
+    qn = oracle.rms_norm(q0.reshape(t, hq, d), qw.float().cpu().numpy(), 1e-6, "bf16")
+    kn = oracle.rms_norm(k0.reshape(t, hk, d), kw.float().cpu().numpy(), 1e-6, "bf16")
+    qr, kr = oracle.rotary(pos.cpu().numpy(), qn.reshape(t, -1), kn.reshape(t, -1), d, cs, True,
+                           "bf16")
+    q, k, v = _split(qkv, hq, hk, d)
+    ops.qk_norm_rope_store(pos, q, k, v, kc, vc, slots, d, cache, True, qw, kw, 1e-6)
+    torch.cuda.synchronize()
+    for got, ref, nm in ((q, qr, "q"), (k, kr, "k")):
+        g = got.float().cpu().numpy()
+        err = np.abs(g - ref)
+        assert (err <= 1e-2 + 1e-2 * np.abs(ref)).all(), f"{nm}: max err {err.max()}"
+    kflat = kc.view(-1, hk * d)
+    vflat = vc.view(-1, hk * d)
+    assert torch.equal(kflat[slots], k) and torch.equal(vflat[slots], v)
+
+
+@pytest.mark.parametrize("dtype,d,rot", [(torch.float32, 128, 128), (torch.float32, 64, 64),
+                                         (torch.bfloat16, 128, 64), (torch.float16, 256, 256)])
+def test_qk_norm_rope_store_dtypes_and_partial_rotary(cuda, dtype, d, rot):
+    _flush(f"qk_norm_rope_store {dtype} d={d} rot={rot}")
+    t, hq, hk = 33, 8, 2
+    qkv, pos, slots, kc, vc, qw, kw = _qkv_case(cuda, dtype, t, hq, hk, d, seed=63)
+    slots = slots.to(torch.int32)
+    inv = 1.0 / (1e4 ** (torch.arange(0, rot, 2, dtype=torch.float32) / rot))
+    ang = torch.outer(torch.arange(4096, dtype=torch.float32), inv)
+    cache = torch.cat((ang.cos(), ang.sin()), -1).to(cuda)
+    for neox in (True, False):
+        a = (qkv.clone(), kc.clone(), vc.clone())
+        _chain(a[0], pos, slots, a[1], a[2], qw, kw, 1e-5, hq, hk, d, cache, neox)
+        b = (qkv.clone(), kc.clone(), vc.clone())
+        q, k, v = _split(b[0], hq, hk, d)
+        ops.qk_norm_rope_store(pos, q, k, v, b[1], b[2], slots, d, cache, neox, qw, kw, 1e-5)
+        torch.cuda.synchronize()
+        for name, x, y in zip(("qkv", "k_cache", "v_cache"), a, b):
+            assert torch.equal(x, y), f"{name} differs (neox={neox})"
+
+
+def test_qk_norm_rope_store_candidate(cuda):
+    """RotaryEmbedding.forward_store with RMSNorm q/k norms == the modules one by one
+    (the reference's Qwen3 path: norms on [N, H, D] views, rotary, StoreKVCache)."""
+    from fastkernels_amd.candidate.L1.rms_norm import RMSNorm
+    from fastkernels_amd.candidate.L1.rotary_emb import RotaryEmbedding
+    from fastkernels_amd.candidate.L1.store_kvcache import StoreKVCache
+    t, hq, hk, d = 48, 32, 8, 128
+    qkv, pos, slots, kc, vc, qw, kw = _qkv_case(cuda, torch.bfloat16, t, hq, hk, d, seed=64)
+    qn, kn = RMSNorm(d, eps=1e-6), RMSNorm(d, eps=1e-6)
+    qn.weight.data.copy_(qw.float())
+    kn.weight.data.copy_(kw.float())
+    qn, kn = qn.to(cuda).to(torch.bfloat16), kn.to(cuda).to(torch.bfloat16)
+    rope = RotaryEmbedding(d, 4096, 1e6).to(cuda)
+    # module by module, as attention.py:120-140 and attention_impl.py:323-325
+    a = qkv.clone()
+    q, k, v = _split(a, hq, hk, d)
+    q2 = qn(q.view(t, hq, d)).view(t, hq * d)
+    k2 = kn(k.view(t, hk, d)).view(t, hk * d)
+    q2, k2 = rope(pos, q2, k2)
+    kc1, vc1 = kc.clone(), vc.clone()
+    StoreKVCache()(k2.view(t, hk, d), v.view(t, hk, d), kc1, vc1, slots)
+    # fused
+    b = qkv.clone()
+    qb, kb, vb = _split(b, hq, hk, d)
+    kc2, vc2 = kc.clone(), vc.clone()
+    rope.forward_store(pos, qb, kb, vb, kc2, vc2, slots, q_norm=qn, k_norm=kn)
+    torch.cuda.synchronize()
+    assert torch.equal(qb, q2) and torch.equal(kb, k2)
+    assert torch.equal(kc1, kc2) and torch.equal(vc1, vc2)
