@@ -1,0 +1,103 @@
+"""Candidate ``FlashAttnPrefill`` for fastkernels/tasks/baseline/L1/flash_attn_prefill.py:18-74.
+
+Same constructor ``(num_heads, num_kv_heads, head_dim)`` (with ``sm_scale``) and
+``forward(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, **kwargs)``.
+
+- With ``block_table`` (the paged path of Attention._forward_pure / _forward_mixed,
+  attention_impl.py:409-434, 682-707): ``k`` / ``v`` are the NHD caches
+  ``[num_blocks, block_size, Hk, D]`` and sequence b's keys are its first
+  ``cu_seqlens_k[b+1] - cu_seqlens_k[b]`` cached tokens (the reference's ``seqused_k``).
+- Without it: ``k`` / ``v`` are ``[total_k, Hk, D]`` and sequence b's keys are rows
+  ``cu_seqlens_k[b] .. cu_seqlens_k[b+1]``.
+
+Keyword arguments: ``softmax_scale`` (default ``head_dim ** -0.5``), ``causal``
+(default True; queries aligned to the end of the keys), ``out``, fp8 descales
+``k_descale`` / ``v_descale`` (or ``k_scale`` / ``v_scale``) for float8_e4m3fn
+caches.  ``window_size`` other than (-1, -1) and ``s_aux`` raise
+NotImplementedError.  ``max_seqlen_q`` must bound every query chunk (it sizes the
+launch); no host synchronisation happens.  Returns ``[total_q, num_heads, head_dim]``.
+"""
+from __future__ import annotations
+
+import sys
+from pathlib import Path
+
+import torch
+import torch.nn as nn
+
+try:
+    import fastkernels_amd  # noqa: F401
+except ImportError:  # loaded by file path from the reference harness
+    sys.path.insert(0, str(Path(__file__).resolve().parents[3]))
+from fastkernels_amd import ops
+
+
+class FlashAttnPrefill(nn.Module):
+    def __init__(self, num_heads: int, num_kv_heads: int, head_dim: int):
+        super().__init__()
+        self.num_heads = num_heads
+        self.num_kv_heads = num_kv_heads
+        self.head_dim = head_dim
+        self.sm_scale = head_dim ** -0.5
+
+    @staticmethod
+    def _scale_vec(s, hk: int, device) -> torch.Tensor | None:
+        if s is None:
+            return None
+        if not isinstance(s, torch.Tensor):
+            s = torch.tensor([float(s)], dtype=torch.float32)
+        s = s.to(device=device, dtype=torch.float32).reshape(-1)
+        if s.numel() == 1:
+            s = s.expand(hk)
+        if s.numel() != hk:
+            raise ValueError(f"FlashAttnPrefill: fp8 scale must have 1 or {hk} entries")
+        return s.contiguous()
+
+    def forward(self, q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
+                **kwargs):
+        block_table = kwargs.pop("block_table", None)
+        softmax_scale = kwargs.pop("softmax_scale", None)
+        causal = bool(kwargs.pop("causal", True))
+        out = kwargs.pop("out", None)
+        k_scale = kwargs.pop("k_scale", kwargs.pop("k_descale", None))
+        v_scale = kwargs.pop("v_scale", kwargs.pop("v_descale", None))
+        window = kwargs.pop("window_size", (-1, -1))
+        s_aux = kwargs.pop("s_aux", None)
+        for ignored in ("scheduler_metadata", "num_splits", "seqused_k", "fa_version"):
+            kwargs.pop(ignored, None)
+        if window is not None and tuple(window) != (-1, -1):
+            raise NotImplementedError("FlashAttnPrefill (gfx950): sliding window is not supported")
+        if s_aux is not None:
+            raise NotImplementedError("FlashAttnPrefill (gfx950): attention sinks are not supported")
+        if kwargs:
+            raise TypeError(f"FlashAttnPrefill: unexpected arguments {sorted(kwargs)}")
+        if softmax_scale is None:
+            softmax_scale = self.sm_scale
+        total = q.shape[0]
+        q3 = q.view(total, self.num_heads, self.head_dim)
+        if cu_seqlens_q.dtype != torch.int32:
+            cu_seqlens_q = cu_seqlens_q.to(torch.int32)
+        if cu_seqlens_k.dtype != torch.int32:
+            cu_seqlens_k = cu_seqlens_k.to(torch.int32)
+        if out is None:
+            out = torch.empty((total, self.num_heads, self.head_dim), dtype=q.dtype,
+                              device=q.device)
+        out3 = out.view(total, self.num_heads, self.head_dim)
+        compiling = torch.compiler.is_compiling()
+        if block_table is not None:
+            if block_table.dtype != torch.int32:
+                block_table = block_table.to(torch.int32)
+            hk = k.shape[2]
+            ks = self._scale_vec(k_scale, hk, q.device)
+            vs = self._scale_vec(v_scale, hk, q.device)
+            call = torch.ops.fastkernels_amd.paged_prefill if compiling else ops.paged_prefill
+            call(out3, q3, k, v, block_table, cu_seqlens_q, cu_seqlens_k, int(max_seqlen_q),
+                 float(softmax_scale), ks, vs, causal)
+        else:
+            hk = k.shape[-2] if k.dim() == 3 else k.shape[-1] // self.head_dim
+            k3 = k.view(k.shape[0], hk, self.head_dim)
+            v3 = v.view(v.shape[0], hk, self.head_dim)
+            call = torch.ops.fastkernels_amd.varlen_prefill if compiling else ops.varlen_prefill
+            call(out3, q3, k3, v3, cu_seqlens_q, cu_seqlens_k, int(max_seqlen_q),
+                 float(softmax_scale), causal)
+        return out

@@ -1,0 +1,164 @@
+// MFMA tile helpers shared by the paged attention kernels (decode and prefill).
+//
+// A wave processes 16 keys x 16 query columns at a time.  Let r = lane % 16,
+// g = lane / 16.
+//   S[t, j] = K[t, :] . Q[j, :]   4 x v_mfma_f32_16x16x32_bf16 over D = 128:
+//     A = K tile (row t = r, 8 dims per lane), B = Q^T (column j = r), both
+//     with the same dim permutation, so lane (r, g) receives S[4g + i, r].
+//   O[j, d] += P[j, t] V[t, d]    8 x v_mfma_f32_16x16x16bf16_1k (one per
+//     16-dim slice): A = P, whose layout (row j = r, tokens 4g..4g+3) is exactly
+//     the S layout above, so the probabilities never leave their lane; B = V
+//     (column = dim 8r + slice, tokens 4g..4g+3).  A lane loads 16 contiguous
+//     bytes (dims 8r..8r+7) of each of its 4 V rows and regroups the halves with
+//     byte permutes.
+// Lane (r, g) of the O accumulators holds O[column 4g + i][dims 8r .. 8r+7].
+#pragma once
+
+#include "fk_common.h"
+
+namespace fk {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef short short4_t __attribute__((ext_vector_type(4)));
+typedef float floatx4_t __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+constexpr int kHead = 128;
+constexpr int kTile = 16;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kNegInf = -__builtin_huge_valf();
+
+// Reductions over the four 16-lane rows of a wave (lanes r, r+16, r+32, r+48)
+// with the gfx950 row-swap permutes (VALU, no LDS traffic): each swap returns
+// a lane's own value and its partner row's value in some order, so combining
+// the two outputs symmetrically reduces each row pair.
+__device__ __forceinline__ float pair_max(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto c = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(c[0]), __uint_as_float(c[1]));
+}
+__device__ __forceinline__ float pair_sum(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto c = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(c[0]) + __uint_as_float(c[1]);
+}
+
+__device__ __forceinline__ uint32_t lo_pair(uint32_t a, uint32_t b) {
+  return (a & 0xffffu) | (b << 16);
+}
+__device__ __forceinline__ uint32_t hi_pair(uint32_t a, uint32_t b) {
+  return (a >> 16) | (b & 0xffff0000u);
+}
+__device__ __forceinline__ uint32_t word(const uint4& v, int i) {
+  return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+
+// 4 OCP e4m3fn bytes -> 4 bf16 (exact: every e4m3fn value is a bf16 value).
+__device__ __forceinline__ uint2 fp8x4_to_bf16x4(uint32_t w) {
+  const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8(w, false);
+  const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8(w, true);
+  return make_uint2(hi_pair(__float_as_uint(lo[0]), __float_as_uint(lo[1])),
+                    hi_pair(__float_as_uint(hi[0]), __float_as_uint(hi[1])));
+}
+
+// KV loads (plain cached loads: marking them non-temporal measured slower).
+__device__ __forceinline__ uint4 ld16(const uint8_t* p) { return *reinterpret_cast<const uint4*>(p); }
+__device__ __forceinline__ uint2 ld8(const uint8_t* p) { return *reinterpret_cast<const uint2*>(p); }
+
+// Raw registers one wave loads for one 16-token tile.  load_tile only issues
+// the loads; conversion and masking happen in the consumer, after the
+// prefetch of the following tile has been issued.
+template <bool kFp8>
+struct TileRegs;
+template <>
+struct TileRegs<false> {
+  uint4 k[4];  // dims 32c + 8g .. +8 of row r
+  uint4 v[4];  // rows 4g+i, dims 8r .. 8r+7
+};
+template <>
+struct TileRegs<true> {
+  uint4 k[2];  // 32 fp8 bytes of row r: dims 32g .. 32g+31
+  uint2 v[4];  // rows 4g+i, dims 8r .. 8r+7 (fp8 bytes)
+};
+
+// K operand chunks (bf16) of a loaded tile.
+__device__ __forceinline__ void k_chunks(const TileRegs<false>& t, uint4 (&k)[4]) {
+#pragma unroll
+  for (int c = 0; c < 4; ++c) k[c] = t.k[c];
+}
+__device__ __forceinline__ void k_chunks(const TileRegs<true>& t, uint4 (&k)[4]) {
+  // chunk c = dims 32g + 8c .. +8 = bytes 8c .. 8c+7 of the lane's 32.
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const uint4& src = t.k[c >> 1];
+    const uint32_t w0 = (c & 1) ? src.z : src.x;
+    const uint32_t w1 = (c & 1) ? src.w : src.y;
+    const uint2 lo = fp8x4_to_bf16x4(w0), hi = fp8x4_to_bf16x4(w1);
+    k[c] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+  }
+}
+// V rows (bf16, dims 8r .. 8r+7) of a loaded tile.
+__device__ __forceinline__ uint4 v_row(const TileRegs<false>& t, int i) { return t.v[i]; }
+__device__ __forceinline__ uint4 v_row(const TileRegs<true>& t, int i) {
+  const uint2 lo = fp8x4_to_bf16x4(t.v[i].x), hi = fp8x4_to_bf16x4(t.v[i].y);
+  return make_uint4(lo.x, lo.y, hi.x, hi.y);
+}
+
+// Value of `x` held by lane 4g + i (g = this lane's row group), for the O
+// row 4g + i this lane accumulates.  Rows >= kG are padding and get lane i's.
+template <int kG>
+__device__ __forceinline__ float row_value(float x, int g, int i) {
+  float a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__float_as_int(x), i));
+  if constexpr (kG > 4) {
+    const float a1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__float_as_int(x), 4 + i));
+    if constexpr (kG > 8) {
+      const float a2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__float_as_int(x), 8 + i));
+      const float a3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__float_as_int(x), 12 + i));
+      a = g == 0 ? a : g == 1 ? a1 : g == 2 ? a2 : a3;
+    } else {
+      a = g == 1 ? a1 : a;
+    }
+  }
+  return a;
+}
+
+// S tile of 16 keys x 16 query columns: acc[i] = S[key 4g + i, column r].
+__device__ __forceinline__ floatx4_t qk_scores(const uint4 (&kc)[4], const bf16x8_t (&qb)[4]) {
+  floatx4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kc[c]), qb[c],
+                                                 acc, 0, 0, 0);
+  return acc;
+}
+
+// P as the A operand: row r (query column), k = keys 4g..4g+3 (RNE bf16 pack).
+__device__ __forceinline__ short4_t p_operand(const float (&pr)[4]) {
+  const bf16x2_t p01 = {static_cast<__bf16>(pr[0]), static_cast<__bf16>(pr[1])};
+  const bf16x2_t p23 = {static_cast<__bf16>(pr[2]), static_cast<__bf16>(pr[3])};
+  return __builtin_bit_cast(
+      short4_t, make_uint2(__builtin_bit_cast(uint32_t, p01), __builtin_bit_cast(uint32_t, p23)));
+}
+
+// o[d] += P . V for the 8 16-dim slices; vr[i] = V row 4g + i, dims 8r .. 8r+7.
+__device__ __forceinline__ void pv_accumulate(floatx4_t (&o)[8], short4_t pa,
+                                              const uint4 (&vr)[4]) {
+#pragma unroll
+  for (int d = 0; d < 8; ++d) {
+    const int wi = d >> 1;
+    uint32_t b01, b23;
+    if (d & 1) {
+      b01 = hi_pair(word(vr[0], wi), word(vr[1], wi));
+      b23 = hi_pair(word(vr[2], wi), word(vr[3], wi));
+    } else {
+      b01 = lo_pair(word(vr[0], wi), word(vr[1], wi));
+      b23 = lo_pair(word(vr[2], wi), word(vr[3], wi));
+    }
+    const short4_t vb = __builtin_bit_cast(short4_t, make_uint2(b01, b23));
+    o[d] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, vb, o[d], 0, 0, 0);
+  }
+}
+
+}  // namespace fk

@@ -363,6 +363,78 @@ def store_paged_decode(out: torch.Tensor, q: torch.Tensor, key: torch.Tensor, va
                  max_parts, _ptr(workspace), ws_bytes, _stream(q))
 
 
+def _check_prefill(out, q, cu_seqlens_q, cu_seqlens_k):
+    if q.dim() != 3 or q.dtype != torch.bfloat16 or q.stride(2) != 1 or q.stride(1) != q.shape[2]:
+        raise ValueError("prefill: q must be bf16 [tokens, Hq, D] with contiguous heads")
+    if out.shape != q.shape or out.dtype != q.dtype or out.stride(2) != 1 or \
+            out.stride(1) != q.shape[2]:
+        raise ValueError("prefill: out must be bf16 [tokens, Hq, D] with contiguous heads")
+    for t, nm in ((cu_seqlens_q, "cu_seqlens_q"), (cu_seqlens_k, "cu_seqlens_k")):
+        if t.dtype != torch.int32 or t.dim() != 1 or not t.is_contiguous():
+            raise TypeError(f"prefill: {nm} must be contiguous int32 [batch + 1]")
+    if cu_seqlens_k.numel() < cu_seqlens_q.numel():
+        raise ValueError("prefill: cu_seqlens_k shorter than cu_seqlens_q")
+
+
+def paged_prefill(out: torch.Tensor, q: torch.Tensor, k_cache: torch.Tensor,
+                  v_cache: torch.Tensor, block_table: torch.Tensor, cu_seqlens_q: torch.Tensor,
+                  cu_seqlens_k: torch.Tensor, max_seqlen_q: int, softmax_scale: float,
+                  k_scale: torch.Tensor | None = None, v_scale: torch.Tensor | None = None,
+                  causal: bool = True) -> None:
+    """Causal prefill over paged K/V into ``out`` ([tokens, Hq, D] bf16): sequence b's
+    queries q[cu_q[b]:cu_q[b+1]] attend to its first cu_k[b+1]-cu_k[b] cached tokens,
+    aligned to their end (flash_attn_varlen_func with block_table, seqused_k)."""
+    _check_prefill(out, q, cu_seqlens_q, cu_seqlens_k)
+    if k_cache.dim() != 4 or v_cache.shape != k_cache.shape or k_cache.shape[3] != q.shape[2]:
+        raise ValueError("paged_prefill: caches must be [num_blocks, block_size, Hk, D]")
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("paged_prefill: caches must be contiguous")
+    if k_cache.dtype != v_cache.dtype or k_cache.dtype not in (torch.bfloat16, _FP8):
+        raise TypeError("paged_prefill: caches must both be bf16 or float8_e4m3fn")
+    batch = cu_seqlens_q.numel() - 1
+    if block_table.dtype != torch.int32 or block_table.dim() != 2 or block_table.stride(1) != 1 \
+            or block_table.shape[0] < batch:
+        raise TypeError("paged_prefill: block_table must be int32 [batch, max_blocks], rows "
+                        "contiguous")
+    hk = k_cache.shape[2]
+    for sc, nm in ((k_scale, "k_scale"), (v_scale, "v_scale")):
+        if sc is not None and (sc.dtype != torch.float32 or sc.numel() != hk or
+                               not sc.is_contiguous()):
+            raise ValueError(f"paged_prefill: {nm} must be float32 [num_kv_heads]")
+    _same_device(out, q, k_cache, v_cache, block_table, cu_seqlens_q, cu_seqlens_k)
+    if batch <= 0 or q.shape[0] == 0:
+        return
+    nb, bs = k_cache.shape[:2]
+    _native.call("fk_paged_prefill", _ptr(out), out.stride(0), _ptr(q), q.stride(0),
+                 _ptr(k_cache), _ptr(v_cache),
+                 _native.FK_DTYPE_FP8_E4M3FN if k_cache.dtype == _FP8 else _native.FK_DTYPE_BF16,
+                 _ptr(k_scale), _ptr(v_scale), _ptr(block_table), block_table.stride(0),
+                 _ptr(cu_seqlens_q), _ptr(cu_seqlens_k), batch, int(max_seqlen_q), q.shape[1],
+                 hk, q.shape[2], bs, nb, float(softmax_scale), int(bool(causal)), _stream(q))
+
+
+def varlen_prefill(out: torch.Tensor, q: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                   cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor, max_seqlen_q: int,
+                   softmax_scale: float, causal: bool = True) -> None:
+    """Causal prefill over dense keys: key/value [total_k, Hk, D] bf16 (rows may be strided
+    views), sequence b's keys being rows cu_k[b]..cu_k[b+1]."""
+    _check_prefill(out, q, cu_seqlens_q, cu_seqlens_k)
+    if key.dim() != 3 or value.shape != key.shape or key.shape[2] != q.shape[2]:
+        raise ValueError("varlen_prefill: key/value must be [total_k, Hk, D]")
+    for t, nm in ((key, "key"), (value, "value")):
+        if t.dtype != torch.bfloat16 or t.stride(2) != 1 or (t.shape[1] > 1 and
+                                                             t.stride(1) != t.shape[2]):
+            raise ValueError(f"varlen_prefill: {nm} must be bf16 with [Hk, D] contiguous rows")
+    _same_device(out, q, key, value, cu_seqlens_q, cu_seqlens_k)
+    batch = cu_seqlens_q.numel() - 1
+    if batch <= 0 or q.shape[0] == 0:
+        return
+    _native.call("fk_varlen_prefill", _ptr(out), out.stride(0), _ptr(q), q.stride(0), _ptr(key),
+                 key.stride(0), _ptr(value), value.stride(0), _ptr(cu_seqlens_q),
+                 _ptr(cu_seqlens_k), batch, int(max_seqlen_q), q.shape[1], key.shape[1],
+                 q.shape[2], float(softmax_scale), int(bool(causal)), _stream(q))
+
+
 def paged_decode_phases(out, q, k_cache, v_cache, block_table, cache_seqlens, softmax_scale,
                         part_tokens, max_parts, workspace, k_scale=None, v_scale=None):
     """The two launches of :func:`paged_decode` as separate callables (for timing)."""
@@ -464,6 +536,12 @@ _LIB.define("qk_norm_rope_store(Tensor positions, Tensor(a!) query, Tensor(b!) k
             "Tensor value, Tensor(c!) k_cache, Tensor(d!) v_cache, Tensor slot_mapping, "
             "int head_size, Tensor cos_sin_cache, bool is_neox, Tensor? q_weight=None, "
             "Tensor? k_weight=None, float eps=1e-6) -> ()")
+_LIB.define("paged_prefill(Tensor(a!) out, Tensor q, Tensor k_cache, Tensor v_cache, "
+            "Tensor block_table, Tensor cu_seqlens_q, Tensor cu_seqlens_k, int max_seqlen_q, "
+            "float softmax_scale, Tensor? k_scale=None, Tensor? v_scale=None, bool causal=True) -> ()")
+_LIB.define("varlen_prefill(Tensor(a!) out, Tensor q, Tensor key, Tensor value, "
+            "Tensor cu_seqlens_q, Tensor cu_seqlens_k, int max_seqlen_q, float softmax_scale, "
+            "bool causal=True) -> ()")
 _LIB.define("silu_and_mul(Tensor! result, Tensor input) -> ()")
 _LIB.define("merge_attn_states(Tensor(a!) output, Tensor prefix_output, Tensor prefix_lse, "
             "Tensor suffix_output, Tensor suffix_lse, Tensor(b!)? output_lse) -> ()")
@@ -478,6 +556,8 @@ _IMPLS = {
     "merge_attn_states": merge_attn_states,
     "store_paged_decode": store_paged_decode,
     "qk_norm_rope_store": qk_norm_rope_store,
+    "paged_prefill": paged_prefill,
+    "varlen_prefill": varlen_prefill,
 }
 for _name, _fn in _IMPLS.items():
     _LIB.impl(_name, _fn, "CUDA")

@@ -39,6 +39,9 @@
  *   fk_store_paged_decode
  *       fastkernels/tasks/baseline/L2/attention_impl.py:313-363 (forward_impl: store,
  *       then the decode branch of _forward_pure :436-450).
+ *   fk_paged_prefill, fk_varlen_prefill
+ *       fastkernels/tasks/baseline/L1/flash_attn_prefill.py:18-74 (FlashAttnPrefill.forward,
+ *       with and without block_table).
  *   fk_qk_norm_rope_store
  *       fastkernels/tasks/baseline/L2/attention.py:120-140 (q_norm/k_norm, rotary_emb)
  *       followed by attention_impl.py:323-325 (store_kvcache).
@@ -180,6 +183,37 @@ int fk_paged_decode_reduce(void* out, int64_t out_row_stride, const void* q,
                            int num_kv_heads, int head_size, int block_size, int64_t num_blocks,
                            float scale, int64_t part_tokens, int64_t max_parts, void* workspace,
                            int64_t workspace_bytes, void* stream);
+
+/* Paged prefill attention: FlashAttnPrefill.forward with a block table
+ * (fastkernels/tasks/baseline/L1/flash_attn_prefill.py:28-74), the prefill half of
+ * Attention._forward_mixed (attention_impl.py:682-731).
+ * Sequence b owns query rows [cu_seqlens_q[b], cu_seqlens_q[b+1]) of q / out
+ * ([rows, Hq*128] bf16, row strides in elements) and the first
+ * k_len = cu_seqlens_k[b+1] - cu_seqlens_k[b] tokens of its paged cache (block_tables
+ * row b, layout as fk_paged_decode).  Query j of a chunk of q_len sees keys
+ * [0, k_len - q_len + j] (causal, aligned to the end); a query with no visible key gets
+ * zeros.  causal = 0 lets every query see all k_len keys (flash_attn causal=False).
+ * max_seqlen_q bounds every chunk (it sizes the grid).  head_size 128; GQA
+ * groups up to 16; kv dtype bf16 or fp8 e4m3fn (with k_scale / v_scale as in
+ * fk_paged_decode).  No workspace; nothing is allocated. */
+int fk_paged_prefill(void* out, int64_t out_row_stride, const void* q, int64_t q_row_stride,
+                     const void* k_cache, const void* v_cache, int kv_dtype, const float* k_scale,
+                     const float* v_scale, const int32_t* block_tables, int64_t bt_row_stride,
+                     const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int64_t batch,
+                     int64_t max_seqlen_q, int num_heads, int num_kv_heads, int head_size,
+                     int block_size, int64_t num_blocks, float scale, int causal, void* stream);
+
+/* The same attention over dense keys: FlashAttnPrefill.forward without a block table
+ * (flash_attn_prefill.py:65-74; Attention._prefill_torch_from_tensors,
+ * attention_impl.py:624-638).  key / value: [total_k, Hk*128] bf16 rows (strides in
+ * elements; views of the qkv buffer allowed); sequence b's keys are rows
+ * [cu_seqlens_k[b], cu_seqlens_k[b+1]). */
+int fk_varlen_prefill(void* out, int64_t out_row_stride, const void* q, int64_t q_row_stride,
+                      const void* key, int64_t key_row_stride, const void* value,
+                      int64_t value_row_stride, const int32_t* cu_seqlens_q,
+                      const int32_t* cu_seqlens_k, int64_t batch, int64_t max_seqlen_q,
+                      int num_heads, int num_kv_heads, int head_size, float scale, int causal,
+                      void* stream);
 
 /* Per-head q/k RMSNorm (optional) + rotary embedding + store_kvcache in one launch:
  * the attention block between the qkv projection and the decode

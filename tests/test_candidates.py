@@ -38,6 +38,9 @@ CONTRACT = {
     "flash_attn_decode": ("FlashAttnDecode", ["num_heads", "num_kv_heads", "head_dim", "page_size"],
                           ["q", "k_cache", "v_cache", "cache_seqlens", "kwargs"]),
     "silu_and_mul": ("SiluAndMul", [], ["x"]),
+    "flash_attn_prefill": ("FlashAttnPrefill", ["num_heads", "num_kv_heads", "head_dim"],
+                           ["q", "k", "v", "cu_seqlens_q", "cu_seqlens_k", "max_seqlen_q",
+                            "max_seqlen_k", "kwargs"]),
     "merge_attn_states": ("MergeAttnStates", None,
                           ["output", "prefix_output", "prefix_lse", "suffix_output", "suffix_lse",
                            "output_lse"]),

@@ -1,0 +1,175 @@
+"""GPU parity of paged / dense prefill attention (fk_paged_prefill, fk_varlen_prefill)
+against the oracle (FlashAttnPrefill semantics, flash_attn_prefill.py:28-74, restated
+from the reference's torch fallback attention_impl.py:606-652).  bf16 bar: every
+element within atol = rtol = 1e-2; fp8 KV: 3e-2."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from fastkernels_amd import ops, workloads
+
+pytestmark = pytest.mark.gpu
+
+
+def _flush(msg):
+    print(msg, flush=True)
+
+
+def _case(cuda, q_lens, k_lens, hq=32, hk=8, bs=16, seed=70, fp8=False, extra_pages=3):
+    g = torch.Generator().manual_seed(seed)
+    pages = [(k + bs - 1) // bs for k in k_lens]
+    nb = sum(pages) + extra_pages
+    perm = torch.randperm(nb, generator=g)
+    bt = torch.full((len(k_lens), max(max(pages), 1)), -1, dtype=torch.int32)
+    off = 0
+    for i, p in enumerate(pages):
+        bt[i, :p] = perm[off:off + p].to(torch.int32)
+        off += p
+    cu_q = torch.tensor([0] + list(np.cumsum(q_lens)), dtype=torch.int32)
+    cu_k = torch.tensor([0] + list(np.cumsum(k_lens)), dtype=torch.int32)
+    q = torch.randn(int(cu_q[-1]), hq, 128, generator=g).to(torch.bfloat16)
+    kc = torch.randn(nb, bs, hk, 128, generator=g)
+    vc = torch.randn(nb, bs, hk, 128, generator=g)
+    ks = vs = None
+    if fp8:
+        ks = (0.01 + 0.09 * torch.rand(hk, generator=g)).float()
+        vs = (0.01 + 0.09 * torch.rand(hk, generator=g)).float()
+        kc = workloads.quantize_fp8(kc, ks)
+        vc = workloads.quantize_fp8(vc, vs)
+    else:
+        kc, vc = kc.to(torch.bfloat16), vc.to(torch.bfloat16)
+    t = lambda x: None if x is None else x.to(cuda)  # noqa: E731
+    return dict(q=q.to(cuda), kc=kc.to(cuda), vc=vc.to(cuda), bt=bt.to(cuda), cu_q=cu_q.to(cuda),
+                cu_k=cu_k.to(cuda), max_q=max(q_lens) if q_lens else 0, ks=t(ks), vs=t(vs))
+
+
+def _run(c, causal=True):
+    out = torch.full_like(c["q"], float("nan"))
+    ops.paged_prefill(out, c["q"], c["kc"], c["vc"], c["bt"], c["cu_q"], c["cu_k"], c["max_q"],
+                      128 ** -0.5, c["ks"], c["vs"], causal)
+    torch.cuda.synchronize()
+    return out
+
+
+def _oracle(c, causal=True):
+    fp8 = c["kc"].dtype == torch.float8_e4m3fn
+    kc = c["kc"].view(torch.uint8).cpu().numpy() if fp8 else c["kc"].float().cpu().numpy()
+    vc = c["vc"].view(torch.uint8).cpu().numpy() if fp8 else c["vc"].float().cpu().numpy()
+    return oracle.paged_prefill(c["q"].float().cpu().numpy(), kc, vc, c["bt"].cpu().numpy(),
+                                c["cu_q"].cpu().numpy(), c["cu_k"].cpu().numpy(), 128 ** -0.5,
+                                None if c["ks"] is None else c["ks"].cpu().numpy(),
+                                None if c["vs"] is None else c["vs"].cpu().numpy(),
+                                causal=causal)
+
+
+def _close(got, ref, tol, what):
+    g = got.float().cpu().numpy()
+    assert np.isfinite(g).all(), f"{what}: non-finite output"
+    err = np.abs(g - ref)
+    bad = err > tol + tol * np.abs(ref)
+    assert not bad.any(), f"{what}: {int(bad.sum())} elements off, max err {err.max():.3g}"
+
+
+@pytest.mark.parametrize("bs", [16, 64, 256])
+def test_paged_prefill_mixed_chunks(cuda, bs):
+    """Whole prompts, chunked prefill over a longer context, single-token chunks and a
+    chunk of 33 (a partial query block), Qwen3-8B heads (GQA 4)."""
+    q_lens = [1, 5, 17, 33, 100, 64, 32]
+    k_lens = [1, 5, 40, 33, 300, 1000, 47]
+    _flush(f"paged prefill bs={bs}")
+    c = _case(cuda, q_lens, k_lens, bs=bs, seed=71 + bs)
+    _close(_run(c), _oracle(c), 1e-2, f"paged prefill bs={bs}")
+
+
+@pytest.mark.parametrize("hq,hk", [(8, 8), (16, 2), (64, 8), (16, 1)])
+def test_paged_prefill_gqa(cuda, hq, hk):
+    _flush(f"paged prefill hq={hq} hk={hk}")
+    c = _case(cuda, [20, 50], [60, 50], hq=hq, hk=hk, seed=72)
+    _close(_run(c), _oracle(c), 1e-2, f"gqa {hq}/{hk}")
+
+
+def test_paged_prefill_noncausal_and_empty_rows(cuda):
+    """causal=False (every query sees all keys), a chunk longer than its context
+    (leading rows see no key: zeros), and an empty chunk."""
+    _flush("paged prefill non-causal / empty rows")
+    c = _case(cuda, [10, 0, 7], [25, 9, 4], seed=73)
+    _close(_run(c, causal=False), _oracle(c, causal=False), 1e-2, "non-causal")
+    got = _run(c)
+    _close(got, _oracle(c), 1e-2, "q_len > k_len")
+    assert torch.equal(got[10:13].float(), torch.zeros_like(got[10:13].float()))
+
+
+def test_paged_prefill_fp8(cuda):
+    _flush("paged prefill fp8")
+    c = _case(cuda, [16, 40, 1], [100, 40, 257], bs=64, seed=74, fp8=True)
+    _close(_run(c), _oracle(c), 3e-2, "fp8")
+
+
+def test_paged_prefill_single_token_equals_decode(cuda):
+    """q_len = 1 per sequence is a decode step: same result as fk_paged_decode."""
+    _flush("paged prefill == decode for one-token chunks")
+    k_lens = [1, 17, 300, 1000, 4097]
+    c = _case(cuda, [1] * 5, k_lens, bs=256, seed=75)
+    got = _run(c)
+    out = torch.empty_like(c["q"])
+    part, nparts, wsb = ops.paged_decode_plan(5, 32, 8, 128, max(k_lens), 0)
+    ws = torch.zeros(max(1, wsb), dtype=torch.uint8, device=cuda)
+    ctx = (c["cu_k"][1:] - c["cu_k"][:-1]).to(torch.int32).contiguous()
+    ops.paged_decode(out, c["q"], c["kc"], c["vc"], c["bt"], ctx, 128 ** -0.5, part, nparts, ws)
+    torch.cuda.synchronize()
+    _close(got, out.float().cpu().numpy(), 1e-2, "prefill vs decode")
+
+
+def test_varlen_prefill_dense_strided(cuda):
+    """Dense keys as strided views of a packed qkv buffer (the no-block-table path)."""
+    _flush("varlen prefill dense")
+    g = torch.Generator().manual_seed(76)
+    q_lens, k_lens = [7, 64, 33], [7, 64, 33]
+    tot = sum(q_lens)
+    hq, hk = 32, 8
+    qkv = torch.randn(tot, (hq + 2 * hk) * 128, generator=g).to(torch.bfloat16).to(cuda)
+    q = qkv[:, :hq * 128].view(tot, hq, 128)
+    k = qkv[:, hq * 128:(hq + hk) * 128].view(tot, hk, 128)
+    v = qkv[:, (hq + hk) * 128:].view(tot, hk, 128)
+    cu = torch.tensor([0] + list(np.cumsum(q_lens)), dtype=torch.int32, device=cuda)
+    out = torch.empty(tot, hq, 128, dtype=torch.bfloat16, device=cuda)
+    ops.varlen_prefill(out, q.contiguous(), k, v, cu, cu, max(q_lens), 128 ** -0.5)
+    torch.cuda.synchronize()
+    ref = oracle.varlen_prefill(q.float().cpu().numpy(), k.float().cpu().numpy(),
+                                v.float().cpu().numpy(), cu.cpu().numpy(), cu.cpu().numpy(),
+                                128 ** -0.5)
+    _close(out, ref, 1e-2, "dense varlen")
+
+
+def test_paged_prefill_qwen3_prompt_2048(cuda):
+    """One 2048-token prompt at Qwen3-8B heads: against torch fp32 causal attention on
+    the device (the oracle would take minutes at this size)."""
+    _flush("paged prefill 2048-token prompt vs torch fp32")
+    c = _case(cuda, [2048], [2048], bs=256, seed=77)
+    got = _run(c)
+    k = c["kc"][c["bt"][0, :8].long()].reshape(2048, 8, 128).float()
+    v = c["vc"][c["bt"][0, :8].long()].reshape(2048, 8, 128).float()
+    qf = c["q"].float().transpose(0, 1)                                   # [32, 2048, 128]
+    kf = k.repeat_interleave(4, dim=1).transpose(0, 1).contiguous()
+    vf = v.repeat_interleave(4, dim=1).transpose(0, 1).contiguous()
+    ref = torch.nn.functional.scaled_dot_product_attention(qf, kf, vf, is_causal=True,
+                                                           scale=128 ** -0.5)
+    _close(got, ref.transpose(0, 1).cpu().numpy(), 1e-2, "2048 prompt")
+
+
+def test_flash_attn_prefill_candidate(cuda):
+    from fastkernels_amd.candidate.L1.flash_attn_prefill import FlashAttnPrefill
+    _flush("FlashAttnPrefill candidate (paged)")
+    c = _case(cuda, [12, 40], [50, 40], bs=16, seed=78)
+    m = FlashAttnPrefill(32, 8, 128)
+    out = m(c["q"], c["kc"], c["vc"], cu_seqlens_q=c["cu_q"], cu_seqlens_k=c["cu_k"],
+            max_seqlen_q=40, max_seqlen_k=50, softmax_scale=128 ** -0.5, causal=True,
+            block_table=c["bt"])
+    torch.cuda.synchronize()
+    _close(out, _oracle(c), 1e-2, "candidate")
+    with pytest.raises(NotImplementedError):
+        m(c["q"], c["kc"], c["vc"], c["cu_q"], c["cu_k"], 40, 50, block_table=c["bt"],
+          window_size=(128, 0))

@@ -17,6 +17,10 @@ its own formula:
                    invariance, split-context merge == unsplit;
   silu_and_mul     torch.nn.functional.silu (library) with the reference's
                    rounding points;
+  paged_prefill    torch SDPA (float64) with is_causal when the chunk is the whole
+                   context and with an explicit bottom-right mask otherwise;
+                   q_len = 1 equals paged_decode; a query's output does not depend
+                   on keys after its position; a planted top-left mask is caught;
   merge_attn_states  attention over a key set split in two and merged equals
                    torch SDPA over the whole set, and out_lse equals
                    torch.logsumexp of all scores (library); the special cases
@@ -320,6 +324,78 @@ def test_fp8_dequant_matches_torch():
     ours = oracle.dequant_kv(codes, scale, "bf16")
     t = torch.from_numpy(codes).view(torch.float8_e4m3fn).float() * torch.from_numpy(scale).view(1, 1, 2, 1)
     assert np.array_equal(ours, t.bfloat16().float().numpy())
+
+
+# ---------------------------------------------------------------------------
+# paged prefill
+# ---------------------------------------------------------------------------
+def _prefill_case(seed=21, q_lens=(5, 1, 9), k_lens=(5, 17, 30), hq=4, hk=2, d=16, bs=8):
+    rng = np.random.default_rng(seed)
+    pages = [(k + bs - 1) // bs for k in k_lens]
+    nb = sum(pages) + 2
+    perm = rng.permutation(nb)
+    bt = np.full((len(k_lens), max(pages)), -1, np.int32)
+    off = 0
+    for i, p in enumerate(pages):
+        bt[i, :p] = perm[off:off + p]
+        off += p
+    kc = rng.standard_normal((nb, bs, hk, d)).astype(np.float32)
+    vc = rng.standard_normal((nb, bs, hk, d)).astype(np.float32)
+    cu_q = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
+    cu_k = np.concatenate([[0], np.cumsum(k_lens)]).astype(np.int32)
+    q = rng.standard_normal((int(cu_q[-1]), hq, d)).astype(np.float32)
+    return q, kc, vc, bt, cu_q, cu_k
+
+
+def test_paged_prefill_vs_torch_sdpa():
+    q, kc, vc, bt, cu_q, cu_k = _prefill_case()
+    scale = 0.3
+    ours = oracle.paged_prefill(q, kc, vc, bt, cu_q, cu_k, scale)
+    hq, hk = q.shape[1], kc.shape[2]
+    for i in range(len(cu_q) - 1):
+        qs, qe = int(cu_q[i]), int(cu_q[i + 1])
+        kl = int(cu_k[i + 1] - cu_k[i])
+        ql = qe - qs
+        k = torch.from_numpy(oracle.gather_seq(kc, bt[i], kl)).double()
+        v = torch.from_numpy(oracle.gather_seq(vc, bt[i], kl)).double()
+        k = k.repeat_interleave(hq // hk, dim=1).transpose(0, 1)   # [hq, kl, d]
+        v = v.repeat_interleave(hq // hk, dim=1).transpose(0, 1)
+        qq = torch.from_numpy(q[qs:qe]).double().transpose(0, 1)   # [hq, ql, d]
+        if ql == kl:
+            ref = F.scaled_dot_product_attention(qq, k, v, is_causal=True, scale=scale)
+        else:
+            mask = torch.arange(kl)[None, :] <= (kl - ql + torch.arange(ql))[:, None]
+            ref = F.scaled_dot_product_attention(qq, k, v, attn_mask=mask, scale=scale)
+        np.testing.assert_allclose(ours[qs:qe], ref.transpose(0, 1).numpy(), rtol=1e-10,
+                                   atol=1e-12)
+        if ql > 1 and kl > ql:  # planted mistake: a top-left aligned mask differs
+            wrong_mask = torch.arange(kl)[None, :] <= torch.arange(ql)[:, None]
+            wrong = F.scaled_dot_product_attention(qq, k, v, attn_mask=wrong_mask, scale=scale)
+            assert not np.allclose(ours[qs:qe], wrong.transpose(0, 1).numpy(), atol=1e-3)
+
+
+def test_paged_prefill_decode_case_and_causality():
+    q, kc, vc, bt, cu_q, cu_k = _prefill_case(seed=22, q_lens=(1, 1), k_lens=(13, 24))
+    lens = np.diff(cu_k)
+    pre = oracle.paged_prefill(q, kc, vc, bt, cu_q, cu_k, 0.25)
+    dec = oracle.paged_decode(q, kc, vc, bt, lens, 0.25)
+    np.testing.assert_allclose(pre, dec, rtol=1e-12, atol=1e-13)
+    # causality: changing the keys after query 2's position leaves queries 0..2 unchanged
+    q, kc, vc, bt, cu_q, cu_k = _prefill_case(seed=23, q_lens=(6,), k_lens=(10,))
+    base = oracle.paged_prefill(q, kc, vc, bt, cu_q, cu_k, 0.25)
+    kc2, vc2 = kc.copy(), vc.copy()
+    bs = kc.shape[1]
+    for t in range(10 - 6 + 3, 10):  # positions after query 2 (at position 6)
+        page, slot = bt[0, t // bs], t % bs
+        kc2[page, slot] += 5.0
+        vc2[page, slot] -= 3.0
+    moved = oracle.paged_prefill(q, kc2, vc2, bt, cu_q, cu_k, 0.25)
+    np.testing.assert_allclose(moved[:3], base[:3], rtol=1e-12, atol=1e-13)
+    assert not np.allclose(moved[3:], base[3:])
+    # a query with no visible key (q_len > k_len) gives zeros
+    q, kc, vc, bt, cu_q, cu_k = _prefill_case(seed=24, q_lens=(5,), k_lens=(3,))
+    z = oracle.paged_prefill(q, kc, vc, bt, cu_q, cu_k, 0.25)
+    assert np.array_equal(z[:2], np.zeros_like(z[:2])) and np.abs(z[2:]).sum() > 0
 
 
 # ---------------------------------------------------------------------------
