@@ -449,6 +449,60 @@ def bench_table(args):
                                      case.ctx_lens, case.scale, part, nparts, ws, case.k_scale,
                                      case.v_scale), case.algorithmic_bytes(),
             decode_cpu(case, nseq) if nseq else None, iters=30)
+    # Prefill (FlashAttnPrefill with a block table) at Qwen3-8B heads, with torch's
+    # own SDPA (flash backend, dense contiguous K/V) on the same GPU beside it.
+    def prefill_case(q_lens, k_lens, seed):
+        g = torch.Generator().manual_seed(seed)
+        bs = 256
+        pages = [(k + bs - 1) // bs for k in k_lens]
+        nb = sum(pages)
+        perm = torch.randperm(nb, generator=g).to(torch.int32)
+        bt = torch.full((len(k_lens), max(pages)), -1, dtype=torch.int32)
+        off = 0
+        for i, p in enumerate(pages):
+            bt[i, :p] = perm[off:off + p]
+            off += p
+        cu_q = torch.tensor([0] + list(np.cumsum(q_lens)), dtype=torch.int32, device=dev)
+        cu_k = torch.tensor([0] + list(np.cumsum(k_lens)), dtype=torch.int32, device=dev)
+        q = torch.randn(sum(q_lens), 32, 128, generator=g).to(torch.bfloat16).to(dev)
+        kc = torch.randn(nb, bs, 8, 128, generator=g).to(torch.bfloat16).to(dev)
+        vc = torch.randn(nb, bs, 8, 128, generator=g).to(torch.bfloat16).to(dev)
+        visible = sum(sum(max(0, min(kl, kl - ql + j + 1)) for j in range(ql))
+                      for ql, kl in zip(q_lens, k_lens))
+        return q, kc, vc, bt.to(dev), cu_q, cu_k, max(q_lens), visible * 32 * 4 * 128
+
+    for label, ql, kl in (("1x2048 prompt", [2048], [2048]),
+                          ("4x512 chunks over 4096", [512] * 4, [4096] * 4),
+                          ("16x512 prompts", [512] * 16, [512] * 16)):
+        q, kc, vc, bt, cu_q, cu_k, mq, flop = prefill_case(ql, kl, workloads.SEED + 11)
+        pout = torch.empty_like(q)
+        med, _ = time_call(lambda: ops.paged_prefill(pout, q, kc, vc, bt, cu_q, cu_k, mq,
+                                                     128 ** -0.5), iters=20, warmup=3,
+                           flush=flush)
+        row = {"config": "prefill", "op": f"paged_prefill bf16 Hq=32 Hk=8 {label}",
+               "us_median": round(med * 1e3, 2), "flop": flop,
+               "TFLOPs": round(flop / (med * 1e-3) / 1e12, 1),
+               "frac_of_2.5PFLOPs": round(flop / (med * 1e-3) / 2.5e15, 4)}
+        rows.append(row)
+        print(json.dumps(row), file=sys.stderr, flush=True)
+    try:  # torch's flash SDPA on dense [1, 32, 2048, 128] bf16 (MHA-expanded K/V)
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+        g = torch.Generator().manual_seed(workloads.SEED + 12)
+        tq, tk, tv = (torch.randn(1, 32, 2048, 128, generator=g).to(torch.bfloat16).to(dev)
+                      for _ in range(3))
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION]):
+            med, _ = time_call(lambda: torch.nn.functional.scaled_dot_product_attention(
+                tq, tk, tv, is_causal=True), iters=20, warmup=3, flush=flush)
+        flop = 2048 * 2049 // 2 * 32 * 4 * 128
+        row = {"config": "prefill", "op": "torch SDPA flash backend, dense 1x2048 causal (comparison)",
+               "us_median": round(med * 1e3, 2), "flop": flop,
+               "TFLOPs": round(flop / (med * 1e-3) / 1e12, 1),
+               "frac_of_2.5PFLOPs": round(flop / (med * 1e-3) / 2.5e15, 4)}
+        rows.append(row)
+        print(json.dumps(row), file=sys.stderr, flush=True)
+    except Exception as e:  # noqa: BLE001 - the comparison row is optional
+        print(f"torch SDPA flash comparison skipped: {e!r}", file=sys.stderr, flush=True)
+
     # Decode step of Attention.forward_impl at C3: store + decode as two calls, and fused.
     rows3 = workloads.decode_step_rows(c3)
     b3, hq3, d3 = c3.q.shape

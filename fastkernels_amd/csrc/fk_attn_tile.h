@@ -142,9 +142,9 @@ __device__ __forceinline__ short4_t p_operand(const float (&pr)[4]) {
       short4_t, make_uint2(__builtin_bit_cast(uint32_t, p01), __builtin_bit_cast(uint32_t, p23)));
 }
 
-// o[d] += P . V for the 8 16-dim slices; vr[i] = V row 4g + i, dims 8r .. 8r+7.
-__device__ __forceinline__ void pv_accumulate(floatx4_t (&o)[8], short4_t pa,
-                                              const uint4 (&vr)[4]) {
+// B operands of P.V for the 8 16-dim slices: vr[i] = V row 4g + i, dims
+// 8r .. 8r+7, regrouped so that slice d holds dim 8r + d of rows 4g .. 4g+3.
+__device__ __forceinline__ void v_operands(const uint4 (&vr)[4], short4_t (&vb)[8]) {
 #pragma unroll
   for (int d = 0; d < 8; ++d) {
     const int wi = d >> 1;
@@ -156,9 +156,23 @@ __device__ __forceinline__ void pv_accumulate(floatx4_t (&o)[8], short4_t pa,
       b01 = lo_pair(word(vr[0], wi), word(vr[1], wi));
       b23 = lo_pair(word(vr[2], wi), word(vr[3], wi));
     }
-    const short4_t vb = __builtin_bit_cast(short4_t, make_uint2(b01, b23));
-    o[d] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, vb, o[d], 0, 0, 0);
+    vb[d] = __builtin_bit_cast(short4_t, make_uint2(b01, b23));
   }
+}
+
+// o[d] += P . V for the 8 16-dim slices, with the V operands from v_operands.
+__device__ __forceinline__ void pv_accumulate(floatx4_t (&o)[8], short4_t pa,
+                                              const short4_t (&vb)[8]) {
+#pragma unroll
+  for (int d = 0; d < 8; ++d) o[d] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, vb[d], o[d], 0, 0, 0);
+}
+
+// o[d] += P . V straight from the V rows.
+__device__ __forceinline__ void pv_accumulate(floatx4_t (&o)[8], short4_t pa,
+                                              const uint4 (&vr)[4]) {
+  short4_t vb[8];
+  v_operands(vr, vb);
+  pv_accumulate(o, pa, vb);
 }
 
 }  // namespace fk

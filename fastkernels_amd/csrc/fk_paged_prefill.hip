@@ -21,12 +21,35 @@
 // per 16-key tile, online softmax per query column, O += P V) and walks the
 // key tiles up to its last visible key.  The blocks with the most keys (the
 // last ones of a sequence) are dispatched first.
+#include <type_traits>
+
 #include "fk_attn_tile.h"
 
 namespace fk {
 namespace {
 
-constexpr int kColBlocks = 2;                  // 16-query column blocks per wave
+#ifndef FK_PREFILL_COLS
+#define FK_PREFILL_COLS 2
+#endif
+#ifndef FK_PREFILL_PREFETCH
+#define FK_PREFILL_PREFETCH 1
+#endif
+// Two waves per SIMD: with the register double buffer the compiler would
+// otherwise settle at one (262 registers), and the causal schedule's longest
+// work-groups are latency-bound.  Measured on MI355X: 155 us for a 2048-token
+// Qwen3-8B prompt against 178-277 us for the other register/occupancy points.
+#ifndef FK_PREFILL_WAVES
+#define FK_PREFILL_WAVES __attribute__((amdgpu_waves_per_eu(2)))
+#endif
+#ifndef FK_PREFILL_CHUNK
+#define FK_PREFILL_CHUNK 1
+#endif
+#ifndef FK_PREFILL_LAZY
+#define FK_PREFILL_LAZY 8.0f
+#endif
+constexpr int kColBlocks = FK_PREFILL_COLS;    // 16-query column blocks per wave
+constexpr float kLazy = FK_PREFILL_LAZY;       // max-update threshold (log2 units)
+constexpr int kChunk = FK_PREFILL_CHUNK;       // key tiles loaded together
 constexpr int kQTokens = 16 * kColBlocks;      // query tokens per work-group
 
 struct PrefillParams {
@@ -102,7 +125,7 @@ __device__ __forceinline__ int64_t key_row(const PrefillParams& P,
 }
 
 template <int NW, bool kFp8, bool kPaged>
-__global__ __launch_bounds__(NW * 64) void paged_prefill_kernel(
+__global__ __launch_bounds__(NW * 64) FK_PREFILL_WAVES void paged_prefill_kernel(
     PrefillParams P, const int32_t* __restrict__ block_tables,
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_k) {
   const int b = blockIdx.z;
@@ -162,49 +185,64 @@ __global__ __launch_bounds__(NW * 64) void paged_prefill_kernel(
   }
 
   const int ntiles = (kend + kTile - 1) / kTile;
-  TileRegs<kFp8> cur;
-  bool page_ok = false;
-  if (ntiles > 0)
-    prefill_load_tile<kFp8>(P, key_row<kPaged>(P, bt_row, k_start, 0, page_ok), row_cap, h, r, g,
-                            cur);
-  for (int t = 0; t < ntiles; ++t) {
-    const int tok0 = t * kTile;
-    // Prefetch the next tile (the last tile re-reads itself, a cache hit).
-    const int tn = min(t + 1, ntiles - 1);
-    bool ok_n;
-    const int64_t row_n = key_row<kPaged>(P, bt_row, k_start, tn * kTile, ok_n);
-    TileRegs<kFp8> nxt;
-    prefill_load_tile<kFp8>(P, row_n, row_cap, h, r, g, nxt);
+  // Tiles every query of the block sees in full need no mask: keys up to
+  // offset + j0 (query j0's last key), inside [0, kend).
+  const int nfull = max(0, min(kend, offset + j0 + 1)) / kTile;
 
+  // One 16-key tile: scores, online softmax per query column, P.V.  kMasked
+  // applies the causal / length / page mask; unmasked tiles skip it (every
+  // score is finite there, so the running max never stays -inf).
+  auto tile_step = [&](auto masked, int tok0, const TileRegs<kFp8>& cur, bool page_ok) {
+    constexpr bool kMasked = decltype(masked)::value;
     uint4 kc[4];
     k_chunks(cur, kc);
     uint4 vr[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      vr[i] = (page_ok && tok0 + 4 * g + i < kend) ? v_row(cur, i) : make_uint4(0, 0, 0, 0);
+      vr[i] = (!kMasked || (page_ok && tok0 + 4 * g + i < kend)) ? v_row(cur, i)
+                                                                 : make_uint4(0, 0, 0, 0);
+    short4_t vb[8];  // shared by the column blocks
+    v_operands(vr, vb);
 #pragma unroll
     for (int nb = 0; nb < kColBlocks; ++nb) {
       const floatx4_t acc = qk_scores(kc, qb[nb]);
-      const int j = j0 + 16 * nb + r;       // this lane's query column
-      const int last = offset + j;           // its last visible key
+      const int j = j0 + 16 * nb + r;  // this lane's query column
+      const int last = offset + j;     // its last visible key
       float s[4];
       float mt = kNegInf;
+      if constexpr (kMasked) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int key = tok0 + 4 * g + i;
-        const bool ok = page_ok && j < q_len && key <= last && key < kend;
-        s[i] = ok ? acc[i] * s2 : kNegInf;
-        mt = fmaxf(mt, s[i]);
+        for (int i = 0; i < 4; ++i) {
+          const int key = tok0 + 4 * g + i;
+          const bool ok = page_ok && j < q_len && key <= last && key < kend;
+          s[i] = ok ? acc[i] * s2 : kNegInf;
+          mt = fmaxf(mt, s[i]);
+        }
+      } else {
+        // s2 > 0: the max of the scaled scores is the scaled max.
+        mt = fmaxf(fmaxf(acc[0], acc[1]), fmaxf(acc[2], acc[3])) * s2;
       }
       mt = pair_max(mt);
-      const float m_new = fmaxf(m_run[nb], mt);
-      const float m_use = m_new == kNegInf ? 0.f : m_new;
-      const float alpha = m_new == kNegInf ? 1.f : __builtin_amdgcn_exp2f(m_run[nb] - m_use);
+      // Lazy rescaling: the running max only moves when a score exceeds it by
+      // more than kLazy (log2 units), so P <= 2^kLazy and the O/l rescale (a
+      // cross-lane fetch per row) is rare after the first tiles.  The final
+      // normalisation divides by l accumulated against the same max, so the
+      // result is unchanged up to rounding.
+      const float m_new = mt > m_run[nb] + kLazy ? mt : m_run[nb];
+      float m_use, alpha;
+      if constexpr (kMasked) {
+        m_use = m_new == kNegInf ? 0.f : m_new;
+        alpha = m_new == m_run[nb] ? 1.f : __builtin_amdgcn_exp2f(m_run[nb] - m_use);
+      } else {
+        m_use = m_new;  // finite
+        alpha = m_new == m_run[nb] ? 1.f : __builtin_amdgcn_exp2f(m_run[nb] - m_new);
+      }
       float pr[4];
       float psum = 0.f;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        pr[i] = __builtin_amdgcn_exp2f(s[i] - m_use);
+        pr[i] = kMasked ? __builtin_amdgcn_exp2f(s[i] - m_use)
+                        : __builtin_amdgcn_exp2f(__builtin_fmaf(acc[i], s2, -m_use));
         psum += pr[i];
       }
       l_run[nb] = l_run[nb] * alpha + psum;
@@ -217,11 +255,90 @@ __global__ __launch_bounds__(NW * 64) void paged_prefill_kernel(
           for (int d = 0; d < 8; ++d) o[nb][d][i] *= a;
         }
       }
-      pv_accumulate(o[nb], p_operand(pr), vr);
+      pv_accumulate(o[nb], p_operand(pr), vb);
     }
+  };
+
+#if FK_PREFILL_PREFETCH
+  // Register double buffer: the next tile's loads are issued before the current
+  // tile is processed (the last tile re-reads itself, a cache hit).
+  TileRegs<kFp8> cur;
+  bool page_ok = false;
+  if (ntiles > 0)
+    prefill_load_tile<kFp8>(P, key_row<kPaged>(P, bt_row, k_start, 0, page_ok), row_cap, h, r, g,
+                            cur);
+  auto advance = [&](auto masked, int t) {
+    const int tn = min(t + 1, ntiles - 1);
+    bool ok_n;
+    const int64_t row_n = key_row<kPaged>(P, bt_row, k_start, tn * kTile, ok_n);
+    TileRegs<kFp8> nxt;
+    prefill_load_tile<kFp8>(P, row_n, row_cap, h, r, g, nxt);
+    tile_step(masked, t * kTile, cur, page_ok);
     cur = nxt;
     page_ok = ok_n;
+  };
+  int t = 0;
+  if constexpr (kPaged) {
+    // A masked page (-1 table entry) needs the mask, so full tiles are only
+    // trusted while their pages are valid: check per tile.
+    for (; t < nfull; ++t) {
+      bool ok;
+      (void)key_row<kPaged>(P, bt_row, k_start, t * kTile, ok);
+      if (!ok) break;
+      advance(std::false_type{}, t);
+    }
+  } else {
+    for (; t < nfull; ++t) advance(std::false_type{}, t);
   }
+  for (; t < ntiles; ++t) advance(std::true_type{}, t);
+#else
+  if constexpr (kChunk == 1) {
+    // One tile at a time; the unmasked tiles (every query sees them in full)
+    // come first, in their own loop, so each loop body holds one variant.  A
+    // masked page (-1 table entry) needs the mask: the unmasked loop stops at
+    // the first one (checked before its loads are issued).
+    auto advance = [&](auto masked, int t) {
+      bool ok;
+      TileRegs<kFp8> cur;
+      prefill_load_tile<kFp8>(P, key_row<kPaged>(P, bt_row, k_start, t * kTile, ok), row_cap, h,
+                              r, g, cur);
+      tile_step(masked, t * kTile, cur, ok);
+    };
+    int t = 0;
+    for (; t < nfull; ++t) {
+      if constexpr (kPaged) {
+        bool ok;
+        (void)key_row<kPaged>(P, bt_row, k_start, t * kTile, ok);
+        if (!ok) break;
+      }
+      advance(std::false_type{}, t);
+    }
+    for (; t < ntiles; ++t) advance(std::true_type{}, t);
+  } else {
+  // Chunks of kChunk tiles: all their loads are issued, then the tiles are
+  // processed in order (each waits only for its own loads).  A tile is
+  // processed unmasked when every query sees it in full and its page is valid.
+  for (int t0 = 0; t0 < ntiles; t0 += kChunk) {
+    TileRegs<kFp8> buf[kChunk];
+    bool ok[kChunk];
+#pragma unroll
+    for (int u = 0; u < kChunk; ++u) {
+      const int tt = min(t0 + u, ntiles - 1);
+      prefill_load_tile<kFp8>(P, key_row<kPaged>(P, bt_row, k_start, tt * kTile, ok[u]), row_cap,
+                              h, r, g, buf[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < kChunk; ++u) {
+      const int tt = t0 + u;
+      if (tt >= ntiles) break;
+      if (tt < nfull && ok[u])
+        tile_step(std::false_type{}, tt * kTile, buf[u], true);
+      else
+        tile_step(std::true_type{}, tt * kTile, buf[u], ok[u]);
+    }
+  }
+  }
+#endif
 
   const float vs = (kFp8 && P.v_scale) ? P.v_scale[h] : 1.f;
 #pragma unroll
