@@ -173,3 +173,30 @@ def test_flash_attn_prefill_candidate(cuda):
     with pytest.raises(NotImplementedError):
         m(c["q"], c["kc"], c["vc"], c["cu_q"], c["cu_k"], 40, 50, block_table=c["bt"],
           window_size=(128, 0))
+
+
+def test_mixed_batch_like_forward_mixed(cuda):
+    """Attention._forward_mixed (attention_impl.py:682-731): the first np_ tokens are
+    prefill chunks (FlashAttnPrefill with a block table), the rest decode tokens
+    (FlashAttnDecode), written into one output; each part against the oracle."""
+    from fastkernels_amd.candidate.L1.flash_attn_decode import FlashAttnDecode
+    from fastkernels_amd.candidate.L1.flash_attn_prefill import FlashAttnPrefill
+    _flush("mixed prefill + decode batch")
+    q_lens, k_lens = [37, 16], [37, 200]          # prefill chunks
+    dec_lens = [5, 300, 1024, 77]                 # decode contexts
+    c = _case(cuda, q_lens + [1] * 4, k_lens + dec_lens, bs=64, seed=79)
+    np_ = sum(q_lens)
+    q = c["q"]
+    out = torch.empty_like(q)
+    pre = FlashAttnPrefill(32, 8, 128)
+    dec = FlashAttnDecode(32, 8, 128, page_size=64)
+    cu_q = c["cu_q"][:3].contiguous()
+    cu_k = c["cu_k"][:3].contiguous()
+    out[:np_] = pre(q[:np_], c["kc"], c["vc"], cu_seqlens_q=cu_q, cu_seqlens_k=cu_k,
+                    max_seqlen_q=max(q_lens), max_seqlen_k=max(k_lens), softmax_scale=128 ** -0.5,
+                    causal=True, block_table=c["bt"][:2])
+    ctx = torch.tensor(dec_lens, dtype=torch.int32, device=cuda)
+    out[np_:] = dec(q[np_:], c["kc"], c["vc"], cache_seqlens=ctx, block_table=c["bt"][2:],
+                    softmax_scale=128 ** -0.5, causal=True, max_seq_len=max(dec_lens))
+    torch.cuda.synchronize()
+    _close(out, _oracle(c), 1e-2, "mixed batch")
