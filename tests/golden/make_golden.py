@@ -84,6 +84,50 @@ def cases() -> dict[str, dict[str, np.ndarray]]:
     for d in (96, 13):
         x = bf16(3 * r.standard_normal((6, 2 * d)))
         out[f"silu_and_mul_d{d}"] = dict(x=x, out=oracle.silu_and_mul(x, "bf16"))
+    # (Fixtures below were added after the ones above; their draws come from
+    # their own generator so the earlier fixtures keep their values.)
+    r2 = np.random.default_rng(2002)
+    # merge_attn_states bf16 [T 6, H 3, D 64] with lse specials; suffix-only tail at 5
+    po, so = bf16(r2.standard_normal((6, 3, 64))), bf16(r2.standard_normal((6, 3, 64)))
+    pl = (3 * r2.standard_normal((3, 6))).astype(np.float32)
+    sl = (3 * r2.standard_normal((3, 6))).astype(np.float32)
+    pl[0, 0] = -np.inf
+    sl[1, 1] = -np.inf
+    pl[2, 2] = sl[2, 2] = -np.inf
+    pl[1, 3] = np.inf
+    mo, ml = oracle.merge_attn_states(po, pl, so, sl, "bf16", prefill_tokens_with_context=5)
+    out["merge_attn_states"] = dict(prefix=po, prefix_lse=pl, suffix=so, suffix_lse=sl,
+                                    prefill_tokens=np.int64(5), out=mo, out_lse=ml)
+    # paged prefill bf16: chunks (q_len, k_len) = (5, 5), (1, 17), (9, 30), (4, 2); Hq 8, Hk 2
+    q_lens, k_lens = [5, 1, 9, 4], [5, 17, 30, 2]
+    bs = 16
+    pages = [(k + bs - 1) // bs for k in k_lens]
+    nbp = sum(pages) + 1
+    permp = r2.permutation(nbp)
+    btp = -np.ones((4, max(pages)), np.int32)
+    off = 0
+    for i, p in enumerate(pages):
+        btp[i, :p] = permp[off:off + p]
+        off += p
+    cu_q = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
+    cu_k = np.concatenate([[0], np.cumsum(k_lens)]).astype(np.int32)
+    qp = bf16(r2.standard_normal((int(cu_q[-1]), 8, 128)))
+    kcp = bf16(r2.standard_normal((nbp, bs, 2, 128)))
+    vcp = bf16(r2.standard_normal((nbp, bs, 2, 128)))
+    out["paged_prefill_bf16"] = dict(
+        q=qp, k_cache=kcp, v_cache=vcp, block_tables=btp, cu_seqlens_q=cu_q, cu_seqlens_k=cu_k,
+        scale=scale, out=oracle.paged_prefill(qp, kcp, vcp, btp, cu_q, cu_k,
+                                              float(scale)).astype(np.float32))
+    # per-head q/k RMSNorm + NeoX rotary (the fused attention prologue), bf16, D 64
+    cs64 = oracle.rope_cos_sin_cache(64, 64, 1e4)
+    posq = np.array([0, 3, 63, 17], np.int64)
+    qh, kh = bf16(r2.standard_normal((4, 4 * 64))), bf16(r2.standard_normal((4, 2 * 64)))
+    qw, kw = bf16(1 + 0.2 * r2.standard_normal(64)), bf16(1 + 0.2 * r2.standard_normal(64))
+    qn = oracle.rms_norm(qh.reshape(4, 4, 64), qw, 1e-6, "bf16").reshape(4, -1)
+    kn = oracle.rms_norm(kh.reshape(4, 2, 64), kw, 1e-6, "bf16").reshape(4, -1)
+    oq, ok = oracle.rotary(posq, qn, kn, 64, cs64, True, "bf16")
+    out["qk_norm_rope"] = dict(positions=posq, q=qh, k=kh, q_weight=qw, k_weight=kw,
+                               cos_sin=cs64, eps=np.float32(1e-6), out_q=oq, out_k=ok)
     return out
 
 

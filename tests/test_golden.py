@@ -26,7 +26,8 @@ def test_fixture_set_present():
     names = {p.stem for p in GOLDEN.glob("*.npz")}
     assert {"rmsnorm_h256", "rmsnorm_h200", "rotary_neox", "rotary_gptj", "store_kvcache",
             "paged_decode_bf16", "paged_decode_fp8", "silu_and_mul_d96",
-            "silu_and_mul_d13"} <= names
+            "silu_and_mul_d13", "merge_attn_states", "paged_prefill_bf16",
+            "qk_norm_rope"} <= names
 
 
 @pytest.mark.parametrize("h", [256, 200])
@@ -64,6 +65,29 @@ def test_oracle_decode_golden(kind):
 def test_oracle_silu_golden(d):
     g = load(f"silu_and_mul_d{d}")
     assert np.array_equal(oracle.silu_and_mul(g["x"], "bf16"), g["out"])
+
+
+def test_oracle_merge_golden():
+    g = load("merge_attn_states")
+    o, lse = oracle.merge_attn_states(g["prefix"], g["prefix_lse"], g["suffix"], g["suffix_lse"],
+                                      "bf16", int(g["prefill_tokens"]))
+    assert np.array_equal(o, g["out"]) and np.array_equal(lse, g["out_lse"])
+
+
+def test_oracle_prefill_golden():
+    g = load("paged_prefill_bf16")
+    out = oracle.paged_prefill(g["q"], g["k_cache"], g["v_cache"], g["block_tables"],
+                               g["cu_seqlens_q"], g["cu_seqlens_k"], float(g["scale"]))
+    assert np.array_equal(out.astype(np.float32), g["out"])
+
+
+def test_oracle_qk_norm_rope_golden():
+    g = load("qk_norm_rope")
+    qn = oracle.rms_norm(g["q"].reshape(4, 4, 64), g["q_weight"], float(g["eps"]), "bf16")
+    kn = oracle.rms_norm(g["k"].reshape(4, 2, 64), g["k_weight"], float(g["eps"]), "bf16")
+    q, k = oracle.rotary(g["positions"], qn.reshape(4, -1), kn.reshape(4, -1), 64, g["cos_sin"],
+                         True, "bf16")
+    assert np.array_equal(q, g["out_q"]) and np.array_equal(k, g["out_k"])
 
 
 # ---------------------------------------------------------------------------
@@ -142,3 +166,38 @@ def test_gpu_golden_all(cuda):
         ops.silu_and_mul(out, x)
         torch.cuda.synchronize()
         _close(f32(out), g["out"], 1e-2)
+
+    g = load("merge_attn_states")
+    po, so = _t(g["prefix"], cuda, bf), _t(g["suffix"], cuda, bf)
+    pl, sl = _t(g["prefix_lse"], cuda), _t(g["suffix_lse"], cuda)
+    mo, ml = torch.empty_like(po), torch.empty_like(pl)
+    ops.merge_attn_states(mo, po, pl, so, sl, ml, int(g["prefill_tokens"]))
+    torch.cuda.synchronize()
+    _close(f32(mo), g["out"], 1e-2)
+    fin = np.isfinite(g["out_lse"])
+    assert np.array_equal(np.isneginf(ml.cpu().numpy()), np.isneginf(g["out_lse"]))
+    _close(ml.cpu().numpy()[fin], g["out_lse"][fin], 1e-5)
+
+    g = load("paged_prefill_bf16")
+    q = _t(g["q"], cuda, bf)
+    out = torch.full_like(q, float("nan"))
+    ops.paged_prefill(out, q, _t(g["k_cache"], cuda, bf), _t(g["v_cache"], cuda, bf),
+                      _t(g["block_tables"], cuda), _t(g["cu_seqlens_q"], cuda),
+                      _t(g["cu_seqlens_k"], cuda), int(np.diff(g["cu_seqlens_q"]).max()),
+                      float(g["scale"]))
+    torch.cuda.synchronize()
+    _close(f32(out), g["out"], 1e-2)
+
+    g = load("qk_norm_rope")
+    q, k = _t(g["q"], cuda, bf), _t(g["k"], cuda, bf)
+    v = torch.zeros_like(k)
+    kc = torch.zeros(2, 16, 2, 64, dtype=bf, device=cuda)
+    vc = torch.zeros_like(kc)
+    slots = torch.tensor([0, 5, 17, 31], dtype=torch.int64, device=cuda)
+    ops.qk_norm_rope_store(_t(g["positions"], cuda), q, k, v, kc, vc, slots, 64,
+                           _t(g["cos_sin"], cuda), True, _t(g["q_weight"], cuda, bf),
+                           _t(g["k_weight"], cuda, bf), float(g["eps"]))
+    torch.cuda.synchronize()
+    _close(f32(q), g["out_q"], 1e-2)
+    _close(f32(k), g["out_k"], 1e-2)
+    assert torch.equal(kc.view(-1, 128)[slots], k)
