@@ -72,6 +72,9 @@ _SIGNATURES = {
     "fk_varlen_prefill": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64,
                                   c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_int64, c_int,
                                   c_int, c_int, c_float, c_int, c_void_p]),
+    "fk_store_kvcache_convert": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_int, c_void_p,
+                                         c_void_p, c_int, c_void_p, c_int, c_int64, c_int64,
+                                         c_int64, c_void_p]),
     "fk_merge_attn_states": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p,
                                      c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int, c_int,
                                      c_int64, c_int, c_void_p]),

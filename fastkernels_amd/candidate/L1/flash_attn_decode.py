@@ -162,6 +162,15 @@ class FlashAttnDecode(nn.Module):
         q3 = q.view(b, self.num_heads, self.head_dim)
         k3 = key.view(b, hk, self.head_dim)
         v3 = value.view(b, hk, self.head_dim)
+        if key.dtype != k_cache.dtype:
+            # A converting store (e.g. bf16 rows into an fp8 cache) is a launch of its
+            # own; the decode then reads the cache as usual.
+            ops.store_kvcache(k3, v3, k_cache, v_cache, slot_mapping)
+            out3 = a["out"].view(b, self.num_heads, self.head_dim)
+            ops.paged_decode(out3, q3, k_cache, v_cache, a["block_table"], a["cache_seqlens"],
+                             a["softmax_scale"], a["part_tokens"], a["max_parts"], a["ws"],
+                             a["k_scale"], a["v_scale"])
+            return a["out"]
         out3 = a["out"].view(b, self.num_heads, self.head_dim)
         call = torch.ops.fastkernels_amd.store_paged_decode if torch.compiler.is_compiling() \
             else ops.store_paged_decode

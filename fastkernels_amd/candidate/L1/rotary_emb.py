@@ -98,6 +98,18 @@ class RotaryEmbedding(nn.Module):
             positions = positions.contiguous()
         k3 = k_cache.view(k_cache.shape[0], k_cache.shape[1], -1, self.head_dim)
         v3 = v_cache.view(v_cache.shape[0], v_cache.shape[1], -1, self.head_dim)
+        if k_cache.dtype != query.dtype:
+            # A cache of another dtype (fp8): the fused kernel stores bit copies, so
+            # run the ops one by one, the store converting as tl.store does.
+            t = positions.numel()
+            if q_norm is not None:
+                query.view(t, -1, self.head_dim).copy_(q_norm(query.view(t, -1, self.head_dim)))
+                key.view(t, -1, self.head_dim).copy_(k_norm(key.view(t, -1, self.head_dim)))
+            ops.rotary_embedding(positions, query, key, self.head_dim, cache, self.is_neox_style)
+            hk = k3.shape[2]
+            ops.store_kvcache(key.view(t, hk, self.head_dim), value.view(t, hk, self.head_dim),
+                              k3, v3, slot_mapping)
+            return query, key
         call = torch.ops.fastkernels_amd.qk_norm_rope_store if torch.compiler.is_compiling() \
             else ops.qk_norm_rope_store
         call(positions, query, key, value, k3, v3, slot_mapping, self.head_dim, cache,

@@ -6,7 +6,10 @@
 skipping slots < 0, and returns None, exactly as the Triton
 ``_store_kvcache_kernel`` (store_kvcache.py:16-35).  int32 and int64 slot
 mappings are read natively (no conversion tensor is allocated), and slots past
-the end of the cache are skipped instead of written.
+the end of the cache are skipped instead of written.  A key/value dtype that
+differs from the cache's (e.g. bf16 rows into a float8_e4m3fn cache) is converted
+as the Triton store's implicit cast does: round to nearest even, fp8 saturating
+at +-448.
 """
 from __future__ import annotations
 

@@ -159,3 +159,165 @@ extern "C" int fk_store_kvcache(const void* key, int64_t key_row_stride, const v
   return fk::launch<int32_t>(key, key_row_stride, value, value_row_stride, k_cache, v_cache,
                              slot_mapping, tokens, row_elems, elem_bytes, num_slots, s);
 }
+
+// ---------------------------------------------------------------------------
+// Store with a dtype conversion: the reference's Triton store writes a bf16 /
+// fp16 / fp32 key into a cache of another dtype with tl.store's implicit cast
+// (store_kvcache.py:32-35), which for a float8_e4m3fn cache rounds to nearest
+// even and saturates to the largest finite value (+-448).
+// ---------------------------------------------------------------------------
+namespace fk {
+namespace {
+
+// fp32 -> OCP e4m3fn code: round to nearest even, |x| >= 448 saturates to
+// +-448, NaN stays NaN (0x7F with the sign), subnormals below 2^-6.
+__device__ __forceinline__ uint8_t f32_to_e4m3fn_sat(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  const float a = __builtin_fabsf(x);
+  if (a != a) return static_cast<uint8_t>(sign | 0x7Fu);
+  if (a >= 448.f) return static_cast<uint8_t>(sign | 0x7Eu);
+  if (a < 0.015625f) {  // 2^-6: subnormal grid of 2^-9 (exact scaling)
+    const uint32_t m = static_cast<uint32_t>(__builtin_rintf(a * 512.f));  // 0..8; 8 = 2^-6
+    return static_cast<uint8_t>(sign | m);
+  }
+  const int e = static_cast<int>((u >> 23) & 0xFFu) - 127;  // -6 .. 8
+  const uint32_t mant = u & 0x7FFFFFu;
+  uint32_t r = mant >> 20;
+  const uint32_t rem = mant & 0xFFFFFu;
+  r += (rem > 0x80000u || (rem == 0x80000u && (r & 1u))) ? 1u : 0u;
+  uint32_t code = (static_cast<uint32_t>(e + 7) << 3) + r;  // r == 8 carries into the exponent
+  if (code > 0x7Eu) code = 0x7Eu;
+  return static_cast<uint8_t>(sign | code);
+}
+
+template <typename Src>
+__device__ __forceinline__ float src_to_f32(typename Src::storage v) { return Src::to_f32(v); }
+
+// Destination element from fp32, by cache dtype tag.
+template <int kDst>
+struct DstConv;
+template <>
+struct DstConv<FK_DTYPE_FP8_E4M3FN> {
+  using storage = uint8_t;
+  __device__ __forceinline__ static storage conv(float f) { return f32_to_e4m3fn_sat(f); }
+};
+template <>
+struct DstConv<FK_DTYPE_BF16> {
+  using storage = uint16_t;
+  __device__ __forceinline__ static storage conv(float f) { return BF16::from_f32(f); }
+};
+template <>
+struct DstConv<FK_DTYPE_F16> {
+  using storage = uint16_t;
+  __device__ __forceinline__ static storage conv(float f) { return F16::from_f32(f); }
+};
+template <>
+struct DstConv<FK_DTYPE_F32> {
+  using storage = float;
+  __device__ __forceinline__ static storage conv(float f) { return f; }
+};
+
+// One work-group per token; lanes stride the row element by element (the
+// conversion store is not on the decode step's hot path: the bf16 cache uses
+// the bit-copy kernels above).
+template <typename IdxT, typename Src, int kDst>
+__global__ __launch_bounds__(256) void store_kvcache_convert(
+    const typename Src::storage* __restrict__ key, int64_t key_row_stride,
+    const typename Src::storage* __restrict__ value, int64_t value_row_stride,
+    typename DstConv<kDst>::storage* __restrict__ k_cache,
+    typename DstConv<kDst>::storage* __restrict__ v_cache, const void* __restrict__ slot_mapping,
+    int64_t row_elems, int64_t num_slots) {
+  const int64_t tok = blockIdx.x;
+  const int64_t slot = load_slot<IdxT>(slot_mapping, tok);
+  if (slot < 0 || slot >= num_slots) return;
+  for (int64_t c = threadIdx.x; c < row_elems; c += 256) {
+    k_cache[slot * row_elems + c] = DstConv<kDst>::conv(Src::to_f32(key[tok * key_row_stride + c]));
+    v_cache[slot * row_elems + c] =
+        DstConv<kDst>::conv(Src::to_f32(value[tok * value_row_stride + c]));
+  }
+}
+
+template <typename IdxT, typename Src, int kDst>
+int launch_convert(const void* key, int64_t key_row_stride, const void* value,
+                   int64_t value_row_stride, void* k_cache, void* v_cache,
+                   const void* slot_mapping, int64_t tokens, int64_t row_elems, int64_t num_slots,
+                   hipStream_t stream) {
+  using S = typename Src::storage;
+  using D = typename DstConv<kDst>::storage;
+  hipLaunchKernelGGL((store_kvcache_convert<IdxT, Src, kDst>), dim3(static_cast<unsigned>(tokens)),
+                     dim3(256), 0, stream, static_cast<const S*>(key), key_row_stride,
+                     static_cast<const S*>(value), value_row_stride, static_cast<D*>(k_cache),
+                     static_cast<D*>(v_cache), slot_mapping, row_elems, num_slots);
+  return check_launch("fk_store_kvcache_convert");
+}
+
+template <typename IdxT, typename Src>
+int convert_dst(int cache_dtype, const void* key, int64_t ks, const void* value, int64_t vs,
+                void* kc, void* vc, const void* sm, int64_t tokens, int64_t row, int64_t slots,
+                hipStream_t s) {
+  switch (cache_dtype) {
+    case FK_DTYPE_FP8_E4M3FN:
+      return launch_convert<IdxT, Src, FK_DTYPE_FP8_E4M3FN>(key, ks, value, vs, kc, vc, sm, tokens,
+                                                             row, slots, s);
+    case FK_DTYPE_BF16:
+      return launch_convert<IdxT, Src, FK_DTYPE_BF16>(key, ks, value, vs, kc, vc, sm, tokens, row,
+                                                       slots, s);
+    case FK_DTYPE_F16:
+      return launch_convert<IdxT, Src, FK_DTYPE_F16>(key, ks, value, vs, kc, vc, sm, tokens, row,
+                                                      slots, s);
+    case FK_DTYPE_F32:
+      return launch_convert<IdxT, Src, FK_DTYPE_F32>(key, ks, value, vs, kc, vc, sm, tokens, row,
+                                                      slots, s);
+    default:
+      return set_error(FK_ERR_UNSUPPORTED, "fk_store_kvcache_convert: cache dtype %d unsupported",
+                       cache_dtype);
+  }
+}
+
+template <typename IdxT>
+int convert_src(int src_dtype, int cache_dtype, const void* key, int64_t ks, const void* value,
+                int64_t vs, void* kc, void* vc, const void* sm, int64_t tokens, int64_t row,
+                int64_t slots, hipStream_t s) {
+  switch (src_dtype) {
+    case FK_DTYPE_BF16:
+      return convert_dst<IdxT, BF16>(cache_dtype, key, ks, value, vs, kc, vc, sm, tokens, row,
+                                     slots, s);
+    case FK_DTYPE_F16:
+      return convert_dst<IdxT, F16>(cache_dtype, key, ks, value, vs, kc, vc, sm, tokens, row,
+                                    slots, s);
+    case FK_DTYPE_F32:
+      return convert_dst<IdxT, F32>(cache_dtype, key, ks, value, vs, kc, vc, sm, tokens, row,
+                                    slots, s);
+    default:
+      return set_error(FK_ERR_UNSUPPORTED, "fk_store_kvcache_convert: key dtype %d unsupported",
+                       src_dtype);
+  }
+}
+
+}  // namespace
+}  // namespace fk
+
+extern "C" int fk_store_kvcache_convert(const void* key, int64_t key_row_stride,
+                                        const void* value, int64_t value_row_stride,
+                                        int src_dtype, void* k_cache, void* v_cache,
+                                        int cache_dtype, const void* slot_mapping,
+                                        int slot_is_i64, int64_t tokens, int64_t row_elems,
+                                        int64_t num_slots, void* stream) {
+  FK_REQUIRE(tokens >= 0 && row_elems >= 0 && num_slots >= 0,
+             "fk_store_kvcache_convert: negative size");
+  FK_REQUIRE(tokens <= 0x7fffffffLL, "fk_store_kvcache_convert: too many tokens");
+  FK_REQUIRE(key_row_stride >= row_elems && value_row_stride >= row_elems,
+             "fk_store_kvcache_convert: row stride shorter than the row");
+  if (tokens == 0 || row_elems == 0) return FK_OK;
+  FK_REQUIRE(key && value && k_cache && v_cache && slot_mapping,
+             "fk_store_kvcache_convert: null pointer");
+  hipStream_t s = fk::as_stream(stream);
+  if (slot_is_i64)
+    return fk::convert_src<int64_t>(src_dtype, cache_dtype, key, key_row_stride, value,
+                                    value_row_stride, k_cache, v_cache, slot_mapping, tokens,
+                                    row_elems, num_slots, s);
+  return fk::convert_src<int32_t>(src_dtype, cache_dtype, key, key_row_stride, value,
+                                  value_row_stride, k_cache, v_cache, slot_mapping, tokens,
+                                  row_elems, num_slots, s);
+}

@@ -160,9 +160,14 @@ def rotary_embedding(positions: torch.Tensor, query: torch.Tensor, key: torch.Te
 # ---------------------------------------------------------------------------
 # store_kvcache
 # ---------------------------------------------------------------------------
+_CONVERT_SRC = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
+_CONVERT_DST = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2, torch.float8_e4m3fn: 3}
+
 def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
                   v_cache: torch.Tensor, slot_mapping: torch.Tensor) -> None:
-    """Scatter key/value [N, Hk, D] rows into NHD caches at slot_mapping (-1 skips)."""
+    """Scatter key/value [N, Hk, D] rows into NHD caches at slot_mapping (-1 skips).
+    Same dtype: a bit copy.  Otherwise each element is converted to the cache dtype
+    (fp8 e4m3fn: round to nearest even, saturating at +-448), as tl.store does."""
     if key.dim() != 3 or value.shape != key.shape:
         raise ValueError("store_kvcache: key/value must be [N, num_kv_heads, head_dim]")
     n, hk, hd = key.shape
@@ -170,8 +175,11 @@ def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
         raise ValueError("store_kvcache: caches must be [num_blocks, block_size, Hk, D]")
     if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
         raise ValueError("store_kvcache: caches must be contiguous")
-    if key.dtype != k_cache.dtype or value.dtype != v_cache.dtype:
-        raise TypeError("store_kvcache: key/value dtype must equal the cache dtype")
+    convert = key.dtype != k_cache.dtype
+    if value.dtype != key.dtype or v_cache.dtype != k_cache.dtype:
+        raise TypeError("store_kvcache: key and value (and the two caches) must share a dtype")
+    if convert and (key.dtype not in _CONVERT_SRC or k_cache.dtype not in _CONVERT_DST):
+        raise TypeError(f"store_kvcache: no conversion from {key.dtype} to {k_cache.dtype}")
     for t, nm in ((key, "key"), (value, "value")):
         if t.stride(2) != 1 or (hk > 1 and t.stride(1) != hd):
             raise ValueError(f"store_kvcache: {nm} rows must be [Hk, D] contiguous")
@@ -183,6 +191,12 @@ def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
     if n == 0:
         return
     num_slots = k_cache.shape[0] * k_cache.shape[1]
+    if convert:  # the reference's tl.store casts to the cache dtype
+        _native.call("fk_store_kvcache_convert", _ptr(key), key.stride(0), _ptr(value),
+                     value.stride(0), _CONVERT_SRC[key.dtype], _ptr(k_cache), _ptr(v_cache),
+                     _CONVERT_DST[k_cache.dtype], _ptr(slot_mapping),
+                     int(slot_mapping.dtype == torch.int64), n, hk * hd, num_slots, _stream(key))
+        return
     _native.call("fk_store_kvcache", _ptr(key), key.stride(0), _ptr(value), value.stride(0),
                  _ptr(k_cache), _ptr(v_cache), _ptr(slot_mapping),
                  int(slot_mapping.dtype == torch.int64), n, hk * hd, key.element_size(),

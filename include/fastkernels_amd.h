@@ -39,6 +39,9 @@
  *   fk_store_paged_decode
  *       fastkernels/tasks/baseline/L2/attention_impl.py:313-363 (forward_impl: store,
  *       then the decode branch of _forward_pure :436-450).
+ *   fk_store_kvcache_convert
+ *       fastkernels/tasks/baseline/L1/store_kvcache.py:16-35,71-82 (StoreKVCache.forward
+ *       when key and cache dtypes differ).
  *   fk_paged_prefill, fk_varlen_prefill
  *       fastkernels/tasks/baseline/L1/flash_attn_prefill.py:18-74 (FlashAttnPrefill.forward,
  *       with and without block_table).
@@ -183,6 +186,19 @@ int fk_paged_decode_reduce(void* out, int64_t out_row_stride, const void* q,
                            int num_kv_heads, int head_size, int block_size, int64_t num_blocks,
                            float scale, int64_t part_tokens, int64_t max_parts, void* workspace,
                            int64_t workspace_bytes, void* stream);
+
+/* store_kvcache into a cache of another dtype (StoreKVCache.forward with, e.g., a bf16
+ * key and a float8_e4m3fn cache: the Triton store converts with tl.store's implicit
+ * cast, store_kvcache.py:32-35).  Each element is widened to fp32 and converted to the
+ * cache dtype: bf16 / fp16 round to nearest even; fp8 e4m3fn rounds to nearest even,
+ * saturates |x| >= 448 to +-448 and keeps NaN.  src_dtype: F32, F16 or BF16;
+ * cache_dtype: F32, F16, BF16 or FP8_E4M3FN.  Other arguments as fk_store_kvcache
+ * (strides in key/value elements; slots < 0 or >= num_slots are skipped). */
+int fk_store_kvcache_convert(const void* key, int64_t key_row_stride, const void* value,
+                             int64_t value_row_stride, int src_dtype, void* k_cache,
+                             void* v_cache, int cache_dtype, const void* slot_mapping,
+                             int slot_is_i64, int64_t tokens, int64_t row_elems,
+                             int64_t num_slots, void* stream);
 
 /* Paged prefill attention: FlashAttnPrefill.forward with a block table
  * (fastkernels/tasks/baseline/L1/flash_attn_prefill.py:28-74), the prefill half of

@@ -78,8 +78,13 @@ def fp8_e4m3fn_decode(codes: np.ndarray) -> np.ndarray:
 
 
 def fp8_e4m3fn_encode(x: np.ndarray) -> np.ndarray:
-    """Saturating round-to-nearest-even float -> e4m3fn code (|x| clamped to 448)."""
-    x = np.clip(np.asarray(x, np.float64), -E4M3FN_MAX, E4M3FN_MAX)
+    """Saturating round-to-nearest-even float -> e4m3fn code (|x| clamped to 448; NaN
+    gives the NaN code with the input's sign), the conversion of a Triton tl.store into a
+    float8e4nv pointer (round to nearest even, saturate to finite)."""
+    x = np.asarray(x, np.float64)
+    nan = np.isnan(x)
+    sign = np.signbit(x).ravel()  # negative values that round to 0 give -0 (0x80)
+    x = np.clip(np.where(nan, 0.0, x), -E4M3FN_MAX, E4M3FN_MAX)
     finite = E4M3FN_TABLE.astype(np.float64)
     pos_codes = np.arange(0, 0x7F, dtype=np.int64)  # 0 .. 0x7E are the finite non-negatives
     pos_vals = finite[pos_codes]
@@ -90,7 +95,7 @@ def fp8_e4m3fn_encode(x: np.ndarray) -> np.ndarray:
     pick_hi = (a - lo > hi - a) | ((a - lo == hi - a) & ((pos_codes[idx] & 1) == 0))
     code = np.where(pick_hi, pos_codes[idx], pos_codes[idx - 1])
     code = np.where(a == 0, 0, code)
-    sign = np.signbit(x).ravel()  # negative values that round to 0 give -0 (0x80)
+    code = np.where(nan.ravel(), 0x7F, code)
     return (code | (sign.astype(np.int64) << 7)).astype(np.uint8).reshape(np.shape(x))
 
 

@@ -299,3 +299,44 @@ def test_qk_norm_rope_store_candidate(cuda):
     torch.cuda.synchronize()
     assert torch.equal(qb, q2) and torch.equal(kb, k2)
     assert torch.equal(kc1, kc2) and torch.equal(vc1, vc2)
+
+
+def test_fused_paths_with_fp8_cache_and_bf16_rows(cuda):
+    """bf16 new rows into an fp8 cache: forward_store (decode) and forward_store
+    (rotary) fall back to the converting store; results equal the module chain."""
+    from fastkernels_amd.candidate.L1.flash_attn_decode import FlashAttnDecode
+    from fastkernels_amd.candidate.L1.rotary_emb import RotaryEmbedding
+    from fastkernels_amd.candidate.L1.store_kvcache import StoreKVCache
+    case = workloads.c5_fp8_decode(cuda, batch=4, ctx_lens=[100, 1, 300, 17], pool_blocks=8,
+                                   seed=49)
+    rows = workloads.decode_step_rows(case)
+    kb, vb = rows.key.float().bfloat16(), rows.value.float().bfloat16()  # bf16 rows
+    attn = FlashAttnDecode(64, 8, 128, page_size=256)
+    kw = dict(cache_seqlens=case.ctx_lens, block_table=case.block_tables, softmax_scale=case.scale,
+              k_scale=case.k_scale, v_scale=case.v_scale, max_seq_len=300)
+    kc1, vc1 = case.k_cache.clone(), case.v_cache.clone()
+    StoreKVCache()(kb, vb, kc1, vc1, rows.slot_mapping)
+    ref = attn(case.q, kc1, vc1, **kw)
+    kc2, vc2 = case.k_cache.clone(), case.v_cache.clone()
+    got = attn.forward_store(case.q, kb, vb, kc2, vc2, rows.slot_mapping, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)
+    assert torch.equal(kc1.view(torch.uint8), kc2.view(torch.uint8))
+    # rotary + store into the fp8 cache
+    t = 4
+    qkv = torch.randn(t, (64 + 16) * 128, device=cuda).bfloat16()
+    pos = torch.tensor([3, 7, 100, 2000], device=cuda)
+    rope = RotaryEmbedding(128, 4096, 1e6).to(cuda)
+    a = qkv.clone()
+    qa, ka, va = a[:, :64 * 128], a[:, 64 * 128:72 * 128], a[:, 72 * 128:]
+    kc3, vc3 = case.k_cache.clone(), case.v_cache.clone()
+    rope(pos, qa, ka)
+    StoreKVCache()(ka.view(t, 8, 128), va.view(t, 8, 128), kc3, vc3, rows.slot_mapping)
+    b = qkv.clone()
+    qb, kb2, vb2 = b[:, :64 * 128], b[:, 64 * 128:72 * 128], b[:, 72 * 128:]
+    kc4, vc4 = case.k_cache.clone(), case.v_cache.clone()
+    rope.forward_store(pos, qb, kb2, vb2, kc4, vc4, rows.slot_mapping)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    assert torch.equal(kc3.view(torch.uint8), kc4.view(torch.uint8))
+    assert torch.equal(vc3.view(torch.uint8), vc4.view(torch.uint8))

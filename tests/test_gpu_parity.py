@@ -552,3 +552,52 @@ def test_merge_attn_states_candidate(cuda):
     MergeAttnStates()(out, po, pl, so, sl, out_lse)
     torch.cuda.synchronize()
     _check_merge(out, out_lse, po, pl, so, sl, torch.bfloat16)
+
+
+# ---------------------------------------------------------------------------
+# store_kvcache with a dtype conversion (bf16/fp16/fp32 key -> fp8 / bf16 cache)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("src", [torch.bfloat16, torch.float16, torch.float32])
+def test_store_kvcache_convert_to_fp8(cuda, src):
+    """The conversion tl.store applies (round to nearest even, saturating at +-448,
+    NaN kept) against the oracle's encoder, bit-exact, with ties, subnormals,
+    saturation, infinities and NaN planted."""
+    _flush(f"store_kvcache convert {src} -> fp8")
+    g = torch.Generator().manual_seed(90)
+    n, hk, d = 300, 8, 128
+    key = (torch.randn(n, hk, d, generator=g) * 40).to(src)
+    val = (torch.randn(n, hk, d, generator=g) * 1e-3).to(src)  # subnormal range of e4m3fn
+    special = torch.tensor([0.0, -0.0, 447.0, 448.0, 460.0, 464.0, 1e4, float("inf"), float("-inf"),
+                            float("nan"), 2.0 ** -9, 1.5 * 2.0 ** -9, 2.0 ** -10, 0.0068359375,
+                            1.0625, 1.1875, -3.25 * 2.0 ** -8, 240.0, 232.0])
+    key.view(-1)[:special.numel()] = special.to(src)
+    slots = torch.randperm(64 * 16, generator=g)[:n].to(torch.int64)
+    slots[7] = -1
+    kc = torch.zeros(64, 16, hk, d, dtype=torch.float8_e4m3fn)
+    vc = torch.zeros_like(kc)
+    key_d, val_d, kc_d, vc_d, sl_d = (t.to(cuda) for t in (key, val, kc, vc, slots))
+    ops.store_kvcache(key_d, val_d, kc_d, vc_d, sl_d)
+    torch.cuda.synchronize()
+    ek = oracle.fp8_e4m3fn_encode(key.float().numpy())
+    ev = oracle.fp8_e4m3fn_encode(val.float().numpy())
+    zk = np.zeros((64 * 16, hk * d), np.uint8)
+    zv = np.zeros_like(zk)
+    ok = slots.numpy() >= 0
+    zk[slots.numpy()[ok]] = ek.reshape(n, -1)[ok]
+    zv[slots.numpy()[ok]] = ev.reshape(n, -1)[ok]
+    assert np.array_equal(kc_d.view(torch.uint8).cpu().numpy().reshape(-1, hk * d), zk)
+    assert np.array_equal(vc_d.view(torch.uint8).cpu().numpy().reshape(-1, hk * d), zv)
+
+
+def test_store_kvcache_convert_f32_to_bf16(cuda):
+    g = torch.Generator().manual_seed(91)
+    key = torch.randn(33, 2, 64, generator=g).to(cuda)
+    val = torch.randn(33, 2, 64, generator=g).to(cuda)
+    kc = torch.zeros(8, 16, 2, 64, dtype=torch.bfloat16, device=cuda)
+    vc = torch.zeros_like(kc)
+    slots = torch.randperm(128, generator=g)[:33].to(torch.int32).to(cuda)
+    ops.store_kvcache(key, val, kc, vc, slots)
+    torch.cuda.synchronize()
+    kf = kc.view(-1, 128)[slots.long()]
+    assert torch.equal(kf, key.view(33, -1).bfloat16())  # torch's RNE cast
+    assert torch.equal(vc.view(-1, 128)[slots.long()], val.view(33, -1).bfloat16())

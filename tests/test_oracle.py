@@ -91,6 +91,9 @@ def test_e4m3fn_encode_matches_torch():
     theirs = torch.from_numpy(xc).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
     ours = oracle.fp8_e4m3fn_encode(x)
     assert np.array_equal(ours, theirs)
+    # saturation (Triton's satfinite store) and NaN with its sign
+    assert list(oracle.fp8_e4m3fn_encode(np.array([np.inf, -np.inf, 1e9, np.nan, -np.nan]))) == \
+        [0x7E, 0xFE, 0x7E, 0x7F, 0xFF]
 
 
 # ---------------------------------------------------------------------------
