@@ -150,3 +150,81 @@ def test_fused_store_decode_graph_capture_and_replay(cuda):
         assert torch.equal(out, eager), f"replay {i}: output differs from eager"
         assert torch.equal(static["k_cache"], eager_bufs["k_cache"]), f"replay {i}: k_cache"
         assert torch.equal(static["v_cache"], eager_bufs["v_cache"]), f"replay {i}: v_cache"
+
+
+def test_prefill_merge_prologue_graph_capture_and_replay(cuda):
+    """The other allocation-free entry points under one captured graph: the q/k
+    norm + rotary + store prologue, paged prefill over the cache it wrote, and an
+    LSE merge.  Replayed on new inputs; every replay equals an eager run."""
+    from fastkernels_amd import ops
+
+    t, hq, hk, d, bs = 64, 32, 8, 128, 16
+    g = torch.Generator().manual_seed(700)
+
+    def inputs(seed):
+        gg = torch.Generator().manual_seed(seed)
+        return dict(
+            qkv=torch.randn(t, (hq + 2 * hk) * d, generator=gg).bfloat16().to(cuda),
+            pos=torch.arange(t).to(cuda),
+            po=torch.randn(t, hq, d, generator=gg).bfloat16().to(cuda),
+            pl=torch.randn(hq, t, generator=gg).to(cuda),
+            sl=torch.randn(hq, t, generator=gg).to(cuda))
+
+    kc0 = torch.randn(8, bs, hk, d, generator=g).bfloat16().to(cuda)
+    vc0 = torch.randn(8, bs, hk, d, generator=g).bfloat16().to(cuda)
+    bt = torch.arange(8, dtype=torch.int32, device=cuda).view(1, 8)
+    slots = torch.arange(t, dtype=torch.int64, device=cuda)   # positions 0..63 of sequence 0
+    cu_q = torch.tensor([0, t], dtype=torch.int32, device=cuda)
+    cu_k = torch.tensor([0, t], dtype=torch.int32, device=cuda)
+    inv = 1.0 / (1e6 ** (torch.arange(0, d, 2, dtype=torch.float32) / d))
+    ang = torch.outer(torch.arange(4096, dtype=torch.float32), inv)
+    cache = torch.cat((ang.cos(), ang.sin()), -1).to(cuda)
+    qw = torch.ones(d, dtype=torch.bfloat16, device=cuda)
+    kw = qw.clone()
+
+    static = inputs(701)
+    static.update(kc=kc0.clone(), vc=vc0.clone(), out=torch.empty(t, hq, d, dtype=torch.bfloat16,
+                                                                 device=cuda),
+                  mo=torch.empty(t, hq, d, dtype=torch.bfloat16, device=cuda),
+                  ml=torch.empty(hq, t, device=cuda))
+
+    def step(bufs):
+        qkv = bufs["qkv"]
+        q, k, v = qkv[:, :hq * d], qkv[:, hq * d:(hq + hk) * d], qkv[:, (hq + hk) * d:]
+        ops.qk_norm_rope_store(bufs["pos"], q, k, v, bufs["kc"], bufs["vc"], slots, d, cache,
+                               True, qw, kw, 1e-6)
+        ops.paged_prefill(bufs["out"], q.view(t, hq, d).contiguous(), bufs["kc"], bufs["vc"],
+                          bt, cu_q, cu_k, t, d ** -0.5)
+        ops.merge_attn_states(bufs["mo"], bufs["out"], bufs["pl"], bufs["po"], bufs["sl"],
+                              bufs["ml"])
+        return bufs["mo"], bufs["ml"]
+
+    def load(src):
+        for key in ("qkv", "pos", "po", "pl", "sl"):
+            static[key].copy_(src[key])
+        static["kc"].copy_(kc0)
+        static["vc"].copy_(vc0)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step(static)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    load(inputs(701))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        mo, ml = step(static)
+    torch.cuda.synchronize()
+    for i, seed in enumerate((702, 703, 701)):
+        src = inputs(seed)
+        load(src)
+        eager = {k: (v.clone() if isinstance(v, torch.Tensor) else v) for k, v in static.items()}
+        emo, eml = (x.clone() for x in step(eager))
+        torch.cuda.synchronize()
+        load(src)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(mo, emo), f"replay {i}: merge output differs"
+        assert torch.equal(ml, eml), f"replay {i}: merge lse differs"
+        assert torch.equal(static["kc"], eager["kc"]), f"replay {i}: cache differs"
