@@ -333,6 +333,27 @@ def test_paged_decode_workspace_reuse(cuda):
         assert_close(f32(out), ref, BF16_TOL, BF16_TOL, f"call {it} part={plan.part_tokens}")
 
 
+def test_paged_decode_balanced_repeatable(cuda):
+    """Repeated balanced launches on one workspace give identical bits (the schedule
+    depends only on the lengths), and match the oracle."""
+    case = workloads.c3_decode(cuda, batch=40, num_heads=32, kv_heads=8, pool_blocks=1024,
+                               ctx_lo=1, ctx_hi=6000, seed=93)
+    b, hq, d = case.q.shape
+    plan = ops.paged_decode_plan(b, hq, 8, d, case.max_seq_len, 0)
+    ws = torch.zeros(plan.workspace_bytes, dtype=torch.uint8, device=cuda)
+    outs = []
+    for _ in range(4):
+        out = torch.full_like(case.q, float("nan"))
+        ops.paged_decode(out, case.q, case.k_cache, case.v_cache, case.block_tables,
+                         case.ctx_lens, case.scale, plan.part_tokens, plan.max_parts, ws)
+        torch.cuda.synchronize()
+        outs.append(out)
+    for o in outs[1:]:
+        assert torch.equal(o.view(torch.int16), outs[0].view(torch.int16))
+    seqs = list(range(0, b, 5))
+    assert_close(f32(outs[0])[seqs], oracle_decode(case, seqs)[seqs], BF16_TOL, BF16_TOL, "C3-like")
+
+
 def test_paged_decode_padded_rows_and_masked_pages(cuda):
     """ctx 0 rows (engine padding, engine.py:5405-5407) give zeros; a -1 page inside
     the context is masked instead of read."""
