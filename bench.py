@@ -38,8 +38,8 @@ METRIC = "paged decode attn µs/call + achieved HBM GB/s (% of 8 TB/s), Qwen3-8B
 def _parse():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=500)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--num-splits", type=int, default=0, help="0 = automatic partitioning")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline time budget")
@@ -63,6 +63,23 @@ def _flush_buffer(device):
     # timed calls.  A read (not a fill) leaves no dirty lines whose write-back
     # would compete with the timed kernel.
     return torch.ones(512 * 1024 * 1024 // 4, dtype=torch.float32, device=device)
+
+
+def settle_clocks(fn, seconds=0.3):
+    """Run fn back to back for `seconds` of wall time before anything is timed.
+
+    An idle MI355X takes tens of milliseconds of sustained load to reach its steady
+    clocks: measured on C5, the first ~25 calls of a process (~10 ms) ran up to 30%
+    slower than the rest, whatever op came first.  A fixed number of warmup calls
+    does not cover that for short ops, so the bench first loads the GPU for a fixed
+    time (untimed), then does its warmup steps."""
+    import torch
+
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(20):
+            fn()
+        torch.cuda.synchronize()
 
 
 def time_call(fn, iters=50, warmup=10, flush=None):
@@ -173,9 +190,13 @@ def bench_decode(args):
     total_bytes = case.algorithmic_bytes()
     out_bytes = out.numel() * out.element_size()
     partial_bytes = total_bytes - out_bytes  # the main kernel's algorithmic bytes (no output)
-    for _ in range(args.warmup):
+    def step():
         partials()
         reduce()
+
+    settle_clocks(step)
+    for _ in range(args.warmup):
+        step()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream(dev)
     ev = _events(2 * args.steps)
@@ -281,6 +302,7 @@ def bench_table(args):
     dev = torch.device("cuda:0")
     flush = _flush_buffer(dev)
     rows = []
+    settle_clocks(lambda: flush.sum())
 
     def add(cfg, op, fn, nbytes, cpu=None, iters=50):
         """cpu = (callable, fraction of the op's bytes it processes, sample text) or None."""

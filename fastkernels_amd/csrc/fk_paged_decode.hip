@@ -535,17 +535,24 @@ __global__ __launch_bounds__(NH * 64) void paged_decode_balanced_kernel(
   }
 }
 
-// Merge of one (query head hq, sequence b): one wave, each lane owns two dims.
-// Partial rows: k = 0 is `alt_first_row`, k >= 1 is first_row + k * row_stride.
-// One online pass (running max with rescaling), so the loads of all partials
-// are independent and overlap instead of costing a latency per dependency.
+// Merge of one (query head hq, sequence b) by a work-group of kMergeWaves
+// waves; each lane owns two dims.  Partial rows: k = 0 is `alt_first_row`,
+// k >= 1 is first_row + k * row_stride.  Wave v folds rows v, v + kMergeWaves,
+// ... in one online pass (running max with rescaling, so the loads of all its
+// rows are independent and overlap), and the waves' (max, sum, O) are combined
+// through LDS: a sequence cut into 32 pieces costs about two load latencies
+// instead of eight.
+constexpr int kMergeWaves = 4;
 __device__ __forceinline__ void merge_rows(uint16_t* orow, const float* part_o,
                                            const float* part_ml, int64_t first_row,
-                                           int64_t row_stride, int nrows, int lane,
-                                           int64_t alt_first_row) {
+                                           int64_t row_stride, int nrows, int64_t alt_first_row) {
+  __shared__ float red_ml[kMergeWaves][2];
+  __shared__ float2 red_o[kMergeWaves][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
   float M = kNegInf, L = 0.f, o0 = 0.f, o1 = 0.f;
 #pragma unroll 4
-  for (int k = 0; k < nrows; ++k) {
+  for (int k = wave; k < nrows; k += kMergeWaves) {
     const int64_t row = (k == 0 ? alt_first_row : first_row + k * row_stride);
     const float m = part_ml[row * 2];
     const float l = part_ml[row * 2 + 1];
@@ -559,20 +566,43 @@ __device__ __forceinline__ void merge_rows(uint16_t* orow, const float* part_o,
     o1 = o1 * a + ov.y * f;
     M = mn;
   }
-  const float inv = L > 0.f ? 1.f / L : 0.f;
-  const bf16x2_t pk = {static_cast<__bf16>(o0 * inv), static_cast<__bf16>(o1 * inv)};
+  if (lane == 0) {
+    red_ml[wave][0] = M;
+    red_ml[wave][1] = L;
+  }
+  red_o[wave][lane] = make_float2(o0, o1);
+  __syncthreads();
+  if (wave != 0) return;
+  float Mt = kNegInf;
+#pragma unroll
+  for (int v = 0; v < kMergeWaves; ++v) Mt = fmaxf(Mt, red_ml[v][0]);
+  float Lt = 0.f, a0 = 0.f, a1 = 0.f;
+  if (Mt != kNegInf) {
+#pragma unroll
+    for (int v = 0; v < kMergeWaves; ++v) {
+      const float f = __builtin_amdgcn_exp2f(red_ml[v][0] - Mt);  // 0 for a wave with no rows
+      const float2 ov = red_o[v][lane];
+      Lt += red_ml[v][1] * f;
+      a0 += ov.x * f;
+      a1 += ov.y * f;
+    }
+  }
+  const float inv = Lt > 0.f ? 1.f / Lt : 0.f;
+  const bf16x2_t pk = {static_cast<__bf16>(a0 * inv), static_cast<__bf16>(a1 * inv)};
   reinterpret_cast<uint32_t*>(orow)[lane] = __builtin_bit_cast(uint32_t, pk);
 }
 
 // Fixed partitions: merge sequences with more than one partition; zero empty ones.
-__global__ __launch_bounds__(64) void paged_decode_partition_reduce_kernel(DecodeParams P) {
+// One work-group of kMergeWaves waves per (query head hq, sequence b).
+__global__ __launch_bounds__(kMergeWaves * 64) void paged_decode_partition_reduce_kernel(
+    DecodeParams P) {
   const int hq = blockIdx.x;
   const int b = blockIdx.y;
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x & 63;
   const int ctx = P.ctx_lens[b];
   uint16_t* orow = P.out + b * P.out_row_stride + static_cast<int64_t>(hq) * kHead;
   if (ctx <= 0) {
-    reinterpret_cast<uint32_t*>(orow)[lane] = 0u;
+    if (threadIdx.x < 64) reinterpret_cast<uint32_t*>(orow)[lane] = 0u;
     return;
   }
   const int nparts = min((ctx + P.part_tokens - 1) / P.part_tokens, P.max_parts);
@@ -580,21 +610,22 @@ __global__ __launch_bounds__(64) void paged_decode_partition_reduce_kernel(Decod
   const int h = hq / P.gqa;
   const int j = hq - h * P.gqa;
   const int64_t first = (static_cast<int64_t>(b) * P.num_kv_heads + h) * P.max_parts * P.gqa + j;
-  merge_rows(orow, P.part_o, P.part_ml, first, P.gqa, nparts, lane, first);
+  merge_rows(orow, P.part_o, P.part_ml, first, P.gqa, nparts, first);
 }
 
 // Balanced schedule: merge sequences cut across work-groups; zero empty ones.
-// One wave per (query head hq, sequence b).
-__global__ __launch_bounds__(64) void paged_decode_balanced_reduce_kernel(DecodeParams P) {
+// One work-group of kMergeWaves waves per (query head hq, sequence b).
+__global__ __launch_bounds__(kMergeWaves * 64) void paged_decode_balanced_reduce_kernel(
+    DecodeParams P) {
   const int hq = blockIdx.x;
   const int b = blockIdx.y;
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x & 63;
   uint16_t* orow = P.out + b * P.out_row_stride + static_cast<int64_t>(hq) * kHead;
   const int t0 = P.tile_off[b];
   const int t1 = P.tile_off[b + 1];
   const int S = P.tile_off[P.batch + 1];
   if (t1 <= t0) {
-    reinterpret_cast<uint32_t*>(orow)[lane] = 0u;
+    if (threadIdx.x < 64) reinterpret_cast<uint32_t*>(orow)[lane] = 0u;
     return;
   }
   const int w0 = t0 / S;
@@ -608,7 +639,7 @@ __global__ __launch_bounds__(64) void paged_decode_balanced_reduce_kernel(Decode
   const int slot0 = t0 > w0 * S ? 1 : 0;
   const int64_t first_alt = ((static_cast<int64_t>(w0) * 2 + slot0) * hk + h) * P.gqa + j;
   const int64_t first = ((static_cast<int64_t>(w0) * 2 + 0) * hk + h) * P.gqa + j;
-  merge_rows(orow, P.part_o, P.part_ml, first, 2 * hk * P.gqa, w1 - w0 + 1, lane, first_alt);
+  merge_rows(orow, P.part_o, P.part_ml, first, 2 * hk * P.gqa, w1 - w0 + 1, first_alt);
 }
 
 // Tuning knobs (compile-time): tiles per load set, and whether two sets are
@@ -878,11 +909,11 @@ extern "C" int fk_paged_decode_reduce(
   if (rc != FK_OK || batch == 0) return rc;
   const dim3 grid(static_cast<unsigned>(num_heads), static_cast<unsigned>(batch));
   if (L.balanced)
-    hipLaunchKernelGGL(paged_decode_balanced_reduce_kernel, grid, dim3(64), 0, as_stream(stream),
-                       L.P);
+    hipLaunchKernelGGL(paged_decode_balanced_reduce_kernel, grid, dim3(kMergeWaves * 64), 0,
+                       as_stream(stream), L.P);
   else
-    hipLaunchKernelGGL(paged_decode_partition_reduce_kernel, grid, dim3(64), 0, as_stream(stream),
-                       L.P);
+    hipLaunchKernelGGL(paged_decode_partition_reduce_kernel, grid, dim3(kMergeWaves * 64), 0,
+                       as_stream(stream), L.P);
   return check_launch("fk_paged_decode_reduce");
 }
 
