@@ -13,14 +13,17 @@
 // with no visible key gets a zero row.  kv head = hq / (Hq / Hk); fp8 pages
 // are dequantised per kv head as in the decode kernel.
 //
-// Work decomposition: work-group = (block of 32 query tokens, kv head,
-// sequence), one wave per query head of the kv head's group (groups above 8
-// heads span two work-groups), so the group's waves stream the same K/V tiles
-// (shared through L1/L2).  A wave keeps two
-// 16-query column blocks of one head in MFMA tiles (fk_attn_tile.h: S = K Q^T
-// per 16-key tile, online softmax per query column, O += P V) and walks the
-// key tiles up to its last visible key.  The blocks with the most keys (the
-// last ones of a sequence) are dispatched first.
+// Work decomposition: work-group = 4 waves over one kv head and one block of
+// query tokens of one sequence: the waves are the group's query heads (up to
+// 4; larger groups span several work-groups) times consecutive 32-token query
+// blocks (4 / heads of them).  A wave keeps two 16-query column blocks of one
+// head in MFMA tiles (fk_attn_tile.h: S = K Q^T per 16-key tile, online
+// softmax per query column, O += P V).  The work-group streams the keys in
+// stages of 64 through LDS (double-buffered: the next stage's global loads are
+// in flight while the current one is consumed), so the waves share each K/V
+// byte and no wave waits on a global load per tile; each wave stops at its own
+// last visible key.  The blocks with the most keys (the last ones of a
+// sequence) are dispatched first.
 #include <type_traits>
 
 #include "fk_attn_tile.h"
@@ -31,26 +34,19 @@ namespace {
 #ifndef FK_PREFILL_COLS
 #define FK_PREFILL_COLS 2
 #endif
-#ifndef FK_PREFILL_PREFETCH
-#define FK_PREFILL_PREFETCH 1
-#endif
-// Two waves per SIMD: with the register double buffer the compiler would
-// otherwise settle at one (262 registers), and the causal schedule's longest
-// work-groups are latency-bound.  Measured on MI355X: 155 us for a 2048-token
-// Qwen3-8B prompt against 178-277 us for the other register/occupancy points.
+// Two waves per SIMD (two 4-wave work-groups per CU; each holds 64 KB of LDS).
 #ifndef FK_PREFILL_WAVES
 #define FK_PREFILL_WAVES __attribute__((amdgpu_waves_per_eu(2)))
-#endif
-#ifndef FK_PREFILL_CHUNK
-#define FK_PREFILL_CHUNK 1
 #endif
 #ifndef FK_PREFILL_LAZY
 #define FK_PREFILL_LAZY 8.0f
 #endif
 constexpr int kColBlocks = FK_PREFILL_COLS;    // 16-query column blocks per wave
 constexpr float kLazy = FK_PREFILL_LAZY;       // max-update threshold (log2 units)
-constexpr int kChunk = FK_PREFILL_CHUNK;       // key tiles loaded together
-constexpr int kQTokens = 16 * kColBlocks;      // query tokens per work-group
+constexpr int kQTokens = 16 * kColBlocks;      // query tokens per wave
+constexpr int kPrefillWaves = 4;               // waves per work-group
+constexpr int kStageKeys = 64;                 // keys per LDS stage
+constexpr int kStageTiles = kStageKeys / kTile;
 
 struct PrefillParams {
   uint16_t* out;
@@ -80,33 +76,6 @@ __device__ __forceinline__ int64_t prefill_page(const PrefillParams& P,
   return (page >= 0 && page < P.num_blocks) ? page : -1;
 }
 
-// Issues the loads of the 16 key rows starting at row index row0 (a tile never
-// spans pages, so its rows are consecutive in both layouts).  Rows above
-// row_cap (past the end of a dense key tensor) re-read row_cap; they are masked.
-template <bool kFp8>
-__device__ __forceinline__ void prefill_load_tile(const PrefillParams& P, int64_t row0,
-                                                  int64_t row_cap, int h, int r, int g,
-                                                  TileRegs<kFp8>& t) {
-  constexpr int kElem = kFp8 ? 1 : 2;
-  const int64_t head_off = static_cast<int64_t>(h) * kHead * kElem;
-  const uint8_t* krow = P.k_cache + min(row0 + r, row_cap) * P.k_row_bytes + head_off;
-  const uint8_t* vbase = P.v_cache + head_off;
-  int64_t vr[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) vr[i] = min(row0 + 4 * g + i, row_cap);
-  if constexpr (!kFp8) {
-#pragma unroll
-    for (int c = 0; c < 4; ++c) t.k[c] = ld16(krow + (32 * c + 8 * g) * 2);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) t.v[i] = ld16(vbase + vr[i] * P.v_row_bytes + 8 * r * 2);
-  } else {
-    t.k[0] = ld16(krow + 32 * g);
-    t.k[1] = ld16(krow + 32 * g + 16);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) t.v[i] = ld8(vbase + vr[i] * P.v_row_bytes + 8 * r);
-  }
-}
-
 // Row index of key `tok` of the sequence and whether it is readable: paged, the
 // slot through the block table (-1 pages masked; page 0 is read instead);
 // dense, row k_start + tok of the key/value tensors.
@@ -124,33 +93,114 @@ __device__ __forceinline__ int64_t key_row(const PrefillParams& P,
   }
 }
 
-template <int NW, bool kFp8, bool kPaged>
-__global__ __launch_bounds__(NW * 64) FK_PREFILL_WAVES void paged_prefill_kernel(
+// LDS staging of key/value rows.  A stage is kStageKeys consecutive keys of one
+// kv head: kStageKeys K rows, then kStageKeys V rows, each kRowBytes long, with
+// the 16-byte chunks of row R stored at chunk index q ^ (R mod kChunks) so
+// that the row-parallel writes and the MFMA-layout reads (16 rows at one chunk
+// index, or one row's 16 chunks) hit distinct banks.
+template <bool kFp8>
+struct Stage {
+  static constexpr int kRowBytes = kFp8 ? kHead : 2 * kHead;
+  static constexpr int kChunks = kRowBytes / 16;
+  static constexpr int kBytes = 2 * kStageKeys * kRowBytes;  // K rows + V rows
+  // Direct-to-LDS loads per thread per stage (16 bytes each).
+  static constexpr int kLoads = 2 * kStageKeys * kChunks / (kPrefillWaves * 64);
+  __device__ __forceinline__ static int offset(int which, int row, int q) {
+    return (which * kStageKeys + row) * kRowBytes + ((q ^ (row & (kChunks - 1))) << 4);
+  }
+};
+
+// 16 bytes from global memory straight into LDS (gfx950 global_load_lds_dwordx4):
+// lane l of the wave writes at byte lds_addr + 16 l.  Written as inline asm, so
+// the compiler's wait-count pass does not see it: its builtin form makes the
+// pass wait for the load before every later LDS read, including reads of the
+// other stage buffer, which would serialise the double buffer.  The kernel
+// orders it explicitly instead (s_waitcnt vmcnt(0), then a barrier, before the
+// buffer is read).  M0 carries the LDS address and is restored afterwards.
+__device__ __forceinline__ void lds_dma16(const uint8_t* src, uint32_t lds_addr) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, off\n\t"
+      "s_nop 0\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(src), "s"(lds_addr)
+      : "memory");
+}
+
+// LDS byte address of a pointer into a __shared__ array.
+__device__ __forceinline__ uint32_t lds_addr_of(const uint8_t* p) {
+  return static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const uint8_t*)p));
+}
+
+// Tile tt (rows 16 tt .. 16 tt + 15) of a staged buffer in the register layout
+// prefill_load_tile produces from global memory.
+template <bool kFp8>
+__device__ __forceinline__ void lds_tile(const uint8_t* buf, int tt, int r, int g,
+                                         TileRegs<kFp8>& t) {
+  using S = Stage<kFp8>;
+  const int kr = 16 * tt + r;
+  if constexpr (!kFp8) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      t.k[c] = *reinterpret_cast<const uint4*>(buf + S::offset(0, kr, 4 * c + g));
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      t.v[i] = *reinterpret_cast<const uint4*>(buf + S::offset(1, 16 * tt + 4 * g + i, r));
+  } else {
+    t.k[0] = *reinterpret_cast<const uint4*>(buf + S::offset(0, kr, 2 * g));
+    t.k[1] = *reinterpret_cast<const uint4*>(buf + S::offset(0, kr, 2 * g + 1));
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      t.v[i] = *reinterpret_cast<const uint2*>(buf + S::offset(1, 16 * tt + 4 * g + i, r >> 1) +
+                                               8 * (r & 1));
+  }
+}
+
+// Work-group = kPrefillWaves waves over one kv head: hw query heads of its group
+// times qs = kPrefillWaves / hw blocks of kQTokens query tokens (a group larger
+// than kPrefillWaves heads spans hsplit work-groups).  All waves share the K/V
+// stages; each walks the tiles up to its own last visible key.
+template <bool kFp8, bool kPaged>
+__global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_prefill_kernel(
     PrefillParams P, const int32_t* __restrict__ block_tables,
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_k) {
+  using S = Stage<kFp8>;
+  __shared__ __align__(16) uint8_t lds0[S::kBytes];
+  __shared__ __align__(16) uint8_t lds1[S::kBytes];
   const int b = blockIdx.z;
-  // Groups of more than 8 query heads per kv head span hsplit work-groups.
-  const int hsplit = (P.gqa + NW - 1) / NW;
+  const int hw = P.gqa < kPrefillWaves ? P.gqa : kPrefillWaves;  // heads per work-group
+  const int qs = kPrefillWaves / hw;                             // query blocks per work-group
+  const int hsplit = (P.gqa + hw - 1) / hw;
   const int h = blockIdx.y / hsplit;
-  const int head0 = (blockIdx.y - h * hsplit) * NW;  // first query head (within the group)
+  const int head0 = (blockIdx.y - h * hsplit) * hw;
   const int q_start = cu_q[b];
   const int q_len = cu_q[b + 1] - q_start;
   const int k_start = cu_k[b];
   const int k_len = cu_k[b + 1] - k_start;
   // Heaviest blocks (most keys) first.
   const int qblk = static_cast<int>(gridDim.x) - 1 - static_cast<int>(blockIdx.x);
-  const int j0 = qblk * kQTokens;
-  if (j0 >= q_len) return;  // uniform over the work-group
+  const int jw0 = qblk * qs * kQTokens;  // first query of the work-group
+  if (jw0 >= q_len) return;              // uniform over the work-group
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  if (head0 + wave >= P.gqa) return;
-  const int hq = h * P.gqa + head0 + wave;
   const int lane = threadIdx.x & 63;
   const int r = lane & 15;
   const int g = lane >> 4;
+  const int head = head0 + wave % hw;
+  const int j0 = jw0 + (wave / hw) * kQTokens;
+  // Waves without queries (past the chunk, or past the group) still stage.
+  const bool active = j0 < q_len && head < P.gqa && wave < qs * hw;
+  const int hq = h * P.gqa + (head < P.gqa ? head : 0);
   // Position of query 0; non-causal, every query sits past the last key.
   const int offset = P.causal ? k_len - q_len : k_len;
-  // Keys [0, kend) cover every query of this block.
-  const int kend = max(0, min(k_len, offset + min(j0 + kQTokens, q_len)));
+  // Keys [0, kend) cover every query of this wave's block; kend_wg every query
+  // of the work-group.
+  const int kend = active ? max(0, min(k_len, offset + min(j0 + kQTokens, q_len))) : 0;
+  const int kend_wg = max(0, min(k_len, offset + min(jw0 + qs * kQTokens, q_len)));
   const int32_t* bt_row = kPaged ? block_tables + static_cast<int64_t>(b) * P.bt_row_stride
                                  : nullptr;
   // Dense keys: rows past the sequence's last key would run off the tensor.
@@ -161,7 +211,7 @@ __global__ __launch_bounds__(NW * 64) FK_PREFILL_WAVES void paged_prefill_kernel
 #pragma unroll
   for (int nb = 0; nb < kColBlocks; ++nb) {
     const int j = j0 + 16 * nb + r;
-    const bool ok = j < q_len;
+    const bool ok = active && j < q_len;
     const uint16_t* qp = P.q + static_cast<int64_t>(q_start + (ok ? j : 0)) * P.q_row_stride +
                          static_cast<int64_t>(hq) * kHead;
 #pragma unroll
@@ -187,7 +237,8 @@ __global__ __launch_bounds__(NW * 64) FK_PREFILL_WAVES void paged_prefill_kernel
   const int ntiles = (kend + kTile - 1) / kTile;
   // Tiles every query of the block sees in full need no mask: keys up to
   // offset + j0 (query j0's last key), inside [0, kend).
-  const int nfull = max(0, min(kend, offset + j0 + 1)) / kTile;
+  const int nfull = active ? max(0, min(kend, offset + j0 + 1)) / kTile : 0;
+  const int nstages = (kend_wg + kStageKeys - 1) / kStageKeys;
 
   // One 16-key tile: scores, online softmax per query column, P.V.  kMasked
   // applies the causal / length / page mask; unmasked tiles skip it (every
@@ -259,86 +310,91 @@ __global__ __launch_bounds__(NW * 64) FK_PREFILL_WAVES void paged_prefill_kernel
     }
   };
 
-#if FK_PREFILL_PREFETCH
-  // Register double buffer: the next tile's loads are issued before the current
-  // tile is processed (the last tile re-reads itself, a cache hit).
-  TileRegs<kFp8> cur;
-  bool page_ok = false;
-  if (ntiles > 0)
-    prefill_load_tile<kFp8>(P, key_row<kPaged>(P, bt_row, k_start, 0, page_ok), row_cap, h, r, g,
-                            cur);
-  auto advance = [&](auto masked, int t) {
-    const int tn = min(t + 1, ntiles - 1);
-    bool ok_n;
-    const int64_t row_n = key_row<kPaged>(P, bt_row, k_start, tn * kTile, ok_n);
-    TileRegs<kFp8> nxt;
-    prefill_load_tile<kFp8>(P, row_n, row_cap, h, r, g, nxt);
-    tile_step(masked, t * kTile, cur, page_ok);
-    cur = nxt;
-    page_ok = ok_n;
+  // Staging with direct global-to-LDS loads (lds_dma16).  Load i of wave w
+  // fills stage chunk positions p = 64 (4 i + w) + lane; position p is physical
+  // chunk p mod kChunks of row p / kChunks (K rows, then V rows), so the lane
+  // reads the logical chunk that the swizzle puts there.  Rows of a masked page
+  // (-1 table entry) read page 0 and rows past a dense tensor's end re-read its
+  // last row; the consumer masks both.
+  const int64_t head_off = static_cast<int64_t>(h) * kHead * (kFp8 ? 1 : 2);
+  auto stage_load = [&](int st, uint8_t* buf) {
+    const uint32_t buf_addr = lds_addr_of(buf);
+    // First rows of the stage's tiles: page lookups once per tile, wave-uniform.
+    int64_t row0[kStageTiles];
+#pragma unroll
+    for (int tt = 0; tt < kStageTiles; ++tt) {
+      bool ok;
+      row0[tt] = key_row<kPaged>(P, bt_row, k_start, st * kStageKeys + tt * kTile, ok);
+    }
+#pragma unroll
+    for (int i = 0; i < S::kLoads; ++i) {
+      const int pos0 = 64 * (kPrefillWaves * i + wave);  // wave-uniform
+      const int pos = pos0 + lane;
+      const int which = pos0 / (kStageKeys * S::kChunks);  // 0: K, 1: V
+      const int rem = pos - which * kStageKeys * S::kChunks;
+      const int row = rem / S::kChunks;
+      const int q = (rem - row * S::kChunks) ^ (row & (S::kChunks - 1));
+      int64_t base = row0[0];
+#pragma unroll
+      for (int tt = 1; tt < kStageTiles; ++tt)
+        if ((row >> 4) == tt) base = row0[tt];
+      const int64_t grow = min(base + (row & 15), row_cap);
+      const uint8_t* src = (which ? P.v_cache : P.k_cache) +
+                           grow * (which ? P.v_row_bytes : P.k_row_bytes) + head_off + 16 * q;
+      lds_dma16(src, buf_addr + 16 * pos0);
+    }
   };
-  int t = 0;
-  if constexpr (kPaged) {
-    // A masked page (-1 table entry) needs the mask, so full tiles are only
-    // trusted while their pages are valid: check per tile.
-    for (; t < nfull; ++t) {
-      bool ok;
-      (void)key_row<kPaged>(P, bt_row, k_start, t * kTile, ok);
-      if (!ok) break;
-      advance(std::false_type{}, t);
-    }
-  } else {
-    for (; t < nfull; ++t) advance(std::false_type{}, t);
-  }
-  for (; t < ntiles; ++t) advance(std::true_type{}, t);
-#else
-  if constexpr (kChunk == 1) {
-    // One tile at a time; the unmasked tiles (every query sees them in full)
-    // come first, in their own loop, so each loop body holds one variant.  A
-    // masked page (-1 table entry) needs the mask: the unmasked loop stops at
-    // the first one (checked before its loads are issued).
-    auto advance = [&](auto masked, int t) {
-      bool ok;
+  // Consumes one stage from `buf` (this wave's tiles only), every tile with the
+  // mask or every tile without it: one variant per loop body keeps the register
+  // count where two waves fit on a SIMD.
+  auto stage_compute = [&](auto masked, int st, const uint8_t* buf) {
+    // Not unrolled: unrolling lets the compiler hoist every tile's LDS reads
+    // (32 registers each) ahead of the first tile's math, and spill.
+#pragma unroll 1
+    for (int tt = 0; tt < kStageTiles; ++tt) {
+      const int t = st * kStageTiles + tt;
+      if (t >= ntiles) break;  // wave-uniform; the rest of the stage is past this wave's keys
+      bool page_ok = true;
+      if constexpr (decltype(masked)::value && kPaged)
+        (void)key_row<kPaged>(P, bt_row, k_start, t * kTile, page_ok);
       TileRegs<kFp8> cur;
-      prefill_load_tile<kFp8>(P, key_row<kPaged>(P, bt_row, k_start, t * kTile, ok), row_cap, h,
-                              r, g, cur);
-      tile_step(masked, t * kTile, cur, ok);
-    };
-    int t = 0;
-    for (; t < nfull; ++t) {
-      if constexpr (kPaged) {
+      lds_tile<kFp8>(buf, tt, r, g, cur);
+      tile_step(masked, t * kTile, cur, page_ok);
+    }
+  };
+  // A stage needs no mask when this wave sees all its keys in full (below nfull)
+  // and none of its pages is masked.
+  auto stage_unmasked = [&](int st) {
+    if ((st + 1) * kStageTiles > nfull) return false;
+    if constexpr (kPaged) {
+#pragma unroll
+      for (int tt = 0; tt < kStageTiles; ++tt) {
         bool ok;
-        (void)key_row<kPaged>(P, bt_row, k_start, t * kTile, ok);
-        if (!ok) break;
+        (void)key_row<kPaged>(P, bt_row, k_start, (st * kStageTiles + tt) * kTile, ok);
+        if (!ok) return false;
       }
-      advance(std::false_type{}, t);
     }
-    for (; t < ntiles; ++t) advance(std::true_type{}, t);
-  } else {
-  // Chunks of kChunk tiles: all their loads are issued, then the tiles are
-  // processed in order (each waits only for its own loads).  A tile is
-  // processed unmasked when every query sees it in full and its page is valid.
-  for (int t0 = 0; t0 < ntiles; t0 += kChunk) {
-    TileRegs<kFp8> buf[kChunk];
-    bool ok[kChunk];
-#pragma unroll
-    for (int u = 0; u < kChunk; ++u) {
-      const int tt = min(t0 + u, ntiles - 1);
-      prefill_load_tile<kFp8>(P, key_row<kPaged>(P, bt_row, k_start, tt * kTile, ok[u]), row_cap,
-                              h, r, g, buf[u]);
-    }
-#pragma unroll
-    for (int u = 0; u < kChunk; ++u) {
-      const int tt = t0 + u;
-      if (tt >= ntiles) break;
-      if (tt < nfull && ok[u])
-        tile_step(std::false_type{}, tt * kTile, buf[u], true);
-      else
-        tile_step(std::true_type{}, tt * kTile, buf[u], ok[u]);
-    }
-  }
-  }
-#endif
+    return true;
+  };
+  // One step: wait for stage st's loads (every thread's, through the barrier,
+  // which also frees the other buffer), issue stage st + 1's, consume stage st.
+  // The unmasked stages (a prefix) and the masked ones run in separate loops;
+  // every wave passes exactly nstages barriers whichever loop it is in.
+  auto step = [&](auto masked, int st) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    uint8_t* cur_buf = (st & 1) ? lds1 : lds0;
+    uint8_t* next_buf = (st & 1) ? lds0 : lds1;
+    if (st + 1 < nstages) stage_load(st + 1, next_buf);
+    stage_compute(masked, st, cur_buf);
+  };
+  if (nstages > 0) stage_load(0, lds0);
+  int st = 0;
+#pragma unroll 1
+  for (; st < nstages && stage_unmasked(st); ++st) step(std::false_type{}, st);
+#pragma unroll 1
+  for (; st < nstages; ++st) step(std::true_type{}, st);
+  if (!active) return;
 
   const float vs = (kFp8 && P.v_scale) ? P.v_scale[h] : 1.f;
 #pragma unroll
@@ -365,16 +421,10 @@ __global__ __launch_bounds__(NW * 64) FK_PREFILL_WAVES void paged_prefill_kernel
 }
 
 template <bool FP8, bool PAGED>
-void launch_prefill(const PrefillParams& P, int nw, dim3 grid, const int32_t* bt,
-                    const int32_t* cu_q, const int32_t* cu_k, hipStream_t stream) {
-#define FK_PF(NW)                                                                        \
-  hipLaunchKernelGGL((paged_prefill_kernel<NW, FP8, PAGED>), grid, dim3(NW * 64), 0, stream, \
-                     P, bt, cu_q, cu_k)
-  if (nw <= 1) FK_PF(1);
-  else if (nw <= 2) FK_PF(2);
-  else if (nw <= 4) FK_PF(4);
-  else FK_PF(8);
-#undef FK_PF
+void launch_prefill(const PrefillParams& P, dim3 grid, const int32_t* bt, const int32_t* cu_q,
+                    const int32_t* cu_k, hipStream_t stream) {
+  hipLaunchKernelGGL((paged_prefill_kernel<FP8, PAGED>), grid, dim3(kPrefillWaves * 64), 0,
+                     stream, P, bt, cu_q, cu_k);
 }
 
 }  // namespace
@@ -424,7 +474,10 @@ int prefill_entry(const char* name, bool paged, void* out, int64_t out_row_strid
                  q_row_stride % 8 == 0 && out_row_stride % 8 == 0 && k_row_bytes % 16 == 0 &&
                  v_row_bytes % 16 == 0,
              "%s: q/out/keys/values must be 16-byte aligned with 16-byte row strides", name);
-  const int64_t qblocks = (max_seqlen_q + kQTokens - 1) / kQTokens;
+  const int gqa = num_heads / num_kv_heads;
+  const int hw = gqa < kPrefillWaves ? gqa : kPrefillWaves;  // query heads per work-group
+  const int64_t wg_tokens = static_cast<int64_t>(kPrefillWaves / hw) * kQTokens;
+  const int64_t qblocks = (max_seqlen_q + wg_tokens - 1) / wg_tokens;
   PrefillParams P;
   P.out = static_cast<uint16_t*>(out);
   P.out_row_stride = out_row_stride;
@@ -443,17 +496,16 @@ int prefill_entry(const char* name, bool paged, void* out, int64_t out_row_strid
   P.num_blocks = paged ? num_blocks : 0;
   P.scale_log2 = scale * kLog2e;
   P.causal = causal ? 1 : 0;
-  const int nw = P.gqa < 8 ? P.gqa : 8;  // waves (query heads) per work-group
-  const int hsplit = (P.gqa + nw - 1) / nw;
+  const int hsplit = (gqa + hw - 1) / hw;
   const dim3 grid(static_cast<unsigned>(qblocks), static_cast<unsigned>(num_kv_heads * hsplit),
                   static_cast<unsigned>(batch));
   hipStream_t s = as_stream(stream);
   if (!paged)
-    launch_prefill<false, false>(P, nw, grid, nullptr, cu_seqlens_q, cu_seqlens_k, s);
+    launch_prefill<false, false>(P, grid, nullptr, cu_seqlens_q, cu_seqlens_k, s);
   else if (kv_dtype == FK_DTYPE_FP8_E4M3FN)
-    launch_prefill<true, true>(P, nw, grid, block_tables, cu_seqlens_q, cu_seqlens_k, s);
+    launch_prefill<true, true>(P, grid, block_tables, cu_seqlens_q, cu_seqlens_k, s);
   else
-    launch_prefill<false, true>(P, nw, grid, block_tables, cu_seqlens_q, cu_seqlens_k, s);
+    launch_prefill<false, true>(P, grid, block_tables, cu_seqlens_q, cu_seqlens_k, s);
   return check_launch(name);
 }
 
