@@ -45,11 +45,13 @@ __device__ __forceinline__ float pair_sum(float v) {
   return __uint_as_float(c[0]) + __uint_as_float(c[1]);
 }
 
+// Low / high 16-bit halves of a and b packed as (a, b): one v_perm_b32 each
+// (byte selectors over {b, a}, a in bytes 0-3).
 __device__ __forceinline__ uint32_t lo_pair(uint32_t a, uint32_t b) {
-  return (a & 0xffffu) | (b << 16);
+  return __builtin_amdgcn_perm(b, a, 0x05040100u);  // (a & 0xffff) | (b << 16)
 }
 __device__ __forceinline__ uint32_t hi_pair(uint32_t a, uint32_t b) {
-  return (a >> 16) | (b & 0xffff0000u);
+  return __builtin_amdgcn_perm(b, a, 0x07060302u);  // (a >> 16) | (b & 0xffff0000)
 }
 __device__ __forceinline__ uint32_t word(const uint4& v, int i) {
   return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;

@@ -22,8 +22,9 @@
 // stages of 64 through LDS (double-buffered: the next stage's global loads are
 // in flight while the current one is consumed), so the waves share each K/V
 // byte and no wave waits on a global load per tile; each wave stops at its own
-// last visible key.  The blocks with the most keys (the last ones of a
-// sequence) are dispatched first.
+// last visible key.  In a causal chunk with few cached keys before it, a
+// work-group takes two query blocks, one near the chunk's end and one near its
+// start, so that the work-groups are even.
 #include <type_traits>
 
 #include "fk_attn_tile.h"
@@ -138,22 +139,31 @@ __device__ __forceinline__ uint32_t lds_addr_of(const uint8_t* p) {
 }
 
 // Tile tt (rows 16 tt .. 16 tt + 15) of a staged buffer in the register layout
-// prefill_load_tile produces from global memory.
+// a global load of the tile would give: the K rows (t.k) and the V rows (t.v),
+// read separately so that a caller can keep them apart in time.
 template <bool kFp8>
-__device__ __forceinline__ void lds_tile(const uint8_t* buf, int tt, int r, int g,
-                                         TileRegs<kFp8>& t) {
+__device__ __forceinline__ void lds_tile_k(const uint8_t* buf, int tt, int r, int g,
+                                           TileRegs<kFp8>& t) {
   using S = Stage<kFp8>;
   const int kr = 16 * tt + r;
   if constexpr (!kFp8) {
 #pragma unroll
     for (int c = 0; c < 4; ++c)
       t.k[c] = *reinterpret_cast<const uint4*>(buf + S::offset(0, kr, 4 * c + g));
+  } else {
+    t.k[0] = *reinterpret_cast<const uint4*>(buf + S::offset(0, kr, 2 * g));
+    t.k[1] = *reinterpret_cast<const uint4*>(buf + S::offset(0, kr, 2 * g + 1));
+  }
+}
+template <bool kFp8>
+__device__ __forceinline__ void lds_tile_v(const uint8_t* buf, int tt, int r, int g,
+                                           TileRegs<kFp8>& t) {
+  using S = Stage<kFp8>;
+  if constexpr (!kFp8) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       t.v[i] = *reinterpret_cast<const uint4*>(buf + S::offset(1, 16 * tt + 4 * g + i, r));
   } else {
-    t.k[0] = *reinterpret_cast<const uint4*>(buf + S::offset(0, kr, 2 * g));
-    t.k[1] = *reinterpret_cast<const uint4*>(buf + S::offset(0, kr, 2 * g + 1));
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       t.v[i] = *reinterpret_cast<const uint2*>(buf + S::offset(1, 16 * tt + 4 * g + i, r >> 1) +
@@ -172,39 +182,57 @@ __global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_pre
   using S = Stage<kFp8>;
   __shared__ __align__(16) uint8_t lds0[S::kBytes];
   __shared__ __align__(16) uint8_t lds1[S::kBytes];
-  const int b = blockIdx.z;
+  // Grid: x = kv head (x hsplit), y = sequence, z = query block.  The block
+  // index varies slowest, so the work-groups that have work (low z when blocks
+  // are paired) are dispatched first and spread over every CU.
+  const int b = blockIdx.y;
   const int hw = P.gqa < kPrefillWaves ? P.gqa : kPrefillWaves;  // heads per work-group
   const int qs = kPrefillWaves / hw;                             // query blocks per work-group
   const int hsplit = (P.gqa + hw - 1) / hw;
-  const int h = blockIdx.y / hsplit;
-  const int head0 = (blockIdx.y - h * hsplit) * hw;
+  const int h = blockIdx.x / hsplit;
+  const int head0 = (blockIdx.x - h * hsplit) * hw;
   const int q_start = cu_q[b];
   const int q_len = cu_q[b + 1] - q_start;
   const int k_start = cu_k[b];
   const int k_len = cu_k[b + 1] - k_start;
-  // Heaviest blocks (most keys) first.
-  const int qblk = static_cast<int>(gridDim.x) - 1 - static_cast<int>(blockIdx.x);
-  const int jw0 = qblk * qs * kQTokens;  // first query of the work-group
-  if (jw0 >= q_len) return;              // uniform over the work-group
+  // Query blocks of the sequence at work-group granularity (wg_tokens queries
+  // each).  When the causal triangle dominates the sequence's work (fewer than
+  // q_len cached keys before the chunk), work-group p takes the pair of blocks
+  // nqb - 1 - p (the most keys) and p (the fewest), one after the other, so its
+  // work-groups stream about the same number of keys and no wave is left with a
+  // long tail on its own; the upper half of the grid then has nothing to do.
+  // Otherwise the blocks' key counts are close, and work-group x takes block
+  // nqb - 1 - x alone (the heaviest first), keeping twice the work-groups.
+  const int wg_tokens = qs * kQTokens;
+  const int nqb = (q_len + wg_tokens - 1) / wg_tokens;
+  const bool paired = P.causal && k_len - q_len < q_len;
+  const int x = static_cast<int>(blockIdx.z);
+  if (x >= (paired ? (nqb + 1) / 2 : nqb)) return;  // uniform over the work-group
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int r = lane & 15;
   const int g = lane >> 4;
   const int head = head0 + wave % hw;
-  const int j0 = jw0 + (wave / hw) * kQTokens;
-  // Waves without queries (past the chunk, or past the group) still stage.
-  const bool active = j0 < q_len && head < P.gqa && wave < qs * hw;
   const int hq = h * P.gqa + (head < P.gqa ? head : 0);
   // Position of query 0; non-causal, every query sits past the last key.
   const int offset = P.causal ? k_len - q_len : k_len;
-  // Keys [0, kend) cover every query of this wave's block; kend_wg every query
-  // of the work-group.
-  const int kend = active ? max(0, min(k_len, offset + min(j0 + kQTokens, q_len))) : 0;
-  const int kend_wg = max(0, min(k_len, offset + min(jw0 + qs * kQTokens, q_len)));
   const int32_t* bt_row = kPaged ? block_tables + static_cast<int64_t>(b) * P.bt_row_stride
                                  : nullptr;
   // Dense keys: rows past the sequence's last key would run off the tensor.
   const int64_t row_cap = kPaged ? INT64_MAX : static_cast<int64_t>(k_start) + max(k_len, 1) - 1;
+  float s2 = P.scale_log2;
+  if (kFp8 && P.k_scale) s2 *= P.k_scale[h];
+
+  // One query block of the work-group, start to finish (its own K/V stages).
+  auto process_block = [&](int qblk) {
+  const int jw0 = qblk * wg_tokens;  // first query of the work-group
+  const int j0 = jw0 + (wave / hw) * kQTokens;
+  // Waves without queries (past the chunk, or past the group) still stage.
+  const bool active = j0 < q_len && head < P.gqa && wave < qs * hw;
+  // Keys [0, kend) cover every query of this wave's block; kend_wg every query
+  // of the work-group.
+  const int kend = active ? max(0, min(k_len, offset + min(j0 + kQTokens, q_len))) : 0;
+  const int kend_wg = max(0, min(k_len, offset + min(jw0 + wg_tokens, q_len)));
 
   // Q^T operands: column r of block nb = query j0 + 16 nb + r.
   bf16x8_t qb[kColBlocks][4];
@@ -221,9 +249,6 @@ __global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_pre
       qb[nb][c] = __builtin_bit_cast(bf16x8_t, v);
     }
   }
-  float s2 = P.scale_log2;
-  if (kFp8 && P.k_scale) s2 *= P.k_scale[h];
-
   float m_run[kColBlocks], l_run[kColBlocks];
   floatx4_t o[kColBlocks][8];
 #pragma unroll
@@ -240,39 +265,47 @@ __global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_pre
   const int nfull = active ? max(0, min(kend, offset + j0 + 1)) / kTile : 0;
   const int nstages = (kend_wg + kStageKeys - 1) / kStageKeys;
 
-  // One 16-key tile: scores, online softmax per query column, P.V.  kMasked
-  // applies the causal / length / page mask; unmasked tiles skip it (every
-  // score is finite there, so the running max never stays -inf).
-  auto tile_step = [&](auto masked, int tok0, const TileRegs<kFp8>& cur, bool page_ok) {
+  // Two 16-key tiles (tiles tt, tt + 1 of `buf`, keys tok0 .. tok0 + 31):
+  // scores, one online-softmax update per query column for the 32 keys, P.V.
+  // kMasked applies the causal / length / page mask; unmasked pairs skip it
+  // (every score is finite there, so the running max never stays -inf).
+  // Updating the running max, the rescale test and the cross-lane row max once
+  // per 32 keys instead of per 16 halves that part of the VALU work, and the two
+  // tiles' score MFMAs form independent chains.  The V rows are read only after
+  // the scores of both column blocks are done, so K, the scores and V are never
+  // all live at once.
+  auto pair_step = [&](auto masked, int tok0, const uint8_t* buf, int tt, bool ok_a,
+                       bool ok_b) {
     constexpr bool kMasked = decltype(masked)::value;
-    uint4 kc[4];
-    k_chunks(cur, kc);
-    uint4 vr[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      vr[i] = (!kMasked || (page_ok && tok0 + 4 * g + i < kend)) ? v_row(cur, i)
-                                                                 : make_uint4(0, 0, 0, 0);
-    short4_t vb[8];  // shared by the column blocks
-    v_operands(vr, vb);
+    TileRegs<kFp8> ta, tb;
+    lds_tile_k<kFp8>(buf, tt, r, g, ta);
+    lds_tile_k<kFp8>(buf, tt + 1, r, g, tb);
+    uint4 ka[4], kb[4];
+    k_chunks(ta, ka);
+    k_chunks(tb, kb);
+    short4_t p_a[kColBlocks], p_b[kColBlocks];
 #pragma unroll
     for (int nb = 0; nb < kColBlocks; ++nb) {
-      const floatx4_t acc = qk_scores(kc, qb[nb]);
+      const floatx4_t acc_a = qk_scores(ka, qb[nb]);
+      const floatx4_t acc_b = qk_scores(kb, qb[nb]);
       const int j = j0 + 16 * nb + r;  // this lane's query column
       const int last = offset + j;     // its last visible key
-      float s[4];
-      float mt = kNegInf;
+      float s[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        s[i] = acc_a[i] * s2;
+        s[4 + i] = acc_b[i] * s2;
+      }
       if constexpr (kMasked) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int key = tok0 + 4 * g + i;
-          const bool ok = page_ok && j < q_len && key <= last && key < kend;
-          s[i] = ok ? acc[i] * s2 : kNegInf;
-          mt = fmaxf(mt, s[i]);
+        for (int i = 0; i < 8; ++i) {
+          const int key = tok0 + (i >> 2) * kTile + 4 * g + (i & 3);
+          const bool ok = ((i >> 2) ? ok_b : ok_a) && j < q_len && key <= last && key < kend;
+          s[i] = ok ? s[i] : kNegInf;
         }
-      } else {
-        // s2 > 0: the max of the scaled scores is the scaled max.
-        mt = fmaxf(fmaxf(acc[0], acc[1]), fmaxf(acc[2], acc[3])) * s2;
       }
+      float mt = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])),
+                       fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
       mt = pair_max(mt);
       // Lazy rescaling: the running max only moves when a score exceeds it by
       // more than kLazy (log2 units), so P <= 2^kLazy and the O/l rescale (a
@@ -288,12 +321,11 @@ __global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_pre
         m_use = m_new;  // finite
         alpha = m_new == m_run[nb] ? 1.f : __builtin_amdgcn_exp2f(m_run[nb] - m_new);
       }
-      float pr[4];
+      float pr[8];
       float psum = 0.f;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        pr[i] = kMasked ? __builtin_amdgcn_exp2f(s[i] - m_use)
-                        : __builtin_amdgcn_exp2f(__builtin_fmaf(acc[i], s2, -m_use));
+      for (int i = 0; i < 8; ++i) {
+        pr[i] = __builtin_amdgcn_exp2f(s[i] - m_use);
         psum += pr[i];
       }
       l_run[nb] = l_run[nb] * alpha + psum;
@@ -306,7 +338,29 @@ __global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_pre
           for (int d = 0; d < 8; ++d) o[nb][d][i] *= a;
         }
       }
-      pv_accumulate(o[nb], p_operand(pr), vb);
+      const float (&pa)[4] = *reinterpret_cast<const float(*)[4]>(&pr[0]);
+      const float (&pb)[4] = *reinterpret_cast<const float(*)[4]>(&pr[4]);
+      p_a[nb] = p_operand(pa);
+      p_b[nb] = p_operand(pb);
+    }
+    asm volatile("" ::: "memory");  // V reads stay after the score work
+    lds_tile_v<kFp8>(buf, tt, r, g, ta);
+    lds_tile_v<kFp8>(buf, tt + 1, r, g, tb);
+    uint4 vra[4], vrb[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      vra[i] = (!kMasked || (ok_a && tok0 + 4 * g + i < kend)) ? v_row(ta, i)
+                                                               : make_uint4(0, 0, 0, 0);
+      vrb[i] = (!kMasked || (ok_b && tok0 + kTile + 4 * g + i < kend)) ? v_row(tb, i)
+                                                                       : make_uint4(0, 0, 0, 0);
+    }
+    short4_t vba[8], vbb[8];  // shared by the column blocks
+    v_operands(vra, vba);
+    v_operands(vrb, vbb);
+#pragma unroll
+    for (int nb = 0; nb < kColBlocks; ++nb) {
+      pv_accumulate(o[nb], p_a[nb], vba);
+      pv_accumulate(o[nb], p_b[nb], vbb);
     }
   };
 
@@ -344,22 +398,23 @@ __global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_pre
       lds_dma16(src, buf_addr + 16 * pos0);
     }
   };
-  // Consumes one stage from `buf` (this wave's tiles only), every tile with the
-  // mask or every tile without it: one variant per loop body keeps the register
-  // count where two waves fit on a SIMD.
+  // Consumes one stage from `buf` (this wave's tiles only, two at a time; a pair
+  // whose second tile is past the wave's keys has those keys masked), every pair
+  // with the mask or every pair without it: one variant per loop body keeps the
+  // register count where two waves fit on a SIMD.
   auto stage_compute = [&](auto masked, int st, const uint8_t* buf) {
     // Not unrolled: unrolling lets the compiler hoist every tile's LDS reads
-    // (32 registers each) ahead of the first tile's math, and spill.
+    // (32 registers each) ahead of the first pair's math, and spill.
 #pragma unroll 1
-    for (int tt = 0; tt < kStageTiles; ++tt) {
+    for (int tt = 0; tt < kStageTiles; tt += 2) {
       const int t = st * kStageTiles + tt;
       if (t >= ntiles) break;  // wave-uniform; the rest of the stage is past this wave's keys
-      bool page_ok = true;
-      if constexpr (decltype(masked)::value && kPaged)
-        (void)key_row<kPaged>(P, bt_row, k_start, t * kTile, page_ok);
-      TileRegs<kFp8> cur;
-      lds_tile<kFp8>(buf, tt, r, g, cur);
-      tile_step(masked, t * kTile, cur, page_ok);
+      bool ok_a = true, ok_b = true;
+      if constexpr (decltype(masked)::value && kPaged) {
+        (void)key_row<kPaged>(P, bt_row, k_start, t * kTile, ok_a);
+        (void)key_row<kPaged>(P, bt_row, k_start, (t + 1) * kTile, ok_b);
+      }
+      pair_step(masked, t * kTile, buf, tt, ok_a, ok_b);
     }
   };
   // A stage needs no mask when this wave sees all its keys in full (below nfull)
@@ -394,7 +449,7 @@ __global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_pre
   for (; st < nstages && stage_unmasked(st); ++st) step(std::false_type{}, st);
 #pragma unroll 1
   for (; st < nstages; ++st) step(std::true_type{}, st);
-  if (!active) return;
+  if (!active) return;  // from process_block: this wave has no queries here
 
   const float vs = (kFp8 && P.v_scale) ? P.v_scale[h] : 1.f;
 #pragma unroll
@@ -417,6 +472,17 @@ __global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_pre
                                 static_cast<int64_t>(hq) * kHead + 8 * r) =
           make_uint4(w[0], w[1], w[2], w[3]);
     }
+  }
+  };
+  const int heavy = nqb - 1 - x;
+  // A loop rather than two calls: one copy of the block code (registers).
+#pragma unroll 1
+  for (int k = 0; k < 2; ++k) {
+    if (k == 1) {
+      if (!paired || x == heavy) break;  // unpaired, or the middle block of an odd count
+      __syncthreads();                   // every wave is done with the last stage buffer
+    }
+    process_block(k == 0 ? heavy : x);
   }
 }
 
@@ -497,8 +563,10 @@ int prefill_entry(const char* name, bool paged, void* out, int64_t out_row_strid
   P.scale_log2 = scale * kLog2e;
   P.causal = causal ? 1 : 0;
   const int hsplit = (gqa + hw - 1) / hw;
-  const dim3 grid(static_cast<unsigned>(qblocks), static_cast<unsigned>(num_kv_heads * hsplit),
-                  static_cast<unsigned>(batch));
+  FK_REQUIRE(qblocks <= 65535, "%s: max_seqlen_q %lld needs more than 65535 query blocks", name,
+             (long long)max_seqlen_q);
+  const dim3 grid(static_cast<unsigned>(num_kv_heads * hsplit), static_cast<unsigned>(batch),
+                  static_cast<unsigned>(qblocks));
   hipStream_t s = as_stream(stream);
   if (!paged)
     launch_prefill<false, false>(P, grid, nullptr, cu_seqlens_q, cu_seqlens_k, s);

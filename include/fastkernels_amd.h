@@ -209,9 +209,10 @@ int fk_store_kvcache_convert(const void* key, int64_t key_row_stride, const void
  * row b, layout as fk_paged_decode).  Query j of a chunk of q_len sees keys
  * [0, k_len - q_len + j] (causal, aligned to the end); a query with no visible key gets
  * zeros.  causal = 0 lets every query see all k_len keys (flash_attn causal=False).
- * max_seqlen_q bounds every chunk (it sizes the grid).  head_size 128; GQA
- * groups up to 16; kv dtype bf16 or fp8 e4m3fn (with k_scale / v_scale as in
- * fk_paged_decode).  No workspace; nothing is allocated. */
+ * max_seqlen_q bounds every chunk (it sizes the grid; at most 65535 blocks of 32
+ * query tokens, 128 for GQA group 1).  head_size 128; GQA groups up to 16; kv dtype
+ * bf16 or fp8 e4m3fn (with k_scale / v_scale as in fk_paged_decode).  No workspace;
+ * nothing is allocated. */
 int fk_paged_prefill(void* out, int64_t out_row_stride, const void* q, int64_t q_row_stride,
                      const void* k_cache, const void* v_cache, int kv_dtype, const float* k_scale,
                      const float* v_scale, const int32_t* block_tables, int64_t bt_row_stride,
