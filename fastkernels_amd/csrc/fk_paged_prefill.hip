@@ -171,6 +171,21 @@ __device__ __forceinline__ void lds_tile_v(const uint8_t* buf, int tt, int r, in
   }
 }
 
+// P.V operand of the 16-dim slice d of tile tt (bf16 stages), read with the LDS
+// transpose load: lane (r, g) gets V[keys 16 tt + 4g .. 16 tt + 4g + 3][dim
+// 16 d + r], the B-operand layout of the 16x16x16 MFMA, with no register
+// regrouping.  ds_read_b64_tr_b16 gives lane j of each 16-lane group, as its
+// element a, element j mod 4 of the 8 bytes addressed by lane 4a + j / 4; so
+// lane 4a + q addresses row 4g + a, dims 16d + 4q .. 16d + 4q + 3.
+__device__ __forceinline__ short4_t lds_v_slice(const uint8_t* buf, int tt, int d, int r, int g) {
+  using S = Stage<false>;
+  const int row = 16 * tt + 4 * g + (r >> 2);
+  const int q = r & 3;
+  const int off = S::offset(1, row, 2 * d + (q >> 1)) + 8 * (q & 1);
+  typedef __attribute__((address_space(3))) short4_t* lds_short4;
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4)(buf + off));
+}
+
 // Work-group = kPrefillWaves waves over one kv head: hw query heads of its group
 // times qs = kPrefillWaves / hw blocks of kQTokens query tokens (a group larger
 // than kPrefillWaves heads spans hsplit work-groups).  All waves share the K/V
@@ -344,19 +359,49 @@ __global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_pre
       p_b[nb] = p_operand(pb);
     }
     asm volatile("" ::: "memory");  // V reads stay after the score work
-    lds_tile_v<kFp8>(buf, tt, r, g, ta);
-    lds_tile_v<kFp8>(buf, tt + 1, r, g, tb);
-    uint4 vra[4], vrb[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      vra[i] = (!kMasked || (ok_a && tok0 + 4 * g + i < kend)) ? v_row(ta, i)
-                                                               : make_uint4(0, 0, 0, 0);
-      vrb[i] = (!kMasked || (ok_b && tok0 + kTile + 4 * g + i < kend)) ? v_row(tb, i)
-                                                                       : make_uint4(0, 0, 0, 0);
-    }
     short4_t vba[8], vbb[8];  // shared by the column blocks
-    v_operands(vra, vba);
-    v_operands(vrb, vbb);
+    if constexpr (!kFp8) {
+      // Slice d holds dims 16d .. 16d + 15 (lane r: dim 16d + r).
+#pragma unroll
+      for (int d = 0; d < 8; ++d) {
+        vba[d] = lds_v_slice(buf, tt, d, r, g);
+        vbb[d] = lds_v_slice(buf, tt + 1, d, r, g);
+      }
+      if constexpr (kMasked) {
+        // Keys past the wave's keys (or on a masked page) may hold anything:
+        // zero them so that P = 0 never meets a NaN.
+        uint32_t ma[2], mb[2];
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2) {
+          const int k0 = tok0 + 4 * g + 2 * h2;
+          ma[h2] = ((ok_a && k0 < kend) ? 0x0000ffffu : 0u) | ((ok_a && k0 + 1 < kend) ? 0xffff0000u : 0u);
+          mb[h2] = ((ok_b && k0 + kTile < kend) ? 0x0000ffffu : 0u) |
+                   ((ok_b && k0 + kTile + 1 < kend) ? 0xffff0000u : 0u);
+        }
+#pragma unroll
+        for (int d = 0; d < 8; ++d) {
+          uint2 wa = __builtin_bit_cast(uint2, vba[d]), wb = __builtin_bit_cast(uint2, vbb[d]);
+          wa.x &= ma[0]; wa.y &= ma[1];
+          wb.x &= mb[0]; wb.y &= mb[1];
+          vba[d] = __builtin_bit_cast(short4_t, wa);
+          vbb[d] = __builtin_bit_cast(short4_t, wb);
+        }
+      }
+    } else {
+      // Slice d holds dims 8r + d (lane r), regrouped from the row loads.
+      lds_tile_v<kFp8>(buf, tt, r, g, ta);
+      lds_tile_v<kFp8>(buf, tt + 1, r, g, tb);
+      uint4 vra[4], vrb[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        vra[i] = (!kMasked || (ok_a && tok0 + 4 * g + i < kend)) ? v_row(ta, i)
+                                                                 : make_uint4(0, 0, 0, 0);
+        vrb[i] = (!kMasked || (ok_b && tok0 + kTile + 4 * g + i < kend)) ? v_row(tb, i)
+                                                                         : make_uint4(0, 0, 0, 0);
+      }
+      v_operands(vra, vba);
+      v_operands(vrb, vbb);
+    }
 #pragma unroll
     for (int nb = 0; nb < kColBlocks; ++nb) {
       pv_accumulate(o[nb], p_a[nb], vba);
@@ -461,16 +506,24 @@ __global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_pre
       const float l = row_value<16>(l_col, g, i);
       if (jr >= q_len) continue;
       const float f = l > 0.f ? vs / l : 0.f;
-      uint32_t w[4];
+      uint16_t* orow = P.out + static_cast<int64_t>(q_start + jr) * P.out_row_stride +
+                       static_cast<int64_t>(hq) * kHead;
+      if constexpr (!kFp8) {
+        // o[nb][d] holds dim 16d + r: lanes r = 0..15 write 16 adjacent dims.
 #pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        const bf16x2_t pk = {static_cast<__bf16>(o[nb][2 * d][i] * f),
-                             static_cast<__bf16>(o[nb][2 * d + 1][i] * f)};
-        w[d] = __builtin_bit_cast(uint32_t, pk);
+        for (int d = 0; d < 8; ++d)
+          orow[16 * d + r] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(o[nb][d][i] * f));
+      } else {
+        // o[nb][d] holds dim 8r + d: eight adjacent dims per lane.
+        uint32_t w[4];
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          const bf16x2_t pk = {static_cast<__bf16>(o[nb][2 * d][i] * f),
+                               static_cast<__bf16>(o[nb][2 * d + 1][i] * f)};
+          w[d] = __builtin_bit_cast(uint32_t, pk);
+        }
+        *reinterpret_cast<uint4*>(orow + 8 * r) = make_uint4(w[0], w[1], w[2], w[3]);
       }
-      *reinterpret_cast<uint4*>(P.out + static_cast<int64_t>(q_start + jr) * P.out_row_stride +
-                                static_cast<int64_t>(hq) * kHead + 8 * r) =
-          make_uint4(w[0], w[1], w[2], w[3]);
     }
   }
   };
