@@ -402,10 +402,24 @@ __global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_pre
       v_operands(vra, vba);
       v_operands(vrb, vbb);
     }
+    // P.V over the 32 keys with the 16x16x32 MFMA (the 16x16x16 one takes as
+    // long on gfx950 for half the work).  Its k index 8g + e stands for key
+    // 4g + e of tile a (e < 4) and 4g + e - 4 of tile b (e >= 4): the A operand
+    // (P) and the B operand (V) both take tile a's four keys then tile b's, so
+    // the sum runs over the same 32 keys.
 #pragma unroll
     for (int nb = 0; nb < kColBlocks; ++nb) {
-      pv_accumulate(o[nb], p_a[nb], vba);
-      pv_accumulate(o[nb], p_b[nb], vbb);
+      const bf16x8_t pab = __builtin_bit_cast(
+          bf16x8_t, make_uint4(__builtin_bit_cast(uint2, p_a[nb]).x,
+                               __builtin_bit_cast(uint2, p_a[nb]).y,
+                               __builtin_bit_cast(uint2, p_b[nb]).x,
+                               __builtin_bit_cast(uint2, p_b[nb]).y));
+#pragma unroll
+      for (int d = 0; d < 8; ++d) {
+        const uint2 va = __builtin_bit_cast(uint2, vba[d]), vb = __builtin_bit_cast(uint2, vbb[d]);
+        const bf16x8_t v8 = __builtin_bit_cast(bf16x8_t, make_uint4(va.x, va.y, vb.x, vb.y));
+        o[nb][d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pab, v8, o[nb][d], 0, 0, 0);
+      }
     }
   };
 
