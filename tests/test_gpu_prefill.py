@@ -91,6 +91,28 @@ def test_paged_prefill_gqa(cuda, hq, hk):
     _close(_run(c), _oracle(c), 1e-2, f"gqa {hq}/{hk}")
 
 
+@pytest.mark.parametrize("hq,hk", [(16, 8), (24, 8)])
+def test_paged_prefill_small_groups(cuda, hq, hk):
+    """GQA 2 (each work-group's waves span two 32-query blocks of two heads) and GQA 3
+    (one of the four waves has no head: it only stages K/V), over chunks that pair
+    and chunks that do not."""
+    _flush(f"paged prefill small groups hq={hq} hk={hk}")
+    c = _case(cuda, [200, 70, 9], [200, 300, 9], hq=hq, hk=hk, bs=64, seed=75)
+    _close(_run(c), _oracle(c), 1e-2, f"gqa {hq}/{hk}")
+
+
+def test_paged_prefill_causal_pairing(cuda):
+    """Causal chunks with few cached keys before them pair query block n-1-p with p:
+    an odd block count (the middle block alone), an even one, a chunk on top of a
+    shorter cached prefix (still paired), one on top of a longer prefix (not paired),
+    and a block count of one."""
+    _flush("paged prefill causal pairing")
+    q_lens = [96, 128, 100, 100, 20]
+    k_lens = [96, 128, 150, 260, 20]
+    c = _case(cuda, q_lens, k_lens, bs=256, seed=76)
+    _close(_run(c), _oracle(c), 1e-2, "pairing")
+
+
 def test_paged_prefill_noncausal_and_empty_rows(cuda):
     """causal=False (every query sees all keys), a chunk longer than its context
     (leading rows see no key: zeros), and an empty chunk."""
