@@ -423,6 +423,42 @@ def bench_table(args):
         256 * 3 * 12288 * 2,
         (lambda: oracle.silu_and_mul(gun, "bf16"), 1.0, "oracle.silu_and_mul on the full input"))
 
+    # The C4 chain end to end, in the engine's order (LlamaDecoderLayer.forward,
+    # llama_decoder.py:34-42, without the GEMMs): add+RMSNorm -> rotary on q/k ->
+    # store_kvcache -> paged decode of the rotated q -> SiLU-and-mul; once as the
+    # separate ops, once with the store fused into the decode launch.
+    hc, rc = c4.hidden.clone(), c4.residual.clone()
+    qkv_c = c4.qkv.clone()
+    qc, kc_, vc_ = qkv_c[:, :4096], qkv_c[:, 4096:5120], qkv_c[:, 5120:]
+    dplan = ops.paged_decode_plan(256, 32, 8, 128, dec.max_seq_len, 0)
+    dws = torch.zeros(max(1, dplan.workspace_bytes), dtype=torch.uint8, device=dev)
+    dout = torch.empty(256, 32, 128, dtype=torch.bfloat16, device=dev)
+    act_c = torch.empty(256, 12288, dtype=torch.bfloat16, device=dev)
+
+    def chain(fused):
+        ops.fused_add_rms_norm(hc, rc, c4.norm_weight, 1e-6)
+        ops.rotary_embedding(c4.positions, qc, kc_, 128, rope.cos_sin_cache, True)
+        if fused:
+            ops.store_paged_decode(dout, qc.view(256, 32, 128), kc_.view(256, 8, 128),
+                                   vc_.view(256, 8, 128), dec.k_cache, dec.v_cache,
+                                   c4.slot_mapping, dec.block_tables, dec.ctx_lens, dec.scale,
+                                   dplan.part_tokens, dplan.max_parts, dws)
+        else:
+            ops.store_kvcache(kc_.view(256, 8, 128), vc_.view(256, 8, 128), dec.k_cache,
+                              dec.v_cache, c4.slot_mapping)
+            ops.paged_decode(dout, qc.view(256, 32, 128), dec.k_cache, dec.v_cache,
+                             dec.block_tables, dec.ctx_lens, dec.scale, dplan.part_tokens,
+                             dplan.max_parts, dws)
+        ops.silu_and_mul(act_c, gu)
+
+    chain_bytes = ((4 * 256 * 4096 + 4096) * 2 + 2 * 256 * 5120 * 2 + 256 * 8 + 256 * 128 * 4
+                   + 8 * 256 + 256 * 4 * 1024 * 2 + dec.algorithmic_bytes()
+                   + 256 * 3 * 12288 * 2)
+    add("C4", "chain: add+RMSNorm, rotary, store_kvcache, paged_decode, silu_and_mul "
+              "(separate launches)", lambda: chain(False), chain_bytes, iters=30)
+    add("C4", "chain with the store fused into the decode (store_paged_decode)",
+        lambda: chain(True), chain_bytes, iters=30)
+
     def decode_cpu(case, nseq):
         """Oracle on nseq sequences (shortest..longest spread) with their pages on the host."""
         ctx = case.ctx_lens.cpu().numpy().astype(np.int64)

@@ -35,10 +35,6 @@
 // cross-lane dot-product reductions, two row-swap permutes per tile for the max).
 #include "fk_attn_tile.h"
 
-#ifndef FK_DECODE_PIPE
-#define FK_DECODE_PIPE 0
-#endif
-
 namespace fk {
 namespace {
 
@@ -311,6 +307,8 @@ struct WaveState {
     const int ntiles = (tok_end - tok_begin + kTile - 1) / kTile;
     // Issues the loads of tiles t0 .. t0+U-1 into `buf` (unconditional; tiles
     // past the end re-read the last tile, which hits in cache).
+    // Issues the loads of tiles t0 .. t0+U-1 into `buf` (unconditional; tiles
+    // past the end re-read the last tile, which hits in cache).
     auto fetch = [&](int t0, TileRegs<kFp8>(&buf)[U], int64_t(&pg)[U]) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
@@ -320,7 +318,9 @@ struct WaveState {
         if constexpr (kStore) {
           // Fused when b's slot is that of position ctx - 1: in this tile's page
           // (a tile never spans pages), at offset (ctx - 1) mod block_size.
-          // Branch-free (selects), so the load sequence stays one block.
+          // Branch-free (selects), so the load sequence stays one block.  (Peeling
+          // the last chunk, the only one that can hold ctx - 1, out of the loop
+          // measured no faster.)
           const int64_t want = (pg[u] << P.block_size_log2) +
                                ((ctx - 1) & ((1 << P.block_size_log2) - 1));
           const bool hit = tok0 == ftok0 && pg[u] >= 0 && slot_value(P, sw) == want;
@@ -335,18 +335,6 @@ struct WaveState {
         if (t0 + u < ntiles) process(tok_begin + kTile * (t0 + u), pg[u], buf[u]);
       }
     };
-#if FK_DECODE_PIPE
-    // Two register sets of U tiles: one is consumed while the other is in flight.
-    TileRegs<kFp8> bufA[U], bufB[U];
-    int64_t pgA[U], pgB[U];
-    fetch(0, bufA, pgA);
-    for (int t0 = 0; t0 < ntiles; t0 += 2 * U) {
-      fetch(t0 + U, bufB, pgB);
-      consume(t0, bufA, pgA);
-      fetch(t0 + 2 * U, bufA, pgA);
-      consume(t0 + U, bufB, pgB);
-    }
-#else
     // Chunks of U tiles: issue all U tiles' loads, then consume them in order
     // (the compiler waits for tile u with vmcnt = loads issued after it).
     for (int t0 = 0; t0 < ntiles; t0 += U) {
@@ -355,7 +343,6 @@ struct WaveState {
       fetch(t0, buf, pg);
       consume(t0, buf, pg);
     }
-#endif
     // Column sums of l over the 4 lane groups: every lane of column j holds l_j.
     l_run = pair_sum(l_run);
     // The wave that streamed position ctx - 1 writes b's row: at that position
@@ -642,8 +629,7 @@ __global__ __launch_bounds__(kMergeWaves * 64) void paged_decode_balanced_reduce
   merge_rows(orow, P.part_o, P.part_ml, first, 2 * hk * P.gqa, w1 - w0 + 1, first_alt);
 }
 
-// Tuning knobs (compile-time): tiles per load set, and whether two sets are
-// double-buffered (FK_DECODE_PIPE=1) or one set is loaded then consumed.
+// Tuning knob (compile-time): tiles per load set.
 #ifndef FK_DECODE_CHUNK
 #define FK_DECODE_CHUNK 2
 #endif
