@@ -436,7 +436,23 @@ __global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_pre
   // reads the logical chunk that the swizzle puts there.  Rows of a masked page
   // (-1 table entry) read page 0 and rows past a dense tensor's end re-read its
   // last row; the consumer masks both.
+  // All lanes of load i fall in one tile of the stage (a load covers 64 chunks,
+  // 4 rows of bf16 or 8 of fp8, and the positions are 64-aligned), so its
+  // source address is a wave-uniform part (that tile's first row) plus a
+  // per-lane part that does not change from stage to stage, computed once here.
   const int64_t head_off = static_cast<int64_t>(h) * kHead * (kFp8 ? 1 : 2);
+  constexpr int kStageChunks = kStageKeys * S::kChunks;  // chunks of K (or V) per stage
+  uint32_t lane_off[S::kLoads];
+#pragma unroll
+  for (int i = 0; i < S::kLoads; ++i) {
+    const int pos0 = 64 * (kPrefillWaves * i + wave);
+    const int which = pos0 / kStageChunks;
+    const int rel = pos0 + lane - which * kStageChunks;
+    const int row = rel / S::kChunks;
+    const int q = (rel - row * S::kChunks) ^ (row & (S::kChunks - 1));
+    const int64_t rb = which ? P.v_row_bytes : P.k_row_bytes;
+    lane_off[i] = static_cast<uint32_t>((row & 15) * rb + head_off + 16 * q);
+  }
   auto stage_load = [&](int st, uint8_t* buf) {
     const uint32_t buf_addr = lds_addr_of(buf);
     // First rows of the stage's tiles: page lookups once per tile, wave-uniform.
@@ -449,18 +465,24 @@ __global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_pre
 #pragma unroll
     for (int i = 0; i < S::kLoads; ++i) {
       const int pos0 = 64 * (kPrefillWaves * i + wave);  // wave-uniform
-      const int pos = pos0 + lane;
-      const int which = pos0 / (kStageKeys * S::kChunks);  // 0: K, 1: V
-      const int rem = pos - which * kStageKeys * S::kChunks;
-      const int row = rem / S::kChunks;
-      const int q = (rem - row * S::kChunks) ^ (row & (S::kChunks - 1));
-      int64_t base = row0[0];
+      const int which = pos0 / kStageChunks;              // 0: K, 1: V
+      const int tt = ((pos0 - which * kStageChunks) / S::kChunks) >> 4;
+      int64_t first = row0[0];
 #pragma unroll
-      for (int tt = 1; tt < kStageTiles; ++tt)
-        if ((row >> 4) == tt) base = row0[tt];
-      const int64_t grow = min(base + (row & 15), row_cap);
-      const uint8_t* src = (which ? P.v_cache : P.k_cache) +
-                           grow * (which ? P.v_row_bytes : P.k_row_bytes) + head_off + 16 * q;
+      for (int u = 1; u < kStageTiles; ++u)
+        if (tt == u) first = row0[u];
+      const int64_t rb = which ? P.v_row_bytes : P.k_row_bytes;
+      const uint8_t* base = which ? P.v_cache : P.k_cache;
+      const uint8_t* src;
+      if (kPaged || first + 15 <= row_cap) {
+        src = base + first * rb + lane_off[i];
+      } else {
+        // Dense keys whose tile runs past the tensor's end: clamp each row.
+        const int rel = pos0 + lane - which * kStageChunks;
+        const int row = rel / S::kChunks;
+        const int q = (rel - row * S::kChunks) ^ (row & (S::kChunks - 1));
+        src = base + min(first + (row & 15), row_cap) * rb + head_off + 16 * q;
+      }
       lds_dma16(src, buf_addr + 16 * pos0);
     }
   };
