@@ -106,6 +106,46 @@ def time_call(fn, iters=50, warmup=10, flush=None):
     return statistics.median(ms), statistics.fmean(ms)
 
 
+ROTATE_BYTES = 512 * 1024 * 1024  # twice the 256 MB MALL
+
+
+def time_rotated(fns, iters=20, warmup=3):
+    """µs per call of fns run back to back inside one captured HIP graph, median of
+    `iters` replays.  Each fn works on its own inputs, and together they touch more
+    than the MALL holds (ROTATE_BYTES), so every call reads its inputs from HBM, as
+    after a flush; the graph removes the host's launch overhead and the per-call
+    event pair, which dominate a single timed call of a few-µs kernel.  This is the
+    setting of a graph-replayed engine step (engine.py:5386-5428)."""
+    import torch
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for fn in fns:
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for fn in fns:
+            fn()
+    for _ in range(warmup):
+        graph.replay()
+    starts, ends = _events(iters), _events(iters)
+    for i in range(iters):
+        starts[i].record()
+        graph.replay()
+        ends[i].record()
+    torch.cuda.synchronize()
+    ms = statistics.median(s.elapsed_time(e) for s, e in zip(starts, ends))
+    del graph
+    return ms * 1e3 / len(fns)
+
+
+def copies_for(footprint: int) -> int:
+    """Input sets needed so that one pass over them touches ROTATE_BYTES."""
+    return max(2, -(-ROTATE_BYTES // max(1, footprint)))
+
+
 # ---------------------------------------------------------------------------
 # CPU baseline: the oracle (numpy restatement of the reference's torch path)
 # ---------------------------------------------------------------------------
@@ -317,8 +357,21 @@ def bench_table(args):
     rows = []
     settle_clocks(lambda: flush.sum())
 
-    def add(cfg, op, fn, nbytes, cpu=None, iters=50):
-        """cpu = (callable, fraction of the op's bytes it processes, sample text) or None."""
+    def verdict(out, ref, tags, bitexact=None):
+        """The reference bench's acceptance status of out against the oracle's ref
+        (oracle.compare: 99% of elements within the dtype's atol/rtol)."""
+        st, max_abs, max_rel, matched, _ = oracle.compare(out, ref, tags)
+        v = {"status": st, "max_abs": float(f"{max_abs:.3g}"), "max_rel": float(f"{max_rel:.3g}"),
+             "matched": round(matched, 5)}
+        if bitexact is not None:
+            v["bitexact"] = bool(bitexact)
+        return v
+
+    def add(cfg, op, fn, nbytes, cpu=None, iters=50, parity=None, rotated=None):
+        """cpu = (callable, fraction of the op's bytes it processes, sample text) or None;
+        parity = a callable giving verdict(...) for one call on fresh inputs, or None;
+        rotated = a callable giving the per-input-set calls for time_rotated, or None
+        (run last: it may write the op's outputs many times over)."""
         med, mean = time_call(fn, iters=iters, warmup=5, flush=flush)
         row = {"config": cfg, "op": op, "us_median": round(med * 1e3, 2),
                "us_mean": round(mean * 1e3, 2), "bytes": nbytes,
@@ -330,6 +383,16 @@ def bench_table(args):
             row["cpu"] = {"us_per_call": round(sec / frac * 1e6, 1),
                           "GBs": round(nbytes * frac / sec / 1e9, 3), "cores": cores,
                           "kind": "port", "sample": f"{sample}; median of {reps}"}
+        if parity is not None:
+            row["parity"] = parity()
+        if rotated is not None:
+            fns = rotated()
+            us = time_rotated(fns)
+            row["graph"] = {"us_per_call": round(us, 2), "copies": len(fns),
+                            "GBs": round(nbytes / (us * 1e-6) / 1e9, 1),
+                            "frac_of_8TBs": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+            del fns
+            torch.cuda.empty_cache()
         rows.append(row)
         print(json.dumps(row), file=sys.stderr, flush=True)
 
@@ -338,13 +401,49 @@ def bench_table(args):
     c1f = workloads.c1_norm("cpu", dtype=torch.float32)
     x1, r1, w1 = c1f.x.numpy(), c1f.residual.numpy(), c1f.weight.numpy()
     x, r = c1.x.clone(), c1.residual.clone()
+    def norm_copies(x0, r0, w):
+        sets = [(x0.clone(), r0.clone()) for _ in range(copies_for(4 * x0.numel() * 2))]
+        return [lambda xx=xx, rx=rx: ops.fused_add_rms_norm(xx, rx, w, 1e-6) for xx, rx in sets]
+
+    def norm_parity(case):
+        xx, rx = case.x.clone() if hasattr(case, "x") else case.hidden.clone(), case.residual.clone()
+        w = case.weight if hasattr(case, "weight") else case.norm_weight
+        x0, r0 = _np(xx), _np(rx)
+        ops.fused_add_rms_norm(xx, rx, w, 1e-6)
+        ref = oracle.rms_norm(x0, _np(w), 1e-6, "bf16", residual=r0)
+        return verdict((_np(xx), _np(rx)), ref, "bf16")
+
     add("C1", "fused_add_rmsnorm bf16 [256,1024]",
         lambda: ops.fused_add_rms_norm(x, r, c1.weight, c1.eps), (4 * 256 * 1024 + 1024) * 2,
         (lambda: oracle.rms_norm(x1, w1, 1e-6, "f32", residual=r1), 2.0,
-         "oracle.rms_norm fp32 on the full [256,1024] (4,198,400 B; GB/s on the fp32 bytes)"))
+         "oracle.rms_norm fp32 on the full [256,1024] (4,198,400 B; GB/s on the fp32 bytes)"),
+        parity=lambda: norm_parity(c1), rotated=lambda: norm_copies(c1.x, c1.residual, c1.weight))
     # C2: store_kvcache (bit copy); CPU: in-place numpy scatter into full-size caches.
     c2 = workloads.c2_store(dev)
     nvalid = int((c2.slot_mapping >= 0).sum().item())
+
+    def store_copies(key, value, kc, vc, valid_frac):
+        """Input sets of fresh rows and slots (a new draw of distinct slots per set, the
+        same share of -1) into the given caches."""
+        n = key.shape[0]
+        row = key[0].numel() * key.element_size()
+        g = torch.Generator().manual_seed(workloads.SEED + 99)
+        sets = []
+        for _ in range(copies_for(n * row * 4)):
+            sl = torch.randperm(kc.shape[0] * kc.shape[1], generator=g)[:n]
+            sl[torch.rand(n, generator=g) >= valid_frac] = -1
+            sets.append((torch.randn(key.shape, generator=g).to(key.dtype).to(dev),
+                         torch.randn(key.shape, generator=g).to(key.dtype).to(dev), sl.to(dev)))
+        return [lambda k_=k_, v_=v_, s_=s_: ops.store_kvcache(k_, v_, kc, vc, s_)
+                for k_, v_, s_ in sets]
+
+    def store_parity(kc, vc, ek, ev):
+        """Whole caches against the oracle's (which the CPU leg has just filled)."""
+        gk, gv = kc.view(torch.int16).cpu().numpy(), vc.view(torch.int16).cpu().numpy()
+        exact = np.array_equal(gk, ek) and np.array_equal(gv, ev)
+        bf = lambda a: oracle.bf16_bits_to_f32(a.view(np.uint16).reshape(-1))
+        return verdict((bf(gk), bf(gv)), (bf(ek), bf(ev)), "bf16", bitexact=exact)
+
     k2 = c2.key.view(torch.int16).cpu().numpy()
     v2 = c2.value.view(torch.int16).cpu().numpy()
     s2 = c2.slot_mapping.cpu().numpy()
@@ -354,7 +453,9 @@ def bench_table(args):
         lambda: ops.store_kvcache(c2.key, c2.value, c2.k_cache, c2.v_cache, c2.slot_mapping),
         8 * 4096 + nvalid * 4 * 8 * 128 * 2,
         (lambda: oracle.store_kvcache_(k2, v2, kc2, vc2, s2), 1.0,
-         "oracle.store_kvcache_ (numpy scatter) on the full C2 inputs and caches"))
+         "oracle.store_kvcache_ (numpy scatter) on the full C2 inputs and caches"),
+        parity=lambda: store_parity(c2.k_cache, c2.v_cache, kc2, vc2),
+        rotated=lambda: store_copies(c2.key, c2.value, c2.k_cache, c2.v_cache, nvalid / 4096))
     del c2, kc2, vc2
     # C4 chain ops
     c4 = workloads.c4_chain(dev)
@@ -363,18 +464,33 @@ def bench_table(args):
     add("C4", "fused_add_rmsnorm bf16 [256,4096]",
         lambda: ops.fused_add_rms_norm(h, rr, c4.norm_weight, 1e-6), (4 * 256 * 4096 + 4096) * 2,
         (lambda: oracle.rms_norm(hn, wn, 1e-6, "bf16", residual=rn), 1.0,
-         "oracle.rms_norm (bf16 rounding points) on the full [256,4096]"))
+         "oracle.rms_norm (bf16 rounding points) on the full [256,4096]"),
+        parity=lambda: norm_parity(c4),
+        rotated=lambda: norm_copies(c4.hidden, c4.residual, c4.norm_weight))
     from fastkernels_amd.candidate.L1.rotary_emb import RotaryEmbedding
 
     rope = RotaryEmbedding(128, c4.max_position, c4.rope_theta).to(dev)
     qkv = c4.qkv.clone()
     q, k = qkv[:, :4096], qkv[:, 4096:5120]
     qn, kn, pn, csn = _np(q), _np(k), c4.positions.cpu().numpy(), _np(rope.cos_sin_cache)
+
+    def rope_copies():
+        sets = [c4.qkv.clone() for _ in range(copies_for(2 * 256 * 5120 * 2))]
+        return [lambda t=t: ops.rotary_embedding(c4.positions, t[:, :4096], t[:, 4096:5120], 128,
+                                                 rope.cos_sin_cache, True) for t in sets]
+
+    def rope_parity():
+        qkv_p = c4.qkv.clone()
+        qp, kp = qkv_p[:, :4096], qkv_p[:, 4096:5120]
+        ref = oracle.rotary(pn, _np(qp), _np(kp), 128, csn, True, "bf16")
+        ops.rotary_embedding(c4.positions, qp, kp, 128, rope.cos_sin_cache, True)
+        return verdict((_np(qp), _np(kp)), ref, "bf16")
+
     add("C4", "rotary q[256,32x128] k[256,8x128]",
         lambda: ops.rotary_embedding(c4.positions, q, k, 128, rope.cos_sin_cache, True),
         2 * 256 * 5120 * 2 + 256 * 8 + 256 * 128 * 4,
         (lambda: oracle.rotary(pn, qn, kn, 128, csn, True, "bf16"), 1.0,
-         "oracle.rotary NeoX on the full q/k"))
+         "oracle.rotary NeoX on the full q/k"), parity=rope_parity, rotated=rope_copies)
     v = qkv[:, 5120:]
     dec = c4.decode
     # Qwen3 attention prologue at C4: per-head q/k RMSNorm + rotary + store_kvcache,
@@ -409,19 +525,39 @@ def bench_table(args):
     kn16 = k.contiguous().view(torch.int16).view(256, 8, 128).cpu().numpy()
     vn16 = v.contiguous().view(torch.int16).view(256, 8, 128).cpu().numpy()
     sn = c4.slot_mapping.cpu().numpy()
+
+    # scratch caches for the rotated C4 store (the decode case's caches stay as they are)
+    scratch_kc = torch.zeros(1024, 256, 8, 128, dtype=torch.bfloat16, device=dev)
+    scratch_vc = torch.zeros_like(scratch_kc)
+
+    def store_rows_parity():
+        """The cache rows at the C4 slots against the stored key/value rows."""
+        kc_ = dec.k_cache.view(-1, 8 * 128)[c4.slot_mapping].view(torch.int16).cpu().numpy()
+        vc_ = dec.v_cache.view(-1, 8 * 128)[c4.slot_mapping].view(torch.int16).cpu().numpy()
+        ek = k.contiguous().view(torch.int16).reshape(256, -1).cpu().numpy()
+        ev = v.contiguous().view(torch.int16).reshape(256, -1).cpu().numpy()
+        exact = np.array_equal(kc_, ek) and np.array_equal(vc_, ev)
+        bf = lambda a: oracle.bf16_bits_to_f32(a.view(np.uint16))
+        return verdict((bf(kc_), bf(vc_)), (bf(ek), bf(ev)), "bf16", bitexact=exact)
     cache_np = np.zeros((dec.k_cache.shape[0],) + tuple(dec.k_cache.shape[1:]), np.int16)
     add("C4", "store_kvcache [256,8,128]",
         lambda: ops.store_kvcache(k.view(256, 8, 128), v.view(256, 8, 128), dec.k_cache,
                                   dec.v_cache, c4.slot_mapping), 8 * 256 + 256 * 4 * 1024 * 2,
         (lambda: oracle.store_kvcache_(kn16, vn16, cache_np, cache_np, sn), 1.0,
-         "oracle.store_kvcache_ on the full C4 tokens"))
-    del cache_np
+         "oracle.store_kvcache_ on the full C4 tokens"), parity=store_rows_parity,
+        rotated=lambda: store_copies(k.view(256, 8, 128), v.view(256, 8, 128), scratch_kc,
+                                     scratch_vc, 1.0))
+    del cache_np, scratch_kc, scratch_vc
     gu = c4.gate_up
     gun = _np(gu)
     act = torch.empty(256, 12288, dtype=torch.bfloat16, device=dev)
     add("C4", "silu_and_mul [256,2x12288]", lambda: ops.silu_and_mul(act, gu),
         256 * 3 * 12288 * 2,
-        (lambda: oracle.silu_and_mul(gun, "bf16"), 1.0, "oracle.silu_and_mul on the full input"))
+        (lambda: oracle.silu_and_mul(gun, "bf16"), 1.0, "oracle.silu_and_mul on the full input"),
+        parity=lambda: verdict(_np(act), oracle.silu_and_mul(gun, "bf16"), "bf16"),
+        rotated=lambda: [lambda x_=x_, o_=o_: ops.silu_and_mul(o_, x_) for x_, o_ in
+                         [(gu.clone(), torch.empty_like(act))
+                          for _ in range(copies_for(256 * 3 * 12288 * 2))]])
 
     # The C4 chain end to end, in the engine's order (LlamaDecoderLayer.forward,
     # llama_decoder.py:34-42, without the GEMMs): add+RMSNorm -> rotary on q/k ->
@@ -482,13 +618,23 @@ def bench_table(args):
         vs = None if case.v_scale is None else case.v_scale.cpu().numpy()
 
         def run():
-            for i, n, kp, vp in data:
+            return pick, np.concatenate([
                 oracle.paged_decode(qh[i:i + 1], kp, vp, np.arange(kp.shape[0])[None],
-                                    np.array([n]), case.scale, ks, vs)
+                                    np.array([n]), case.scale, ks, vs) for i, n, kp, vp in data])
 
         frac = sum(n for _, n, _, _ in data) / float(ctx.sum())
         return (run, frac, f"oracle.paged_decode on {len(pick)} of {len(ctx)} sequences "
                            f"({frac * 100:.1f}% of the cached tokens), scaled to the batch")
+
+    decode_refs = {}
+
+    def decode_parity(name, out, cpu):
+        """The oracle's rows for the sampled sequences (computed once per configuration)
+        against the same rows of the GPU output, rounded to bf16 as the baseline's."""
+        if name not in decode_refs:
+            decode_refs[name] = cpu[0]()
+        pick, ref = decode_refs[name]
+        return verdict(_np(out)[pick], oracle.round_to(ref, "bf16"), "bf16")
 
     for t, hh in ((64, 32), (8192, 32)):
         g = torch.Generator().manual_seed(workloads.SEED)
@@ -503,10 +649,19 @@ def bench_table(args):
             ops.merge_attn_states(mo, po, pl, so, sl, ml),
             3 * t * hh * 128 * 2 + 3 * hh * t * 4,
             (lambda arrs=arrs: oracle.merge_attn_states(*arrs, "bf16"), 1.0,
-             "oracle.merge_attn_states on the full input"))
+             "oracle.merge_attn_states on the full input"),
+            parity=lambda mo=mo, ml=ml, arrs=arrs: verdict(
+                (_np(mo), _np(ml)), oracle.merge_attn_states(*arrs, "bf16"), ["bf16", "f32"]),
+            rotated=(lambda po=po, pl=pl, so=so, sl=sl, t=t, hh=hh: [
+                lambda a=a: ops.merge_attn_states(*a) for a in [
+                    (torch.empty_like(po), po.clone(), pl.clone(), so.clone(), sl.clone(),
+                     torch.empty_like(pl))
+                    for _ in range(copies_for(3 * t * hh * 128 * 2 + 3 * hh * t * 4))]])
+            if t <= 1024 else None)
 
     c3 = workloads.c3_decode(dev)
     c5 = workloads.c5_fp8_decode(dev)
+    cpu_legs = {}
     for name, case, splits, nseq in (("C4", dec, 0, 4), ("C3", c3, 0, 4), ("C5", c5, 0, 1),
                                      ("C5", c5, 16, 0), ("C5", c5, 32, 0), ("C5", c5, 64, 0)):
         b, hq, d = case.q.shape
@@ -514,12 +669,15 @@ def bench_table(args):
         part, nparts, wsb = ops.paged_decode_plan(b, hq, hk, d, case.max_seq_len, splits)
         ws = torch.zeros(max(1, wsb), dtype=torch.uint8, device=dev)
         out = torch.empty_like(case.q)
+        if nseq:
+            cpu_legs[name] = decode_cpu(case, nseq)
         add(name, f"paged_decode {str(case.k_cache.dtype).replace('torch.', '')} B={b} Hq={hq} "
                   f"{'balanced' if part == 0 else f'{nparts} partitions'}",
             lambda: ops.paged_decode(out, case.q, case.k_cache, case.v_cache, case.block_tables,
                                      case.ctx_lens, case.scale, part, nparts, ws, case.k_scale,
                                      case.v_scale), case.algorithmic_bytes(),
-            decode_cpu(case, nseq) if nseq else None, iters=30)
+            cpu_legs[name] if nseq else None, iters=30,
+            parity=lambda name=name, out=out: decode_parity(name, out, cpu_legs[name]))
     # Prefill (FlashAttnPrefill with a block table) at Qwen3-8B heads, with torch's
     # own SDPA (flash backend, dense contiguous K/V) on the same GPU beside it.
     def prefill_case(q_lens, k_lens, seed):

@@ -411,3 +411,98 @@ def silu_and_mul(x: np.ndarray, dtype: str) -> np.ndarray:
     g = x[..., :d].astype(np.float64)
     act = round_to((g / (1.0 + np.exp(-g))).astype(np.float32), dtype)
     return round_to(act * x[..., d:], dtype)
+
+
+# ---------------------------------------------------------------------------
+# Acceptance rule of the reference's bench: candidate output vs baseline output,
+# fastkernels/bench.py:141-155 (tolerances), :172-178 (statuses), :1824-1896
+# (_tensor_leaves, _compare_tensor, _compare)
+# ---------------------------------------------------------------------------
+PASSED = "PASSED"
+INCORRECT_NUMERICAL = "INCORRECT_NUMERICAL"
+INCORRECT_SHAPE = "INCORRECT_SHAPE"
+INCORRECT_DTYPE = "INCORRECT_DTYPE"
+SKIPPED = "SKIPPED"
+
+REQUIRED_MATCHED_RATIO = 0.99
+# (atol, rtol) by the reference tensor's dtype; fp8 outputs use (0.125, 0.125).
+TOLERANCES = {"f32": (1e-5, 1e-3), "f64": (1e-5, 1e-3), "f16": (1e-2, 1e-2),
+              "bf16": (1e-2, 1e-2), "fp8": (0.125, 0.125)}
+DEFAULT_TOL = (1e-2, 1e-2)
+
+
+def leaves(obj) -> list:
+    """Array leaves of a nested tuple / list / dict (dict values in order); anything
+    that is not an array (None, ints, strings) is dropped, as _tensor_leaves does."""
+    if isinstance(obj, np.ndarray):
+        return [obj]
+    if isinstance(obj, (list, tuple)):
+        return [t for x in obj for t in leaves(x)]
+    if isinstance(obj, dict):
+        return [t for v in obj.values() for t in leaves(v)]
+    return []
+
+
+def _norm32(x: np.ndarray) -> float:
+    return float(np.sqrt(np.sum(np.square(x, dtype=np.float32), dtype=np.float32)))
+
+
+def compare_tensor(out: np.ndarray, ref: np.ndarray, ref_dtype: str):
+    """(ok, max_abs, max_rel, matched_ratio, detail) for one output, values compared in
+    float32.  An element matches when |out - ref| <= atol + rtol * |ref| (and is
+    finite); the output passes when at least REQUIRED_MATCHED_RATIO of its elements
+    match.  NaN or Inf anywhere, or an all-zero output against a nonzero reference,
+    fails outright."""
+    atol, rtol = TOLERANCES.get(ref_dtype, DEFAULT_TOL)
+    x = np.asarray(out, np.float32)
+    y = np.asarray(ref, np.float32)
+    inf = float("inf")
+    if np.isnan(x).any() or np.isnan(y).any():
+        return False, inf, inf, 0.0, "NaN in output"
+    if np.isinf(x).any() or np.isinf(y).any():
+        return False, inf, inf, 0.0, "Inf in output"
+    ref_norm = _norm32(y)
+    if ref_norm > 0 and _norm32(x) == 0:
+        return False, ref_norm, ref_norm, 0.0, "output is all-zeros"
+    if x.size == 0:
+        return True, 0.0, 0.0, 1.0, ""
+    abs_err = np.abs(x - y)
+    max_abs = float(abs_err.max())
+    exceed = (abs_err > atol + rtol * np.abs(y)) | ~np.isfinite(abs_err)
+    matched = 1.0 - float(exceed.sum()) / exceed.size
+    max_rel = float((abs_err / np.maximum(np.abs(y), np.float32(atol))).max())
+    ok = matched >= REQUIRED_MATCHED_RATIO
+    detail = "" if ok else f"only {matched:.4f} within atol={atol},rtol={rtol}"
+    return ok, max_abs, max_rel, matched, detail
+
+
+def compare(out, ref, ref_dtypes, out_dtypes=None, check_dtype: bool = True):
+    """(status, max_abs, max_rel, matched_ratio, detail) for a candidate's outputs
+    against the baseline's.  ``out`` and ``ref`` are arrays or nested tuples / lists /
+    dicts of arrays (values); ``ref_dtypes`` / ``out_dtypes`` give each leaf's dtype
+    tag (one tag for all leaves, or a list; ``out_dtypes`` defaults to ``ref_dtypes``).
+    A reference whose nonempty leaves are all zero is SKIPPED (it cannot tell a
+    stub from a kernel); otherwise leaves are compared in order and the first
+    failing one decides."""
+    o, r = leaves(out), leaves(ref)
+    inf = float("inf")
+    if len(o) != len(r):
+        return INCORRECT_SHAPE, inf, inf, 0.0, f"output tensor count {len(o)} != {len(r)}"
+    rd = [ref_dtypes] * len(r) if isinstance(ref_dtypes, str) else list(ref_dtypes)
+    od = rd if out_dtypes is None else (
+        [out_dtypes] * len(o) if isinstance(out_dtypes, str) else list(out_dtypes))
+    nonempty = [x for x in r if x.size > 0]
+    if nonempty and all(_norm32(np.asarray(x, np.float32)) == 0 for x in nonempty):
+        return SKIPPED, 0.0, 0.0, 0.0, "skip: reference output is all-zeros"
+    worst, max_abs, max_rel = 1.0, 0.0, 0.0
+    for x, y, tx, ty in zip(o, r, od, rd):
+        if tuple(x.shape) != tuple(y.shape):
+            return INCORRECT_SHAPE, inf, inf, 0.0, f"shape {tuple(x.shape)} != {tuple(y.shape)}"
+        if check_dtype and tx != ty:
+            return INCORRECT_DTYPE, inf, inf, 0.0, f"dtype {tx} != {ty}"
+        ok, a, rl, matched, detail = compare_tensor(x, y, ty)
+        max_abs, max_rel = max(max_abs, a), max(max_rel, rl)
+        worst = min(worst, matched)
+        if not ok:
+            return INCORRECT_NUMERICAL, max_abs, max_rel, worst, detail
+    return PASSED, max_abs, max_rel, worst, ""

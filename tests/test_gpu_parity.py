@@ -402,6 +402,51 @@ def test_paged_decode_fp8_c5(cuda):
     assert_close(f32(out16), got, FP8_TOL, FP8_TOL, "C5 16 vs 64 partitions")
 
 
+@pytest.mark.parametrize("kv_dtype", [torch.bfloat16, torch.float8_e4m3fn])
+@pytest.mark.parametrize("num_splits", [0, 5])
+def test_candidate_decode_reference_harness_inputs(cuda, kv_dtype, num_splits):
+    """FlashAttnDecode on inputs built as the reference bench builds a paged decode's:
+    random caches, then ``_fix_paged_decode`` (page ids drawn with repetition, so
+    sequences share pages and a page may recur within one; lengths up to the
+    table's reach).  Judged by the reference's acceptance rule against the oracle
+    rounded to the output dtype (PASSED), and by this suite's per-element bar."""
+    from fastkernels_amd.candidate.L1.flash_attn_decode import FlashAttnDecode
+
+    _flush(f"candidate decode, harness inputs {kv_dtype} splits={num_splits}")
+    fp8 = kv_dtype == torch.float8_e4m3fn
+    g = torch.Generator().manual_seed(43 + num_splits)
+    b, hq, hk, d, nb, bs, width = 12, 32, 8, 128, 20, 64, 14
+    q = torch.randn(b, hq, d, generator=g).to(torch.bfloat16).to(cuda)
+    k = torch.randn(nb, bs, hk, d, generator=g).to(cuda)
+    v = torch.randn(nb, bs, hk, d, generator=g).to(cuda)
+    scales = {}
+    if fp8:
+        ks = (0.01 + 0.09 * torch.rand(hk, generator=g)).to(cuda)
+        vs = (0.01 + 0.09 * torch.rand(hk, generator=g)).to(cuda)
+        k, v = workloads.quantize_fp8(k, ks), workloads.quantize_fp8(v, vs)  # as C5
+        scales = {"k_scale": ks, "v_scale": vs}
+    else:
+        k, v = k.to(torch.bfloat16), v.to(torch.bfloat16)
+    kw = {"k_cache": k, "v_cache": v, "block_table": torch.zeros(b, width, dtype=torch.int32),
+          "cache_seqlens": torch.zeros(b, dtype=torch.int32), "max_seq_len": 0}
+    workloads.fix_paged_decode(kw, generator=g, page_dim=1)
+    bt = kw["block_table"].cpu().numpy()
+    assert any(len(set(row.tolist())) < width for row in bt)  # pages recur within a sequence
+    mod = FlashAttnDecode(hq, hk, d, page_size=bs)
+    out = mod(q, k, v, kw["cache_seqlens"], block_table=kw["block_table"],
+              max_seq_len=kw["max_seq_len"], softmax_scale=d ** -0.5, causal=True,
+              num_splits=num_splits, **scales)
+    torch.cuda.synchronize()
+    raw = (lambda t: t.view(torch.uint8).cpu().numpy()) if fp8 else f32
+    ref = oracle.paged_decode(f32(q), raw(k), raw(v), bt, kw["cache_seqlens"].cpu().numpy(),
+                              d ** -0.5, *(s.cpu().numpy() for s in scales.values()))
+    got = f32(out)
+    status, max_abs, _, matched, detail = oracle.compare(got, oracle.round_to(ref, "bf16"), "bf16")
+    assert status == oracle.PASSED, (status, max_abs, matched, detail)
+    tol = FP8_TOL if fp8 else BF16_TOL
+    assert_close(got, ref, tol, tol, "harness inputs")
+
+
 # ---------------------------------------------------------------------------
 # Candidate classes (drop-in surface) and the C4 chain
 # ---------------------------------------------------------------------------
