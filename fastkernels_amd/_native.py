@@ -42,25 +42,26 @@ _SIGNATURES = {
                                      ctypes.POINTER(c_int64)]),
     "fk_paged_decode": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_int,
                                 c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_int,
-                                c_int, c_int, c_int, c_int64, c_float, c_int64, c_int64,
-                                c_void_p, c_int64, c_void_p]),
+                                c_int, c_int, c_int, c_int64, c_float, c_int, c_void_p,
+                                c_int64, c_int64, c_void_p, c_int64, c_void_p]),
     "fk_paged_decode_partials": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p,
                                          c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_int64,
                                          c_void_p, c_int64, c_int, c_int, c_int, c_int, c_int64,
-                                         c_float, c_int64, c_int64, c_void_p, c_int64,
-                                         c_void_p]),
+                                         c_float, c_int, c_void_p, c_int64, c_int64, c_void_p,
+                                         c_int64, c_void_p]),
     "fk_paged_decode_reduce": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p,
                                        c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_int64,
                                        c_void_p, c_int64, c_int, c_int, c_int, c_int, c_int64,
-                                       c_float, c_int64, c_int64, c_void_p, c_int64,
-                                       c_void_p]),
+                                       c_float, c_int, c_void_p, c_int64, c_int64, c_void_p,
+                                       c_int64, c_void_p]),
     "fk_silu_and_mul": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_int64, c_int64, c_int,
                                 c_void_p]),
     "fk_store_paged_decode": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64,
                                       c_void_p, c_int64, c_void_p, c_int, c_void_p, c_void_p,
                                       c_int, c_void_p, c_void_p, c_void_p, c_int64, c_void_p,
                                       c_int64, c_int, c_int, c_int, c_int, c_int64, c_float,
-                                      c_int64, c_int64, c_void_p, c_int64, c_void_p]),
+                                      c_int, c_void_p, c_int64, c_int64, c_void_p, c_int64,
+                                      c_void_p]),
     "fk_qk_norm_rope_store": (c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_void_p,
                                       c_int64, c_void_p, c_void_p, c_float, c_void_p, c_int,
                                       c_int64, c_int, c_int, c_void_p, c_void_p, c_void_p, c_int,

@@ -4,8 +4,19 @@ Same constructor ``(num_heads, num_kv_heads, head_dim, page_size=None)`` and
 ``forward(q, k_cache, v_cache, cache_seqlens=None, **kwargs)`` with the kwargs
 the reference forwards to ``flash_attn_varlen_func`` (flash_attn_decode.py:
 113-181): ``block_table``, ``max_seq_len``, ``softmax_scale``, ``causal``
-(decode: every cached key is visible), ``num_splits``, ``out``.  Returns
+(decode: every cached key is visible), ``num_splits``, ``out``,
+``window_size`` (default: the ``_window_size`` attribute that
+``Attention.__init__`` sets, attention_impl.py:242-244, :282; ``(left, right)``
+with left >= 0 keeps the last left + 1 keys) and ``s_aux`` (attention-sink
+logits, one per query head, attention_impl.py:401-406).  Returns
 ``[B, num_heads, head_dim]`` in q's dtype.
+
+The engine's FA3 hooks work unchanged: ``preallocate(max_batch_size, device)``
+(engine.py:1545), the shared ``_cu_seqlens_q`` / ``_sched_buf`` / ``_sched_meta``
+attributes it copies between grouped ops, ``_force_graph_splits``, and
+``update_scheduler_metadata``.  ``fa_version`` is None, so the engine's
+scheduler refresh (fa_utils.py:120-145) skips this op: its schedule is computed
+on the device from the lengths of each call.
 
 The gfx950 kernel is split-context flash-decoding.  By default
 (``num_splits`` 0) the 16-token tiles of all sequences are cut into equal
@@ -56,13 +67,25 @@ class FlashAttnDecode(nn.Module):
         self.head_dim = head_dim
         self.page_size = page_size
         self._workspace: torch.Tensor | None = None
+        # Attributes the reference's engine reads or shares between grouped decode
+        # ops (engine.py:1538-1550, fa_utils.py:108-145, jamba_engine.py:719-856).
+        self.fa_version = None
+        self._cu_seqlens_q: torch.Tensor | None = None
+        self._sched_buf: torch.Tensor | None = None
+        self._sched_meta: torch.Tensor | None = None
+        self._graph_num_splits = 32
+        self._force_graph_splits = False
+        self._window_size = (-1, -1)
+        self._qkv_dtype = torch.bfloat16
+        self._sinks_src = None  # (tensor, version) of the cached float32 s_aux copy
+        self._sinks_f32: torch.Tensor | None = None
 
     def _get_workspace(self, nbytes: int, device: torch.device) -> torch.Tensor | None:
         if nbytes <= 0:
             return None
         ws = self._workspace
         if ws is None or ws.device != device or ws.numel() < nbytes:
-            if torch.cuda.is_current_stream_capturing():
+            if device.type == "cuda" and torch.cuda.is_current_stream_capturing():
                 raise RuntimeError(
                     "FlashAttnDecode: split-context workspace must be allocated before graph "
                     f"capture ({nbytes} bytes needed); call preallocate() or run eagerly once")
@@ -70,12 +93,59 @@ class FlashAttnDecode(nn.Module):
             self._workspace = ws
         return ws
 
-    def preallocate(self, max_batch_size: int, max_seq_len: int, device: torch.device,
-                    num_splits: int = 0) -> None:
-        """Allocate the workspace for batches up to max_batch_size (outside capture)."""
+    def preallocate(self, max_batch_size: int, device: torch.device,
+                    max_seq_len: int | None = None, num_splits: int = 0) -> None:
+        """Allocate graph-stable buffers for batches up to max_batch_size, outside
+        capture: the reference's signature (flash_attn_decode.py:97-111, called at
+        engine.py:1545).  The default (length-balanced) schedule's workspace does not
+        depend on the context lengths; a fixed ``num_splits`` also needs the
+        ``max_seq_len`` bound."""
+        device = torch.device(device)
+        if self._cu_seqlens_q is None or self._cu_seqlens_q.numel() < max_batch_size + 1:
+            self._cu_seqlens_q = torch.arange(max_batch_size + 1, dtype=torch.int32,
+                                              device=device)
+        if num_splits and max_seq_len is None:
+            raise ValueError("FlashAttnDecode.preallocate: num_splits needs max_seq_len")
         plan = ops.paged_decode_plan(max_batch_size, self.num_heads, self.num_kv_heads,
-                                     self.head_dim, max_seq_len, num_splits)
-        self._get_workspace(plan.workspace_bytes, torch.device(device))
+                                     self.head_dim, int(max_seq_len or 1), num_splits)
+        self._get_workspace(plan.workspace_bytes, device)
+
+    def update_scheduler_metadata(self, cache_seqlens: torch.Tensor, max_seqlen_k: int,
+                                  qkv_dtype: torch.dtype | None = None,
+                                  window_size: tuple[int, int] = (-1, -1),
+                                  max_seqlen_q: int = 1) -> None:
+        """The reference recomputes FA3 tile-scheduler metadata here
+        (flash_attn_decode.py:50-95).  The gfx950 kernel reads the lengths on the
+        device at every call, so only the window and dtype are recorded."""
+        if qkv_dtype is not None:
+            self._qkv_dtype = qkv_dtype
+        self._window_size = tuple(window_size)
+        self._sched_meta = None
+
+    def _sinks(self, s_aux, device) -> torch.Tensor | None:
+        """s_aux as contiguous float32 [num_heads] on the device; the copy is kept
+        while the source tensor is unchanged (the layer passes the same sinks
+        parameter every step), so a decode step makes no conversion."""
+        if s_aux is None:
+            return None
+        if not isinstance(s_aux, torch.Tensor):
+            raise TypeError("FlashAttnDecode: s_aux must be a tensor of num_heads logits")
+        if s_aux.numel() != self.num_heads:
+            raise ValueError(f"FlashAttnDecode: s_aux must have {self.num_heads} entries")
+        if s_aux.dtype == torch.float32 and s_aux.is_contiguous() and s_aux.device == device:
+            return s_aux.reshape(-1)
+        if device.type != "cuda":
+            return s_aux.detach().to(device=device, dtype=torch.float32).reshape(-1)
+        key = (s_aux, s_aux._version)
+        src = self._sinks_src
+        if self._sinks_f32 is None or src is None or src[0] is not s_aux or src[1] != key[1] \
+                or self._sinks_f32.device != device:
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError("FlashAttnDecode: convert s_aux to float32 before graph "
+                                   "capture (run the step eagerly once)")
+            self._sinks_f32 = s_aux.detach().to(device=device, dtype=torch.float32).reshape(-1)
+            self._sinks_src = key
+        return self._sinks_f32
 
     @staticmethod
     def _scale_vec(s, hk: int, device) -> torch.Tensor | None:
@@ -100,15 +170,16 @@ class FlashAttnDecode(nn.Module):
         out = kwargs.pop("out", None)
         k_scale = kwargs.pop("k_scale", kwargs.pop("k_descale", None))
         v_scale = kwargs.pop("v_scale", kwargs.pop("v_descale", None))
-        window = kwargs.pop("window_size", (-1, -1))
+        window = kwargs.pop("window_size", None)
+        if window is None:
+            window = self._window_size
         s_aux = kwargs.pop("s_aux", None)
         kwargs.pop("scheduler_metadata", None)
-        if window is not None and tuple(window) != (-1, -1):
-            raise NotImplementedError("FlashAttnDecode (gfx950): sliding window is not supported")
-        if s_aux is not None:
-            raise NotImplementedError("FlashAttnDecode (gfx950): attention sinks are not supported")
+        # A decode query is the last token, so only the left extent matters.
+        window_left = int(window[0]) if window is not None and int(window[0]) >= 0 else -1
         if kwargs:
             raise TypeError(f"FlashAttnDecode: unexpected arguments {sorted(kwargs)}")
+        sinks = self._sinks(s_aux, q.device)
         if block_table is None or cache_seqlens is None:
             raise ValueError("FlashAttnDecode: block_table and cache_seqlens are required")
 
@@ -133,7 +204,8 @@ class FlashAttnDecode(nn.Module):
             out = torch.empty((b, self.num_heads, self.head_dim), dtype=q.dtype, device=q.device)
         return dict(out=out, block_table=block_table, cache_seqlens=cache_seqlens,
                     softmax_scale=float(softmax_scale), part_tokens=plan.part_tokens,
-                    max_parts=plan.max_parts, ws=ws, k_scale=k_scale, v_scale=v_scale)
+                    max_parts=plan.max_parts, ws=ws, k_scale=k_scale, v_scale=v_scale,
+                    window_left=window_left, sinks=sinks)
 
     def forward(self, q, k_cache, v_cache, cache_seqlens=None, **kwargs):
         a = self._launch_args(q, k_cache, cache_seqlens, kwargs)
@@ -143,7 +215,8 @@ class FlashAttnDecode(nn.Module):
         call = torch.ops.fastkernels_amd.paged_decode if torch.compiler.is_compiling() \
             else ops.paged_decode
         call(out3, q3, k_cache, v_cache, a["block_table"], a["cache_seqlens"], a["softmax_scale"],
-             a["part_tokens"], a["max_parts"], a["ws"], a["k_scale"], a["v_scale"])
+             a["part_tokens"], a["max_parts"], a["ws"], a["k_scale"], a["v_scale"],
+             a["window_left"], a["sinks"])
         return a["out"]
 
     def forward_store(self, q, key, value, k_cache, v_cache, slot_mapping, cache_seqlens=None,
@@ -169,12 +242,12 @@ class FlashAttnDecode(nn.Module):
             out3 = a["out"].view(b, self.num_heads, self.head_dim)
             ops.paged_decode(out3, q3, k_cache, v_cache, a["block_table"], a["cache_seqlens"],
                              a["softmax_scale"], a["part_tokens"], a["max_parts"], a["ws"],
-                             a["k_scale"], a["v_scale"])
+                             a["k_scale"], a["v_scale"], a["window_left"], a["sinks"])
             return a["out"]
         out3 = a["out"].view(b, self.num_heads, self.head_dim)
         call = torch.ops.fastkernels_amd.store_paged_decode if torch.compiler.is_compiling() \
             else ops.store_paged_decode
         call(out3, q3, k3, v3, k_cache, v_cache, slot_mapping, a["block_table"],
              a["cache_seqlens"], a["softmax_scale"], a["part_tokens"], a["max_parts"], a["ws"],
-             a["k_scale"], a["v_scale"])
+             a["k_scale"], a["v_scale"], a["window_left"], a["sinks"])
         return a["out"]

@@ -1,8 +1,16 @@
 // Paged decode attention for MI355X (gfx950): split-context ("flash-decoding")
 // with GQA-packed MFMA tiles and a length-balanced schedule.
 //
-// Semantics (one query token per sequence, all cached keys visible):
-//   out[b, hq] = sum_t softmax_t(scale * q[b,hq] . K[b,t]) V[b,t],  t < ctx_lens[b]
+// Semantics (one query token per sequence, at position ctx_lens[b] - 1):
+//   out[b, hq] = sum_t softmax_t(scale * q[b,hq] . K[b,t]) V[b,t],  lo_b <= t < ctx_lens[b]
+// with lo_b = 0, or ctx_lens[b] - 1 - window_left under a sliding window
+// (window_size = (window_left, 0): keys [q_pos - window_left, q_pos], the
+// SLIDING_WINDOW = 1 + window_size[0] mask of triton_unified_attention.py:
+// 577-590).  Optional attention sinks (s_aux, one logit per query head, in
+// the units of scale * q . k) join the softmax's denominator only, once per
+// row: out = sum_t e^(s_t - m) V_t / (sum_t e^(s_t - m) + e^(sink - m)), as
+// init_softmax_M seeds M = sink, L = 1 (infra/triton_attention_helpers.py)
+// and reduce_segments adds it once across segments.
 // K/V rows of sequence b are gathered through block_tables[b, t / block_size]
 // from NHD pages [num_blocks, block_size, Hk, D]; kv head = hq / (Hq/Hk).  This is
 // FlashAttnDecode.forward (fastkernels/tasks/baseline/L1/flash_attn_decode.py:
@@ -62,6 +70,8 @@ struct DecodeParams {
   int32_t* tile_off; // balanced schedule: [batch + 1] tile prefix sums, then range size
   int batch;
   int num_groups;    // balanced schedule: work-groups per kv-head group
+  int window_left;   // sliding window: keys >= ctx - 1 - window_left (-1: none)
+  const float* sinks;  // attention sink logits [num_heads] fp32, or nullptr
   // Fused store (fk_store_paged_decode); new_k == nullptr for a plain decode.
   // Row b of new_k / new_v (cache element type, heads contiguous) is sequence
   // b's new token, stored at slot slot_mapping[b] (skipped when out of range).
@@ -84,6 +94,23 @@ __device__ __forceinline__ int64_t page_of(const DecodeParams& P, const int32_t*
   if (idx >= P.bt_row_stride) return -1;
   const int64_t page = bt[b * P.bt_row_stride + idx];
   return (page >= 0 && page < P.num_blocks) ? page : -1;
+}
+
+// First visible key of a sequence of ctx tokens under the sliding window.
+__device__ __forceinline__ int key_lo(const DecodeParams& P, int ctx) {
+  return P.window_left >= 0 ? max(0, ctx - 1 - P.window_left) : 0;
+}
+
+// Sink logit of query head hq in the kernel's log2 units (scale * q . k
+// scaled by log2(e)), or -inf without sinks.
+__device__ __forceinline__ float sink_log2(const DecodeParams& P, int hq) {
+  return P.sinks ? P.sinks[hq] * kLog2e : kNegInf;
+}
+
+// Softmax denominator of a row with running (max m, sum l) once the sink
+// joins it: l + 2^(sink - m); a row with no visible key (l = 0) stays 0.
+__device__ __forceinline__ float with_sink(float l, float m, float sink2) {
+  return (l > 0.f && sink2 != kNegInf) ? l + __builtin_amdgcn_exp2f(sink2 - m) : l;
 }
 
 // Issues the loads of one tile from page `page` (>= 0, < num_blocks).  Loads
@@ -219,9 +246,11 @@ struct WaveState {
   // read from sequence b's new row instead of the cache (load_tile's row j),
   // and the row (one 16-byte chunk per lane, loaded up front) is written to the
   // cache after the loop, so no load waits for the store.
+  // Keys below key_lo (the sliding window's start) are masked; tok_begin is
+  // the start of the tile holding key_lo or later.
   __device__ __forceinline__ void run(const DecodeParams& P, const int32_t* __restrict__ bt,
                                       const void* __restrict__ sm, int b, int h, int tok_begin,
-                                      int tok_end, int ctx, int r, int g) {
+                                      int tok_end, int ctx, int key_lo, int r, int g) {
     const int gqa = P.gqa;
     SlotWords sw{-1, -1};
     uint4 new_chunk = make_uint4(0, 0, 0, 0);  // this lane's chunk of b's new row
@@ -267,7 +296,8 @@ struct WaveState {
       float mt = kNegInf;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const bool ok = head_ok && page >= 0 && (tok0 + 4 * g + i < tok_end);
+        const int tok = tok0 + 4 * g + i;
+        const bool ok = head_ok && page >= 0 && tok < tok_end && tok >= key_lo;
         s[i] = ok ? acc[i] * s2 : kNegInf;
         mt = fmaxf(mt, s[i]);
       }
@@ -300,7 +330,9 @@ struct WaveState {
       uint4 vr[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        vr[i] = (page >= 0 && tok0 + 4 * g + i < tok_end) ? v_row(cur, i) : make_uint4(0, 0, 0, 0);
+        vr[i] = (page >= 0 && tok0 + 4 * g + i < tok_end && tok0 + 4 * g + i >= key_lo)
+                    ? v_row(cur, i)
+                    : make_uint4(0, 0, 0, 0);
       pv_accumulate(o, pa, vr);
     };
 
@@ -362,7 +394,8 @@ struct WaveState {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int j = 4 * g + i;
-      const float l = row_value<kG>(l_run, g, i);
+      float l = row_value<kG>(l_run, g, i);
+      if (P.sinks) l = with_sink(l, row_value<kG>(m_run, g, i), sink_log2(P, h * P.gqa + (j < P.gqa ? j : 0)));
       if (j >= kG || j >= P.gqa) continue;
       const float f = l > 0.f ? vs / l : 0.f;
       uint32_t w[4];
@@ -424,8 +457,13 @@ __global__ __launch_bounds__(NH * 64) void paged_decode_partition_kernel(
     const int nparts = min((ctx + P.part_tokens - 1) / P.part_tokens, P.max_parts);
     const int r = lane & 15;
     const int g = lane >> 4;
+    // Under a sliding window a partition starts no earlier than the tile of the
+    // window's first key; one wholly before it streams nothing and leaves an
+    // empty partial (max -inf, sum 0).
+    const int lo = key_lo(P, ctx);
     WaveState<kG, kFp8, U, kStore> st;
-    st.run(P, block_tables, slot_mapping, b, h, tok_begin, tok_end, ctx, r, g);
+    st.run(P, block_tables, slot_mapping, b, h, max(tok_begin, lo & ~(kTile - 1)), tok_end, ctx,
+           lo, r, g);
     if (nparts == 1) {
       st.write_final(P, b, h, r, g);
     } else {
@@ -443,7 +481,11 @@ __global__ __launch_bounds__(NH * 64) void paged_decode_partition_kernel(
   }
 }
 
-__device__ __forceinline__ int tiles_of(int ctx) { return ctx > 0 ? (ctx + kTile - 1) / kTile : 0; }
+// Tiles a sequence of ctx tokens streams: from the tile of its first visible
+// key (the sliding window's start) to the end.
+__device__ __forceinline__ int tiles_of(const DecodeParams& P, int ctx) {
+  return ctx > 0 ? (ctx + kTile - 1) / kTile - key_lo(P, ctx) / kTile : 0;
+}
 
 // Balanced schedule: work-group w (of num_groups per kv-head group) takes
 // tiles [w * S, (w+1) * S) of the concatenation of all sequences' tiles,
@@ -462,7 +504,7 @@ __global__ __launch_bounds__(NH * 64) void paged_decode_balanced_kernel(
     int carry = 0;
     for (int base = 0; base < batch; base += 64) {
       const int i = base + lane;
-      int v = i < batch ? tiles_of(ctx_lens[i]) : 0;
+      int v = i < batch ? tiles_of(P, ctx_lens[i]) : 0;
 #pragma unroll
       for (int off = 1; off < 64; off <<= 1) {
         const int y = __shfl_up(v, off, 64);
@@ -500,8 +542,10 @@ __global__ __launch_bounds__(NH * 64) void paged_decode_balanced_kernel(
       const int s_hi = min(t_hi, toff[b + 1]) - toff[b];
       if (s_hi <= s_lo) continue;  // empty sequence
       const int ctx = ctx_lens[b];
-      st.run(P, block_tables, slot_mapping, b, h, kTile * s_lo, min(ctx, kTile * s_hi), ctx, r,
-             g);
+      const int lo = key_lo(P, ctx);
+      const int t_first = lo / kTile;  // the sequence's tile s is its tile t_first + s
+      st.run(P, block_tables, slot_mapping, b, h, kTile * (t_first + s_lo),
+             min(ctx, kTile * (t_first + s_hi)), ctx, lo, r, g);
       if (toff[b] >= t_lo && toff[b + 1] <= t_hi) {
         st.write_final(P, b, h, r, g);
       } else {
@@ -532,7 +576,8 @@ __global__ __launch_bounds__(NH * 64) void paged_decode_balanced_kernel(
 constexpr int kMergeWaves = 4;
 __device__ __forceinline__ void merge_rows(uint16_t* orow, const float* part_o,
                                            const float* part_ml, int64_t first_row,
-                                           int64_t row_stride, int nrows, int64_t alt_first_row) {
+                                           int64_t row_stride, int nrows, int64_t alt_first_row,
+                                           float sink2) {
   __shared__ float red_ml[kMergeWaves][2];
   __shared__ float2 red_o[kMergeWaves][64];
   const int lane = threadIdx.x & 63;
@@ -574,6 +619,7 @@ __device__ __forceinline__ void merge_rows(uint16_t* orow, const float* part_o,
       a1 += ov.y * f;
     }
   }
+  Lt = with_sink(Lt, Mt, sink2);  // the sink joins the merged row once
   const float inv = Lt > 0.f ? 1.f / Lt : 0.f;
   const bf16x2_t pk = {static_cast<__bf16>(a0 * inv), static_cast<__bf16>(a1 * inv)};
   reinterpret_cast<uint32_t*>(orow)[lane] = __builtin_bit_cast(uint32_t, pk);
@@ -597,7 +643,7 @@ __global__ __launch_bounds__(kMergeWaves * 64) void paged_decode_partition_reduc
   const int h = hq / P.gqa;
   const int j = hq - h * P.gqa;
   const int64_t first = (static_cast<int64_t>(b) * P.num_kv_heads + h) * P.max_parts * P.gqa + j;
-  merge_rows(orow, P.part_o, P.part_ml, first, P.gqa, nparts, first);
+  merge_rows(orow, P.part_o, P.part_ml, first, P.gqa, nparts, first, sink_log2(P, hq));
 }
 
 // Balanced schedule: merge sequences cut across work-groups; zero empty ones.
@@ -626,7 +672,8 @@ __global__ __launch_bounds__(kMergeWaves * 64) void paged_decode_balanced_reduce
   const int slot0 = t0 > w0 * S ? 1 : 0;
   const int64_t first_alt = ((static_cast<int64_t>(w0) * 2 + slot0) * hk + h) * P.gqa + j;
   const int64_t first = ((static_cast<int64_t>(w0) * 2 + 0) * hk + h) * P.gqa + j;
-  merge_rows(orow, P.part_o, P.part_ml, first, 2 * hk * P.gqa, w1 - w0 + 1, first_alt);
+  merge_rows(orow, P.part_o, P.part_ml, first, 2 * hk * P.gqa, w1 - w0 + 1, first_alt,
+             sink_log2(P, hq));
 }
 
 // Tuning knob (compile-time): tiles per load set.
@@ -712,9 +759,12 @@ int prepare(const char* name, Launch& L, void* out, int64_t out_row_stride, cons
             const float* k_scale, const float* v_scale, const int32_t* block_tables,
             int64_t bt_row_stride, const int32_t* ctx_lens, int64_t batch, int num_heads,
             int num_kv_heads, int head_size, int block_size, int64_t num_blocks, float scale,
-            int64_t part_tokens, int64_t max_parts, void* workspace, int64_t ws_bytes) {
+            int window_left, const float* sinks, int64_t part_tokens, int64_t max_parts,
+            void* workspace, int64_t ws_bytes) {
   int rc = validate(name, batch, num_heads, num_kv_heads, head_size, part_tokens, max_parts);
   if (rc != FK_OK) return rc;
+  FK_REQUIRE(window_left >= -1, "%s: window_left %d must be -1 (no window) or >= 0", name,
+             window_left);
   FK_REQUIRE(block_size >= kTile && (block_size & (block_size - 1)) == 0,
              "%s: block_size %d must be a power of two >= 16", name, block_size);
   FK_REQUIRE(kv_dtype == FK_DTYPE_BF16 || kv_dtype == FK_DTYPE_FP8_E4M3FN,
@@ -758,6 +808,8 @@ int prepare(const char* name, Launch& L, void* out, int64_t out_row_stride, cons
   P.scale_log2 = scale * kLog2e;
   P.batch = static_cast<int>(batch);
   P.num_groups = static_cast<int>(max_parts);
+  P.window_left = window_left;
+  P.sinks = sinks;
   P.new_k = nullptr;
   P.new_v = nullptr;
   P.new_k_stride = P.new_v_stride = 0;
@@ -862,13 +914,13 @@ extern "C" int fk_paged_decode_partials(
     const void* v_cache, int kv_dtype, const float* k_scale, const float* v_scale,
     const int32_t* block_tables, int64_t bt_row_stride, const int32_t* ctx_lens, int64_t batch,
     int num_heads, int num_kv_heads, int head_size, int block_size, int64_t num_blocks,
-    float scale, int64_t part_tokens, int64_t max_parts, void* workspace, int64_t ws_bytes,
-    void* stream) {
+    float scale, int window_left, const float* sinks, int64_t part_tokens, int64_t max_parts,
+    void* workspace, int64_t ws_bytes, void* stream) {
   Launch L;
   int rc = prepare("fk_paged_decode_partials", L, out, out_row_stride, q, q_row_stride, k_cache,
                    v_cache, kv_dtype, k_scale, v_scale, block_tables, bt_row_stride, ctx_lens,
                    batch, num_heads, num_kv_heads, head_size, block_size, num_blocks, scale,
-                   part_tokens, max_parts, workspace, ws_bytes);
+                   window_left, sinks, part_tokens, max_parts, workspace, ws_bytes);
   if (rc != FK_OK || batch == 0) return rc;
   hipStream_t s = as_stream(stream);
   if (L.P.gqa <= 4)
@@ -885,13 +937,13 @@ extern "C" int fk_paged_decode_reduce(
     const void* v_cache, int kv_dtype, const float* k_scale, const float* v_scale,
     const int32_t* block_tables, int64_t bt_row_stride, const int32_t* ctx_lens, int64_t batch,
     int num_heads, int num_kv_heads, int head_size, int block_size, int64_t num_blocks,
-    float scale, int64_t part_tokens, int64_t max_parts, void* workspace, int64_t ws_bytes,
-    void* stream) {
+    float scale, int window_left, const float* sinks, int64_t part_tokens, int64_t max_parts,
+    void* workspace, int64_t ws_bytes, void* stream) {
   Launch L;
   int rc = prepare("fk_paged_decode_reduce", L, out, out_row_stride, q, q_row_stride, k_cache,
                    v_cache, kv_dtype, k_scale, v_scale, block_tables, bt_row_stride, ctx_lens,
                    batch, num_heads, num_kv_heads, head_size, block_size, num_blocks, scale,
-                   part_tokens, max_parts, workspace, ws_bytes);
+                   window_left, sinks, part_tokens, max_parts, workspace, ws_bytes);
   if (rc != FK_OK || batch == 0) return rc;
   const dim3 grid(static_cast<unsigned>(num_heads), static_cast<unsigned>(batch));
   if (L.balanced)
@@ -909,19 +961,20 @@ extern "C" int fk_paged_decode(void* out, int64_t out_row_stride, const void* q,
                                const int32_t* block_tables, int64_t bt_row_stride,
                                const int32_t* ctx_lens, int64_t batch, int num_heads,
                                int num_kv_heads, int head_size, int block_size,
-                               int64_t num_blocks, float scale, int64_t part_tokens,
-                               int64_t max_parts, void* workspace, int64_t ws_bytes,
-                               void* stream) {
+                               int64_t num_blocks, float scale, int window_left,
+                               const float* sinks, int64_t part_tokens, int64_t max_parts,
+                               void* workspace, int64_t ws_bytes, void* stream) {
   int rc = fk_paged_decode_partials(out, out_row_stride, q, q_row_stride, k_cache, v_cache,
                                     kv_dtype, k_scale, v_scale, block_tables, bt_row_stride,
                                     ctx_lens, batch, num_heads, num_kv_heads, head_size,
-                                    block_size, num_blocks, scale, part_tokens, max_parts,
-                                    workspace, ws_bytes, stream);
+                                    block_size, num_blocks, scale, window_left, sinks,
+                                    part_tokens, max_parts, workspace, ws_bytes, stream);
   if (rc != FK_OK) return rc;
   return fk_paged_decode_reduce(out, out_row_stride, q, q_row_stride, k_cache, v_cache, kv_dtype,
                                 k_scale, v_scale, block_tables, bt_row_stride, ctx_lens, batch,
                                 num_heads, num_kv_heads, head_size, block_size, num_blocks, scale,
-                                part_tokens, max_parts, workspace, ws_bytes, stream);
+                                window_left, sinks, part_tokens, max_parts, workspace, ws_bytes,
+                                stream);
 }
 
 extern "C" int fk_store_paged_decode(
@@ -930,14 +983,14 @@ extern "C" int fk_store_paged_decode(
     int slot_is_i64, void* k_cache, void* v_cache, int kv_dtype, const float* k_scale,
     const float* v_scale, const int32_t* block_tables, int64_t bt_row_stride,
     const int32_t* ctx_lens, int64_t batch, int num_heads, int num_kv_heads, int head_size,
-    int block_size, int64_t num_blocks, float scale, int64_t part_tokens, int64_t max_parts,
-    void* workspace, int64_t ws_bytes, void* stream) {
+    int block_size, int64_t num_blocks, float scale, int window_left, const float* sinks,
+    int64_t part_tokens, int64_t max_parts, void* workspace, int64_t ws_bytes, void* stream) {
   const char* name = "fk_store_paged_decode";
   Launch L;
   int rc = prepare(name, L, out, out_row_stride, q, q_row_stride, k_cache, v_cache, kv_dtype,
                    k_scale, v_scale, block_tables, bt_row_stride, ctx_lens, batch, num_heads,
-                   num_kv_heads, head_size, block_size, num_blocks, scale, part_tokens, max_parts,
-                   workspace, ws_bytes);
+                   num_kv_heads, head_size, block_size, num_blocks, scale, window_left, sinks,
+                   part_tokens, max_parts, workspace, ws_bytes);
   if (rc != FK_OK) return rc;
   const int64_t elem = kv_dtype == FK_DTYPE_FP8_E4M3FN ? 1 : 2;
   const int64_t row = static_cast<int64_t>(num_kv_heads) * kHead;
@@ -967,5 +1020,6 @@ extern "C" int fk_store_paged_decode(
   return fk_paged_decode_reduce(out, out_row_stride, q, q_row_stride, k_cache, v_cache, kv_dtype,
                                 k_scale, v_scale, block_tables, bt_row_stride, ctx_lens, batch,
                                 num_heads, num_kv_heads, head_size, block_size, num_blocks, scale,
-                                part_tokens, max_parts, workspace, ws_bytes, stream);
+                                window_left, sinks, part_tokens, max_parts, workspace, ws_bytes,
+                                stream);
 }

@@ -271,15 +271,22 @@ __global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_pre
       qb[nb][c] = __builtin_bit_cast(bf16x8_t, v);
     }
   }
-  float m_run[kColBlocks], l_run[kColBlocks];
-  floatx4_t o[kColBlocks][8];
+  // Running max per query column (log2 units, this lane's column r), and the
+  // softmax denominators in the O layout: l_acc[nb][i] is the sum for query row
+  // 4g + i, accumulated by an MFMA of P against ones beside the P.V ones (the
+  // same bf16 P weights as the numerator), so no VALU adds and no cross-lane
+  // fetch at the end.
+  float m_run[kColBlocks];
+  floatx4_t o[kColBlocks][8], l_acc[kColBlocks];
 #pragma unroll
   for (int nb = 0; nb < kColBlocks; ++nb) {
     m_run[nb] = kNegInf;
-    l_run[nb] = 0.f;
+    l_acc[nb] = floatx4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int d = 0; d < 8; ++d) o[nb][d] = floatx4_t{0.f, 0.f, 0.f, 0.f};
   }
+  const bf16x8_t ones = __builtin_bit_cast(
+      bf16x8_t, make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u));
 
   const int ntiles = (kend + kTile - 1) / kTile;
   // Tiles every query of the block sees in full need no mask: keys up to
@@ -312,53 +319,58 @@ __global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_pre
       const floatx4_t acc_b = qk_scores(kb, qb[nb]);
       const int j = j0 + 16 * nb + r;  // this lane's query column
       const int last = offset + j;     // its last visible key
-      float s[8];
+      // Raw scores K.Q: the scale goes into the exponent's FMA (s2 >= 0, so the
+      // row max of the raw scores, scaled, is the max of the scaled ones).
+      // Masked keys take -inf in the max and P = 0 after the exponent.
+      float s[8], sm[8];
+      bool ok[8];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        s[i] = acc_a[i] * s2;
-        s[4 + i] = acc_b[i] * s2;
+        s[i] = acc_a[i];
+        s[4 + i] = acc_b[i];
       }
-      if constexpr (kMasked) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const int key = tok0 + (i >> 2) * kTile + 4 * g + (i & 3);
-          const bool ok = ((i >> 2) ? ok_b : ok_a) && j < q_len && key <= last && key < kend;
-          s[i] = ok ? s[i] : kNegInf;
-        }
-      }
-      float mt = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])),
-                       fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
-      mt = pair_max(mt);
-      // Lazy rescaling: the running max only moves when a score exceeds it by
-      // more than kLazy (log2 units), so P <= 2^kLazy and the O/l rescale (a
-      // cross-lane fetch per row) is rare after the first tiles.  The final
-      // normalisation divides by l accumulated against the same max, so the
-      // result is unchanged up to rounding.
-      const float m_new = mt > m_run[nb] + kLazy ? mt : m_run[nb];
-      float m_use, alpha;
-      if constexpr (kMasked) {
-        m_use = m_new == kNegInf ? 0.f : m_new;
-        alpha = m_new == m_run[nb] ? 1.f : __builtin_amdgcn_exp2f(m_run[nb] - m_use);
-      } else {
-        m_use = m_new;  // finite
-        alpha = m_new == m_run[nb] ? 1.f : __builtin_amdgcn_exp2f(m_run[nb] - m_new);
-      }
-      float pr[8];
-      float psum = 0.f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        pr[i] = __builtin_amdgcn_exp2f(s[i] - m_use);
-        psum += pr[i];
+        if constexpr (kMasked) {
+          const int key = tok0 + (i >> 2) * kTile + 4 * g + (i & 3);
+          ok[i] = ((i >> 2) ? ok_b : ok_a) && j < q_len && key <= last && key < kend;
+          sm[i] = ok[i] ? s[i] : kNegInf;
+        } else {
+          ok[i] = true;
+          sm[i] = s[i];
+        }
       }
-      l_run[nb] = l_run[nb] * alpha + psum;
-      m_run[nb] = m_new;
-      if (__ballot(alpha != 1.f) != 0) {
+      float mt = fmaxf(fmaxf(fmaxf(sm[0], sm[1]), fmaxf(sm[2], sm[3])),
+                       fmaxf(fmaxf(sm[4], sm[5]), fmaxf(sm[6], sm[7])));
+      mt = pair_max(mt);
+      mt = (kMasked && mt == kNegInf) ? kNegInf : mt * s2;
+      // Lazy rescaling: the running max only moves when a score exceeds it by
+      // more than kLazy (log2 units), so P <= 2^kLazy and the O / l rescale (a
+      // cross-lane fetch per row) is rare after the first tiles.  The common
+      // path is the one compare; the final normalisation divides by l
+      // accumulated against the same max, so the result is unchanged up to
+      // rounding.
+      if (__ballot(mt > m_run[nb] + kLazy) != 0) {
+        const float m_new = mt > m_run[nb] + kLazy ? mt : m_run[nb];
+        // 1 where the column's max stays (also -inf to -inf), 0 from -inf.
+        const float alpha = m_new == m_run[nb] ? 1.f : __builtin_amdgcn_exp2f(m_run[nb] - m_new);
+        m_run[nb] = m_new;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const float a = row_value<16>(alpha, g, i);
 #pragma unroll
           for (int d = 0; d < 8; ++d) o[nb][d][i] *= a;
+          l_acc[nb][i] *= a;
         }
+      }
+      // A column with no visible key yet (masked stages only) keeps m = -inf;
+      // all its P are masked to 0.
+      const float m_use = (kMasked && m_run[nb] == kNegInf) ? 0.f : m_run[nb];
+      float pr[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        pr[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], s2, -m_use));
+        if constexpr (kMasked) pr[i] = ok[i] ? pr[i] : 0.f;
       }
       const float (&pa)[4] = *reinterpret_cast<const float(*)[4]>(&pr[0]);
       const float (&pb)[4] = *reinterpret_cast<const float(*)[4]>(&pr[4]);
@@ -427,6 +439,7 @@ __global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_pre
         const bf16x8_t v8 = __builtin_bit_cast(bf16x8_t, make_uint4(va.x, va.y, vb.x, vb.y));
         o[nb][d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pab, v8, o[nb][d], 0, 0, 0);
       }
+      l_acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pab, ones, l_acc[nb], 0, 0, 0);
     }
   };
 
@@ -542,11 +555,10 @@ __global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_pre
   const float vs = (kFp8 && P.v_scale) ? P.v_scale[h] : 1.f;
 #pragma unroll
   for (int nb = 0; nb < kColBlocks; ++nb) {
-    const float l_col = pair_sum(l_run[nb]);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int jr = j0 + 16 * nb + 4 * g + i;  // query row this lane holds
-      const float l = row_value<16>(l_col, g, i);
+      const float l = l_acc[nb][i];
       if (jr >= q_len) continue;
       const float f = l > 0.f ? vs / l : 0.f;
       uint16_t* orow = P.out + static_cast<int64_t>(q_start + jr) * P.out_row_stride +
@@ -656,6 +668,8 @@ int prefill_entry(const char* name, bool paged, void* out, int64_t out_row_strid
   P.gqa = num_heads / num_kv_heads;
   P.block_size_log2 = paged ? __builtin_ctz(static_cast<unsigned>(block_size)) : 0;
   P.num_blocks = paged ? num_blocks : 0;
+  FK_REQUIRE(scale > 0.f && scale < __builtin_huge_valf(),
+             "%s: softmax scale must be positive and finite (got %g)", name, (double)scale);
   P.scale_log2 = scale * kLog2e;
   P.causal = causal ? 1 : 0;
   const int hsplit = (gqa + hw - 1) / hw;

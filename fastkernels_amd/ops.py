@@ -290,7 +290,8 @@ def paged_decode_plan(batch: int, num_heads: int, num_kv_heads: int, head_size: 
                                     num_splits))
 
 
-def _check_decode(out, q, k_cache, v_cache, block_table, cache_seqlens, k_scale, v_scale):
+def _check_decode(out, q, k_cache, v_cache, block_table, cache_seqlens, k_scale, v_scale,
+                  window_left=-1, sinks=None):
     if q.dim() != 3 or q.dtype != torch.bfloat16 or q.stride(2) != 1 or q.stride(1) != q.shape[2]:
         raise ValueError("paged_decode: q must be bf16 [B, Hq, D] with contiguous heads")
     b, hq, d = q.shape
@@ -314,6 +315,12 @@ def _check_decode(out, q, k_cache, v_cache, block_table, cache_seqlens, k_scale,
         if s is not None and (s.dtype != torch.float32 or s.numel() != hk or
                               not s.is_contiguous()):
             raise ValueError(f"paged_decode: {nm} must be float32 [num_kv_heads]")
+    if int(window_left) < -1:
+        raise ValueError("paged_decode: window_left must be -1 (no window) or >= 0")
+    if sinks is not None:
+        if sinks.dtype != torch.float32 or sinks.numel() != hq or not sinks.is_contiguous():
+            raise ValueError("paged_decode: sinks must be contiguous float32 [num_heads]")
+        _same_device(q, sinks)
     _same_device(out, q, k_cache, v_cache, block_table, cache_seqlens)
 
 
@@ -321,9 +328,14 @@ def paged_decode(out: torch.Tensor, q: torch.Tensor, k_cache: torch.Tensor,
                  v_cache: torch.Tensor, block_table: torch.Tensor, cache_seqlens: torch.Tensor,
                  softmax_scale: float, part_tokens: int, max_parts: int,
                  workspace: torch.Tensor | None, k_scale: torch.Tensor | None = None,
-                 v_scale: torch.Tensor | None = None) -> None:
-    """Paged decode attention into ``out`` ([B, Hq, D] bf16)."""
-    _check_decode(out, q, k_cache, v_cache, block_table, cache_seqlens, k_scale, v_scale)
+                 v_scale: torch.Tensor | None = None, window_left: int = -1,
+                 sinks: torch.Tensor | None = None) -> None:
+    """Paged decode attention into ``out`` ([B, Hq, D] bf16).  window_left >= 0 limits
+    each sequence to its last window_left + 1 keys (flash-attn window_size =
+    (window_left, 0)); sinks (float32 [Hq], flash-attn s_aux) join each row's softmax
+    denominator."""
+    _check_decode(out, q, k_cache, v_cache, block_table, cache_seqlens, k_scale, v_scale,
+                  window_left, sinks)
     b, hq, d = q.shape
     if b == 0:
         return
@@ -333,8 +345,9 @@ def paged_decode(out: torch.Tensor, q: torch.Tensor, k_cache: torch.Tensor,
                  _ptr(k_cache), _ptr(v_cache),
                  _native.FK_DTYPE_FP8_E4M3FN if k_cache.dtype == _FP8 else _native.FK_DTYPE_BF16,
                  _ptr(k_scale), _ptr(v_scale), _ptr(block_table), block_table.stride(0),
-                 _ptr(cache_seqlens), b, hq, hk, d, bs, nb, float(softmax_scale), part_tokens,
-                 max_parts, _ptr(workspace), ws_bytes, _stream(q))
+                 _ptr(cache_seqlens), b, hq, hk, d, bs, nb, float(softmax_scale),
+                 int(window_left), _ptr(sinks), part_tokens, max_parts, _ptr(workspace),
+                 ws_bytes, _stream(q))
 
 
 def store_paged_decode(out: torch.Tensor, q: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
@@ -342,7 +355,8 @@ def store_paged_decode(out: torch.Tensor, q: torch.Tensor, key: torch.Tensor, va
                        block_table: torch.Tensor, cache_seqlens: torch.Tensor,
                        softmax_scale: float, part_tokens: int, max_parts: int,
                        workspace: torch.Tensor | None, k_scale: torch.Tensor | None = None,
-                       v_scale: torch.Tensor | None = None) -> None:
+                       v_scale: torch.Tensor | None = None, window_left: int = -1,
+                       sinks: torch.Tensor | None = None) -> None:
     """store_kvcache(key, value, k_cache, v_cache, slot_mapping) followed by
     paged_decode(...) in one launch (plus the merge launch).
 
@@ -351,7 +365,8 @@ def store_paged_decode(out: torch.Tensor, q: torch.Tensor, key: torch.Tensor, va
     in block_table[b] (fastkernels/infra/engine.py:5020-5024).  The result then equals
     the two separate calls bit for bit.  Other slots are still written, but the
     attention output of a sequence that reads another token's slot is unspecified."""
-    _check_decode(out, q, k_cache, v_cache, block_table, cache_seqlens, k_scale, v_scale)
+    _check_decode(out, q, k_cache, v_cache, block_table, cache_seqlens, k_scale, v_scale,
+                  window_left, sinks)
     b, hq, d = q.shape
     nb, bs, hk, _ = k_cache.shape
     if key.shape != (b, hk, d) or value.shape != key.shape:
@@ -373,8 +388,9 @@ def store_paged_decode(out: torch.Tensor, q: torch.Tensor, key: torch.Tensor, va
                  int(slot_mapping.dtype == torch.int64), _ptr(k_cache), _ptr(v_cache),
                  _native.FK_DTYPE_FP8_E4M3FN if k_cache.dtype == _FP8 else _native.FK_DTYPE_BF16,
                  _ptr(k_scale), _ptr(v_scale), _ptr(block_table), block_table.stride(0),
-                 _ptr(cache_seqlens), b, hq, hk, d, bs, nb, float(softmax_scale), part_tokens,
-                 max_parts, _ptr(workspace), ws_bytes, _stream(q))
+                 _ptr(cache_seqlens), b, hq, hk, d, bs, nb, float(softmax_scale),
+                 int(window_left), _ptr(sinks), part_tokens, max_parts, _ptr(workspace),
+                 ws_bytes, _stream(q))
 
 
 def _check_prefill(out, q, cu_seqlens_q, cu_seqlens_k):
@@ -450,9 +466,11 @@ def varlen_prefill(out: torch.Tensor, q: torch.Tensor, key: torch.Tensor, value:
 
 
 def paged_decode_phases(out, q, k_cache, v_cache, block_table, cache_seqlens, softmax_scale,
-                        part_tokens, max_parts, workspace, k_scale=None, v_scale=None):
+                        part_tokens, max_parts, workspace, k_scale=None, v_scale=None,
+                        window_left=-1, sinks=None):
     """The two launches of :func:`paged_decode` as separate callables (for timing)."""
-    _check_decode(out, q, k_cache, v_cache, block_table, cache_seqlens, k_scale, v_scale)
+    _check_decode(out, q, k_cache, v_cache, block_table, cache_seqlens, k_scale, v_scale,
+                  window_left, sinks)
     b, hq, d = q.shape
     nb, bs, hk, _ = k_cache.shape
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
@@ -461,8 +479,9 @@ def paged_decode_phases(out, q, k_cache, v_cache, block_table, cache_seqlens, so
     lib = _native.lib()
     part_args = (_ptr(out), out.stride(0), _ptr(q), q.stride(0), _ptr(k_cache), _ptr(v_cache),
                  kvd, _ptr(k_scale), _ptr(v_scale), _ptr(block_table), block_table.stride(0),
-                 _ptr(cache_seqlens), b, hq, hk, d, bs, nb, float(softmax_scale), part_tokens,
-                 max_parts, _ptr(workspace), ws_bytes, stream)
+                 _ptr(cache_seqlens), b, hq, hk, d, bs, nb, float(softmax_scale),
+                 int(window_left), _ptr(sinks), part_tokens, max_parts, _ptr(workspace), ws_bytes,
+                 stream)
     fp, fr = lib.fk_paged_decode_partials, lib.fk_paged_decode_reduce
 
     def partials():
@@ -541,11 +560,13 @@ _LIB.define("store_kvcache(Tensor key, Tensor value, Tensor(a!) k_cache, Tensor(
             "Tensor slot_mapping) -> ()")
 _LIB.define("paged_decode(Tensor(a!) out, Tensor q, Tensor k_cache, Tensor v_cache, "
             "Tensor block_table, Tensor cache_seqlens, float softmax_scale, int part_tokens, "
-            "int max_parts, Tensor(b!)? workspace, Tensor? k_scale, Tensor? v_scale) -> ()")
+            "int max_parts, Tensor(b!)? workspace, Tensor? k_scale, Tensor? v_scale, "
+            "int window_left=-1, Tensor? sinks=None) -> ()")
 _LIB.define("store_paged_decode(Tensor(a!) out, Tensor q, Tensor key, Tensor value, "
             "Tensor(b!) k_cache, Tensor(c!) v_cache, Tensor slot_mapping, Tensor block_table, "
             "Tensor cache_seqlens, float softmax_scale, int part_tokens, int max_parts, "
-            "Tensor? workspace, Tensor? k_scale=None, Tensor? v_scale=None) -> ()")
+            "Tensor? workspace, Tensor? k_scale=None, Tensor? v_scale=None, "
+            "int window_left=-1, Tensor? sinks=None) -> ()")
 _LIB.define("qk_norm_rope_store(Tensor positions, Tensor(a!) query, Tensor(b!) key, "
             "Tensor value, Tensor(c!) k_cache, Tensor(d!) v_cache, Tensor slot_mapping, "
             "int head_size, Tensor cos_sin_cache, bool is_neox, Tensor? q_weight=None, "

@@ -137,9 +137,15 @@ int fk_paged_decode_plan(int64_t batch, int num_heads, int num_kv_heads, int hea
                          int64_t max_seq_len, int num_splits, int64_t* part_tokens,
                          int64_t* max_parts, int64_t* workspace_bytes);
 
-/* Paged decode attention (one query token per sequence):
- *   out[b,h,:] = softmax(scale * q[b,h,:] . K_b^T) V_b  over the first ctx_lens[b]
- * tokens of sequence b, gathered through block_tables[b, :]; kv head = h / (Hq/Hk).
+/* Paged decode attention (one query token per sequence, at position ctx_lens[b] - 1):
+ *   out[b,h,:] = softmax(scale * q[b,h,:] . K_b^T) V_b  over tokens [lo_b, ctx_lens[b])
+ * of sequence b, gathered through block_tables[b, :]; kv head = h / (Hq/Hk).
+ * window_left: -1 = every token (lo_b = 0); >= 0 = sliding window (flash-attn
+ *    window_size = (window_left, 0)): lo_b = max(0, ctx_lens[b] - 1 - window_left).
+ * sinks: NULL, or device fp32 [num_heads] attention-sink logits (flash-attn s_aux),
+ *    in the units of scale * q . k: they join each row's softmax denominator only,
+ *    out = sum_t e^(s_t - m) V_t / (sum_t e^(s_t - m) + e^(sink - m)); an empty row
+ *    stays 0.
  * q: [batch, num_heads, head_size] rows `q_row_stride` elements apart (head_size
  *    contiguous, heads head_size apart); dtype BF16.
  * k_cache, v_cache: [num_blocks, block_size, num_kv_heads, head_size] of kv_dtype
@@ -162,8 +168,9 @@ int fk_paged_decode(void* out, int64_t out_row_stride, const void* q, int64_t q_
                     const float* k_scale, const float* v_scale, const int32_t* block_tables,
                     int64_t bt_row_stride, const int32_t* ctx_lens, int64_t batch,
                     int num_heads, int num_kv_heads, int head_size, int block_size,
-                    int64_t num_blocks, float scale, int64_t part_tokens, int64_t max_parts,
-                    void* workspace, int64_t workspace_bytes, void* stream);
+                    int64_t num_blocks, float scale, int window_left, const float* sinks,
+                    int64_t part_tokens, int64_t max_parts, void* workspace,
+                    int64_t workspace_bytes, void* stream);
 
 /* The two launches fk_paged_decode makes, exposed so a profiler or benchmark can
  * time them separately.  Same arguments as fk_paged_decode.  The partials launch
@@ -175,16 +182,17 @@ int fk_paged_decode_partials(void* out, int64_t out_row_stride, const void* q,
                              const int32_t* block_tables, int64_t bt_row_stride,
                              const int32_t* ctx_lens, int64_t batch, int num_heads,
                              int num_kv_heads, int head_size, int block_size,
-                             int64_t num_blocks, float scale, int64_t part_tokens,
-                             int64_t max_parts, void* workspace, int64_t workspace_bytes,
-                             void* stream);
+                             int64_t num_blocks, float scale, int window_left,
+                             const float* sinks, int64_t part_tokens, int64_t max_parts,
+                             void* workspace, int64_t workspace_bytes, void* stream);
 int fk_paged_decode_reduce(void* out, int64_t out_row_stride, const void* q,
                            int64_t q_row_stride, const void* k_cache, const void* v_cache,
                            int kv_dtype, const float* k_scale, const float* v_scale,
                            const int32_t* block_tables, int64_t bt_row_stride,
                            const int32_t* ctx_lens, int64_t batch, int num_heads,
                            int num_kv_heads, int head_size, int block_size, int64_t num_blocks,
-                           float scale, int64_t part_tokens, int64_t max_parts, void* workspace,
+                           float scale, int window_left, const float* sinks,
+                           int64_t part_tokens, int64_t max_parts, void* workspace,
                            int64_t workspace_bytes, void* stream);
 
 /* store_kvcache into a cache of another dtype (StoreKVCache.forward with, e.g., a bf16
@@ -274,8 +282,9 @@ int fk_store_paged_decode(void* out, int64_t out_row_stride, const void* q, int6
                           const float* v_scale, const int32_t* block_tables,
                           int64_t bt_row_stride, const int32_t* ctx_lens, int64_t batch,
                           int num_heads, int num_kv_heads, int head_size, int block_size,
-                          int64_t num_blocks, float scale, int64_t part_tokens, int64_t max_parts,
-                          void* workspace, int64_t workspace_bytes, void* stream);
+                          int64_t num_blocks, float scale, int window_left, const float* sinks,
+                          int64_t part_tokens, int64_t max_parts, void* workspace,
+                          int64_t workspace_bytes, void* stream);
 
 /* Log-sum-exp merge of two partial attention results (split-KV / prefix+suffix):
  *   out[t,h,:] = (prefix[t,h,:] e^(p - M) + suffix[t,h,:] e^(s - M)) / (e^(p - M) + e^(s - M))

@@ -219,9 +219,17 @@ def dequant_kv(cache: np.ndarray, scale: np.ndarray | None, q_dtype: str) -> np.
     return round_to(v, q_dtype)
 
 
-def attend_one(q: np.ndarray, k_seq: np.ndarray, v_seq: np.ndarray, scale: float) -> np.ndarray:
+def attend_one(q: np.ndarray, k_seq: np.ndarray, v_seq: np.ndarray, scale: float,
+               sinks: np.ndarray | None = None) -> np.ndarray:
     """softmax(scale * q k^T) v for one query token; GQA by head // (Hq/Hk)
-    (repeat_interleave, attention_impl.py:592-596).  float64; 0 rows when empty."""
+    (repeat_interleave, attention_impl.py:592-596).  float64; 0 rows when empty.
+
+    sinks ([Hq], the flash-attn ``s_aux`` logits, in the units of scale * q.k) join
+    the denominator only: the online softmax starts from M = sink, L = 1
+    (init_softmax_M, fastkernels/infra/triton_attention_helpers.py) and the
+    split-K reduce adds the sink once (reduce_segments,
+    triton_unified_attention.py:741-776), so a row is
+    sum_t e^(s_t - m) v_t / (sum_t e^(s_t - m) + e^(sink - m))."""
     hq, d = q.shape
     n, hk, _ = k_seq.shape
     if n == 0:
@@ -231,21 +239,31 @@ def attend_one(q: np.ndarray, k_seq: np.ndarray, v_seq: np.ndarray, scale: float
     k = k_seq.astype(np.float64).transpose(1, 2, 0)  # [Hk, D, n]
     v = v_seq.astype(np.float64).transpose(1, 0, 2)  # [Hk, n, D]
     s = np.matmul(qh, k) * scale  # [Hk, grp, n]
-    s -= s.max(axis=-1, keepdims=True)
-    p = np.exp(s)
-    p /= p.sum(axis=-1, keepdims=True)
-    return np.matmul(p, v).reshape(hq, d)
+    m = s.max(axis=-1, keepdims=True)
+    if sinks is not None:
+        m = np.maximum(m, np.asarray(sinks, np.float64).reshape(hk, grp, 1))
+    p = np.exp(s - m)
+    den = p.sum(axis=-1, keepdims=True)
+    if sinks is not None:
+        den = den + np.exp(np.asarray(sinks, np.float64).reshape(hk, grp, 1) - m)
+    return np.matmul(p / den, v).reshape(hq, d)
 
 
 def paged_decode(q: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray,
                  block_tables: np.ndarray, ctx_lens: np.ndarray, scale: float,
                  k_scale: np.ndarray | None = None, v_scale: np.ndarray | None = None,
-                 q_dtype: str = "bf16", seqs=None) -> np.ndarray:
+                 q_dtype: str = "bf16", seqs=None, window_left: int = -1,
+                 sinks: np.ndarray | None = None) -> np.ndarray:
     """Decode attention output [B, Hq, D] (float64, unrounded) — `_decode_torch`.
 
     q: [B, Hq, D] values; caches [num_blocks, block_size, Hk, D] values, or uint8
     e4m3fn codes with per-kv-head scales.  ``seqs`` restricts the sequences
-    computed (others stay 0), for bounded CPU-baseline samples."""
+    computed (others stay 0), for bounded CPU-baseline samples.
+
+    window_left >= 0 is a sliding window, flash-attn window_size = (window_left, 0):
+    the query at position n - 1 sees keys [n - 1 - window_left, n - 1] (the
+    SLIDING_WINDOW = 1 + window_size[0] mask of triton_unified_attention.py:577-590
+    and :953).  sinks: see attend_one."""
     b, hq, d = q.shape
     out = np.zeros((b, hq, d), np.float64)
     fp8 = k_cache.dtype == np.uint8
@@ -256,7 +274,8 @@ def paged_decode(q: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray,
         if fp8:
             k_seq = dequant_kv(k_seq[None], k_scale, q_dtype)[0]
             v_seq = dequant_kv(v_seq[None], v_scale, q_dtype)[0]
-        out[i] = attend_one(q[i], k_seq, v_seq, scale)
+        lo = max(0, n - 1 - window_left) if window_left >= 0 else 0
+        out[i] = attend_one(q[i], k_seq[lo:], v_seq[lo:], scale, sinks)
     return out
 
 

@@ -104,12 +104,12 @@ def test_argument_errors_return_before_launch(lib):
 
     def decode(**kw):
         a = dict(head=128, hq=32, hk=8, bs=256, nb=64, part=512, nparts=4, ws=fake, wsb=1 << 30,
-                 kv=N.FK_DTYPE_BF16)
+                 kv=N.FK_DTYPE_BF16, window=-1)
         a.update(kw)
         return lib.fk_paged_decode(fake, a["hq"] * 128, fake, a["hq"] * 128, fake, fake, a["kv"],
                                    None, None, fake, 32, fake, 4, a["hq"], a["hk"], a["head"],
-                                   a["bs"], a["nb"], 0.088, a["part"], a["nparts"], a["ws"],
-                                   a["wsb"], stream)
+                                   a["bs"], a["nb"], 0.088, a["window"], None, a["part"],
+                                   a["nparts"], a["ws"], a["wsb"], stream)
 
     assert decode(head=64) == N.FK_ERR_UNSUPPORTED and "head_size" in _last_error(lib)
     assert decode(hq=256, hk=8) == N.FK_ERR_UNSUPPORTED and "GQA" in _last_error(lib)
@@ -120,6 +120,7 @@ def test_argument_errors_return_before_launch(lib):
     assert decode(nb=0) == N.FK_ERR_INVALID_ARG and "block" in _last_error(lib)
     assert decode(wsb=16) == N.FK_ERR_WORKSPACE and "workspace" in _last_error(lib)
     assert decode(ws=None, part=0, nparts=256) == N.FK_ERR_WORKSPACE
+    assert decode(window=-2) == N.FK_ERR_INVALID_ARG and "window_left" in _last_error(lib)
 
 
 def test_python_layer_fails_loudly_without_gpu(lib):

@@ -142,17 +142,62 @@ def test_custom_ops_registered_with_fake_impls():
                                                                   dtype=torch.bfloat16), 1e-6)
 
 
-def test_flash_attn_decode_rejects_unsupported_features():
+def test_flash_attn_decode_argument_errors():
+    """Unknown kwargs and malformed sinks are rejected before any launch; CPU tensors
+    are refused (no CPU fallback), with or without a window."""
     FlashAttnDecode = load_by_path("flash_attn_decode").FlashAttnDecode
     m = FlashAttnDecode(32, 8, 128, page_size=256)
     q = torch.zeros(2, 32, 128, dtype=torch.bfloat16)
     kc = torch.zeros(4, 256, 8, 128, dtype=torch.bfloat16)
-    with pytest.raises(NotImplementedError):
-        m(q, kc, kc, torch.ones(2, dtype=torch.int32), block_table=torch.zeros(2, 1, dtype=torch.int32),
-          window_size=(128, 0))
+    lens, bt = torch.ones(2, dtype=torch.int32), torch.zeros(2, 1, dtype=torch.int32)
     with pytest.raises(TypeError):
-        m(q, kc, kc, torch.ones(2, dtype=torch.int32), block_table=torch.zeros(2, 1, dtype=torch.int32),
-          bogus=1)
+        m(q, kc, kc, lens, block_table=bt, bogus=1)
+    with pytest.raises(ValueError, match="s_aux"):
+        m(q, kc, kc, lens, block_table=bt, s_aux=torch.zeros(7))
+    with pytest.raises(RuntimeError, match="GPU"):
+        m(q, kc, kc, lens, block_table=bt, window_size=(128, 0))
+
+
+def test_flash_attn_decode_engine_hooks():
+    """What the reference engine does with its decode ops works on the candidate:
+    group them by (heads, kv heads, head dim, window) and share the lead's buffers
+    (engine.py:1538-1550, fa_utils.py:108-118), skip the FA3 scheduler refresh for
+    an op whose fa_version is not 3 (fa_utils.py:127-145), toggle
+    _force_graph_splits (jamba_engine.py:846-856), and set _window_size from the
+    layer's sliding window (attention_impl.py:242-244, :282)."""
+    FlashAttnDecode = load_by_path("flash_attn_decode").FlashAttnDecode
+    ref_pre = ["max_batch_size", "device"]
+    pre = [p for p in inspect.signature(FlashAttnDecode.preallocate).parameters if p != "self"]
+    assert pre[:2] == ref_pre
+    upd = [p for p in inspect.signature(FlashAttnDecode.update_scheduler_metadata).parameters
+           if p != "self"]
+    assert upd == ["cache_seqlens", "max_seqlen_k", "qkv_dtype", "window_size", "max_seqlen_q"]
+    ops_ = [FlashAttnDecode(32, 8, 128) for _ in range(3)]
+    ops_[2]._window_size = (4095, 0)
+    groups = {}
+    for op in ops_:
+        key = (op.num_heads, op.num_kv_heads, op.head_dim, tuple(getattr(op, "_window_size")))
+        groups.setdefault(key, []).append(op)
+    assert [len(g) for g in groups.values()] == [2, 1]
+    for group in groups.values():
+        lead = group[0]
+        if not lead.page_size:
+            lead.page_size = 256
+        lead.preallocate(8, torch.device("cpu"))
+        for op in group[1:]:
+            op.page_size = lead.page_size
+            op._cu_seqlens_q = lead._cu_seqlens_q
+            op._sched_buf = lead._sched_buf
+            op._sched_meta = lead._sched_meta
+        assert torch.equal(lead._cu_seqlens_q, torch.arange(9, dtype=torch.int32))
+        assert getattr(lead, "fa_version", 3) != 3  # the FA3 refresh skips it
+        lead.update_scheduler_metadata(torch.ones(8, dtype=torch.int32), 4096,
+                                       qkv_dtype=torch.bfloat16,
+                                       window_size=getattr(lead, "_window_size", (-1, -1)))
+    was = ops_[0]._force_graph_splits
+    ops_[0]._force_graph_splits = True
+    ops_[0]._force_graph_splits = was
+    assert ops_[2]._window_size == (4095, 0)
 
 
 def test_bench_refuses_multi_gpu():

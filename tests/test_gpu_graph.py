@@ -54,7 +54,7 @@ def test_decode_step_graph_capture_and_replay(cuda):
                   slots=c0.slot_mapping.clone(), ctx=c0.decode.ctx_lens.clone(),
                   bt=torch.full((t, 16), -1, dtype=torch.int32, device=cuda),
                   dims=(t, hq, hk, d), max_seq_len=4096)
-    mods[3].preallocate(t, 4096, cuda)
+    mods[3].preallocate(t, cuda)
 
     def load(case):
         for key, src in (("hidden", case.hidden), ("residual", case.residual), ("qkv", case.qkv),
@@ -106,7 +106,7 @@ def test_fused_store_decode_graph_capture_and_replay(cuda):
                                  seed=500 + i) for i in range(3)]
     steps = [workloads.decode_step_rows(c, seed=600 + i) for i, c in enumerate(cases)]
     attn = FlashAttnDecode(32, 8, 128, page_size=256)
-    attn.preallocate(b, 4096, cuda)
+    attn.preallocate(b, cuda)
     c0, s0 = cases[0], steps[0]
     static = dict(q=c0.q.clone(), key=s0.key.clone(), value=s0.value.clone(),
                   k_cache=c0.k_cache.clone(), v_cache=c0.v_cache.clone(),

@@ -228,7 +228,7 @@ def run_decode(case, num_splits=0, max_seq_len=None):
     return out
 
 
-def oracle_decode(case, seqs=None):
+def oracle_decode(case, seqs=None, window_left=-1, sinks=None):
     """Oracle on the pages the selected sequences use (host copies of those pages only)."""
     b = case.q.shape[0]
     seqs = list(range(b)) if seqs is None else list(seqs)
@@ -252,7 +252,8 @@ def oracle_decode(case, seqs=None):
         ks = None if case.k_scale is None else case.k_scale.cpu().numpy()
         vs = None if case.v_scale is None else case.v_scale.cpu().numpy()
         out[i] = oracle.paged_decode(q[i:i + 1], kp, vp, local_bt, np.array([n]), case.scale,
-                                     ks, vs)[0]
+                                     ks, vs, window_left=window_left,
+                                     sinks=None if sinks is None else f32(sinks))[0]
     return out
 
 
@@ -400,6 +401,94 @@ def test_paged_decode_fp8_c5(cuda):
     assert_close(got[[0, 7]], ref[[0, 7]], FP8_TOL, FP8_TOL, "C5 vs oracle")
     assert_close(f32(outb)[[0, 7]], ref[[0, 7]], FP8_TOL, FP8_TOL, "C5 balanced vs oracle")
     assert_close(f32(out16), got, FP8_TOL, FP8_TOL, "C5 16 vs 64 partitions")
+
+
+def run_decode_ws(case, num_splits=0, window_left=-1, sinks=None):
+    b, hq, d = case.q.shape
+    hk = case.k_cache.shape[2]
+    part, nparts, wsb = ops.paged_decode_plan(b, hq, hk, d, case.max_seq_len, num_splits)
+    ws = torch.zeros(max(1, wsb), dtype=torch.uint8, device=case.q.device)
+    out = torch.full_like(case.q, float("nan"))
+    ops.paged_decode(out, case.q, case.k_cache, case.v_cache, case.block_tables, case.ctx_lens,
+                     case.scale, part, nparts, ws, case.k_scale, case.v_scale, window_left, sinks)
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("num_splits", [0, 3, 16])
+@pytest.mark.parametrize("window_left", [0, 1, 15, 16, 100, 1000, 5000])
+def test_paged_decode_sliding_window_and_sinks(cuda, num_splits, window_left):
+    """Sliding window (flash-attn window_size = (window_left, 0)) at edges of tiles
+    (16 tokens), pages (64) and partitions, with and without attention sinks, on the
+    balanced schedule and on fixed partitions (some wholly before the window)."""
+    _flush(f"decode window={window_left} splits={num_splits}")
+    ctx = [1, 15, 16, 17, 255, 256, 257, 1000, 4000, 0, 2047]
+    pool = sum((n + 63) // 64 for n in ctx) + 3
+    case = workloads.c3_decode(cuda, num_heads=32, kv_heads=8, block_size=64, pool_blocks=pool,
+                               ctx_lens=ctx, seed=61 + window_left)
+    g = torch.Generator().manual_seed(62)
+    sinks = (2 * torch.randn(32, generator=g)).float().to(cuda)
+    for sk in (None, sinks):
+        got = f32(run_decode_ws(case, num_splits, window_left, sk))
+        ref = oracle_decode(case, window_left=window_left, sinks=sk)
+        assert_close(got, ref, BF16_TOL, BF16_TOL, f"window={window_left} sinks={sk is not None}")
+        assert not got[9].any()  # empty context: zero row, sinks or not
+
+
+def test_paged_decode_sinks_c3_and_fp8(cuda):
+    """Sinks at C3 size (balanced; sequences cut across work-groups merge the sink
+    once) and on fp8 pages with a window, against the oracle."""
+    _flush("decode sinks C3 + fp8 window")
+    case = workloads.c3_decode(cuda)
+    g = torch.Generator().manual_seed(63)
+    sinks = (3 * torch.randn(32, generator=g)).float().to(cuda)
+    got = f32(run_decode_ws(case, 0, -1, sinks))
+    ctx = case.ctx_lens.cpu().numpy()
+    seqs = [int(i) for i in np.argsort(ctx)[::9]]
+    assert_close(got[seqs], oracle_decode(case, seqs, sinks=sinks)[seqs], BF16_TOL, BF16_TOL, "C3")
+    c5 = workloads.c5_fp8_decode(cuda, batch=3, ctx_lens=[5000, 8192, 333], seed=64)
+    s64 = (2 * torch.randn(64, generator=g)).float().to(cuda)
+    for splits in (0, 16):
+        assert_close(f32(run_decode_ws(c5, splits, 700, s64)),
+                     oracle_decode(c5, window_left=700, sinks=s64), FP8_TOL, FP8_TOL,
+                     f"fp8 window splits={splits}")
+
+
+def test_candidate_decode_window_and_sinks_kwargs(cuda):
+    """FlashAttnDecode as Attention drives it: the window from the _window_size
+    attribute (attention_impl.py:242-244, :282) or the window_size kwarg, sinks as
+    s_aux in the model dtype (attention_impl.py:401-406), both through forward and
+    forward_store, against the oracle."""
+    from fastkernels_amd.candidate.L1.flash_attn_decode import FlashAttnDecode
+
+    ctx = [300, 77, 1024, 5]
+    case = workloads.c3_decode(cuda, num_heads=16, kv_heads=4, block_size=64, pool_blocks=64,
+                               ctx_lens=ctx, seed=65)
+    g = torch.Generator().manual_seed(66)
+    s_aux = (2 * torch.randn(16, generator=g)).to(torch.bfloat16).to(cuda)
+    ref = oracle_decode(case, window_left=127, sinks=s_aux.float())
+    mod = FlashAttnDecode(16, 4, 128, page_size=64)
+    mod._window_size = (127, 0)
+    kw = dict(block_table=case.block_tables, softmax_scale=case.scale, causal=True,
+              max_seq_len=case.max_seq_len, s_aux=s_aux)
+    assert_close(f32(mod(case.q, case.k_cache, case.v_cache, case.ctx_lens, **kw)), ref,
+                 BF16_TOL, BF16_TOL, "attribute window")
+    mod2 = FlashAttnDecode(16, 4, 128, page_size=64)
+    assert_close(f32(mod2(case.q, case.k_cache, case.v_cache, case.ctx_lens,
+                          window_size=(127, 0), **kw)), ref, BF16_TOL, BF16_TOL, "kwarg window")
+    assert_close(f32(mod2(case.q, case.k_cache, case.v_cache, case.ctx_lens,
+                          window_size=(127, 0), num_splits=4, **kw)), ref, BF16_TOL, BF16_TOL,
+                 "kwarg window, 4 splits")
+    # forward_store: the new rows stored at each sequence's last slot, then decode
+    rows = workloads.decode_step_rows(case)
+    kc, vc = case.k_cache.clone(), case.v_cache.clone()
+    got = mod.forward_store(case.q, rows.key, rows.value, kc, vc, rows.slot_mapping,
+                            case.ctx_lens, **kw)
+    ops.store_kvcache(rows.key, rows.value, case.k_cache, case.v_cache, rows.slot_mapping)
+    torch.cuda.synchronize()
+    assert torch.equal(kc, case.k_cache) and torch.equal(vc, case.v_cache)
+    assert_close(f32(got), oracle_decode(case, window_left=127, sinks=s_aux.float()), BF16_TOL,
+                 BF16_TOL, "forward_store window + sinks")
 
 
 @pytest.mark.parametrize("kv_dtype", [torch.bfloat16, torch.float8_e4m3fn])

@@ -310,6 +310,80 @@ def test_paged_decode_page_permutation_invariance():
     np.testing.assert_allclose(oracle.paged_decode(q, kc2, vc2, bt2, lens, 0.3), base, atol=0)
 
 
+def _sdpa_sink_window_ref(q, kc, vc, bt, lens, scale, sinks=None, window_left=-1):
+    """Brute force for sinks and windows in float64 torch: the window slices each
+    sequence's keys to its last window_left + 1; a sink is one more key per query
+    head whose score is exactly the sink logit (k = sink / (scale |q|^2) q) and whose
+    value row is zero, so it joins the denominator only."""
+    out = np.zeros(q.shape, np.float64)
+    hq, hk = q.shape[1], kc.shape[2]
+    idx = torch.tensor([h // (hq // hk) for h in range(hq)])
+    for i in range(q.shape[0]):
+        n = int(lens[i])
+        lo = max(0, n - 1 - window_left) if window_left >= 0 else 0
+        ks = torch.from_numpy(oracle.gather_seq(kc, bt[i], n)[lo:]).double()
+        vs = torch.from_numpy(oracle.gather_seq(vc, bt[i], n)[lo:]).double()
+        kh = ks[:, idx].transpose(0, 1).contiguous()  # [Hq, n', D]
+        vh = vs[:, idx].transpose(0, 1).contiguous()
+        qh = torch.from_numpy(q[i]).double()[:, None, :]  # [Hq, 1, D]
+        if sinks is not None:
+            qq = torch.from_numpy(q[i]).double()
+            ke = (torch.from_numpy(np.asarray(sinks, np.float64))[:, None] * qq
+                  / (scale * (qq * qq).sum(-1, keepdim=True)))
+            kh = torch.cat([kh, ke[:, None, :]], 1)
+            vh = torch.cat([vh, torch.zeros(hq, 1, vh.shape[2], dtype=vh.dtype)], 1)
+        if kh.shape[1] == 0:
+            continue
+        out[i] = F.scaled_dot_product_attention(qh, kh, vh, scale=scale)[:, 0].numpy()
+    return out
+
+
+def test_paged_decode_sinks_vs_torch():
+    """Sinks: against SDPA with one zero-value key per head scoring the sink; -inf
+    sinks change nothing; a dominant sink drives the row to 0; an empty row stays 0."""
+    q, kc, vc, bt, lens = _decode_case(seed=5, lens=[0, 1, 13, 37])
+    sinks = np.array([0.5, -1.0, 2.0, 0.0, 1.5, -3.0, 4.0, 0.25])[:q.shape[1]]
+    ours = oracle.paged_decode(q, kc, vc, bt, lens, 0.3, sinks=sinks)
+    ref = _sdpa_sink_window_ref(q, kc, vc, bt, lens, 0.3, sinks=sinks)
+    np.testing.assert_allclose(ours, ref, rtol=1e-9, atol=1e-12)
+    assert np.array_equal(ours[0], np.zeros_like(ours[0]))
+    none = oracle.paged_decode(q, kc, vc, bt, lens, 0.3)
+    np.testing.assert_allclose(
+        oracle.paged_decode(q, kc, vc, bt, lens, 0.3, sinks=np.full(q.shape[1], -np.inf)), none,
+        rtol=0, atol=0)
+    big = oracle.paged_decode(q, kc, vc, bt, lens, 0.3, sinks=np.full(q.shape[1], 200.0))
+    assert np.abs(big).max() < 1e-40
+    # a dropped sink is caught (the sinks move the rows)
+    assert not np.allclose(ours[2], none[2], atol=1e-3)
+
+
+@pytest.mark.parametrize("window_left", [0, 1, 5, 12, 36, 100])
+def test_paged_decode_window_vs_torch(window_left):
+    """Sliding window: the last window_left + 1 keys, against SDPA on the sliced
+    sequence (window 0 is the last V row; a window past the start is no window),
+    with and without sinks; a window one key short is caught."""
+    q, kc, vc, bt, lens = _decode_case(seed=6, lens=[1, 13, 37])
+    ours = oracle.paged_decode(q, kc, vc, bt, lens, 0.3, window_left=window_left)
+    ref = _sdpa_sink_window_ref(q, kc, vc, bt, lens, 0.3, window_left=window_left)
+    np.testing.assert_allclose(ours, ref, rtol=1e-9, atol=1e-12)
+    sinks = np.linspace(-1, 2, q.shape[1])
+    np.testing.assert_allclose(
+        oracle.paged_decode(q, kc, vc, bt, lens, 0.3, window_left=window_left, sinks=sinks),
+        _sdpa_sink_window_ref(q, kc, vc, bt, lens, 0.3, sinks=sinks, window_left=window_left),
+        rtol=1e-9, atol=1e-12)
+    grp = q.shape[1] // kc.shape[2]
+    for i, n in enumerate(lens):
+        if window_left == 0:
+            last = oracle.gather_seq(vc, bt[i], int(n))[-1].astype(np.float64)
+            np.testing.assert_allclose(ours[i], np.repeat(last, grp, axis=0), atol=1e-12)
+        if window_left >= n - 1:
+            np.testing.assert_allclose(ours[i], oracle.paged_decode(q, kc, vc, bt, lens, 0.3)[i],
+                                       atol=0, rtol=0)
+    if 1 <= window_left < 36:
+        short = _sdpa_sink_window_ref(q, kc, vc, bt, lens, 0.3, window_left=window_left - 1)
+        assert not np.allclose(ours[2], short[2], atol=1e-3), "off-by-one window not caught"
+
+
 @pytest.mark.parametrize("part", [1, 3, 4, 16, 1000])
 def test_split_merge_equals_unsplit(part):
     q, kc, vc, bt, lens = _decode_case(seed=4, lens=[37])
