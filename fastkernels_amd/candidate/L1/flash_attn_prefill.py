@@ -13,9 +13,13 @@ Same constructor ``(num_heads, num_kv_heads, head_dim)`` (with ``sm_scale``) and
 Keyword arguments: ``softmax_scale`` (default ``head_dim ** -0.5``), ``causal``
 (default True; queries aligned to the end of the keys), ``out``, fp8 descales
 ``k_descale`` / ``v_descale`` (or ``k_scale`` / ``v_scale``) for float8_e4m3fn
-caches.  ``window_size`` other than (-1, -1) and ``s_aux`` raise
-NotImplementedError.  ``max_seqlen_q`` must bound every query chunk (it sizes the
-launch); no host synchronisation happens.  Returns ``[total_q, num_heads, head_dim]``.
+caches, ``window_size`` (causal sliding window ``(left, right)``: query j keeps
+its last left + 1 positions; left = -1 is no window; a window with
+``causal=False`` raises NotImplementedError) and ``s_aux`` (attention-sink
+logits, one per query head) as ``Attention._forward_pure`` passes them
+(attention_impl.py:401-434).  ``max_seqlen_q`` must bound every query chunk (it
+sizes the launch); no host synchronisation happens.  Returns
+``[total_q, num_heads, head_dim]``.
 """
 from __future__ import annotations
 
@@ -39,6 +43,27 @@ class FlashAttnPrefill(nn.Module):
         self.num_kv_heads = num_kv_heads
         self.head_dim = head_dim
         self.sm_scale = head_dim ** -0.5
+        self._sinks_src = None  # (tensor, version) of the cached float32 s_aux copy
+        self._sinks_f32: torch.Tensor | None = None
+
+    def _sinks(self, s_aux, device) -> torch.Tensor | None:
+        """s_aux as contiguous float32 [num_heads] on the device, converted once per
+        source tensor version (the layer passes the same sinks parameter each step)."""
+        if s_aux is None:
+            return None
+        if not isinstance(s_aux, torch.Tensor) or s_aux.numel() != self.num_heads:
+            raise ValueError(f"FlashAttnPrefill: s_aux must hold {self.num_heads} logits")
+        if s_aux.dtype == torch.float32 and s_aux.is_contiguous() and s_aux.device == device:
+            return s_aux.reshape(-1)
+        src = self._sinks_src
+        if (self._sinks_f32 is None or src is None or src[0] is not s_aux
+                or src[1] != s_aux._version or self._sinks_f32.device != device):
+            if device.type == "cuda" and torch.cuda.is_current_stream_capturing():
+                raise RuntimeError("FlashAttnPrefill: convert s_aux to float32 before graph "
+                                   "capture (run the step eagerly once)")
+            self._sinks_f32 = s_aux.detach().to(device=device, dtype=torch.float32).reshape(-1)
+            self._sinks_src = (s_aux, s_aux._version)
+        return self._sinks_f32
 
     @staticmethod
     def _scale_vec(s, hk: int, device) -> torch.Tensor | None:
@@ -65,12 +90,15 @@ class FlashAttnPrefill(nn.Module):
         s_aux = kwargs.pop("s_aux", None)
         for ignored in ("scheduler_metadata", "num_splits", "seqused_k", "fa_version"):
             kwargs.pop(ignored, None)
-        if window is not None and tuple(window) != (-1, -1):
-            raise NotImplementedError("FlashAttnPrefill (gfx950): sliding window is not supported")
-        if s_aux is not None:
-            raise NotImplementedError("FlashAttnPrefill (gfx950): attention sinks are not supported")
         if kwargs:
             raise TypeError(f"FlashAttnPrefill: unexpected arguments {sorted(kwargs)}")
+        window_left = -1
+        if window is not None and tuple(window) != (-1, -1):
+            if not causal:
+                raise NotImplementedError("FlashAttnPrefill (gfx950): a sliding window needs "
+                                          "causal=True")
+            window_left = int(window[0]) if int(window[0]) >= 0 else -1
+        sinks = self._sinks(s_aux, q.device)
         if softmax_scale is None:
             softmax_scale = self.sm_scale
         total = q.shape[0]
@@ -92,12 +120,12 @@ class FlashAttnPrefill(nn.Module):
             vs = self._scale_vec(v_scale, hk, q.device)
             call = torch.ops.fastkernels_amd.paged_prefill if compiling else ops.paged_prefill
             call(out3, q3, k, v, block_table, cu_seqlens_q, cu_seqlens_k, int(max_seqlen_q),
-                 float(softmax_scale), ks, vs, causal)
+                 float(softmax_scale), ks, vs, causal, window_left, sinks)
         else:
             hk = k.shape[-2] if k.dim() == 3 else k.shape[-1] // self.head_dim
             k3 = k.view(k.shape[0], hk, self.head_dim)
             v3 = v.view(v.shape[0], hk, self.head_dim)
             call = torch.ops.fastkernels_amd.varlen_prefill if compiling else ops.varlen_prefill
             call(out3, q3, k3, v3, cu_seqlens_q, cu_seqlens_k, int(max_seqlen_q),
-                 float(softmax_scale), causal)
+                 float(softmax_scale), causal, window_left, sinks)
         return out

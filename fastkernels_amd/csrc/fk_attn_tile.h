@@ -45,6 +45,13 @@ __device__ __forceinline__ float pair_sum(float v) {
   return __uint_as_float(c[0]) + __uint_as_float(c[1]);
 }
 
+// Softmax denominator of a row with running max m and sum l (log2 units) once
+// an attention sink of logit sink2 (log2 units; -inf = none) joins it:
+// l + 2^(sink2 - m).  A row with no visible key (l = 0) stays 0.
+__device__ __forceinline__ float with_sink(float l, float m, float sink2) {
+  return (l > 0.f && sink2 != kNegInf) ? l + __builtin_amdgcn_exp2f(sink2 - m) : l;
+}
+
 // Low / high 16-bit halves of a and b packed as (a, b): one v_perm_b32 each
 // (byte selectors over {b, a}, a in bytes 0-3).
 __device__ __forceinline__ uint32_t lo_pair(uint32_t a, uint32_t b) {

@@ -107,12 +107,6 @@ __device__ __forceinline__ float sink_log2(const DecodeParams& P, int hq) {
   return P.sinks ? P.sinks[hq] * kLog2e : kNegInf;
 }
 
-// Softmax denominator of a row with running (max m, sum l) once the sink
-// joins it: l + 2^(sink - m); a row with no visible key (l = 0) stays 0.
-__device__ __forceinline__ float with_sink(float l, float m, float sink2) {
-  return (l > 0.f && sink2 != kNegInf) ? l + __builtin_amdgcn_exp2f(sink2 - m) : l;
-}
-
 // Issues the loads of one tile from page `page` (>= 0, < num_blocks).  Loads
 // are unconditional so that every pipeline stage has the same number of loads
 // in flight and the compiler can wait for one stage with vmcnt(N) instead of

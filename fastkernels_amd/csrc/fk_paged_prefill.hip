@@ -9,9 +9,13 @@
 // sequence b owns query rows [cu_q[b], cu_q[b+1]) (q_len of them) and the first
 // k_len = cu_k[b+1] - cu_k[b] tokens of its paged cache.  Query j (0-based in
 // its chunk) sits at position k_len - q_len + j and sees keys
-// [0, k_len - q_len + j] (causal, aligned to the end of the keys).  A query
-// with no visible key gets a zero row.  kv head = hq / (Hq / Hk); fp8 pages
-// are dequantised per kv head as in the decode kernel.
+// [0, k_len - q_len + j] (causal, aligned to the end of the keys), or, under
+// a sliding window (flash-attn window_size = (window_left, 0)), keys
+// [k_len - q_len + j - window_left, k_len - q_len + j].  A query with no
+// visible key gets a zero row.  Attention sinks (s_aux: one logit per query
+// head) join each row's softmax denominator, as in the decode kernel.  kv head
+// = hq / (Hq / Hk); fp8 pages are dequantised per kv head as in the decode
+// kernel.
 //
 // Work decomposition: work-group = 4 waves over one kv head and one block of
 // query tokens of one sequence: the waves are the group's query heads (up to
@@ -73,7 +77,9 @@ struct PrefillParams {
   int block_size_log2;
   int64_t num_blocks;
   float scale_log2;
-  int causal;  // 0: every query sees all k_len keys
+  int causal;        // 0: every query sees all k_len keys
+  int window_left;   // causal sliding window: keys >= position - window_left (-1: none)
+  const float* sinks;  // attention sink logits [num_heads] fp32, or nullptr
 };
 
 __device__ __forceinline__ int64_t prefill_page(const PrefillParams& P,
@@ -255,6 +261,14 @@ __global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_pre
   // of the work-group.
   const int kend = active ? max(0, min(k_len, offset + min(j0 + kQTokens, q_len))) : 0;
   const int kend_wg = max(0, min(k_len, offset + min(jw0 + wg_tokens, q_len)));
+  // Sliding window: query j sees keys from offset + j - win.  kbeg (this wave's
+  // first query) and kbeg_wg (the work-group's) bound the keys from below; the
+  // work-group starts streaming at the stage holding kbeg_wg, and a stage at or
+  // after khead (the last query's window start) is inside every query's window.
+  const int win = P.window_left;
+  const int kbeg = (win >= 0 && active) ? max(0, offset + j0 - win) : 0;
+  const int kbeg_wg = win >= 0 ? max(0, offset + jw0 - win) : 0;
+  const int khead = (win >= 0 && active) ? offset + min(j0 + kQTokens, q_len) - 1 - win : 0;
 
   // Q^T operands: column r of block nb = query j0 + 16 nb + r.
   bf16x8_t qb[kColBlocks][4];
@@ -293,6 +307,8 @@ __global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_pre
   // offset + j0 (query j0's last key), inside [0, kend).
   const int nfull = active ? max(0, min(kend, offset + j0 + 1)) / kTile : 0;
   const int nstages = (kend_wg + kStageKeys - 1) / kStageKeys;
+  const int st0 = min(kbeg_wg / kStageKeys, nstages);  // first stage the work-group streams
+  const int tbeg = kbeg / kTile;                      // this wave's first tile
 
   // Two 16-key tiles (tiles tt, tt + 1 of `buf`, keys tok0 .. tok0 + 31):
   // scores, one online-softmax update per query column for the 32 keys, P.V.
@@ -333,7 +349,8 @@ __global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_pre
       for (int i = 0; i < 8; ++i) {
         if constexpr (kMasked) {
           const int key = tok0 + (i >> 2) * kTile + 4 * g + (i & 3);
-          ok[i] = ((i >> 2) ? ok_b : ok_a) && j < q_len && key <= last && key < kend;
+          ok[i] = ((i >> 2) ? ok_b : ok_a) && j < q_len && key <= last && key < kend &&
+                  (win < 0 || key >= last - win);
           sm[i] = ok[i] ? s[i] : kNegInf;
         } else {
           ok[i] = true;
@@ -510,6 +527,7 @@ __global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_pre
     for (int tt = 0; tt < kStageTiles; tt += 2) {
       const int t = st * kStageTiles + tt;
       if (t >= ntiles) break;  // wave-uniform; the rest of the stage is past this wave's keys
+      if (t + 1 < tbeg) continue;  // wave-uniform; both tiles precede this wave's window
       bool ok_a = true, ok_b = true;
       if constexpr (decltype(masked)::value && kPaged) {
         (void)key_row<kPaged>(P, bt_row, k_start, t * kTile, ok_a);
@@ -522,6 +540,7 @@ __global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_pre
   // and none of its pages is masked.
   auto stage_unmasked = [&](int st) {
     if ((st + 1) * kStageTiles > nfull) return false;
+    if (win >= 0 && st * kStageKeys < khead) return false;
     if constexpr (kPaged) {
 #pragma unroll
       for (int tt = 0; tt < kStageTiles; ++tt) {
@@ -534,8 +553,8 @@ __global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_pre
   };
   // One step: wait for stage st's loads (every thread's, through the barrier,
   // which also frees the other buffer), issue stage st + 1's, consume stage st.
-  // The unmasked stages (a prefix) and the masked ones run in separate loops;
-  // every wave passes exactly nstages barriers whichever loop it is in.
+  // The unmasked and masked stages run in separate loops; every wave passes
+  // exactly nstages - st0 barriers whichever loops it is in.
   auto step = [&](auto masked, int st) {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
@@ -544,8 +563,13 @@ __global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_pre
     if (st + 1 < nstages) stage_load(st + 1, next_buf);
     stage_compute(masked, st, cur_buf);
   };
-  if (nstages > 0) stage_load(0, lds0);
-  int st = 0;
+  // Stages [st0, nstages): under a window, a masked head (keys some query's
+  // window starts after), then the unmasked stages, then the masked rest.
+  if (st0 < nstages) stage_load(st0, (st0 & 1) ? lds1 : lds0);
+  int st = st0;
+  const int head_end = win >= 0 ? max(st0, (khead + kStageKeys - 1) / kStageKeys) : st0;
+#pragma unroll 1
+  for (; st < nstages && st < head_end; ++st) step(std::true_type{}, st);
 #pragma unroll 1
   for (; st < nstages && stage_unmasked(st); ++st) step(std::false_type{}, st);
 #pragma unroll 1
@@ -558,7 +582,8 @@ __global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_pre
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int jr = j0 + 16 * nb + 4 * g + i;  // query row this lane holds
-      const float l = l_acc[nb][i];
+      float l = l_acc[nb][i];
+      if (P.sinks) l = with_sink(l, row_value<16>(m_run[nb], g, i), P.sinks[hq] * kLog2e);
       if (jr >= q_len) continue;
       const float f = l > 0.f ? vs / l : 0.f;
       uint16_t* orow = P.out + static_cast<int64_t>(q_start + jr) * P.out_row_stride +
@@ -613,9 +638,14 @@ int prefill_entry(const char* name, bool paged, void* out, int64_t out_row_strid
                   const int32_t* block_tables, int64_t bt_row_stride,
                   const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int64_t batch,
                   int64_t max_seqlen_q, int num_heads, int num_kv_heads, int head_size,
-                  int block_size, int64_t num_blocks, float scale, int causal, void* stream) {
+                  int block_size, int64_t num_blocks, float scale, int causal,
+                  int window_left, const float* sinks, void* stream) {
   FK_REQUIRE(batch >= 0 && batch <= 65535, "%s: batch %lld out of range [0, 65535]", name,
              (long long)batch);
+  FK_REQUIRE(window_left >= -1, "%s: window_left %d must be -1 (no window) or >= 0", name,
+             window_left);
+  FK_REQUIRE(window_left < 0 || causal,
+             "%s: a sliding window needs causal attention (window_size = (left, 0))", name);
   FK_REQUIRE(max_seqlen_q >= 0 && max_seqlen_q <= (int64_t(1) << 30),
              "%s: max_seqlen_q %lld out of range", name, (long long)max_seqlen_q);
   FK_REQUIRE(num_heads > 0 && num_kv_heads > 0 && num_heads % num_kv_heads == 0,
@@ -672,6 +702,8 @@ int prefill_entry(const char* name, bool paged, void* out, int64_t out_row_strid
              "%s: softmax scale must be positive and finite (got %g)", name, (double)scale);
   P.scale_log2 = scale * kLog2e;
   P.causal = causal ? 1 : 0;
+  P.window_left = window_left;
+  P.sinks = sinks;
   const int hsplit = (gqa + hw - 1) / hw;
   FK_REQUIRE(qblocks <= 65535, "%s: max_seqlen_q %lld needs more than 65535 query blocks", name,
              (long long)max_seqlen_q);
@@ -697,14 +729,15 @@ extern "C" int fk_paged_prefill(void* out, int64_t out_row_stride, const void* q
                                 const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
                                 int64_t batch, int64_t max_seqlen_q, int num_heads,
                                 int num_kv_heads, int head_size, int block_size,
-                                int64_t num_blocks, float scale, int causal, void* stream) {
+                                int64_t num_blocks, float scale, int causal, int window_left,
+                                const float* sinks, void* stream) {
   const int64_t row = static_cast<int64_t>(num_kv_heads) * head_size *
                       (kv_dtype == FK_DTYPE_FP8_E4M3FN ? 1 : 2);
   return fk::prefill_entry("fk_paged_prefill", true, out, out_row_stride, q, q_row_stride,
                            k_cache, row, v_cache, row, kv_dtype, k_scale, v_scale, block_tables,
                            bt_row_stride, cu_seqlens_q, cu_seqlens_k, batch, max_seqlen_q,
                            num_heads, num_kv_heads, head_size, block_size, num_blocks, scale,
-                           causal, stream);
+                           causal, window_left, sinks, stream);
 }
 
 extern "C" int fk_varlen_prefill(void* out, int64_t out_row_stride, const void* q,
@@ -713,10 +746,10 @@ extern "C" int fk_varlen_prefill(void* out, int64_t out_row_stride, const void* 
                                  const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
                                  int64_t batch, int64_t max_seqlen_q, int num_heads,
                                  int num_kv_heads, int head_size, float scale, int causal,
-                                 void* stream) {
+                                 int window_left, const float* sinks, void* stream) {
   return fk::prefill_entry("fk_varlen_prefill", false, out, out_row_stride, q, q_row_stride, key,
                            key_row_stride * 2, value, value_row_stride * 2, FK_DTYPE_BF16,
                            nullptr, nullptr, nullptr, 0, cu_seqlens_q, cu_seqlens_k, batch,
                            max_seqlen_q, num_heads, num_kv_heads, head_size, 16, 0, scale, causal,
-                           stream);
+                           window_left, sinks, stream);
 }

@@ -217,6 +217,10 @@ int fk_store_kvcache_convert(const void* key, int64_t key_row_stride, const void
  * row b, layout as fk_paged_decode).  Query j of a chunk of q_len sees keys
  * [0, k_len - q_len + j] (causal, aligned to the end); a query with no visible key gets
  * zeros.  causal = 0 lets every query see all k_len keys (flash_attn causal=False).
+ * window_left >= 0 (causal only; flash-attn window_size = (window_left, 0)) limits
+ * query j to keys [k_len - q_len + j - window_left, k_len - q_len + j]; -1 = no window.
+ * sinks: NULL or device fp32 [num_heads] attention-sink logits (s_aux), joining each
+ * row's softmax denominator as in fk_paged_decode.
  * max_seqlen_q bounds every chunk (it sizes the grid; at most 65535 blocks of 32
  * query tokens, 128 for GQA group 1).  head_size 128; GQA groups up to 16; kv dtype
  * bf16 or fp8 e4m3fn (with k_scale / v_scale as in fk_paged_decode).  No workspace;
@@ -226,19 +230,20 @@ int fk_paged_prefill(void* out, int64_t out_row_stride, const void* q, int64_t q
                      const float* v_scale, const int32_t* block_tables, int64_t bt_row_stride,
                      const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int64_t batch,
                      int64_t max_seqlen_q, int num_heads, int num_kv_heads, int head_size,
-                     int block_size, int64_t num_blocks, float scale, int causal, void* stream);
+                     int block_size, int64_t num_blocks, float scale, int causal,
+                     int window_left, const float* sinks, void* stream);
 
 /* The same attention over dense keys: FlashAttnPrefill.forward without a block table
  * (flash_attn_prefill.py:65-74; Attention._prefill_torch_from_tensors,
  * attention_impl.py:624-638).  key / value: [total_k, Hk*128] bf16 rows (strides in
  * elements; views of the qkv buffer allowed); sequence b's keys are rows
- * [cu_seqlens_k[b], cu_seqlens_k[b+1]). */
+ * [cu_seqlens_k[b], cu_seqlens_k[b+1]).  window_left and sinks as fk_paged_prefill. */
 int fk_varlen_prefill(void* out, int64_t out_row_stride, const void* q, int64_t q_row_stride,
                       const void* key, int64_t key_row_stride, const void* value,
                       int64_t value_row_stride, const int32_t* cu_seqlens_q,
                       const int32_t* cu_seqlens_k, int64_t batch, int64_t max_seqlen_q,
                       int num_heads, int num_kv_heads, int head_size, float scale, int causal,
-                      void* stream);
+                      int window_left, const float* sinks, void* stream);
 
 /* Per-head q/k RMSNorm (optional) + rotary embedding + store_kvcache in one launch:
  * the attention block between the qkv projection and the decode

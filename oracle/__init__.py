@@ -280,9 +280,11 @@ def paged_decode(q: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray,
 
 
 def _prefill_one(qq: np.ndarray, ks: np.ndarray, vs: np.ndarray, scale: float,
-                 causal: bool) -> np.ndarray:
+                 causal: bool, window_left: int = -1, sinks: np.ndarray | None = None) -> np.ndarray:
     """_sdpa_one (attention_impl.py:606-622) in float64: qq [q_len, hq, d], ks/vs
-    [k_len, hk, d]; key_offset = k_len - q_len when causal, else all keys visible."""
+    [k_len, hk, d]; key_offset = k_len - q_len when causal, else all keys visible.
+    window_left >= 0 (causal): query j also drops keys before pos_j - window_left
+    (triton_unified_attention.py:577-590); sinks as in attend_one."""
     q_len, hq, _ = qq.shape
     k_len, hk, _ = ks.shape
     grp = hq // hk
@@ -291,17 +293,25 @@ def _prefill_one(qq: np.ndarray, ks: np.ndarray, vs: np.ndarray, scale: float,
     sc = np.einsum("jhd,thd->hjt", qq.astype(np.float64), kh) * scale  # [hq, q_len, k_len]
     pos = ((k_len - q_len) + np.arange(q_len)) if causal else np.full(q_len, k_len - 1)
     mask = np.arange(k_len)[None, :] <= pos[:, None]
+    if window_left >= 0:
+        mask &= np.arange(k_len)[None, :] >= pos[:, None] - window_left
     sc = np.where(mask[None], sc, -np.inf)
     m = sc.max(axis=-1, keepdims=True) if k_len else np.full((hq, q_len, 1), -np.inf)
     has = np.isfinite(m)
+    if sinks is not None:  # the sink joins the max (only rows with a visible key matter)
+        m = np.where(has, np.maximum(m, np.asarray(sinks, np.float64).reshape(hq, 1, 1)), m)
     e = np.where(has, np.exp(sc - np.where(has, m, 0.0)), 0.0)
     l = e.sum(-1, keepdims=True)
+    if sinks is not None:
+        l = np.where(l > 0, l + np.exp(np.asarray(sinks, np.float64).reshape(hq, 1, 1)
+                                       - np.where(has, m, 0.0)), l)
     p = np.where(l > 0, e / np.where(l > 0, l, 1.0), 0.0)
     return np.einsum("hjt,thd->jhd", p, vh)
 
 
 def varlen_prefill(q: np.ndarray, key: np.ndarray, value: np.ndarray, cu_seqlens_q: np.ndarray,
-                   cu_seqlens_k: np.ndarray, scale: float, causal: bool = True) -> np.ndarray:
+                   cu_seqlens_k: np.ndarray, scale: float, causal: bool = True,
+                   window_left: int = -1, sinks: np.ndarray | None = None) -> np.ndarray:
     """_prefill_torch_from_tensors (attention_impl.py:624-638): dense keys, sequence i's
     being rows cu_k[i]..cu_k[i+1] of key/value [total_k, hk, d]."""
     out = np.zeros(q.shape, np.float64)
@@ -309,7 +319,8 @@ def varlen_prefill(q: np.ndarray, key: np.ndarray, value: np.ndarray, cu_seqlens
         qs, qe = int(cu_seqlens_q[i]), int(cu_seqlens_q[i + 1])
         ks, ke = int(cu_seqlens_k[i]), int(cu_seqlens_k[i + 1])
         if qe > qs:
-            out[qs:qe] = _prefill_one(q[qs:qe], key[ks:ke], value[ks:ke], scale, causal)
+            out[qs:qe] = _prefill_one(q[qs:qe], key[ks:ke], value[ks:ke], scale, causal,
+                                      window_left, sinks)
     return out
 
 
@@ -317,7 +328,8 @@ def paged_prefill(q: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray,
                   block_tables: np.ndarray, cu_seqlens_q: np.ndarray, cu_seqlens_k: np.ndarray,
                   scale: float, k_scale: np.ndarray | None = None,
                   v_scale: np.ndarray | None = None, q_dtype: str = "bf16",
-                  causal: bool = True) -> np.ndarray:
+                  causal: bool = True, window_left: int = -1,
+                  sinks: np.ndarray | None = None) -> np.ndarray:
     """_prefill_torch_from_cache + _sdpa_one (attention_impl.py:606-622, 640-652), the
     torch restatement of FlashAttnPrefill with a block table (flash_attn_prefill.py:28-74):
     sequence i's queries q[cu_q[i]:cu_q[i+1]] attend to the first k_len = cu_k[i+1]-cu_k[i]
@@ -335,7 +347,7 @@ def paged_prefill(q: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray,
         if fp8:
             ks = dequant_kv(ks[None], k_scale, q_dtype)[0]
             vs = dequant_kv(vs[None], v_scale, q_dtype)[0]
-        out[qs:qe] = _prefill_one(q[qs:qe], ks, vs, scale, causal)
+        out[qs:qe] = _prefill_one(q[qs:qe], ks, vs, scale, causal, window_left, sinks)
     return out
 
 

@@ -46,15 +46,15 @@ def _case(cuda, q_lens, k_lens, hq=32, hk=8, bs=16, seed=70, fp8=False, extra_pa
                 cu_k=cu_k.to(cuda), max_q=max(q_lens) if q_lens else 0, ks=t(ks), vs=t(vs))
 
 
-def _run(c, causal=True):
+def _run(c, causal=True, window_left=-1, sinks=None):
     out = torch.full_like(c["q"], float("nan"))
     ops.paged_prefill(out, c["q"], c["kc"], c["vc"], c["bt"], c["cu_q"], c["cu_k"], c["max_q"],
-                      128 ** -0.5, c["ks"], c["vs"], causal)
+                      128 ** -0.5, c["ks"], c["vs"], causal, window_left, sinks)
     torch.cuda.synchronize()
     return out
 
 
-def _oracle(c, causal=True):
+def _oracle(c, causal=True, window_left=-1, sinks=None):
     fp8 = c["kc"].dtype == torch.float8_e4m3fn
     kc = c["kc"].view(torch.uint8).cpu().numpy() if fp8 else c["kc"].float().cpu().numpy()
     vc = c["vc"].view(torch.uint8).cpu().numpy() if fp8 else c["vc"].float().cpu().numpy()
@@ -62,7 +62,8 @@ def _oracle(c, causal=True):
                                 c["cu_q"].cpu().numpy(), c["cu_k"].cpu().numpy(), 128 ** -0.5,
                                 None if c["ks"] is None else c["ks"].cpu().numpy(),
                                 None if c["vs"] is None else c["vs"].cpu().numpy(),
-                                causal=causal)
+                                causal=causal, window_left=window_left,
+                                sinks=None if sinks is None else sinks.cpu().numpy())
 
 
 def _close(got, ref, tol, what):
@@ -192,9 +193,10 @@ def test_flash_attn_prefill_candidate(cuda):
             block_table=c["bt"])
     torch.cuda.synchronize()
     _close(out, _oracle(c), 1e-2, "candidate")
-    with pytest.raises(NotImplementedError):
-        m(c["q"], c["kc"], c["vc"], c["cu_q"], c["cu_k"], 40, 50, block_table=c["bt"],
-          window_size=(128, 0))
+    out = m(c["q"], c["kc"], c["vc"], c["cu_q"], c["cu_k"], 40, 50, block_table=c["bt"],
+            window_size=(20, 0))
+    torch.cuda.synchronize()
+    _close(out, _oracle(c, window_left=20), 1e-2, "candidate, window (20, 0)")
 
 
 def test_mixed_batch_like_forward_mixed(cuda):
@@ -222,3 +224,57 @@ def test_mixed_batch_like_forward_mixed(cuda):
                     softmax_scale=128 ** -0.5, causal=True, max_seq_len=max(dec_lens))
     torch.cuda.synchronize()
     _close(out, _oracle(c), 1e-2, "mixed batch")
+
+
+@pytest.mark.parametrize("window_left", [0, 7, 31, 32, 100, 511, 4000])
+@pytest.mark.parametrize("fp8", [False, True])
+def test_paged_prefill_sliding_window_and_sinks(cuda, window_left, fp8):
+    """Causal sliding window (window_size = (window_left, 0)) across tile (16), stage
+    (32) and page edges, in whole prompts, chunks over a longer context and a
+    one-token chunk, with and without attention sinks; GQA 4 (Qwen3-8B heads)."""
+    _flush(f"prefill window={window_left} fp8={fp8}")
+    q_lens = [1, 17, 100, 257, 64]
+    k_lens = [40, 17, 612, 257, 1000]
+    c = _case(cuda, q_lens, k_lens, bs=64, seed=90 + window_left, fp8=fp8)
+    g = torch.Generator().manual_seed(91)
+    sinks = (2 * torch.randn(32, generator=g)).float().to(cuda)
+    tol = 3e-2 if fp8 else 1e-2
+    for sk in (None, sinks):
+        _close(_run(c, True, window_left, sk), _oracle(c, True, window_left, sk), tol,
+               f"window={window_left} sinks={sk is not None}")
+
+
+def test_prefill_window_sinks_dense_and_candidate(cuda):
+    """The dense path (fk_varlen_prefill) with a window and sinks, and FlashAttnPrefill
+    as Attention._forward_pure calls it (window_size, s_aux in the model dtype;
+    attention_impl.py:401-434), paged and dense; a window without causal is refused."""
+    from fastkernels_amd.candidate.L1.flash_attn_prefill import FlashAttnPrefill
+
+    q_lens, k_lens = [33, 200, 5], [33, 200, 5]
+    c = _case(cuda, q_lens, k_lens, hq=16, hk=4, bs=16, seed=92)
+    g = torch.Generator().manual_seed(93)
+    s_aux = (2 * torch.randn(16, generator=g)).to(torch.bfloat16).to(cuda)
+    ref = _oracle(c, True, 63, s_aux.float())
+    # dense keys: the sequences' pages gathered into [total_k, Hk, D]
+    bt, cu_k = c["bt"].cpu(), c["cu_k"].cpu()
+    rows = torch.cat([torch.arange(int(bt[i, t // 16]) * 16 + t % 16, int(bt[i, t // 16]) * 16
+                                   + t % 16 + 1) for i, n in enumerate(k_lens) for t in range(n)])
+    k = c["kc"].view(-1, 4, 128)[rows.to(cuda)]
+    v = c["vc"].view(-1, 4, 128)[rows.to(cuda)]
+    out = torch.full_like(c["q"], float("nan"))
+    ops.varlen_prefill(out, c["q"], k, v, c["cu_q"], c["cu_k"], c["max_q"], 128 ** -0.5, True,
+                       63, s_aux.float())
+    torch.cuda.synchronize()
+    _close(out, ref, 1e-2, "dense window + sinks")
+    mod = FlashAttnPrefill(16, 4, 128)
+    kw = dict(softmax_scale=128 ** -0.5, causal=True, window_size=(63, 0), s_aux=s_aux)
+    got = mod(c["q"], c["kc"], c["vc"], cu_seqlens_q=c["cu_q"], cu_seqlens_k=c["cu_k"],
+              max_seqlen_q=c["max_q"], max_seqlen_k=max(k_lens), block_table=c["bt"], **kw)
+    _close(got, ref, 1e-2, "candidate paged")
+    got = mod(c["q"], k.reshape(-1, 4 * 128), v.reshape(-1, 4 * 128), cu_seqlens_q=c["cu_q"],
+              cu_seqlens_k=c["cu_k"], max_seqlen_q=c["max_q"], max_seqlen_k=max(k_lens), **kw)
+    _close(got, ref, 1e-2, "candidate dense")
+    with pytest.raises(NotImplementedError):
+        mod(c["q"], c["kc"], c["vc"], cu_seqlens_q=c["cu_q"], cu_seqlens_k=c["cu_k"],
+            max_seqlen_q=c["max_q"], max_seqlen_k=max(k_lens), block_table=c["bt"],
+            causal=False, window_size=(63, 0))

@@ -475,6 +475,53 @@ def test_paged_prefill_decode_case_and_causality():
     assert np.array_equal(z[:2], np.zeros_like(z[:2])) and np.abs(z[2:]).sum() > 0
 
 
+@pytest.mark.parametrize("window_left", [0, 3, 9, 40])
+def test_paged_prefill_window_and_sinks(window_left):
+    """Prefill with a sliding window and sinks: one-query chunks equal the decode
+    (itself pinned against SDPA); a multi-query chunk equals torch's softmax over the
+    masked scores with the sink as one more column; keys before a query's window
+    start do not move its output and keys inside do."""
+    q, kc, vc, bt, cu_q, cu_k = _prefill_case(seed=25, q_lens=(1, 1), k_lens=(13, 24))
+    sinks = np.linspace(-1.0, 1.5, q.shape[1])
+    pre = oracle.paged_prefill(q, kc, vc, bt, cu_q, cu_k, 0.25, window_left=window_left,
+                               sinks=sinks)
+    dec = oracle.paged_decode(q, kc, vc, bt, np.diff(cu_k), 0.25, window_left=window_left,
+                              sinks=sinks)
+    np.testing.assert_allclose(pre, dec, rtol=1e-12, atol=1e-13)
+    q, kc, vc, bt, cu_q, cu_k = _prefill_case(seed=26, q_lens=(7,), k_lens=(19,))
+    out = oracle.paged_prefill(q, kc, vc, bt, cu_q, cu_k, 0.25, window_left=window_left,
+                               sinks=sinks)
+    hq, hk = q.shape[1], kc.shape[2]
+    ks = torch.from_numpy(oracle.gather_seq(kc, bt[0], 19)).double()[:, torch.arange(hq) // (hq // hk)]
+    vs = torch.from_numpy(oracle.gather_seq(vc, bt[0], 19)).double()[:, torch.arange(hq) // (hq // hk)]
+    qt = torch.from_numpy(q).double()  # [7, Hq, D]
+    sc = torch.einsum("jhd,thd->hjt", qt, ks) * 0.25
+    pos = torch.arange(7) + 12
+    t = torch.arange(19)
+    mask = (t[None, :] <= pos[:, None]) & (t[None, :] >= pos[:, None] - window_left)
+    sc = sc.masked_fill(~mask[None], float("-inf"))
+    sink = torch.from_numpy(sinks).double()[:, None, None].expand(hq, 7, 1)
+    p = torch.softmax(torch.cat([sc, sink], -1), -1)[..., :19]
+    ref = torch.einsum("hjt,thd->jhd", p, vs).numpy()
+    np.testing.assert_allclose(out, ref, rtol=1e-10, atol=1e-12)
+    # locality: key 12 + 3 - window_left - 1 is before query 3's window, key pos_3 is inside
+    kc2, vc2 = kc.copy(), vc.copy()
+    bs = kc.shape[1]
+    before = 12 + 3 - window_left - 1
+    if before >= 0:
+        page, slot = bt[0, before // bs], before % bs
+        kc2[page, slot] += 5.0
+        vc2[page, slot] -= 3.0
+        moved = oracle.paged_prefill(q, kc2, vc2, bt, cu_q, cu_k, 0.25, window_left=window_left,
+                                     sinks=sinks)
+        np.testing.assert_allclose(moved[3:], out[3:], rtol=1e-12, atol=1e-13)
+    page, slot = bt[0, 15 // bs], 15 % bs
+    kc2[page, slot] += 5.0
+    moved = oracle.paged_prefill(q, kc2, vc2, bt, cu_q, cu_k, 0.25, window_left=window_left,
+                                 sinks=sinks)
+    assert not np.allclose(moved[3], out[3])
+
+
 # ---------------------------------------------------------------------------
 # merge_attn_states
 # ---------------------------------------------------------------------------
