@@ -37,6 +37,9 @@ _SIGNATURES = {
                                     c_int, c_void_p]),
     "fk_store_kvcache": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p,
                                  c_void_p, c_int, c_int64, c_int64, c_int, c_int64, c_void_p]),
+    "fk_store_kvcache_hnd": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p,
+                                     c_void_p, c_int, c_int64, c_int, c_int, c_int, c_int,
+                                     c_int64, c_void_p]),
     "fk_paged_decode_plan": (c_int, [c_int64, c_int, c_int, c_int, c_int64, c_int,
                                      ctypes.POINTER(c_int64), ctypes.POINTER(c_int64),
                                      ctypes.POINTER(c_int64)]),

@@ -1,4 +1,5 @@
-"""Candidate ``RotaryEmbedding`` for fastkernels/tasks/baseline/L1/rotary_emb.py:71-191.
+"""Candidates ``RotaryEmbedding`` and ``Gemma4ProportionalRotaryEmbedding`` for
+fastkernels/tasks/baseline/L1/rotary_emb.py:71-230.
 
 Same constructor (including the Llama-3.1 frequency scaling of
 rotary_emb.py:44-68,95-102), the same ``cos_sin_cache`` buffer
@@ -132,3 +133,26 @@ class RotaryEmbedding(nn.Module):
         else:
             ops.rotary_embedding(positions, query, key, self.head_dim, cache, self.is_neox_style)
         return query, key
+
+
+class Gemma4ProportionalRotaryEmbedding(RotaryEmbedding):
+    """Gemma4 proportional RoPE (rotary_emb.py:194-230): a partial rotary factor whose
+    frequency exponents are divided by the full head dimension, the non-rotated angle
+    pairs kept as identity rotations (inv_freq 0, so cos 1 and sin 0).  The cache spans
+    the whole head, [max_position, head_dim], built by the same float32 steps as the
+    reference; forward is the base class's (NeoX pairs over the whole head)."""
+
+    def __init__(self, head_dim: int, rotary_dim: int, max_position_embeddings: int,
+                 rope_theta: float):
+        nn.Module.__init__(self)
+        self.head_dim = head_dim
+        self.is_neox_style = True
+        rope_angles = rotary_dim // 2
+        nope_angles = head_dim // 2 - rope_angles
+        exponents = torch.arange(0, 2 * rope_angles, 2, dtype=torch.float) / head_dim
+        inv_freq = 1.0 / (rope_theta ** exponents)
+        if nope_angles > 0:
+            inv_freq = torch.cat([inv_freq, torch.zeros(nope_angles, dtype=torch.float)])
+        angles = torch.outer(torch.arange(max_position_embeddings, dtype=torch.float), inv_freq)
+        cache = torch.cat((angles.cos(), angles.sin()), dim=-1).float()
+        self.register_buffer("cos_sin_cache", cache, persistent=False)

@@ -321,3 +321,130 @@ extern "C" int fk_store_kvcache_convert(const void* key, int64_t key_row_stride,
                                   value_row_stride, k_cache, v_cache, slot_mapping, tokens,
                                   row_elems, num_slots, s);
 }
+
+// ---------------------------------------------------------------------------
+// HND layout: StoreKVCacheHND (store_kvcache.py:36-99) writes token i's head h
+// row to cache[slot / page][h][slot % page][:] of a
+// [num_blocks, num_kv_heads, page_size, head_size] cache, so one token's heads
+// land page_size * head_size elements apart.  A lane moves one 16-byte chunk; a
+// (token, head) row of cpr chunks is handled by cpr consecutive lanes.
+// ---------------------------------------------------------------------------
+namespace fk {
+namespace {
+
+template <typename IdxT>
+__global__ __launch_bounds__(256) void store_kvcache_hnd_vec16(
+    const uint4* __restrict__ key, int64_t key_row_chunks, const uint4* __restrict__ value,
+    int64_t value_row_chunks, uint4* __restrict__ k_cache, uint4* __restrict__ v_cache,
+    const void* __restrict__ slot_mapping, int64_t rows, int num_kv_heads, int cpr,
+    int page_size, int64_t num_slots) {
+  const int64_t lin = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t row = lin / cpr;  // (token, head) row
+  if (row >= rows) return;
+  const int c = static_cast<int>(lin - row * cpr);
+  const int64_t tok = row / num_kv_heads;
+  const int h = static_cast<int>(row - tok * num_kv_heads);
+  // Source loads first, independent of the slot, so the wait is one round trip.
+  const uint4 kv = key[tok * key_row_chunks + static_cast<int64_t>(h) * cpr + c];
+  const uint4 vv = value[tok * value_row_chunks + static_cast<int64_t>(h) * cpr + c];
+  const int64_t slot = load_slot<IdxT>(slot_mapping, tok);
+  if (slot < 0 || slot >= num_slots) return;
+  const int64_t blk = slot / page_size;
+  const int64_t dst = ((blk * num_kv_heads + h) * page_size + (slot - blk * page_size)) * cpr + c;
+  k_cache[dst] = kv;
+  v_cache[dst] = vv;
+}
+
+template <typename IdxT, typename ElemT>
+__global__ __launch_bounds__(256) void store_kvcache_hnd_scalar(
+    const ElemT* __restrict__ key, int64_t key_row_stride, const ElemT* __restrict__ value,
+    int64_t value_row_stride, ElemT* __restrict__ k_cache, ElemT* __restrict__ v_cache,
+    const void* __restrict__ slot_mapping, int num_kv_heads, int head_size, int page_size,
+    int64_t num_slots) {
+  const int64_t tok = blockIdx.x;
+  const int h = blockIdx.y;
+  const int64_t slot = load_slot<IdxT>(slot_mapping, tok);
+  if (slot < 0 || slot >= num_slots) return;
+  const int64_t blk = slot / page_size;
+  const int64_t dst = ((blk * num_kv_heads + h) * page_size + (slot - blk * page_size)) * head_size;
+  for (int e = threadIdx.x; e < head_size; e += 256) {
+    k_cache[dst + e] = key[tok * key_row_stride + static_cast<int64_t>(h) * head_size + e];
+    v_cache[dst + e] = value[tok * value_row_stride + static_cast<int64_t>(h) * head_size + e];
+  }
+}
+
+template <typename IdxT>
+int launch_hnd(const void* key, int64_t ks, const void* value, int64_t vs, void* kc, void* vc,
+               const void* sm, int64_t tokens, int hk, int head_size, int page_size,
+               int elem_bytes, int64_t num_slots, hipStream_t stream) {
+  const int64_t head_bytes = static_cast<int64_t>(head_size) * elem_bytes;
+  const bool vec = head_bytes % 16 == 0 && (ks * elem_bytes) % 16 == 0 &&
+                   (vs * elem_bytes) % 16 == 0 && aligned16(key) && aligned16(value) &&
+                   aligned16(kc) && aligned16(vc);
+  if (vec) {
+    const int cpr = static_cast<int>(head_bytes / 16);
+    const int64_t rows = tokens * hk;
+    const int64_t blocks = (rows * cpr + 255) / 256;
+    FK_REQUIRE(blocks <= 0x7fffffffLL, "fk_store_kvcache_hnd: too many rows");
+    hipLaunchKernelGGL(store_kvcache_hnd_vec16<IdxT>, dim3(static_cast<unsigned>(blocks)),
+                       dim3(256), 0, stream, static_cast<const uint4*>(key), ks * elem_bytes / 16,
+                       static_cast<const uint4*>(value), vs * elem_bytes / 16,
+                       static_cast<uint4*>(kc), static_cast<uint4*>(vc), sm, rows, hk, cpr,
+                       page_size, num_slots);
+    return check_launch("fk_store_kvcache_hnd");
+  }
+  const dim3 grid(static_cast<unsigned>(tokens), static_cast<unsigned>(hk));
+  switch (elem_bytes) {
+    case 1:
+      hipLaunchKernelGGL((store_kvcache_hnd_scalar<IdxT, uint8_t>), grid, dim3(256), 0, stream,
+                         static_cast<const uint8_t*>(key), ks, static_cast<const uint8_t*>(value),
+                         vs, static_cast<uint8_t*>(kc), static_cast<uint8_t*>(vc), sm, hk,
+                         head_size, page_size, num_slots);
+      break;
+    case 2:
+      hipLaunchKernelGGL((store_kvcache_hnd_scalar<IdxT, uint16_t>), grid, dim3(256), 0, stream,
+                         static_cast<const uint16_t*>(key), ks,
+                         static_cast<const uint16_t*>(value), vs, static_cast<uint16_t*>(kc),
+                         static_cast<uint16_t*>(vc), sm, hk, head_size, page_size, num_slots);
+      break;
+    default:
+      hipLaunchKernelGGL((store_kvcache_hnd_scalar<IdxT, uint32_t>), grid, dim3(256), 0, stream,
+                         static_cast<const uint32_t*>(key), ks,
+                         static_cast<const uint32_t*>(value), vs, static_cast<uint32_t*>(kc),
+                         static_cast<uint32_t*>(vc), sm, hk, head_size, page_size, num_slots);
+      break;
+  }
+  return check_launch("fk_store_kvcache_hnd");
+}
+
+}  // namespace
+}  // namespace fk
+
+extern "C" int fk_store_kvcache_hnd(const void* key, int64_t key_row_stride, const void* value,
+                                    int64_t value_row_stride, void* k_cache, void* v_cache,
+                                    const void* slot_mapping, int slot_is_i64, int64_t tokens,
+                                    int num_kv_heads, int head_size, int page_size,
+                                    int elem_bytes, int64_t num_slots, void* stream) {
+  const char* name = "fk_store_kvcache_hnd";
+  FK_REQUIRE(tokens >= 0 && num_kv_heads > 0 && head_size > 0 && num_slots >= 0,
+             "%s: bad size (tokens=%lld heads=%d head_size=%d)", name, (long long)tokens,
+             num_kv_heads, head_size);
+  FK_REQUIRE(num_kv_heads <= 65535, "%s: too many kv heads (%d)", name, num_kv_heads);
+  FK_REQUIRE(page_size > 0, "%s: page_size %d must be positive", name, page_size);
+  FK_REQUIRE(elem_bytes == 1 || elem_bytes == 2 || elem_bytes == 4,
+             "%s: elem_bytes must be 1, 2 or 4 (got %d)", name, elem_bytes);
+  FK_REQUIRE(tokens <= 0x7fffffffLL, "%s: too many tokens (%lld)", name, (long long)tokens);
+  const int64_t row = static_cast<int64_t>(num_kv_heads) * head_size;
+  FK_REQUIRE(key_row_stride >= row && value_row_stride >= row,
+             "%s: row stride shorter than num_kv_heads * head_size", name);
+  if (tokens == 0) return FK_OK;
+  FK_REQUIRE(key && value && k_cache && v_cache && slot_mapping, "%s: null pointer", name);
+  hipStream_t s = fk::as_stream(stream);
+  if (slot_is_i64)
+    return fk::launch_hnd<int64_t>(key, key_row_stride, value, value_row_stride, k_cache, v_cache,
+                                   slot_mapping, tokens, num_kv_heads, head_size, page_size,
+                                   elem_bytes, num_slots, s);
+  return fk::launch_hnd<int32_t>(key, key_row_stride, value, value_row_stride, k_cache, v_cache,
+                                 slot_mapping, tokens, num_kv_heads, head_size, page_size,
+                                 elem_bytes, num_slots, s);
+}

@@ -203,6 +203,45 @@ def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
                  num_slots, _stream(key))
 
 
+
+def store_kvcache_hnd(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
+                      v_cache: torch.Tensor, slot_mapping: torch.Tensor,
+                      page_size: int | None = None) -> None:
+    """Scatter key/value [N, Hk, D] rows into HND caches [num_blocks, Hk, page_size, D]:
+    token i's head h row goes to cache[s // page_size, h, s % page_size] with
+    s = slot_mapping[i] (-1 skips), bit for bit (StoreKVCacheHND, store_kvcache.py:85-99).
+    Key and cache dtypes must match (a converting HND store is not provided)."""
+    if key.dim() != 3 or value.shape != key.shape:
+        raise ValueError("store_kvcache_hnd: key/value must be [N, num_kv_heads, head_dim]")
+    n, hk, hd = key.shape
+    if k_cache.dim() != 4 or v_cache.shape != k_cache.shape or k_cache.shape[1] != hk or \
+            k_cache.shape[3] != hd:
+        raise ValueError("store_kvcache_hnd: caches must be [num_blocks, Hk, page_size, D]")
+    page = k_cache.shape[2] if page_size is None else int(page_size)
+    if page != k_cache.shape[2]:
+        raise ValueError(f"store_kvcache_hnd: page_size {page} != cache dim 2 "
+                         f"({k_cache.shape[2]})")
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("store_kvcache_hnd: caches must be contiguous")
+    if not (key.dtype == value.dtype == k_cache.dtype == v_cache.dtype):
+        raise TypeError("store_kvcache_hnd: key, value and both caches must share a dtype")
+    if key.element_size() not in (1, 2, 4):
+        raise TypeError(f"store_kvcache_hnd: element size {key.element_size()} unsupported")
+    for t, nm in ((key, "key"), (value, "value")):
+        if t.stride(2) != 1 or (hk > 1 and t.stride(1) != hd):
+            raise ValueError(f"store_kvcache_hnd: {nm} rows must be [Hk, D] contiguous")
+    if slot_mapping.dtype not in (torch.int32, torch.int64) or not slot_mapping.is_contiguous():
+        raise TypeError("store_kvcache_hnd: slot_mapping must be contiguous int32 or int64")
+    if slot_mapping.numel() < n:
+        raise ValueError("store_kvcache_hnd: slot_mapping shorter than the token count")
+    _same_device(key, value, k_cache, v_cache, slot_mapping)
+    if n == 0:
+        return
+    _native.call("fk_store_kvcache_hnd", _ptr(key), key.stride(0), _ptr(value), value.stride(0),
+                 _ptr(k_cache), _ptr(v_cache), _ptr(slot_mapping),
+                 int(slot_mapping.dtype == torch.int64), n, hk, hd, page, key.element_size(),
+                 k_cache.shape[0] * page, _stream(key))
+
 # ---------------------------------------------------------------------------
 # Fused per-head q/k RMSNorm + rotary + store_kvcache
 # ---------------------------------------------------------------------------
@@ -579,6 +618,8 @@ _LIB.define("rotary_embedding(Tensor positions, Tensor(a!) query, Tensor(b!)? ke
             "int head_size, Tensor cos_sin_cache, bool is_neox) -> ()")
 _LIB.define("store_kvcache(Tensor key, Tensor value, Tensor(a!) k_cache, Tensor(b!) v_cache, "
             "Tensor slot_mapping) -> ()")
+_LIB.define("store_kvcache_hnd(Tensor key, Tensor value, Tensor(a!) k_cache, Tensor(b!) v_cache, "
+            "Tensor slot_mapping, int? page_size=None) -> ()")
 _LIB.define("paged_decode(Tensor(a!) out, Tensor q, Tensor k_cache, Tensor v_cache, "
             "Tensor block_table, Tensor cache_seqlens, float softmax_scale, int part_tokens, "
             "int max_parts, Tensor(b!)? workspace, Tensor? k_scale, Tensor? v_scale, "
@@ -608,6 +649,7 @@ _IMPLS = {
     "fused_add_rmsnorm": fused_add_rms_norm,
     "rotary_embedding": rotary_embedding,
     "store_kvcache": store_kvcache,
+    "store_kvcache_hnd": store_kvcache_hnd,
     "paged_decode": paged_decode,
     "silu_and_mul": lambda result, input: silu_and_mul(result, input),
     "merge_attn_states": merge_attn_states,

@@ -42,6 +42,9 @@
  *   fk_store_kvcache_convert
  *       fastkernels/tasks/baseline/L1/store_kvcache.py:16-35,71-82 (StoreKVCache.forward
  *       when key and cache dtypes differ).
+ *   fk_store_kvcache_hnd
+ *       fastkernels/tasks/baseline/L1/store_kvcache.py:36-68,85-99 (Triton
+ *       _store_kvcache_hnd_kernel, StoreKVCacheHND.forward, HND layout).
  *   fk_paged_prefill, fk_varlen_prefill
  *       fastkernels/tasks/baseline/L1/flash_attn_prefill.py:18-74 (FlashAttnPrefill.forward,
  *       with and without block_table).
@@ -121,6 +124,19 @@ int fk_store_kvcache(const void* key, int64_t key_row_stride, const void* value,
                      int64_t value_row_stride, void* k_cache, void* v_cache,
                      const void* slot_mapping, int slot_is_i64, int64_t tokens,
                      int64_t row_elems, int elem_bytes, int64_t num_slots, void* stream);
+
+/* store_kvcache into the HND paged layout [num_blocks, num_kv_heads, page_size,
+ * head_size] (a bit-exact scatter): for i < tokens with s = slot_mapping[i] in
+ * [0, num_slots), head h's row of key/value goes to
+ *   cache[((s / page_size) * num_kv_heads + h) * page_size + s % page_size][0 : head_size].
+ * key/value rows `*_row_stride` elements apart, heads head_size apart within a row.
+ * Slots outside [0, num_slots) are skipped.  elem_bytes 1, 2 or 4.
+ * Replaces StoreKVCacheHND.forward (store_kvcache.py:85-99, kernel :36-68). */
+int fk_store_kvcache_hnd(const void* key, int64_t key_row_stride, const void* value,
+                         int64_t value_row_stride, void* k_cache, void* v_cache,
+                         const void* slot_mapping, int slot_is_i64, int64_t tokens,
+                         int num_kv_heads, int head_size, int page_size, int elem_bytes,
+                         int64_t num_slots, void* stream);
 
 /* Chooses the schedule of a paged-decode launch (host-only; may query the
  * device's CU count once).  Outputs:

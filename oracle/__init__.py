@@ -200,6 +200,22 @@ def store_kvcache(key: np.ndarray, value: np.ndarray, k_cache: np.ndarray, v_cac
 # ---------------------------------------------------------------------------
 
 
+def store_kvcache_hnd(key: np.ndarray, value: np.ndarray, k_cache: np.ndarray,
+                      v_cache: np.ndarray, slot_mapping: np.ndarray, page_size: int):
+    """StoreKVCacheHND (store_kvcache.py:36-68, 85-99) on copies of the caches:
+    caches [num_blocks, Hk, page_size, D]; token i's head h row goes to
+    cache[s // page_size, h, s % page_size] for s = slot_mapping[i] >= 0 (and, as the
+    kernel does, slots past the cache are skipped)."""
+    kc, vc = k_cache.copy(), v_cache.copy()
+    nslots = kc.shape[0] * page_size
+    for i, s in enumerate(np.asarray(slot_mapping, np.int64)[:key.shape[0]]):
+        if s < 0 or s >= nslots:
+            continue
+        kc[s // page_size, :, s % page_size] = key[i]
+        vc[s // page_size, :, s % page_size] = value[i]
+    return kc, vc
+
+
 def gather_seq(cache: np.ndarray, block_row: np.ndarray, length: int) -> np.ndarray:
     """_cache_seq (attention_impl.py:598-604): the first `length` token rows of a sequence."""
     bs = cache.shape[1]

@@ -111,6 +111,47 @@ def test_rotary_cache_matches_reference_construction():
     assert "cos_sin_cache" not in m.state_dict()  # non-persistent, as the reference
 
 
+def test_gemma4_proportional_rotary_cache():
+    """Gemma4ProportionalRotaryEmbedding (rotary_emb.py:194-230): the reference's
+    constructor, a [max_pos, head_dim] cache whose rotated pairs use exponents over the
+    full head dim and whose remaining pairs are identity (cos 1, sin 0); dividing by
+    rotary_dim instead would be caught."""
+    mod = load_by_path("rotary_emb")
+    G = mod.Gemma4ProportionalRotaryEmbedding
+    assert issubclass(G, mod.RotaryEmbedding)
+    params = [p for p in inspect.signature(G.__init__).parameters if p != "self"]
+    assert params == ["head_dim", "rotary_dim", "max_position_embeddings", "rope_theta"]
+    m = G(256, 64, 1000, 1e6)
+    c = m.cos_sin_cache
+    assert c.dtype == torch.float32 and tuple(c.shape) == (1000, 256)
+    cos, sin = c[:, :128].double(), c[:, 128:].double()
+    assert torch.equal(cos[:, 32:], torch.ones_like(cos[:, 32:]))
+    assert torch.equal(sin[:, 32:], torch.zeros_like(sin[:, 32:]))
+    i = torch.arange(32, dtype=torch.float64)
+    t = torch.arange(1000, dtype=torch.float64)[:, None]
+    ang = t * (1e6 ** (-2 * i / 256))[None]
+    torch.testing.assert_close(cos[:, :32], torch.cos(ang), atol=5e-4, rtol=0)
+    torch.testing.assert_close(sin[:, :32], torch.sin(ang), atol=5e-4, rtol=0)
+    wrong = t * (1e6 ** (-2 * i / 64))[None]
+    assert not torch.allclose(cos[:, :32], torch.cos(wrong), atol=1e-2)
+    assert m.is_neox_style and m.head_dim == 256 and "cos_sin_cache" not in m.state_dict()
+
+
+def test_store_kvcache_hnd_class():
+    """StoreKVCacheHND(page_size).forward(key, value, k_cache, v_cache, slot_mapping)
+    (store_kvcache.py:85-99); CPU tensors are refused, not computed."""
+    H = load_by_path("store_kvcache").StoreKVCacheHND
+    assert [p for p in inspect.signature(H.__init__).parameters if p != "self"] == ["page_size"]
+    assert [p for p in inspect.signature(H.forward).parameters if p != "self"] == \
+        ["key", "value", "k_cache", "v_cache", "slot_mapping"]
+    m = H(16)
+    assert m.page_size == 16
+    kv = torch.zeros(3, 2, 128, dtype=torch.bfloat16)
+    cache = torch.zeros(4, 2, 16, 128, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="GPU"):
+        m(kv, kv, cache, cache, torch.zeros(3, dtype=torch.int64))
+
+
 def test_rotary_llama31_scaling():
     """Llama-3.1 frequency scaling (rotary_emb.py:44-68): high frequencies kept, low
     frequencies divided by the factor, a smooth blend in between."""

@@ -105,6 +105,61 @@ def test_store_kvcache_dtypes(cuda, dtype, hk, d):
     assert np.array_equal(raw(kc), ek) and np.array_equal(raw(vc), ev)
 
 
+@pytest.mark.parametrize("dtype,hk,d,page", [(torch.bfloat16, 8, 128, 16), (torch.bfloat16, 8, 128, 64),
+                                             (torch.float8_e4m3fn, 4, 128, 32),
+                                             (torch.float32, 2, 64, 16), (torch.bfloat16, 3, 5, 8)])
+@pytest.mark.parametrize("slot_dtype", [torch.int64, torch.int32])
+def test_store_kvcache_hnd_bitexact(cuda, dtype, hk, d, page, slot_dtype):
+    """StoreKVCacheHND (store_kvcache.py:85-99): HND caches [num_blocks, Hk, page, D],
+    key/value as strided views of a fused qkv row, slots -1 and past the end skipped;
+    the 16-byte path and the element path (D = 5)."""
+    from fastkernels_amd.candidate.L1.store_kvcache import StoreKVCacheHND
+
+    g = torch.Generator().manual_seed(13 + d + page)
+    n, nb, hq = 300, 40, 2 * hk
+    qkv = torch.randn(n, (hq + 2 * hk) * d, generator=g).to(dtype).to(cuda)
+    k = qkv[:, hq * d:(hq + hk) * d].view(n, hk, d)
+    v = qkv[:, (hq + hk) * d:].view(n, hk, d)
+    slots = torch.randperm(nb * page, generator=g)[:n] if n <= nb * page else None
+    if slots is None:
+        pytest.skip("cache too small for distinct slots")
+    slots[::7] = -1
+    slots[5] = nb * page + 2
+    kc = torch.zeros(nb, hk, page, d, dtype=dtype, device=cuda)
+    vc = torch.zeros_like(kc)
+    StoreKVCacheHND(page)(k, v, kc, vc, slots.to(slot_dtype).to(cuda))
+    torch.cuda.synchronize()
+    iv = {1: torch.int8, 2: torch.int16, 4: torch.int32}[kc.element_size()]
+    raw = lambda t: t.contiguous().view(iv).cpu().numpy()  # noqa: E731
+    z = np.zeros(kc.shape, raw(kc).dtype)
+    ek, ev = oracle.store_kvcache_hnd(raw(k), raw(v), z, z, slots.numpy(), page)
+    assert np.array_equal(raw(kc), ek) and np.array_equal(raw(vc), ev)
+
+
+def test_gemma4_proportional_rotary(cuda):
+    """Gemma4ProportionalRotaryEmbedding: base-class forward over the whole head with the
+    proportional cache (identity pairs past rotary_dim), against the oracle's NeoX
+    rotation with the same cache."""
+    from fastkernels_amd.candidate.L1.rotary_emb import Gemma4ProportionalRotaryEmbedding
+
+    g = torch.Generator().manual_seed(17)
+    t, hq, hk, d = 64, 8, 2, 256
+    rope = Gemma4ProportionalRotaryEmbedding(d, 64, 4096, 1e6).to(cuda)
+    qkv = torch.randn(t, (hq + 2 * hk) * d, generator=g).to(torch.bfloat16).to(cuda)
+    q, k = qkv[:, :hq * d], qkv[:, hq * d:(hq + hk) * d]
+    pos = torch.randint(0, 4096, (t,), generator=g).to(cuda)
+    q0, k0 = f32(q), f32(k)
+    rope(pos, q, k)
+    torch.cuda.synchronize()
+    rq, rk = oracle.rotary(pos.cpu().numpy(), q0, k0, d, f32(rope.cos_sin_cache), True, "bf16")
+    assert_close(f32(q), rq, BF16_TOL, BF16_TOL, "q")
+    assert_close(f32(k), rk, BF16_TOL, BF16_TOL, "k")
+    # the identity pairs (dims 32..127 and 160..255 of each head) are untouched
+    qh, q0h = f32(q).reshape(t, hq, d), q0.reshape(t, hq, d)
+    assert np.array_equal(qh[..., 32:128], q0h[..., 32:128])
+    assert np.array_equal(qh[..., 160:], q0h[..., 160:])
+
+
 # ---------------------------------------------------------------------------
 # RMSNorm
 # ---------------------------------------------------------------------------

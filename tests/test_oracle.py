@@ -231,6 +231,32 @@ def test_store_kvcache_vs_loop():
     assert np.array_equal(ek.reshape(nb * bs, -1)[untouched], kc.reshape(nb * bs, -1)[untouched])
 
 
+def test_store_kvcache_hnd_is_the_nhd_store_transposed():
+    """The HND store equals the NHD store with the cache's head and slot axes swapped
+    (a closed-form relation between the two layouts); a swapped (page, head) index is
+    caught."""
+    nb, bs, hk, d, n = 5, 8, 3, 4, 25
+    key = RNG.integers(-30000, 30000, (n, hk, d)).astype(np.int16)
+    val = RNG.integers(-30000, 30000, (n, hk, d)).astype(np.int16)
+    slots = RNG.permutation(nb * bs)[:n]
+    slots[[0, 9]] = -1
+    slots[4] = nb * bs + 3  # past the cache: skipped
+    kc_hnd = RNG.integers(-5, 5, (nb, hk, bs, d)).astype(np.int16)
+    vc_hnd = kc_hnd.copy()
+    ek, ev = oracle.store_kvcache_hnd(key, val, kc_hnd, vc_hnd, slots, bs)
+    nhd_k = np.ascontiguousarray(kc_hnd.transpose(0, 2, 1, 3))
+    nhd_v = np.ascontiguousarray(vc_hnd.transpose(0, 2, 1, 3))
+    sl = np.where(slots >= nb * bs, -1, slots)
+    rk, rv = oracle.store_kvcache(key, val, nhd_k, nhd_v, sl)
+    assert np.array_equal(ek, rk.transpose(0, 2, 1, 3))
+    assert np.array_equal(ev, rv.transpose(0, 2, 1, 3))
+    wrong = kc_hnd.copy()
+    for i, s_ in enumerate(sl):
+        if s_ >= 0:
+            wrong[s_ // bs, :, s_ % bs] = key[i][::-1]  # heads reversed
+    assert not np.array_equal(wrong, ek)
+
+
 # ---------------------------------------------------------------------------
 # Paged decode attention
 # ---------------------------------------------------------------------------
