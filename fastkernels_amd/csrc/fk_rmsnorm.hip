@@ -8,21 +8,24 @@
 //   out      = cast(fp32(x_hat) * fp32(weight))
 // where cast() rounds to the tensor dtype (round-to-nearest-even).
 //
-// MI355X mapping: one wave64 per row.  The row stays in VGPRs between the
-// sum-of-squares pass and the normalise pass, so HBM traffic is the minimal
-// read x, read residual, write residual, write x (the vLLM kernel re-reads the
-// residual for its second pass, rms_norm.cu:1370-1407).  Every access is a
-// 16-byte vector; the row reduction is a 6-step wave64 butterfly.  Rows that
-// do not fit the register-resident path use a work-group-per-row kernel that
-// re-reads the row.
+// MI355X mapping: one work-group of W wave64s per row (W = 1 up to 128
+// 16-byte vectors, else 4: one wave per SIMD, so a long row's conversion and
+// normalisation work is spread over the CU instead of one SIMD).  The row stays
+// in VGPRs between the sum-of-squares pass and the normalise pass, so HBM
+// traffic is the minimal read x, read residual, write residual, write x (the
+// vLLM kernel re-reads the residual for its second pass, rms_norm.cu:
+// 1370-1407).  Every access is a 16-byte vector; the row reduction is a 6-step
+// wave64 butterfly, then LDS across the W waves.  Rows that do not fit the
+// register-resident path use a work-group-per-row kernel that re-reads the row.
 #include "fk_common.h"
 
 namespace fk {
 namespace {
 
-// One wave per row; each lane holds VPT 16-byte vectors of the row.
-template <typename T, int VPT, bool kFused>
-__global__ __launch_bounds__(64) void rmsnorm_wave_row(
+// W waves per row; each lane holds VPT 16-byte vectors of the row (vector
+// tid + 64 W j, j < VPT).
+template <typename T, int VPT, int W, bool kFused>
+__global__ __launch_bounds__(64 * W) void rmsnorm_wave_row(
     typename T::storage* out, int64_t out_row_stride,  // may alias x (fused, in place)
     typename T::storage* x, int64_t x_row_stride,
     typename T::storage* __restrict__ residual, int64_t residual_row_stride,
@@ -30,7 +33,7 @@ __global__ __launch_bounds__(64) void rmsnorm_wave_row(
   using V = Vec16<T>;
   constexpr int N = V::N;
   const int64_t row = blockIdx.x;
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x;  // 0 .. 64 W - 1
   const int64_t nvec = hidden / N;
   const uint4* xr = reinterpret_cast<const uint4*>(x + row * x_row_stride);
 
@@ -42,7 +45,7 @@ __global__ __launch_bounds__(64) void rmsnorm_wave_row(
   V xv[VPT];
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
-    const int64_t vi = lane + 64 * j;
+    const int64_t vi = lane + 64 * W * j;
     xv[j].raw = xr[vi < nvec ? vi : nvec - 1];
   }
   // The weight row is needed only after the reduction; issue it now.
@@ -50,7 +53,7 @@ __global__ __launch_bounds__(64) void rmsnorm_wave_row(
   V wv[VPT];
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
-    const int64_t vi = lane + 64 * j;
+    const int64_t vi = lane + 64 * W * j;
     wv[j].raw = wr[vi < nvec ? vi : nvec - 1];
   }
   if constexpr (kFused) {
@@ -58,12 +61,12 @@ __global__ __launch_bounds__(64) void rmsnorm_wave_row(
     V rv[VPT];
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
-      const int64_t vi = lane + 64 * j;
+      const int64_t vi = lane + 64 * W * j;
       rv[j].raw = rr[vi < nvec ? vi : nvec - 1];
     }
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
-      const int64_t vi = lane + 64 * j;
+      const int64_t vi = lane + 64 * W * j;
       const bool in_row = vi < nvec;
       V nr;
 #pragma unroll
@@ -77,7 +80,7 @@ __global__ __launch_bounds__(64) void rmsnorm_wave_row(
   } else {
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
-      const bool in_row = lane + 64 * j < nvec;
+      const bool in_row = lane + 64 * W * j < nvec;
 #pragma unroll
       for (int e = 0; e < N; ++e) {
         s[j][e] = T::to_f32(xv[j].e[e]);
@@ -86,11 +89,19 @@ __global__ __launch_bounds__(64) void rmsnorm_wave_row(
     }
   }
   ss = wave_sum(ss);
+  if constexpr (W > 1) {
+    __shared__ float red[W];
+    if ((lane & 63) == 0) red[lane >> 6] = ss;
+    __syncthreads();
+    ss = red[0];
+#pragma unroll
+    for (int w = 1; w < W; ++w) ss += red[w];
+  }
   const float inv = rms_inv(ss, static_cast<float>(hidden), eps);
   uint4* orow = reinterpret_cast<uint4*>(out + row * out_row_stride);
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
-    const int64_t vi = lane + 64 * j;
+    const int64_t vi = lane + 64 * W * j;
     V ov;
 #pragma unroll
     for (int e = 0; e < N; ++e) ov.e[e] = rms_apply<T>(s[j][e], inv, T::to_f32(wv[j].e[e]));
@@ -153,19 +164,23 @@ int launch_t(void* out, int64_t out_row_stride, void* x, int64_t x_row_stride, v
   auto* xp = static_cast<S*>(x);
   auto* rp = static_cast<S*>(residual);
   const auto* wp = static_cast<const S*>(weight);
-#define FK_RMS_WAVE(VPT)                                                                       \
-  hipLaunchKernelGGL((rmsnorm_wave_row<T, VPT, kFused>), grid, dim3(64), 0, stream, o,          \
+#define FK_RMS_WAVE(VPT, W)                                                                    \
+  hipLaunchKernelGGL((rmsnorm_wave_row<T, VPT, W, kFused>), grid, dim3(64 * W), 0, stream, o,   \
                      out_row_stride, xp, x_row_stride, rp, residual_row_stride, wp, hidden, eps)
   if (vec && nvec <= 64) {
-    FK_RMS_WAVE(1);
+    FK_RMS_WAVE(1, 1);
   } else if (vec && nvec <= 128) {
-    FK_RMS_WAVE(2);
+    FK_RMS_WAVE(2, 1);
   } else if (vec && nvec <= 256) {
-    FK_RMS_WAVE(4);
+    FK_RMS_WAVE(1, 4);
   } else if (vec && nvec <= 512) {
-    FK_RMS_WAVE(8);
+    FK_RMS_WAVE(2, 4);
   } else if (vec && nvec <= 1024) {
-    FK_RMS_WAVE(16);
+    FK_RMS_WAVE(4, 4);
+  } else if (vec && nvec <= 2048) {
+    FK_RMS_WAVE(8, 4);
+  } else if (vec && nvec <= 4096) {
+    FK_RMS_WAVE(16, 4);
   } else {
     hipLaunchKernelGGL((rmsnorm_block_row<T, kFused>), grid, dim3(256), 0, stream, o,
                        out_row_stride, xp, x_row_stride, rp, residual_row_stride, wp, hidden,
