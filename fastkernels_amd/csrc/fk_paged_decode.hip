@@ -281,8 +281,12 @@ struct WaveState {
 #pragma unroll
     for (int d = 0; d < 8; ++d) o[d] = floatx4_t{0.f, 0.f, 0.f, 0.f};
 
+    // Visible tokens are [key_lo, tok_end): one unsigned compare of tok - key_lo
+    // against their count checks both bounds.
+    const uint32_t span = static_cast<uint32_t>(tok_end - key_lo);
     // One 16-token tile: scores, online softmax update, P.V accumulation.
     auto process = [&](int tok0, int64_t page, const TileRegs<kFp8>& cur) {
+      const int rel0 = tok0 + 4 * g - key_lo;
       uint4 kc[4];
       k_chunks(cur, kc);
       const floatx4_t acc = qk_scores(kc, qb);
@@ -290,8 +294,7 @@ struct WaveState {
       float mt = kNegInf;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int tok = tok0 + 4 * g + i;
-        const bool ok = head_ok && page >= 0 && tok < tok_end && tok >= key_lo;
+        const bool ok = head_ok && page >= 0 && static_cast<uint32_t>(rel0 + i) < span;
         s[i] = ok ? acc[i] * s2 : kNegInf;
         mt = fmaxf(mt, s[i]);
       }
@@ -324,9 +327,8 @@ struct WaveState {
       uint4 vr[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        vr[i] = (page >= 0 && tok0 + 4 * g + i < tok_end && tok0 + 4 * g + i >= key_lo)
-                    ? v_row(cur, i)
-                    : make_uint4(0, 0, 0, 0);
+        vr[i] = (page >= 0 && static_cast<uint32_t>(rel0 + i) < span) ? v_row(cur, i)
+                                                                     : make_uint4(0, 0, 0, 0);
       pv_accumulate(o, pa, vr);
     };
 
