@@ -370,6 +370,32 @@ def test_paged_decode_balanced_schedule(cuda, lens):
             assert not got[i].any()
 
 
+def test_paged_decode_batch_above_balanced_limit(cuda):
+    """More than 8192 sequences: the plan falls back to fixed partitions (the balanced
+    schedule keeps its tile prefix sums in LDS); every row against the oracle, empty
+    sequences zero, with and without a window and sinks."""
+    _flush("decode batch 9000 (fixed-partition fallback)")
+    rng = np.random.default_rng(97)
+    lens = rng.integers(0, 40, 9000).tolist()
+    bs = 16
+    pool = sum((n + bs - 1) // bs for n in lens) + 2
+    case = workloads.c3_decode(cuda, num_heads=8, kv_heads=2, block_size=bs, pool_blocks=pool,
+                               ctx_lens=lens, seed=98)
+    plan = ops.paged_decode_plan(9000, 8, 2, 128, case.max_seq_len, 0)
+    assert plan.part_tokens > 0  # fixed partitions
+    seqs = list(range(0, 9000, 37))
+    got = f32(run_decode_ws(case))
+    assert_close(got[seqs], oracle_decode(case, seqs)[seqs], BF16_TOL, BF16_TOL, "batch 9000")
+    for i, n in enumerate(lens):
+        if n == 0:
+            assert not got[i].any()
+    g = torch.Generator().manual_seed(99)
+    sinks = torch.randn(8, generator=g).float().to(cuda)
+    got = f32(run_decode_ws(case, 0, 7, sinks))
+    assert_close(got[seqs], oracle_decode(case, seqs, window_left=7, sinks=sinks)[seqs], BF16_TOL,
+                 BF16_TOL, "batch 9000, window 7 + sinks")
+
+
 def test_paged_decode_workspace_reuse(cuda):
     """One workspace across repeated balanced launches and interleaved fixed-partition
     launches (stale partials from an earlier call never leak into a later one)."""
