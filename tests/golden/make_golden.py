@@ -128,6 +128,19 @@ def cases() -> dict[str, dict[str, np.ndarray]]:
     oq, ok = oracle.rotary(posq, qn, kn, 64, cs64, True, "bf16")
     out["qk_norm_rope"] = dict(positions=posq, q=qh, k=kh, q_weight=qw, k_weight=kw,
                                cos_sin=cs64, eps=np.float32(1e-6), out_q=oq, out_k=ok)
+    # Sliding window + attention sinks (flash-attn window_size = (w, 0), s_aux) on the
+    # inputs of paged_decode_bf16 (window 20) and paged_prefill_bf16 (window 6): these
+    # fixtures hold only the window, the sinks (their own generator) and the output.
+    r3 = np.random.default_rng(2003)
+    sinks8 = (2 * r3.standard_normal(8)).astype(np.float32)
+    out["paged_decode_window_sinks"] = dict(
+        window_left=np.int64(20), sinks=sinks8,
+        out=oracle.paged_decode(q, kcache, vcache, bt, lens, float(scale), window_left=20,
+                                sinks=sinks8).astype(np.float32))
+    out["paged_prefill_window_sinks"] = dict(
+        window_left=np.int64(6), sinks=sinks8,
+        out=oracle.paged_prefill(qp, kcp, vcp, btp, cu_q, cu_k, float(scale), window_left=6,
+                                 sinks=sinks8).astype(np.float32))
     return out
 
 

@@ -27,7 +27,7 @@ def test_fixture_set_present():
     assert {"rmsnorm_h256", "rmsnorm_h200", "rotary_neox", "rotary_gptj", "store_kvcache",
             "paged_decode_bf16", "paged_decode_fp8", "silu_and_mul_d96",
             "silu_and_mul_d13", "merge_attn_states", "paged_prefill_bf16",
-            "qk_norm_rope"} <= names
+            "qk_norm_rope", "paged_decode_window_sinks", "paged_prefill_window_sinks"} <= names
 
 
 @pytest.mark.parametrize("h", [256, 200])
@@ -79,6 +79,20 @@ def test_oracle_prefill_golden():
     out = oracle.paged_prefill(g["q"], g["k_cache"], g["v_cache"], g["block_tables"],
                                g["cu_seqlens_q"], g["cu_seqlens_k"], float(g["scale"]))
     assert np.array_equal(out.astype(np.float32), g["out"])
+
+
+def test_oracle_window_sinks_golden():
+    """Window + sinks fixtures, on the inputs of the plain decode / prefill fixtures."""
+    g, w = load("paged_decode_bf16"), load("paged_decode_window_sinks")
+    out = oracle.paged_decode(g["q"], g["k_cache"], g["v_cache"], g["block_tables"], g["ctx_lens"],
+                              float(g["scale"]), window_left=int(w["window_left"]),
+                              sinks=w["sinks"])
+    assert np.array_equal(out.astype(np.float32), w["out"])
+    g, w = load("paged_prefill_bf16"), load("paged_prefill_window_sinks")
+    out = oracle.paged_prefill(g["q"], g["k_cache"], g["v_cache"], g["block_tables"],
+                               g["cu_seqlens_q"], g["cu_seqlens_k"], float(g["scale"]),
+                               window_left=int(w["window_left"]), sinks=w["sinks"])
+    assert np.array_equal(out.astype(np.float32), w["out"])
 
 
 def test_oracle_qk_norm_rope_golden():
@@ -187,6 +201,29 @@ def test_gpu_golden_all(cuda):
                       float(g["scale"]))
     torch.cuda.synchronize()
     _close(f32(out), g["out"], 1e-2)
+    w = load("paged_prefill_window_sinks")
+    out = torch.full_like(q, float("nan"))
+    ops.paged_prefill(out, q, _t(g["k_cache"], cuda, bf), _t(g["v_cache"], cuda, bf),
+                      _t(g["block_tables"], cuda), _t(g["cu_seqlens_q"], cuda),
+                      _t(g["cu_seqlens_k"], cuda), int(np.diff(g["cu_seqlens_q"]).max()),
+                      float(g["scale"]), window_left=int(w["window_left"]),
+                      sinks=_t(w["sinks"], cuda))
+    torch.cuda.synchronize()
+    _close(f32(out), w["out"], 1e-2)
+
+    g, w = load("paged_decode_bf16"), load("paged_decode_window_sinks")
+    q = _t(g["q"], cuda, bf)
+    kc, vc = _t(g["k_cache"], cuda, bf), _t(g["v_cache"], cuda, bf)
+    b, hq, d = q.shape
+    for splits in (0, 2):
+        plan = ops.paged_decode_plan(b, hq, kc.shape[2], d, int(g["ctx_lens"].max()), splits)
+        ws = torch.zeros(max(1, plan.workspace_bytes), dtype=torch.uint8, device=cuda)
+        out = torch.full_like(q, float("nan"))
+        ops.paged_decode(out, q, kc, vc, _t(g["block_tables"], cuda), _t(g["ctx_lens"], cuda),
+                         float(g["scale"]), plan.part_tokens, plan.max_parts, ws, None, None,
+                         int(w["window_left"]), _t(w["sinks"], cuda))
+        torch.cuda.synchronize()
+        _close(f32(out), w["out"], 1e-2)
 
     g = load("qk_norm_rope")
     q, k = _t(g["q"], cuda, bf), _t(g["k"], cuda, bf)
