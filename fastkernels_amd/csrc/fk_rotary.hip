@@ -25,54 +25,72 @@ __global__ __launch_bounds__(256) void rotary_vec(
     const typename CT::storage* __restrict__ cos_sin, int64_t max_position, int num_heads,
     int num_kv_heads, int head_size, int rot_dim) {
   using V = Vec16<T>;
+  using S = typename T::storage;
   constexpr int N = V::N;
+  // Work items (16-byte vectors) per lane per pass: all of a pass's q/k loads are
+  // issued together with the position load, so a token costs one round trip for
+  // q/k and the position and one for cos/sin, not one per item.
+  constexpr int kItems = 2;
   const int64_t tok = blockIdx.x;
-  const int64_t pos = positions[tok];
-  if (pos < 0 || pos >= max_position) return;
   const int half = rot_dim / 2;
   // kNeox: a vector holds N consecutive first-half (or second-half) elements,
   // npv vectors cover the first half.  GPT-J: a vector holds N/2 whole pairs.
   const int npv = kNeox ? half / N : rot_dim / N;
   const int total = (num_heads + num_kv_heads) * npv;
-  const typename CT::storage* cs = cos_sin + pos * rot_dim;
-  for (int w = threadIdx.x; w < total; w += 256) {
-    const int head = w / npv;
-    const int pv = w - head * npv;
-    typename T::storage* base =
-        head < num_heads ? query + tok * q_row_stride + static_cast<int64_t>(head) * head_size
-                         : key + tok * k_row_stride +
-                               static_cast<int64_t>(head - num_heads) * head_size;
-    if constexpr (kNeox) {
-      const int i0 = pv * N;
-      V xv, yv;
-      xv.raw = *reinterpret_cast<const uint4*>(base + i0);
-      yv.raw = *reinterpret_cast<const uint4*>(base + half + i0);
+  const int64_t pos = positions[tok];
+  // No early exit on the position: the loads above and below stay independent of
+  // it; an out-of-range position only suppresses the stores.
+  const bool pos_ok = pos >= 0 && pos < max_position;
+  const typename CT::storage* cs = cos_sin + (pos_ok ? pos : 0) * rot_dim;
+  for (int w0 = threadIdx.x; w0 < total; w0 += 256 * kItems) {
+    S* base[kItems];
+    int i0[kItems];
+    bool ok[kItems];
+    V xv[kItems], yv[kItems];
 #pragma unroll
-      for (int e = 0; e < N; ++e) {
-        const float c = T::round(CT::to_f32(cs[i0 + e]));
-        const float s = T::round(CT::to_f32(cs[half + i0 + e]));
-        const float x = T::to_f32(xv.e[e]);
-        const float y = T::to_f32(yv.e[e]);
-        xv.e[e] = T::from_f32(rope_x(x, y, c, s));
-        yv.e[e] = T::from_f32(rope_y(x, y, c, s));
-      }
-      *reinterpret_cast<uint4*>(base + i0) = xv.raw;
-      *reinterpret_cast<uint4*>(base + half + i0) = yv.raw;
-    } else {
-      const int e0 = pv * N;  // element offset; pairs (e0 + 2j, e0 + 2j + 1)
-      V v;
-      v.raw = *reinterpret_cast<const uint4*>(base + e0);
+    for (int u = 0; u < kItems; ++u) {
+      const int w = w0 + 256 * u;
+      ok[u] = w < total;
+      const int wc = ok[u] ? w : w0;  // an idle slot re-reads the pass's first item
+      const int head = wc / npv;
+      const int pv = wc - head * npv;
+      base[u] = head < num_heads
+                    ? query + tok * q_row_stride + static_cast<int64_t>(head) * head_size
+                    : key + tok * k_row_stride + static_cast<int64_t>(head - num_heads) * head_size;
+      i0[u] = pv * N;
+      xv[u].raw = *reinterpret_cast<const uint4*>(base[u] + i0[u]);
+      if constexpr (kNeox) yv[u].raw = *reinterpret_cast<const uint4*>(base[u] + half + i0[u]);
+    }
 #pragma unroll
-      for (int j = 0; j < N / 2; ++j) {
-        const int i = e0 / 2 + j;
-        const float c = T::round(CT::to_f32(cs[i]));
-        const float s = T::round(CT::to_f32(cs[half + i]));
-        const float x = T::to_f32(v.e[2 * j]);
-        const float y = T::to_f32(v.e[2 * j + 1]);
-        v.e[2 * j] = T::from_f32(rope_x(x, y, c, s));
-        v.e[2 * j + 1] = T::from_f32(rope_y(x, y, c, s));
+    for (int u = 0; u < kItems; ++u) {
+      if constexpr (kNeox) {
+#pragma unroll
+        for (int e = 0; e < N; ++e) {
+          const float c = T::round(CT::to_f32(cs[i0[u] + e]));
+          const float sn = T::round(CT::to_f32(cs[half + i0[u] + e]));
+          const float x = T::to_f32(xv[u].e[e]);
+          const float y = T::to_f32(yv[u].e[e]);
+          xv[u].e[e] = T::from_f32(rope_x(x, y, c, sn));
+          yv[u].e[e] = T::from_f32(rope_y(x, y, c, sn));
+        }
+        if (ok[u] && pos_ok) {
+          *reinterpret_cast<uint4*>(base[u] + i0[u]) = xv[u].raw;
+          *reinterpret_cast<uint4*>(base[u] + half + i0[u]) = yv[u].raw;
+        }
+      } else {
+        // element offset i0; pairs (i0 + 2j, i0 + 2j + 1)
+#pragma unroll
+        for (int j = 0; j < N / 2; ++j) {
+          const int i = i0[u] / 2 + j;
+          const float c = T::round(CT::to_f32(cs[i]));
+          const float sn = T::round(CT::to_f32(cs[half + i]));
+          const float x = T::to_f32(xv[u].e[2 * j]);
+          const float y = T::to_f32(xv[u].e[2 * j + 1]);
+          xv[u].e[2 * j] = T::from_f32(rope_x(x, y, c, sn));
+          xv[u].e[2 * j + 1] = T::from_f32(rope_y(x, y, c, sn));
+        }
+        if (ok[u] && pos_ok) *reinterpret_cast<uint4*>(base[u] + i0[u]) = xv[u].raw;
       }
-      *reinterpret_cast<uint4*>(base + e0) = v.raw;
     }
   }
 }
@@ -175,7 +193,9 @@ extern "C" int fk_rotary_embedding(const int64_t* positions, void* query, int64_
   FK_REQUIRE(q_row_stride >= static_cast<int64_t>(num_heads) * head_size &&
                  (!key || k_row_stride >= static_cast<int64_t>(num_kv_heads) * head_size),
              "fk_rotary_embedding: row stride shorter than the heads it holds");
-  if (tokens == 0) return FK_OK;
+  FK_REQUIRE(max_position >= 0, "fk_rotary_embedding: negative max_position");
+  // No cache rows: every position is out of range and leaves its token unchanged.
+  if (tokens == 0 || max_position == 0) return FK_OK;
   FK_REQUIRE(positions && query && cos_sin, "fk_rotary_embedding: null pointer");
   hipStream_t s = fk::as_stream(stream);
   const bool neox = is_neox != 0;
