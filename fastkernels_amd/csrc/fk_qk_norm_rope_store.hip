@@ -72,84 +72,103 @@ __global__ __launch_bounds__(256) void qk_norm_rope_store_kernel(QkParams P) {
   const int e0 = sub * N;  // first element of this lane's vector in the head row
   // Rows of the 16 lanes of a group are processed in lock step; every lane of
   // the wave runs the same trip count, so the cross-lane reads below always
-  // have their partner lanes active.
+  // have their partner lanes active.  Up to kBatch trips' row loads (and the
+  // norm weights) are issued before any of them is processed: the stores of one
+  // trip would otherwise keep the next trip's loads (same qkv buffer, unknown
+  // aliasing to the compiler) behind them, one memory round trip per trip.
+  constexpr int kBatch = 4;
   const int units = hq + 2 * hk;
   const int trips = (units + kGroups - 1) / kGroups;
-  for (int t = 0; t < trips; ++t) {
-    const int u = grp + t * kGroups;
-    const bool live = u < units;
-    const int uu = live ? u : units - 1;  // dead groups recompute the last row, store nothing
-    const bool is_q = uu < hq;
-    const bool is_v = uu >= hq + hk;
-    const int head = is_q ? uu : (is_v ? uu - hq - hk : uu - hq);
-    S* row;
-    if (is_q)
-      row = static_cast<S*>(P.query) + tok * P.q_row_stride + static_cast<int64_t>(head) * D;
-    else if (is_v)
-      row = const_cast<S*>(static_cast<const S*>(P.value)) + tok * P.v_row_stride +
-            static_cast<int64_t>(head) * D;
-    else
-      row = static_cast<S*>(P.key) + tok * P.k_row_stride + static_cast<int64_t>(head) * D;
-    V x;
-    x.raw = *reinterpret_cast<const uint4*>(row + e0);
-    if (!is_v) {  // uniform over the lane group
-      if constexpr (kNorm) {
-        V w;
-        w.raw = *reinterpret_cast<const uint4*>(static_cast<const S*>(is_q ? P.q_weight
-                                                                           : P.k_weight) +
-                                                e0);
-        float ss = 0.f;
+  V wq, wk;
+  if constexpr (kNorm) {
+    wq.raw = *reinterpret_cast<const uint4*>(static_cast<const S*>(P.q_weight) + e0);
+    wk.raw = *reinterpret_cast<const uint4*>(static_cast<const S*>(P.k_weight) + e0);
+  }
+  for (int t0 = 0; t0 < trips; t0 += kBatch) {
+    V xb[kBatch];
+    S* rows[kBatch];
+    int heads[kBatch];
+    bool lives[kBatch], qs[kBatch], vs[kBatch];
 #pragma unroll
-        for (int e = 0; e < N; ++e) ss = sumsq_add(ss, T::to_f32(x.e[e]));
-#pragma unroll
-        for (int off = kLanes / 2; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
-        const float inv = rms_inv(ss, static_cast<float>(D), P.eps);
-#pragma unroll
-        for (int e = 0; e < N; ++e) x.e[e] = rms_apply<T>(T::to_f32(x.e[e]), inv, T::to_f32(w.e[e]));
-      }
-      if constexpr (kNeox) {
-        // Lane vectors of the first half pair with those half/N lanes later.
-        const int hv = half / N;
-        const bool first = sub < hv;
-        const bool in_rot = sub < 2 * hv;
-        const int src = static_cast<int>(threadIdx.x & 63) + (first ? hv : (in_rot ? -hv : 0));
-        V y;
-        y.raw.x = __shfl(x.raw.x, src, 64);
-        y.raw.y = __shfl(x.raw.y, src, 64);
-        y.raw.z = __shfl(x.raw.z, src, 64);
-        y.raw.w = __shfl(x.raw.w, src, 64);
-        if (rotate && in_rot) {
-          const int i0 = first ? e0 : e0 - half;  // cos/sin index of element 0
-#pragma unroll
-          for (int e = 0; e < N; ++e) {
-            const float c = T::round(CT::to_f32(cs[i0 + e]));
-            const float s = T::round(CT::to_f32(cs[half + i0 + e]));
-            const float mine = T::to_f32(x.e[e]);
-            const float other = T::to_f32(y.e[e]);
-            x.e[e] = first ? T::from_f32(rope_x(mine, other, c, s))
-                           : T::from_f32(rope_y(other, mine, c, s));
-          }
-        }
-      } else {
-        if (rotate && e0 < P.rot_dim) {
-#pragma unroll
-          for (int j = 0; j < N / 2; ++j) {
-            const int i = e0 / 2 + j;
-            const float c = T::round(CT::to_f32(cs[i]));
-            const float s = T::round(CT::to_f32(cs[half + i]));
-            const float a = T::to_f32(x.e[2 * j]);
-            const float b = T::to_f32(x.e[2 * j + 1]);
-            x.e[2 * j] = T::from_f32(rope_x(a, b, c, s));
-            x.e[2 * j + 1] = T::from_f32(rope_y(a, b, c, s));
-          }
-        }
-      }
-      if (live) *reinterpret_cast<uint4*>(row + e0) = x.raw;
+    for (int b = 0; b < kBatch; ++b) {
+      const int u = grp + (t0 + b) * kGroups;
+      lives[b] = t0 + b < trips && u < units;
+      const int uu = (t0 + b < trips && u < units) ? u : units - 1;  // dead slots re-read the last row
+      qs[b] = uu < hq;
+      vs[b] = uu >= hq + hk;
+      heads[b] = qs[b] ? uu : (vs[b] ? uu - hq - hk : uu - hq);
+      if (qs[b])
+        rows[b] = static_cast<S*>(P.query) + tok * P.q_row_stride + static_cast<int64_t>(heads[b]) * D;
+      else if (vs[b])
+        rows[b] = const_cast<S*>(static_cast<const S*>(P.value)) + tok * P.v_row_stride +
+                  static_cast<int64_t>(heads[b]) * D;
+      else
+        rows[b] = static_cast<S*>(P.key) + tok * P.k_row_stride + static_cast<int64_t>(heads[b]) * D;
+      xb[b].raw = *reinterpret_cast<const uint4*>(rows[b] + e0);
     }
-    if (live && !is_q && store) {
-      S* dst = static_cast<S*>(is_v ? P.v_cache : P.k_cache) + slot * cache_row +
-               static_cast<int64_t>(head) * D + e0;
-      *reinterpret_cast<uint4*>(dst) = x.raw;
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      if (t0 + b >= trips) break;  // uniform over the work-group
+      const bool live = lives[b], is_q = qs[b], is_v = vs[b];
+      const int head = heads[b];
+      S* row = rows[b];
+      V x = xb[b];
+      if (!is_v) {  // uniform over the lane group
+        if constexpr (kNorm) {
+          const V& w = is_q ? wq : wk;
+          float ss = 0.f;
+#pragma unroll
+          for (int e = 0; e < N; ++e) ss = sumsq_add(ss, T::to_f32(x.e[e]));
+#pragma unroll
+          for (int off = kLanes / 2; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
+          const float inv = rms_inv(ss, static_cast<float>(D), P.eps);
+#pragma unroll
+          for (int e = 0; e < N; ++e) x.e[e] = rms_apply<T>(T::to_f32(x.e[e]), inv, T::to_f32(w.e[e]));
+        }
+        if constexpr (kNeox) {
+          // Lane vectors of the first half pair with those half/N lanes later.
+          const int hv = half / N;
+          const bool first = sub < hv;
+          const bool in_rot = sub < 2 * hv;
+          const int src = static_cast<int>(threadIdx.x & 63) + (first ? hv : (in_rot ? -hv : 0));
+          V y;
+          y.raw.x = __shfl(x.raw.x, src, 64);
+          y.raw.y = __shfl(x.raw.y, src, 64);
+          y.raw.z = __shfl(x.raw.z, src, 64);
+          y.raw.w = __shfl(x.raw.w, src, 64);
+          if (rotate && in_rot) {
+            const int i0 = first ? e0 : e0 - half;  // cos/sin index of element 0
+#pragma unroll
+            for (int e = 0; e < N; ++e) {
+              const float c = T::round(CT::to_f32(cs[i0 + e]));
+              const float sn = T::round(CT::to_f32(cs[half + i0 + e]));
+              const float mine = T::to_f32(x.e[e]);
+              const float other = T::to_f32(y.e[e]);
+              x.e[e] = first ? T::from_f32(rope_x(mine, other, c, sn))
+                             : T::from_f32(rope_y(other, mine, c, sn));
+            }
+          }
+        } else {
+          if (rotate && e0 < P.rot_dim) {
+#pragma unroll
+            for (int j = 0; j < N / 2; ++j) {
+              const int i = e0 / 2 + j;
+              const float c = T::round(CT::to_f32(cs[i]));
+              const float sn = T::round(CT::to_f32(cs[half + i]));
+              const float a = T::to_f32(x.e[2 * j]);
+              const float bb = T::to_f32(x.e[2 * j + 1]);
+              x.e[2 * j] = T::from_f32(rope_x(a, bb, c, sn));
+              x.e[2 * j + 1] = T::from_f32(rope_y(a, bb, c, sn));
+            }
+          }
+        }
+        if (live) *reinterpret_cast<uint4*>(row + e0) = x.raw;
+      }
+      if (live && !is_q && store) {
+        S* dst = static_cast<S*>(is_v ? P.v_cache : P.k_cache) + slot * cache_row +
+                 static_cast<int64_t>(head) * D + e0;
+        *reinterpret_cast<uint4*>(dst) = x.raw;
+      }
     }
   }
 }
