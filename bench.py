@@ -520,8 +520,20 @@ def bench_table(args):
                 + 256 * 16 + 256 * 128 * 4 + 2 * 128 * 2)
     add("C4", "q/k RMSNorm + rotary + store_kvcache, separate (the reference's op sequence)",
         qk_separate, qk_bytes)
+    def qk_fused_copies():
+        """Input sets for the fused prologue: fresh qkv rows and slots into scratch caches
+        (the decode case's cache keeps its contents)."""
+        gs = torch.Generator().manual_seed(workloads.SEED + 98)
+        kcs = torch.zeros(1024, 256, 8, 128, dtype=torch.bfloat16, device=dev)
+        vcs = torch.zeros_like(kcs)
+        sets = [(c4.qkv.clone(), torch.randperm(1024 * 256, generator=gs)[:256].to(dev))
+                for _ in range(copies_for(qk_bytes))]
+        return [lambda t=t, sl=sl: ops.qk_norm_rope_store(
+            c4.positions, t[:, :4096], t[:, 4096:5120], t[:, 5120:], kcs, vcs, sl, 128,
+            rope.cos_sin_cache, True, qw, kw, 1e-6) for t, sl in sets]
+
     add("C4", "q/k RMSNorm + rotary + store_kvcache, fused (qk_norm_rope_store)", qk_fused,
-        qk_bytes)
+        qk_bytes, rotated=qk_fused_copies)
     kn16 = k.contiguous().view(torch.int16).view(256, 8, 128).cpu().numpy()
     vn16 = v.contiguous().view(torch.int16).view(256, 8, 128).cpu().numpy()
     sn = c4.slot_mapping.cpu().numpy()

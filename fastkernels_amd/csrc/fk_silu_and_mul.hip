@@ -14,7 +14,13 @@
 namespace fk {
 namespace {
 
-__device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + __expf(-g)); }
+// silu(g) = g / (1 + e^-g) with the hardware reciprocal (v_rcp_f32, about 1 ulp)
+// instead of an IEEE division: the activation is rounded to the 8-bit-mantissa
+// dtype right after, so the two agree except at rounding ties.  g -> -inf gives
+// -0 as the division does (rcp(inf) = 0); g = -inf gives NaN, as -inf / inf does.
+__device__ __forceinline__ float silu_f32(float g) {
+  return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g));
+}
 
 template <typename T>
 __global__ __launch_bounds__(256) void silu_and_mul_vec(typename T::storage* __restrict__ out,
