@@ -90,15 +90,28 @@ __device__ __forceinline__ int64_t prefill_page(const PrefillParams& P,
   return (page >= 0 && page < P.num_blocks) ? page : -1;
 }
 
+// The last block-table entry a wave looked up (wave-uniform): a page spans
+// block_size / 32 stages, so most lookups reuse it instead of waiting for a
+// scalar load.
+struct PageCache {
+  int idx = -1;
+  int64_t page = -1;
+};
+
 // Row index of key `tok` of the sequence and whether it is readable: paged, the
 // slot through the block table (-1 pages masked; page 0 is read instead);
 // dense, row k_start + tok of the key/value tensors.
 template <bool kPaged>
 __device__ __forceinline__ int64_t key_row(const PrefillParams& P,
                                            const int32_t* __restrict__ bt_row, int k_start,
-                                           int tok, bool& ok) {
+                                           int tok, bool& ok, PageCache& pc) {
   if constexpr (kPaged) {
-    const int64_t page = prefill_page(P, bt_row, tok);
+    const int idx = tok >> P.block_size_log2;
+    if (idx != pc.idx) {
+      pc.page = prefill_page(P, bt_row, tok);
+      pc.idx = idx;
+    }
+    const int64_t page = pc.page;
     ok = page >= 0;
     return ((page < 0 ? 0 : page) << P.block_size_log2) + (tok & ((1 << P.block_size_log2) - 1));
   } else {
@@ -251,6 +264,7 @@ __global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_pre
   float s2 = P.scale_log2;
   if (kFp8 && P.k_scale) s2 *= P.k_scale[h];
 
+  PageCache pc;
   // One query block of the work-group, start to finish (its own K/V stages).
   auto process_block = [&](int qblk) {
   const int jw0 = qblk * wg_tokens;  // first query of the work-group
@@ -490,7 +504,7 @@ __global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_pre
 #pragma unroll
     for (int tt = 0; tt < kStageTiles; ++tt) {
       bool ok;
-      row0[tt] = key_row<kPaged>(P, bt_row, k_start, st * kStageKeys + tt * kTile, ok);
+      row0[tt] = key_row<kPaged>(P, bt_row, k_start, st * kStageKeys + tt * kTile, ok, pc);
     }
 #pragma unroll
     for (int i = 0; i < S::kLoads; ++i) {
@@ -530,8 +544,8 @@ __global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_pre
       if (t + 1 < tbeg) continue;  // wave-uniform; both tiles precede this wave's window
       bool ok_a = true, ok_b = true;
       if constexpr (decltype(masked)::value && kPaged) {
-        (void)key_row<kPaged>(P, bt_row, k_start, t * kTile, ok_a);
-        (void)key_row<kPaged>(P, bt_row, k_start, (t + 1) * kTile, ok_b);
+        (void)key_row<kPaged>(P, bt_row, k_start, t * kTile, ok_a, pc);
+        (void)key_row<kPaged>(P, bt_row, k_start, (t + 1) * kTile, ok_b, pc);
       }
       pair_step(masked, t * kTile, buf, tt, ok_a, ok_b);
     }
@@ -545,7 +559,7 @@ __global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_pre
 #pragma unroll
       for (int tt = 0; tt < kStageTiles; ++tt) {
         bool ok;
-        (void)key_row<kPaged>(P, bt_row, k_start, (st * kStageTiles + tt) * kTile, ok);
+        (void)key_row<kPaged>(P, bt_row, k_start, (st * kStageTiles + tt) * kTile, ok, pc);
         if (!ok) return false;
       }
     }
