@@ -333,6 +333,10 @@ struct WaveState {
     };
 
     const int ntiles = (tok_end - tok_begin + kTile - 1) / kTile;
+    // The last block-table entry looked up (wave-uniform): a page holds
+    // block_size / 16 tiles, so most tiles reuse it instead of a scalar load.
+    int pc_idx = -1;
+    int64_t pc_page = -1;
     // Issues the loads of tiles t0 .. t0+U-1 into `buf` (unconditional; tiles
     // past the end re-read the last tile, which hits in cache).
     // Issues the loads of tiles t0 .. t0+U-1 into `buf` (unconditional; tiles
@@ -341,7 +345,12 @@ struct WaveState {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int tok0 = tok_begin + kTile * min(t0 + u, ntiles - 1);
-        pg[u] = page_of(P, bt, b, tok0);
+        const int idx = tok0 >> P.block_size_log2;
+        if (idx != pc_idx) {
+          pc_page = page_of(P, bt, b, tok0);
+          pc_idx = idx;
+        }
+        pg[u] = pc_page;
         int j = -1;
         if constexpr (kStore) {
           // Fused when b's slot is that of position ctx - 1: in this tile's page
