@@ -371,17 +371,20 @@ __global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_pre
           sm[i] = s[i];
         }
       }
-      float mt = fmaxf(fmaxf(fmaxf(sm[0], sm[1]), fmaxf(sm[2], sm[3])),
-                       fmaxf(fmaxf(sm[4], sm[5]), fmaxf(sm[6], sm[7])));
-      mt = pair_max(mt);
-      mt = (kMasked && mt == kNegInf) ? kNegInf : mt * s2;
+      // This lane's max over its 8 keys of the column, scaled.
+      float lt = max3_raw(max3_raw(sm[0], sm[1], sm[2]), max3_raw(sm[3], sm[4], sm[5]),
+                          max3_raw(sm[6], sm[7], sm[7]));
+      lt = (kMasked && lt == kNegInf) ? kNegInf : lt * s2;
       // Lazy rescaling: the running max only moves when a score exceeds it by
       // more than kLazy (log2 units), so P <= 2^kLazy and the O / l rescale (a
-      // cross-lane fetch per row) is rare after the first tiles.  The common
-      // path is the one compare; the final normalisation divides by l
-      // accumulated against the same max, so the result is unchanged up to
-      // rounding.
-      if (__ballot(mt > m_run[nb] + kLazy) != 0) {
+      // cross-lane fetch per row) is rare after the first tiles.  The test
+      // needs no cross-lane max: some column's max exceeds its m_run + kLazy
+      // exactly when some lane's own max does, and the ballot spans every
+      // lane.  The column max itself is taken only in the rare branch.  The
+      // final normalisation divides by l accumulated against the same max, so
+      // the result is unchanged up to rounding.
+      if (__ballot(lt > m_run[nb] + kLazy) != 0) {
+        const float mt = pair_max(lt);
         const float m_new = mt > m_run[nb] + kLazy ? mt : m_run[nb];
         // 1 where the column's max stays (also -inf to -inf), 0 from -inf.
         const float alpha = m_new == m_run[nb] ? 1.f : __builtin_amdgcn_exp2f(m_run[nb] - m_new);
