@@ -32,15 +32,6 @@ constexpr float kNegInf = -__builtin_huge_valf();
 // with the gfx950 row-swap permutes (VALU, no LDS traffic): each swap returns
 // a lane's own value and its partner row's value in some order, so combining
 // the two outputs symmetrically reduces each row pair.
-// max(a, b, c) in one v_max3_f32.  fmaxf on MFMA results costs a quieting
-// max(x, x) per operand first (the compiler cannot prove them canonical); the
-// scores here are finite or -inf, so that step buys nothing.
-__device__ __forceinline__ float max3_raw(float a, float b, float c) {
-  float d;
-  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
-  return d;
-}
-
 __device__ __forceinline__ float pair_max(float v) {
   const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
   v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));

@@ -349,15 +349,16 @@ __global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_pre
       const floatx4_t acc_b = qk_scores(kb, qb[nb]);
       const int j = j0 + 16 * nb + r;  // this lane's query column
       const int last = offset + j;     // its last visible key
-      // Raw scores K.Q: the scale goes into the exponent's FMA (s2 >= 0, so the
-      // row max of the raw scores, scaled, is the max of the scaled ones).
+      // Scores in log2 units, s = s2 * (K.Q), one product each: a product is
+      // canonical, so the max below compiles to plain v_max3 with no
+      // NaN-quieting step per operand (as the raw MFMA results would need).
       // Masked keys take -inf in the max and P = 0 after the exponent.
       float s[8], sm[8];
       bool ok[8];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        s[i] = acc_a[i];
-        s[4 + i] = acc_b[i];
+        s[i] = acc_a[i] * s2;
+        s[4 + i] = acc_b[i] * s2;
       }
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
@@ -371,10 +372,9 @@ __global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_pre
           sm[i] = s[i];
         }
       }
-      // This lane's max over its 8 keys of the column, scaled.
-      float lt = max3_raw(max3_raw(sm[0], sm[1], sm[2]), max3_raw(sm[3], sm[4], sm[5]),
-                          max3_raw(sm[6], sm[7], sm[7]));
-      lt = (kMasked && lt == kNegInf) ? kNegInf : lt * s2;
+      // This lane's max over its 8 keys of the column.
+      const float lt = fmaxf(fmaxf(fmaxf(sm[0], sm[1]), fmaxf(sm[2], sm[3])),
+                             fmaxf(fmaxf(sm[4], sm[5]), fmaxf(sm[6], sm[7])));
       // Lazy rescaling: the running max only moves when a score exceeds it by
       // more than kLazy (log2 units), so P <= 2^kLazy and the O / l rescale (a
       // cross-lane fetch per row) is rare after the first tiles.  The test
@@ -403,7 +403,7 @@ __global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_pre
       float pr[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        pr[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], s2, -m_use));
+        pr[i] = __builtin_amdgcn_exp2f(s[i] - m_use);
         if constexpr (kMasked) pr[i] = ok[i] ? pr[i] : 0.f;
       }
       const float (&pa)[4] = *reinterpret_cast<const float(*)[4]>(&pr[0]);

@@ -183,6 +183,22 @@ def test_paged_prefill_qwen3_prompt_2048(cuda):
     _close(got, ref.transpose(0, 1).cpu().numpy(), 1e-2, "2048 prompt")
 
 
+@pytest.mark.parametrize("fp8", [False, True])
+def test_paged_prefill_deterministic(cuda, fp8):
+    """The same call repeated gives bit-identical outputs (causal chunks, masked and
+    unmasked stages, paired work-groups, a window with sinks).  A tolerance check
+    cannot see a kernel that reads MFMA results before they are written: its
+    outputs change from run to run in the last bits."""
+    _flush(f"paged prefill determinism fp8={fp8}")
+    c = _case(cuda, [64, 512, 300, 1], [64, 1024, 300, 900], bs=16, seed=81, fp8=fp8)
+    sinks = torch.linspace(-1.0, 2.0, 32, device=cuda)
+    for kw in ({}, {"window_left": 100, "sinks": sinks}):
+        first = _run(c, **kw)
+        for _ in range(4):
+            again = _run(c, **kw)
+            assert torch.equal(again, first), f"prefill output changed between calls ({kw.keys()})"
+
+
 def test_flash_attn_prefill_candidate(cuda):
     from fastkernels_amd.candidate.L1.flash_attn_prefill import FlashAttnPrefill
     _flush("FlashAttnPrefill candidate (paged)")
