@@ -337,16 +337,30 @@ __global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_pre
                        bool ok_b) {
     constexpr bool kMasked = decltype(masked)::value;
     TileRegs<kFp8> ta, tb;
-    lds_tile_k<kFp8>(buf, tt, r, g, ta);
-    lds_tile_k<kFp8>(buf, tt + 1, r, g, tb);
-    uint4 ka[4], kb[4];
-    k_chunks(ta, ka);
-    k_chunks(tb, kb);
+    // Scores of tile a for every column block, then tile b's K is read: the two
+    // K tiles are never live at once (20 fewer VGPRs in the compiler's own
+    // allocation; measured 1% faster).
+    floatx4_t sc_a[kColBlocks], sc_b[kColBlocks];
+    {
+      lds_tile_k<kFp8>(buf, tt, r, g, ta);
+      uint4 ka[4];
+      k_chunks(ta, ka);
+#pragma unroll
+      for (int nb = 0; nb < kColBlocks; ++nb) sc_a[nb] = qk_scores(ka, qb[nb]);
+    }
+    asm volatile("" ::: "memory");  // tile b's K reads stay after tile a's
+    {
+      lds_tile_k<kFp8>(buf, tt + 1, r, g, tb);
+      uint4 kb[4];
+      k_chunks(tb, kb);
+#pragma unroll
+      for (int nb = 0; nb < kColBlocks; ++nb) sc_b[nb] = qk_scores(kb, qb[nb]);
+    }
     short4_t p_a[kColBlocks], p_b[kColBlocks];
 #pragma unroll
     for (int nb = 0; nb < kColBlocks; ++nb) {
-      const floatx4_t acc_a = qk_scores(ka, qb[nb]);
-      const floatx4_t acc_b = qk_scores(kb, qb[nb]);
+      const floatx4_t acc_a = sc_a[nb];
+      const floatx4_t acc_b = sc_b[nb];
       const int j = j0 + 16 * nb + r;  // this lane's query column
       const int last = offset + j;     // its last visible key
       // Scores in log2 units, s = s2 * (K.Q), one product each: a product is
