@@ -56,7 +56,8 @@ constexpr int kPrefillWaves = 4;               // waves per work-group
 #endif
 // Keys per LDS stage (a multiple of 32).  Measured on MI355X (bf16, 1x2048,
 // 4x512 over 4096, 16x512 prompts): 32 keys 102 / 220 / 89 us against 117 /
-// 244 / 99 us for 64.
+// 244 / 99 us for 64; again with the current loop, 88 / 187 / 83 against
+// 98 / 208 / 91.
 constexpr int kStageKeys = FK_PREFILL_STAGE;
 constexpr int kStageTiles = kStageKeys / kTile;
 
