@@ -10,8 +10,10 @@ over the batch, with all inputs resident in HBM.
 Prints ONE JSON line: value = whole-call throughput in algorithmic GB/s
 (K+V bytes attended + q + out + block-table entries + ctx, per call, divided by
 the mean step time), the per-call time, the roofline of the dominant kernel
-(the partials kernel, timed live with HIP events on its stream) against the
-8 TB/s HBM peak, and the CPU oracle timed on a bounded sample.
+(the partials kernel, timed live with HIP events on its stream on at least 10 of
+the timed steps) against the 8 TB/s HBM peak, the same call replayed from a HIP
+graph, and the reference's PyTorch decode path (oracle/torch_path.py) timed over
+the whole batch on the host's cores.
 
   python bench.py [--steps K] [--warmup W] [--num-splits S] [--no-cpu]
   python bench.py --table          # per-op table for C1-C5 to stderr (+ --table-json PATH)
@@ -50,12 +52,6 @@ def _parse():
     return ap.parse_args()
 
 
-def _events(n):
-    import torch
-
-    return [torch.cuda.Event(enable_timing=True) for _ in range(n)]
-
-
 def _flush_buffer(device):
     import torch
 
@@ -65,7 +61,56 @@ def _flush_buffer(device):
     return torch.ones(512 * 1024 * 1024 // 4, dtype=torch.float32, device=device)
 
 
-EVENT_EVERY = 10  # bench_decode: steps between HIP-event samples of the partials kernel
+KERNEL_SAMPLES = 10  # bench_decode: HIP-event samples of the partials kernel per run (at least)
+
+
+class HipEvents:
+    """HIP events created with hipEventDisableSystemFence, recorded on a given stream.
+
+    A default event (torch.cuda.Event) performs a system-scope release when it is
+    recorded: on MI355X that writes back and invalidates the caches, which measured
+    ~6 us per event pair on the C3 step (and slows the next kernel).  These timing
+    events skip that fence (hip_runtime_api.h: "events that are only being used to
+    measure timing"): ~2 us per pair, and they time the kernel within 1 us of the
+    rocprofv3 trace."""
+
+    FLAG_DISABLE_SYSTEM_FENCE = 0x20000000
+
+    def __init__(self, n: int):
+        import ctypes
+
+        self._ct = ctypes
+        hip = ctypes.CDLL("libamdhip64.so")
+        hip.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
+        hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p,
+                                            ctypes.c_void_p]
+        hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        self._hip = hip
+        self.ev = []
+        for _ in range(n):
+            e = ctypes.c_void_p()
+            rc = hip.hipEventCreateWithFlags(ctypes.byref(e), self.FLAG_DISABLE_SYSTEM_FENCE)
+            if rc != 0:
+                raise RuntimeError(f"hipEventCreateWithFlags failed ({rc})")
+            self.ev.append(e)
+
+    def record(self, i: int, stream_handle: int) -> None:
+        rc = self._hip.hipEventRecord(self.ev[i], self._ct.c_void_p(stream_handle))
+        if rc != 0:
+            raise RuntimeError(f"hipEventRecord failed ({rc})")
+
+    def elapsed_ms(self, i: int, j: int) -> float:
+        f = self._ct.c_float()
+        rc = self._hip.hipEventElapsedTime(self._ct.byref(f), self.ev[i], self.ev[j])
+        if rc != 0:
+            raise RuntimeError(f"hipEventElapsedTime failed ({rc})")
+        return f.value
+
+    def close(self) -> None:
+        for e in self.ev:
+            self._hip.hipEventDestroy(e)
+        self.ev = []
 
 
 def settle_clocks(fn, seconds=0.3):
@@ -86,23 +131,25 @@ def settle_clocks(fn, seconds=0.3):
 
 
 def time_call(fn, iters=50, warmup=10, flush=None):
-    """Median and mean of fn's GPU time (events bracket only fn; an optional cache
-    flush is enqueued before each start event)."""
+    """Median and mean of fn's GPU time (fence-free HIP events bracket only fn; an
+    optional cache flush is enqueued before each start event)."""
     import torch
 
     for _ in range(warmup):
         fn()
-    starts, ends = _events(iters), _events(iters)
+    ev = HipEvents(2 * iters)
+    sh = torch.cuda.current_stream().cuda_stream
     sink = None
     for i in range(iters):
         if flush is not None:
             sink = flush.sum()
-        starts[i].record()
+        ev.record(2 * i, sh)
         fn()
-        ends[i].record()
+        ev.record(2 * i + 1, sh)
     torch.cuda.synchronize()
     del sink
-    ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    ms = [ev.elapsed_ms(2 * i, 2 * i + 1) for i in range(iters)]
+    ev.close()
     return statistics.median(ms), statistics.fmean(ms)
 
 
@@ -130,13 +177,15 @@ def time_rotated(fns, iters=20, warmup=3):
             fn()
     for _ in range(warmup):
         graph.replay()
-    starts, ends = _events(iters), _events(iters)
+    ev = HipEvents(2 * iters)
+    sh = torch.cuda.current_stream().cuda_stream
     for i in range(iters):
-        starts[i].record()
+        ev.record(2 * i, sh)
         graph.replay()
-        ends[i].record()
+        ev.record(2 * i + 1, sh)
     torch.cuda.synchronize()
-    ms = statistics.median(s.elapsed_time(e) for s, e in zip(starts, ends))
+    ms = statistics.median(ev.elapsed_ms(2 * i, 2 * i + 1) for i in range(iters))
+    ev.close()
     del graph
     return ms * 1e3 / len(fns)
 
@@ -147,68 +196,71 @@ def copies_for(footprint: int) -> int:
 
 
 # ---------------------------------------------------------------------------
-# CPU baseline: the oracle (numpy restatement of the reference's torch path)
+# CPU baseline: the reference's PyTorch decode path (Attention._decode_torch,
+# attention_impl.py:592-664), restated in oracle/torch_path.py, on the host cores
 # ---------------------------------------------------------------------------
-def cpu_baseline_decode(case, budget_s: float):
-    import numpy as np
+def cpu_baseline_decode(case, budget_s: float, gpu_out=None):
+    """Times oracle.torch_path.decode_torch (per-sequence page gather, repeat_interleave,
+    F.scaled_dot_product_attention, bf16) over the WHOLE C3 batch on the host, with
+    torch's intra-op threads set to every core this process may use.  Only the pages
+    the batch uses are copied to the host (the block tables are renumbered to match),
+    which changes no value the path reads."""
     import torch
 
-    import oracle
+    from oracle.torch_path import decode_torch
 
+    cores_avail = len(os.sched_getaffinity(0))
+    # The GPU box sets OMP_NUM_THREADS to this process's CPU share; use all of it.
+    threads = min(cores_avail, int(os.environ.get("OMP_NUM_THREADS", cores_avail) or cores_avail))
+    prev_threads = torch.get_num_threads()
+    torch.set_num_threads(threads)
     try:
-        from threadpoolctl import threadpool_limits
-    except ImportError:  # pragma: no cover
-        threadpool_limits = None
-    cores = min(len(os.sched_getaffinity(0)), 16)
-    ctx = case.ctx_lens.cpu().numpy().astype(np.int64)
-    bt = case.block_tables.cpu().numpy()
-    bs = case.k_cache.shape[1]
-    order = np.argsort(ctx)
-    sample = [int(order[len(order) // 2]), int(order[-1]), int(order[0]), int(order[len(order) // 4])]
-    q = case.q.float().cpu().numpy()
-    data = []
-    for i in sample:
-        n = int(ctx[i])
-        pages = (n + bs - 1) // bs
-        ids = torch.from_numpy(bt[i, :pages].astype(np.int64)).to(case.k_cache.device)
-        data.append((i, n, case.k_cache[ids].float().cpu().numpy(),
-                     case.v_cache[ids].float().cpu().numpy()))
-    hk, d = case.k_cache.shape[2], case.k_cache.shape[3]
-    per_tok = 2 * hk * d * case.k_cache.element_size()
-
-    def run_once():
-        for i, n, kp, vp in data:
-            oracle.paged_decode(q[i:i + 1], kp, vp, np.arange(kp.shape[0])[None], np.array([n]),
-                                case.scale)
-
-    ctx_mgr = threadpool_limits(limits=cores) if threadpool_limits else None
-    try:
-        run_once()  # warmup
-        t0 = time.perf_counter()
-        reps = 0
-        while True:
-            run_once()
-            reps += 1
-            if time.perf_counter() - t0 >= budget_s:
-                break
-        el = (time.perf_counter() - t0) / reps
+        bs = case.k_cache.shape[1]
+        ctx = case.ctx_lens.to(torch.int64)
+        pages = (ctx + bs - 1) // bs
+        bt = case.block_tables.to(torch.int64)
+        used = torch.cat([bt[i, :int(pages[i])] for i in range(bt.shape[0])])
+        k_host = case.k_cache[used].cpu()
+        v_host = case.v_cache[used].cpu()
+        # sequence i's pages are rows [off_i, off_i + pages_i) of the compacted caches
+        off = torch.cumsum(pages, 0) - pages
+        bt_host = torch.full(tuple(bt.shape), -1, dtype=torch.int32)
+        for i in range(bt.shape[0]):
+            bt_host[i, :int(pages[i])] = torch.arange(int(off[i]), int(off[i] + pages[i]),
+                                                      dtype=torch.int32)
+        q_host = case.q.cpu()
+        ctx_host = case.ctx_lens.cpu()
+        out = decode_torch(q_host, k_host, v_host, ctx_host, bt_host, case.scale)  # warmup
+        times = []
+        t_end = time.perf_counter() + budget_s
+        while not times or time.perf_counter() < t_end:
+            t0 = time.perf_counter()
+            out = decode_torch(q_host, k_host, v_host, ctx_host, bt_host, case.scale)
+            times.append(time.perf_counter() - t0)
     finally:
-        if ctx_mgr is not None:
-            ctx_mgr.__exit__(None, None, None)
-    toks = sum(n for _, n, _, _ in data)
-    gbs = toks * per_tok / el / 1e9
-    total_toks = int(ctx.sum())
-    return {
-        "value": round(gbs, 3),
+        torch.set_num_threads(prev_threads)
+    el = statistics.median(times)
+    total_bytes = case.algorithmic_bytes()
+    res = {
+        "value": round(total_bytes / el / 1e9, 3),
         "unit": "GB/s",
-        "cores": cores,
+        "cores": threads,
         "kind": "port",
-        "sample": (f"oracle.paged_decode (numpy float64, gather + softmax attention as "
-                   f"attention_impl.py:592-664) on {len(sample)} of {len(ctx)} C3 sequences "
-                   f"({toks} of {total_toks} cached tokens), {reps} reps in {budget_s:.0f}s; "
-                   f"whole-batch estimate {el * total_toks / toks * 1e6:.0f} us/call"),
-        "us_per_call_estimate": round(el * total_toks / toks * 1e6, 1),
+        "sample": (f"oracle.torch_path.decode_torch (the reference's _decode_torch, "
+                   f"attention_impl.py:592-664: page gather, repeat_interleave, "
+                   f"F.scaled_dot_product_attention in bf16) over the whole C3 batch "
+                   f"({case.q.shape[0]} sequences, {int(ctx.sum())} cached tokens), "
+                   f"median of {len(times)} calls in {budget_s:.0f}s; "
+                   f"torch threads {threads} of {cores_avail} cores in this process's "
+                   f"affinity mask"),
+        "us_per_call": round(el * 1e6, 1),
+        "torch_threads": threads,
+        "cores_in_affinity": cores_avail,
     }
+    if gpu_out is not None:  # the two outputs side by side (a sanity check, not the parity test)
+        diff = (out.float() - gpu_out.float().cpu()).abs()
+        res["max_abs_vs_gpu"] = float(f"{diff.max().item():.3g}")
+    return res
 
 
 # ---------------------------------------------------------------------------
@@ -242,29 +294,35 @@ def bench_decode(args):
         step()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream(dev)
-    # The partials kernel is timed live with HIP events on every EVENT_EVERY-th step
-    # only: an event record is a timestamped barrier in the queue, and a pair on every
-    # step measured ~5.7 us/call of added whole-call time.
-    sampled = list(range(0, args.steps, EVENT_EVERY))
-    ev = _events(2 * len(sampled))
+    # The partials kernel is timed live with HIP events (recorded on its stream,
+    # without the system-scope fence) on every `every`-th timed step, so that any
+    # run has at least KERNEL_SAMPLES samples; an event pair costs ~2 us of the step.
+    every = max(1, args.steps // KERNEL_SAMPLES)
+    sampled = list(range(0, args.steps, every))
+    ev = HipEvents(2 * len(sampled))
+    sh = stream.cuda_stream
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     j = 0
     for i in range(args.steps):
         if j < len(sampled) and sampled[j] == i:
-            ev[2 * j].record(stream)
+            ev.record(2 * j, sh)
             partials()
-            ev[2 * j + 1].record(stream)
+            ev.record(2 * j + 1, sh)
             j += 1
         else:
             partials()
         reduce()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    kern_ms = [ev[2 * k].elapsed_time(ev[2 * k + 1]) for k in range(len(sampled))]
+    kern_ms = [ev.elapsed_ms(2 * k, 2 * k + 1) for k in range(len(sampled))]
+    ev.close()
     ms_per_step = wall * 1e3 / args.steps
     kavg = statistics.fmean(kern_ms)
     achieved = partial_bytes / (kavg * 1e-3) / 1e9
+    graph_us = _graph_replay_us(lambda: ops.paged_decode(
+        out, case.q, case.k_cache, case.v_cache, case.block_tables, case.ctx_lens, case.scale,
+        part, nparts, ws), replays=max(20, args.steps))
     result = {
         "metric": METRIC,
         "value": round(total_bytes / (ms_per_step * 1e-3) / 1e9, 2),
@@ -300,10 +358,43 @@ def bench_decode(args):
             "traffic_source": "profiles/paged_decode_c3_traffic.json (rocprofv3 FETCH_SIZE/WRITE_SIZE, copy-calibrated)",
             "avg_kernel_us": round(kavg * 1e3, 2),
             "kernel_samples": len(kern_ms),
+            "event_every_steps": every,
             "algorithmic_bytes_per_launch": partial_bytes,
         },
+        # The same call as the engine's decode step runs it: both launches captured
+        # in one HIP graph and replayed (engine.py:5386-5428).  Reported beside the
+        # eager figure above, which is `value`.
+        "graph_replay": {"us_per_call": round(graph_us, 2),
+                         "GBs": round(total_bytes / (graph_us * 1e-6) / 1e9, 1),
+                         "frac": round(total_bytes / (graph_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)},
     }
-    return result, case
+    return result, case, out
+
+
+def _graph_replay_us(call, replays: int) -> float:
+    """Wall-clock µs per replay of `call` captured alone in a HIP graph, over `replays`
+    back-to-back replays (after 3 untimed ones)."""
+    import torch
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        call()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        call()
+    for _ in range(3):
+        graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(replays):
+        graph.replay()
+    torch.cuda.synchronize()
+    us = (time.perf_counter() - t0) * 1e6 / replays
+    del graph
+    return us
 
 
 def _committed_traffic(kernel: str, part: int):
@@ -805,9 +896,9 @@ def main():
     if args.table:
         bench_table(args)
         return
-    result, case = bench_decode(args)
+    result, case, out = bench_decode(args)
     if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline_decode(case, args.cpu_seconds)
+        result["cpu_baseline"] = cpu_baseline_decode(case, args.cpu_seconds, gpu_out=out)
     else:
         result["cpu_baseline"] = None
     print(json.dumps(result), flush=True)

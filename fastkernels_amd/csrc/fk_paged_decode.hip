@@ -455,10 +455,10 @@ __global__ __launch_bounds__(NH * 64) void paged_decode_partition_kernel(
   if (h >= P.num_kv_heads) return;  // uniform over the wave; no barriers follow
   const int lane = threadIdx.x & 63;
   if (tok_begin < ctx) {  // uniform over the work-group
-    const int tok_end = min(ctx, tok_begin + P.part_tokens);
-    // Tokens past part_tokens * max_parts are outside the launch (the plan's
-    // max_seq_len bounds every context); clamp so the partition count matches
-    // the grid and the reduce kernel.
+    // The launch has max_parts partitions; the last one runs on to the context
+    // end, so a context longer than the plan's max_seq_len bound (a graph
+    // replayed after contexts grew) is still attended whole.
+    const int tok_end = p == P.max_parts - 1 ? ctx : min(ctx, tok_begin + P.part_tokens);
     const int nparts = min((ctx + P.part_tokens - 1) / P.part_tokens, P.max_parts);
     const int r = lane & 15;
     const int g = lane >> 4;
@@ -477,10 +477,9 @@ __global__ __launch_bounds__(NH * 64) void paged_decode_partition_kernel(
       st.write_partial(P, row0, h, r, g);
     }
   }
-  // No partition streams position ctx - 1 (no context, or past the launch's
-  // partitions): partition 0 writes b's row.
-  if (kStore && p == 0 &&
-      (ctx <= 0 || ctx - 1 >= static_cast<int64_t>(P.part_tokens) * P.max_parts)) {
+  // No partition streams position ctx - 1 (no context): partition 0 writes b's
+  // row.
+  if (kStore && p == 0 && ctx <= 0) {
     const int64_t os = valid_slot(P, slot_mapping, b);
     if (os >= 0) store_new_row<kFp8>(P, b, h, os, lane);
   }
@@ -571,76 +570,84 @@ __global__ __launch_bounds__(NH * 64) void paged_decode_balanced_kernel(
   }
 }
 
-// Merge of one (query head hq, sequence b) by a work-group of kMergeWaves
-// waves; each lane owns two dims.  Partial rows: k = 0 is `alt_first_row`,
-// k >= 1 is first_row + k * row_stride.  Wave v folds rows v, v + kMergeWaves,
-// ... in one online pass (running max with rescaling, so the loads of all its
-// rows are independent and overlap), and the waves' (max, sum, O) are combined
-// through LDS: a sequence cut into 32 pieces costs about two load latencies
-// instead of eight.
-constexpr int kMergeWaves = 4;
+// Merge of one (query head hq, sequence b) by one wave; each lane owns two
+// dims.  Partial rows: k = 0 is `alt_first_row`, k >= 1 is first_row + k *
+// row_stride.  The pieces are taken kMergeBatch at a time (one batch for up to
+// 64 pieces): lane k loads piece k's (max, sum) while the wave issues the O
+// loads of every piece in the batch, all independent, so the merge costs one
+// load latency; the batch max and sum are wave reductions, and a running
+// (M, L, O) carries across batches with the reduce_segments rescaling.
+constexpr int kMergeBatch = 64;  // pieces per batch: one (max, sum) per lane
+constexpr int kMergeUnroll = 8;  // O rows in flight per wave
+constexpr int kMergeWaves = 4;   // independent merge rows per work-group
 __device__ __forceinline__ void merge_rows(uint16_t* orow, const float* part_o,
                                            const float* part_ml, int64_t first_row,
                                            int64_t row_stride, int nrows, int64_t alt_first_row,
-                                           float sink2) {
-  __shared__ float red_ml[kMergeWaves][2];
-  __shared__ float2 red_o[kMergeWaves][64];
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+                                           float sink2, int lane) {
+  auto row_of = [&](int k) -> int64_t { return k == 0 ? alt_first_row : first_row + k * row_stride; };
   float M = kNegInf, L = 0.f, o0 = 0.f, o1 = 0.f;
-#pragma unroll 4
-  for (int k = wave; k < nrows; k += kMergeWaves) {
-    const int64_t row = (k == 0 ? alt_first_row : first_row + k * row_stride);
-    const float m = part_ml[row * 2];
-    const float l = part_ml[row * 2 + 1];
-    const float2 ov = reinterpret_cast<const float2*>(part_o + row * kHead)[lane];
-    const float mn = fmaxf(M, m);
-    if (mn == kNegInf) continue;  // nothing valid yet
+  for (int k0 = 0; k0 < nrows; k0 += kMergeBatch) {
+    const int n = min(kMergeBatch, nrows - k0);
+    // (max, sum) of piece k0 + lane; lanes past the batch hold an empty piece.
+    float m = kNegInf, l = 0.f;
+    if (lane < n) {
+      const float2 ml = *reinterpret_cast<const float2*>(part_ml + row_of(k0 + lane) * 2);
+      m = ml.x;
+      l = ml.y;
+    }
+    // O of the batch's pieces, kMergeUnroll rows in flight at a time.
+    float2 ov[kMergeUnroll];
+#pragma unroll
+    for (int u = 0; u < kMergeUnroll; ++u)
+      ov[u] = u < n ? reinterpret_cast<const float2*>(part_o + row_of(k0 + u) * kHead)[lane]
+                    : make_float2(0.f, 0.f);
+    const float mb = wave_max(m);
+    const float mn = fmaxf(M, mb);
+    if (mn == kNegInf) continue;  // no valid piece yet (all rows empty)
     const float a = __builtin_amdgcn_exp2f(M - mn);  // 0 when M = -inf
-    const float f = __builtin_amdgcn_exp2f(m - mn);  // 0 when m = -inf
-    L = L * a + l * f;
-    o0 = o0 * a + ov.x * f;
-    o1 = o1 * a + ov.y * f;
+    const float f = __builtin_amdgcn_exp2f(m - mn);  // lane k's weight; 0 for empty pieces
+    L = L * a + wave_sum(l * f);
+    o0 *= a;
+    o1 *= a;
+    for (int u0 = 0; u0 < n; u0 += kMergeUnroll) {
+      if (u0 > 0) {
+#pragma unroll
+        for (int u = 0; u < kMergeUnroll; ++u)
+          ov[u] = u0 + u < n
+                      ? reinterpret_cast<const float2*>(part_o + row_of(k0 + u0 + u) * kHead)[lane]
+                      : make_float2(0.f, 0.f);
+      }
+#pragma unroll
+      for (int u = 0; u < kMergeUnroll; ++u) {
+        const float w = __builtin_bit_cast(
+            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, f), min(u0 + u, 63)));
+        if (u0 + u < n) {
+          o0 = __builtin_fmaf(ov[u].x, w, o0);
+          o1 = __builtin_fmaf(ov[u].y, w, o1);
+        }
+      }
+    }
     M = mn;
   }
-  if (lane == 0) {
-    red_ml[wave][0] = M;
-    red_ml[wave][1] = L;
-  }
-  red_o[wave][lane] = make_float2(o0, o1);
-  __syncthreads();
-  if (wave != 0) return;
-  float Mt = kNegInf;
-#pragma unroll
-  for (int v = 0; v < kMergeWaves; ++v) Mt = fmaxf(Mt, red_ml[v][0]);
-  float Lt = 0.f, a0 = 0.f, a1 = 0.f;
-  if (Mt != kNegInf) {
-#pragma unroll
-    for (int v = 0; v < kMergeWaves; ++v) {
-      const float f = __builtin_amdgcn_exp2f(red_ml[v][0] - Mt);  // 0 for a wave with no rows
-      const float2 ov = red_o[v][lane];
-      Lt += red_ml[v][1] * f;
-      a0 += ov.x * f;
-      a1 += ov.y * f;
-    }
-  }
-  Lt = with_sink(Lt, Mt, sink2);  // the sink joins the merged row once
-  const float inv = Lt > 0.f ? 1.f / Lt : 0.f;
-  const bf16x2_t pk = {static_cast<__bf16>(a0 * inv), static_cast<__bf16>(a1 * inv)};
+  L = with_sink(L, M, sink2);  // the sink joins the merged row once
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  const bf16x2_t pk = {static_cast<__bf16>(o0 * inv), static_cast<__bf16>(o1 * inv)};
   reinterpret_cast<uint32_t*>(orow)[lane] = __builtin_bit_cast(uint32_t, pk);
 }
 
 // Fixed partitions: merge sequences with more than one partition; zero empty ones.
-// One work-group of kMergeWaves waves per (query head hq, sequence b).
+// Work-group = kMergeWaves independent waves, wave v = query head
+// blockIdx.x * kMergeWaves + v of sequence blockIdx.y.
 __global__ __launch_bounds__(kMergeWaves * 64) void paged_decode_partition_reduce_kernel(
-    DecodeParams P) {
-  const int hq = blockIdx.x;
+    DecodeParams P, int num_heads) {
+  const int hq = blockIdx.x * kMergeWaves + (threadIdx.x >> 6);
   const int b = blockIdx.y;
   const int lane = threadIdx.x & 63;
+  if (hq >= num_heads) return;  // no barriers in this kernel
   const int ctx = P.ctx_lens[b];
   uint16_t* orow = P.out + b * P.out_row_stride + static_cast<int64_t>(hq) * kHead;
   if (ctx <= 0) {
-    if (threadIdx.x < 64) reinterpret_cast<uint32_t*>(orow)[lane] = 0u;
+    reinterpret_cast<uint32_t*>(orow)[lane] = 0u;
     return;
   }
   const int nparts = min((ctx + P.part_tokens - 1) / P.part_tokens, P.max_parts);
@@ -648,22 +655,23 @@ __global__ __launch_bounds__(kMergeWaves * 64) void paged_decode_partition_reduc
   const int h = hq / P.gqa;
   const int j = hq - h * P.gqa;
   const int64_t first = (static_cast<int64_t>(b) * P.num_kv_heads + h) * P.max_parts * P.gqa + j;
-  merge_rows(orow, P.part_o, P.part_ml, first, P.gqa, nparts, first, sink_log2(P, hq));
+  merge_rows(orow, P.part_o, P.part_ml, first, P.gqa, nparts, first, sink_log2(P, hq), lane);
 }
 
 // Balanced schedule: merge sequences cut across work-groups; zero empty ones.
-// One work-group of kMergeWaves waves per (query head hq, sequence b).
+// Work-group = kMergeWaves independent waves, as the partition reduce.
 __global__ __launch_bounds__(kMergeWaves * 64) void paged_decode_balanced_reduce_kernel(
-    DecodeParams P) {
-  const int hq = blockIdx.x;
+    DecodeParams P, int num_heads) {
+  const int hq = blockIdx.x * kMergeWaves + (threadIdx.x >> 6);
   const int b = blockIdx.y;
   const int lane = threadIdx.x & 63;
+  if (hq >= num_heads) return;  // no barriers in this kernel
   uint16_t* orow = P.out + b * P.out_row_stride + static_cast<int64_t>(hq) * kHead;
   const int t0 = P.tile_off[b];
   const int t1 = P.tile_off[b + 1];
   const int S = P.tile_off[P.batch + 1];
   if (t1 <= t0) {
-    if (threadIdx.x < 64) reinterpret_cast<uint32_t*>(orow)[lane] = 0u;
+    reinterpret_cast<uint32_t*>(orow)[lane] = 0u;
     return;
   }
   const int w0 = t0 / S;
@@ -678,7 +686,7 @@ __global__ __launch_bounds__(kMergeWaves * 64) void paged_decode_balanced_reduce
   const int64_t first_alt = ((static_cast<int64_t>(w0) * 2 + slot0) * hk + h) * P.gqa + j;
   const int64_t first = ((static_cast<int64_t>(w0) * 2 + 0) * hk + h) * P.gqa + j;
   merge_rows(orow, P.part_o, P.part_ml, first, 2 * hk * P.gqa, w1 - w0 + 1, first_alt,
-             sink_log2(P, hq));
+             sink_log2(P, hq), lane);
 }
 
 // Tuning knob (compile-time): tiles per load set.
@@ -950,13 +958,14 @@ extern "C" int fk_paged_decode_reduce(
                    batch, num_heads, num_kv_heads, head_size, block_size, num_blocks, scale,
                    window_left, sinks, part_tokens, max_parts, workspace, ws_bytes);
   if (rc != FK_OK || batch == 0) return rc;
-  const dim3 grid(static_cast<unsigned>(num_heads), static_cast<unsigned>(batch));
+  const dim3 grid(static_cast<unsigned>((num_heads + kMergeWaves - 1) / kMergeWaves),
+                  static_cast<unsigned>(batch));
   if (L.balanced)
     hipLaunchKernelGGL(paged_decode_balanced_reduce_kernel, grid, dim3(kMergeWaves * 64), 0,
-                       as_stream(stream), L.P);
+                       as_stream(stream), L.P, num_heads);
   else
     hipLaunchKernelGGL(paged_decode_partition_reduce_kernel, grid, dim3(kMergeWaves * 64), 0,
-                       as_stream(stream), L.P);
+                       as_stream(stream), L.P, num_heads);
   return check_launch("fk_paged_decode_reduce");
 }
 

@@ -172,9 +172,10 @@ int fk_paged_decode_plan(int64_t batch, int num_heads, int num_kv_heads, int hea
  *    ctx_lens: int32 [batch]; 0 gives a zero output row.
  * out: [batch, num_heads, head_size] BF16 rows `out_row_stride` elements apart.
  * part_tokens / max_parts: from fk_paged_decode_plan.  With fixed partitions,
- *    max_seq_len must be >= every ctx_lens[b] (tokens past part_tokens *
- *    max_parts are not attended); the balanced schedule reads the lengths on
- *    the device and has no such bound.
+ *    partition p covers tokens [p * part_tokens, (p + 1) * part_tokens) and the
+ *    last one runs on to the context end, so every key is attended whatever the
+ *    plan's max_seq_len (a context longer than it makes the last partition
+ *    longer); the balanced schedule reads the lengths on the device.
  * workspace: device memory of the plan's workspace_bytes, 16-byte aligned.
  * Supported: head_size 128; Hq/Hk in 1..16; block_size a power of two >= 16;
  *    batch <= 65535 (<= 8192 for the balanced schedule).

@@ -229,10 +229,15 @@ def dequant_kv(cache: np.ndarray, scale: np.ndarray | None, q_dtype: str) -> np.
     (_cast_kv_tile, triton_unified_attention.py:64-67).  Non-fp8 caches pass through."""
     if cache.dtype != np.uint8:
         return np.asarray(cache, np.float32)
-    v = fp8_e4m3fn_decode(cache)
-    if scale is not None:
-        v = v * np.asarray(scale, np.float32).reshape(1, 1, -1, 1)
-    return round_to(v, q_dtype)
+    hk = cache.shape[2]
+    sc = np.ones(hk, np.float32) if scale is None else np.asarray(scale, np.float32).reshape(hk)
+    # The value is a function of (code, kv head) only: tabulate round(decode(c) * s_h)
+    # for the 256 codes of each head, then gather (the same values, one pass).
+    tables = round_to(E4M3FN_TABLE[None, :] * sc[:, None], q_dtype)  # [Hk, 256]
+    out = np.empty(cache.shape, np.float32)
+    for h in range(hk):
+        out[:, :, h, :] = tables[h][cache[:, :, h, :]]
+    return out
 
 
 def attend_one(q: np.ndarray, k_seq: np.ndarray, v_seq: np.ndarray, scale: float,
@@ -252,17 +257,21 @@ def attend_one(q: np.ndarray, k_seq: np.ndarray, v_seq: np.ndarray, scale: float
         return np.zeros((hq, d), np.float64)
     grp = hq // hk
     qh = q.astype(np.float64).reshape(hk, grp, d)
-    k = k_seq.astype(np.float64).transpose(1, 2, 0)  # [Hk, D, n]
-    v = v_seq.astype(np.float64).transpose(1, 0, 2)  # [Hk, n, D]
-    s = np.matmul(qh, k) * scale  # [Hk, grp, n]
-    m = s.max(axis=-1, keepdims=True)
-    if sinks is not None:
-        m = np.maximum(m, np.asarray(sinks, np.float64).reshape(hk, grp, 1))
-    p = np.exp(s - m)
-    den = p.sum(axis=-1, keepdims=True)
-    if sinks is not None:
-        den = den + np.exp(np.asarray(sinks, np.float64).reshape(hk, grp, 1) - m)
-    return np.matmul(p / den, v).reshape(hq, d)
+    sk = None if sinks is None else np.asarray(sinks, np.float64).reshape(hk, grp, 1)
+    out = np.empty((hk, grp, d), np.float64)
+    for h in range(hk):  # one kv head at a time: contiguous [n, D] operands, 2-D products
+        k = np.ascontiguousarray(k_seq[:, h, :], np.float64)
+        v = np.ascontiguousarray(v_seq[:, h, :], np.float64)
+        s = (qh[h] @ k.T) * scale  # [grp, n]
+        m = s.max(axis=-1, keepdims=True)
+        if sk is not None:
+            m = np.maximum(m, sk[h])
+        p = np.exp(s - m)
+        den = p.sum(axis=-1, keepdims=True)
+        if sk is not None:
+            den = den + np.exp(sk[h] - m)
+        out[h] = (p / den) @ v
+    return out.reshape(hq, d)
 
 
 def paged_decode(q: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray,

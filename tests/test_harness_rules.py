@@ -1,5 +1,5 @@
 """The reference bench's acceptance rule and paged-decode input fixer, restated here
-(``oracle.compare``, ``workloads.fix_paged_decode``), pinned on the CPU.
+(``oracle.compare``, ``oracle.harness.fix_paged_decode``), pinned on the CPU.
 
 The first two tests make the same assertions as the reference's harness test
 (tests/test_bench.py:269-316, sections 7a and 7b).  The others pin the rule's
@@ -15,7 +15,7 @@ import pytest
 import torch
 
 import oracle
-from fastkernels_amd import workloads
+from oracle.harness import fix_paged_decode
 
 
 def test_compare_statuses_as_reference_harness():
@@ -36,7 +36,7 @@ def test_fix_paged_decode_as_reference_harness():
     k0, v0 = k.clone(), v.clone()
     kw = {"k_cache": k, "v_cache": v, "block_table": torch.zeros(2, 3, dtype=torch.int32),
           "cache_seqlens": torch.zeros(2, dtype=torch.int32), "max_seq_len": 0}
-    workloads.fix_paged_decode(kw, ("k_cache", "v_cache"), generator=g)
+    fix_paged_decode(kw, ("k_cache", "v_cache"), generator=g)
     assert torch.equal(kw["k_cache"], k0) and torch.equal(kw["v_cache"], v0)
     assert int(kw["block_table"].min()) >= 0 and int(kw["block_table"].max()) < 4
     assert int(kw["cache_seqlens"].min()) >= 1
@@ -51,17 +51,17 @@ def test_fix_paged_decode_ranges_and_layouts():
     nhd = torch.randn(6, 16, 2, 8)  # [num_blocks, page 16, Hk 2, D 8]
     kw = {"k_cache": nhd, "v_cache": nhd, "block_table": torch.zeros(4000, 5, dtype=torch.int32),
           "cache_seqlens": torch.zeros(4000, dtype=torch.int32)}
-    workloads.fix_paged_decode(kw, generator=g, page_dim=1)
+    fix_paged_decode(kw, generator=g, page_dim=1)
     sl, bt = kw["cache_seqlens"], kw["block_table"]
     assert int(sl.min()) == 1 and int(sl.max()) == 5 * 16
     assert set(bt.unique().tolist()) == set(range(6))
     assert "max_seq_len" not in kw
     kw = {"k_cache": nhd, "v_cache": nhd, "block_table": torch.zeros(4000, 5, dtype=torch.int32),
           "cache_seqlens": torch.zeros(4000, dtype=torch.int32)}
-    workloads.fix_paged_decode(kw, generator=g)  # reference geometry: page size = shape[-2] = 2
+    fix_paged_decode(kw, generator=g)  # reference geometry: page size = shape[-2] = 2
     assert int(kw["cache_seqlens"].max()) == 5 * 2
     with pytest.raises(ValueError):
-        workloads.fix_paged_decode({"k_cache": nhd}, generator=g)
+        fix_paged_decode({"k_cache": nhd}, generator=g)
 
 
 def test_compare_matched_ratio_boundary():

@@ -21,6 +21,11 @@ its own formula:
                    context and with an explicit bottom-right mask otherwise;
                    q_len = 1 equals paged_decode; a query's output does not depend
                    on keys after its position; a planted top-left mask is caught;
+  varlen_prefill   torch SDPA (float64) per sequence over its dense K/V slice with the
+                   end-aligned mask (and without it, non-causal); equal to
+                   paged_prefill on the same keys scattered into shuffled pages; a
+                   planted cu_seqlens_q / cu_seqlens_k swap is caught;
+  torch_path       decode_torch (the CPU baseline leg) against paged_decode;
   merge_attn_states  attention over a key set split in two and merged equals
                    torch SDPA over the whole set, and out_lse equals
                    torch.logsumexp of all scores (library); the special cases
@@ -499,6 +504,104 @@ def test_paged_prefill_decode_case_and_causality():
     q, kc, vc, bt, cu_q, cu_k = _prefill_case(seed=24, q_lens=(5,), k_lens=(3,))
     z = oracle.paged_prefill(q, kc, vc, bt, cu_q, cu_k, 0.25)
     assert np.array_equal(z[:2], np.zeros_like(z[:2])) and np.abs(z[2:]).sum() > 0
+
+
+# ---------------------------------------------------------------------------
+# dense (varlen) prefill: _prefill_torch_from_tensors, attention_impl.py:624-638
+# ---------------------------------------------------------------------------
+def _varlen_case(seed=31, q_lens=(5, 1, 9, 4), k_lens=(5, 17, 30, 4), hq=4, hk=2, d=16):
+    """Dense keys of several sequences packed back to back, with k_len > q_len for some
+    (chunks over a cached prefix) and k_len == q_len for others (whole prompts)."""
+    rng = np.random.default_rng(seed)
+    cu_q = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
+    cu_k = np.concatenate([[0], np.cumsum(k_lens)]).astype(np.int32)
+    q = rng.standard_normal((int(cu_q[-1]), hq, d)).astype(np.float32)
+    key = rng.standard_normal((int(cu_k[-1]), hk, d)).astype(np.float32)
+    value = rng.standard_normal((int(cu_k[-1]), hk, d)).astype(np.float32)
+    return q, key, value, cu_q, cu_k
+
+
+def test_varlen_prefill_vs_torch_sdpa():
+    """Each sequence against float64 torch SDPA over its own dense K/V slice, with the
+    end-aligned causal mask (key_offset = k_len - q_len, attention_impl.py:630-636)."""
+    q, key, value, cu_q, cu_k = _varlen_case()
+    scale = 0.3
+    ours = oracle.varlen_prefill(q, key, value, cu_q, cu_k, scale)
+    hq, hk = q.shape[1], key.shape[1]
+    for i in range(len(cu_q) - 1):
+        qs, qe, ks, ke = int(cu_q[i]), int(cu_q[i + 1]), int(cu_k[i]), int(cu_k[i + 1])
+        ql, kl = qe - qs, ke - ks
+        k = torch.from_numpy(key[ks:ke]).double().repeat_interleave(hq // hk, 1).transpose(0, 1)
+        v = torch.from_numpy(value[ks:ke]).double().repeat_interleave(hq // hk, 1).transpose(0, 1)
+        qq = torch.from_numpy(q[qs:qe]).double().transpose(0, 1)
+        mask = torch.arange(kl)[None, :] <= (kl - ql + torch.arange(ql))[:, None]
+        ref = F.scaled_dot_product_attention(qq, k, v, attn_mask=mask, scale=scale)
+        np.testing.assert_allclose(ours[qs:qe], ref.transpose(0, 1).numpy(), rtol=1e-10,
+                                   atol=1e-12)
+    # non-causal: every query sees its sequence's whole slice
+    full = oracle.varlen_prefill(q, key, value, cu_q, cu_k, scale, causal=False)
+    i = 2
+    qs, qe, ks, ke = int(cu_q[i]), int(cu_q[i + 1]), int(cu_k[i]), int(cu_k[i + 1])
+    k = torch.from_numpy(key[ks:ke]).double().repeat_interleave(hq // hk, 1).transpose(0, 1)
+    v = torch.from_numpy(value[ks:ke]).double().repeat_interleave(hq // hk, 1).transpose(0, 1)
+    qq = torch.from_numpy(q[qs:qe]).double().transpose(0, 1)
+    ref = F.scaled_dot_product_attention(qq, k, v, scale=scale)
+    np.testing.assert_allclose(full[qs:qe], ref.transpose(0, 1).numpy(), rtol=1e-10, atol=1e-12)
+
+
+def test_varlen_prefill_equals_paged_prefill_on_scattered_keys():
+    """Closed-form layout relation: the same keys scattered into shuffled pages and read
+    through a block table give the dense result (varlen == paged)."""
+    q, key, value, cu_q, cu_k = _varlen_case(seed=32)
+    hk, d = key.shape[1], key.shape[2]
+    bs = 8
+    k_lens = np.diff(cu_k)
+    pages = [(int(n) + bs - 1) // bs for n in k_lens]
+    nb = sum(pages) + 3
+    rng = np.random.default_rng(5)
+    perm = rng.permutation(nb)
+    kc = rng.standard_normal((nb, bs, hk, d)).astype(np.float32)  # junk outside the keys
+    vc = rng.standard_normal((nb, bs, hk, d)).astype(np.float32)
+    bt = np.full((len(k_lens), max(pages)), -1, np.int32)
+    off = 0
+    for i, n in enumerate(k_lens):
+        bt[i, :pages[i]] = perm[off:off + pages[i]]
+        off += pages[i]
+        for t in range(int(n)):
+            kc[bt[i, t // bs], t % bs] = key[cu_k[i] + t]
+            vc[bt[i, t // bs], t % bs] = value[cu_k[i] + t]
+    dense = oracle.varlen_prefill(q, key, value, cu_q, cu_k, 0.25)
+    paged = oracle.paged_prefill(q, kc, vc, bt, cu_q, cu_k, 0.25)
+    np.testing.assert_allclose(dense, paged, rtol=1e-12, atol=1e-13)
+
+
+def test_varlen_prefill_planted_cu_seqlens_swap_is_caught():
+    """A plausible slip, slicing Q by cu_seqlens_k and K by cu_seqlens_q, changes the
+    result: the checks above would catch an oracle that made it."""
+    q, key, value, cu_q, cu_k = _varlen_case(seed=33, q_lens=(3, 6), k_lens=(7, 6))
+    good = oracle.varlen_prefill(q, key, value, cu_q, cu_k, 0.25)
+    qpad = np.concatenate([q, np.zeros((int(cu_k[-1]) - q.shape[0],) + q.shape[1:], q.dtype)])
+    swapped = oracle.varlen_prefill(qpad, key, value, cu_k, cu_q, 0.25)[:q.shape[0]]
+    assert not np.allclose(good, swapped, atol=1e-3)
+
+
+# ---------------------------------------------------------------------------
+# the reference's torch decode path (the CPU baseline leg), oracle/torch_path.py
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 2e-2)])
+def test_decode_torch_matches_oracle(dtype, tol):
+    """oracle.torch_path.decode_torch (what bench.py's cpu_baseline times) against the
+    pinned numpy paged_decode: float32 to rounding, bf16 within the bf16 bar."""
+    from oracle.torch_path import decode_torch
+
+    q, kc, vc, bt, lens = _decode_case(b=5, hq=8, hk=2, d=32, bs=8, nb=64, seed=3)
+    out = decode_torch(torch.from_numpy(q).to(dtype), torch.from_numpy(kc).to(dtype),
+                       torch.from_numpy(vc).to(dtype), torch.from_numpy(lens),
+                       torch.from_numpy(bt), 0.2)
+    qr, kr, vr = (oracle.round_to(a, "bf16") if dtype == torch.bfloat16 else a
+                  for a in (q, kc, vc))
+    ref = oracle.paged_decode(qr, kr, vr, bt, lens, 0.2)
+    np.testing.assert_allclose(out.float().numpy(), ref, rtol=tol, atol=tol)
 
 
 @pytest.mark.parametrize("window_left", [0, 3, 9, 40])
