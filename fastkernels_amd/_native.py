@@ -57,6 +57,10 @@ _SIGNATURES = {
                                        c_void_p, c_int64, c_int, c_int, c_int, c_int, c_int64,
                                        c_float, c_int, c_void_p, c_int64, c_int64, c_void_p,
                                        c_int64, c_void_p]),
+    "fk_paged_decode_noalloc": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p,
+                                        c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_int64,
+                                        c_void_p, c_int64, c_int, c_int, c_int, c_int, c_int64,
+                                        c_float, c_int, c_void_p, c_int64, c_int64, c_void_p]),
     "fk_silu_and_mul": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_int64, c_int64, c_int,
                                 c_void_p]),
     "fk_store_paged_decode": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64,

@@ -212,6 +212,26 @@ int fk_paged_decode_reduce(void* out, int64_t out_row_stride, const void* q,
                            int64_t part_tokens, int64_t max_parts, void* workspace,
                            int64_t workspace_bytes, void* stream);
 
+/* Paged decode attention for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  No counterpart in the
+ * reference: it is fk_paged_decode without the workspace argument.  The split-context
+ * workspace is a static device array of FK_PAGED_DECODE_NOALLOC_MAX_BYTES that each GPU
+ * holds from the library's load until the process ends; its address is resolved on the
+ * first call on each device.  Arguments and results as fk_paged_decode (same plan from
+ * fk_paged_decode_plan); a plan whose workspace_bytes exceeds the static array is
+ * rejected with FK_ERR_WORKSPACE (use fk_paged_decode then).  Nothing is allocated.
+ * Every call on one device shares the array: calls that overlap on one device
+ * (concurrent streams or host threads) race on it and must be serialised by the caller. */
+#define FK_PAGED_DECODE_NOALLOC_MAX_BYTES (32LL << 20)
+int fk_paged_decode_noalloc(void* out, int64_t out_row_stride, const void* q,
+                            int64_t q_row_stride, const void* k_cache, const void* v_cache,
+                            int kv_dtype, const float* k_scale, const float* v_scale,
+                            const int32_t* block_tables, int64_t bt_row_stride,
+                            const int32_t* ctx_lens, int64_t batch, int num_heads,
+                            int num_kv_heads, int head_size, int block_size, int64_t num_blocks,
+                            float scale, int window_left, const float* sinks,
+                            int64_t part_tokens, int64_t max_parts, void* stream);
+
 /* store_kvcache into a cache of another dtype (StoreKVCache.forward with, e.g., a bf16
  * key and a float8_e4m3fn cache: the Triton store converts with tl.store's implicit
  * cast, store_kvcache.py:32-35).  Each element is widened to fp32 and converted to the
