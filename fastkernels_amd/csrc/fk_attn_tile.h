@@ -184,4 +184,49 @@ __device__ __forceinline__ void pv_accumulate(floatx4_t (&o)[8], short4_t pa,
   pv_accumulate(o, pa, vb);
 }
 
+// ---------------------------------------------------------------------------
+// Head-size-generic forms (the decode kernel's head sizes 64, 128, 256).  With
+// N = D / 32 K chunks per row and D / 16 dims per lane: S = K Q^T takes N
+// 16x16x32 MFMAs; lane (r, g) holds V dims (D/16) r .. (D/16) r + D/16 - 1 of
+// rows 4g .. 4g+3 as NW = D / 32 words per row, and P.V takes D / 16 16x16x16
+// MFMAs, slice d accumulating dim (D/16) r + d of query column 4g + i in o[d][i].
+// At D = 128 these are exactly the functions above.
+// ---------------------------------------------------------------------------
+template <int N>
+__device__ __forceinline__ floatx4_t qk_scores_n(const uint4 (&kc)[N], const bf16x8_t (&qb)[N]) {
+  floatx4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int c = 0; c < N; ++c)
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kc[c]), qb[c],
+                                                 acc, 0, 0, 0);
+  return acc;
+}
+
+// B operands of P.V from the V rows held as words (2 bf16 dims per word): slice d
+// takes dim d of rows 4g .. 4g+3.
+template <int NW>
+__device__ __forceinline__ void v_operands_w(const uint32_t (&vw)[4][NW], short4_t (&vb)[2 * NW]) {
+#pragma unroll
+  for (int d = 0; d < 2 * NW; ++d) {
+    const int wi = d >> 1;
+    uint32_t b01, b23;
+    if (d & 1) {
+      b01 = hi_pair(vw[0][wi], vw[1][wi]);
+      b23 = hi_pair(vw[2][wi], vw[3][wi]);
+    } else {
+      b01 = lo_pair(vw[0][wi], vw[1][wi]);
+      b23 = lo_pair(vw[2][wi], vw[3][wi]);
+    }
+    vb[d] = __builtin_bit_cast(short4_t, make_uint2(b01, b23));
+  }
+}
+
+template <int N>
+__device__ __forceinline__ void pv_accumulate_n(floatx4_t (&o)[N], short4_t pa,
+                                                const short4_t (&vb)[N]) {
+#pragma unroll
+  for (int d = 0; d < N; ++d)
+    o[d] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, vb[d], o[d], 0, 0, 0);
+}
+
 }  // namespace fk

@@ -22,11 +22,17 @@
 // dequantised per kv head as float(x) * scale, the per-tensor rule of
 // _cast_kv_tile (triton_unified_attention.py:51-67): k_scale is folded into the
 // score scale and v_scale into the output, which is algebraically the same.
+// Head sizes D = 64, 128 and 256 (the reference builds FlashAttnDecode at 128,
+// and at 256 and 64 for Qwen3-Next and Whisper, L2/qwen3_next_attention.py:
+// 148-150, L2/whisper_attention.py:185-190) are template instantiations.
 //
-// Work decomposition.  A work-group has one wave64 per kv head (up to 8); the
-// waves of a group stream the same token rows of the NHD cache, so each
-// token's Hk * 256-byte row is read whole within a short window.  Two
-// schedules share the per-wave tile loop:
+// Work decomposition.  A wave owns one "virtual head": a kv head and a block
+// of up to 16 of its G query heads (the 16 query columns of an MFMA tile), so
+// groups larger than 16 take ceil(G / 16) waves per kv head, which stream the
+// same K/V rows.  A work-group has up to 8 such waves; the waves of a group
+// stream the same token rows of the NHD cache, so each token's Hk * D-element
+// row is read whole within a short window.  Two schedules share the per-wave
+// tile loop:
 //   balanced (default): the 16-token tiles of all sequences are concatenated
 //     and cut into one equal range per work-group, with one work-group per
 //     CU.  A sequence wholly inside a range is finished in place; a sequence
@@ -36,11 +42,11 @@
 //   fixed partitions (explicit num_splits): work-group = (partition p of
 //     part_tokens tokens, sequence b), the classic flash-decoding split.
 //
-// MFMA mapping: fk_attn_tile.h, with the G query heads of a kv head as the
-// 16 query columns of each tile.  Rows j >= G of the 16-row MFMA tiles are padding (zero Q, zero P): the matrix
-// cores have ~80x the throughput this HBM-bound loop needs, so the padding is
-// free, while the VALU work per token stays at a few instructions (no
-// cross-lane dot-product reductions, two row-swap permutes per tile for the max).
+// MFMA mapping: fk_attn_tile.h.  Rows j >= G of the 16-row MFMA tiles are
+// padding (zero Q, zero P): the matrix cores have ~80x the throughput this
+// HBM-bound loop needs, so the padding is free, while the VALU work per token
+// stays at a few instructions (no cross-lane dot-product reductions, two
+// row-swap permutes per tile for the max).
 #include "fk_attn_tile.h"
 
 namespace fk {
@@ -58,18 +64,20 @@ struct DecodeParams {
   const int32_t* block_tables;
   int64_t bt_row_stride;
   const int32_t* ctx_lens;
+  int num_heads;
   int num_kv_heads;
-  int gqa;
+  int gqa;           // query heads per kv head
+  int col_blocks;    // waves per kv head: ceil(gqa / 16)
   int block_size_log2;
   int part_tokens;
   int max_parts;
   int64_t num_blocks;
   float scale_log2;  // softmax scale * log2(e)
-  float* part_o;     // partial outputs (unnormalised), rows of 128 floats
+  float* part_o;     // partial outputs (unnormalised), rows of D floats
   float* part_ml;    // per partial row: (max, sum) in the log2 domain
   int32_t* tile_off; // balanced schedule: [batch + 1] tile prefix sums, then range size
   int batch;
-  int num_groups;    // balanced schedule: work-groups per kv-head group
+  int num_groups;    // balanced schedule: work-groups per virtual-head group
   int window_left;   // sliding window: keys >= ctx - 1 - window_left (-1: none)
   const float* sinks;  // attention sink logits [num_heads] fp32, or nullptr
   // Fused store (fk_store_paged_decode); new_k == nullptr for a plain decode.
@@ -81,6 +89,24 @@ struct DecodeParams {
   int64_t new_v_stride;
   int slot_is_i64;
 };
+
+// The query heads one wave handles: kv head kvh, query heads qbase .. qbase +
+// ncols - 1 (a block of at most 16 of the kv head's group).
+struct VHead {
+  int kvh;
+  int qbase;
+  int ncols;
+  bool first;  // the kv head's first column block (it writes the fused-store row)
+};
+__device__ __forceinline__ VHead vhead(const DecodeParams& P, int v) {
+  VHead vh;
+  vh.kvh = v / P.col_blocks;
+  const int cb = v - vh.kvh * P.col_blocks;
+  vh.qbase = vh.kvh * P.gqa + 16 * cb;
+  vh.ncols = min(16, P.gqa - 16 * cb);
+  vh.first = cb == 0;
+  return vh;
+}
 
 // Page id of token `tok` of sequence b, or -1 when the block-table entry is
 // negative, >= num_blocks, or past the row (index >= bt_row_stride): such a
@@ -107,6 +133,78 @@ __device__ __forceinline__ float sink_log2(const DecodeParams& P, int hq) {
   return P.sinks ? P.sinks[hq] * kLog2e : kNegInf;
 }
 
+// Loads of N 32-bit words from p (16-, 8- or 4-byte vectors; p is aligned to
+// the vector).
+template <int N>
+__device__ __forceinline__ void ld_words(const uint8_t* p, uint32_t (&w)[N]) {
+  if constexpr (N == 1) {
+    w[0] = *reinterpret_cast<const uint32_t*>(p);
+  } else if constexpr (N == 2) {
+    const uint2 x = *reinterpret_cast<const uint2*>(p);
+    w[0] = x.x;
+    w[1] = x.y;
+  } else {
+#pragma unroll
+    for (int q = 0; q < N / 4; ++q) {
+      const uint4 x = *reinterpret_cast<const uint4*>(p + 16 * q);
+      w[4 * q] = x.x;
+      w[4 * q + 1] = x.y;
+      w[4 * q + 2] = x.z;
+      w[4 * q + 3] = x.w;
+    }
+  }
+}
+
+// Raw registers one wave loads for one 16-token tile of head size D.  Lane
+// (r, g): K row r -- bf16: the D/32 16-byte chunks of dims 32c + 8g .. +7;
+// fp8: the D/4 bytes of dims (D/4) g .. (D/4) g + D/4 - 1 -- and V rows 4g+i,
+// dims (D/16) r .. (D/16) r + D/16 - 1, as kVWords words.  load_tile only
+// issues the loads; conversion and masking happen in the consumer, after the
+// loads of the following tile have been issued.
+template <bool kFp8, int D>
+struct DTile {
+  static constexpr int kKLoads = kFp8 ? D / 64 : D / 32;  // 16-byte K loads
+  static constexpr int kVWords = kFp8 ? D / 64 : D / 32;  // 32-bit words per V row
+  uint4 k[kKLoads];
+  uint32_t v[4][kVWords];
+};
+
+// K operand chunks (bf16, dims as described at DTile) of a loaded tile.
+template <bool kFp8, int D>
+__device__ __forceinline__ void k_chunks_d(const DTile<kFp8, D>& t, uint4 (&kc)[D / 32]) {
+  if constexpr (!kFp8) {
+#pragma unroll
+    for (int c = 0; c < D / 32; ++c) kc[c] = t.k[c];
+  } else {
+    // chunk c = bytes 8c .. 8c+7 of the lane's D/4.
+#pragma unroll
+    for (int c = 0; c < D / 32; ++c) {
+      const uint4& src = t.k[c >> 1];
+      const uint32_t w0 = (c & 1) ? src.z : src.x;
+      const uint32_t w1 = (c & 1) ? src.w : src.y;
+      const uint2 lo = fp8x4_to_bf16x4(w0), hi = fp8x4_to_bf16x4(w1);
+      kc[c] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+    }
+  }
+}
+
+// V row i of a loaded tile as D/32 words of bf16 pairs (zero when !keep).
+template <bool kFp8, int D>
+__device__ __forceinline__ void v_words(const DTile<kFp8, D>& t, int i, bool keep,
+                                        uint32_t (&w)[D / 32]) {
+  if constexpr (!kFp8) {
+#pragma unroll
+    for (int q = 0; q < D / 32; ++q) w[q] = keep ? t.v[i][q] : 0u;
+  } else {
+#pragma unroll
+    for (int q = 0; q < D / 64; ++q) {
+      const uint2 x = fp8x4_to_bf16x4(t.v[i][q]);
+      w[2 * q] = keep ? x.x : 0u;
+      w[2 * q + 1] = keep ? x.y : 0u;
+    }
+  }
+}
+
 // Issues the loads of one tile from page `page` (>= 0, < num_blocks).  Loads
 // are unconditional so that every pipeline stage has the same number of loads
 // in flight and the compiler can wait for one stage with vmcnt(N) instead of
@@ -114,16 +212,16 @@ __device__ __forceinline__ float sink_log2(const DecodeParams& P, int hq) {
 // are discarded by the consumer.  Fused store: tile row j (-1: none) is read
 // from the new K/V row (nk / nv, this kv head's slice) instead of the cache,
 // by selecting each lane's address, so the loop has no extra control flow.
-template <bool kFp8>
-__device__ __forceinline__ void load_tile(const DecodeParams& P, int64_t page, int h, int tok0,
-                                          int r, int g, TileRegs<kFp8>& t, int j = -1,
+template <bool kFp8, int D>
+__device__ __forceinline__ void load_tile(const DecodeParams& P, int64_t page, int kvh, int tok0,
+                                          int r, int g, DTile<kFp8, D>& t, int j = -1,
                                           const uint8_t* nk = nullptr,
                                           const uint8_t* nv = nullptr) {
   const int bs_mask = (1 << P.block_size_log2) - 1;
   const int64_t slot0 = (page << P.block_size_log2) + (tok0 & bs_mask);
   constexpr int kElem = kFp8 ? 1 : 2;
-  const int64_t row_bytes = static_cast<int64_t>(P.num_kv_heads) * kHead * kElem;
-  const int64_t head_off = static_cast<int64_t>(h) * kHead * kElem;
+  const int64_t row_bytes = static_cast<int64_t>(P.num_kv_heads) * D * kElem;
+  const int64_t head_off = static_cast<int64_t>(kvh) * D * kElem;
   const uint8_t* krow = P.k_cache + (slot0 + r) * row_bytes + head_off;
   if (r == j) krow = nk;
   const uint8_t* vrow[4];
@@ -135,27 +233,27 @@ __device__ __forceinline__ void load_tile(const DecodeParams& P, int64_t page, i
   if constexpr (!kFp8) {
     // Per instruction: 16 rows x 64 contiguous bytes.
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
-      t.k[c] = ld16(krow + (32 * c + 8 * g) * 2);
+    for (int c = 0; c < D / 32; ++c) t.k[c] = ld16(krow + (32 * c + 8 * g) * 2);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) t.v[i] = ld16(vrow[i] + 8 * r * 2);
+    for (int i = 0; i < 4; ++i) ld_words(vrow[i] + (D / 16) * r * 2, t.v[i]);
   } else {
-    t.k[0] = ld16(krow + 32 * g);
-    t.k[1] = ld16(krow + 32 * g + 16);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) t.v[i] = ld8(vrow[i] + 8 * r);
+    for (int c = 0; c < D / 64; ++c) t.k[c] = ld16(krow + (D / 4) * g + 16 * c);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ld_words(vrow[i] + (D / 16) * r, t.v[i]);
   }
 }
 
 // ---------------------------------------------------------------------------
 // Fused store.  Sequence b's new token is at position p = ctx - 1.  The wave
-// that streams p's tile (one per kv head) loads b's new K/V row up front and,
-// when slot_mapping[b] is the slot of p in b's block table (the decode step),
-// uses it in place of the cache row at p, then writes it to the cache after
-// its tile loop, so no load waits for the store.  A slot that is not p's
-// ("orphan") is written by that same wave, or, when no wave streams p (no
-// context, or p past the launch's partitions), by a designated work-group; the
-// order of an orphan write against other reads of its slot is unspecified.
+// that streams p's tile (the kv head's first column block) loads b's new K/V
+// row up front and, when slot_mapping[b] is the slot of p in b's block table
+// (the decode step), uses it in place of the cache row at p, then writes it to
+// the cache after its tile loop, so no load waits for the store.  A slot that
+// is not p's ("orphan") is written by that same wave, or, when no wave streams
+// p (no context), by a designated work-group; the order of an orphan write
+// against other reads of its slot is unspecified.  Other column blocks of the
+// kv head read p from the new row too and write nothing.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ int64_t slot_of(const DecodeParams& P, const void* __restrict__ sm,
                                            int b) {
@@ -191,105 +289,110 @@ __device__ __forceinline__ int64_t valid_slot(const DecodeParams& P, const void*
   return (slot >= 0 && slot < (P.num_blocks << P.block_size_log2)) ? slot : -1;
 }
 
-// Writes kv head h of sequence b's new K and V rows to cache slot `slot`.
-template <bool kFp8>
-__device__ __forceinline__ void store_new_row(const DecodeParams& P, int b, int h, int64_t slot,
-                                              int lane) {
-  store_new_chunk<kFp8>(P, slot, h, lane, load_new_chunk<kFp8>(P, b, h, lane));
-}
-
-// One 16-byte chunk of sequence b's new K/V row for kv head h, in the layout
-// store_new_chunk writes: lanes 0..15 hold K chunk (lane & 15), lanes 16..31 V
-// chunk (lane & 15); chunk indices past the row (fp8) and lanes >= 32 re-read a
-// valid chunk and are not stored.
-template <bool kFp8>
-__device__ __forceinline__ uint4 load_new_chunk(const DecodeParams& P, int b, int h, int lane) {
+// One 16-byte chunk of sequence b's new K/V row for kv head kvh, in the layout
+// store_new_chunk writes: lanes 0..31 hold K chunk (lane & 31), lanes 32..63 V
+// chunk (lane & 31); chunk indices past the row re-read a valid chunk and are
+// not stored.
+template <bool kFp8, int D>
+__device__ __forceinline__ uint4 load_new_chunk(const DecodeParams& P, int b, int kvh, int lane) {
   constexpr int kElem = kFp8 ? 1 : 2;
-  constexpr int kChunks = kHead * kElem / 16;
-  const int c = min(lane & 15, kChunks - 1);
-  const int64_t head_off = static_cast<int64_t>(h) * kHead * kElem;
-  const bool is_v = (lane & 16) != 0;
+  constexpr int kChunks = D * kElem / 16;
+  const int c = min(lane & 31, kChunks - 1);
+  const int64_t head_off = static_cast<int64_t>(kvh) * D * kElem;
+  const bool is_v = lane >= 32;
   const uint8_t* src = (is_v ? P.new_v + b * P.new_v_stride : P.new_k + b * P.new_k_stride) +
                        head_off + 16 * c;
   return ld16(src);
 }
-template <bool kFp8>
-__device__ __forceinline__ void store_new_chunk(const DecodeParams& P, int64_t slot, int h,
+template <bool kFp8, int D>
+__device__ __forceinline__ void store_new_chunk(const DecodeParams& P, int64_t slot, int kvh,
                                                 int lane, const uint4& v) {
   constexpr int kElem = kFp8 ? 1 : 2;
-  constexpr int kChunks = kHead * kElem / 16;
-  const int c = lane & 15;
-  if (lane >= 32 || c >= kChunks) return;
-  const int64_t row_bytes = static_cast<int64_t>(P.num_kv_heads) * kHead * kElem;
-  uint8_t* dst = const_cast<uint8_t*>((lane & 16) ? P.v_cache : P.k_cache) + slot * row_bytes +
-                 static_cast<int64_t>(h) * kHead * kElem + 16 * c;
+  constexpr int kChunks = D * kElem / 16;
+  const int c = lane & 31;
+  if (c >= kChunks) return;
+  const int64_t row_bytes = static_cast<int64_t>(P.num_kv_heads) * D * kElem;
+  uint8_t* dst = const_cast<uint8_t*>(lane >= 32 ? P.v_cache : P.k_cache) + slot * row_bytes +
+                 static_cast<int64_t>(kvh) * D * kElem + 16 * c;
   *reinterpret_cast<uint4*>(dst) = v;
 }
 
-// Online-softmax state of one wave over the G query heads of one kv head, and
-// the tile loop that streams a token range [tok_begin, tok_end) of a sequence
-// through it (tok_begin a multiple of 16).
-template <int kG, bool kFp8, int U, bool kStore>
+// Writes kv head kvh of sequence b's new K and V rows to cache slot `slot`.
+template <bool kFp8, int D>
+__device__ __forceinline__ void store_new_row(const DecodeParams& P, int b, int kvh, int64_t slot,
+                                              int lane) {
+  store_new_chunk<kFp8, D>(P, slot, kvh, lane, load_new_chunk<kFp8, D>(P, b, kvh, lane));
+}
+
+// Online-softmax state of one wave over the query heads of one virtual head,
+// and the tile loop that streams a token range [tok_begin, tok_end) of a
+// sequence through it (tok_begin a multiple of 16).  Lane (r, g) of the O
+// accumulators holds O[column 4g + i][dims (D/16) r .. (D/16) r + D/16 - 1].
+template <int kG, int D, bool kFp8, int U, bool kStore>
 struct WaveState {
+  static constexpr int kKc = D / 32;  // K chunks per row (QK^T MFMAs per tile)
+  static constexpr int kSl = D / 16;  // P.V slices; also dims per lane
   float m_run;  // running max of column r (same in the 4 lanes of a column)
   float l_run;  // this lane's share of the running sum of column r
-  floatx4_t o[8];
+  floatx4_t o[kSl];
 
   // kStore: when the segment ends at the context end (tok_end == ctx) and
   // slot_mapping[b] is the slot of position ctx - 1, that position's K/V are
   // read from sequence b's new row instead of the cache (load_tile's row j),
   // and the row (one 16-byte chunk per lane, loaded up front) is written to the
-  // cache after the loop, so no load waits for the store.
+  // cache after the loop by the kv head's first column block, so no load waits
+  // for the store.
   // Keys below key_lo (the sliding window's start) are masked; tok_begin is
   // the start of the tile holding key_lo or later.
   __device__ __forceinline__ void run(const DecodeParams& P, const int32_t* __restrict__ bt,
-                                      const void* __restrict__ sm, int b, int h, int tok_begin,
-                                      int tok_end, int ctx, int key_lo, int r, int g) {
-    const int gqa = P.gqa;
+                                      const void* __restrict__ sm, int b, const VHead& vh,
+                                      int tok_begin, int tok_end, int ctx, int key_lo, int r,
+                                      int g) {
+    const int kvh = vh.kvh;
     SlotWords sw{-1, -1};
     uint4 new_chunk = make_uint4(0, 0, 0, 0);  // this lane's chunk of b's new row
-    const uint8_t* nk = nullptr;  // b's new K / V row, kv head h
+    const uint8_t* nk = nullptr;  // b's new K / V row, kv head kvh
     const uint8_t* nv = nullptr;
     int ftok0 = -1;  // first token of the tile holding ctx - 1, if this segment ends there
     if constexpr (kStore) {
       constexpr int kElem = kFp8 ? 1 : 2;
-      const int64_t head_off = static_cast<int64_t>(h) * kHead * kElem;
+      const int64_t head_off = static_cast<int64_t>(kvh) * D * kElem;
       nk = P.new_k + b * P.new_k_stride + head_off;
       nv = P.new_v + b * P.new_v_stride + head_off;
-      new_chunk = load_new_chunk<kFp8>(P, b, h, 16 * g + r);
+      new_chunk = load_new_chunk<kFp8, D>(P, b, kvh, 16 * g + r);
       sw = slot_words(P, sm, b);
       if (tok_end == ctx && ctx > tok_begin)
         ftok0 = tok_begin + kTile * ((ctx - 1 - tok_begin) / kTile);
     }
-    const bool head_ok = r < gqa;
-    // Q^T operand: column r = query head h*G + r; dims permuted as the K loads.
-    bf16x8_t qb[4];
+    const bool head_ok = r < vh.ncols;
+    // Q^T operand: column r = query head qbase + r; dims permuted as the K loads.
+    bf16x8_t qb[kKc];
     {
-      const uint16_t* qp = P.q + b * P.q_row_stride + static_cast<int64_t>(h * gqa + r) * kHead;
+      const uint16_t* qp = P.q + b * P.q_row_stride + static_cast<int64_t>(vh.qbase + r) * D;
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int d0 = kFp8 ? 32 * g + 8 * c : 32 * c + 8 * g;
+      for (int c = 0; c < kKc; ++c) {
+        const int d0 = kFp8 ? (D / 4) * g + 8 * c : 32 * c + 8 * g;
         uint4 v = head_ok ? *reinterpret_cast<const uint4*>(qp + d0) : make_uint4(0, 0, 0, 0);
         qb[c] = __builtin_bit_cast(bf16x8_t, v);
       }
     }
     float s2 = P.scale_log2;
-    if (kFp8 && P.k_scale) s2 *= P.k_scale[h];
+    if (kFp8 && P.k_scale) s2 *= P.k_scale[kvh];
 
     m_run = kNegInf;
     l_run = 0.f;
 #pragma unroll
-    for (int d = 0; d < 8; ++d) o[d] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+    for (int d = 0; d < kSl; ++d) o[d] = floatx4_t{0.f, 0.f, 0.f, 0.f};
 
     // Visible tokens are [key_lo, tok_end): one unsigned compare of tok - key_lo
     // against their count checks both bounds.
     const uint32_t span = static_cast<uint32_t>(tok_end - key_lo);
     // One 16-token tile: scores, online softmax update, P.V accumulation.
-    auto process = [&](int tok0, int64_t page, const TileRegs<kFp8>& cur) {
+    auto process = [&](int tok0, int64_t page, const DTile<kFp8, D>& cur) {
       const int rel0 = tok0 + 4 * g - key_lo;
-      uint4 kc[4];
-      k_chunks(cur, kc);
-      const floatx4_t acc = qk_scores(kc, qb);
+      uint4 kc[kKc];
+      k_chunks_d(cur, kc);
+      const floatx4_t acc = qk_scores_n(kc, qb);
       float s[4];
       float mt = kNegInf;
 #pragma unroll
@@ -318,18 +421,19 @@ struct WaveState {
         for (int i = 0; i < 4; ++i) {
           const float a = row_value<kG>(alpha, g, i);
 #pragma unroll
-          for (int d = 0; d < 8; ++d) o[d][i] *= a;
+          for (int d = 0; d < kSl; ++d) o[d][i] *= a;
         }
       }
       const short4_t pa = p_operand(pr);
       // V rows past the context (inside a valid page) may hold anything: zero
       // them so that P = 0 never meets a NaN.
-      uint4 vr[4];
+      uint32_t vw[4][D / 32];
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        vr[i] = (page >= 0 && static_cast<uint32_t>(rel0 + i) < span) ? v_row(cur, i)
-                                                                     : make_uint4(0, 0, 0, 0);
-      pv_accumulate(o, pa, vr);
+        v_words(cur, i, page >= 0 && static_cast<uint32_t>(rel0 + i) < span, vw[i]);
+      short4_t vb[kSl];
+      v_operands_w(vw, vb);
+      pv_accumulate_n(o, pa, vb);
     };
 
     const int ntiles = (tok_end - tok_begin + kTile - 1) / kTile;
@@ -339,9 +443,7 @@ struct WaveState {
     int64_t pc_page = -1;
     // Issues the loads of tiles t0 .. t0+U-1 into `buf` (unconditional; tiles
     // past the end re-read the last tile, which hits in cache).
-    // Issues the loads of tiles t0 .. t0+U-1 into `buf` (unconditional; tiles
-    // past the end re-read the last tile, which hits in cache).
-    auto fetch = [&](int t0, TileRegs<kFp8>(&buf)[U], int64_t(&pg)[U]) {
+    auto fetch = [&](int t0, DTile<kFp8, D>(&buf)[U], int64_t(&pg)[U]) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int tok0 = tok_begin + kTile * min(t0 + u, ntiles - 1);
@@ -363,10 +465,10 @@ struct WaveState {
           const bool hit = tok0 == ftok0 && pg[u] >= 0 && slot_value(P, sw) == want;
           j = hit ? ctx - 1 - tok0 : -1;
         }
-        load_tile<kFp8>(P, pg[u] < 0 ? 0 : pg[u], h, tok0, r, g, buf[u], j, nk, nv);
+        load_tile<kFp8, D>(P, pg[u] < 0 ? 0 : pg[u], kvh, tok0, r, g, buf[u], j, nk, nv);
       }
     };
-    auto consume = [&](int t0, const TileRegs<kFp8>(&buf)[U], const int64_t(&pg)[U]) {
+    auto consume = [&](int t0, const DTile<kFp8, D>(&buf)[U], const int64_t(&pg)[U]) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         if (t0 + u < ntiles) process(tok_begin + kTile * (t0 + u), pg[u], buf[u]);
@@ -375,7 +477,7 @@ struct WaveState {
     // Chunks of U tiles: issue all U tiles' loads, then consume them in order
     // (the compiler waits for tile u with vmcnt = loads issued after it).
     for (int t0 = 0; t0 < ntiles; t0 += U) {
-      TileRegs<kFp8> buf[U];
+      DTile<kFp8, D> buf[U];
       int64_t pg[U];
       fetch(t0, buf, pg);
       consume(t0, buf, pg);
@@ -384,64 +486,73 @@ struct WaveState {
     l_run = pair_sum(l_run);
     // The wave that streamed position ctx - 1 writes b's row: at that position
     // (fused) or, for any other in-range slot, there (an orphan).
-    if (kStore && ftok0 >= 0) {
+    if (kStore && ftok0 >= 0 && vh.first) {
       const int64_t slot = slot_value(P, sw);
       if (slot >= 0 && slot < (P.num_blocks << P.block_size_log2))
-        store_new_chunk<kFp8>(P, slot, h, 16 * g + r, new_chunk);
+        store_new_chunk<kFp8, D>(P, slot, kvh, 16 * g + r, new_chunk);
     }
   }
 
-  // Normalised output row(s) of kv head h for a sequence finished in place.
-  // Lane (r, g) holds O[head 4g+i][dims 8r .. 8r+7].
-  __device__ __forceinline__ void write_final(const DecodeParams& P, int b, int h, int r,
-                                              int g) const {
-    const float vs = (kFp8 && P.v_scale) ? P.v_scale[h] : 1.f;
+  // Normalised output rows of the virtual head for a sequence finished in place.
+  __device__ __forceinline__ void write_final(const DecodeParams& P, int b, const VHead& vh,
+                                              int r, int g) const {
+    const float vs = (kFp8 && P.v_scale) ? P.v_scale[vh.kvh] : 1.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int j = 4 * g + i;
       float l = row_value<kG>(l_run, g, i);
-      if (P.sinks) l = with_sink(l, row_value<kG>(m_run, g, i), sink_log2(P, h * P.gqa + (j < P.gqa ? j : 0)));
-      if (j >= kG || j >= P.gqa) continue;
+      if (P.sinks)
+        l = with_sink(l, row_value<kG>(m_run, g, i),
+                      sink_log2(P, vh.qbase + (j < vh.ncols ? j : 0)));
+      if (j >= kG || j >= vh.ncols) continue;
       const float f = l > 0.f ? vs / l : 0.f;
-      uint32_t w[4];
+      uint32_t w[D / 32];
 #pragma unroll
-      for (int d = 0; d < 4; ++d) {
+      for (int d = 0; d < D / 32; ++d) {
         const bf16x2_t pk = {static_cast<__bf16>(o[2 * d][i] * f),
                              static_cast<__bf16>(o[2 * d + 1][i] * f)};
         w[d] = __builtin_bit_cast(uint32_t, pk);
       }
-      *reinterpret_cast<uint4*>(P.out + b * P.out_row_stride +
-                                static_cast<int64_t>(h * P.gqa + j) * kHead + 8 * r) =
-          make_uint4(w[0], w[1], w[2], w[3]);
+      uint16_t* dst = P.out + b * P.out_row_stride + static_cast<int64_t>(vh.qbase + j) * D +
+                      (D / 16) * r;
+      if constexpr (D == 64) {
+        *reinterpret_cast<uint2*>(dst) = make_uint2(w[0], w[1]);
+      } else {
+#pragma unroll
+        for (int q = 0; q < D / 128; ++q)
+          *reinterpret_cast<uint4*>(dst + 8 * q) =
+              make_uint4(w[4 * q], w[4 * q + 1], w[4 * q + 2], w[4 * q + 3]);
+      }
     }
   }
 
   // Unnormalised partial (O scaled by v_scale, and (max, sum)) into partial
-  // rows row0 + j, j < G.
-  __device__ __forceinline__ void write_partial(const DecodeParams& P, int64_t row0, int h, int r,
-                                                int g) const {
-    const float vs = (kFp8 && P.v_scale) ? P.v_scale[h] : 1.f;
+  // rows row0 + hq for the virtual head's query heads hq.
+  __device__ __forceinline__ void write_partial(const DecodeParams& P, int64_t row0,
+                                                const VHead& vh, int r, int g) const {
+    const float vs = (kFp8 && P.v_scale) ? P.v_scale[vh.kvh] : 1.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int j = 4 * g + i;
-      if (j >= kG || j >= P.gqa) continue;
-      float* dst = P.part_o + (row0 + j) * kHead + 8 * r;
-      *reinterpret_cast<float4*>(dst) =
-          make_float4(o[0][i] * vs, o[1][i] * vs, o[2][i] * vs, o[3][i] * vs);
-      *reinterpret_cast<float4*>(dst + 4) =
-          make_float4(o[4][i] * vs, o[5][i] * vs, o[6][i] * vs, o[7][i] * vs);
+      if (j >= kG || j >= vh.ncols) continue;
+      float* dst = P.part_o + (row0 + vh.qbase + j) * D + (D / 16) * r;
+#pragma unroll
+      for (int q = 0; q < kSl / 4; ++q)
+        *reinterpret_cast<float4*>(dst + 4 * q) =
+            make_float4(o[4 * q][i] * vs, o[4 * q + 1][i] * vs, o[4 * q + 2][i] * vs,
+                        o[4 * q + 3][i] * vs);
     }
-    if (g == 0 && r < P.gqa) {
-      P.part_ml[(row0 + r) * 2 + 0] = m_run;
-      P.part_ml[(row0 + r) * 2 + 1] = l_run;
+    if (g == 0 && r < vh.ncols) {
+      P.part_ml[(row0 + vh.qbase + r) * 2 + 0] = m_run;
+      P.part_ml[(row0 + vh.qbase + r) * 2 + 1] = l_run;
     }
   }
 };
 
-// Fixed partitions: work-group = (partition p, kv-head group, sequence b);
-// wave w owns kv head h = blockIdx.y * NH + w and streams the partition.
-// Partial rows: ((b * Hk + h) * max_parts + p) * G + j.
-template <int NH, int kG, bool kFp8, int U, bool kStore>
+// Fixed partitions: work-group = (partition p, virtual-head group, sequence b);
+// wave w owns virtual head blockIdx.y * NH + w and streams the partition.
+// Partial rows: (b * max_parts + p) * Hq + hq.
+template <int NH, int kG, int D, bool kFp8, int U, bool kStore>
 __global__ __launch_bounds__(NH * 64) void paged_decode_partition_kernel(
     DecodeParams P, const int32_t* __restrict__ block_tables, const int32_t* __restrict__ ctx_lens,
     const void* __restrict__ slot_mapping) {
@@ -451,8 +562,9 @@ __global__ __launch_bounds__(NH * 64) void paged_decode_partition_kernel(
   const int tok_begin = p * P.part_tokens;
   // Wave index made provably uniform so that page lookups are scalar loads.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int h = blockIdx.y * NH + wave;
-  if (h >= P.num_kv_heads) return;  // uniform over the wave; no barriers follow
+  const int v = blockIdx.y * NH + wave;
+  if (v >= P.num_kv_heads * P.col_blocks) return;  // uniform over the wave; no barriers follow
+  const VHead vh = vhead(P, v);
   const int lane = threadIdx.x & 63;
   if (tok_begin < ctx) {  // uniform over the work-group
     // The launch has max_parts partitions; the last one runs on to the context
@@ -466,22 +578,21 @@ __global__ __launch_bounds__(NH * 64) void paged_decode_partition_kernel(
     // window's first key; one wholly before it streams nothing and leaves an
     // empty partial (max -inf, sum 0).
     const int lo = key_lo(P, ctx);
-    WaveState<kG, kFp8, U, kStore> st;
-    st.run(P, block_tables, slot_mapping, b, h, max(tok_begin, lo & ~(kTile - 1)), tok_end, ctx,
+    WaveState<kG, D, kFp8, U, kStore> st;
+    st.run(P, block_tables, slot_mapping, b, vh, max(tok_begin, lo & ~(kTile - 1)), tok_end, ctx,
            lo, r, g);
     if (nparts == 1) {
-      st.write_final(P, b, h, r, g);
+      st.write_final(P, b, vh, r, g);
     } else {
-      const int64_t row0 =
-          ((static_cast<int64_t>(b) * P.num_kv_heads + h) * P.max_parts + p) * P.gqa;
-      st.write_partial(P, row0, h, r, g);
+      const int64_t row0 = (static_cast<int64_t>(b) * P.max_parts + p) * P.num_heads;
+      st.write_partial(P, row0, vh, r, g);
     }
   }
   // No partition streams position ctx - 1 (no context): partition 0 writes b's
   // row.
-  if (kStore && p == 0 && ctx <= 0) {
+  if (kStore && p == 0 && ctx <= 0 && vh.first) {
     const int64_t os = valid_slot(P, slot_mapping, b);
-    if (os >= 0) store_new_row<kFp8>(P, b, h, os, lane);
+    if (os >= 0) store_new_row<kFp8, D>(P, b, vh.kvh, os, lane);
   }
 }
 
@@ -491,12 +602,12 @@ __device__ __forceinline__ int tiles_of(const DecodeParams& P, int ctx) {
   return ctx > 0 ? (ctx + kTile - 1) / kTile - key_lo(P, ctx) / kTile : 0;
 }
 
-// Balanced schedule: work-group w (of num_groups per kv-head group) takes
+// Balanced schedule: work-group w (of num_groups per virtual-head group) takes
 // tiles [w * S, (w+1) * S) of the concatenation of all sequences' tiles,
 // S = ceil(total / num_groups).  Partial rows of a cut sequence:
-// ((w * 2 + slot) * Hk + h) * G + j, slot 0 = the group's first segment,
-// slot 1 = its last (a group holds at most one cut sequence at each end).
-template <int NH, int kG, bool kFp8, int U, bool kStore>
+// (w * 2 + slot) * Hq + hq, slot 0 = the group's first segment, slot 1 = its
+// last (a group holds at most one cut sequence at each end).
+template <int NH, int kG, int D, bool kFp8, int U, bool kStore>
 __global__ __launch_bounds__(NH * 64) void paged_decode_balanced_kernel(
     DecodeParams P, const int32_t* __restrict__ block_tables, const int32_t* __restrict__ ctx_lens,
     const void* __restrict__ slot_mapping) {
@@ -527,8 +638,9 @@ __global__ __launch_bounds__(NH * 64) void paged_decode_balanced_kernel(
     for (int i = threadIdx.x; i <= batch; i += blockDim.x) P.tile_off[i] = toff[i];
     if (threadIdx.x == 0) P.tile_off[batch + 1] = S;
   }
-  const int h = blockIdx.y * NH + wave;
-  if (h >= P.num_kv_heads) return;  // uniform over the wave; no barriers follow
+  const int v = blockIdx.y * NH + wave;
+  if (v >= P.num_kv_heads * P.col_blocks) return;  // uniform over the wave; no barriers follow
+  const VHead vh = vhead(P, v);
   const int t_lo = w * S;
   const int t_hi = min(total, t_lo + S);
   if (t_lo < total) {
@@ -540,37 +652,37 @@ __global__ __launch_bounds__(NH * 64) void paged_decode_balanced_kernel(
       const int mid = (lo + hi) >> 1;
       if (toff[mid] <= t_lo) lo = mid; else hi = mid;
     }
-    WaveState<kG, kFp8, U, kStore> st;
+    WaveState<kG, D, kFp8, U, kStore> st;
     for (int b = lo; b < batch && toff[b] < t_hi; ++b) {
       const int s_lo = max(t_lo, toff[b]) - toff[b];
       const int s_hi = min(t_hi, toff[b + 1]) - toff[b];
       if (s_hi <= s_lo) continue;  // empty sequence
       const int ctx = ctx_lens[b];
-      const int lo = key_lo(P, ctx);
-      const int t_first = lo / kTile;  // the sequence's tile s is its tile t_first + s
-      st.run(P, block_tables, slot_mapping, b, h, kTile * (t_first + s_lo),
-             min(ctx, kTile * (t_first + s_hi)), ctx, lo, r, g);
+      const int klo = key_lo(P, ctx);
+      const int t_first = klo / kTile;  // the sequence's tile s is its tile t_first + s
+      st.run(P, block_tables, slot_mapping, b, vh, kTile * (t_first + s_lo),
+             min(ctx, kTile * (t_first + s_hi)), ctx, klo, r, g);
       if (toff[b] >= t_lo && toff[b + 1] <= t_hi) {
-        st.write_final(P, b, h, r, g);
+        st.write_final(P, b, vh, r, g);
       } else {
         const int slot = toff[b] <= t_lo ? 0 : 1;
-        const int64_t row0 = ((static_cast<int64_t>(w) * 2 + slot) * P.num_kv_heads + h) * P.gqa;
-        st.write_partial(P, row0, h, r, g);
+        const int64_t row0 = (static_cast<int64_t>(w) * 2 + slot) * P.num_heads;
+        st.write_partial(P, row0, vh, r, g);
       }
     }
   }
   // Sequences without tiles (no context) have no wave that streams their
   // last position: group w writes the rows of those with b = w mod G.
-  if (kStore) {
+  if (kStore && vh.first) {
     for (int b = w; b < batch; b += P.num_groups) {
       if (toff[b + 1] != toff[b]) continue;
       const int64_t os = valid_slot(P, slot_mapping, b);
-      if (os >= 0) store_new_row<kFp8>(P, b, h, os, lane);
+      if (os >= 0) store_new_row<kFp8, D>(P, b, vh.kvh, os, lane);
     }
   }
 }
 
-// Merge of one (query head hq, sequence b) by one wave; each lane owns two
+// Merge of one (query head hq, sequence b) by one wave; each lane owns D / 64
 // dims.  Partial rows: k = 0 is `alt_first_row`, k >= 1 is first_row + k *
 // row_stride.  The pieces are taken kMergeBatch at a time (one batch for up to
 // 64 pieces): lane k loads piece k's (max, sum) while the wave issues the O
@@ -580,12 +692,48 @@ __global__ __launch_bounds__(NH * 64) void paged_decode_balanced_kernel(
 constexpr int kMergeBatch = 64;  // pieces per batch: one (max, sum) per lane
 constexpr int kMergeUnroll = 8;  // O rows in flight per wave
 constexpr int kMergeWaves = 4;   // independent merge rows per work-group
+
+template <int D>
+struct MergeVec {
+  static constexpr int N = D / 64;  // dims per lane
+  float x[N];
+  __device__ __forceinline__ static MergeVec load(const float* p) {
+    MergeVec v;
+    if constexpr (N == 1) {
+      v.x[0] = *p;
+    } else if constexpr (N == 2) {
+      const float2 t = *reinterpret_cast<const float2*>(p);
+      v.x[0] = t.x;
+      v.x[1] = t.y;
+    } else {
+      const float4 t = *reinterpret_cast<const float4*>(p);
+      v.x[0] = t.x;
+      v.x[1] = t.y;
+      v.x[2] = t.z;
+      v.x[3] = t.w;
+    }
+    return v;
+  }
+  __device__ __forceinline__ static MergeVec zero() {
+    MergeVec v;
+#pragma unroll
+    for (int e = 0; e < N; ++e) v.x[e] = 0.f;
+    return v;
+  }
+};
+
+template <int D>
 __device__ __forceinline__ void merge_rows(uint16_t* orow, const float* part_o,
                                            const float* part_ml, int64_t first_row,
                                            int64_t row_stride, int nrows, int64_t alt_first_row,
                                            float sink2, int lane) {
+  using V = MergeVec<D>;
+  constexpr int N = V::N;
   auto row_of = [&](int k) -> int64_t { return k == 0 ? alt_first_row : first_row + k * row_stride; };
-  float M = kNegInf, L = 0.f, o0 = 0.f, o1 = 0.f;
+  float M = kNegInf, L = 0.f;
+  float acc[N];
+#pragma unroll
+  for (int e = 0; e < N; ++e) acc[e] = 0.f;
   for (int k0 = 0; k0 < nrows; k0 += kMergeBatch) {
     const int n = min(kMergeBatch, nrows - k0);
     // (max, sum) of piece k0 + lane; lanes past the batch hold an empty piece.
@@ -596,34 +744,31 @@ __device__ __forceinline__ void merge_rows(uint16_t* orow, const float* part_o,
       l = ml.y;
     }
     // O of the batch's pieces, kMergeUnroll rows in flight at a time.
-    float2 ov[kMergeUnroll];
+    V ov[kMergeUnroll];
 #pragma unroll
     for (int u = 0; u < kMergeUnroll; ++u)
-      ov[u] = u < n ? reinterpret_cast<const float2*>(part_o + row_of(k0 + u) * kHead)[lane]
-                    : make_float2(0.f, 0.f);
+      ov[u] = u < n ? V::load(part_o + row_of(k0 + u) * D + N * lane) : V::zero();
     const float mb = wave_max(m);
     const float mn = fmaxf(M, mb);
     if (mn == kNegInf) continue;  // no valid piece yet (all rows empty)
     const float a = __builtin_amdgcn_exp2f(M - mn);  // 0 when M = -inf
     const float f = __builtin_amdgcn_exp2f(m - mn);  // lane k's weight; 0 for empty pieces
     L = L * a + wave_sum(l * f);
-    o0 *= a;
-    o1 *= a;
+#pragma unroll
+    for (int e = 0; e < N; ++e) acc[e] *= a;
     for (int u0 = 0; u0 < n; u0 += kMergeUnroll) {
       if (u0 > 0) {
 #pragma unroll
         for (int u = 0; u < kMergeUnroll; ++u)
-          ov[u] = u0 + u < n
-                      ? reinterpret_cast<const float2*>(part_o + row_of(k0 + u0 + u) * kHead)[lane]
-                      : make_float2(0.f, 0.f);
+          ov[u] = u0 + u < n ? V::load(part_o + row_of(k0 + u0 + u) * D + N * lane) : V::zero();
       }
 #pragma unroll
       for (int u = 0; u < kMergeUnroll; ++u) {
-        const float w = __builtin_bit_cast(
+        const float wgt = __builtin_bit_cast(
             float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, f), min(u0 + u, 63)));
         if (u0 + u < n) {
-          o0 = __builtin_fmaf(ov[u].x, w, o0);
-          o1 = __builtin_fmaf(ov[u].y, w, o1);
+#pragma unroll
+          for (int e = 0; e < N; ++e) acc[e] = __builtin_fmaf(ov[u].x[e], wgt, acc[e]);
         }
       }
     }
@@ -631,70 +776,93 @@ __device__ __forceinline__ void merge_rows(uint16_t* orow, const float* part_o,
   }
   L = with_sink(L, M, sink2);  // the sink joins the merged row once
   const float inv = L > 0.f ? 1.f / L : 0.f;
-  const bf16x2_t pk = {static_cast<__bf16>(o0 * inv), static_cast<__bf16>(o1 * inv)};
-  reinterpret_cast<uint32_t*>(orow)[lane] = __builtin_bit_cast(uint32_t, pk);
+  if constexpr (N == 1) {
+    orow[lane] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(acc[0] * inv));
+  } else {
+    uint32_t w[N / 2];
+#pragma unroll
+    for (int e = 0; e < N / 2; ++e) {
+      const bf16x2_t pk = {static_cast<__bf16>(acc[2 * e] * inv),
+                           static_cast<__bf16>(acc[2 * e + 1] * inv)};
+      w[e] = __builtin_bit_cast(uint32_t, pk);
+    }
+    if constexpr (N == 2)
+      reinterpret_cast<uint32_t*>(orow)[lane] = w[0];
+    else
+      reinterpret_cast<uint2*>(orow)[lane] = make_uint2(w[0], w[1]);
+  }
+}
+
+// Zero row of D bf16 for an empty sequence (one wave; each lane D / 64 dims).
+template <int D>
+__device__ __forceinline__ void zero_row(uint16_t* orow, int lane) {
+#pragma unroll
+  for (int e = 0; e < D / 64; ++e) orow[(D / 64) * lane + e] = 0;
 }
 
 // Fixed partitions: merge sequences with more than one partition; zero empty ones.
 // Work-group = kMergeWaves independent waves, wave v = query head
 // blockIdx.x * kMergeWaves + v of sequence blockIdx.y.
+template <int D>
 __global__ __launch_bounds__(kMergeWaves * 64) void paged_decode_partition_reduce_kernel(
-    DecodeParams P, int num_heads) {
+    DecodeParams P) {
   const int hq = blockIdx.x * kMergeWaves + (threadIdx.x >> 6);
   const int b = blockIdx.y;
   const int lane = threadIdx.x & 63;
-  if (hq >= num_heads) return;  // no barriers in this kernel
+  if (hq >= P.num_heads) return;  // no barriers in this kernel
   const int ctx = P.ctx_lens[b];
-  uint16_t* orow = P.out + b * P.out_row_stride + static_cast<int64_t>(hq) * kHead;
+  uint16_t* orow = P.out + b * P.out_row_stride + static_cast<int64_t>(hq) * D;
   if (ctx <= 0) {
-    reinterpret_cast<uint32_t*>(orow)[lane] = 0u;
+    zero_row<D>(orow, lane);
     return;
   }
   const int nparts = min((ctx + P.part_tokens - 1) / P.part_tokens, P.max_parts);
   if (nparts <= 1) return;  // written by the partition kernel
-  const int h = hq / P.gqa;
-  const int j = hq - h * P.gqa;
-  const int64_t first = (static_cast<int64_t>(b) * P.num_kv_heads + h) * P.max_parts * P.gqa + j;
-  merge_rows(orow, P.part_o, P.part_ml, first, P.gqa, nparts, first, sink_log2(P, hq), lane);
+  const int64_t first = static_cast<int64_t>(b) * P.max_parts * P.num_heads + hq;
+  merge_rows<D>(orow, P.part_o, P.part_ml, first, P.num_heads, nparts, first, sink_log2(P, hq),
+                lane);
 }
 
 // Balanced schedule: merge sequences cut across work-groups; zero empty ones.
 // Work-group = kMergeWaves independent waves, as the partition reduce.
+template <int D>
 __global__ __launch_bounds__(kMergeWaves * 64) void paged_decode_balanced_reduce_kernel(
-    DecodeParams P, int num_heads) {
+    DecodeParams P) {
   const int hq = blockIdx.x * kMergeWaves + (threadIdx.x >> 6);
   const int b = blockIdx.y;
   const int lane = threadIdx.x & 63;
-  if (hq >= num_heads) return;  // no barriers in this kernel
-  uint16_t* orow = P.out + b * P.out_row_stride + static_cast<int64_t>(hq) * kHead;
+  if (hq >= P.num_heads) return;  // no barriers in this kernel
+  uint16_t* orow = P.out + b * P.out_row_stride + static_cast<int64_t>(hq) * D;
   const int t0 = P.tile_off[b];
   const int t1 = P.tile_off[b + 1];
   const int S = P.tile_off[P.batch + 1];
   if (t1 <= t0) {
-    reinterpret_cast<uint32_t*>(orow)[lane] = 0u;
+    zero_row<D>(orow, lane);
     return;
   }
   const int w0 = t0 / S;
   const int w1 = (t1 - 1) / S;
   if (w0 == w1) return;  // finished in place by work-group w0
-  const int h = hq / P.gqa;
-  const int j = hq - h * P.gqa;
-  const int64_t hk = P.num_kv_heads;
+  const int64_t hqn = P.num_heads;
   // Group w0 holds the sequence in slot 1 unless the sequence starts its range;
   // groups w0+1 .. w1 hold it in slot 0.
   const int slot0 = t0 > w0 * S ? 1 : 0;
-  const int64_t first_alt = ((static_cast<int64_t>(w0) * 2 + slot0) * hk + h) * P.gqa + j;
-  const int64_t first = ((static_cast<int64_t>(w0) * 2 + 0) * hk + h) * P.gqa + j;
-  merge_rows(orow, P.part_o, P.part_ml, first, 2 * hk * P.gqa, w1 - w0 + 1, first_alt,
-             sink_log2(P, hq), lane);
+  const int64_t first_alt = (static_cast<int64_t>(w0) * 2 + slot0) * hqn + hq;
+  const int64_t first = (static_cast<int64_t>(w0) * 2 + 0) * hqn + hq;
+  merge_rows<D>(orow, P.part_o, P.part_ml, first, 2 * hqn, w1 - w0 + 1, first_alt,
+                sink_log2(P, hq), lane);
 }
 
-// Tuning knob (compile-time): tiles per load set.
+// Tuning knob (compile-time): tiles per load set at head sizes up to 128 (at
+// 256 a tile's loads fill as many registers as two tiles do at 128, so one).
 #ifndef FK_DECODE_CHUNK
 #define FK_DECODE_CHUNK 2
 #endif
-constexpr int kChunk = FK_DECODE_CHUNK;  // tiles loaded per wave per set
-constexpr int kMaxWavesPerGroup = 8;     // kv heads (waves) per work-group
+template <int D>
+constexpr int chunk_tiles() {
+  return D >= 256 ? 1 : FK_DECODE_CHUNK;
+}
+constexpr int kMaxWavesPerGroup = 8;     // virtual heads (waves) per work-group
 constexpr int kPartQuant = 64;           // fixed-partition granularity in tokens
 constexpr int kMaxBalancedBatch = 8192;  // tile prefix sums live in LDS
 
@@ -713,23 +881,38 @@ int num_cus() {
   return cached;
 }
 
-int waves_per_group(int num_kv_heads) {
-  return num_kv_heads < kMaxWavesPerGroup ? num_kv_heads : kMaxWavesPerGroup;
+// Waves per kv head (column blocks of up to 16 query heads) and virtual heads.
+int col_blocks(int num_heads, int num_kv_heads) {
+  return (num_heads / num_kv_heads + 15) / 16;
+}
+int virtual_heads(int num_heads, int num_kv_heads) {
+  return num_kv_heads * col_blocks(num_heads, num_kv_heads);
+}
+int waves_per_group(int vheads) {
+  return vheads < kMaxWavesPerGroup ? vheads : kMaxWavesPerGroup;
 }
 
-// Workspace layout: part_o rows, part_ml rows (256-byte aligned), then (balanced
-// only) batch + 2 int32 for the tile prefix sums and the range size.
-int64_t o_region(int64_t rows) { return (rows * kHead * 4 + 255) / 256 * 256; }
+// Workspace layout: part_o rows of head_size floats, part_ml rows (256-byte
+// aligned), then (balanced only) batch + 2 int32 for the tile prefix sums and
+// the range size.
+int64_t o_region(int64_t rows, int head_size) {
+  return (rows * head_size * 4 + 255) / 256 * 256;
+}
 int64_t ml_region(int64_t rows) { return (rows * 2 * 4 + 255) / 256 * 256; }
 
 int64_t partial_rows(bool balanced, int64_t batch, int num_heads, int64_t max_parts) {
-  // balanced: max_parts = work-groups per kv-head group, 2 slots each.
+  // balanced: max_parts = work-groups per virtual-head group, 2 slots each.
   return balanced ? max_parts * 2 * num_heads : batch * num_heads * max_parts;
 }
 
-int64_t workspace_bytes(bool balanced, int64_t batch, int num_heads, int64_t max_parts) {
+int64_t workspace_bytes(bool balanced, int64_t batch, int num_heads, int head_size,
+                        int64_t max_parts) {
   const int64_t rows = partial_rows(balanced, batch, num_heads, max_parts);
-  return o_region(rows) + ml_region(rows) + (balanced ? (batch + 2) * 4 : 0);
+  return o_region(rows, head_size) + ml_region(rows) + (balanced ? (batch + 2) * 4 : 0);
+}
+
+bool supported_head(int head_size) {
+  return head_size == 64 || head_size == 128 || head_size == 256;
 }
 
 int validate(const char* name, int64_t batch, int num_heads, int num_kv_heads, int head_size,
@@ -739,12 +922,13 @@ int validate(const char* name, int64_t batch, int num_heads, int num_kv_heads, i
   FK_REQUIRE(num_heads > 0 && num_kv_heads > 0 && num_heads % num_kv_heads == 0,
              "%s: num_heads %d must be a positive multiple of num_kv_heads %d", name, num_heads,
              num_kv_heads);
-  if (head_size != kHead)
-    return set_error(FK_ERR_UNSUPPORTED, "%s: head_size %d unsupported (128 only)", name,
+  if (!supported_head(head_size))
+    return set_error(FK_ERR_UNSUPPORTED, "%s: head_size %d unsupported (64, 128 or 256)", name,
                      head_size);
-  if (num_heads / num_kv_heads > 16)
-    return set_error(FK_ERR_UNSUPPORTED, "%s: GQA group %d > 16 unsupported", name,
-                     num_heads / num_kv_heads);
+  const int vh = virtual_heads(num_heads, num_kv_heads);
+  FK_REQUIRE((vh + kMaxWavesPerGroup - 1) / kMaxWavesPerGroup <= 65535,
+             "%s: %d kv heads x %d column blocks exceed the grid", name, num_kv_heads,
+             col_blocks(num_heads, num_kv_heads));
   if (part_tokens == 0) {
     FK_REQUIRE(batch <= kMaxBalancedBatch, "%s: balanced schedule supports batch <= %d", name,
                kMaxBalancedBatch);
@@ -764,6 +948,7 @@ struct Launch {
   bool balanced;
   bool fp8;
   int nh;
+  int head_size;
   dim3 grid;
 };
 
@@ -794,7 +979,7 @@ int prepare(const char* name, Launch& L, void* out, int64_t out_row_stride, cons
              "%s: q/out/cache must be 16-byte aligned with rows a multiple of 8 elements", name);
   const bool balanced = part_tokens == 0;
   const bool needs_ws = balanced || max_parts > 1;
-  const int64_t need = workspace_bytes(balanced, batch, num_heads, max_parts);
+  const int64_t need = workspace_bytes(balanced, batch, num_heads, head_size, max_parts);
   if (needs_ws && (workspace == nullptr || ws_bytes < need))
     return set_error(FK_ERR_WORKSPACE, "%s: workspace of %lld bytes < %lld required", name,
                      (long long)ws_bytes, (long long)need);
@@ -812,8 +997,10 @@ int prepare(const char* name, Launch& L, void* out, int64_t out_row_stride, cons
   P.block_tables = block_tables;
   P.bt_row_stride = bt_row_stride;
   P.ctx_lens = ctx_lens;
+  P.num_heads = num_heads;
   P.num_kv_heads = num_kv_heads;
   P.gqa = num_heads / num_kv_heads;
+  P.col_blocks = col_blocks(num_heads, num_kv_heads);
   P.block_size_log2 = __builtin_ctz(static_cast<unsigned>(block_size));
   P.part_tokens = static_cast<int>(part_tokens);
   P.max_parts = static_cast<int>(max_parts);
@@ -830,56 +1017,90 @@ int prepare(const char* name, Launch& L, void* out, int64_t out_row_stride, cons
   const int64_t rows = partial_rows(balanced, batch, num_heads, max_parts);
   char* ws = static_cast<char*>(workspace);
   P.part_o = needs_ws ? reinterpret_cast<float*>(ws) : nullptr;
-  P.part_ml = needs_ws ? reinterpret_cast<float*>(ws + o_region(rows)) : nullptr;
-  P.tile_off = balanced ? reinterpret_cast<int32_t*>(ws + o_region(rows) + ml_region(rows))
+  P.part_ml = needs_ws ? reinterpret_cast<float*>(ws + o_region(rows, head_size)) : nullptr;
+  P.tile_off = balanced ? reinterpret_cast<int32_t*>(ws + o_region(rows, head_size) +
+                                                     ml_region(rows))
                         : nullptr;
   L.balanced = balanced;
   L.fp8 = kv_dtype == FK_DTYPE_FP8_E4M3FN;
-  L.nh = waves_per_group(num_kv_heads);
-  const unsigned hgroups = static_cast<unsigned>((num_kv_heads + L.nh - 1) / L.nh);
+  L.head_size = head_size;
+  const int vh = virtual_heads(num_heads, num_kv_heads);
+  L.nh = waves_per_group(vh);
+  const unsigned hgroups = static_cast<unsigned>((vh + L.nh - 1) / L.nh);
   L.grid = balanced ? dim3(static_cast<unsigned>(max_parts), hgroups, 1)
                     : dim3(static_cast<unsigned>(max_parts), hgroups, static_cast<unsigned>(batch));
   return FK_OK;
 }
 
-template <int NH, int G, bool FP8, bool ST>
+template <int NH, int G, int D, bool FP8, bool ST>
 void launch_main_st(const Launch& L, hipStream_t stream) {
+  constexpr int U = chunk_tiles<D>();
   if (L.balanced) {
     const size_t lds = static_cast<size_t>(L.P.batch + 1) * sizeof(int32_t);
-    hipLaunchKernelGGL((paged_decode_balanced_kernel<NH, G, FP8, kChunk, ST>), L.grid,
+    hipLaunchKernelGGL((paged_decode_balanced_kernel<NH, G, D, FP8, U, ST>), L.grid,
                        dim3(NH * 64), lds, stream, L.P, L.P.block_tables, L.P.ctx_lens,
                        L.slot_mapping);
   } else {
-    hipLaunchKernelGGL((paged_decode_partition_kernel<NH, G, FP8, kChunk, ST>), L.grid,
+    hipLaunchKernelGGL((paged_decode_partition_kernel<NH, G, D, FP8, U, ST>), L.grid,
                        dim3(NH * 64), 0, stream, L.P, L.P.block_tables, L.P.ctx_lens,
                        L.slot_mapping);
   }
 }
 
-template <int NH, int G, bool FP8>
+template <int NH, int G, int D, bool FP8>
 void launch_main(const Launch& L, hipStream_t stream) {
   if (L.P.new_k != nullptr)
-    launch_main_st<NH, G, FP8, true>(L, stream);
+    launch_main_st<NH, G, D, FP8, true>(L, stream);
   else
-    launch_main_st<NH, G, FP8, false>(L, stream);
+    launch_main_st<NH, G, D, FP8, false>(L, stream);
 }
 
-template <int G, bool FP8>
+template <int G, int D, bool FP8>
 void launch_main_nh(const Launch& L, hipStream_t stream) {
   switch (L.nh) {
-    case 1: launch_main<1, G, FP8>(L, stream); break;
-    case 2: launch_main<2, G, FP8>(L, stream); break;
-    case 4: launch_main<4, G, FP8>(L, stream); break;
-    default: launch_main<8, G, FP8>(L, stream); break;
+    case 1: launch_main<1, G, D, FP8>(L, stream); break;
+    case 2: launch_main<2, G, D, FP8>(L, stream); break;
+    case 4: launch_main<4, G, D, FP8>(L, stream); break;
+    default: launch_main<8, G, D, FP8>(L, stream); break;
   }
 }
 
-template <int G>
-void launch_main_g(const Launch& L, hipStream_t stream) {
+template <int G, int D>
+void launch_main_gd(const Launch& L, hipStream_t stream) {
   if (L.fp8)
-    launch_main_nh<G, true>(L, stream);
+    launch_main_nh<G, D, true>(L, stream);
   else
-    launch_main_nh<G, false>(L, stream);
+    launch_main_nh<G, D, false>(L, stream);
+}
+
+template <int D>
+void launch_main_d(const Launch& L, hipStream_t stream) {
+  // Query columns per wave: the group size, rounded up to 4, 8 or 16 (groups
+  // above 16 take several 16-column waves per kv head).
+  if (L.P.gqa <= 4)
+    launch_main_gd<4, D>(L, stream);
+  else if (L.P.gqa <= 8)
+    launch_main_gd<8, D>(L, stream);
+  else
+    launch_main_gd<16, D>(L, stream);
+}
+
+void launch_main_any(const Launch& L, hipStream_t stream) {
+  switch (L.head_size) {
+    case 64: launch_main_d<64>(L, stream); break;
+    case 256: launch_main_d<256>(L, stream); break;
+    default: launch_main_d<128>(L, stream); break;
+  }
+}
+
+template <int D>
+void launch_reduce_d(const Launch& L, dim3 grid, hipStream_t stream) {
+  if (L.balanced)
+    hipLaunchKernelGGL(paged_decode_balanced_reduce_kernel<D>, grid, dim3(kMergeWaves * 64), 0,
+                       stream, L.P);
+  else
+    hipLaunchKernelGGL(paged_decode_partition_reduce_kernel<D>, grid, dim3(kMergeWaves * 64), 0,
+                       stream, L.P);
 }
 
 }  // namespace
@@ -893,13 +1114,18 @@ extern "C" int fk_paged_decode_plan(int64_t batch, int num_heads, int num_kv_hea
   FK_REQUIRE(part_tokens && max_parts && workspace_bytes_out,
              "fk_paged_decode_plan: null output pointer");
   FK_REQUIRE(batch >= 0 && num_heads > 0 && num_kv_heads > 0 && max_seq_len >= 0 &&
-                 num_splits >= 0,
-             "fk_paged_decode_plan: negative argument");
+                 num_splits >= 0 && num_heads % num_kv_heads == 0,
+             "fk_paged_decode_plan: invalid argument");
+  if (!supported_head(head_size))
+    return set_error(FK_ERR_UNSUPPORTED,
+                     "fk_paged_decode_plan: head_size %d unsupported (64, 128 or 256)",
+                     head_size);
   const int64_t L = max_seq_len > 0 ? max_seq_len : 1;
+  const int vh = virtual_heads(num_heads, num_kv_heads);
   if (num_splits == 0 && batch <= kMaxBalancedBatch) {
-    // Balanced: one work-group per CU for each kv-head group when a group
-    // fills a CU (8 waves), proportionally more for fewer kv heads.
-    const int nh = waves_per_group(num_kv_heads);
+    // Balanced: one work-group per CU for each virtual-head group when a group
+    // fills a CU (8 waves), proportionally more for fewer virtual heads.
+    const int nh = waves_per_group(vh);
     *part_tokens = 0;
     *max_parts = static_cast<int64_t>(num_cus()) * (kMaxWavesPerGroup / nh);
   } else {
@@ -907,8 +1133,8 @@ extern "C" int fk_paged_decode_plan(int64_t batch, int num_heads, int num_kv_hea
     if (num_splits > 0) {
       part = (L + num_splits - 1) / num_splits;
     } else {
-      // ~8192 waves (one per (sequence, kv head, partition)), >= 256 tokens each.
-      const int64_t units = (batch > 0 ? batch : 1) * num_kv_heads;
+      // ~8192 waves (one per (sequence, virtual head, partition)), >= 256 tokens each.
+      const int64_t units = (batch > 0 ? batch : 1) * vh;
       part = (L * units + 8191) / 8192;
       if (part < 256) part = 256;
     }
@@ -916,9 +1142,8 @@ extern "C" int fk_paged_decode_plan(int64_t batch, int num_heads, int num_kv_hea
     *part_tokens = part;
     *max_parts = (L + part - 1) / part;
   }
-  (void)head_size;
   *workspace_bytes_out =
-      batch > 0 ? workspace_bytes(*part_tokens == 0, batch, num_heads, *max_parts) : 0;
+      batch > 0 ? workspace_bytes(*part_tokens == 0, batch, num_heads, head_size, *max_parts) : 0;
   return FK_OK;
 }
 
@@ -935,13 +1160,7 @@ extern "C" int fk_paged_decode_partials(
                    batch, num_heads, num_kv_heads, head_size, block_size, num_blocks, scale,
                    window_left, sinks, part_tokens, max_parts, workspace, ws_bytes);
   if (rc != FK_OK || batch == 0) return rc;
-  hipStream_t s = as_stream(stream);
-  if (L.P.gqa <= 4)
-    launch_main_g<4>(L, s);
-  else if (L.P.gqa <= 8)
-    launch_main_g<8>(L, s);
-  else
-    launch_main_g<16>(L, s);
+  launch_main_any(L, as_stream(stream));
   return check_launch("fk_paged_decode_partials");
 }
 
@@ -960,12 +1179,12 @@ extern "C" int fk_paged_decode_reduce(
   if (rc != FK_OK || batch == 0) return rc;
   const dim3 grid(static_cast<unsigned>((num_heads + kMergeWaves - 1) / kMergeWaves),
                   static_cast<unsigned>(batch));
-  if (L.balanced)
-    hipLaunchKernelGGL(paged_decode_balanced_reduce_kernel, grid, dim3(kMergeWaves * 64), 0,
-                       as_stream(stream), L.P, num_heads);
-  else
-    hipLaunchKernelGGL(paged_decode_partition_reduce_kernel, grid, dim3(kMergeWaves * 64), 0,
-                       as_stream(stream), L.P, num_heads);
+  hipStream_t s = as_stream(stream);
+  switch (head_size) {
+    case 64: launch_reduce_d<64>(L, grid, s); break;
+    case 256: launch_reduce_d<256>(L, grid, s); break;
+    default: launch_reduce_d<128>(L, grid, s); break;
+  }
   return check_launch("fk_paged_decode_reduce");
 }
 
@@ -1007,7 +1226,7 @@ extern "C" int fk_store_paged_decode(
                    part_tokens, max_parts, workspace, ws_bytes);
   if (rc != FK_OK) return rc;
   const int64_t elem = kv_dtype == FK_DTYPE_FP8_E4M3FN ? 1 : 2;
-  const int64_t row = static_cast<int64_t>(num_kv_heads) * kHead;
+  const int64_t row = static_cast<int64_t>(num_kv_heads) * head_size;
   FK_REQUIRE(key_row_stride >= row && value_row_stride >= row,
              "%s: key/value row stride shorter than num_kv_heads * head_size", name);
   if (batch == 0) return FK_OK;
@@ -1022,13 +1241,7 @@ extern "C" int fk_store_paged_decode(
   L.P.new_v_stride = value_row_stride * elem;
   L.P.slot_is_i64 = slot_is_i64 ? 1 : 0;
   L.slot_mapping = slot_mapping;
-  hipStream_t s = as_stream(stream);
-  if (L.P.gqa <= 4)
-    launch_main_g<4>(L, s);
-  else if (L.P.gqa <= 8)
-    launch_main_g<8>(L, s);
-  else
-    launch_main_g<16>(L, s);
+  launch_main_any(L, as_stream(stream));
   rc = check_launch(name);
   if (rc != FK_OK) return rc;
   return fk_paged_decode_reduce(out, out_row_stride, q, q_row_stride, k_cache, v_cache, kv_dtype,

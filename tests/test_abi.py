@@ -79,6 +79,16 @@ def test_plan_host_logic(lib):
     assert part == 64 and nparts == 2
     part, nparts, _ = _native.plan(10000, 32, 8, 128, 4096, 0)  # too many for LDS prefix sums
     assert part > 0
+    # head sizes 64 / 256: partial rows of head_size floats
+    _, n64, ws64 = _native.plan(64, 32, 8, 64, 8192, 0)
+    _, n256, ws256 = _native.plan(64, 32, 8, 256, 8192, 0)
+    assert n64 == n256 and ws256 - ws64 >= n64 * 2 * 32 * (256 - 64) * 4
+    # groups above 16: one wave per 16 query columns, so fewer work-groups fill a CU
+    _, n_g32, _ = _native.plan(64, 64, 2, 128, 8192, 0)  # 2 kv heads x 2 column blocks
+    _, n_g8, _ = _native.plan(64, 16, 2, 128, 8192, 0)   # 2 kv heads x 1 column block
+    assert n_g8 == 2 * n_g32
+    with pytest.raises(_native.FkError, match="head_size"):
+        _native.plan(64, 32, 8, 96, 8192, 0)
     with pytest.raises(_native.FkError):
         _native.plan(-1, 32, 8, 128, 10, 0)
 
@@ -111,8 +121,8 @@ def test_argument_errors_return_before_launch(lib):
                                    a["bs"], a["nb"], 0.088, a["window"], None, a["part"],
                                    a["nparts"], a["ws"], a["wsb"], stream)
 
-    assert decode(head=64) == N.FK_ERR_UNSUPPORTED and "head_size" in _last_error(lib)
-    assert decode(hq=256, hk=8) == N.FK_ERR_UNSUPPORTED and "GQA" in _last_error(lib)
+    assert decode(head=96) == N.FK_ERR_UNSUPPORTED and "head_size" in _last_error(lib)
+    assert decode(head=512) == N.FK_ERR_UNSUPPORTED and "head_size" in _last_error(lib)
     assert decode(hq=30, hk=8) == N.FK_ERR_INVALID_ARG
     assert decode(bs=24) == N.FK_ERR_INVALID_ARG and "block_size" in _last_error(lib)
     assert decode(part=100) == N.FK_ERR_INVALID_ARG and "part_tokens" in _last_error(lib)
