@@ -133,78 +133,6 @@ __device__ __forceinline__ float sink_log2(const DecodeParams& P, int hq) {
   return P.sinks ? P.sinks[hq] * kLog2e : kNegInf;
 }
 
-// Loads of N 32-bit words from p (16-, 8- or 4-byte vectors; p is aligned to
-// the vector).
-template <int N>
-__device__ __forceinline__ void ld_words(const uint8_t* p, uint32_t (&w)[N]) {
-  if constexpr (N == 1) {
-    w[0] = *reinterpret_cast<const uint32_t*>(p);
-  } else if constexpr (N == 2) {
-    const uint2 x = *reinterpret_cast<const uint2*>(p);
-    w[0] = x.x;
-    w[1] = x.y;
-  } else {
-#pragma unroll
-    for (int q = 0; q < N / 4; ++q) {
-      const uint4 x = *reinterpret_cast<const uint4*>(p + 16 * q);
-      w[4 * q] = x.x;
-      w[4 * q + 1] = x.y;
-      w[4 * q + 2] = x.z;
-      w[4 * q + 3] = x.w;
-    }
-  }
-}
-
-// Raw registers one wave loads for one 16-token tile of head size D.  Lane
-// (r, g): K row r -- bf16: the D/32 16-byte chunks of dims 32c + 8g .. +7;
-// fp8: the D/4 bytes of dims (D/4) g .. (D/4) g + D/4 - 1 -- and V rows 4g+i,
-// dims (D/16) r .. (D/16) r + D/16 - 1, as kVWords words.  load_tile only
-// issues the loads; conversion and masking happen in the consumer, after the
-// loads of the following tile have been issued.
-template <bool kFp8, int D>
-struct DTile {
-  static constexpr int kKLoads = kFp8 ? D / 64 : D / 32;  // 16-byte K loads
-  static constexpr int kVWords = kFp8 ? D / 64 : D / 32;  // 32-bit words per V row
-  uint4 k[kKLoads];
-  uint32_t v[4][kVWords];
-};
-
-// K operand chunks (bf16, dims as described at DTile) of a loaded tile.
-template <bool kFp8, int D>
-__device__ __forceinline__ void k_chunks_d(const DTile<kFp8, D>& t, uint4 (&kc)[D / 32]) {
-  if constexpr (!kFp8) {
-#pragma unroll
-    for (int c = 0; c < D / 32; ++c) kc[c] = t.k[c];
-  } else {
-    // chunk c = bytes 8c .. 8c+7 of the lane's D/4.
-#pragma unroll
-    for (int c = 0; c < D / 32; ++c) {
-      const uint4& src = t.k[c >> 1];
-      const uint32_t w0 = (c & 1) ? src.z : src.x;
-      const uint32_t w1 = (c & 1) ? src.w : src.y;
-      const uint2 lo = fp8x4_to_bf16x4(w0), hi = fp8x4_to_bf16x4(w1);
-      kc[c] = make_uint4(lo.x, lo.y, hi.x, hi.y);
-    }
-  }
-}
-
-// V row i of a loaded tile as D/32 words of bf16 pairs (zero when !keep).
-template <bool kFp8, int D>
-__device__ __forceinline__ void v_words(const DTile<kFp8, D>& t, int i, bool keep,
-                                        uint32_t (&w)[D / 32]) {
-  if constexpr (!kFp8) {
-#pragma unroll
-    for (int q = 0; q < D / 32; ++q) w[q] = keep ? t.v[i][q] : 0u;
-  } else {
-#pragma unroll
-    for (int q = 0; q < D / 64; ++q) {
-      const uint2 x = fp8x4_to_bf16x4(t.v[i][q]);
-      w[2 * q] = keep ? x.x : 0u;
-      w[2 * q + 1] = keep ? x.y : 0u;
-    }
-  }
-}
-
 // Issues the loads of one tile from page `page` (>= 0, < num_blocks).  Loads
 // are unconditional so that every pipeline stage has the same number of loads
 // in flight and the compiler can wait for one stage with vmcnt(N) instead of

@@ -39,17 +39,19 @@ namespace {
 #ifndef FK_PREFILL_COLS
 #define FK_PREFILL_COLS 2
 #endif
-// Two waves per SIMD (two 4-wave work-groups per CU; each holds 32 KB of LDS for
-// bf16 pages).
-#ifndef FK_PREFILL_WAVES
-#define FK_PREFILL_WAVES __attribute__((amdgpu_waves_per_eu(2)))
-#endif
+// Two waves per SIMD at head sizes up to 128 (two 4-wave work-groups per CU;
+// each holds 32 KB of LDS for bf16 pages at 128); at 256 one column block per
+// wave still needs more than the 256 registers two waves leave, so one.
+constexpr int prefill_waves_per_simd(int D) { return D >= 256 ? 1 : 2; }
 #ifndef FK_PREFILL_LAZY
 #define FK_PREFILL_LAZY 8.0f
 #endif
 constexpr int kColBlocks = FK_PREFILL_COLS;    // 16-query column blocks per wave
 constexpr float kLazy = FK_PREFILL_LAZY;       // max-update threshold (log2 units)
-constexpr int kQTokens = 16 * kColBlocks;      // query tokens per wave
+constexpr int kQTokens = 16 * kColBlocks;      // query tokens per wave at head size 128
+// Column blocks per wave at head size D: at 256 the O accumulators of one block
+// (16 tiles of 4 fp32 per lane) already take what two take at 128.
+constexpr int col_blocks_for(int D) { return D >= 256 ? 1 : kColBlocks; }
 constexpr int kPrefillWaves = 4;               // waves per work-group
 #ifndef FK_PREFILL_STAGE
 #define FK_PREFILL_STAGE 32
@@ -126,9 +128,9 @@ __device__ __forceinline__ int64_t key_row(const PrefillParams& P,
 // the 16-byte chunks of row R stored at chunk index q ^ (R mod kChunks) so
 // that the row-parallel writes and the MFMA-layout reads (16 rows at one chunk
 // index, or one row's 16 chunks) hit distinct banks.
-template <bool kFp8>
+template <bool kFp8, int D>
 struct Stage {
-  static constexpr int kRowBytes = kFp8 ? kHead : 2 * kHead;
+  static constexpr int kRowBytes = kFp8 ? D : 2 * D;
   static constexpr int kChunks = kRowBytes / 16;
   static constexpr int kBytes = 2 * kStageKeys * kRowBytes;  // K rows + V rows
   // Direct-to-LDS loads per thread per stage (16 bytes each).
@@ -166,36 +168,34 @@ __device__ __forceinline__ uint32_t lds_addr_of(const uint8_t* p) {
 }
 
 // Tile tt (rows 16 tt .. 16 tt + 15) of a staged buffer in the register layout
-// a global load of the tile would give: the K rows (t.k) and the V rows (t.v),
-// read separately so that a caller can keep them apart in time.
-template <bool kFp8>
+// a global load of the tile would give (DTile, fk_attn_tile.h): the K rows (t.k)
+// and, for fp8 stages, the V rows (t.v), read separately so that a caller can
+// keep them apart in time.
+template <bool kFp8, int D>
 __device__ __forceinline__ void lds_tile_k(const uint8_t* buf, int tt, int r, int g,
-                                           TileRegs<kFp8>& t) {
-  using S = Stage<kFp8>;
+                                           DTile<kFp8, D>& t) {
+  using S = Stage<kFp8, D>;
   const int kr = 16 * tt + r;
   if constexpr (!kFp8) {
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
+    for (int c = 0; c < D / 32; ++c)
       t.k[c] = *reinterpret_cast<const uint4*>(buf + S::offset(0, kr, 4 * c + g));
   } else {
-    t.k[0] = *reinterpret_cast<const uint4*>(buf + S::offset(0, kr, 2 * g));
-    t.k[1] = *reinterpret_cast<const uint4*>(buf + S::offset(0, kr, 2 * g + 1));
+#pragma unroll
+    for (int c = 0; c < D / 64; ++c)
+      t.k[c] = *reinterpret_cast<const uint4*>(buf + S::offset(0, kr, (D / 64) * g + c));
   }
 }
-template <bool kFp8>
+// fp8 V rows 4g + i: lane r's D / 16 bytes (dims (D/16) r ..), inside one chunk.
+template <bool kFp8, int D>
 __device__ __forceinline__ void lds_tile_v(const uint8_t* buf, int tt, int r, int g,
-                                           TileRegs<kFp8>& t) {
-  using S = Stage<kFp8>;
-  if constexpr (!kFp8) {
+                                           DTile<kFp8, D>& t) {
+  static_assert(kFp8, "bf16 V rows are read with lds_v_slice");
+  using S = Stage<kFp8, D>;
+  const int byte = (D / 16) * r;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      t.v[i] = *reinterpret_cast<const uint4*>(buf + S::offset(1, 16 * tt + 4 * g + i, r));
-  } else {
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      t.v[i] = *reinterpret_cast<const uint2*>(buf + S::offset(1, 16 * tt + 4 * g + i, r >> 1) +
-                                               8 * (r & 1));
-  }
+  for (int i = 0; i < 4; ++i)
+    ld_words(buf + S::offset(1, 16 * tt + 4 * g + i, byte >> 4) + (byte & 15), t.v[i]);
 }
 
 // P.V operand of the 16-dim slice d of tile tt (bf16 stages), read with the LDS
@@ -204,8 +204,9 @@ __device__ __forceinline__ void lds_tile_v(const uint8_t* buf, int tt, int r, in
 // regrouping.  ds_read_b64_tr_b16 gives lane j of each 16-lane group, as its
 // element a, element j mod 4 of the 8 bytes addressed by lane 4a + j / 4; so
 // lane 4a + q addresses row 4g + a, dims 16d + 4q .. 16d + 4q + 3.
+template <int D>
 __device__ __forceinline__ short4_t lds_v_slice(const uint8_t* buf, int tt, int d, int r, int g) {
-  using S = Stage<false>;
+  using S = Stage<false, D>;
   const int row = 16 * tt + 4 * g + (r >> 2);
   const int q = r & 3;
   const int off = S::offset(1, row, 2 * d + (q >> 1)) + 8 * (q & 1);
@@ -217,11 +218,14 @@ __device__ __forceinline__ short4_t lds_v_slice(const uint8_t* buf, int tt, int 
 // times qs = kPrefillWaves / hw blocks of kQTokens query tokens (a group larger
 // than kPrefillWaves heads spans hsplit work-groups).  All waves share the K/V
 // stages; each walks the tiles up to its own last visible key.
-template <bool kFp8, bool kPaged>
-__global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_prefill_kernel(
+template <bool kFp8, bool kPaged, int D>
+__global__ __launch_bounds__(kPrefillWaves * 64)
+__attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D)))) void paged_prefill_kernel(
     PrefillParams P, const int32_t* __restrict__ block_tables,
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_k) {
-  using S = Stage<kFp8>;
+  using S = Stage<kFp8, D>;
+  constexpr int kCB = col_blocks_for(D);  // 16-query column blocks per wave
+  constexpr int kQT = 16 * kCB;           // query tokens per wave
   __shared__ __align__(16) uint8_t lds0[S::kBytes];
   __shared__ __align__(16) uint8_t lds1[S::kBytes];
   // Grid: x = kv head (x hsplit), y = sequence, z = query block.  The block
@@ -245,7 +249,7 @@ __global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_pre
   // long tail on its own; the upper half of the grid then has nothing to do.
   // Otherwise the blocks' key counts are close, and work-group x takes block
   // nqb - 1 - x alone (the heaviest first), keeping twice the work-groups.
-  const int wg_tokens = qs * kQTokens;
+  const int wg_tokens = qs * kQT;
   const int nqb = (q_len + wg_tokens - 1) / wg_tokens;
   const bool paired = P.causal && k_len - q_len < q_len;
   const int x = static_cast<int>(blockIdx.z);
@@ -269,12 +273,12 @@ __global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_pre
   // One query block of the work-group, start to finish (its own K/V stages).
   auto process_block = [&](int qblk) {
   const int jw0 = qblk * wg_tokens;  // first query of the work-group
-  const int j0 = jw0 + (wave / hw) * kQTokens;
+  const int j0 = jw0 + (wave / hw) * kQT;
   // Waves without queries (past the chunk, or past the group) still stage.
   const bool active = j0 < q_len && head < P.gqa && wave < qs * hw;
   // Keys [0, kend) cover every query of this wave's block; kend_wg every query
   // of the work-group.
-  const int kend = active ? max(0, min(k_len, offset + min(j0 + kQTokens, q_len))) : 0;
+  const int kend = active ? max(0, min(k_len, offset + min(j0 + kQT, q_len))) : 0;
   const int kend_wg = max(0, min(k_len, offset + min(jw0 + wg_tokens, q_len)));
   // Sliding window: query j sees keys from offset + j - win.  kbeg (this wave's
   // first query) and kbeg_wg (the work-group's) bound the keys from below; the
@@ -283,19 +287,19 @@ __global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_pre
   const int win = P.window_left;
   const int kbeg = (win >= 0 && active) ? max(0, offset + j0 - win) : 0;
   const int kbeg_wg = win >= 0 ? max(0, offset + jw0 - win) : 0;
-  const int khead = (win >= 0 && active) ? offset + min(j0 + kQTokens, q_len) - 1 - win : 0;
+  const int khead = (win >= 0 && active) ? offset + min(j0 + kQT, q_len) - 1 - win : 0;
 
   // Q^T operands: column r of block nb = query j0 + 16 nb + r.
-  bf16x8_t qb[kColBlocks][4];
+  bf16x8_t qb[kCB][D / 32];
 #pragma unroll
-  for (int nb = 0; nb < kColBlocks; ++nb) {
+  for (int nb = 0; nb < kCB; ++nb) {
     const int j = j0 + 16 * nb + r;
     const bool ok = active && j < q_len;
     const uint16_t* qp = P.q + static_cast<int64_t>(q_start + (ok ? j : 0)) * P.q_row_stride +
-                         static_cast<int64_t>(hq) * kHead;
+                         static_cast<int64_t>(hq) * D;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int d0 = kFp8 ? 32 * g + 8 * c : 32 * c + 8 * g;
+    for (int c = 0; c < D / 32; ++c) {
+      const int d0 = kFp8 ? (D / 4) * g + 8 * c : 32 * c + 8 * g;
       const uint4 v = ok ? *reinterpret_cast<const uint4*>(qp + d0) : make_uint4(0, 0, 0, 0);
       qb[nb][c] = __builtin_bit_cast(bf16x8_t, v);
     }
@@ -305,14 +309,14 @@ __global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_pre
   // 4g + i, accumulated by an MFMA of P against ones beside the P.V ones (the
   // same bf16 P weights as the numerator), so no VALU adds and no cross-lane
   // fetch at the end.
-  float m_run[kColBlocks];
-  floatx4_t o[kColBlocks][8], l_acc[kColBlocks];
+  float m_run[kCB];
+  floatx4_t o[kCB][D / 16], l_acc[kCB];
 #pragma unroll
-  for (int nb = 0; nb < kColBlocks; ++nb) {
+  for (int nb = 0; nb < kCB; ++nb) {
     m_run[nb] = kNegInf;
     l_acc[nb] = floatx4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int d = 0; d < 8; ++d) o[nb][d] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+    for (int d = 0; d < D / 16; ++d) o[nb][d] = floatx4_t{0.f, 0.f, 0.f, 0.f};
   }
   const bf16x8_t ones = __builtin_bit_cast(
       bf16x8_t, make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u));
@@ -337,29 +341,29 @@ __global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_pre
   auto pair_step = [&](auto masked, int tok0, const uint8_t* buf, int tt, bool ok_a,
                        bool ok_b) {
     constexpr bool kMasked = decltype(masked)::value;
-    TileRegs<kFp8> ta, tb;
+    DTile<kFp8, D> ta, tb;
     // Scores of tile a for every column block, then tile b's K is read: the two
     // K tiles are never live at once (20 fewer VGPRs in the compiler's own
     // allocation; measured 1% faster).
-    floatx4_t sc_a[kColBlocks], sc_b[kColBlocks];
+    floatx4_t sc_a[kCB], sc_b[kCB];
     {
-      lds_tile_k<kFp8>(buf, tt, r, g, ta);
-      uint4 ka[4];
-      k_chunks(ta, ka);
+      lds_tile_k<kFp8, D>(buf, tt, r, g, ta);
+      uint4 ka[D / 32];
+      k_chunks_d(ta, ka);
 #pragma unroll
-      for (int nb = 0; nb < kColBlocks; ++nb) sc_a[nb] = qk_scores(ka, qb[nb]);
+      for (int nb = 0; nb < kCB; ++nb) sc_a[nb] = qk_scores_n(ka, qb[nb]);
     }
     asm volatile("" ::: "memory");  // tile b's K reads stay after tile a's
     {
-      lds_tile_k<kFp8>(buf, tt + 1, r, g, tb);
-      uint4 kb[4];
-      k_chunks(tb, kb);
+      lds_tile_k<kFp8, D>(buf, tt + 1, r, g, tb);
+      uint4 kb[D / 32];
+      k_chunks_d(tb, kb);
 #pragma unroll
-      for (int nb = 0; nb < kColBlocks; ++nb) sc_b[nb] = qk_scores(kb, qb[nb]);
+      for (int nb = 0; nb < kCB; ++nb) sc_b[nb] = qk_scores_n(kb, qb[nb]);
     }
-    short4_t p_a[kColBlocks], p_b[kColBlocks];
+    short4_t p_a[kCB], p_b[kCB];
 #pragma unroll
-    for (int nb = 0; nb < kColBlocks; ++nb) {
+    for (int nb = 0; nb < kCB; ++nb) {
       const floatx4_t acc_a = sc_a[nb];
       const floatx4_t acc_b = sc_b[nb];
       const int j = j0 + 16 * nb + r;  // this lane's query column
@@ -408,7 +412,7 @@ __global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_pre
         for (int i = 0; i < 4; ++i) {
           const float a = row_value<16>(alpha, g, i);
 #pragma unroll
-          for (int d = 0; d < 8; ++d) o[nb][d][i] *= a;
+          for (int d = 0; d < D / 16; ++d) o[nb][d][i] *= a;
           l_acc[nb][i] *= a;
         }
       }
@@ -427,13 +431,13 @@ __global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_pre
       p_b[nb] = p_operand(pb);
     }
     asm volatile("" ::: "memory");  // V reads stay after the score work
-    short4_t vba[8], vbb[8];  // shared by the column blocks
+    short4_t vba[D / 16], vbb[D / 16];  // shared by the column blocks
     if constexpr (!kFp8) {
       // Slice d holds dims 16d .. 16d + 15 (lane r: dim 16d + r).
 #pragma unroll
-      for (int d = 0; d < 8; ++d) {
-        vba[d] = lds_v_slice(buf, tt, d, r, g);
-        vbb[d] = lds_v_slice(buf, tt + 1, d, r, g);
+      for (int d = 0; d < D / 16; ++d) {
+        vba[d] = lds_v_slice<D>(buf, tt, d, r, g);
+        vbb[d] = lds_v_slice<D>(buf, tt + 1, d, r, g);
       }
       if constexpr (kMasked) {
         // Keys past the wave's keys (or on a masked page) may hold anything:
@@ -447,7 +451,7 @@ __global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_pre
                    ((ok_b && k0 + kTile + 1 < kend) ? 0xffff0000u : 0u);
         }
 #pragma unroll
-        for (int d = 0; d < 8; ++d) {
+        for (int d = 0; d < D / 16; ++d) {
           uint2 wa = __builtin_bit_cast(uint2, vba[d]), wb = __builtin_bit_cast(uint2, vbb[d]);
           wa.x &= ma[0]; wa.y &= ma[1];
           wb.x &= mb[0]; wb.y &= mb[1];
@@ -456,19 +460,17 @@ __global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_pre
         }
       }
     } else {
-      // Slice d holds dims 8r + d (lane r), regrouped from the row loads.
-      lds_tile_v<kFp8>(buf, tt, r, g, ta);
-      lds_tile_v<kFp8>(buf, tt + 1, r, g, tb);
-      uint4 vra[4], vrb[4];
+      // Slice d holds dims (D/16) r + d (lane r), regrouped from the row loads.
+      lds_tile_v<kFp8, D>(buf, tt, r, g, ta);
+      lds_tile_v<kFp8, D>(buf, tt + 1, r, g, tb);
+      uint32_t vwa[4][D / 32], vwb[4][D / 32];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        vra[i] = (!kMasked || (ok_a && tok0 + 4 * g + i < kend)) ? v_row(ta, i)
-                                                                 : make_uint4(0, 0, 0, 0);
-        vrb[i] = (!kMasked || (ok_b && tok0 + kTile + 4 * g + i < kend)) ? v_row(tb, i)
-                                                                         : make_uint4(0, 0, 0, 0);
+        v_words(ta, i, !kMasked || (ok_a && tok0 + 4 * g + i < kend), vwa[i]);
+        v_words(tb, i, !kMasked || (ok_b && tok0 + kTile + 4 * g + i < kend), vwb[i]);
       }
-      v_operands(vra, vba);
-      v_operands(vrb, vbb);
+      v_operands_w(vwa, vba);
+      v_operands_w(vwb, vbb);
     }
     // P.V over the 32 keys with the 16x16x32 MFMA (the 16x16x16 one takes as
     // long on gfx950 for half the work).  Its k index 8g + e stands for key
@@ -476,14 +478,14 @@ __global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_pre
     // (P) and the B operand (V) both take tile a's four keys then tile b's, so
     // the sum runs over the same 32 keys.
 #pragma unroll
-    for (int nb = 0; nb < kColBlocks; ++nb) {
+    for (int nb = 0; nb < kCB; ++nb) {
       const bf16x8_t pab = __builtin_bit_cast(
           bf16x8_t, make_uint4(__builtin_bit_cast(uint2, p_a[nb]).x,
                                __builtin_bit_cast(uint2, p_a[nb]).y,
                                __builtin_bit_cast(uint2, p_b[nb]).x,
                                __builtin_bit_cast(uint2, p_b[nb]).y));
 #pragma unroll
-      for (int d = 0; d < 8; ++d) {
+      for (int d = 0; d < D / 16; ++d) {
         const uint2 va = __builtin_bit_cast(uint2, vba[d]), vb = __builtin_bit_cast(uint2, vbb[d]);
         const bf16x8_t v8 = __builtin_bit_cast(bf16x8_t, make_uint4(va.x, va.y, vb.x, vb.y));
         o[nb][d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pab, v8, o[nb][d], 0, 0, 0);
@@ -502,7 +504,7 @@ __global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_pre
   // 4 rows of bf16 or 8 of fp8, and the positions are 64-aligned), so its
   // source address is a wave-uniform part (that tile's first row) plus a
   // per-lane part that does not change from stage to stage, computed once here.
-  const int64_t head_off = static_cast<int64_t>(h) * kHead * (kFp8 ? 1 : 2);
+  const int64_t head_off = static_cast<int64_t>(h) * D * (kFp8 ? 1 : 2);
   constexpr int kStageChunks = kStageKeys * S::kChunks;  // chunks of K (or V) per stage
   uint32_t lane_off[S::kLoads];
 #pragma unroll
@@ -610,7 +612,7 @@ __global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_pre
 
   const float vs = (kFp8 && P.v_scale) ? P.v_scale[h] : 1.f;
 #pragma unroll
-  for (int nb = 0; nb < kColBlocks; ++nb) {
+  for (int nb = 0; nb < kCB; ++nb) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int jr = j0 + 16 * nb + 4 * g + i;  // query row this lane holds
@@ -619,22 +621,30 @@ __global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_pre
       if (jr >= q_len) continue;
       const float f = l > 0.f ? vs / l : 0.f;
       uint16_t* orow = P.out + static_cast<int64_t>(q_start + jr) * P.out_row_stride +
-                       static_cast<int64_t>(hq) * kHead;
+                       static_cast<int64_t>(hq) * D;
       if constexpr (!kFp8) {
         // o[nb][d] holds dim 16d + r: lanes r = 0..15 write 16 adjacent dims.
 #pragma unroll
-        for (int d = 0; d < 8; ++d)
+        for (int d = 0; d < D / 16; ++d)
           orow[16 * d + r] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(o[nb][d][i] * f));
       } else {
-        // o[nb][d] holds dim 8r + d: eight adjacent dims per lane.
-        uint32_t w[4];
+        // o[nb][d] holds dim (D/16) r + d: D/16 adjacent dims per lane.
+        uint32_t w[D / 32];
 #pragma unroll
-        for (int d = 0; d < 4; ++d) {
+        for (int d = 0; d < D / 32; ++d) {
           const bf16x2_t pk = {static_cast<__bf16>(o[nb][2 * d][i] * f),
                                static_cast<__bf16>(o[nb][2 * d + 1][i] * f)};
           w[d] = __builtin_bit_cast(uint32_t, pk);
         }
-        *reinterpret_cast<uint4*>(orow + 8 * r) = make_uint4(w[0], w[1], w[2], w[3]);
+        uint16_t* dst = orow + (D / 16) * r;
+        if constexpr (D == 64) {
+          *reinterpret_cast<uint2*>(dst) = make_uint2(w[0], w[1]);
+        } else {
+#pragma unroll
+          for (int q = 0; q < D / 128; ++q)
+            *reinterpret_cast<uint4*>(dst + 8 * q) =
+                make_uint4(w[4 * q], w[4 * q + 1], w[4 * q + 2], w[4 * q + 3]);
+        }
       }
     }
   }
@@ -651,11 +661,22 @@ __global__ __launch_bounds__(kPrefillWaves * 64) FK_PREFILL_WAVES void paged_pre
   }
 }
 
-template <bool FP8, bool PAGED>
+template <bool FP8, bool PAGED, int D>
 void launch_prefill(const PrefillParams& P, dim3 grid, const int32_t* bt, const int32_t* cu_q,
                     const int32_t* cu_k, hipStream_t stream) {
-  hipLaunchKernelGGL((paged_prefill_kernel<FP8, PAGED>), grid, dim3(kPrefillWaves * 64), 0,
+  hipLaunchKernelGGL((paged_prefill_kernel<FP8, PAGED, D>), grid, dim3(kPrefillWaves * 64), 0,
                      stream, P, bt, cu_q, cu_k);
+}
+
+template <int D>
+void launch_prefill_d(bool paged, bool fp8, const PrefillParams& P, dim3 grid, const int32_t* bt,
+                      const int32_t* cu_q, const int32_t* cu_k, hipStream_t stream) {
+  if (!paged)
+    launch_prefill<false, false, D>(P, grid, nullptr, cu_q, cu_k, stream);
+  else if (fp8)
+    launch_prefill<true, true, D>(P, grid, bt, cu_q, cu_k, stream);
+  else
+    launch_prefill<false, true, D>(P, grid, bt, cu_q, cu_k, stream);
 }
 
 }  // namespace
@@ -683,12 +704,9 @@ int prefill_entry(const char* name, bool paged, void* out, int64_t out_row_strid
   FK_REQUIRE(num_heads > 0 && num_kv_heads > 0 && num_heads % num_kv_heads == 0,
              "%s: num_heads %d must be a positive multiple of num_kv_heads %d", name, num_heads,
              num_kv_heads);
-  if (head_size != kHead)
-    return set_error(FK_ERR_UNSUPPORTED, "%s: head_size %d unsupported (128 only)", name,
+  if (head_size != 64 && head_size != 128 && head_size != 256)
+    return set_error(FK_ERR_UNSUPPORTED, "%s: head_size %d unsupported (64, 128 or 256)", name,
                      head_size);
-  if (num_heads / num_kv_heads > 16)
-    return set_error(FK_ERR_UNSUPPORTED, "%s: GQA group %d > 16 unsupported", name,
-                     num_heads / num_kv_heads);
   FK_REQUIRE(num_kv_heads <= 32767, "%s: too many kv heads", name);
   if (paged) {
     FK_REQUIRE(block_size >= kTile && (block_size & (block_size - 1)) == 0,
@@ -700,7 +718,8 @@ int prefill_entry(const char* name, bool paged, void* out, int64_t out_row_strid
                  out_row_stride >= static_cast<int64_t>(num_heads) * head_size,
              "%s: row stride shorter than num_heads * head_size", name);
   const int64_t elem = kv_dtype == FK_DTYPE_FP8_E4M3FN ? 1 : 2;
-  FK_REQUIRE(k_row_bytes >= num_kv_heads * kHead * elem && v_row_bytes >= num_kv_heads * kHead * elem,
+  FK_REQUIRE(k_row_bytes >= num_kv_heads * head_size * elem &&
+                 v_row_bytes >= num_kv_heads * head_size * elem,
              "%s: key/value rows shorter than num_kv_heads * head_size", name);
   if (batch == 0 || max_seqlen_q == 0) return FK_OK;
   FK_REQUIRE(out && q && k && v && cu_seqlens_q && cu_seqlens_k && (!paged || block_tables),
@@ -712,7 +731,8 @@ int prefill_entry(const char* name, bool paged, void* out, int64_t out_row_strid
              "%s: q/out/keys/values must be 16-byte aligned with 16-byte row strides", name);
   const int gqa = num_heads / num_kv_heads;
   const int hw = gqa < kPrefillWaves ? gqa : kPrefillWaves;  // query heads per work-group
-  const int64_t wg_tokens = static_cast<int64_t>(kPrefillWaves / hw) * kQTokens;
+  const int64_t wg_tokens =
+      static_cast<int64_t>(kPrefillWaves / hw) * 16 * col_blocks_for(head_size);
   const int64_t qblocks = (max_seqlen_q + wg_tokens - 1) / wg_tokens;
   PrefillParams P;
   P.out = static_cast<uint16_t*>(out);
@@ -742,12 +762,12 @@ int prefill_entry(const char* name, bool paged, void* out, int64_t out_row_strid
   const dim3 grid(static_cast<unsigned>(num_kv_heads * hsplit), static_cast<unsigned>(batch),
                   static_cast<unsigned>(qblocks));
   hipStream_t s = as_stream(stream);
-  if (!paged)
-    launch_prefill<false, false>(P, grid, nullptr, cu_seqlens_q, cu_seqlens_k, s);
-  else if (kv_dtype == FK_DTYPE_FP8_E4M3FN)
-    launch_prefill<true, true>(P, grid, block_tables, cu_seqlens_q, cu_seqlens_k, s);
-  else
-    launch_prefill<false, true>(P, grid, block_tables, cu_seqlens_q, cu_seqlens_k, s);
+  const bool fp8 = kv_dtype == FK_DTYPE_FP8_E4M3FN;
+  switch (head_size) {
+    case 64: launch_prefill_d<64>(paged, fp8, P, grid, block_tables, cu_seqlens_q, cu_seqlens_k, s); break;
+    case 256: launch_prefill_d<256>(paged, fp8, P, grid, block_tables, cu_seqlens_q, cu_seqlens_k, s); break;
+    default: launch_prefill_d<128>(paged, fp8, P, grid, block_tables, cu_seqlens_q, cu_seqlens_k, s); break;
+  }
   return check_launch(name);
 }
 

@@ -18,7 +18,7 @@ def _flush(msg):
     print(msg, flush=True)
 
 
-def _case(cuda, q_lens, k_lens, hq=32, hk=8, bs=16, seed=70, fp8=False, extra_pages=3):
+def _case(cuda, q_lens, k_lens, hq=32, hk=8, bs=16, seed=70, fp8=False, extra_pages=3, d=128):
     g = torch.Generator().manual_seed(seed)
     pages = [(k + bs - 1) // bs for k in k_lens]
     nb = sum(pages) + extra_pages
@@ -30,9 +30,9 @@ def _case(cuda, q_lens, k_lens, hq=32, hk=8, bs=16, seed=70, fp8=False, extra_pa
         off += p
     cu_q = torch.tensor([0] + list(np.cumsum(q_lens)), dtype=torch.int32)
     cu_k = torch.tensor([0] + list(np.cumsum(k_lens)), dtype=torch.int32)
-    q = torch.randn(int(cu_q[-1]), hq, 128, generator=g).to(torch.bfloat16)
-    kc = torch.randn(nb, bs, hk, 128, generator=g)
-    vc = torch.randn(nb, bs, hk, 128, generator=g)
+    q = torch.randn(int(cu_q[-1]), hq, d, generator=g).to(torch.bfloat16)
+    kc = torch.randn(nb, bs, hk, d, generator=g)
+    vc = torch.randn(nb, bs, hk, d, generator=g)
     ks = vs = None
     if fp8:
         ks = (0.01 + 0.09 * torch.rand(hk, generator=g)).float()
@@ -43,13 +43,14 @@ def _case(cuda, q_lens, k_lens, hq=32, hk=8, bs=16, seed=70, fp8=False, extra_pa
         kc, vc = kc.to(torch.bfloat16), vc.to(torch.bfloat16)
     t = lambda x: None if x is None else x.to(cuda)  # noqa: E731
     return dict(q=q.to(cuda), kc=kc.to(cuda), vc=vc.to(cuda), bt=bt.to(cuda), cu_q=cu_q.to(cuda),
-                cu_k=cu_k.to(cuda), max_q=max(q_lens) if q_lens else 0, ks=t(ks), vs=t(vs))
+                cu_k=cu_k.to(cuda), max_q=max(q_lens) if q_lens else 0, ks=t(ks), vs=t(vs),
+                scale=d ** -0.5)
 
 
 def _run(c, causal=True, window_left=-1, sinks=None):
     out = torch.full_like(c["q"], float("nan"))
     ops.paged_prefill(out, c["q"], c["kc"], c["vc"], c["bt"], c["cu_q"], c["cu_k"], c["max_q"],
-                      128 ** -0.5, c["ks"], c["vs"], causal, window_left, sinks)
+                      c["scale"], c["ks"], c["vs"], causal, window_left, sinks)
     torch.cuda.synchronize()
     return out
 
@@ -59,7 +60,7 @@ def _oracle(c, causal=True, window_left=-1, sinks=None):
     kc = c["kc"].view(torch.uint8).cpu().numpy() if fp8 else c["kc"].float().cpu().numpy()
     vc = c["vc"].view(torch.uint8).cpu().numpy() if fp8 else c["vc"].float().cpu().numpy()
     return oracle.paged_prefill(c["q"].float().cpu().numpy(), kc, vc, c["bt"].cpu().numpy(),
-                                c["cu_q"].cpu().numpy(), c["cu_k"].cpu().numpy(), 128 ** -0.5,
+                                c["cu_q"].cpu().numpy(), c["cu_k"].cpu().numpy(), c["scale"],
                                 None if c["ks"] is None else c["ks"].cpu().numpy(),
                                 None if c["vs"] is None else c["vs"].cpu().numpy(),
                                 causal=causal, window_left=window_left,
@@ -294,3 +295,73 @@ def test_prefill_window_sinks_dense_and_candidate(cuda):
         mod(c["q"], c["kc"], c["vc"], cu_seqlens_q=c["cu_q"], cu_seqlens_k=c["cu_k"],
             max_seqlen_q=c["max_q"], max_seqlen_k=max(k_lens), block_table=c["bt"],
             causal=False, window_size=(63, 0))
+
+
+# ---------------------------------------------------------------------------
+# Head sizes 64 and 256, and query groups above 16 (the shapes the reference builds
+# FlashAttnPrefill with besides Qwen3-8B's: Qwen3-Next 16/2/256,
+# L2/qwen3_next_attention.py:148-150; Whisper's self-attention, MHA at 64,
+# L2/whisper_attention.py:185-190).
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("hq,hk,d", [(16, 2, 256), (20, 20, 64), (64, 8, 64), (64, 2, 128),
+                                     (40, 1, 256), (71, 1, 64)])
+def test_paged_prefill_head_sizes_and_groups(cuda, hq, hk, d):
+    _flush(f"paged prefill hq={hq} hk={hk} d={d}")
+    c = _case(cuda, [1, 33, 100, 64], [1, 33, 300, 1000], hq=hq, hk=hk, bs=64, d=d,
+              seed=hq + hk + d)
+    _close(_run(c), _oracle(c), 1e-2, f"{hq}/{hk}/{d}")
+    _close(_run(c, causal=False), _oracle(c, causal=False), 1e-2, f"{hq}/{hk}/{d} non-causal")
+
+
+@pytest.mark.parametrize("d", [64, 256])
+def test_paged_prefill_head_sizes_fp8(cuda, d):
+    _flush(f"paged prefill fp8 d={d}")
+    c = _case(cuda, [16, 40, 1], [100, 40, 257], hq=16, hk=2, bs=64, seed=74 + d, fp8=True, d=d)
+    _close(_run(c), _oracle(c), 3e-2, f"fp8 d={d}")
+
+
+@pytest.mark.parametrize("d", [64, 256])
+def test_paged_prefill_head_sizes_window_and_sinks(cuda, d):
+    """A gpt-oss-like layer (64 query heads, 8 kv heads, a 128-token window, sinks)
+    at head size 64, and the same at 256."""
+    _flush(f"paged prefill window+sinks d={d}")
+    c = _case(cuda, [300, 7], [500, 200], hq=64, hk=8, bs=16, seed=80 + d, d=d)
+    g = torch.Generator().manual_seed(81)
+    sinks = (2 * torch.randn(64, generator=g)).to(cuda)
+    _close(_run(c, window_left=127, sinks=sinks), _oracle(c, window_left=127, sinks=sinks), 1e-2,
+           f"window+sinks d={d}")
+
+
+@pytest.mark.parametrize("hq,hk,d", [(20, 20, 64), (16, 2, 256)])
+def test_varlen_prefill_head_sizes(cuda, hq, hk, d):
+    """Dense keys (no block table) at head sizes 64 and 256: Whisper's encoder
+    self-attention is this path, non-causal over the whole segment."""
+    _flush(f"varlen prefill hq={hq} hk={hk} d={d}")
+    g = torch.Generator().manual_seed(90 + d)
+    q_lens, k_lens = [50, 1500, 3], [50, 1500, 9]
+    cu_q = torch.tensor([0] + list(np.cumsum(q_lens)), dtype=torch.int32)
+    cu_k = torch.tensor([0] + list(np.cumsum(k_lens)), dtype=torch.int32)
+    q = torch.randn(int(cu_q[-1]), hq, d, generator=g).to(torch.bfloat16).to(cuda)
+    kv = torch.randn(int(cu_k[-1]), 2, hk, d, generator=g).to(torch.bfloat16).to(cuda)
+    key, value = kv[:, 0], kv[:, 1]  # strided views, rows 2 * hk * d apart
+    for causal in (False, True):
+        out = torch.full_like(q, float("nan"))
+        ops.varlen_prefill(out, q, key, value, cu_q.to(cuda), cu_k.to(cuda), max(q_lens),
+                           d ** -0.5, causal)
+        torch.cuda.synchronize()
+        ref = oracle.varlen_prefill(q.float().cpu().numpy(), key.float().cpu().numpy(),
+                                    value.float().cpu().numpy(), cu_q.numpy(), cu_k.numpy(),
+                                    d ** -0.5, causal)
+        _close(out, ref, 1e-2, f"varlen {hq}/{hk}/{d} causal={causal}")
+
+
+def test_candidate_prefill_head_size_256(cuda):
+    """FlashAttnPrefill (the drop-in class) at Qwen3-Next's head size, paged and dense."""
+    from fastkernels_amd.candidate.L1.flash_attn_prefill import FlashAttnPrefill
+
+    c = _case(cuda, [40, 200], [40, 600], hq=16, hk=2, bs=64, d=256, seed=95)
+    mod = FlashAttnPrefill(16, 2, 256)
+    out = mod(c["q"], c["kc"], c["vc"], c["cu_q"], c["cu_k"], c["max_q"], 600,
+              block_table=c["bt"])
+    torch.cuda.synchronize()
+    _close(out, _oracle(c), 1e-2, "candidate d=256")
