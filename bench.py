@@ -18,6 +18,7 @@ the whole batch on the host's cores.
   python bench.py [--steps K] [--warmup W] [--num-splits S] [--no-cpu]
   python bench.py --table          # per-op table for C1-C5 to stderr (+ --table-json PATH)
   python bench.py --calib-copy     # plain 1 GiB device copy, for rocprof counter scaling
+  python bench.py --profile-ops    # each op after a cache flush, for rocprof counter passes
 """
 from __future__ import annotations
 
@@ -48,6 +49,8 @@ def _parse():
     ap.add_argument("--table", action="store_true", help="per-op table for C1-C5")
     ap.add_argument("--table-json", type=str, default=None)
     ap.add_argument("--calib-copy", action="store_true")
+    ap.add_argument("--profile-ops", action="store_true",
+                    help="each op on its C1-C5 inputs after a cache flush, for rocprofv3 --pmc")
     ap.add_argument("--seed", type=int, default=200)
     return ap.parse_args()
 
@@ -864,6 +867,79 @@ def bench_table(args):
     return rows
 
 
+def profile_ops(reps: int = 3):
+    """Each op of the decode step on its C1-C5 inputs, `reps` times, every call after a
+    512 MB read that evicts L2 and the MALL: the program rocprofv3 --pmc runs to count
+    the HBM bytes (FETCH_SIZE / WRITE_SIZE) each kernel moves per dispatch.  Prints one
+    JSON line per op: its kernels' name fragment and algorithmic bytes per call."""
+    import torch
+
+    from fastkernels_amd import ops, workloads
+    from fastkernels_amd.candidate.L1.rotary_emb import RotaryEmbedding
+
+    dev = torch.device("cuda:0")
+    flush = _flush_buffer(dev)
+    rows = []
+
+    def run(op, kernel, nbytes, fn):
+        for _ in range(reps):
+            flush.sum()
+            fn()
+        torch.cuda.synchronize()
+        rows.append({"op": op, "kernel": kernel, "algorithmic_bytes": nbytes, "calls": reps})
+        print(json.dumps(rows[-1]), flush=True)
+
+    c1 = workloads.c1_norm(dev)
+    run("C1 fused_add_rmsnorm bf16 [256,1024]", "fused_add_rmsnorm", (4 * 256 * 1024 + 1024) * 2,
+        lambda: ops.fused_add_rms_norm(c1.x, c1.residual, c1.weight, c1.eps))
+    c2 = workloads.c2_store(dev)
+    nvalid = int((c2.slot_mapping >= 0).sum().item())
+    run("C2 store_kvcache [4096,8,128]", "store_kvcache", 8 * 4096 + nvalid * 4 * 8 * 128 * 2,
+        lambda: ops.store_kvcache(c2.key, c2.value, c2.k_cache, c2.v_cache, c2.slot_mapping))
+    del c2
+    c4 = workloads.c4_chain(dev)
+    run("C4 fused_add_rmsnorm bf16 [256,4096]", "fused_add_rmsnorm", (4 * 256 * 4096 + 4096) * 2,
+        lambda: ops.fused_add_rms_norm(c4.hidden, c4.residual, c4.norm_weight, 1e-6))
+    rope = RotaryEmbedding(128, c4.max_position, c4.rope_theta).to(dev)
+    q, k, v = c4.qkv[:, :4096], c4.qkv[:, 4096:5120], c4.qkv[:, 5120:]
+    run("C4 rotary q[256,32x128] k[256,8x128]", "rotary",
+        2 * 256 * 5120 * 2 + 256 * 8 + 256 * 128 * 4,
+        lambda: ops.rotary_embedding(c4.positions, q, k, 128, rope.cos_sin_cache, True))
+    dec = c4.decode
+    run("C4 store_kvcache [256,8,128]", "store_kvcache", 8 * 256 + 256 * 4 * 1024 * 2,
+        lambda: ops.store_kvcache(k.view(256, 8, 128), v.view(256, 8, 128), dec.k_cache,
+                                  dec.v_cache, c4.slot_mapping))
+    act = torch.empty(256, 12288, dtype=torch.bfloat16, device=dev)
+    run("C4 silu_and_mul [256,2x12288]", "silu_and_mul", 256 * 3 * 12288 * 2,
+        lambda: ops.silu_and_mul(act, c4.gate_up))
+    g = torch.Generator().manual_seed(workloads.SEED + 7)
+    qw = (1 + 0.1 * torch.randn(128, generator=g)).to(torch.bfloat16).to(dev)
+    kw = (1 + 0.1 * torch.randn(128, generator=g)).to(torch.bfloat16).to(dev)
+    qk_bytes = (256 * (4096 + 2 * 1024) * 2 + 256 * (4096 + 1024) * 2 + 256 * 2 * 1024 * 2
+                + 256 * 16 + 256 * 128 * 4 + 2 * 128 * 2)
+    run("C4 qk_norm_rope_store", "qk_norm_rope_store", qk_bytes,
+        lambda: ops.qk_norm_rope_store(c4.positions, q, k, v, dec.k_cache, dec.v_cache,
+                                       c4.slot_mapping, 128, rope.cos_sin_cache, True, qw, kw,
+                                       1e-6))
+    for name, case in (("C4", dec), ("C5", None)):
+        if case is None:
+            del c4, dec
+            torch.cuda.empty_cache()
+            case = workloads.c5_fp8_decode(dev)
+        b, hq, d = case.q.shape
+        plan = ops.paged_decode_plan(b, hq, case.k_cache.shape[2], d, case.max_seq_len, 0)
+        ws = torch.zeros(max(1, plan.workspace_bytes), dtype=torch.uint8, device=dev)
+        out = torch.empty_like(case.q)
+        total = case.algorithmic_bytes()
+        run(f"{name} paged_decode {str(case.k_cache.dtype).replace('torch.', '')} B={b} Hq={hq} "
+            "balanced (main kernel; the merge is listed separately)", "paged_decode_balanced",
+            total - out.numel() * out.element_size(),
+            lambda case=case, plan=plan, ws=ws, out=out: ops.paged_decode(
+                out, case.q, case.k_cache, case.v_cache, case.block_tables, case.ctx_lens,
+                case.scale, plan.part_tokens, plan.max_parts, ws, case.k_scale, case.v_scale))
+    return rows
+
+
 def calib_copy():
     import torch
 
@@ -892,6 +968,9 @@ def main():
     _native.lib()
     if args.calib_copy:
         calib_copy()
+        return
+    if args.profile_ops:
+        profile_ops()
         return
     if args.table:
         bench_table(args)
