@@ -6,9 +6,13 @@ snapshot of the repository carries it to a GPU host).  The build always
 recompiles: it is the "does it build" check as well as the build.
 
 Usage: ``python -m fastkernels_amd.build`` (or ``__graft_entry__.build()``).
+``python -m fastkernels_amd.build --define NAME --out DIR`` builds a variant
+library with extra preprocessor definitions into DIR/libfk_amd.so instead (the
+A/B tile forms of fk_paged_decode.hip); load it with FASTKERNELS_AMD_LIB.
 """
 from __future__ import annotations
 
+import argparse
 import concurrent.futures as cf
 import os
 import shutil
@@ -47,35 +51,45 @@ def _hipcc() -> str:
     return found
 
 
-def _compile(src: Path) -> Path:
-    obj = OBJ_DIR / (src.stem + ".o")
-    cmd = [_hipcc(), *HIP_FLAGS, "-c", str(src), "-o", str(obj)]
+def _compile(src: Path, obj_dir: Path = OBJ_DIR, defines: tuple = ()) -> Path:
+    obj = obj_dir / (src.stem + ".o")
+    cmd = [_hipcc(), *HIP_FLAGS, *(f"-D{d}" for d in defines), "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{proc.stderr}")
     return obj
 
 
-def build(verbose: bool = True) -> Path:
-    """Compile every csrc/*.hip for gfx950 and link libfk_amd.so; return its path."""
-    OBJ_DIR.mkdir(exist_ok=True)
-    LIB_DIR.mkdir(exist_ok=True)
+def build(verbose: bool = True, defines: tuple = (), out_dir: Path | None = None) -> Path:
+    """Compile every csrc/*.hip for gfx950 and link libfk_amd.so; return its path.
+    With out_dir, objects and library go there (a variant build with `defines`)."""
+    obj_dir = OBJ_DIR if out_dir is None else Path(out_dir) / "_obj"
+    lib_path = LIB_PATH if out_dir is None else Path(out_dir) / "libfk_amd.so"
+    obj_dir.mkdir(parents=True, exist_ok=True)
+    lib_path.parent.mkdir(parents=True, exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))
     if not sources:
         raise RuntimeError(f"no HIP sources under {CSRC}")
     workers = min(len(sources), os.cpu_count() or 4, 8)
     with cf.ThreadPoolExecutor(max_workers=workers) as ex:
-        objs = list(ex.map(_compile, sources))
-    tmp = LIB_PATH.with_suffix(".so.tmp")
+        objs = list(ex.map(lambda src: _compile(src, obj_dir, tuple(defines)), sources))
+    tmp = lib_path.with_suffix(".so.tmp")
     cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stderr}")
-    os.replace(tmp, LIB_PATH)
+    os.replace(tmp, lib_path)
     if verbose:
-        print(f"built {LIB_PATH} from {len(sources)} sources", file=sys.stderr)
-    return LIB_PATH
+        extra = f" with {', '.join(defines)}" if defines else ""
+        print(f"built {lib_path} from {len(sources)} sources{extra}", file=sys.stderr)
+    return lib_path
 
 
 if __name__ == "__main__":
-    build()
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--define", action="append", default=[], help="preprocessor macro (repeatable)")
+    ap.add_argument("--out", type=Path, default=None, help="output directory of a variant build")
+    a = ap.parse_args()
+    if a.define and a.out is None:
+        ap.error("--define needs --out (the in-tree library is always the default build)")
+    build(defines=tuple(a.define), out_dir=a.out)

@@ -47,10 +47,29 @@
 // HBM-bound loop needs, so the padding is free, while the VALU work per token
 // stays at a few instructions (no cross-lane dot-product reductions, two
 // row-swap permutes per tile for the max).
+//
+// Two alternative tile forms are compiled in only for A/B measurement; the
+// shipped library defines neither macro, and both measured slower on C3:
+//   FK_DECODE_VALU_TILE  bf16, head size 128, groups of up to 4 query heads:
+//     Q K^T and P V on the VALU (v_dot2_f32_bf16) instead of the matrix cores.
+//   FK_DECODE_LDS_STAGE  bf16, head size 128, plain decode: K/V tiles go from
+//     HBM straight to LDS (global_load_lds_dwordx4) through a two-stage ring
+//     per wave, so the next tile's loads are in flight while a tile is used.
 #include "fk_attn_tile.h"
 
 namespace fk {
 namespace {
+
+#ifdef FK_DECODE_VALU_TILE
+constexpr bool kValuBuild = true;
+#else
+constexpr bool kValuBuild = false;
+#endif
+#ifdef FK_DECODE_LDS_STAGE
+constexpr bool kLdsBuild = true;
+#else
+constexpr bool kLdsBuild = false;
+#endif
 
 struct DecodeParams {
   uint16_t* out;
@@ -252,6 +271,63 @@ __device__ __forceinline__ void store_new_row(const DecodeParams& P, int b, int 
   store_new_chunk<kFp8, D>(P, slot, kvh, lane, load_new_chunk<kFp8, D>(P, b, kvh, lane));
 }
 
+// ---------------------------------------------------------------------------
+// Helpers of the A/B tile forms (FK_DECODE_VALU_TILE, FK_DECODE_LDS_STAGE).
+// ---------------------------------------------------------------------------
+// DPP row reductions over the 16 lanes of each row: quad_perm [1,0,3,2] and
+// [2,3,0,1], then row_half_mirror and row_mirror; every lane gets the result.
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_f<0xB1>(v));
+  v = fmaxf(v, dpp_f<0x4E>(v));
+  v = fmaxf(v, dpp_f<0x141>(v));
+  return fmaxf(v, dpp_f<0x140>(v));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_f<0xB1>(v);
+  v += dpp_f<0x4E>(v);
+  v += dpp_f<0x141>(v);
+  return v + dpp_f<0x140>(v);
+}
+// c + a.lo * b.lo + a.hi * b.hi over bf16 pairs (v_dot2_f32_bf16).
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                         __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  const bf16x2_t p = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
+  return __builtin_bit_cast(uint32_t, p);
+}
+// Word v of lane src (ds_bpermute).
+__device__ __forceinline__ uint32_t lane_word(uint32_t v, int src) {
+  return static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src << 2, static_cast<int>(v)));
+}
+// 16 bytes from global memory straight into LDS: lane l writes at lds_addr +
+// 16 l.  Inline asm, so the compiler's wait-count pass does not track it; the
+// ring below orders it with explicit s_waitcnt.  M0 carries the LDS address
+// and is restored afterwards.
+__device__ __forceinline__ void lds_dma16(const uint8_t* src, uint32_t lds_addr) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, off\n\t"
+      "s_nop 0\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(src), "s"(lds_addr)
+      : "memory");
+}
+__device__ __forceinline__ uint32_t lds_addr_of(const uint8_t* p) {
+  return static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const uint8_t*)p));
+}
+constexpr int kStageBytes = 8192;  // one bf16 tile at head size 128: K 4 KiB, then V 4 KiB
+
 // Online-softmax state of one wave over the query heads of one virtual head,
 // and the tile loop that streams a token range [tok_begin, tok_end) of a
 // sequence through it (tok_begin a multiple of 16).  Lane (r, g) of the O
@@ -260,6 +336,10 @@ template <int kG, int D, bool kFp8, int U, bool kStore>
 struct WaveState {
   static constexpr int kKc = D / 32;  // K chunks per row (QK^T MFMAs per tile)
   static constexpr int kSl = D / 16;  // P.V slices; also dims per lane
+  // A/B forms (off in the shipped build).
+  static constexpr bool kValu = kValuBuild && !kFp8 && D == 128 && kG == 4;
+  static constexpr bool kLds = kLdsBuild && !kFp8 && D == 128 && !kStore;
+  uint8_t* ring;  // kLds: this wave's two LDS stages
   float m_run;  // running max of column r (same in the 4 lanes of a column)
   float l_run;  // this lane's share of the running sum of column r
   floatx4_t o[kSl];
@@ -293,6 +373,22 @@ struct WaveState {
         ftok0 = tok_begin + kTile * ((ctx - 1 - tok_begin) / kTile);
     }
     const bool head_ok = r < vh.ncols;
+    // kValu: lane (r, g) holds Q[head j][dims 32c + 8g .. +7] of the 4 heads, and
+    // (vm, vl) are head j's running max and this lane's share of its sum.
+    uint4 qv[kValu ? 4 : 1][kValu ? 4 : 1];
+    float vm[4], vl[4];
+    if constexpr (kValu) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint16_t* qp = P.q + b * P.q_row_stride + static_cast<int64_t>(vh.qbase + j) * D;
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          qv[j][c] = j < vh.ncols ? *reinterpret_cast<const uint4*>(qp + 32 * c + 8 * g)
+                                  : make_uint4(0, 0, 0, 0);
+        vm[j] = kNegInf;
+        vl[j] = 0.f;
+      }
+    }
     // Q^T operand: column r = query head qbase + r; dims permuted as the K loads.
     bf16x8_t qb[kKc];
     {
@@ -318,6 +414,72 @@ struct WaveState {
     // One 16-token tile: scores, online softmax update, P.V accumulation.
     auto process = [&](int tok0, int64_t page, const DTile<kFp8, D>& cur) {
       const int rel0 = tok0 + 4 * g - key_lo;
+      if constexpr (kValu) {
+        // Scores of token r for the 4 heads: dot products over the lane's 32
+        // dims, summed over the 4 lane groups (every lane of row r gets them).
+        const bool tok_ok = page >= 0 && static_cast<uint32_t>(tok0 + r - key_lo) < span;
+        float pj[4], alpha[4];
+        bool moved = false;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float a = 0.f;
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            a = dot2_bf16(cur.k[c].x, qv[j][c].x, a);
+            a = dot2_bf16(cur.k[c].y, qv[j][c].y, a);
+            a = dot2_bf16(cur.k[c].z, qv[j][c].z, a);
+            a = dot2_bf16(cur.k[c].w, qv[j][c].w, a);
+          }
+          a = pair_sum(a);
+          const float sj = (tok_ok && j < vh.ncols) ? a * s2 : kNegInf;
+          const float m_new = fmaxf(vm[j], row16_max(sj));
+          const float m_use = m_new == kNegInf ? 0.f : m_new;
+          alpha[j] = m_new == kNegInf ? 1.f : __builtin_amdgcn_exp2f(vm[j] - m_use);
+          moved |= alpha[j] != 1.f;
+          pj[j] = __builtin_amdgcn_exp2f(sj - m_use);
+          vl[j] = vl[j] * alpha[j] + pj[j];
+          vm[j] = m_new;
+        }
+        // o[e][j]: head j, dim 8r + e, summed over this lane's 4 tokens.
+        if (__ballot(moved) != 0) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) o[e][j] *= alpha[j];
+        }
+        // P[head j, token 4g + i] from lane 16g + 4g + i (heads packed in
+        // pairs), regrouped into token pairs for the dot products.
+        const uint32_t w01 = pack_bf16x2(pj[0], pj[1]), w23 = pack_bf16x2(pj[2], pj[3]);
+        uint32_t f01[4], f23[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          f01[i] = lane_word(w01, 20 * g + i);
+          f23[i] = lane_word(w23, 20 * g + i);
+        }
+        uint32_t pp[4][2];
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+          pp[0][k] = lo_pair(f01[2 * k], f01[2 * k + 1]);
+          pp[1][k] = hi_pair(f01[2 * k], f01[2 * k + 1]);
+          pp[2][k] = lo_pair(f23[2 * k], f23[2 * k + 1]);
+          pp[3][k] = hi_pair(f23[2 * k], f23[2 * k + 1]);
+        }
+        uint32_t vw[4][D / 32];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          v_words(cur, i, page >= 0 && static_cast<uint32_t>(rel0 + i) < span, vw[i]);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t v0l = lo_pair(vw[0][q], vw[1][q]), v1l = lo_pair(vw[2][q], vw[3][q]);
+          const uint32_t v0h = hi_pair(vw[0][q], vw[1][q]), v1h = hi_pair(vw[2][q], vw[3][q]);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            o[2 * q][j] = dot2_bf16(pp[j][1], v1l, dot2_bf16(pp[j][0], v0l, o[2 * q][j]));
+            o[2 * q + 1][j] = dot2_bf16(pp[j][1], v1h, dot2_bf16(pp[j][0], v0h, o[2 * q + 1][j]));
+          }
+        }
+        return;
+      }
       uint4 kc[kKc];
       k_chunks_d(cur, kc);
       const floatx4_t acc = qk_scores_n(kc, qb);
@@ -404,14 +566,33 @@ struct WaveState {
     };
     // Chunks of U tiles: issue all U tiles' loads, then consume them in order
     // (the compiler waits for tile u with vmcnt = loads issued after it).
-    for (int t0 = 0; t0 < ntiles; t0 += U) {
-      DTile<kFp8, D> buf[U];
-      int64_t pg[U];
-      fetch(t0, buf, pg);
-      consume(t0, buf, pg);
+    if constexpr (kLds) {
+      run_lds_ring(P, bt, b, kvh, tok_begin, ntiles, r, g, pc_idx, pc_page, process);
+    } else {
+      for (int t0 = 0; t0 < ntiles; t0 += U) {
+        DTile<kFp8, D> buf[U];
+        int64_t pg[U];
+        fetch(t0, buf, pg);
+        consume(t0, buf, pg);
+      }
     }
-    // Column sums of l over the 4 lane groups: every lane of column j holds l_j.
-    l_run = pair_sum(l_run);
+    if constexpr (kValu) {
+      // Sum O over the 4 lane groups: lanes of group 0 then hold the MFMA
+      // layout (column i = head i), which is what the writers read.
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[e][j] = pair_sum(o[e][j]);
+      float lt[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) lt[j] = row16_sum(vl[j]);
+      const int rr = r & 3;
+      m_run = rr == 0 ? vm[0] : rr == 1 ? vm[1] : rr == 2 ? vm[2] : vm[3];
+      l_run = rr == 0 ? lt[0] : rr == 1 ? lt[1] : rr == 2 ? lt[2] : lt[3];
+    } else {
+      // Column sums of l over the 4 lane groups: every lane of column j holds l_j.
+      l_run = pair_sum(l_run);
+    }
     // The wave that streamed position ctx - 1 writes b's row: at that position
     // (fused) or, for any other in-range slot, there (an orphan).
     if (kStore && ftok0 >= 0 && vh.first) {
@@ -419,6 +600,73 @@ struct WaveState {
       if (slot >= 0 && slot < (P.num_blocks << P.block_size_log2))
         store_new_chunk<kFp8, D>(P, slot, kvh, 16 * g + r, new_chunk);
     }
+  }
+
+  // kLds tile loop: tile t is staged in ring stage t % 2, tile t + 1's 8 loads
+  // are issued before tile t is waited for, read from LDS and processed.
+  // Tiles past the end re-read the last tile, so every wait is vmcnt(8).
+  template <typename Process>
+  __device__ __forceinline__ void run_lds_ring(const DecodeParams& P,
+                                               const int32_t* __restrict__ bt, int b, int kvh,
+                                               int tok_begin, int ntiles, int r, int g,
+                                               int& pc_idx, int64_t& pc_page, Process& process) {
+    const int lane = 16 * g + r;
+    const uint32_t ring_addr = __builtin_amdgcn_readfirstlane(lds_addr_of(ring));
+    const int64_t row_bytes = static_cast<int64_t>(P.num_kv_heads) * D * 2;
+    const int64_t head_off = static_cast<int64_t>(kvh) * D * 2;
+    auto issue = [&](int t, int stage) -> int64_t {
+      const int tok0 = tok_begin + kTile * min(t, ntiles - 1);
+      const int idx = tok0 >> P.block_size_log2;
+      if (idx != pc_idx) {
+        pc_page = page_of(P, bt, b, tok0);
+        pc_idx = idx;
+      }
+      const int64_t page = pc_page < 0 ? 0 : pc_page;
+      const int64_t slot0 = (page << P.block_size_log2) + (tok0 & ((1 << P.block_size_log2) - 1));
+      const uint8_t* krow = P.k_cache + (slot0 + r) * row_bytes + head_off;
+      const uint32_t base = ring_addr + stage * kStageBytes;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) lds_dma16(krow + (32 * c + 8 * g) * 2, base + 1024 * c);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        lds_dma16(P.v_cache + (slot0 + 4 * g + i) * row_bytes + head_off + 16 * r,
+                  base + 4096 + 1024 * i);
+      return pc_page;
+    };
+    auto read = [&](int stage, DTile<kFp8, D>& t) {
+      const uint8_t* p = ring + stage * kStageBytes + 16 * lane;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) t.k[c] = *reinterpret_cast<const uint4*>(p + 1024 * c);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint4 x = *reinterpret_cast<const uint4*>(p + 4096 + 1024 * i);
+        t.v[i][0] = x.x;
+        t.v[i][1] = x.y;
+        t.v[i][2] = x.z;
+        t.v[i][3] = x.w;
+      }
+    };
+    int64_t pg0 = issue(0, 0), pg1 = -1;
+    for (int t = 0; t < ntiles; t += 2) {
+      pg1 = issue(t + 1, 1);
+      asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+      {
+        DTile<kFp8, D> cur;
+        read(0, cur);
+        process(tok_begin + kTile * t, pg0, cur);
+      }
+      if (t + 1 >= ntiles) break;
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // stage 0's reads are done
+      pg0 = issue(t + 2, 0);
+      asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+      {
+        DTile<kFp8, D> cur;
+        read(1, cur);
+        process(tok_begin + kTile * (t + 1), pg1, cur);
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // stage 1's reads are done
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the ring is free for the next segment
   }
 
   // Normalised output rows of the virtual head for a sequence finished in place.
@@ -506,7 +754,10 @@ __global__ __launch_bounds__(NH * 64) void paged_decode_partition_kernel(
     // window's first key; one wholly before it streams nothing and leaves an
     // empty partial (max -inf, sum 0).
     const int lo = key_lo(P, ctx);
-    WaveState<kG, D, kFp8, U, kStore> st;
+    using WS = WaveState<kG, D, kFp8, U, kStore>;
+    WS st;
+    __shared__ __align__(16) uint8_t ring[WS::kLds ? NH * 2 * kStageBytes : 16];
+    st.ring = ring + wave * 2 * kStageBytes;
     st.run(P, block_tables, slot_mapping, b, vh, max(tok_begin, lo & ~(kTile - 1)), tok_end, ctx,
            lo, r, g);
     if (nparts == 1) {
@@ -580,7 +831,10 @@ __global__ __launch_bounds__(NH * 64) void paged_decode_balanced_kernel(
       const int mid = (lo + hi) >> 1;
       if (toff[mid] <= t_lo) lo = mid; else hi = mid;
     }
-    WaveState<kG, D, kFp8, U, kStore> st;
+    using WS = WaveState<kG, D, kFp8, U, kStore>;
+    WS st;
+    __shared__ __align__(16) uint8_t ring[WS::kLds ? NH * 2 * kStageBytes : 16];
+    st.ring = ring + wave * 2 * kStageBytes;
     for (int b = lo; b < batch && toff[b] < t_hi; ++b) {
       const int s_lo = max(t_lo, toff[b]) - toff[b];
       const int s_hi = min(t_hi, toff[b + 1]) - toff[b];
