@@ -177,8 +177,9 @@ int fk_paged_decode_plan(int64_t batch, int num_heads, int num_kv_heads, int hea
  *    plan's max_seq_len (a context longer than it makes the last partition
  *    longer); the balanced schedule reads the lengths on the device.
  * workspace: device memory of the plan's workspace_bytes, 16-byte aligned.
- * Supported: head_size 128; Hq/Hk in 1..16; block_size a power of two >= 16;
- *    batch <= 65535 (<= 8192 for the balanced schedule).
+ * Supported: head_size 64, 128 or 256; num_heads any multiple of num_kv_heads
+ *    (groups above 16 query heads take ceil(G / 16) waves per kv head); block_size a
+ *    power of two >= 16; batch <= 65535 (<= 8192 for the balanced schedule).
  * Replaces FlashAttnDecode.forward (flash_attn_decode.py:113-181). */
 int fk_paged_decode(void* out, int64_t out_row_stride, const void* q, int64_t q_row_stride,
                     const void* k_cache, const void* v_cache, int kv_dtype,
@@ -249,7 +250,7 @@ int fk_store_kvcache_convert(const void* key, int64_t key_row_stride, const void
  * (fastkernels/tasks/baseline/L1/flash_attn_prefill.py:28-74), the prefill half of
  * Attention._forward_mixed (attention_impl.py:682-731).
  * Sequence b owns query rows [cu_seqlens_q[b], cu_seqlens_q[b+1]) of q / out
- * ([rows, Hq*128] bf16, row strides in elements) and the first
+ * ([rows, Hq*head_size] bf16, row strides in elements) and the first
  * k_len = cu_seqlens_k[b+1] - cu_seqlens_k[b] tokens of its paged cache (block_tables
  * row b, layout as fk_paged_decode).  Query j of a chunk of q_len sees keys
  * [0, k_len - q_len + j] (causal, aligned to the end); a query with no visible key gets
@@ -259,9 +260,9 @@ int fk_store_kvcache_convert(const void* key, int64_t key_row_stride, const void
  * sinks: NULL or device fp32 [num_heads] attention-sink logits (s_aux), joining each
  * row's softmax denominator as in fk_paged_decode.
  * max_seqlen_q bounds every chunk (it sizes the grid; at most 65535 blocks of 32
- * query tokens, 128 for GQA group 1).  head_size 128; GQA groups up to 16; kv dtype
- * bf16 or fp8 e4m3fn (with k_scale / v_scale as in fk_paged_decode).  No workspace;
- * nothing is allocated. */
+ * query tokens, 128 for GQA group 1).  head_size 64, 128 or 256; num_heads any
+ * multiple of num_kv_heads; kv dtype bf16 or fp8 e4m3fn (with k_scale / v_scale as in
+ * fk_paged_decode).  No workspace; nothing is allocated. */
 int fk_paged_prefill(void* out, int64_t out_row_stride, const void* q, int64_t q_row_stride,
                      const void* k_cache, const void* v_cache, int kv_dtype, const float* k_scale,
                      const float* v_scale, const int32_t* block_tables, int64_t bt_row_stride,
@@ -272,7 +273,7 @@ int fk_paged_prefill(void* out, int64_t out_row_stride, const void* q, int64_t q
 
 /* The same attention over dense keys: FlashAttnPrefill.forward without a block table
  * (flash_attn_prefill.py:65-74; Attention._prefill_torch_from_tensors,
- * attention_impl.py:624-638).  key / value: [total_k, Hk*128] bf16 rows (strides in
+ * attention_impl.py:624-638).  key / value: [total_k, Hk*head_size] bf16 rows (strides in
  * elements; views of the qkv buffer allowed); sequence b's keys are rows
  * [cu_seqlens_k[b], cu_seqlens_k[b+1]).  window_left and sinks as fk_paged_prefill. */
 int fk_varlen_prefill(void* out, int64_t out_row_stride, const void* q, int64_t q_row_stride,
