@@ -1,17 +1,18 @@
 // MFMA tile helpers shared by the paged attention kernels (decode and prefill).
 //
-// A wave processes 16 keys x 16 query columns at a time.  Let r = lane % 16,
-// g = lane / 16.
-//   S[t, j] = K[t, :] . Q[j, :]   4 x v_mfma_f32_16x16x32_bf16 over D = 128:
-//     A = K tile (row t = r, 8 dims per lane), B = Q^T (column j = r), both
-//     with the same dim permutation, so lane (r, g) receives S[4g + i, r].
-//   O[j, d] += P[j, t] V[t, d]    8 x v_mfma_f32_16x16x16bf16_1k (one per
+// A wave processes 16 keys x 16 query columns at a time, at head size D = 64,
+// 128 or 256.  Let r = lane % 16, g = lane / 16.
+//   S[t, j] = K[t, :] . Q[j, :]   D / 32 x v_mfma_f32_16x16x32_bf16:
+//     A = K tile (row t = r, 8 dims per lane per MFMA), B = Q^T (column j = r),
+//     both with the same dim permutation, so lane (r, g) receives S[4g + i, r].
+//   O[j, d] += P[j, t] V[t, d]    D / 16 x v_mfma_f32_16x16x16bf16_1k (one per
 //     16-dim slice): A = P, whose layout (row j = r, tokens 4g..4g+3) is exactly
 //     the S layout above, so the probabilities never leave their lane; B = V
-//     (column = dim 8r + slice, tokens 4g..4g+3).  A lane loads 16 contiguous
-//     bytes (dims 8r..8r+7) of each of its 4 V rows and regroups the halves with
-//     byte permutes.
-// Lane (r, g) of the O accumulators holds O[column 4g + i][dims 8r .. 8r+7].
+//     (column = dim (D/16) r + slice, tokens 4g..4g+3).  A lane loads D / 16
+//     contiguous dims of each of its 4 V rows and regroups them with byte
+//     permutes.
+// Lane (r, g) of the O accumulators holds O[column 4g + i][dims (D/16) r ..
+// (D/16) r + D/16 - 1].
 #pragma once
 
 #include "fk_common.h"
@@ -23,7 +24,6 @@ typedef short short4_t __attribute__((ext_vector_type(4)));
 typedef float floatx4_t __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
-constexpr int kHead = 128;
 constexpr int kTile = 16;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegInf = -__builtin_huge_valf();
@@ -60,60 +60,22 @@ __device__ __forceinline__ uint32_t lo_pair(uint32_t a, uint32_t b) {
 __device__ __forceinline__ uint32_t hi_pair(uint32_t a, uint32_t b) {
   return __builtin_amdgcn_perm(b, a, 0x07060302u);  // (a >> 16) | (b & 0xffff0000)
 }
-__device__ __forceinline__ uint32_t word(const uint4& v, int i) {
-  return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
-}
 
-// 4 OCP e4m3fn bytes -> 4 bf16 (exact: every e4m3fn value is a bf16 value).
-__device__ __forceinline__ uint2 fp8x4_to_bf16x4(uint32_t w) {
+// 4 OCP e4m3fn bytes -> 4 bf16 holding float(x) * s rounded to nearest even:
+// the per-tensor fp8 dequant of _cast_kv_tile (triton_unified_attention.py:
+// 64-67), (data.to(float32) * scale).to(q.dtype).  With s = 1 it is exact (every
+// e4m3fn value is a bf16 value).
+__device__ __forceinline__ uint2 fp8x4_to_bf16x4(uint32_t w, float s) {
   const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8(w, false);
   const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8(w, true);
-  return make_uint2(hi_pair(__float_as_uint(lo[0]), __float_as_uint(lo[1])),
-                    hi_pair(__float_as_uint(hi[0]), __float_as_uint(hi[1])));
+  const bf16x2_t a = {static_cast<__bf16>(lo[0] * s), static_cast<__bf16>(lo[1] * s)};
+  const bf16x2_t b = {static_cast<__bf16>(hi[0] * s), static_cast<__bf16>(hi[1] * s)};
+  return make_uint2(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b));
 }
 
 // KV loads (plain cached loads: marking them non-temporal measured slower).
 __device__ __forceinline__ uint4 ld16(const uint8_t* p) { return *reinterpret_cast<const uint4*>(p); }
 __device__ __forceinline__ uint2 ld8(const uint8_t* p) { return *reinterpret_cast<const uint2*>(p); }
-
-// Raw registers one wave loads for one 16-token tile.  load_tile only issues
-// the loads; conversion and masking happen in the consumer, after the
-// prefetch of the following tile has been issued.
-template <bool kFp8>
-struct TileRegs;
-template <>
-struct TileRegs<false> {
-  uint4 k[4];  // dims 32c + 8g .. +8 of row r
-  uint4 v[4];  // rows 4g+i, dims 8r .. 8r+7
-};
-template <>
-struct TileRegs<true> {
-  uint4 k[2];  // 32 fp8 bytes of row r: dims 32g .. 32g+31
-  uint2 v[4];  // rows 4g+i, dims 8r .. 8r+7 (fp8 bytes)
-};
-
-// K operand chunks (bf16) of a loaded tile.
-__device__ __forceinline__ void k_chunks(const TileRegs<false>& t, uint4 (&k)[4]) {
-#pragma unroll
-  for (int c = 0; c < 4; ++c) k[c] = t.k[c];
-}
-__device__ __forceinline__ void k_chunks(const TileRegs<true>& t, uint4 (&k)[4]) {
-  // chunk c = dims 32g + 8c .. +8 = bytes 8c .. 8c+7 of the lane's 32.
-#pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    const uint4& src = t.k[c >> 1];
-    const uint32_t w0 = (c & 1) ? src.z : src.x;
-    const uint32_t w1 = (c & 1) ? src.w : src.y;
-    const uint2 lo = fp8x4_to_bf16x4(w0), hi = fp8x4_to_bf16x4(w1);
-    k[c] = make_uint4(lo.x, lo.y, hi.x, hi.y);
-  }
-}
-// V rows (bf16, dims 8r .. 8r+7) of a loaded tile.
-__device__ __forceinline__ uint4 v_row(const TileRegs<false>& t, int i) { return t.v[i]; }
-__device__ __forceinline__ uint4 v_row(const TileRegs<true>& t, int i) {
-  const uint2 lo = fp8x4_to_bf16x4(t.v[i].x), hi = fp8x4_to_bf16x4(t.v[i].y);
-  return make_uint4(lo.x, lo.y, hi.x, hi.y);
-}
 
 // Value of `x` held by lane 4g + i (g = this lane's row group), for the O
 // row 4g + i this lane accumulates.  Rows >= kG are padding and get lane i's.
@@ -133,16 +95,6 @@ __device__ __forceinline__ float row_value(float x, int g, int i) {
   return a;
 }
 
-// S tile of 16 keys x 16 query columns: acc[i] = S[key 4g + i, column r].
-__device__ __forceinline__ floatx4_t qk_scores(const uint4 (&kc)[4], const bf16x8_t (&qb)[4]) {
-  floatx4_t acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int c = 0; c < 4; ++c)
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kc[c]), qb[c],
-                                                 acc, 0, 0, 0);
-  return acc;
-}
-
 // P as the A operand: row r (query column), k = keys 4g..4g+3 (RNE bf16 pack).
 __device__ __forceinline__ short4_t p_operand(const float (&pr)[4]) {
   const bf16x2_t p01 = {static_cast<__bf16>(pr[0]), static_cast<__bf16>(pr[1])};
@@ -151,46 +103,11 @@ __device__ __forceinline__ short4_t p_operand(const float (&pr)[4]) {
       short4_t, make_uint2(__builtin_bit_cast(uint32_t, p01), __builtin_bit_cast(uint32_t, p23)));
 }
 
-// B operands of P.V for the 8 16-dim slices: vr[i] = V row 4g + i, dims
-// 8r .. 8r+7, regrouped so that slice d holds dim 8r + d of rows 4g .. 4g+3.
-__device__ __forceinline__ void v_operands(const uint4 (&vr)[4], short4_t (&vb)[8]) {
-#pragma unroll
-  for (int d = 0; d < 8; ++d) {
-    const int wi = d >> 1;
-    uint32_t b01, b23;
-    if (d & 1) {
-      b01 = hi_pair(word(vr[0], wi), word(vr[1], wi));
-      b23 = hi_pair(word(vr[2], wi), word(vr[3], wi));
-    } else {
-      b01 = lo_pair(word(vr[0], wi), word(vr[1], wi));
-      b23 = lo_pair(word(vr[2], wi), word(vr[3], wi));
-    }
-    vb[d] = __builtin_bit_cast(short4_t, make_uint2(b01, b23));
-  }
-}
-
-// o[d] += P . V for the 8 16-dim slices, with the V operands from v_operands.
-__device__ __forceinline__ void pv_accumulate(floatx4_t (&o)[8], short4_t pa,
-                                              const short4_t (&vb)[8]) {
-#pragma unroll
-  for (int d = 0; d < 8; ++d) o[d] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, vb[d], o[d], 0, 0, 0);
-}
-
-// o[d] += P . V straight from the V rows.
-__device__ __forceinline__ void pv_accumulate(floatx4_t (&o)[8], short4_t pa,
-                                              const uint4 (&vr)[4]) {
-  short4_t vb[8];
-  v_operands(vr, vb);
-  pv_accumulate(o, pa, vb);
-}
-
 // ---------------------------------------------------------------------------
-// Head-size-generic forms (the decode kernel's head sizes 64, 128, 256).  With
-// N = D / 32 K chunks per row and D / 16 dims per lane: S = K Q^T takes N
+// With N = D / 32 K chunks per row and D / 16 dims per lane: S = K Q^T takes N
 // 16x16x32 MFMAs; lane (r, g) holds V dims (D/16) r .. (D/16) r + D/16 - 1 of
 // rows 4g .. 4g+3 as NW = D / 32 words per row, and P.V takes D / 16 16x16x16
 // MFMAs, slice d accumulating dim (D/16) r + d of query column 4g + i in o[d][i].
-// At D = 128 these are exactly the functions above.
 // ---------------------------------------------------------------------------
 template <int N>
 __device__ __forceinline__ floatx4_t qk_scores_n(const uint4 (&kc)[N], const bf16x8_t (&qb)[N]) {
@@ -269,9 +186,11 @@ struct DTile {
   uint32_t v[4][kVWords];
 };
 
-// K operand chunks (bf16, dims as described at DTile) of a loaded tile.
+// K operand chunks (bf16, dims as described at DTile) of a loaded tile; fp8
+// bytes are dequantised with scale s (fp8x4_to_bf16x4).
 template <bool kFp8, int D>
-__device__ __forceinline__ void k_chunks_d(const DTile<kFp8, D>& t, uint4 (&kc)[D / 32]) {
+__device__ __forceinline__ void k_chunks_d(const DTile<kFp8, D>& t, uint4 (&kc)[D / 32],
+                                           float s = 1.f) {
   if constexpr (!kFp8) {
 #pragma unroll
     for (int c = 0; c < D / 32; ++c) kc[c] = t.k[c];
@@ -282,23 +201,24 @@ __device__ __forceinline__ void k_chunks_d(const DTile<kFp8, D>& t, uint4 (&kc)[
       const uint4& src = t.k[c >> 1];
       const uint32_t w0 = (c & 1) ? src.z : src.x;
       const uint32_t w1 = (c & 1) ? src.w : src.y;
-      const uint2 lo = fp8x4_to_bf16x4(w0), hi = fp8x4_to_bf16x4(w1);
+      const uint2 lo = fp8x4_to_bf16x4(w0, s), hi = fp8x4_to_bf16x4(w1, s);
       kc[c] = make_uint4(lo.x, lo.y, hi.x, hi.y);
     }
   }
 }
 
-// V row i of a loaded tile as D/32 words of bf16 pairs (zero when !keep).
+// V row i of a loaded tile as D/32 words of bf16 pairs (zero when !keep); fp8
+// bytes are dequantised with scale s.
 template <bool kFp8, int D>
 __device__ __forceinline__ void v_words(const DTile<kFp8, D>& t, int i, bool keep,
-                                        uint32_t (&w)[D / 32]) {
+                                        uint32_t (&w)[D / 32], float s = 1.f) {
   if constexpr (!kFp8) {
 #pragma unroll
     for (int q = 0; q < D / 32; ++q) w[q] = keep ? t.v[i][q] : 0u;
   } else {
 #pragma unroll
     for (int q = 0; q < D / 64; ++q) {
-      const uint2 x = fp8x4_to_bf16x4(t.v[i][q]);
+      const uint2 x = fp8x4_to_bf16x4(t.v[i][q], s);
       w[2 * q] = keep ? x.x : 0u;
       w[2 * q + 1] = keep ? x.y : 0u;
     }

@@ -20,8 +20,9 @@
 // (triton_unified_attention.py:741-776): M = max m_s, L = sum l_s e^(m_s - M),
 // O = sum o_s e^(m_s - M) / L, and O = 0 when L = 0.  fp8 KV pages are
 // dequantised per kv head as float(x) * scale, the per-tensor rule of
-// _cast_kv_tile (triton_unified_attention.py:51-67): k_scale is folded into the
-// score scale and v_scale into the output, which is algebraically the same.
+// _cast_kv_tile (triton_unified_attention.py:51-67): each K and V element is
+// float(x) * scale rounded to bf16 before it enters the MFMAs, as the reference
+// casts the scaled tile to the query dtype.
 // Head sizes D = 64, 128 and 256 (the reference builds FlashAttnDecode at 128,
 // and at 256 and 64 for Qwen3-Next and Whisper, L2/qwen3_next_attention.py:
 // 148-150, L2/whisper_attention.py:185-190) are template instantiations.
@@ -400,8 +401,10 @@ struct WaveState {
         qb[c] = __builtin_bit_cast(bf16x8_t, v);
       }
     }
-    float s2 = P.scale_log2;
-    if (kFp8 && P.k_scale) s2 *= P.k_scale[kvh];
+    const float s2 = P.scale_log2;
+    // fp8 dequant scales of this kv head (1 for bf16 pages or no scale tensor).
+    const float ks = (kFp8 && P.k_scale) ? P.k_scale[kvh] : 1.f;
+    const float vsc = (kFp8 && P.v_scale) ? P.v_scale[kvh] : 1.f;
 
     m_run = kNegInf;
     l_run = 0.f;
@@ -481,7 +484,7 @@ struct WaveState {
         return;
       }
       uint4 kc[kKc];
-      k_chunks_d(cur, kc);
+      k_chunks_d(cur, kc, ks);
       const floatx4_t acc = qk_scores_n(kc, qb);
       float s[4];
       float mt = kNegInf;
@@ -520,7 +523,7 @@ struct WaveState {
       uint32_t vw[4][D / 32];
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        v_words(cur, i, page >= 0 && static_cast<uint32_t>(rel0 + i) < span, vw[i]);
+        v_words(cur, i, page >= 0 && static_cast<uint32_t>(rel0 + i) < span, vw[i], vsc);
       short4_t vb[kSl];
       v_operands_w(vw, vb);
       pv_accumulate_n(o, pa, vb);
@@ -672,7 +675,6 @@ struct WaveState {
   // Normalised output rows of the virtual head for a sequence finished in place.
   __device__ __forceinline__ void write_final(const DecodeParams& P, int b, const VHead& vh,
                                               int r, int g) const {
-    const float vs = (kFp8 && P.v_scale) ? P.v_scale[vh.kvh] : 1.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int j = 4 * g + i;
@@ -681,7 +683,7 @@ struct WaveState {
         l = with_sink(l, row_value<kG>(m_run, g, i),
                       sink_log2(P, vh.qbase + (j < vh.ncols ? j : 0)));
       if (j >= kG || j >= vh.ncols) continue;
-      const float f = l > 0.f ? vs / l : 0.f;
+      const float f = l > 0.f ? 1.f / l : 0.f;
       uint32_t w[D / 32];
 #pragma unroll
       for (int d = 0; d < D / 32; ++d) {
@@ -702,11 +704,10 @@ struct WaveState {
     }
   }
 
-  // Unnormalised partial (O scaled by v_scale, and (max, sum)) into partial
-  // rows row0 + hq for the virtual head's query heads hq.
+  // Unnormalised partial (O, and (max, sum)) into partial rows row0 + hq for
+  // the virtual head's query heads hq.
   __device__ __forceinline__ void write_partial(const DecodeParams& P, int64_t row0,
                                                 const VHead& vh, int r, int g) const {
-    const float vs = (kFp8 && P.v_scale) ? P.v_scale[vh.kvh] : 1.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int j = 4 * g + i;
@@ -715,8 +716,7 @@ struct WaveState {
 #pragma unroll
       for (int q = 0; q < kSl / 4; ++q)
         *reinterpret_cast<float4*>(dst + 4 * q) =
-            make_float4(o[4 * q][i] * vs, o[4 * q + 1][i] * vs, o[4 * q + 2][i] * vs,
-                        o[4 * q + 3][i] * vs);
+            make_float4(o[4 * q][i], o[4 * q + 1][i], o[4 * q + 2][i], o[4 * q + 3][i]);
     }
     if (g == 0 && r < vh.ncols) {
       P.part_ml[(row0 + vh.qbase + r) * 2 + 0] = m_run;

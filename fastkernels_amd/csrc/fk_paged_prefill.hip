@@ -266,8 +266,11 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D)))) void paged_prefi
                                  : nullptr;
   // Dense keys: rows past the sequence's last key would run off the tensor.
   const int64_t row_cap = kPaged ? INT64_MAX : static_cast<int64_t>(k_start) + max(k_len, 1) - 1;
-  float s2 = P.scale_log2;
-  if (kFp8 && P.k_scale) s2 *= P.k_scale[h];
+  const float s2 = P.scale_log2;
+  // fp8 dequant scales of kv head h (1 for bf16 pages or no scale tensor): each
+  // K / V element enters the MFMAs as float(x) * scale rounded to bf16.
+  const float ks = (kFp8 && P.k_scale) ? P.k_scale[h] : 1.f;
+  const float vsc = (kFp8 && P.v_scale) ? P.v_scale[h] : 1.f;
 
   PageCache pc;
   // One query block of the work-group, start to finish (its own K/V stages).
@@ -349,7 +352,7 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D)))) void paged_prefi
     {
       lds_tile_k<kFp8, D>(buf, tt, r, g, ta);
       uint4 ka[D / 32];
-      k_chunks_d(ta, ka);
+      k_chunks_d(ta, ka, ks);
 #pragma unroll
       for (int nb = 0; nb < kCB; ++nb) sc_a[nb] = qk_scores_n(ka, qb[nb]);
     }
@@ -357,7 +360,7 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D)))) void paged_prefi
     {
       lds_tile_k<kFp8, D>(buf, tt + 1, r, g, tb);
       uint4 kb[D / 32];
-      k_chunks_d(tb, kb);
+      k_chunks_d(tb, kb, ks);
 #pragma unroll
       for (int nb = 0; nb < kCB; ++nb) sc_b[nb] = qk_scores_n(kb, qb[nb]);
     }
@@ -466,8 +469,8 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D)))) void paged_prefi
       uint32_t vwa[4][D / 32], vwb[4][D / 32];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        v_words(ta, i, !kMasked || (ok_a && tok0 + 4 * g + i < kend), vwa[i]);
-        v_words(tb, i, !kMasked || (ok_b && tok0 + kTile + 4 * g + i < kend), vwb[i]);
+        v_words(ta, i, !kMasked || (ok_a && tok0 + 4 * g + i < kend), vwa[i], vsc);
+        v_words(tb, i, !kMasked || (ok_b && tok0 + kTile + 4 * g + i < kend), vwb[i], vsc);
       }
       v_operands_w(vwa, vba);
       v_operands_w(vwb, vbb);
@@ -610,7 +613,6 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D)))) void paged_prefi
   for (; st < nstages; ++st) step(std::true_type{}, st);
   if (!active) return;  // from process_block: this wave has no queries here
 
-  const float vs = (kFp8 && P.v_scale) ? P.v_scale[h] : 1.f;
 #pragma unroll
   for (int nb = 0; nb < kCB; ++nb) {
 #pragma unroll
@@ -619,7 +621,7 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D)))) void paged_prefi
       float l = l_acc[nb][i];
       if (P.sinks) l = with_sink(l, row_value<16>(m_run[nb], g, i), P.sinks[hq] * kLog2e);
       if (jr >= q_len) continue;
-      const float f = l > 0.f ? vs / l : 0.f;
+      const float f = l > 0.f ? 1.f / l : 0.f;
       uint16_t* orow = P.out + static_cast<int64_t>(q_start + jr) * P.out_row_stride +
                        static_cast<int64_t>(hq) * D;
       if constexpr (!kFp8) {

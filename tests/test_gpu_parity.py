@@ -493,6 +493,25 @@ def test_paged_decode_fp8_small(cuda):
         assert_close(f32(run_decode(case, splits)), ref, FP8_TOL, FP8_TOL, f"fp8 splits={splits}")
 
 
+def test_paged_decode_fp8_dequant_rounding(cuda):
+    """One key per sequence: the output row is that key's V row, so each element must be
+    float(v8) * v_scale rounded to nearest even in bf16, bit for bit (_cast_kv_tile's
+    (data.to(float32) * scale).to(q.dtype), triton_unified_attention.py:64-67)."""
+    _flush("paged_decode fp8 dequant rounding")
+    case = workloads.c5_fp8_decode(cuda, batch=6, ctx_lens=[1] * 6, block_size=16, seed=57)
+    got = run_decode(case, 0)
+    vs = case.v_scale.float().cpu()
+    b, hq, d = case.q.shape
+    hk = case.v_cache.shape[2]
+    bt = case.block_tables.cpu()
+    v8 = case.v_cache.cpu()
+    for i in range(b):
+        row = v8[int(bt[i, 0]), 0]  # [Hk, D], token 0 of the sequence's first page
+        want = (row.float() * vs[:, None]).to(torch.bfloat16)  # RNE
+        want = want.repeat_interleave(hq // hk, dim=0)
+        assert torch.equal(got[i].cpu(), want), f"sequence {i}"
+
+
 @pytest.fixture(scope="module")
 def c5_outputs(cuda):
     """The full C5 launch (8 x 131072, fp8 KV with per-kv-head scales) under the balanced
@@ -506,9 +525,8 @@ def c5_outputs(cuda):
 @pytest.mark.parametrize("seqs", [(0, 1), (2, 3), (4, 5), (6, 7)])
 def test_paged_decode_fp8_c5(c5_outputs, seqs):
     """Every C5 sequence against the oracle (two per test, so each oracle leg stays well
-    inside the per-test timeout), for every schedule: the oracle rounds float(K8) *
-    k_scale to bf16 before the dot product (_cast_kv_tile), the kernel folds k_scale into
-    the score scale instead; both stay within the fp8 bar."""
+    inside the per-test timeout), for every schedule.  Kernel and oracle both round
+    float(x) * scale to bf16 before the products (_cast_kv_tile)."""
     case, outs = c5_outputs
     _flush(f"paged_decode C5 fp8: oracle for sequences {seqs}")
     seqs = list(seqs)
