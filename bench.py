@@ -819,8 +819,8 @@ def bench_table(args):
         q, kc, vc, bt, cu_q, cu_k, mq, flop = prefill_case(ql, kl, workloads.SEED + 11)
         pout = torch.empty_like(q)
         med, _ = time_call(lambda: ops.paged_prefill(pout, q, kc, vc, bt, cu_q, cu_k, mq,
-                                                     128 ** -0.5), iters=20, warmup=3,
-                           flush=flush)
+                                                     128 ** -0.5, max_seqlen_k=max(kl)),
+                           iters=20, warmup=3, flush=flush)
         row = {"config": "prefill", "op": f"paged_prefill bf16 Hq=32 Hk=8 {label}",
                "us_median": round(med * 1e3, 2), "flop": flop,
                "TFLOPs": round(flop / (med * 1e-3) / 1e12, 1),

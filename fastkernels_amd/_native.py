@@ -75,11 +75,12 @@ _SIGNATURES = {
                                       c_int64, c_int64, c_int, c_int, c_int, c_int, c_void_p]),
     "fk_paged_prefill": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_int,
                                  c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_void_p,
-                                 c_int64, c_int64, c_int, c_int, c_int, c_int, c_int64, c_float,
-                                 c_int, c_int, c_void_p, c_void_p]),
+                                 c_int64, c_int64, c_int64, c_int, c_int, c_int, c_int, c_int64,
+                                 c_float, c_int, c_int, c_void_p, c_void_p]),
     "fk_varlen_prefill": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64,
-                                  c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_int64, c_int,
-                                  c_int, c_int, c_float, c_int, c_int, c_void_p, c_void_p]),
+                                  c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_int64,
+                                  c_int64, c_int, c_int, c_int, c_float, c_int, c_int, c_void_p,
+                                  c_void_p]),
     "fk_store_kvcache_convert": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_int, c_void_p,
                                          c_void_p, c_int, c_void_p, c_int, c_int64, c_int64,
                                          c_int64, c_void_p]),

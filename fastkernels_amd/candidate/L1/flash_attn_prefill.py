@@ -101,6 +101,8 @@ class FlashAttnPrefill(nn.Module):
         sinks = self._sinks(s_aux, q.device)
         if softmax_scale is None:
             softmax_scale = self.sm_scale
+        # A bound on every sequence's key count; it only chooses the launch shape.
+        mk = int(max_seqlen_k) if max_seqlen_k is not None else 0
         total = q.shape[0]
         q3 = q.view(total, self.num_heads, self.head_dim)
         if cu_seqlens_q.dtype != torch.int32:
@@ -120,12 +122,12 @@ class FlashAttnPrefill(nn.Module):
             vs = self._scale_vec(v_scale, hk, q.device)
             call = torch.ops.fastkernels_amd.paged_prefill if compiling else ops.paged_prefill
             call(out3, q3, k, v, block_table, cu_seqlens_q, cu_seqlens_k, int(max_seqlen_q),
-                 float(softmax_scale), ks, vs, causal, window_left, sinks)
+                 float(softmax_scale), ks, vs, causal, window_left, sinks, mk)
         else:
             hk = k.shape[-2] if k.dim() == 3 else k.shape[-1] // self.head_dim
             k3 = k.view(k.shape[0], hk, self.head_dim)
             v3 = v.view(v.shape[0], hk, self.head_dim)
             call = torch.ops.fastkernels_amd.varlen_prefill if compiling else ops.varlen_prefill
             call(out3, q3, k3, v3, cu_seqlens_q, cu_seqlens_k, int(max_seqlen_q),
-                 float(softmax_scale), causal, window_left, sinks)
+                 float(softmax_scale), causal, window_left, sinks, mk)
         return out

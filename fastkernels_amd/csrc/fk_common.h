@@ -17,6 +17,8 @@ namespace fk {
 // ---------------------------------------------------------------------------
 int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
+// Compute units of the current device (queried once per device).
+int num_cus();
 
 #define FK_REQUIRE(cond, ...)                                  \
   do {                                                         \

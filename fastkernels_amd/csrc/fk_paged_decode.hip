@@ -1048,20 +1048,6 @@ constexpr int kMaxWavesPerGroup = 8;     // virtual heads (waves) per work-group
 constexpr int kPartQuant = 64;           // fixed-partition granularity in tokens
 constexpr int kMaxBalancedBatch = 8192;  // tile prefix sums live in LDS
 
-int num_cus() {
-  static int cached = -1;
-  if (cached < 0) {
-    int dev = 0;
-    hipDeviceProp_t prop;
-    if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&prop, dev) == hipSuccess &&
-        prop.multiProcessorCount > 0)
-      cached = prop.multiProcessorCount;
-    else
-      cached = 256;  // MI355X
-    (void)hipGetLastError();
-  }
-  return cached;
-}
 
 // Waves per kv head (column blocks of up to 16 query heads) and virtual heads.
 int col_blocks(int num_heads, int num_kv_heads) {

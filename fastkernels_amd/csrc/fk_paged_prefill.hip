@@ -29,6 +29,17 @@
 // last visible key.  In a causal chunk with few cached keys before it, a
 // work-group takes two query blocks, one near the chunk's end and one near its
 // start, so that the work-groups are even.
+//
+// Key split.  When the launch has too few work-groups to give every SIMD two
+// waves (a single prompt: 2048 tokens over 8 kv heads make 256 work-groups
+// after pairing), the work-group has 8 waves in two halves of 4: both halves
+// take the same queries, the first half streams the first half of the block's
+// key stages and the second half the rest, each through its own LDS buffers,
+// in lock step (one barrier per stage; the half with fewer stages passes empty
+// barriers).  At the end the second half leaves its (O, max, sum) in LDS and
+// the first half merges them with the log-sum-exp rule before it writes the
+// rows.  Each block's serial chain of stages halves, and every SIMD runs two
+// waves.
 #include <type_traits>
 
 #include "fk_attn_tile.h"
@@ -167,6 +178,14 @@ __device__ __forceinline__ uint32_t lds_addr_of(const uint8_t* p) {
       reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const uint8_t*)p));
 }
 
+// Floats one wave of the key split's second half leaves in LDS for its partner:
+// O (kCB x D/16 MFMA tiles of 4 floats per lane), the row sums (kCB x 4 per
+// lane) and the column maxima (kCB per lane).
+template <int D, int kCB>
+constexpr int split_exchange_floats() {
+  return kCB * (D / 16) * 64 * 4 + kCB * 64 * 4 + kCB * 64;
+}
+
 // Tile tt (rows 16 tt .. 16 tt + 15) of a staged buffer in the register layout
 // a global load of the tile would give (DTile, fk_attn_tile.h): the K rows (t.k)
 // and, for fp8 stages, the V rows (t.v), read separately so that a caller can
@@ -218,16 +237,22 @@ __device__ __forceinline__ short4_t lds_v_slice(const uint8_t* buf, int tt, int 
 // times qs = kPrefillWaves / hw blocks of kQTokens query tokens (a group larger
 // than kPrefillWaves heads spans hsplit work-groups).  All waves share the K/V
 // stages; each walks the tiles up to its own last visible key.
-template <bool kFp8, bool kPaged, int D>
-__global__ __launch_bounds__(kPrefillWaves * 64)
+// kKS = 2: the key split (8 waves; head sizes up to 128).
+template <bool kFp8, bool kPaged, int D, int kKS>
+__global__ __launch_bounds__(kKS * kPrefillWaves * 64)
 __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D)))) void paged_prefill_kernel(
     PrefillParams P, const int32_t* __restrict__ block_tables,
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_k) {
   using S = Stage<kFp8, D>;
+  static_assert(kKS == 1 || (kKS == 2 && D <= 128), "key split: two halves, head size <= 128");
   constexpr int kCB = col_blocks_for(D);  // 16-query column blocks per wave
   constexpr int kQT = 16 * kCB;           // query tokens per wave
-  __shared__ __align__(16) uint8_t lds0[S::kBytes];
-  __shared__ __align__(16) uint8_t lds1[S::kBytes];
+  // Stage buffers (two per half), and with the key split the exchange area
+  // that reuses them once the last stage is consumed.
+  constexpr int kXFloats = split_exchange_floats<D, kCB>();
+  constexpr int kStageAll = kKS * 2 * S::kBytes;
+  constexpr int kXBytes = kKS > 1 ? kPrefillWaves * kXFloats * 4 : 0;
+  __shared__ __align__(16) uint8_t lds_all[kStageAll > kXBytes ? kStageAll : kXBytes];
   // Grid: x = kv head (x hsplit), y = sequence, z = query block.  The block
   // index varies slowest, so the work-groups that have work (low z when blocks
   // are paired) are dispatched first and spread over every CU.
@@ -254,7 +279,11 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D)))) void paged_prefi
   const bool paired = P.causal && k_len - q_len < q_len;
   const int x = static_cast<int>(blockIdx.z);
   if (x >= (paired ? (nqb + 1) / 2 : nqb)) return;  // uniform over the work-group
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wave_id = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int half = kKS > 1 ? wave_id / kPrefillWaves : 0;  // key-split half
+  const int wave = wave_id - half * kPrefillWaves;          // role within the half
+  uint8_t* const lds0 = lds_all + half * 2 * S::kBytes;
+  uint8_t* const lds1 = lds0 + S::kBytes;
   const int lane = threadIdx.x & 63;
   const int r = lane & 15;
   const int g = lane >> 4;
@@ -272,24 +301,32 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D)))) void paged_prefi
   const float ks = (kFp8 && P.k_scale) ? P.k_scale[h] : 1.f;
   const float vsc = (kFp8 && P.v_scale) ? P.v_scale[h] : 1.f;
 
+  const int win = P.window_left;
+  // Stages [st0, nstages) of 32 keys that query block qblk streams: up to its
+  // last query's last key, from its first query's window start.
+  auto block_stages = [&](int qblk, int& st0, int& nstages) {
+    const int jw0 = qblk * wg_tokens;
+    const int kend_wg = max(0, min(k_len, offset + min(jw0 + wg_tokens, q_len)));
+    const int kbeg_wg = win >= 0 ? max(0, offset + jw0 - win) : 0;
+    nstages = (kend_wg + kStageKeys - 1) / kStageKeys;
+    st0 = min(kbeg_wg / kStageKeys, nstages);
+  };
+
   PageCache pc;
-  // One query block of the work-group, start to finish (its own K/V stages).
+  // One query block of the work-group, start to finish (its own K/V stages);
+  // with the key split both halves take it, each streaming half its stages.
   auto process_block = [&](int qblk) {
   const int jw0 = qblk * wg_tokens;  // first query of the work-group
   const int j0 = jw0 + (wave / hw) * kQT;
   // Waves without queries (past the chunk, or past the group) still stage.
   const bool active = j0 < q_len && head < P.gqa && wave < qs * hw;
-  // Keys [0, kend) cover every query of this wave's block; kend_wg every query
-  // of the work-group.
+  // Keys [0, kend) cover every query of this wave's block.
   const int kend = active ? max(0, min(k_len, offset + min(j0 + kQT, q_len))) : 0;
-  const int kend_wg = max(0, min(k_len, offset + min(jw0 + wg_tokens, q_len)));
   // Sliding window: query j sees keys from offset + j - win.  kbeg (this wave's
-  // first query) and kbeg_wg (the work-group's) bound the keys from below; the
-  // work-group starts streaming at the stage holding kbeg_wg, and a stage at or
-  // after khead (the last query's window start) is inside every query's window.
-  const int win = P.window_left;
+  // first query) bounds the keys from below; the work-group starts streaming at
+  // the stage holding its first query's (block_stages), and a stage at or after
+  // khead (the last query's window start) is inside every query's window.
   const int kbeg = (win >= 0 && active) ? max(0, offset + j0 - win) : 0;
-  const int kbeg_wg = win >= 0 ? max(0, offset + jw0 - win) : 0;
   const int khead = (win >= 0 && active) ? offset + min(j0 + kQT, q_len) - 1 - win : 0;
 
   // Q^T operands: column r of block nb = query j0 + 16 nb + r.
@@ -328,9 +365,18 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D)))) void paged_prefi
   // Tiles every query of the block sees in full need no mask: keys up to
   // offset + j0 (query j0's last key), inside [0, kend).
   const int nfull = active ? max(0, min(kend, offset + j0 + 1)) / kTile : 0;
-  const int nstages = (kend_wg + kStageKeys - 1) / kStageKeys;
-  const int st0 = min(kbeg_wg / kStageKeys, nstages);  // first stage the work-group streams
+  int st0, nstages;  // the block's stages
+  block_stages(qblk, st0, nstages);
   const int tbeg = kbeg / kTile;                      // this wave's first tile
+  // This half's stages [st_lo, st_hi) and the barriers every wave passes
+  // (nsteps): the whole range, or with the key split its first or second half.
+  int st_lo = st0, st_hi = nstages, nsteps = nstages - st0;
+  if constexpr (kKS > 1) {
+    const int n0 = (nstages - st0 + 1) / 2;
+    st_lo = half == 0 ? st0 : st0 + n0;
+    st_hi = half == 0 ? st0 + n0 : nstages;
+    nsteps = n0;
+  }
 
   // Two 16-key tiles (tiles tt, tt + 1 of `buf`, keys tok0 .. tok0 + 31):
   // scores, one online-softmax update per query column for the 32 keys, P.V.
@@ -521,7 +567,9 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D)))) void paged_prefi
     lane_off[i] = static_cast<uint32_t>((row & 15) * rb + head_off + 16 * q);
   }
   auto stage_load = [&](int st, uint8_t* buf) {
-    const uint32_t buf_addr = lds_addr_of(buf);
+    // Wave-uniform (the buffer is the half's); readfirstlane keeps it in an SGPR
+    // for M0 where the compiler cannot prove it.
+    const uint32_t buf_addr = __builtin_amdgcn_readfirstlane(lds_addr_of(buf));
     // First rows of the stage's tiles: page lookups once per tile, wave-uniform.
     int64_t row0[kStageTiles];
 #pragma unroll
@@ -591,26 +639,87 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D)))) void paged_prefi
   // One step: wait for stage st's loads (every thread's, through the barrier,
   // which also frees the other buffer), issue stage st + 1's, consume stage st.
   // The unmasked and masked stages run in separate loops; every wave passes
-  // exactly nstages - st0 barriers whichever loops it is in.
+  // exactly nsteps barriers whichever loops it is in.
   auto step = [&](auto masked, int st) {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     uint8_t* cur_buf = (st & 1) ? lds1 : lds0;
     uint8_t* next_buf = (st & 1) ? lds0 : lds1;
-    if (st + 1 < nstages) stage_load(st + 1, next_buf);
+    if (st + 1 < st_hi) stage_load(st + 1, next_buf);
     stage_compute(masked, st, cur_buf);
   };
   // Stages [st0, nstages): under a window, a masked head (keys some query's
   // window starts after), then the unmasked stages, then the masked rest.
-  if (st0 < nstages) stage_load(st0, (st0 & 1) ? lds1 : lds0);
-  int st = st0;
+  if (st_lo < st_hi) stage_load(st_lo, (st_lo & 1) ? lds1 : lds0);
+  int st = st_lo;
   const int head_end = win >= 0 ? max(st0, (khead + kStageKeys - 1) / kStageKeys) : st0;
 #pragma unroll 1
-  for (; st < nstages && st < head_end; ++st) step(std::true_type{}, st);
+  for (; st < st_hi && st < head_end; ++st) step(std::true_type{}, st);
 #pragma unroll 1
-  for (; st < nstages && stage_unmasked(st); ++st) step(std::false_type{}, st);
+  for (; st < st_hi && stage_unmasked(st); ++st) step(std::false_type{}, st);
 #pragma unroll 1
-  for (; st < nstages; ++st) step(std::true_type{}, st);
+  for (; st < st_hi; ++st) step(std::true_type{}, st);
+  // Row maxima and sums of the rows this lane holds (row 4g + i of block nb).
+  float m_row[kCB][4], l_row[kCB][4];
+#pragma unroll
+  for (int nb = 0; nb < kCB; ++nb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      m_row[nb][i] = row_value<16>(m_run[nb], g, i);
+      l_row[nb][i] = l_acc[nb][i];
+    }
+  if constexpr (kKS > 1) {
+#pragma unroll 1
+    for (int k = st_hi - st_lo; k < nsteps; ++k) {  // the shorter half's empty steps
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+    }
+    __syncthreads();  // every wave is done with the stage buffers
+    // Exchange area of this wave role: O tiles, row sums, column maxima.
+    float* const xo = reinterpret_cast<float*>(lds_all) + wave * kXFloats;
+    float* const xl = xo + kCB * (D / 16) * 64 * 4;
+    float* const xm = xl + kCB * 64 * 4;
+    if (half == 1 && active) {
+#pragma unroll
+      for (int nb = 0; nb < kCB; ++nb) {
+#pragma unroll
+        for (int d = 0; d < D / 16; ++d)
+          *reinterpret_cast<floatx4_t*>(xo + ((nb * (D / 16) + d) * 64 + lane) * 4) = o[nb][d];
+        *reinterpret_cast<floatx4_t*>(xl + (nb * 64 + lane) * 4) = l_acc[nb];
+        xm[nb * 64 + lane] = m_run[nb];
+      }
+    }
+    __syncthreads();
+    if (half == 1) return;  // from process_block: the first half writes the rows
+    if (active) {
+      // Log-sum-exp merge of the two halves, row by row (reduce_segments'
+      // rule): M = max(m_a, m_b), O = O_a 2^(m_a - M) + O_b 2^(m_b - M), and
+      // the same for the sums; a half that saw no key (max -inf) weighs 0.
+#pragma unroll
+      for (int nb = 0; nb < kCB; ++nb) {
+        const float mb_col = xm[nb * 64 + lane];
+        const floatx4_t lb = *reinterpret_cast<const floatx4_t*>(xl + (nb * 64 + lane) * 4);
+        float wa[4], wb[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float ma = m_row[nb][i];
+          const float mb = row_value<16>(mb_col, g, i);
+          const float mx = fmaxf(ma, mb);
+          wa[i] = ma == kNegInf ? 0.f : __builtin_amdgcn_exp2f(ma - mx);
+          wb[i] = mb == kNegInf ? 0.f : __builtin_amdgcn_exp2f(mb - mx);
+          m_row[nb][i] = mx;
+          l_row[nb][i] = l_row[nb][i] * wa[i] + lb[i] * wb[i];
+        }
+#pragma unroll
+        for (int d = 0; d < D / 16; ++d) {
+          const floatx4_t ob =
+              *reinterpret_cast<const floatx4_t*>(xo + ((nb * (D / 16) + d) * 64 + lane) * 4);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) o[nb][d][i] = o[nb][d][i] * wa[i] + ob[i] * wb[i];
+        }
+      }
+    }
+  }
   if (!active) return;  // from process_block: this wave has no queries here
 
 #pragma unroll
@@ -618,8 +727,8 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D)))) void paged_prefi
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int jr = j0 + 16 * nb + 4 * g + i;  // query row this lane holds
-      float l = l_acc[nb][i];
-      if (P.sinks) l = with_sink(l, row_value<16>(m_run[nb], g, i), P.sinks[hq] * kLog2e);
+      float l = l_row[nb][i];
+      if (P.sinks) l = with_sink(l, m_row[nb][i], P.sinks[hq] * kLog2e);
       if (jr >= q_len) continue;
       const float f = l > 0.f ? 1.f / l : 0.f;
       uint16_t* orow = P.out + static_cast<int64_t>(q_start + jr) * P.out_row_stride +
@@ -664,21 +773,29 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D)))) void paged_prefi
 }
 
 template <bool FP8, bool PAGED, int D>
-void launch_prefill(const PrefillParams& P, dim3 grid, const int32_t* bt, const int32_t* cu_q,
-                    const int32_t* cu_k, hipStream_t stream) {
-  hipLaunchKernelGGL((paged_prefill_kernel<FP8, PAGED, D>), grid, dim3(kPrefillWaves * 64), 0,
+void launch_prefill(bool split, const PrefillParams& P, dim3 grid, const int32_t* bt,
+                    const int32_t* cu_q, const int32_t* cu_k, hipStream_t stream) {
+  if constexpr (D <= 128) {
+    if (split) {
+      hipLaunchKernelGGL((paged_prefill_kernel<FP8, PAGED, D, 2>), grid,
+                         dim3(2 * kPrefillWaves * 64), 0, stream, P, bt, cu_q, cu_k);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((paged_prefill_kernel<FP8, PAGED, D, 1>), grid, dim3(kPrefillWaves * 64), 0,
                      stream, P, bt, cu_q, cu_k);
 }
 
 template <int D>
-void launch_prefill_d(bool paged, bool fp8, const PrefillParams& P, dim3 grid, const int32_t* bt,
-                      const int32_t* cu_q, const int32_t* cu_k, hipStream_t stream) {
+void launch_prefill_d(bool paged, bool fp8, bool split, const PrefillParams& P, dim3 grid,
+                      const int32_t* bt, const int32_t* cu_q, const int32_t* cu_k,
+                      hipStream_t stream) {
   if (!paged)
-    launch_prefill<false, false, D>(P, grid, nullptr, cu_q, cu_k, stream);
+    launch_prefill<false, false, D>(split, P, grid, nullptr, cu_q, cu_k, stream);
   else if (fp8)
-    launch_prefill<true, true, D>(P, grid, bt, cu_q, cu_k, stream);
+    launch_prefill<true, true, D>(split, P, grid, bt, cu_q, cu_k, stream);
   else
-    launch_prefill<false, true, D>(P, grid, bt, cu_q, cu_k, stream);
+    launch_prefill<false, true, D>(split, P, grid, bt, cu_q, cu_k, stream);
 }
 
 }  // namespace
@@ -692,8 +809,8 @@ int prefill_entry(const char* name, bool paged, void* out, int64_t out_row_strid
                   int64_t v_row_bytes, int kv_dtype, const float* k_scale, const float* v_scale,
                   const int32_t* block_tables, int64_t bt_row_stride,
                   const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int64_t batch,
-                  int64_t max_seqlen_q, int num_heads, int num_kv_heads, int head_size,
-                  int block_size, int64_t num_blocks, float scale, int causal,
+                  int64_t max_seqlen_q, int64_t max_seqlen_k, int num_heads, int num_kv_heads,
+                  int head_size, int block_size, int64_t num_blocks, float scale, int causal,
                   int window_left, const float* sinks, void* stream) {
   FK_REQUIRE(batch >= 0 && batch <= 65535, "%s: batch %lld out of range [0, 65535]", name,
              (long long)batch);
@@ -703,6 +820,8 @@ int prefill_entry(const char* name, bool paged, void* out, int64_t out_row_strid
              "%s: a sliding window needs causal attention (window_size = (left, 0))", name);
   FK_REQUIRE(max_seqlen_q >= 0 && max_seqlen_q <= (int64_t(1) << 30),
              "%s: max_seqlen_q %lld out of range", name, (long long)max_seqlen_q);
+  FK_REQUIRE(max_seqlen_k >= 0, "%s: max_seqlen_k %lld must be >= 0 (0: unknown)", name,
+             (long long)max_seqlen_k);
   FK_REQUIRE(num_heads > 0 && num_kv_heads > 0 && num_heads % num_kv_heads == 0,
              "%s: num_heads %d must be a positive multiple of num_kv_heads %d", name, num_heads,
              num_kv_heads);
@@ -765,10 +884,20 @@ int prefill_entry(const char* name, bool paged, void* out, int64_t out_row_strid
                   static_cast<unsigned>(qblocks));
   hipStream_t s = as_stream(stream);
   const bool fp8 = kv_dtype == FK_DTYPE_FP8_E4M3FN;
+  // Key split when the grid (before pairing) holds at most two 4-wave
+  // work-groups per CU: pairing then leaves at most one, so one wave per SIMD.
+  // Key split when the 4-wave launch would leave SIMDs with one wave: fewer
+  // work-groups than two per CU.  A causal sequence with fewer cached keys than
+  // twice its queries pairs its blocks two per work-group; max_seqlen_k (a
+  // bound on every sequence's keys, 0 = unknown) tells whether that can happen.
+  const bool may_pair = causal && max_seqlen_k > 0 && max_seqlen_k < 2 * max_seqlen_q;
+  const int64_t wgs = static_cast<int64_t>(num_kv_heads) * hsplit * batch *
+                      (may_pair ? (qblocks + 1) / 2 : qblocks);
+  const bool split = head_size <= 128 && wgs < 2LL * num_cus();
   switch (head_size) {
-    case 64: launch_prefill_d<64>(paged, fp8, P, grid, block_tables, cu_seqlens_q, cu_seqlens_k, s); break;
-    case 256: launch_prefill_d<256>(paged, fp8, P, grid, block_tables, cu_seqlens_q, cu_seqlens_k, s); break;
-    default: launch_prefill_d<128>(paged, fp8, P, grid, block_tables, cu_seqlens_q, cu_seqlens_k, s); break;
+    case 64: launch_prefill_d<64>(paged, fp8, split, P, grid, block_tables, cu_seqlens_q, cu_seqlens_k, s); break;
+    case 256: launch_prefill_d<256>(paged, fp8, split, P, grid, block_tables, cu_seqlens_q, cu_seqlens_k, s); break;
+    default: launch_prefill_d<128>(paged, fp8, split, P, grid, block_tables, cu_seqlens_q, cu_seqlens_k, s); break;
   }
   return check_launch(name);
 }
@@ -781,8 +910,8 @@ extern "C" int fk_paged_prefill(void* out, int64_t out_row_stride, const void* q
                                 int kv_dtype, const float* k_scale, const float* v_scale,
                                 const int32_t* block_tables, int64_t bt_row_stride,
                                 const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
-                                int64_t batch, int64_t max_seqlen_q, int num_heads,
-                                int num_kv_heads, int head_size, int block_size,
+                                int64_t batch, int64_t max_seqlen_q, int64_t max_seqlen_k,
+                                int num_heads, int num_kv_heads, int head_size, int block_size,
                                 int64_t num_blocks, float scale, int causal, int window_left,
                                 const float* sinks, void* stream) {
   const int64_t row = static_cast<int64_t>(num_kv_heads) * head_size *
@@ -790,20 +919,21 @@ extern "C" int fk_paged_prefill(void* out, int64_t out_row_stride, const void* q
   return fk::prefill_entry("fk_paged_prefill", true, out, out_row_stride, q, q_row_stride,
                            k_cache, row, v_cache, row, kv_dtype, k_scale, v_scale, block_tables,
                            bt_row_stride, cu_seqlens_q, cu_seqlens_k, batch, max_seqlen_q,
-                           num_heads, num_kv_heads, head_size, block_size, num_blocks, scale,
-                           causal, window_left, sinks, stream);
+                           max_seqlen_k, num_heads, num_kv_heads, head_size, block_size,
+                           num_blocks, scale, causal, window_left, sinks, stream);
 }
 
 extern "C" int fk_varlen_prefill(void* out, int64_t out_row_stride, const void* q,
                                  int64_t q_row_stride, const void* key, int64_t key_row_stride,
                                  const void* value, int64_t value_row_stride,
                                  const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
-                                 int64_t batch, int64_t max_seqlen_q, int num_heads,
-                                 int num_kv_heads, int head_size, float scale, int causal,
-                                 int window_left, const float* sinks, void* stream) {
+                                 int64_t batch, int64_t max_seqlen_q, int64_t max_seqlen_k,
+                                 int num_heads, int num_kv_heads, int head_size, float scale,
+                                 int causal, int window_left, const float* sinks,
+                                 void* stream) {
   return fk::prefill_entry("fk_varlen_prefill", false, out, out_row_stride, q, q_row_stride, key,
                            key_row_stride * 2, value, value_row_stride * 2, FK_DTYPE_BF16,
                            nullptr, nullptr, nullptr, 0, cu_seqlens_q, cu_seqlens_k, batch,
-                           max_seqlen_q, num_heads, num_kv_heads, head_size, 16, 0, scale, causal,
-                           window_left, sinks, stream);
+                           max_seqlen_q, max_seqlen_k, num_heads, num_kv_heads, head_size, 16, 0,
+                           scale, causal, window_left, sinks, stream);
 }

@@ -27,6 +27,24 @@ int check_launch(const char* what) {
   return FK_OK;
 }
 
+int num_cus() {
+  static int cached[64] = {};  // per device; 0 = not yet queried
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    (void)hipGetLastError();
+    return 256;  // MI355X
+  }
+  if (cached[dev] == 0) {
+    hipDeviceProp_t prop;
+    int n = 256;
+    if (hipGetDeviceProperties(&prop, dev) == hipSuccess && prop.multiProcessorCount > 0)
+      n = prop.multiProcessorCount;
+    (void)hipGetLastError();
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
 }  // namespace fk
 
 extern "C" int fk_version(void) { return 100; }  // 0.1.0

@@ -462,12 +462,13 @@ def paged_prefill(out: torch.Tensor, q: torch.Tensor, k_cache: torch.Tensor,
                   cu_seqlens_k: torch.Tensor, max_seqlen_q: int, softmax_scale: float,
                   k_scale: torch.Tensor | None = None, v_scale: torch.Tensor | None = None,
                   causal: bool = True, window_left: int = -1,
-                  sinks: torch.Tensor | None = None) -> None:
+                  sinks: torch.Tensor | None = None, max_seqlen_k: int = 0) -> None:
     """Causal prefill over paged K/V into ``out`` ([tokens, Hq, D] bf16): sequence b's
     queries q[cu_q[b]:cu_q[b+1]] attend to its first cu_k[b+1]-cu_k[b] cached tokens,
     aligned to their end (flash_attn_varlen_func with block_table, seqused_k).
     window_left >= 0: each query sees its last window_left + 1 positions; sinks
-    (float32 [Hq]) join each row's softmax denominator."""
+    (float32 [Hq]) join each row's softmax denominator.  max_seqlen_k bounds every
+    sequence's key count (0: unknown); it only chooses the launch shape."""
     _check_prefill(out, q, cu_seqlens_q, cu_seqlens_k)
     _check_prefill_extras(q, causal, window_left, sinks)
     if k_cache.dim() != 4 or v_cache.shape != k_cache.shape or k_cache.shape[3] != q.shape[2]:
@@ -494,18 +495,18 @@ def paged_prefill(out: torch.Tensor, q: torch.Tensor, k_cache: torch.Tensor,
                  _ptr(k_cache), _ptr(v_cache),
                  _native.FK_DTYPE_FP8_E4M3FN if k_cache.dtype == _FP8 else _native.FK_DTYPE_BF16,
                  _ptr(k_scale), _ptr(v_scale), _ptr(block_table), block_table.stride(0),
-                 _ptr(cu_seqlens_q), _ptr(cu_seqlens_k), batch, int(max_seqlen_q), q.shape[1],
-                 hk, q.shape[2], bs, nb, float(softmax_scale), int(bool(causal)),
-                 int(window_left), _ptr(sinks), _stream(q))
+                 _ptr(cu_seqlens_q), _ptr(cu_seqlens_k), batch, int(max_seqlen_q),
+                 int(max_seqlen_k), q.shape[1], hk, q.shape[2], bs, nb, float(softmax_scale),
+                 int(bool(causal)), int(window_left), _ptr(sinks), _stream(q))
 
 
 def varlen_prefill(out: torch.Tensor, q: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
                    cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor, max_seqlen_q: int,
                    softmax_scale: float, causal: bool = True, window_left: int = -1,
-                   sinks: torch.Tensor | None = None) -> None:
+                   sinks: torch.Tensor | None = None, max_seqlen_k: int = 0) -> None:
     """Causal prefill over dense keys: key/value [total_k, Hk, D] bf16 (rows may be strided
-    views), sequence b's keys being rows cu_k[b]..cu_k[b+1].  window_left and sinks as
-    in :func:`paged_prefill`."""
+    views), sequence b's keys being rows cu_k[b]..cu_k[b+1].  window_left, sinks and
+    max_seqlen_k as in :func:`paged_prefill`."""
     _check_prefill(out, q, cu_seqlens_q, cu_seqlens_k)
     _check_prefill_extras(q, causal, window_left, sinks)
     if key.dim() != 3 or value.shape != key.shape or key.shape[2] != q.shape[2]:
@@ -520,9 +521,9 @@ def varlen_prefill(out: torch.Tensor, q: torch.Tensor, key: torch.Tensor, value:
         return
     _native.call("fk_varlen_prefill", _ptr(out), out.stride(0), _ptr(q), q.stride(0), _ptr(key),
                  key.stride(0), _ptr(value), value.stride(0), _ptr(cu_seqlens_q),
-                 _ptr(cu_seqlens_k), batch, int(max_seqlen_q), q.shape[1], key.shape[1],
-                 q.shape[2], float(softmax_scale), int(bool(causal)), int(window_left),
-                 _ptr(sinks), _stream(q))
+                 _ptr(cu_seqlens_k), batch, int(max_seqlen_q), int(max_seqlen_k), q.shape[1],
+                 key.shape[1], q.shape[2], float(softmax_scale), int(bool(causal)),
+                 int(window_left), _ptr(sinks), _stream(q))
 
 
 def paged_decode_phases(out, q, k_cache, v_cache, block_table, cache_seqlens, softmax_scale,
@@ -636,10 +637,11 @@ _LIB.define("qk_norm_rope_store(Tensor positions, Tensor(a!) query, Tensor(b!) k
 _LIB.define("paged_prefill(Tensor(a!) out, Tensor q, Tensor k_cache, Tensor v_cache, "
             "Tensor block_table, Tensor cu_seqlens_q, Tensor cu_seqlens_k, int max_seqlen_q, "
             "float softmax_scale, Tensor? k_scale=None, Tensor? v_scale=None, bool causal=True, "
-            "int window_left=-1, Tensor? sinks=None) -> ()")
+            "int window_left=-1, Tensor? sinks=None, int max_seqlen_k=0) -> ()")
 _LIB.define("varlen_prefill(Tensor(a!) out, Tensor q, Tensor key, Tensor value, "
             "Tensor cu_seqlens_q, Tensor cu_seqlens_k, int max_seqlen_q, float softmax_scale, "
-            "bool causal=True, int window_left=-1, Tensor? sinks=None) -> ()")
+            "bool causal=True, int window_left=-1, Tensor? sinks=None, "
+            "int max_seqlen_k=0) -> ()")
 _LIB.define("silu_and_mul(Tensor! result, Tensor input) -> ()")
 _LIB.define("merge_attn_states(Tensor(a!) output, Tensor prefix_output, Tensor prefix_lse, "
             "Tensor suffix_output, Tensor suffix_lse, Tensor(b!)? output_lse) -> ()")

@@ -260,28 +260,34 @@ int fk_store_kvcache_convert(const void* key, int64_t key_row_stride, const void
  * sinks: NULL or device fp32 [num_heads] attention-sink logits (s_aux), joining each
  * row's softmax denominator as in fk_paged_decode.
  * max_seqlen_q bounds every chunk (it sizes the grid; at most 65535 blocks of 32
- * query tokens, 128 for GQA group 1).  head_size 64, 128 or 256; num_heads any
+ * query tokens, 128 for GQA group 1).  max_seqlen_k (flash_attn_varlen_func's
+ * max_seqlen_k): a bound on every sequence's key count, or 0 if unknown; it only
+ * chooses the launch shape (with few query blocks, each block's keys are split over
+ * two halves of a work-group and merged).  head_size 64, 128 or 256; num_heads any
  * multiple of num_kv_heads; kv dtype bf16 or fp8 e4m3fn (with k_scale / v_scale as in
  * fk_paged_decode).  No workspace; nothing is allocated. */
 int fk_paged_prefill(void* out, int64_t out_row_stride, const void* q, int64_t q_row_stride,
                      const void* k_cache, const void* v_cache, int kv_dtype, const float* k_scale,
                      const float* v_scale, const int32_t* block_tables, int64_t bt_row_stride,
                      const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int64_t batch,
-                     int64_t max_seqlen_q, int num_heads, int num_kv_heads, int head_size,
-                     int block_size, int64_t num_blocks, float scale, int causal,
-                     int window_left, const float* sinks, void* stream);
+                     int64_t max_seqlen_q, int64_t max_seqlen_k, int num_heads,
+                     int num_kv_heads, int head_size, int block_size, int64_t num_blocks,
+                     float scale, int causal, int window_left, const float* sinks,
+                     void* stream);
 
 /* The same attention over dense keys: FlashAttnPrefill.forward without a block table
  * (flash_attn_prefill.py:65-74; Attention._prefill_torch_from_tensors,
  * attention_impl.py:624-638).  key / value: [total_k, Hk*head_size] bf16 rows (strides in
  * elements; views of the qkv buffer allowed); sequence b's keys are rows
- * [cu_seqlens_k[b], cu_seqlens_k[b+1]).  window_left and sinks as fk_paged_prefill. */
+ * [cu_seqlens_k[b], cu_seqlens_k[b+1]).  max_seqlen_k, window_left and sinks as
+ * fk_paged_prefill. */
 int fk_varlen_prefill(void* out, int64_t out_row_stride, const void* q, int64_t q_row_stride,
                       const void* key, int64_t key_row_stride, const void* value,
                       int64_t value_row_stride, const int32_t* cu_seqlens_q,
                       const int32_t* cu_seqlens_k, int64_t batch, int64_t max_seqlen_q,
-                      int num_heads, int num_kv_heads, int head_size, float scale, int causal,
-                      int window_left, const float* sinks, void* stream);
+                      int64_t max_seqlen_k, int num_heads, int num_kv_heads, int head_size,
+                      float scale, int causal, int window_left, const float* sinks,
+                      void* stream);
 
 /* Per-head q/k RMSNorm (optional) + rotary embedding + store_kvcache in one launch:
  * the attention block between the qkv projection and the decode

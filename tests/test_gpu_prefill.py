@@ -43,14 +43,15 @@ def _case(cuda, q_lens, k_lens, hq=32, hk=8, bs=16, seed=70, fp8=False, extra_pa
         kc, vc = kc.to(torch.bfloat16), vc.to(torch.bfloat16)
     t = lambda x: None if x is None else x.to(cuda)  # noqa: E731
     return dict(q=q.to(cuda), kc=kc.to(cuda), vc=vc.to(cuda), bt=bt.to(cuda), cu_q=cu_q.to(cuda),
-                cu_k=cu_k.to(cuda), max_q=max(q_lens) if q_lens else 0, ks=t(ks), vs=t(vs),
-                scale=d ** -0.5)
+                cu_k=cu_k.to(cuda), max_q=max(q_lens) if q_lens else 0,
+                max_k=max(k_lens) if k_lens else 0, ks=t(ks), vs=t(vs), scale=d ** -0.5)
 
 
 def _run(c, causal=True, window_left=-1, sinks=None):
     out = torch.full_like(c["q"], float("nan"))
     ops.paged_prefill(out, c["q"], c["kc"], c["vc"], c["bt"], c["cu_q"], c["cu_k"], c["max_q"],
-                      c["scale"], c["ks"], c["vs"], causal, window_left, sinks)
+                      c["scale"], c["ks"], c["vs"], causal, window_left, sinks,
+                      max_seqlen_k=c["max_k"])
     torch.cuda.synchronize()
     return out
 
@@ -365,3 +366,46 @@ def test_candidate_prefill_head_size_256(cuda):
               block_table=c["bt"])
     torch.cuda.synchronize()
     _close(out, _oracle(c), 1e-2, "candidate d=256")
+
+
+# The kernel splits each query block's keys between two halves of an 8-wave work-group
+# when the grid (sized by max_seqlen_q) would have fewer than two work-groups per CU,
+# and streams them in one pass otherwise.  The same inputs with max_seqlen_q at its
+# exact value and raised to 20000 (a larger bound is allowed; the extra blocks have no
+# work) take the two forms.
+SPLIT_CASES = [
+    # (label, q_lens, k_lens, kwargs)
+    ("prompt 700 (paired blocks)", [700], [700], {}),
+    ("chunk 96 over 3000", [96], [3000], {}),
+    ("mixed", [1, 257, 33], [900, 257, 2000], {"bs": 64}),
+    ("fp8", [130, 5], [1000, 77], {"fp8": True, "bs": 64}),
+    ("head 64, group 8", [300, 64], [300, 1000], {"hq": 64, "hk": 8, "d": 64}),
+]
+
+
+@pytest.mark.parametrize("label,q_lens,k_lens,kw", SPLIT_CASES)
+def test_paged_prefill_key_split_and_single_pass(cuda, label, q_lens, k_lens, kw):
+    _flush(f"prefill key split vs single pass: {label}")
+    c = _case(cuda, q_lens, k_lens, seed=300 + len(label), **kw)
+    tol = 3e-2 if kw.get("fp8") else 1e-2
+    ref = _oracle(c)
+    split = _run(c)
+    whole = _run(dict(c, max_q=20000))
+    _close(split, ref, tol, f"{label}: key split")
+    _close(whole, ref, tol, f"{label}: single pass")
+    assert torch.equal(_run(dict(c, max_q=20000)), whole), f"{label}: single pass repeat"
+    assert torch.equal(_run(c), split), f"{label}: key split repeat"
+
+
+@pytest.mark.parametrize("window_left", [0, 31, 200])
+def test_paged_prefill_key_split_window_and_sinks(cuda, window_left):
+    """Sliding window and sinks through both halves of the key split (the first
+    half's stages may all lie before a query's window) and the single pass."""
+    _flush(f"prefill key split window={window_left}")
+    c = _case(cuda, [400, 9], [1200, 300], bs=16, seed=310 + window_left)
+    g = torch.Generator().manual_seed(311)
+    sinks = (2 * torch.randn(32, generator=g)).float().to(cuda)
+    ref = _oracle(c, window_left=window_left, sinks=sinks)
+    _close(_run(c, window_left=window_left, sinks=sinks), ref, 1e-2, "key split")
+    _close(_run(dict(c, max_q=20000), window_left=window_left, sinks=sinks), ref, 1e-2,
+           "single pass")
