@@ -157,27 +157,19 @@ __device__ __forceinline__ float sink_log2(const DecodeParams& P, int hq) {
 // are unconditional so that every pipeline stage has the same number of loads
 // in flight and the compiler can wait for one stage with vmcnt(N) instead of
 // draining the queue; masked pages and tiles past the end load a safe page and
-// are discarded by the consumer.  Fused store: tile row j (-1: none) is read
-// from the new K/V row (nk / nv, this kv head's slice) instead of the cache,
-// by selecting each lane's address, so the loop has no extra control flow.
+// are discarded by the consumer.
 template <bool kFp8, int D>
 __device__ __forceinline__ void load_tile(const DecodeParams& P, int64_t page, int kvh, int tok0,
-                                          int r, int g, DTile<kFp8, D>& t, int j = -1,
-                                          const uint8_t* nk = nullptr,
-                                          const uint8_t* nv = nullptr) {
+                                          int r, int g, DTile<kFp8, D>& t) {
   const int bs_mask = (1 << P.block_size_log2) - 1;
   const int64_t slot0 = (page << P.block_size_log2) + (tok0 & bs_mask);
   constexpr int kElem = kFp8 ? 1 : 2;
   const int64_t row_bytes = static_cast<int64_t>(P.num_kv_heads) * D * kElem;
   const int64_t head_off = static_cast<int64_t>(kvh) * D * kElem;
   const uint8_t* krow = P.k_cache + (slot0 + r) * row_bytes + head_off;
-  if (r == j) krow = nk;
   const uint8_t* vrow[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    vrow[i] = P.v_cache + (slot0 + 4 * g + i) * row_bytes + head_off;
-    if (4 * g + i == j) vrow[i] = nv;
-  }
+  for (int i = 0; i < 4; ++i) vrow[i] = P.v_cache + (slot0 + 4 * g + i) * row_bytes + head_off;
   if constexpr (!kFp8) {
     // Per instruction: 16 rows x 64 contiguous bytes.
 #pragma unroll
@@ -193,41 +185,23 @@ __device__ __forceinline__ void load_tile(const DecodeParams& P, int64_t page, i
 }
 
 // ---------------------------------------------------------------------------
-// Fused store.  Sequence b's new token is at position p = ctx - 1.  The wave
-// that streams p's tile (the kv head's first column block) loads b's new K/V
-// row up front and, when slot_mapping[b] is the slot of p in b's block table
-// (the decode step), uses it in place of the cache row at p, then writes it to
-// the cache after its tile loop, so no load waits for the store.  A slot that
-// is not p's ("orphan") is written by that same wave, or, when no wave streams
-// p (no context), by a designated work-group; the order of an orphan write
-// against other reads of its slot is unspecified.  Other column blocks of the
-// kv head read p from the new row too and write nothing.
+// Fused store (fk_store_paged_decode).  Sequence b's new token is at position
+// ctx - 1, in the sequence's last tile.  Each wave that streams that tile
+// writes its kv head's slice of b's new K/V row to slot_mapping[b] (when in
+// range) right before it fetches the tile, and then reads position ctx - 1
+// from the cache like any other, as the reference's store-then-decode does: a
+// wave's vector memory operations complete in order and its lanes share one
+// L1, so its own writes are visible to its later loads.  The row is loaded at
+// the start of the segment, so the write does not wait for it.  Every column
+// block of a kv head writes the same bytes.  Sequences with no context are
+// written by a designated work-group.  A slot that other work-groups read in
+// the same launch (one that is not position ctx - 1 of its own sequence) is
+// written in no defined order against those reads.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ int64_t slot_of(const DecodeParams& P, const void* __restrict__ sm,
                                            int b) {
   return P.slot_is_i64 ? static_cast<const int64_t*>(sm)[b]
                        : static_cast<int64_t>(static_cast<const int32_t*>(sm)[b]);
-}
-
-// The raw 32-bit words of slot_mapping[b] (both halves of an int64 entry, or
-// the int32 entry twice), loaded at computed indices without a branch so that
-// they issue with the wave's first page lookups; slot_value() combines them
-// behind a compiler barrier, so the wait for them lands where the slot is used.
-struct SlotWords {
-  int32_t lo, hi;
-};
-__device__ __forceinline__ SlotWords slot_words(const DecodeParams& P,
-                                                const void* __restrict__ sm, int b) {
-  const int32_t* s32 = static_cast<const int32_t*>(sm);
-  const int w = P.slot_is_i64;  // 0 or 1
-  const int i = b << w;
-  return SlotWords{s32[i], s32[i + w]};
-}
-__device__ __forceinline__ int64_t slot_value(const DecodeParams& P, SlotWords s) {
-  asm volatile("" : "+s"(s.lo), "+s"(s.hi));
-  const int64_t wide = static_cast<int64_t>(
-      (static_cast<uint64_t>(static_cast<uint32_t>(s.hi)) << 32) | static_cast<uint32_t>(s.lo));
-  return P.slot_is_i64 ? wide : static_cast<int64_t>(s.lo);
 }
 
 // In-range slot of sequence b's new row, or -1.
@@ -345,33 +319,23 @@ struct WaveState {
   float l_run;  // this lane's share of the running sum of column r
   floatx4_t o[kSl];
 
-  // kStore: when the segment ends at the context end (tok_end == ctx) and
-  // slot_mapping[b] is the slot of position ctx - 1, that position's K/V are
-  // read from sequence b's new row instead of the cache (load_tile's row j),
-  // and the row (one 16-byte chunk per lane, loaded up front) is written to the
-  // cache after the loop by the kv head's first column block, so no load waits
-  // for the store.
   // Keys below key_lo (the sliding window's start) are masked; tok_begin is
-  // the start of the tile holding key_lo or later.
+  // the start of the tile holding key_lo or later.  kStore: a segment that ends
+  // at the context end writes b's new row before it fetches the last tile.
   __device__ __forceinline__ void run(const DecodeParams& P, const int32_t* __restrict__ bt,
                                       const void* __restrict__ sm, int b, const VHead& vh,
                                       int tok_begin, int tok_end, int ctx, int key_lo, int r,
                                       int g) {
     const int kvh = vh.kvh;
-    SlotWords sw{-1, -1};
     uint4 new_chunk = make_uint4(0, 0, 0, 0);  // this lane's chunk of b's new row
-    const uint8_t* nk = nullptr;  // b's new K / V row, kv head kvh
-    const uint8_t* nv = nullptr;
-    int ftok0 = -1;  // first token of the tile holding ctx - 1, if this segment ends there
+    int64_t new_slot = -1;
+    int t_store = -1;  // the tile (from tok_begin) holding position ctx - 1
     if constexpr (kStore) {
-      constexpr int kElem = kFp8 ? 1 : 2;
-      const int64_t head_off = static_cast<int64_t>(kvh) * D * kElem;
-      nk = P.new_k + b * P.new_k_stride + head_off;
-      nv = P.new_v + b * P.new_v_stride + head_off;
-      new_chunk = load_new_chunk<kFp8, D>(P, b, kvh, 16 * g + r);
-      sw = slot_words(P, sm, b);
-      if (tok_end == ctx && ctx > tok_begin)
-        ftok0 = tok_begin + kTile * ((ctx - 1 - tok_begin) / kTile);
+      if (tok_end == ctx && ctx > tok_begin) {  // wave-uniform
+        new_chunk = load_new_chunk<kFp8, D>(P, b, kvh, 16 * g + r);
+        new_slot = valid_slot(P, sm, b);
+        t_store = (ctx - 1 - tok_begin) / kTile;
+      }
     }
     const bool head_ok = r < vh.ncols;
     // kValu: lane (r, g) holds Q[head j][dims 32c + 8g .. +7] of the 4 heads, and
@@ -546,19 +510,7 @@ struct WaveState {
           pc_idx = idx;
         }
         pg[u] = pc_page;
-        int j = -1;
-        if constexpr (kStore) {
-          // Fused when b's slot is that of position ctx - 1: in this tile's page
-          // (a tile never spans pages), at offset (ctx - 1) mod block_size.
-          // Branch-free (selects), so the load sequence stays one block.  (Peeling
-          // the last chunk, the only one that can hold ctx - 1, out of the loop
-          // measured no faster.)
-          const int64_t want = (pg[u] << P.block_size_log2) +
-                               ((ctx - 1) & ((1 << P.block_size_log2) - 1));
-          const bool hit = tok0 == ftok0 && pg[u] >= 0 && slot_value(P, sw) == want;
-          j = hit ? ctx - 1 - tok0 : -1;
-        }
-        load_tile<kFp8, D>(P, pg[u] < 0 ? 0 : pg[u], kvh, tok0, r, g, buf[u], j, nk, nv);
+        load_tile<kFp8, D>(P, pg[u] < 0 ? 0 : pg[u], kvh, tok0, r, g, buf[u]);
       }
     };
     auto consume = [&](int t0, const DTile<kFp8, D>(&buf)[U], const int64_t(&pg)[U]) {
@@ -573,6 +525,10 @@ struct WaveState {
       run_lds_ring(P, bt, b, kvh, tok_begin, ntiles, r, g, pc_idx, pc_page, process);
     } else {
       for (int t0 = 0; t0 < ntiles; t0 += U) {
+        if constexpr (kStore) {
+          if (t_store >= t0 && t_store < t0 + U && new_slot >= 0)
+            store_new_chunk<kFp8, D>(P, new_slot, kvh, 16 * g + r, new_chunk);
+        }
         DTile<kFp8, D> buf[U];
         int64_t pg[U];
         fetch(t0, buf, pg);
@@ -595,13 +551,6 @@ struct WaveState {
     } else {
       // Column sums of l over the 4 lane groups: every lane of column j holds l_j.
       l_run = pair_sum(l_run);
-    }
-    // The wave that streamed position ctx - 1 writes b's row: at that position
-    // (fused) or, for any other in-range slot, there (an orphan).
-    if (kStore && ftok0 >= 0 && vh.first) {
-      const int64_t slot = slot_value(P, sw);
-      if (slot >= 0 && slot < (P.num_blocks << P.block_size_log2))
-        store_new_chunk<kFp8, D>(P, slot, kvh, 16 * g + r, new_chunk);
     }
   }
 
@@ -853,8 +802,8 @@ __global__ __launch_bounds__(NH * 64) void paged_decode_balanced_kernel(
       }
     }
   }
-  // Sequences without tiles (no context) have no wave that streams their
-  // last position: group w writes the rows of those with b = w mod G.
+  // Sequences without tiles (no context) have no range that holds their last
+  // position: group w writes the rows of those with b = w mod G.
   if (kStore && vh.first) {
     for (int b = w; b < batch; b += P.num_groups) {
       if (toff[b + 1] != toff[b]) continue;

@@ -315,15 +315,16 @@ int fk_qk_norm_rope_store(const int64_t* positions, void* query, int64_t q_row_s
  * (fastkernels/tasks/baseline/L2/attention_impl.py:313-363, :436-450), which calls
  * StoreKVCache (store_kvcache.py:16-35) and then FlashAttnDecode.forward
  * (flash_attn_decode.py:113-181).
- * key/value: [batch, Hk, 128] of the cache element type (bf16 or fp8 e4m3fn), row
- * strides in elements, 16-byte aligned.  slot_mapping: int32 or int64 [batch].  All
- * other arguments as fk_paged_decode (same plan and workspace).
- * Decode-step layout: slot_mapping[b] is negative (not stored) or the slot of position
- * ctx_lens[b] - 1 in block_tables[b] (engine.py:5020-5024).  Then the cache and the
- * output equal fk_store_kvcache followed by fk_paged_decode, bit for bit: the wave
- * that streams that position writes the row and takes it from registers.  Other
- * in-range slots are written too, but the output of a sequence that reads such a
- * slot in the same call is unspecified. */
+ * key/value: [batch, Hk, head_size] of the cache element type (bf16 or fp8 e4m3fn),
+ * row strides in elements, 16-byte aligned.  slot_mapping: int32 or int64 [batch];
+ * negative or out-of-range entries are not stored.  All other arguments as
+ * fk_paged_decode (same plan and workspace).
+ * Decode-step layout: slot_mapping[b] is the slot of position ctx_lens[b] - 1 in
+ * block_tables[b] (engine.py:5020-5024).  Then the cache and the output equal
+ * fk_store_kvcache followed by fk_paged_decode, bit for bit: the waves that stream
+ * that position write the row just before they load it.  A slot that another
+ * sequence reads in the same call is written too, but that sequence's output is
+ * unspecified. */
 int fk_store_paged_decode(void* out, int64_t out_row_stride, const void* q, int64_t q_row_stride,
                           const void* key, int64_t key_row_stride, const void* value,
                           int64_t value_row_stride, const void* slot_mapping, int slot_is_i64,
