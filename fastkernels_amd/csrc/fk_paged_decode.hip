@@ -984,14 +984,18 @@ __global__ __launch_bounds__(kMergeWaves * 64) void paged_decode_balanced_reduce
                 sink_log2(P, hq), lane);
 }
 
-// Tuning knob (compile-time): tiles per load set at head sizes up to 128 (at
-// 256 a tile's loads fill as many registers as two tiles do at 128, so one).
+// Tuning knobs (compile-time): tiles per load set for bf16 pages at head sizes
+// up to 128 (at 256 a tile's loads fill as many registers as two tiles do at
+// 128, so one), and for fp8 pages.
 #ifndef FK_DECODE_CHUNK
 #define FK_DECODE_CHUNK 2
 #endif
-template <int D>
+#ifndef FK_DECODE_CHUNK_FP8
+#define FK_DECODE_CHUNK_FP8 2
+#endif
+template <int D, bool kFp8>
 constexpr int chunk_tiles() {
-  return D >= 256 ? 1 : FK_DECODE_CHUNK;
+  return D >= 256 ? 1 : kFp8 ? FK_DECODE_CHUNK_FP8 : FK_DECODE_CHUNK;
 }
 constexpr int kMaxWavesPerGroup = 8;     // virtual heads (waves) per work-group
 constexpr int kPartQuant = 64;           // fixed-partition granularity in tokens
@@ -1151,7 +1155,7 @@ int prepare(const char* name, Launch& L, void* out, int64_t out_row_stride, cons
 
 template <int NH, int G, int D, bool FP8, bool ST>
 void launch_main_st(const Launch& L, hipStream_t stream) {
-  constexpr int U = chunk_tiles<D>();
+  constexpr int U = chunk_tiles<D, FP8>();
   if (L.balanced) {
     const size_t lds = static_cast<size_t>(L.P.batch + 1) * sizeof(int32_t);
     hipLaunchKernelGGL((paged_decode_balanced_kernel<NH, G, D, FP8, U, ST>), L.grid,
