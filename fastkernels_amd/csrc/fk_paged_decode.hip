@@ -61,6 +61,15 @@
 namespace fk {
 namespace {
 
+// Lock step: the waves of a work-group stream the same token rows (one kv head
+// each), and meet at a barrier every kSyncChunks load sets, so that a row's
+// kv-head slices are read together rather than drifting apart (the younger
+// wave on each SIMD falls behind by several µs otherwise).  0 disables it.
+#ifndef FK_DECODE_SYNC_CHUNKS
+#define FK_DECODE_SYNC_CHUNKS 2
+#endif
+constexpr int kSyncChunks = FK_DECODE_SYNC_CHUNKS;
+
 #ifdef FK_DECODE_VALU_TILE
 constexpr bool kValuBuild = true;
 #else
@@ -322,10 +331,22 @@ struct WaveState {
   // Keys below key_lo (the sliding window's start) are masked; tok_begin is
   // the start of the tile holding key_lo or later.  kStore: a segment that ends
   // at the context end writes b's new row before it fetches the last tile.
+  // idle: a wave past the last virtual head; it loads nothing and only keeps
+  // the work-group's barrier count.
   __device__ __forceinline__ void run(const DecodeParams& P, const int32_t* __restrict__ bt,
                                       const void* __restrict__ sm, int b, const VHead& vh,
                                       int tok_begin, int tok_end, int ctx, int key_lo, int r,
-                                      int g) {
+                                      int g, bool idle) {
+    constexpr bool kSync = kSyncChunks > 0 && !kLds;
+    if (idle) {
+      if constexpr (kSync) {
+        const int n = (tok_end - tok_begin + kTile - 1) / kTile;
+#pragma unroll 1
+        for (int t0 = 0, c = 0; t0 < n; t0 += U, ++c)
+          if (c % kSyncChunks == 0) __builtin_amdgcn_s_barrier();
+      }
+      return;
+    }
     const int kvh = vh.kvh;
     uint4 new_chunk = make_uint4(0, 0, 0, 0);  // this lane's chunk of b's new row
     int64_t new_slot = -1;
@@ -524,7 +545,12 @@ struct WaveState {
     if constexpr (kLds) {
       run_lds_ring(P, bt, b, kvh, tok_begin, ntiles, r, g, pc_idx, pc_page, process);
     } else {
-      for (int t0 = 0; t0 < ntiles; t0 += U) {
+      for (int t0 = 0, c = 0; t0 < ntiles; t0 += U, ++c) {
+        // Lock step (no wait for memory: gfx950's barrier does not drain the
+        // loads in flight).
+        if constexpr (kSync) {
+          if (c % kSyncChunks == 0) __builtin_amdgcn_s_barrier();
+        }
         if constexpr (kStore) {
           if (t_store >= t0 && t_store < t0 + U && new_slot >= 0)
             store_new_chunk<kFp8, D>(P, new_slot, kvh, 16 * g + r, new_chunk);
@@ -688,8 +714,9 @@ __global__ __launch_bounds__(NH * 64) void paged_decode_partition_kernel(
   // Wave index made provably uniform so that page lookups are scalar loads.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int v = blockIdx.y * NH + wave;
-  if (v >= P.num_kv_heads * P.col_blocks) return;  // uniform over the wave; no barriers follow
-  const VHead vh = vhead(P, v);
+  // Waves past the last virtual head only keep the work-group's barrier count.
+  const bool idle = v >= P.num_kv_heads * P.col_blocks;  // uniform over the wave
+  const VHead vh = vhead(P, idle ? 0 : v);
   const int lane = threadIdx.x & 63;
   if (tok_begin < ctx) {  // uniform over the work-group
     // The launch has max_parts partitions; the last one runs on to the context
@@ -708,7 +735,8 @@ __global__ __launch_bounds__(NH * 64) void paged_decode_partition_kernel(
     __shared__ __align__(16) uint8_t ring[WS::kLds ? NH * 2 * kStageBytes : 16];
     st.ring = ring + wave * 2 * kStageBytes;
     st.run(P, block_tables, slot_mapping, b, vh, max(tok_begin, lo & ~(kTile - 1)), tok_end, ctx,
-           lo, r, g);
+           lo, r, g, idle);
+    if (idle) return;
     if (nparts == 1) {
       st.write_final(P, b, vh, r, g);
     } else {
@@ -718,7 +746,7 @@ __global__ __launch_bounds__(NH * 64) void paged_decode_partition_kernel(
   }
   // No partition streams position ctx - 1 (no context): partition 0 writes b's
   // row.
-  if (kStore && p == 0 && ctx <= 0 && vh.first) {
+  if (kStore && p == 0 && ctx <= 0 && vh.first && !idle) {
     const int64_t os = valid_slot(P, slot_mapping, b);
     if (os >= 0) store_new_row<kFp8, D>(P, b, vh.kvh, os, lane);
   }
@@ -767,8 +795,9 @@ __global__ __launch_bounds__(NH * 64) void paged_decode_balanced_kernel(
     if (threadIdx.x == 0) P.tile_off[batch + 1] = S;
   }
   const int v = blockIdx.y * NH + wave;
-  if (v >= P.num_kv_heads * P.col_blocks) return;  // uniform over the wave; no barriers follow
-  const VHead vh = vhead(P, v);
+  // Waves past the last virtual head only keep the work-group's barrier count.
+  const bool idle = v >= P.num_kv_heads * P.col_blocks;  // uniform over the wave
+  const VHead vh = vhead(P, idle ? 0 : v);
   const int t_lo = w * S;
   const int t_hi = min(total, t_lo + S);
   if (t_lo < total) {
@@ -792,7 +821,8 @@ __global__ __launch_bounds__(NH * 64) void paged_decode_balanced_kernel(
       const int klo = key_lo(P, ctx);
       const int t_first = klo / kTile;  // the sequence's tile s is its tile t_first + s
       st.run(P, block_tables, slot_mapping, b, vh, kTile * (t_first + s_lo),
-             min(ctx, kTile * (t_first + s_hi)), ctx, klo, r, g);
+             min(ctx, kTile * (t_first + s_hi)), ctx, klo, r, g, idle);
+      if (idle) continue;
       if (toff[b] >= t_lo && toff[b + 1] <= t_hi) {
         st.write_final(P, b, vh, r, g);
       } else {
@@ -804,7 +834,7 @@ __global__ __launch_bounds__(NH * 64) void paged_decode_balanced_kernel(
   }
   // Sequences without tiles (no context) have no range that holds their last
   // position: group w writes the rows of those with b = w mod G.
-  if (kStore && vh.first) {
+  if (kStore && vh.first && !idle) {
     for (int b = w; b < batch; b += P.num_groups) {
       if (toff[b + 1] != toff[b]) continue;
       const int64_t os = valid_slot(P, slot_mapping, b);
