@@ -62,13 +62,16 @@ namespace fk {
 namespace {
 
 // Lock step: the waves of a work-group stream the same token rows (one kv head
-// each), and meet at a barrier every kSyncChunks load sets, so that a row's
+// each), and meet at a barrier every so many load sets, so that a row's
 // kv-head slices are read together rather than drifting apart (the younger
-// wave on each SIMD falls behind by several µs otherwise).  0 disables it.
+// wave on each SIMD falls behind by several µs otherwise).  0 disables it; fp8
+// pages (half the bytes per row) measured no gain from it.
 #ifndef FK_DECODE_SYNC_CHUNKS
 #define FK_DECODE_SYNC_CHUNKS 2
 #endif
-constexpr int kSyncChunks = FK_DECODE_SYNC_CHUNKS;
+#ifndef FK_DECODE_SYNC_CHUNKS_FP8
+#define FK_DECODE_SYNC_CHUNKS_FP8 0
+#endif
 
 #ifdef FK_DECODE_VALU_TILE
 constexpr bool kValuBuild = true;
@@ -337,6 +340,7 @@ struct WaveState {
                                       const void* __restrict__ sm, int b, const VHead& vh,
                                       int tok_begin, int tok_end, int ctx, int key_lo, int r,
                                       int g, bool idle) {
+    constexpr int kSyncChunks = kFp8 ? FK_DECODE_SYNC_CHUNKS_FP8 : FK_DECODE_SYNC_CHUNKS;
     constexpr bool kSync = kSyncChunks > 0 && !kLds;
     if (idle) {
       if constexpr (kSync) {
