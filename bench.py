@@ -438,8 +438,9 @@ def _np(t):
 
 def bench_table(args):
     """Per-op µs/call and GB/s for C1-C5 on the GPU (L2 + MALL flushed before each
-    timed call), each beside the CPU oracle timed on a bounded sample of the same
-    inputs on this host's cores."""
+    timed call), each beside the reference's PyTorch path for the op (restated in
+    oracle/torch_path.py) timed on this host's cores, and a parity verdict against
+    the numpy oracle."""
     import numpy as np
     import torch
 
@@ -499,8 +500,9 @@ def bench_table(args):
 
     # C1: fused add+RMSNorm; CPU path in fp32 (forward_native), GPU in bf16.
     c1 = workloads.c1_norm(dev)
+    from oracle import torch_path as tp
+
     c1f = workloads.c1_norm("cpu", dtype=torch.float32)
-    x1, r1, w1 = c1f.x.numpy(), c1f.residual.numpy(), c1f.weight.numpy()
     x, r = c1.x.clone(), c1.residual.clone()
     def norm_copies(x0, r0, w):
         sets = [(x0.clone(), r0.clone()) for _ in range(copies_for(4 * x0.numel() * 2))]
@@ -516,8 +518,9 @@ def bench_table(args):
 
     add("C1", "fused_add_rmsnorm bf16 [256,1024]",
         lambda: ops.fused_add_rms_norm(x, r, c1.weight, c1.eps), (4 * 256 * 1024 + 1024) * 2,
-        (lambda: oracle.rms_norm(x1, w1, 1e-6, "f32", residual=r1), 2.0,
-         "oracle.rms_norm fp32 on the full [256,1024] (4,198,400 B; GB/s on the fp32 bytes)"),
+        (lambda: tp.rms_norm_native(c1f.x, c1f.weight, 1e-6, residual=c1f.residual), 2.0,
+         "torch RMSNorm.forward_native (rms_norm.py:97-118) fp32 on the full [256,1024] "
+         "(4,198,400 B; GB/s on the fp32 bytes)"),
         parity=lambda: norm_parity(c1), rotated=lambda: norm_copies(c1.x, c1.residual, c1.weight))
     # C2: store_kvcache (bit copy); CPU: in-place numpy scatter into full-size caches.
     c2 = workloads.c2_store(dev)
@@ -550,22 +553,26 @@ def bench_table(args):
     s2 = c2.slot_mapping.cpu().numpy()
     kc2 = np.zeros(tuple(c2.k_cache.shape), np.int16)
     vc2 = np.zeros_like(kc2)
+    oracle.store_kvcache_(k2, v2, kc2, vc2, s2)  # the parity reference
+    kt2, vt2, st2 = c2.key.cpu(), c2.value.cpu(), c2.slot_mapping.cpu()
+    kct2 = torch.zeros(tuple(c2.k_cache.shape), dtype=torch.bfloat16)
+    vct2 = torch.zeros_like(kct2)
     add("C2", "store_kvcache [4096,8,128]",
         lambda: ops.store_kvcache(c2.key, c2.value, c2.k_cache, c2.v_cache, c2.slot_mapping),
         8 * 4096 + nvalid * 4 * 8 * 128 * 2,
-        (lambda: oracle.store_kvcache_(k2, v2, kc2, vc2, s2), 1.0,
-         "oracle.store_kvcache_ (numpy scatter) on the full C2 inputs and caches"),
+        (lambda: tp.store_kvcache_torch(kt2, vt2, kct2, vct2, st2), 1.0,
+         "torch index_copy_ scatter of the C2 rows into full-size host caches"),
         parity=lambda: store_parity(c2.k_cache, c2.v_cache, kc2, vc2),
         rotated=lambda: store_copies(c2.key, c2.value, c2.k_cache, c2.v_cache, nvalid / 4096))
-    del c2, kc2, vc2
+    del c2, kc2, vc2, kct2, vct2
     # C4 chain ops
     c4 = workloads.c4_chain(dev)
     h, rr = c4.hidden.clone(), c4.residual.clone()
-    hn, rn, wn = _np(c4.hidden), _np(c4.residual), _np(c4.norm_weight)
+    hc4, rc4, wc4 = c4.hidden.cpu(), c4.residual.cpu(), c4.norm_weight.cpu()
     add("C4", "fused_add_rmsnorm bf16 [256,4096]",
         lambda: ops.fused_add_rms_norm(h, rr, c4.norm_weight, 1e-6), (4 * 256 * 4096 + 4096) * 2,
-        (lambda: oracle.rms_norm(hn, wn, 1e-6, "bf16", residual=rn), 1.0,
-         "oracle.rms_norm (bf16 rounding points) on the full [256,4096]"),
+        (lambda: tp.rms_norm_native(hc4, wc4, 1e-6, residual=rc4), 1.0,
+         "torch RMSNorm.forward_native bf16 on the full [256,4096]"),
         parity=lambda: norm_parity(c4),
         rotated=lambda: norm_copies(c4.hidden, c4.residual, c4.norm_weight))
     from fastkernels_amd.candidate.L1.rotary_emb import RotaryEmbedding
@@ -573,7 +580,8 @@ def bench_table(args):
     rope = RotaryEmbedding(128, c4.max_position, c4.rope_theta).to(dev)
     qkv = c4.qkv.clone()
     q, k = qkv[:, :4096], qkv[:, 4096:5120]
-    qn, kn, pn, csn = _np(q), _np(k), c4.positions.cpu().numpy(), _np(rope.cos_sin_cache)
+    pn, csn = c4.positions.cpu().numpy(), _np(rope.cos_sin_cache)
+    qt4, kt4, pt4, cst4 = q.cpu(), k.cpu(), c4.positions.cpu(), rope.cos_sin_cache.cpu()
 
     def rope_copies():
         sets = [c4.qkv.clone() for _ in range(copies_for(2 * 256 * 5120 * 2))]
@@ -590,8 +598,9 @@ def bench_table(args):
     add("C4", "rotary q[256,32x128] k[256,8x128]",
         lambda: ops.rotary_embedding(c4.positions, q, k, 128, rope.cos_sin_cache, True),
         2 * 256 * 5120 * 2 + 256 * 8 + 256 * 128 * 4,
-        (lambda: oracle.rotary(pn, qn, kn, 128, csn, True, "bf16"), 1.0,
-         "oracle.rotary NeoX on the full q/k"), parity=rope_parity, rotated=rope_copies)
+        (lambda: tp.rotary_native(pt4, qt4, kt4, 128, cst4), 1.0,
+         "torch RotaryEmbedding.forward_native (NeoX) on the full q/k"), parity=rope_parity,
+        rotated=rope_copies)
     v = qkv[:, 5120:]
     dec = c4.decode
     # Qwen3 attention prologue at C4: per-head q/k RMSNorm + rotary + store_kvcache,
@@ -635,9 +644,8 @@ def bench_table(args):
 
     add("C4", "q/k RMSNorm + rotary + store_kvcache, fused (qk_norm_rope_store)", qk_fused,
         qk_bytes, rotated=qk_fused_copies)
-    kn16 = k.contiguous().view(torch.int16).view(256, 8, 128).cpu().numpy()
-    vn16 = v.contiguous().view(torch.int16).view(256, 8, 128).cpu().numpy()
-    sn = c4.slot_mapping.cpu().numpy()
+    kt16, vt16 = k.contiguous().view(256, 8, 128).cpu(), v.contiguous().view(256, 8, 128).cpu()
+    st4 = c4.slot_mapping.cpu()
 
     # scratch caches for the rotated C4 store (the decode case's caches stay as they are)
     scratch_kc = torch.zeros(1024, 256, 8, 128, dtype=torch.bfloat16, device=dev)
@@ -652,21 +660,24 @@ def bench_table(args):
         exact = np.array_equal(kc_, ek) and np.array_equal(vc_, ev)
         bf = lambda a: oracle.bf16_bits_to_f32(a.view(np.uint16))
         return verdict((bf(kc_), bf(vc_)), (bf(ek), bf(ev)), "bf16", bitexact=exact)
-    cache_np = np.zeros((dec.k_cache.shape[0],) + tuple(dec.k_cache.shape[1:]), np.int16)
+    cache_t = torch.zeros(tuple(dec.k_cache.shape), dtype=torch.bfloat16)
     add("C4", "store_kvcache [256,8,128]",
         lambda: ops.store_kvcache(k.view(256, 8, 128), v.view(256, 8, 128), dec.k_cache,
                                   dec.v_cache, c4.slot_mapping), 8 * 256 + 256 * 4 * 1024 * 2,
-        (lambda: oracle.store_kvcache_(kn16, vn16, cache_np, cache_np, sn), 1.0,
-         "oracle.store_kvcache_ on the full C4 tokens"), parity=store_rows_parity,
+        (lambda: tp.store_kvcache_torch(kt16, vt16, cache_t, cache_t, st4), 1.0,
+         "torch index_copy_ scatter of the C4 tokens into a full-size host cache"),
+        parity=store_rows_parity,
         rotated=lambda: store_copies(k.view(256, 8, 128), v.view(256, 8, 128), scratch_kc,
                                      scratch_vc, 1.0))
-    del cache_np, scratch_kc, scratch_vc
+    del cache_t, scratch_kc, scratch_vc
     gu = c4.gate_up
     gun = _np(gu)
+    gut = gu.cpu()
     act = torch.empty(256, 12288, dtype=torch.bfloat16, device=dev)
     add("C4", "silu_and_mul [256,2x12288]", lambda: ops.silu_and_mul(act, gu),
         256 * 3 * 12288 * 2,
-        (lambda: oracle.silu_and_mul(gun, "bf16"), 1.0, "oracle.silu_and_mul on the full input"),
+        (lambda: tp.silu_and_mul_native(gut), 1.0,
+         "torch SiluAndMul.forward_native on the full input"),
         parity=lambda: verdict(_np(act), oracle.silu_and_mul(gun, "bf16"), "bf16"),
         rotated=lambda: [lambda x_=x_, o_=o_: ops.silu_and_mul(o_, x_) for x_, o_ in
                          [(gu.clone(), torch.empty_like(act))
@@ -709,43 +720,65 @@ def bench_table(args):
         lambda: chain(True), chain_bytes, iters=30)
 
     def decode_cpu(case, nseq):
-        """Oracle on nseq sequences (shortest..longest spread) with their pages on the host."""
+        """The reference's torch decode path (oracle.torch_path.decode_torch: page gather,
+        repeat_interleave, SDPA in bf16; fp8 pages dequantised per kv head) on nseq
+        sequences (shortest..longest spread; all of them when nseq >= batch), their pages
+        copied to the host first; and the numpy oracle on the same sequences for the
+        parity verdict."""
+        from oracle.torch_path import decode_torch
+
         ctx = case.ctx_lens.cpu().numpy().astype(np.int64)
         bt = case.block_tables.cpu().numpy()
         bs = case.k_cache.shape[1]
         order = np.argsort(ctx)
-        pick = sorted(set(order[np.linspace(0, len(ctx) - 1, nseq).astype(int)].tolist()))
-        qh = _np(case.q)
+        pick = (list(range(len(ctx))) if nseq >= len(ctx) else
+                sorted(set(order[np.linspace(0, len(ctx) - 1, nseq).astype(int)].tolist())))
+        qh = case.q.cpu()
         fp8 = case.k_cache.dtype == torch.float8_e4m3fn
+        ks = None if case.k_scale is None else case.k_scale.cpu()
+        vs = None if case.v_scale is None else case.v_scale.cpu()
         data = []
         for i in pick:
             n = int(ctx[i])
             ids = torch.from_numpy(bt[i, :(n + bs - 1) // bs].astype(np.int64)).to(dev)
-            if fp8:
-                kp = case.k_cache[ids].view(torch.uint8).cpu().numpy()
-                vp = case.v_cache[ids].view(torch.uint8).cpu().numpy()
-            else:
-                kp, vp = _np(case.k_cache[ids]), _np(case.v_cache[ids])
-            data.append((i, n, kp, vp))
-        ks = None if case.k_scale is None else case.k_scale.cpu().numpy()
-        vs = None if case.v_scale is None else case.v_scale.cpu().numpy()
+            data.append((i, n, case.k_cache[ids].cpu(), case.v_cache[ids].cpu()))
+        data.sort(key=lambda e: e[1])  # by length, so `check` below spans short to long
 
-        def run():
-            return pick, np.concatenate([
-                oracle.paged_decode(qh[i:i + 1], kp, vp, np.arange(kp.shape[0])[None],
-                                    np.array([n]), case.scale, ks, vs) for i, n, kp, vp in data])
+        def run_torch():
+            for i, n, kp, vp in data:
+                decode_torch(qh[i:i + 1], kp, vp, torch.tensor([n]),
+                             torch.arange(kp.shape[0])[None], case.scale, k_scale=ks, v_scale=vs)
+
+        # The parity verdict: the numpy oracle on up to 4 of those sequences (shortest,
+        # longest and two between).
+        check = [data[j] for j in sorted(set(np.linspace(0, len(data) - 1,
+                                                         min(4, len(data))).astype(int)))]
+
+        def run_oracle():
+            ksn = None if ks is None else ks.numpy()
+            vsn = None if vs is None else vs.numpy()
+            qn = _np(case.q)
+            return [i for i, _, _, _ in check], np.concatenate([
+                oracle.paged_decode(qn[i:i + 1],
+                                    kp.view(torch.uint8).numpy() if fp8 else kp.float().numpy(),
+                                    vp.view(torch.uint8).numpy() if fp8 else vp.float().numpy(),
+                                    np.arange(kp.shape[0])[None], np.array([n]), case.scale,
+                                    ksn, vsn) for i, n, kp, vp in check])
 
         frac = sum(n for _, n, _, _ in data) / float(ctx.sum())
-        return (run, frac, f"oracle.paged_decode on {len(pick)} of {len(ctx)} sequences "
-                           f"({frac * 100:.1f}% of the cached tokens), scaled to the batch")
+        where = ("the whole batch" if len(pick) == len(ctx) else
+                 f"{len(pick)} of {len(ctx)} sequences ({frac * 100:.1f}% of the cached tokens), "
+                 "scaled to the batch")
+        return (run_torch, frac, "oracle.torch_path.decode_torch (the reference's _decode_torch, "
+                                 f"attention_impl.py:592-664) on {where}"), run_oracle
 
     decode_refs = {}
 
-    def decode_parity(name, out, cpu):
+    def decode_parity(name, out, oracle_fn):
         """The oracle's rows for the sampled sequences (computed once per configuration)
         against the same rows of the GPU output, rounded to bf16 as the baseline's."""
         if name not in decode_refs:
-            decode_refs[name] = cpu[0]()
+            decode_refs[name] = oracle_fn()
         pick, ref = decode_refs[name]
         return verdict(_np(out)[pick], oracle.round_to(ref, "bf16"), "bf16")
 
@@ -774,8 +807,8 @@ def bench_table(args):
 
     c3 = workloads.c3_decode(dev)
     c5 = workloads.c5_fp8_decode(dev)
-    cpu_legs = {}
-    for name, case, splits, nseq in (("C4", dec, 0, 4), ("C3", c3, 0, 4), ("C5", c5, 0, 1),
+    cpu_legs, oracle_legs = {}, {}
+    for name, case, splits, nseq in (("C4", dec, 0, 256), ("C3", c3, 0, 64), ("C5", c5, 0, 1),
                                      ("C5", c5, 16, 0), ("C5", c5, 32, 0), ("C5", c5, 64, 0)):
         b, hq, d = case.q.shape
         hk = case.k_cache.shape[2]
@@ -783,14 +816,14 @@ def bench_table(args):
         ws = torch.zeros(max(1, wsb), dtype=torch.uint8, device=dev)
         out = torch.empty_like(case.q)
         if nseq:
-            cpu_legs[name] = decode_cpu(case, nseq)
+            cpu_legs[name], oracle_legs[name] = decode_cpu(case, nseq)
         add(name, f"paged_decode {str(case.k_cache.dtype).replace('torch.', '')} B={b} Hq={hq} "
                   f"{'balanced' if part == 0 else f'{nparts} partitions'}",
             lambda: ops.paged_decode(out, case.q, case.k_cache, case.v_cache, case.block_tables,
                                      case.ctx_lens, case.scale, part, nparts, ws, case.k_scale,
                                      case.v_scale), case.algorithmic_bytes(),
             cpu_legs[name] if nseq else None, iters=30,
-            parity=lambda name=name, out=out: decode_parity(name, out, cpu_legs[name]))
+            parity=lambda name=name, out=out: decode_parity(name, out, oracle_legs[name]))
     # Prefill (FlashAttnPrefill with a block table) at Qwen3-8B heads, with torch's
     # own SDPA (flash backend, dense contiguous K/V) on the same GPU beside it.
     def prefill_case(q_lens, k_lens, seed):

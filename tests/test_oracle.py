@@ -604,6 +604,24 @@ def test_decode_torch_matches_oracle(dtype, tol):
     np.testing.assert_allclose(out.float().numpy(), ref, rtol=tol, atol=tol)
 
 
+def test_decode_torch_fp8_matches_oracle():
+    """The torch path on fp8 pages (dequantised per kv head after the gather) against
+    the numpy paged_decode on the same bytes and scales, within the fp8 bar."""
+    from oracle.torch_path import decode_torch
+
+    q, kc, vc, bt, lens = _decode_case(b=4, hq=8, hk=2, d=32, bs=8, nb=64, seed=4)
+    ks = np.array([0.05, 0.09], np.float32)
+    vs = np.array([0.02, 0.07], np.float32)
+    k8 = (torch.from_numpy(kc) / torch.from_numpy(ks).view(1, 1, 2, 1)).to(torch.float8_e4m3fn)
+    v8 = (torch.from_numpy(vc) / torch.from_numpy(vs).view(1, 1, 2, 1)).to(torch.float8_e4m3fn)
+    qb = torch.from_numpy(q).to(torch.bfloat16)
+    out = decode_torch(qb, k8, v8, torch.from_numpy(lens), torch.from_numpy(bt), 0.2,
+                       k_scale=torch.from_numpy(ks), v_scale=torch.from_numpy(vs))
+    ref = oracle.paged_decode(qb.float().numpy(), k8.view(torch.uint8).numpy(),
+                              v8.view(torch.uint8).numpy(), bt, lens, 0.2, ks, vs)
+    np.testing.assert_allclose(out.float().numpy(), ref, rtol=3e-2, atol=3e-2)
+
+
 @pytest.mark.parametrize("window_left", [0, 3, 9, 40])
 def test_paged_prefill_window_and_sinks(window_left):
     """Prefill with a sliding window and sinks: one-query chunks equal the decode
@@ -722,3 +740,41 @@ def test_silu_and_mul_matches_torch():
     np.testing.assert_allclose(oracle.silu_and_mul(np.array([[0.0, 3.0]], np.float32), "f32"), [[0.0]])
     big = oracle.silu_and_mul(np.array([[30.0, 2.0]], np.float32), "f32")
     np.testing.assert_allclose(big, [[60.0]], rtol=1e-6)  # silu(x) -> x for large x
+
+
+def test_torch_native_paths_match_oracle():
+    """The torch restatements bench.py times as CPU baselines (RMSNorm / rotary /
+    SiLU forward_native, the store as a scatter) against the pinned numpy oracle on
+    the same inputs: fp32 to rounding, the store bit for bit."""
+    from oracle import torch_path as tp
+
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(6, 64, generator=g)
+    r = torch.randn(6, 64, generator=g)
+    w = 1 + 0.1 * torch.randn(64, generator=g)
+    out, res = tp.rms_norm_native(x, w, 1e-6, residual=r)
+    ref_out, ref_res = oracle.rms_norm(x.numpy(), w.numpy(), 1e-6, "f32", residual=r.numpy())
+    np.testing.assert_allclose(out.numpy(), ref_out, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(res.numpy(), ref_res, rtol=0, atol=0)
+
+    cache = oracle.rope_cos_sin_cache(16, 32, 10000.0)
+    pos = torch.tensor([0, 3, 31, 7])
+    q = torch.randn(4, 2 * 16, generator=g)
+    k = torch.randn(4, 1 * 16, generator=g)
+    qo, ko = tp.rotary_native(pos, q, k, 16, torch.from_numpy(cache).float())
+    rq, rk = oracle.rotary(pos.numpy(), q.numpy(), k.numpy(), 16, cache, True, "f32")
+    np.testing.assert_allclose(qo.numpy(), rq, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(ko.numpy(), rk, rtol=1e-5, atol=1e-6)
+
+    key = torch.randn(5, 2, 8, generator=g)
+    val = torch.randn(5, 2, 8, generator=g)
+    slots = torch.tensor([3, -1, 0, 9, 6])
+    kc, vc = torch.zeros(3, 4, 2, 8), torch.zeros(3, 4, 2, 8)
+    tp.store_kvcache_torch(key, val, kc, vc, slots)
+    kr, vr = np.zeros((3, 4, 2, 8), np.float32), np.zeros((3, 4, 2, 8), np.float32)
+    oracle.store_kvcache_(key.numpy(), val.numpy(), kr, vr, slots.numpy())
+    assert np.array_equal(kc.numpy(), kr) and np.array_equal(vc.numpy(), vr)
+
+    gu = torch.randn(3, 2 * 24, generator=g)
+    np.testing.assert_allclose(tp.silu_and_mul_native(gu).numpy(),
+                               oracle.silu_and_mul(gu.numpy(), "f32"), rtol=1e-5, atol=1e-6)
