@@ -851,12 +851,17 @@ __global__ __launch_bounds__(NH * 64) void paged_decode_balanced_kernel(
 // dims.  Partial rows: k = 0 is `alt_first_row`, k >= 1 is first_row + k *
 // row_stride.  The pieces are taken kMergeBatch at a time (one batch for up to
 // 64 pieces): lane k loads piece k's (max, sum) while the wave issues the O
-// loads of every piece in the batch, all independent, so the merge costs one
-// load latency; the batch max and sum are wave reductions, and a running
-// (M, L, O) carries across batches with the reduce_segments rescaling.
+// loads of the batch's first merge_unroll<D>() pieces (32 VGPRs of loads, all
+// independent; each row's base address is a scalar pair, as the wave's query
+// head is uniform), so up to that many pieces (16 at D = 128) cost one load
+// latency; the batch max and sum are wave reductions, and a running (M, L, O)
+// carries across batches with the reduce_segments rescaling.
 constexpr int kMergeBatch = 64;  // pieces per batch: one (max, sum) per lane
-constexpr int kMergeUnroll = 8;  // O rows in flight per wave
 constexpr int kMergeWaves = 4;   // independent merge rows per work-group
+template <int D>
+constexpr int merge_unroll() {  // O rows in flight per wave: 32 registers per lane
+  return 2048 / D;
+}
 
 template <int D>
 struct MergeVec {
@@ -894,6 +899,7 @@ __device__ __forceinline__ void merge_rows(uint16_t* orow, const float* part_o,
                                            float sink2, int lane) {
   using V = MergeVec<D>;
   constexpr int N = V::N;
+  constexpr int kMergeUnroll = merge_unroll<D>();
   auto row_of = [&](int k) -> int64_t { return k == 0 ? alt_first_row : first_row + k * row_stride; };
   float M = kNegInf, L = 0.f;
   float acc[N];
@@ -971,7 +977,7 @@ __device__ __forceinline__ void zero_row(uint16_t* orow, int lane) {
 template <int D>
 __global__ __launch_bounds__(kMergeWaves * 64) void paged_decode_partition_reduce_kernel(
     DecodeParams P) {
-  const int hq = blockIdx.x * kMergeWaves + (threadIdx.x >> 6);
+  const int hq = blockIdx.x * kMergeWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int b = blockIdx.y;
   const int lane = threadIdx.x & 63;
   if (hq >= P.num_heads) return;  // no barriers in this kernel
@@ -993,7 +999,7 @@ __global__ __launch_bounds__(kMergeWaves * 64) void paged_decode_partition_reduc
 template <int D>
 __global__ __launch_bounds__(kMergeWaves * 64) void paged_decode_balanced_reduce_kernel(
     DecodeParams P) {
-  const int hq = blockIdx.x * kMergeWaves + (threadIdx.x >> 6);
+  const int hq = blockIdx.x * kMergeWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int b = blockIdx.y;
   const int lane = threadIdx.x & 63;
   if (hq >= P.num_heads) return;  // no barriers in this kernel
