@@ -225,4 +225,47 @@ __device__ __forceinline__ void v_words(const DTile<kFp8, D>& t, int i, bool kee
   }
 }
 
+// P.V B operands straight from the fp8 V rows of a loaded tile: slice d takes
+// dim (D/16) r + d of rows 4g .. 4g+3, each float(x) * s rounded to bf16 (the
+// dequant of fp8x4_to_bf16x4).  The rounding instruction packs two rows' values
+// of one dim, so the pairs come out in operand order with no byte regrouping
+// (v_words + v_operands_w pack two dims of one row, then permute).  Unless
+// `all`, the bytes of row i are zeroed where !keep[i] (a NaN byte becomes 0).
+template <int D>
+__device__ __forceinline__ void v_operands_fp8(const DTile<true, D>& t, float s, bool all,
+                                               const bool (&keep)[4], short4_t (&vb)[D / 16]) {
+  constexpr int NW = D / 64;  // fp8 words per row: dims 4q .. 4q + 3 in word q
+  uint32_t w[4][NW];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int q = 0; q < NW; ++q) w[i][q] = t.v[i][q];
+  if (!all) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int q = 0; q < NW; ++q) w[i][q] = keep[i] ? w[i][q] : 0u;
+  }
+#pragma unroll
+  for (int q = 0; q < NW; ++q) {
+    float f[4][4];  // [row][dim 4q + e]
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8(w[i][q], false);
+      const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8(w[i][q], true);
+      f[i][0] = lo[0] * s;
+      f[i][1] = lo[1] * s;
+      f[i][2] = hi[0] * s;
+      f[i][3] = hi[1] * s;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const bf16x2_t a = {static_cast<__bf16>(f[0][e]), static_cast<__bf16>(f[1][e])};
+      const bf16x2_t b = {static_cast<__bf16>(f[2][e]), static_cast<__bf16>(f[3][e])};
+      vb[4 * q + e] = __builtin_bit_cast(
+          short4_t, make_uint2(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b)));
+    }
+  }
+}
+
 }  // namespace fk

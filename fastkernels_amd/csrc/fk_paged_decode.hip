@@ -475,14 +475,20 @@ struct WaveState {
       uint4 kc[kKc];
       k_chunks_d(cur, kc, ks);
       const floatx4_t acc = qk_scores_n(kc, qb);
+      // A tile wholly inside the visible keys on a readable page (every tile but
+      // those at a segment's edges) needs no mask: one wave-uniform test skips
+      // the per-token compares and selects.  Padding columns (r >= ncols) have a
+      // zero Q, so their scores stay finite; their rows are never written.
+      const bool full = page >= 0 && tok0 >= key_lo && tok0 + kTile <= tok_end;
       float s[4];
-      float mt = kNegInf;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const bool ok = head_ok && page >= 0 && static_cast<uint32_t>(rel0 + i) < span;
-        s[i] = ok ? acc[i] * s2 : kNegInf;
-        mt = fmaxf(mt, s[i]);
+      for (int i = 0; i < 4; ++i) s[i] = acc[i] * s2;
+      if (!full) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (!(page >= 0 && static_cast<uint32_t>(rel0 + i) < span)) s[i] = kNegInf;
       }
+      float mt = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
       mt = pair_max(mt);  // max over the column's 4 lane groups (16 tokens)
       const float m_new = fmaxf(m_run, mt);
       const float m_use = m_new == kNegInf ? 0.f : m_new;
@@ -509,12 +515,26 @@ struct WaveState {
       const short4_t pa = p_operand(pr);
       // V rows past the context (inside a valid page) may hold anything: zero
       // them so that P = 0 never meets a NaN.
-      uint32_t vw[4][D / 32];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        v_words(cur, i, page >= 0 && static_cast<uint32_t>(rel0 + i) < span, vw[i], vsc);
       short4_t vb[kSl];
-      v_operands_w(vw, vb);
+      if constexpr (kFp8) {
+        bool keep[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) keep[i] = page >= 0 && static_cast<uint32_t>(rel0 + i) < span;
+        v_operands_fp8(cur, vsc, full, keep, vb);
+      } else {
+        uint32_t vw[4][D / 32];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v_words(cur, i, true, vw[i]);
+        if (!full) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const bool keep = page >= 0 && static_cast<uint32_t>(rel0 + i) < span;
+#pragma unroll
+            for (int q = 0; q < D / 32; ++q) vw[i][q] = keep ? vw[i][q] : 0u;
+          }
+        }
+        v_operands_w(vw, vb);
+      }
       pv_accumulate_n(o, pa, vb);
     };
 

@@ -509,17 +509,17 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D)))) void paged_prefi
         }
       }
     } else {
-      // Slice d holds dims (D/16) r + d (lane r), regrouped from the row loads.
+      // Slice d holds dims (D/16) r + d (lane r), packed from the row loads.
       lds_tile_v<kFp8, D>(buf, tt, r, g, ta);
       lds_tile_v<kFp8, D>(buf, tt + 1, r, g, tb);
-      uint32_t vwa[4][D / 32], vwb[4][D / 32];
+      bool keep_a[4], keep_b[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        v_words(ta, i, !kMasked || (ok_a && tok0 + 4 * g + i < kend), vwa[i], vsc);
-        v_words(tb, i, !kMasked || (ok_b && tok0 + kTile + 4 * g + i < kend), vwb[i], vsc);
+        keep_a[i] = ok_a && tok0 + 4 * g + i < kend;
+        keep_b[i] = ok_b && tok0 + kTile + 4 * g + i < kend;
       }
-      v_operands_w(vwa, vba);
-      v_operands_w(vwb, vbb);
+      v_operands_fp8(ta, vsc, !kMasked, keep_a, vba);
+      v_operands_fp8(tb, vsc, !kMasked, keep_b, vbb);
     }
     // P.V over the 32 keys with the 16x16x32 MFMA (the 16x16x16 one takes as
     // long on gfx950 for half the work).  Its k index 8g + e stands for key
