@@ -21,6 +21,7 @@ the whole batch on the host's cores.
   python bench.py --table          # per-op table for C1-C5 to stderr (+ --table-json PATH)
   python bench.py --calib-copy     # plain 1 GiB device copy, for rocprof counter scaling
   python bench.py --profile-ops    # each op after a cache flush, for rocprof counter passes
+  python bench.py --profile-prefill  # the table's prefill cases, for rocprof counter passes
 """
 from __future__ import annotations
 
@@ -53,6 +54,8 @@ def _parse():
     ap.add_argument("--calib-copy", action="store_true")
     ap.add_argument("--profile-ops", action="store_true",
                     help="each op on its C1-C5 inputs after a cache flush, for rocprofv3 --pmc")
+    ap.add_argument("--profile-prefill", action="store_true",
+                    help="the table's prefill cases after a cache flush, for rocprofv3")
     ap.add_argument("--seed", type=int, default=200)
     return ap.parse_args()
 
@@ -826,30 +829,8 @@ def bench_table(args):
             parity=lambda name=name, out=out: decode_parity(name, out, oracle_legs[name]))
     # Prefill (FlashAttnPrefill with a block table) at Qwen3-8B heads, with torch's
     # own SDPA (flash backend, dense contiguous K/V) on the same GPU beside it.
-    def prefill_case(q_lens, k_lens, seed):
-        g = torch.Generator().manual_seed(seed)
-        bs = 256
-        pages = [(k + bs - 1) // bs for k in k_lens]
-        nb = sum(pages)
-        perm = torch.randperm(nb, generator=g).to(torch.int32)
-        bt = torch.full((len(k_lens), max(pages)), -1, dtype=torch.int32)
-        off = 0
-        for i, p in enumerate(pages):
-            bt[i, :p] = perm[off:off + p]
-            off += p
-        cu_q = torch.tensor([0] + list(np.cumsum(q_lens)), dtype=torch.int32, device=dev)
-        cu_k = torch.tensor([0] + list(np.cumsum(k_lens)), dtype=torch.int32, device=dev)
-        q = torch.randn(sum(q_lens), 32, 128, generator=g).to(torch.bfloat16).to(dev)
-        kc = torch.randn(nb, bs, 8, 128, generator=g).to(torch.bfloat16).to(dev)
-        vc = torch.randn(nb, bs, 8, 128, generator=g).to(torch.bfloat16).to(dev)
-        visible = sum(sum(max(0, min(kl, kl - ql + j + 1)) for j in range(ql))
-                      for ql, kl in zip(q_lens, k_lens))
-        return q, kc, vc, bt.to(dev), cu_q, cu_k, max(q_lens), visible * 32 * 4 * 128
-
-    for label, ql, kl in (("1x2048 prompt", [2048], [2048]),
-                          ("4x512 chunks over 4096", [512] * 4, [4096] * 4),
-                          ("16x512 prompts", [512] * 16, [512] * 16)):
-        q, kc, vc, bt, cu_q, cu_k, mq, flop = prefill_case(ql, kl, workloads.SEED + 11)
+    for label, ql, kl in PREFILL_CASES:
+        q, kc, vc, bt, cu_q, cu_k, mq, flop = prefill_case(dev, ql, kl, workloads.SEED + 11)
         pout = torch.empty_like(q)
         med, _ = time_call(lambda: ops.paged_prefill(pout, q, kc, vc, bt, cu_q, cu_k, mq,
                                                      128 ** -0.5, max_seqlen_k=max(kl)),
@@ -905,6 +886,59 @@ def bench_table(args):
         Path(args.table_json).parent.mkdir(parents=True, exist_ok=True)
         Path(args.table_json).write_text(json.dumps(rows, indent=1))
     return rows
+
+
+# The prefill rows of the per-op table: (label, query lengths, key lengths).
+PREFILL_CASES = (("1x2048 prompt", [2048], [2048]),
+                 ("4x512 chunks over 4096", [512] * 4, [4096] * 4),
+                 ("16x512 prompts", [512] * 16, [512] * 16))
+
+
+def prefill_case(dev, q_lens, k_lens, seed):
+    """Paged prefill inputs at Qwen3-8B heads (Hq 32, Hk 8, head 128, 256-token pages
+    from a seeded permutation), and the FLOPs of the visible (query, key) pairs."""
+    import numpy as np
+    import torch
+
+    g = torch.Generator().manual_seed(seed)
+    bs = 256
+    pages = [(k + bs - 1) // bs for k in k_lens]
+    nb = sum(pages)
+    perm = torch.randperm(nb, generator=g).to(torch.int32)
+    bt = torch.full((len(k_lens), max(pages)), -1, dtype=torch.int32)
+    off = 0
+    for i, p in enumerate(pages):
+        bt[i, :p] = perm[off:off + p]
+        off += p
+    cu_q = torch.tensor([0] + list(np.cumsum(q_lens)), dtype=torch.int32, device=dev)
+    cu_k = torch.tensor([0] + list(np.cumsum(k_lens)), dtype=torch.int32, device=dev)
+    q = torch.randn(sum(q_lens), 32, 128, generator=g).to(torch.bfloat16).to(dev)
+    kc = torch.randn(nb, bs, 8, 128, generator=g).to(torch.bfloat16).to(dev)
+    vc = torch.randn(nb, bs, 8, 128, generator=g).to(torch.bfloat16).to(dev)
+    visible = sum(sum(max(0, min(kl, kl - ql + j + 1)) for j in range(ql))
+                  for ql, kl in zip(q_lens, k_lens))
+    return q, kc, vc, bt.to(dev), cu_q, cu_k, max(q_lens), visible * 32 * 4 * 128
+
+
+def profile_prefill(reps: int = 3):
+    """The per-op table's prefill cases, `reps` calls each, every call after a 512 MB
+    read that evicts L2 and the MALL: the program rocprofv3 --pmc / --kernel-trace runs
+    for the prefill kernel's counters.  Prints one JSON line per case."""
+    import torch
+
+    from fastkernels_amd import ops, workloads
+
+    dev = torch.device("cuda:0")
+    flush = _flush_buffer(dev)
+    for label, ql, kl in PREFILL_CASES:
+        q, kc, vc, bt, cu_q, cu_k, mq, flop = prefill_case(dev, ql, kl, workloads.SEED + 11)
+        out = torch.empty_like(q)
+        for _ in range(reps):
+            flush.sum()
+            ops.paged_prefill(out, q, kc, vc, bt, cu_q, cu_k, mq, 128 ** -0.5,
+                              max_seqlen_k=max(kl))
+        torch.cuda.synchronize()
+        print(json.dumps({"case": label, "flop": flop, "calls": reps}), flush=True)
 
 
 def profile_ops(reps: int = 3):
@@ -1011,6 +1045,9 @@ def main():
         return
     if args.profile_ops:
         profile_ops()
+        return
+    if args.profile_prefill:
+        profile_prefill()
         return
     if args.table:
         bench_table(args)

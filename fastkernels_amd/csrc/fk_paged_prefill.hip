@@ -281,7 +281,7 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D)))) void paged_prefi
   if (x >= (paired ? (nqb + 1) / 2 : nqb)) return;  // uniform over the work-group
   const int wave_id = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int half = kKS > 1 ? wave_id / kPrefillWaves : 0;  // key-split half
-  const int wave = wave_id - half * kPrefillWaves;          // role within the half
+  const int wave = wave_id & (kPrefillWaves - 1);           // role within the half
   uint8_t* const lds0 = lds_all + half * 2 * S::kBytes;
   uint8_t* const lds1 = lds0 + S::kBytes;
   const int lane = threadIdx.x & 63;
