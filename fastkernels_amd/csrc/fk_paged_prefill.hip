@@ -157,18 +157,15 @@ struct Stage {
 // pass wait for the load before every later LDS read, including reads of the
 // other stage buffer, which would serialise the double buffer.  The kernel
 // orders it explicitly instead (s_waitcnt vmcnt(0), then a barrier, before the
-// buffer is read).  M0 carries the LDS address and is restored afterwards.
+// buffer is read).  M0 carries the LDS address: an input operand bound to M0, so
+// the compiler writes it (and knows it changed) with no save and restore; the
+// s_nop is the wait state between that write and the load that reads M0.
 __device__ __forceinline__ void lds_dma16(const uint8_t* src, uint32_t lds_addr) {
-  uint32_t saved;
   asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %2\n\t"
       "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %1, off\n\t"
-      "s_nop 0\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "v"(src), "s"(lds_addr)
+      "global_load_lds_dwordx4 %0, off"
+      :
+      : "v"(src), "{m0}"(lds_addr)
       : "memory");
 }
 
@@ -566,17 +563,23 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D)))) void paged_prefi
     const int64_t rb = which ? P.v_row_bytes : P.k_row_bytes;
     lane_off[i] = static_cast<uint32_t>((row & 15) * rb + head_off + 16 * q);
   }
+  // Whether every page of the stage staged last is readable (the unmasked loop's
+  // test for that stage, so it needs no page lookups of its own).
+  bool staged_ok = true;
   auto stage_load = [&](int st, uint8_t* buf) {
     // Wave-uniform (the buffer is the half's); readfirstlane keeps it in an SGPR
     // for M0 where the compiler cannot prove it.
     const uint32_t buf_addr = __builtin_amdgcn_readfirstlane(lds_addr_of(buf));
     // First rows of the stage's tiles: page lookups once per tile, wave-uniform.
     int64_t row0[kStageTiles];
+    bool all_ok = true;
 #pragma unroll
     for (int tt = 0; tt < kStageTiles; ++tt) {
       bool ok;
       row0[tt] = key_row<kPaged>(P, bt_row, k_start, st * kStageKeys + tt * kTile, ok, pc);
+      all_ok = all_ok && ok;
     }
+    staged_ok = all_ok;
 #pragma unroll
     for (int i = 0; i < S::kLoads; ++i) {
       const int pos0 = 64 * (kPrefillWaves * i + wave);  // wave-uniform
@@ -622,19 +625,13 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D)))) void paged_prefi
     }
   };
   // A stage needs no mask when this wave sees all its keys in full (below nfull)
-  // and none of its pages is masked.
+  // and none of its pages is masked.  Called for stage st only when st is the
+  // stage staged last (the loop below tests stage st after step(st - 1), or
+  // after the first stage_load), so its page test is staged_ok.
   auto stage_unmasked = [&](int st) {
     if ((st + 1) * kStageTiles > nfull) return false;
     if (win >= 0 && st * kStageKeys < khead) return false;
-    if constexpr (kPaged) {
-#pragma unroll
-      for (int tt = 0; tt < kStageTiles; ++tt) {
-        bool ok;
-        (void)key_row<kPaged>(P, bt_row, k_start, (st * kStageTiles + tt) * kTile, ok, pc);
-        if (!ok) return false;
-      }
-    }
-    return true;
+    return staged_ok;
   };
   // One step: wait for stage st's loads (every thread's, through the barrier,
   // which also frees the other buffer), issue stage st + 1's, consume stage st.
