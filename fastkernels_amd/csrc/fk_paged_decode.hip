@@ -867,17 +867,23 @@ __global__ __launch_bounds__(NH * 64) void paged_decode_balanced_kernel(
   }
 }
 
-// Merge of one (query head hq, sequence b) by one wave; each lane owns D / 64
-// dims.  Partial rows: k = 0 is `alt_first_row`, k >= 1 is first_row + k *
-// row_stride.  The pieces are taken kMergeBatch at a time (one batch for up to
-// 64 pieces): lane k loads piece k's (max, sum) while the wave issues the O
-// loads of the batch's first merge_unroll<D>() pieces (32 VGPRs of loads, all
+// Merge of one (query head hq, sequence b) by one wave (merge_fold); each lane
+// owns D / 64 dims.  The pieces are taken kMergeBatch at a time (one batch for
+// up to 64 pieces): lane k loads piece k's (max, sum) while the wave issues the
+// O loads of the batch's first merge_unroll<D>() pieces (32 VGPRs of loads, all
 // independent; each row's base address is a scalar pair, as the wave's query
 // head is uniform), so up to that many pieces (16 at D = 128) cost one load
 // latency; the batch max and sum are wave reductions, and a running (M, L, O)
-// carries across batches with the reduce_segments rescaling.
+// carries across batches with the reduce_segments rescaling.  A row with more
+// pieces than that (a long sequence in a small batch: one sequence over 256
+// work-groups leaves 256) takes kMergeWaves / kRows waves, which fold pieces
+// w, w + kMergeWaves / kRows, ... each and are combined through LDS
+// (merge_group).  Work-groups hold kMergeRowsBig rows, or one row when the
+// launch expects more pieces per row than their waves fold in one round (a
+// batch of one to three sequences over the balanced schedule's 256 ranges).
 constexpr int kMergeBatch = 64;  // pieces per batch: one (max, sum) per lane
-constexpr int kMergeWaves = 4;   // independent merge rows per work-group
+constexpr int kMergeWaves = 16;  // waves per merge work-group
+constexpr int kMergeRowsBig = 4; // rows (query heads of one sequence) per work-group
 template <int D>
 constexpr int merge_unroll() {  // O rows in flight per wave: 32 registers per lane
   return 2048 / D;
@@ -912,15 +918,21 @@ struct MergeVec {
   }
 };
 
+// Running log-sum-exp state of a merge: max M and sum L (the same in every
+// lane) and this lane's D / 64 dims of the unnormalised O.
 template <int D>
-__device__ __forceinline__ void merge_rows(uint16_t* orow, const float* part_o,
-                                           const float* part_ml, int64_t first_row,
-                                           int64_t row_stride, int nrows, int64_t alt_first_row,
-                                           float sink2, int lane) {
+struct MergeState {
+  float M, L;
+  float acc[D / 64];
+};
+
+// Folds pieces k = 0 .. nrows - 1 (partial row row_of(k)) into a fresh state.
+template <int D, class RowOf>
+__device__ __forceinline__ MergeState<D> merge_fold(const float* part_o, const float* part_ml,
+                                                    RowOf row_of, int nrows, int lane) {
   using V = MergeVec<D>;
   constexpr int N = V::N;
   constexpr int kMergeUnroll = merge_unroll<D>();
-  auto row_of = [&](int k) -> int64_t { return k == 0 ? alt_first_row : first_row + k * row_stride; };
   float M = kNegInf, L = 0.f;
   float acc[N];
 #pragma unroll
@@ -965,16 +977,29 @@ __device__ __forceinline__ void merge_rows(uint16_t* orow, const float* part_o,
     }
     M = mn;
   }
-  L = with_sink(L, M, sink2);  // the sink joins the merged row once
+  MergeState<D> st;
+  st.M = M;
+  st.L = L;
+#pragma unroll
+  for (int e = 0; e < N; ++e) st.acc[e] = acc[e];
+  return st;
+}
+
+// Normalised bf16 row from a merged state; the sink joins the row once.
+template <int D>
+__device__ __forceinline__ void merge_write(uint16_t* orow, const MergeState<D>& st, float sink2,
+                                            int lane) {
+  constexpr int N = D / 64;
+  const float L = with_sink(st.L, st.M, sink2);
   const float inv = L > 0.f ? 1.f / L : 0.f;
   if constexpr (N == 1) {
-    orow[lane] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(acc[0] * inv));
+    orow[lane] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(st.acc[0] * inv));
   } else {
     uint32_t w[N / 2];
 #pragma unroll
     for (int e = 0; e < N / 2; ++e) {
-      const bf16x2_t pk = {static_cast<__bf16>(acc[2 * e] * inv),
-                           static_cast<__bf16>(acc[2 * e + 1] * inv)};
+      const bf16x2_t pk = {static_cast<__bf16>(st.acc[2 * e] * inv),
+                           static_cast<__bf16>(st.acc[2 * e + 1] * inv)};
       w[e] = __builtin_bit_cast(uint32_t, pk);
     }
     if constexpr (N == 2)
@@ -982,6 +1007,74 @@ __device__ __forceinline__ void merge_rows(uint16_t* orow, const float* part_o,
     else
       reinterpret_cast<uint2*>(orow)[lane] = make_uint2(w[0], w[1]);
   }
+}
+
+// The merge rows of one work-group: query heads hq0 .. hq0 + kRows - 1 of one
+// sequence, all with the same piece count nrows (the pieces of a sequence are
+// the same for every head).  Partial row of piece k of head hq: k = 0 is
+// alt0 + hq, k >= 1 is first0 + hq + k * row_stride.  Up to merge_unroll<D>()
+// pieces, wave r merges row r alone; more pieces take kSplit = kMergeWaves /
+// kRows waves per row (wave w folds pieces w, w + kSplit, ...), whose states
+// wave 0 of the row combines from LDS with the same rescaling.  nrows is
+// uniform over the work-group, so every wave meets the barrier or none does.
+template <int D, int kRows>
+__device__ __forceinline__ void merge_group(const DecodeParams& P, uint16_t* out_b, int hq0,
+                                            int64_t first0, int64_t alt0, int64_t row_stride,
+                                            int nrows, int wave, int lane) {
+  constexpr int N = D / 64;
+  constexpr int kSplit = kMergeWaves / kRows;
+  constexpr int kSlot = 2 + 64 * N;  // floats per wave in LDS: M, L, O
+  __shared__ float xs[kMergeWaves * kSlot];
+  if (nrows <= merge_unroll<D>()) {
+    const int hq = hq0 + wave;
+    if (wave >= kRows || hq >= P.num_heads) return;
+    auto row_of = [&](int k) -> int64_t {
+      return k == 0 ? alt0 + hq : first0 + hq + k * row_stride;
+    };
+    merge_write<D>(out_b + static_cast<int64_t>(hq) * D,
+                   merge_fold<D>(P.part_o, P.part_ml, row_of, nrows, lane), sink_log2(P, hq),
+                   lane);
+    return;
+  }
+  const int r = wave / kSplit;
+  const int part = wave - r * kSplit;
+  const int hq = hq0 + r;
+  const bool valid = hq < P.num_heads;
+  auto row_of = [&](int j) -> int64_t {
+    const int k = part + kSplit * j;
+    return k == 0 ? alt0 + hq : first0 + hq + k * row_stride;
+  };
+  const int mine = valid && nrows > part ? (nrows - part + kSplit - 1) / kSplit : 0;
+  const MergeState<D> st = merge_fold<D>(P.part_o, P.part_ml, row_of, mine, lane);
+  float* x = xs + wave * kSlot;
+  if (lane == 0) {
+    x[0] = st.M;
+    x[1] = st.L;
+  }
+#pragma unroll
+  for (int e = 0; e < N; ++e) x[2 + e * 64 + lane] = st.acc[e];
+  __syncthreads();
+  if (part != 0 || !valid) return;
+  const float* xr = xs + r * kSplit * kSlot;
+  float M = kNegInf;
+#pragma unroll
+  for (int v = 0; v < kSplit; ++v) M = fmaxf(M, xr[v * kSlot]);
+  MergeState<D> out;
+  out.M = M;
+  out.L = 0.f;
+#pragma unroll
+  for (int e = 0; e < N; ++e) out.acc[e] = 0.f;
+  if (M != kNegInf) {
+#pragma unroll
+    for (int v = 0; v < kSplit; ++v) {
+      const float mv = xr[v * kSlot];
+      const float f = mv == kNegInf ? 0.f : __builtin_amdgcn_exp2f(mv - M);
+      out.L += xr[v * kSlot + 1] * f;
+#pragma unroll
+      for (int e = 0; e < N; ++e) out.acc[e] += xr[v * kSlot + 2 + e * 64 + lane] * f;
+    }
+  }
+  merge_write<D>(out_b + static_cast<int64_t>(hq) * D, out, sink_log2(P, hq), lane);
 }
 
 // Zero row of D bf16 for an empty sequence (one wave; each lane D / 64 dims).
@@ -992,43 +1085,44 @@ __device__ __forceinline__ void zero_row(uint16_t* orow, int lane) {
 }
 
 // Fixed partitions: merge sequences with more than one partition; zero empty ones.
-// Work-group = kMergeWaves independent waves, wave v = query head
-// blockIdx.x * kMergeWaves + v of sequence blockIdx.y.
-template <int D>
+// Work-group = kRows query heads blockIdx.x * kRows .. of sequence blockIdx.y
+// (merge_group).
+template <int D, int kRows>
 __global__ __launch_bounds__(kMergeWaves * 64) void paged_decode_partition_reduce_kernel(
     DecodeParams P) {
-  const int hq = blockIdx.x * kMergeWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int hq0 = blockIdx.x * kRows;
   const int b = blockIdx.y;
   const int lane = threadIdx.x & 63;
-  if (hq >= P.num_heads) return;  // no barriers in this kernel
   const int ctx = P.ctx_lens[b];
-  uint16_t* orow = P.out + b * P.out_row_stride + static_cast<int64_t>(hq) * D;
+  uint16_t* out_b = P.out + b * P.out_row_stride;
   if (ctx <= 0) {
-    zero_row<D>(orow, lane);
+    if (wave < kRows && hq0 + wave < P.num_heads)
+      zero_row<D>(out_b + static_cast<int64_t>(hq0 + wave) * D, lane);
     return;
   }
   const int nparts = min((ctx + P.part_tokens - 1) / P.part_tokens, P.max_parts);
   if (nparts <= 1) return;  // written by the partition kernel
-  const int64_t first = static_cast<int64_t>(b) * P.max_parts * P.num_heads + hq;
-  merge_rows<D>(orow, P.part_o, P.part_ml, first, P.num_heads, nparts, first, sink_log2(P, hq),
-                lane);
+  const int64_t first = static_cast<int64_t>(b) * P.max_parts * P.num_heads;
+  merge_group<D, kRows>(P, out_b, hq0, first, first, P.num_heads, nparts, wave, lane);
 }
 
 // Balanced schedule: merge sequences cut across work-groups; zero empty ones.
-// Work-group = kMergeWaves independent waves, as the partition reduce.
-template <int D>
+// Work-group as the partition reduce.
+template <int D, int kRows>
 __global__ __launch_bounds__(kMergeWaves * 64) void paged_decode_balanced_reduce_kernel(
     DecodeParams P) {
-  const int hq = blockIdx.x * kMergeWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int hq0 = blockIdx.x * kRows;
   const int b = blockIdx.y;
   const int lane = threadIdx.x & 63;
-  if (hq >= P.num_heads) return;  // no barriers in this kernel
-  uint16_t* orow = P.out + b * P.out_row_stride + static_cast<int64_t>(hq) * D;
+  uint16_t* out_b = P.out + b * P.out_row_stride;
   const int t0 = P.tile_off[b];
   const int t1 = P.tile_off[b + 1];
   const int S = P.tile_off[P.batch + 1];
   if (t1 <= t0) {
-    zero_row<D>(orow, lane);
+    if (wave < kRows && hq0 + wave < P.num_heads)
+      zero_row<D>(out_b + static_cast<int64_t>(hq0 + wave) * D, lane);
     return;
   }
   const int w0 = t0 / S;
@@ -1038,10 +1132,9 @@ __global__ __launch_bounds__(kMergeWaves * 64) void paged_decode_balanced_reduce
   // Group w0 holds the sequence in slot 1 unless the sequence starts its range;
   // groups w0+1 .. w1 hold it in slot 0.
   const int slot0 = t0 > w0 * S ? 1 : 0;
-  const int64_t first_alt = (static_cast<int64_t>(w0) * 2 + slot0) * hqn + hq;
-  const int64_t first = (static_cast<int64_t>(w0) * 2 + 0) * hqn + hq;
-  merge_rows<D>(orow, P.part_o, P.part_ml, first, 2 * hqn, w1 - w0 + 1, first_alt,
-                sink_log2(P, hq), lane);
+  const int64_t first_alt = (static_cast<int64_t>(w0) * 2 + slot0) * hqn;
+  const int64_t first = (static_cast<int64_t>(w0) * 2 + 0) * hqn;
+  merge_group<D, kRows>(P, out_b, hq0, first, first_alt, 2 * hqn, w1 - w0 + 1, wave, lane);
 }
 
 // Tuning knobs (compile-time): tiles per load set for bf16 pages at head sizes
@@ -1274,14 +1367,32 @@ void launch_main_any(const Launch& L, hipStream_t stream) {
   }
 }
 
-template <int D>
-void launch_reduce_d(const Launch& L, dim3 grid, hipStream_t stream) {
+template <int D, int kRows>
+void launch_reduce_rows(const Launch& L, dim3 grid, hipStream_t stream) {
   if (L.balanced)
-    hipLaunchKernelGGL(paged_decode_balanced_reduce_kernel<D>, grid, dim3(kMergeWaves * 64), 0,
-                       stream, L.P);
+    hipLaunchKernelGGL((paged_decode_balanced_reduce_kernel<D, kRows>), grid,
+                       dim3(kMergeWaves * 64), 0, stream, L.P);
   else
-    hipLaunchKernelGGL(paged_decode_partition_reduce_kernel<D>, grid, dim3(kMergeWaves * 64), 0,
-                       stream, L.P);
+    hipLaunchKernelGGL((paged_decode_partition_reduce_kernel<D, kRows>), grid,
+                       dim3(kMergeWaves * 64), 0, stream, L.P);
+}
+
+// Rows per merge work-group: one when a row is expected to hold more pieces
+// than kMergeRowsBig-row work-groups fold in one round (balanced: about
+// ranges / batch + 1 per sequence; fixed partitions: max_parts), else
+// kMergeRowsBig.  Either form merges any piece count; this only picks the
+// faster one for the batch.
+template <int D>
+void launch_reduce_d(const Launch& L, int64_t batch, int num_heads, hipStream_t stream) {
+  const int64_t pieces = L.balanced ? (L.P.max_parts + batch - 1) / batch + 1 : L.P.max_parts;
+  const bool small = pieces > static_cast<int64_t>(kMergeWaves / kMergeRowsBig) * merge_unroll<D>();
+  const int rows = small ? 1 : kMergeRowsBig;
+  const dim3 grid(static_cast<unsigned>((num_heads + rows - 1) / rows),
+                  static_cast<unsigned>(batch));
+  if (small)
+    launch_reduce_rows<D, 1>(L, grid, stream);
+  else
+    launch_reduce_rows<D, kMergeRowsBig>(L, grid, stream);
 }
 
 }  // namespace
@@ -1358,13 +1469,11 @@ extern "C" int fk_paged_decode_reduce(
                    batch, num_heads, num_kv_heads, head_size, block_size, num_blocks, scale,
                    window_left, sinks, part_tokens, max_parts, workspace, ws_bytes);
   if (rc != FK_OK || batch == 0) return rc;
-  const dim3 grid(static_cast<unsigned>((num_heads + kMergeWaves - 1) / kMergeWaves),
-                  static_cast<unsigned>(batch));
   hipStream_t s = as_stream(stream);
   switch (head_size) {
-    case 64: launch_reduce_d<64>(L, grid, s); break;
-    case 256: launch_reduce_d<256>(L, grid, s); break;
-    default: launch_reduce_d<128>(L, grid, s); break;
+    case 64: launch_reduce_d<64>(L, batch, num_heads, s); break;
+    case 256: launch_reduce_d<256>(L, batch, num_heads, s); break;
+    default: launch_reduce_d<128>(L, batch, num_heads, s); break;
   }
   return check_launch("fk_paged_decode_reduce");
 }

@@ -568,6 +568,33 @@ def test_paged_decode_sliding_window_and_sinks(cuda, num_splits, window_left):
         assert not got[9].any()  # empty context: zero row, sinks or not
 
 
+@pytest.mark.parametrize("lens,num_splits,hd", [
+    ([20_000], 0, 128),          # one sequence over every range: one merge row per work-group
+    ([5_000, 30_000], 0, 128),   # two, cut into ~130 and ~230 pieces
+    ([3, 9_000, 0], 0, 64),      # three, with a short and an empty one
+    ([8_192, 100], 128, 128),    # 128 fixed partitions
+    ([12_000], 0, 256),
+])
+def test_paged_decode_merge_many_pieces(cuda, lens, num_splits, hd):
+    """Rows cut into more pieces than one wave folds in a round: several waves per
+    row fold strided subsets and are combined through LDS (with a work-group per
+    row for small batches), with and without sinks, against the oracle."""
+    _flush(f"decode many pieces lens={lens} splits={num_splits} D={hd}")
+    bs = 256
+    pool = sum((n + bs - 1) // bs for n in lens) + 2
+    case = workloads.c3_decode(cuda, num_heads=16, kv_heads=4, head_dim=hd, block_size=bs,
+                               pool_blocks=pool, ctx_lens=lens, seed=91 + hd)
+    g = torch.Generator().manual_seed(92)
+    sinks = (2 * torch.randn(16, generator=g)).float().to(cuda)
+    for sk in (None, sinks):
+        got = f32(run_decode_ws(case, num_splits, -1, sk))
+        ref = oracle_decode(case, sinks=sk)
+        assert_close(got, ref, BF16_TOL, BF16_TOL, f"lens={lens} splits={num_splits} D={hd}")
+        for i, n in enumerate(lens):
+            if n == 0:
+                assert not got[i].any()
+
+
 def test_paged_decode_sinks_c3_and_fp8(cuda):
     """Sinks at C3 size (balanced; sequences cut across work-groups merge the sink
     once) and on fp8 pages with a window, against the oracle."""
