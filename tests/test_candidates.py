@@ -41,6 +41,9 @@ CONTRACT = {
     "flash_attn_prefill": ("FlashAttnPrefill", ["num_heads", "num_kv_heads", "head_dim"],
                            ["q", "k", "v", "cu_seqlens_q", "cu_seqlens_k", "max_seqlen_q",
                             "max_seqlen_k", "kwargs"]),
+    "flash_attn_varlen": ("FlashAttnVarlen", None,
+                          ["q", "k", "v", "cu_seqlens_q", "cu_seqlens_k", "max_seqlen_q",
+                           "max_seqlen_k", "softmax_scale", "causal", "return_softmax_lse"]),
     "merge_attn_states": ("MergeAttnStates", None,
                           ["output", "prefix_output", "prefix_lse", "suffix_output", "suffix_lse",
                            "output_lse"]),

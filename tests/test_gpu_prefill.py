@@ -169,6 +169,34 @@ def test_varlen_prefill_dense_strided(cuda):
     _close(out, ref, 1e-2, "dense varlen")
 
 
+@pytest.mark.parametrize("causal,hq,hk,d,q_lens,k_lens", [
+    (False, 20, 20, 64, [1500, 37], [1500, 37]),      # Whisper encoder: bidirectional, MHA, D 64
+    (True, 16, 4, 128, [5, 100, 260], [5, 300, 260]),  # causal GQA, keys beyond the queries
+    (False, 8, 2, 256, [64, 1], [200, 9]),
+])
+def test_flash_attn_varlen_candidate(cuda, causal, hq, hk, d, q_lens, k_lens):
+    """FlashAttnVarlen (flash_attn_varlen.py:21-47): dense varlen attention through the
+    candidate class, against oracle.varlen_prefill; return_softmax_lse and unequal
+    head sizes raise."""
+    from fastkernels_amd.candidate.L1.flash_attn_varlen import FlashAttnVarlen
+    _flush(f"FlashAttnVarlen causal={causal} hq={hq} hk={hk} d={d}")
+    g = torch.Generator().manual_seed(83 + d)
+    q = torch.randn(sum(q_lens), hq, d, generator=g).to(torch.bfloat16).to(cuda)
+    k = torch.randn(sum(k_lens), hk, d, generator=g).to(torch.bfloat16).to(cuda)
+    v = torch.randn(sum(k_lens), hk, d, generator=g).to(torch.bfloat16).to(cuda)
+    cu_q = torch.tensor([0] + list(np.cumsum(q_lens)), dtype=torch.int32, device=cuda)
+    cu_k = torch.tensor([0] + list(np.cumsum(k_lens)), dtype=torch.int32, device=cuda)
+    m = FlashAttnVarlen()
+    out = m(q, k, v, cu_q, cu_k, max(q_lens), max(k_lens), d ** -0.5, causal=causal)
+    torch.cuda.synchronize()
+    ref = oracle.varlen_prefill(q.float().cpu().numpy(), k.float().cpu().numpy(),
+                                v.float().cpu().numpy(), cu_q.cpu().numpy(), cu_k.cpu().numpy(),
+                                d ** -0.5, causal=causal)
+    _close(out, ref, 1e-2, f"FlashAttnVarlen causal={causal} d={d}")
+    with pytest.raises(NotImplementedError):
+        m(q, k, v, cu_q, cu_k, max(q_lens), max(k_lens), d ** -0.5, return_softmax_lse=True)
+
+
 def test_paged_prefill_qwen3_prompt_2048(cuda):
     """One 2048-token prompt at Qwen3-8B heads: against torch fp32 causal attention on
     the device (the oracle would take minutes at this size)."""
