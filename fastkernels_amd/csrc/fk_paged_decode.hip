@@ -876,14 +876,14 @@ __global__ __launch_bounds__(NH * 64) void paged_decode_balanced_kernel(
 // latency; the batch max and sum are wave reductions, and a running (M, L, O)
 // carries across batches with the reduce_segments rescaling.  A row with more
 // pieces than that (a long sequence in a small batch: one sequence over 256
-// work-groups leaves 256) takes kMergeWaves / kRows waves, which fold pieces
-// w, w + kMergeWaves / kRows, ... each and are combined through LDS
-// (merge_group).  Work-groups hold kMergeRowsBig rows, or one row when the
-// launch expects more pieces per row than their waves fold in one round (a
-// batch of one to three sequences over the balanced schedule's 256 ranges).
+// work-groups leaves 256) takes kWaves / kRows waves, which fold pieces w,
+// w + kWaves / kRows, ... each and are combined through LDS (merge_group).
+// Three work-group layouts, picked per launch from the pieces a row is
+// expected to hold (launch_reduce_d): 4 rows of one wave (few pieces: idle
+// waves would only take dispatch slots), 4 rows of 4 waves, 1 row of 16 waves.
 constexpr int kMergeBatch = 64;  // pieces per batch: one (max, sum) per lane
-constexpr int kMergeWaves = 16;  // waves per merge work-group
-constexpr int kMergeRowsBig = 4; // rows (query heads of one sequence) per work-group
+constexpr int kMergeRows = 4;    // rows (query heads of one sequence) per work-group
+constexpr int kMergeWide = 16;   // waves per work-group of the split layouts
 template <int D>
 constexpr int merge_unroll() {  // O rows in flight per wave: 32 registers per lane
   return 2048 / D;
@@ -1013,19 +1013,20 @@ __device__ __forceinline__ void merge_write(uint16_t* orow, const MergeState<D>&
 // sequence, all with the same piece count nrows (the pieces of a sequence are
 // the same for every head).  Partial row of piece k of head hq: k = 0 is
 // alt0 + hq, k >= 1 is first0 + hq + k * row_stride.  Up to merge_unroll<D>()
-// pieces, wave r merges row r alone; more pieces take kSplit = kMergeWaves /
-// kRows waves per row (wave w folds pieces w, w + kSplit, ...), whose states
-// wave 0 of the row combines from LDS with the same rescaling.  nrows is
-// uniform over the work-group, so every wave meets the barrier or none does.
-template <int D, int kRows>
+// pieces (or with one wave per row), wave r merges row r alone; more pieces
+// take kSplit = kWaves / kRows waves per row (wave w folds pieces w,
+// w + kSplit, ...), whose states wave 0 of the row combines from LDS with the
+// same rescaling.  nrows is uniform over the work-group, so every wave meets
+// the barrier or none does.
+template <int D, int kRows, int kWaves>
 __device__ __forceinline__ void merge_group(const DecodeParams& P, uint16_t* out_b, int hq0,
                                             int64_t first0, int64_t alt0, int64_t row_stride,
                                             int nrows, int wave, int lane) {
   constexpr int N = D / 64;
-  constexpr int kSplit = kMergeWaves / kRows;
+  constexpr int kSplit = kWaves / kRows;
   constexpr int kSlot = 2 + 64 * N;  // floats per wave in LDS: M, L, O
-  __shared__ float xs[kMergeWaves * kSlot];
-  if (nrows <= merge_unroll<D>()) {
+  __shared__ float xs[kSplit > 1 ? kWaves * kSlot : 1];
+  if (kSplit == 1 || nrows <= merge_unroll<D>()) {
     const int hq = hq0 + wave;
     if (wave >= kRows || hq >= P.num_heads) return;
     auto row_of = [&](int k) -> int64_t {
@@ -1087,8 +1088,8 @@ __device__ __forceinline__ void zero_row(uint16_t* orow, int lane) {
 // Fixed partitions: merge sequences with more than one partition; zero empty ones.
 // Work-group = kRows query heads blockIdx.x * kRows .. of sequence blockIdx.y
 // (merge_group).
-template <int D, int kRows>
-__global__ __launch_bounds__(kMergeWaves * 64) void paged_decode_partition_reduce_kernel(
+template <int D, int kRows, int kWaves>
+__global__ __launch_bounds__(kWaves * 64) void paged_decode_partition_reduce_kernel(
     DecodeParams P) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int hq0 = blockIdx.x * kRows;
@@ -1104,13 +1105,13 @@ __global__ __launch_bounds__(kMergeWaves * 64) void paged_decode_partition_reduc
   const int nparts = min((ctx + P.part_tokens - 1) / P.part_tokens, P.max_parts);
   if (nparts <= 1) return;  // written by the partition kernel
   const int64_t first = static_cast<int64_t>(b) * P.max_parts * P.num_heads;
-  merge_group<D, kRows>(P, out_b, hq0, first, first, P.num_heads, nparts, wave, lane);
+  merge_group<D, kRows, kWaves>(P, out_b, hq0, first, first, P.num_heads, nparts, wave, lane);
 }
 
 // Balanced schedule: merge sequences cut across work-groups; zero empty ones.
 // Work-group as the partition reduce.
-template <int D, int kRows>
-__global__ __launch_bounds__(kMergeWaves * 64) void paged_decode_balanced_reduce_kernel(
+template <int D, int kRows, int kWaves>
+__global__ __launch_bounds__(kWaves * 64) void paged_decode_balanced_reduce_kernel(
     DecodeParams P) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int hq0 = blockIdx.x * kRows;
@@ -1134,7 +1135,8 @@ __global__ __launch_bounds__(kMergeWaves * 64) void paged_decode_balanced_reduce
   const int slot0 = t0 > w0 * S ? 1 : 0;
   const int64_t first_alt = (static_cast<int64_t>(w0) * 2 + slot0) * hqn;
   const int64_t first = (static_cast<int64_t>(w0) * 2 + 0) * hqn;
-  merge_group<D, kRows>(P, out_b, hq0, first, first_alt, 2 * hqn, w1 - w0 + 1, wave, lane);
+  merge_group<D, kRows, kWaves>(P, out_b, hq0, first, first_alt, 2 * hqn, w1 - w0 + 1, wave,
+                                lane);
 }
 
 // Tuning knobs (compile-time): tiles per load set for bf16 pages at head sizes
@@ -1367,32 +1369,33 @@ void launch_main_any(const Launch& L, hipStream_t stream) {
   }
 }
 
-template <int D, int kRows>
-void launch_reduce_rows(const Launch& L, dim3 grid, hipStream_t stream) {
+template <int D, int kRows, int kWaves>
+void launch_reduce_rows(const Launch& L, int64_t batch, int num_heads, hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>((num_heads + kRows - 1) / kRows),
+                  static_cast<unsigned>(batch));
   if (L.balanced)
-    hipLaunchKernelGGL((paged_decode_balanced_reduce_kernel<D, kRows>), grid,
-                       dim3(kMergeWaves * 64), 0, stream, L.P);
+    hipLaunchKernelGGL((paged_decode_balanced_reduce_kernel<D, kRows, kWaves>), grid,
+                       dim3(kWaves * 64), 0, stream, L.P);
   else
-    hipLaunchKernelGGL((paged_decode_partition_reduce_kernel<D, kRows>), grid,
-                       dim3(kMergeWaves * 64), 0, stream, L.P);
+    hipLaunchKernelGGL((paged_decode_partition_reduce_kernel<D, kRows, kWaves>), grid,
+                       dim3(kWaves * 64), 0, stream, L.P);
 }
 
-// Rows per merge work-group: one when a row is expected to hold more pieces
-// than kMergeRowsBig-row work-groups fold in one round (balanced: about
-// ranges / batch + 1 per sequence; fixed partitions: max_parts), else
-// kMergeRowsBig.  Either form merges any piece count; this only picks the
-// faster one for the batch.
+// Merge layout from the pieces a row is expected to hold (balanced: about
+// ranges / batch + 1 per sequence; fixed partitions: max_parts): one wave per
+// row when one wave folds them in one round, four waves per row up to four
+// rounds' worth, else a work-group of 16 waves per row.  Every layout merges any
+// piece count; this only picks the faster one for the batch.
 template <int D>
 void launch_reduce_d(const Launch& L, int64_t batch, int num_heads, hipStream_t stream) {
   const int64_t pieces = L.balanced ? (L.P.max_parts + batch - 1) / batch + 1 : L.P.max_parts;
-  const bool small = pieces > static_cast<int64_t>(kMergeWaves / kMergeRowsBig) * merge_unroll<D>();
-  const int rows = small ? 1 : kMergeRowsBig;
-  const dim3 grid(static_cast<unsigned>((num_heads + rows - 1) / rows),
-                  static_cast<unsigned>(batch));
-  if (small)
-    launch_reduce_rows<D, 1>(L, grid, stream);
+  const int64_t round = merge_unroll<D>();
+  if (pieces <= round)
+    launch_reduce_rows<D, kMergeRows, kMergeRows>(L, batch, num_heads, stream);
+  else if (pieces <= (kMergeWide / kMergeRows) * round)
+    launch_reduce_rows<D, kMergeRows, kMergeWide>(L, batch, num_heads, stream);
   else
-    launch_reduce_rows<D, kMergeRowsBig>(L, grid, stream);
+    launch_reduce_rows<D, 1, kMergeWide>(L, batch, num_heads, stream);
 }
 
 }  // namespace
