@@ -377,8 +377,8 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D)))) void paged_prefi
 
   // Two 16-key tiles (tiles tt, tt + 1 of `buf`, keys tok0 .. tok0 + 31):
   // scores, one online-softmax update per query column for the 32 keys, P.V.
-  // kMasked applies the causal / length / page mask; unmasked pairs skip it
-  // (every score is finite there, so the running max never stays -inf).
+  // kMasked applies the causal / length / window / page mask; unmasked pairs skip
+  // it (every score is finite there, so the running max never stays -inf).
   // Updating the running max, the rescale test and the cross-lane row max once
   // per 32 keys instead of per 16 halves that part of the VALU work, and the two
   // tiles' score MFMAs form independent chains.  The V rows are read only after
@@ -414,12 +414,22 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D)))) void paged_prefi
       const floatx4_t acc_b = sc_b[nb];
       const int j = j0 + 16 * nb + r;  // this lane's query column
       const int last = offset + j;     // its last visible key
+      // Masked pairs: key tok0 + rel (rel = 16 * tile + 4g + e) is visible when
+      // its tile's page is readable and dl <= rel - 4g <= dh: one range test per
+      // key instead of the causal, length, chunk and window tests each.
       // Scores in log2 units, s = s2 * (K.Q), one product each: a product is
       // canonical, so the max below compiles to plain v_max3 with no
       // NaN-quieting step per operand (as the raw MFMA results would need).
       // Masked keys take -inf in the max and P = 0 after the exponent.
       float s[8], sm[8];
       bool ok[8];
+      int dh = 0, dl = 0;
+      if constexpr (kMasked) {
+        const int hi = j < q_len ? min(last, kend - 1) : -1;  // last visible key
+        const int lo = win >= 0 ? last - win : 0;             // first visible key
+        dh = hi - tok0 - 4 * g;
+        dl = lo - tok0 - 4 * g;
+      }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         s[i] = acc_a[i] * s2;
@@ -428,9 +438,8 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D)))) void paged_prefi
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         if constexpr (kMasked) {
-          const int key = tok0 + (i >> 2) * kTile + 4 * g + (i & 3);
-          ok[i] = ((i >> 2) ? ok_b : ok_a) && j < q_len && key <= last && key < kend &&
-                  (win < 0 || key >= last - win);
+          const int rel = (i >> 2) * kTile + (i & 3);  // compile-time
+          ok[i] = ((i >> 2) ? ok_b : ok_a) && rel <= dh && rel >= dl;
           sm[i] = ok[i] ? s[i] : kNegInf;
         } else {
           ok[i] = true;
@@ -468,8 +477,8 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D)))) void paged_prefi
       float pr[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        pr[i] = __builtin_amdgcn_exp2f(s[i] - m_use);
-        if constexpr (kMasked) pr[i] = ok[i] ? pr[i] : 0.f;
+        // Masked scores are -inf in sm, so their P is 2^-inf = 0.
+        pr[i] = __builtin_amdgcn_exp2f(sm[i] - m_use);
       }
       const float (&pa)[4] = *reinterpret_cast<const float(*)[4]>(&pr[0]);
       const float (&pb)[4] = *reinterpret_cast<const float(*)[4]>(&pr[4]);
@@ -485,9 +494,10 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D)))) void paged_prefi
         vba[d] = lds_v_slice<D>(buf, tt, d, r, g);
         vbb[d] = lds_v_slice<D>(buf, tt + 1, d, r, g);
       }
-      if constexpr (kMasked) {
-        // Keys past the wave's keys (or on a masked page) may hold anything:
-        // zero them so that P = 0 never meets a NaN.
+      // Keys past the wave's keys (or on a masked page) may hold anything: zero
+      // them so that P = 0 never meets a NaN.  A pair of readable tiles wholly
+      // below kend (the causal diagonal of a prompt) needs none of it.
+      if (kMasked && (!ok_a || !ok_b || tok0 + 2 * kTile > kend)) {
         uint32_t ma[2], mb[2];
 #pragma unroll
         for (int h2 = 0; h2 < 2; ++h2) {
@@ -515,8 +525,9 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D)))) void paged_prefi
         keep_a[i] = ok_a && tok0 + 4 * g + i < kend;
         keep_b[i] = ok_b && tok0 + kTile + 4 * g + i < kend;
       }
-      v_operands_fp8(ta, vsc, !kMasked, keep_a, vba);
-      v_operands_fp8(tb, vsc, !kMasked, keep_b, vbb);
+      const bool vall = !kMasked || (ok_a && ok_b && tok0 + 2 * kTile <= kend);
+      v_operands_fp8(ta, vsc, vall, keep_a, vba);
+      v_operands_fp8(tb, vsc, vall, keep_b, vbb);
     }
     // P.V over the 32 keys with the 16x16x32 MFMA (the 16x16x16 one takes as
     // long on gfx950 for half the work).  Its k index 8g + e stands for key
