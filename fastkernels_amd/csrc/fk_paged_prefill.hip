@@ -392,6 +392,10 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D)))) void paged_prefi
     // K tiles are never live at once (20 fewer VGPRs in the compiler's own
     // allocation; measured 1% faster).
     floatx4_t sc_a[kCB], sc_b[kCB];
+    // The MFMA blocks run at raised wave priority: while one wave of a SIMD is in
+    // its softmax, the other's MFMAs issue first (4x512 chunks over 4096 keys
+    // 174.3 -> 168.7 us; the shorter cases unchanged).
+    __builtin_amdgcn_s_setprio(1);
     {
       lds_tile_k<kFp8, D>(buf, tt, r, g, ta);
       uint4 ka[D / 32];
@@ -407,6 +411,7 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D)))) void paged_prefi
 #pragma unroll
       for (int nb = 0; nb < kCB; ++nb) sc_b[nb] = qk_scores_n(kb, qb[nb]);
     }
+    __builtin_amdgcn_s_setprio(0);
     short4_t p_a[kCB], p_b[kCB];
 #pragma unroll
     for (int nb = 0; nb < kCB; ++nb) {
@@ -529,6 +534,7 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D)))) void paged_prefi
       v_operands_fp8(ta, vsc, vall, keep_a, vba);
       v_operands_fp8(tb, vsc, vall, keep_b, vbb);
     }
+    __builtin_amdgcn_s_setprio(1);
     // P.V over the 32 keys with the 16x16x32 MFMA (the 16x16x16 one takes as
     // long on gfx950 for half the work).  Its k index 8g + e stands for key
     // 4g + e of tile a (e < 4) and 4g + e - 4 of tile b (e >= 4): the A operand
@@ -549,6 +555,7 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D)))) void paged_prefi
       }
       l_acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pab, ones, l_acc[nb], 0, 0, 0);
     }
+    __builtin_amdgcn_s_setprio(0);
   };
 
   // Staging with direct global-to-LDS loads (lds_dma16).  Load i of wave w
