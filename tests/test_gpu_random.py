@@ -167,3 +167,45 @@ def test_random_prefill(cuda, i):
                                window_left=p["window"],
                                sinks=None if sinks is None else sinks.numpy())
     _close(out, ref, 3e-2 if p["fp8"] else 1e-2, f"random prefill {i} {p}")
+
+
+N_FUSED = 40
+
+
+@pytest.mark.parametrize("i", range(N_FUSED))
+def test_random_fused_store_decode(cuda, i):
+    """store_paged_decode against store_kvcache then paged_decode on copies of the
+    caches (bit for bit: output and both caches), over random decode options."""
+    p = _decode_params(500 + i)
+    p["ctx"] = [n + 1 for n in p["ctx"]]  # a decode step: the new token is position ctx - 1
+    print(f"random fused store + decode {i}: {p}", flush=True)
+    pool = sum((n + p["bs"] - 1) // p["bs"] for n in p["ctx"]) + 2
+    build = workloads.c5_fp8_decode if p["fp8"] else workloads.c3_decode
+    case = build(cuda, num_heads=p["hq"], kv_heads=p["hk"], head_dim=p["d"], block_size=p["bs"],
+                 pool_blocks=pool, seed=p["seed"], ctx_lens=p["ctx"])
+    rows = workloads.decode_step_rows(case, seed=p["seed"] + 1)
+    sinks = None
+    if p["sinks"]:
+        g = torch.Generator().manual_seed(p["seed"])
+        sinks = (2 * torch.randn(p["hq"], generator=g)).float().to(cuda)
+    b, hq, d = case.q.shape
+    part, nparts, wsb = ops.paged_decode_plan(b, hq, p["hk"], d, case.max_seq_len, p["splits"])
+    res = []
+    for fused in (False, True):
+        kc, vc = case.k_cache.clone(), case.v_cache.clone()
+        ws = torch.zeros(max(1, wsb), dtype=torch.uint8, device=cuda)
+        out = torch.full_like(case.q, float("nan"))
+        if fused:
+            ops.store_paged_decode(out, case.q, rows.key, rows.value, kc, vc, rows.slot_mapping,
+                                   case.block_tables, case.ctx_lens, case.scale, part, nparts,
+                                   ws, case.k_scale, case.v_scale, p["window"], sinks)
+        else:
+            ops.store_kvcache(rows.key, rows.value, kc, vc, rows.slot_mapping)
+            ops.paged_decode(out, case.q, kc, vc, case.block_tables, case.ctx_lens, case.scale,
+                             part, nparts, ws, case.k_scale, case.v_scale, p["window"], sinks)
+        torch.cuda.synchronize()
+        res.append((out, kc, vc))
+    for name, a, c in zip(("out", "k_cache", "v_cache"), res[1], res[0]):
+        if a.dtype == torch.float8_e4m3fn:
+            a, c = a.view(torch.uint8), c.view(torch.uint8)
+        assert torch.equal(a, c), f"random fused {i} {p}: {name} differs from the two calls"
