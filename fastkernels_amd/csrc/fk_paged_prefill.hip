@@ -247,7 +247,11 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D)))) void paged_prefi
   // Stage buffers (two per half), and with the key split the exchange area
   // that reuses them once the last stage is consumed.
   constexpr int kXFloats = split_exchange_floats<D, kCB>();
-  constexpr int kStageAll = kKS * 2 * S::kBytes;
+  // Key split with one pair per stage: the halves run opposite phases (half 1
+  // defers each pair's P.V past the next barrier), three stage buffers a half.
+  constexpr bool kPingPong = kKS > 1 && kStageTiles == 2;
+  constexpr int kBufs = kPingPong ? 3 : 2;
+  constexpr int kStageAll = kKS * kBufs * S::kBytes;
   constexpr int kXBytes = kKS > 1 ? kPrefillWaves * kXFloats * 4 : 0;
   __shared__ __align__(16) uint8_t lds_all[kStageAll > kXBytes ? kStageAll : kXBytes];
   // Grid: x = kv head (x hsplit), y = sequence, z = query block.  The block
@@ -279,8 +283,11 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D)))) void paged_prefi
   const int wave_id = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int half = kKS > 1 ? wave_id / kPrefillWaves : 0;  // key-split half
   const int wave = wave_id & (kPrefillWaves - 1);           // role within the half
-  uint8_t* const lds0 = lds_all + half * 2 * S::kBytes;
-  uint8_t* const lds1 = lds0 + S::kBytes;
+  uint8_t* const lds_half = lds_all + half * kBufs * S::kBytes;
+  // Stage st's buffer: two alternate; with three, stage st mod 3.
+  auto stage_buf = [&](int st) {
+    return lds_half + (kBufs == 2 ? (st & 1) : st % kBufs) * S::kBytes;
+  };
   const int lane = threadIdx.x & 63;
   const int r = lane & 15;
   const int g = lane >> 4;
@@ -384,8 +391,12 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D)))) void paged_prefi
   // tiles' score MFMAs form independent chains.  The V rows are read only after
   // the scores of both column blocks are done, so K, the scores and V are never
   // all live at once.
-  auto pair_step = [&](auto masked, int tok0, const uint8_t* buf, int tt, bool ok_a,
-                       bool ok_b) {
+  //
+  // pair_scores runs the scores and the softmax update (P into p_a / p_b) and
+  // returns whether the pair's V rows need masking; pair_pv runs P.V.
+  auto pair_scores = [&](auto masked, int tok0, const uint8_t* buf, int tt, bool ok_a,
+                         bool ok_b, short4_t (&p_a)[kCB],
+                         short4_t (&p_b)[kCB]) __attribute__((always_inline)) {
     constexpr bool kMasked = decltype(masked)::value;
     DTile<kFp8, D> ta, tb;
     // Scores of tile a for every column block, then tile b's K is read: the two
@@ -412,7 +423,6 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D)))) void paged_prefi
       for (int nb = 0; nb < kCB; ++nb) sc_b[nb] = qk_scores_n(kb, qb[nb]);
     }
     __builtin_amdgcn_s_setprio(0);
-    short4_t p_a[kCB], p_b[kCB];
 #pragma unroll
     for (int nb = 0; nb < kCB; ++nb) {
       const floatx4_t acc_a = sc_a[nb];
@@ -490,6 +500,14 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D)))) void paged_prefi
       p_a[nb] = p_operand(pa);
       p_b[nb] = p_operand(pb);
     }
+    // Keys past the wave's keys (or on a masked page) may hold anything in V.
+    // A pair of readable tiles wholly below kend (the causal diagonal of a
+    // prompt) needs no V mask.
+    return kMasked && (!ok_a || !ok_b || tok0 + 2 * kTile > kend);
+  };
+  auto pair_pv = [&](int tok0, const uint8_t* buf, int tt, bool ok_a, bool ok_b, bool vmask,
+                     const short4_t (&p_a)[kCB],
+                     const short4_t (&p_b)[kCB]) __attribute__((always_inline)) {
     asm volatile("" ::: "memory");  // V reads stay after the score work
     short4_t vba[D / 16], vbb[D / 16];  // shared by the column blocks
     if constexpr (!kFp8) {
@@ -499,10 +517,8 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D)))) void paged_prefi
         vba[d] = lds_v_slice<D>(buf, tt, d, r, g);
         vbb[d] = lds_v_slice<D>(buf, tt + 1, d, r, g);
       }
-      // Keys past the wave's keys (or on a masked page) may hold anything: zero
-      // them so that P = 0 never meets a NaN.  A pair of readable tiles wholly
-      // below kend (the causal diagonal of a prompt) needs none of it.
-      if (kMasked && (!ok_a || !ok_b || tok0 + 2 * kTile > kend)) {
+      // Zero the masked keys' V rows so that P = 0 never meets a NaN.
+      if (vmask) {
         uint32_t ma[2], mb[2];
 #pragma unroll
         for (int h2 = 0; h2 < 2; ++h2) {
@@ -522,6 +538,7 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D)))) void paged_prefi
       }
     } else {
       // Slice d holds dims (D/16) r + d (lane r), packed from the row loads.
+      DTile<kFp8, D> ta, tb;
       lds_tile_v<kFp8, D>(buf, tt, r, g, ta);
       lds_tile_v<kFp8, D>(buf, tt + 1, r, g, tb);
       bool keep_a[4], keep_b[4];
@@ -530,7 +547,7 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D)))) void paged_prefi
         keep_a[i] = ok_a && tok0 + 4 * g + i < kend;
         keep_b[i] = ok_b && tok0 + kTile + 4 * g + i < kend;
       }
-      const bool vall = !kMasked || (ok_a && ok_b && tok0 + 2 * kTile <= kend);
+      const bool vall = !vmask;
       v_operands_fp8(ta, vsc, vall, keep_a, vba);
       v_operands_fp8(tb, vsc, vall, keep_b, vbb);
     }
@@ -622,11 +639,25 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D)))) void paged_prefi
       lds_dma16(src, buf_addr + 16 * pos0);
     }
   };
+  // Key split, half 1: each pair's P.V waits for the next step and runs right
+  // after its barrier, before that step's loads and scores (the pair's V stays in
+  // its stage buffer: three buffers per half, so the loads issued in step s,
+  // into buffer (s + 1) mod 3, never meet the V of stage s - 1).  The two halves
+  // then run opposite phases between barriers: while half 0's waves issue
+  // their score MFMAs half 1's run the previous softmax's P.V, and while half 0
+  // runs its softmax half 1 issues score MFMAs, instead of both waves of a SIMD
+  // contending for the same pipe at the same time.
+  short4_t pend_pa[kCB], pend_pb[kCB];  // P of the pending pair
+  bool pend = false, pend_ok_a = true, pend_ok_b = true, pend_vm = false;
+  int pend_tok0 = 0;
+  const uint8_t* pend_buf = nullptr;
   // Consumes one stage from `buf` (this wave's tiles only, two at a time; a pair
   // whose second tile is past the wave's keys has those keys masked), every pair
   // with the mask or every pair without it: one variant per loop body keeps the
-  // register count where two waves fit on a SIMD.
-  auto stage_compute = [&](auto masked, int st, const uint8_t* buf) {
+  // register count where two waves fit on a SIMD.  With `defer` (half 1 of the
+  // key split, one pair per stage) the pair's P.V is left pending.
+  auto stage_compute = [&](auto masked, int st, const uint8_t* buf,
+                           auto defer) __attribute__((always_inline)) {
     // Not unrolled: unrolling lets the compiler hoist every tile's LDS reads
     // (32 registers each) ahead of the first pair's math, and spill.
 #pragma unroll 1
@@ -639,8 +670,23 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D)))) void paged_prefi
         (void)key_row<kPaged>(P, bt_row, k_start, t * kTile, ok_a, pc);
         (void)key_row<kPaged>(P, bt_row, k_start, (t + 1) * kTile, ok_b, pc);
       }
-      pair_step(masked, t * kTile, buf, tt, ok_a, ok_b);
+      if constexpr (decltype(defer)::value) {
+        pend_vm = pair_scores(masked, t * kTile, buf, tt, ok_a, ok_b, pend_pa, pend_pb);
+        pend = true;
+        pend_tok0 = t * kTile;
+        pend_buf = buf;
+        pend_ok_a = ok_a;
+        pend_ok_b = ok_b;
+      } else {
+        short4_t p_a[kCB], p_b[kCB];
+        const bool vm = pair_scores(masked, t * kTile, buf, tt, ok_a, ok_b, p_a, p_b);
+        pair_pv(t * kTile, buf, tt, ok_a, ok_b, vm, p_a, p_b);
+      }
     }
+  };
+  auto run_pending = [&]() __attribute__((always_inline)) {
+    if (pend) pair_pv(pend_tok0, pend_buf, 0, pend_ok_a, pend_ok_b, pend_vm, pend_pa, pend_pb);
+    pend = false;
   };
   // A stage needs no mask when this wave sees all its keys in full (below nfull)
   // and none of its pages is masked.  Called for stage st only when st is the
@@ -652,28 +698,38 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D)))) void paged_prefi
     return staged_ok;
   };
   // One step: wait for stage st's loads (every thread's, through the barrier,
-  // which also frees the other buffer), issue stage st + 1's, consume stage st.
-  // The unmasked and masked stages run in separate loops; every wave passes
-  // exactly nsteps barriers whichever loops it is in.
-  auto step = [&](auto masked, int st) {
+  // which also frees the buffer the next loads go to), issue stage st + 1's,
+  // consume stage st.  The unmasked and masked stages run in separate loops;
+  // every wave passes exactly nsteps barriers whichever loops it is in.
+  auto step = [&](auto masked, int st, auto defer) __attribute__((always_inline)) {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    uint8_t* cur_buf = (st & 1) ? lds1 : lds0;
-    uint8_t* next_buf = (st & 1) ? lds0 : lds1;
-    if (st + 1 < st_hi) stage_load(st + 1, next_buf);
-    stage_compute(masked, st, cur_buf);
+    if constexpr (decltype(defer)::value) run_pending();
+    if (st + 1 < st_hi) stage_load(st + 1, stage_buf(st + 1));
+    stage_compute(masked, st, stage_buf(st), defer);
   };
   // Stages [st0, nstages): under a window, a masked head (keys some query's
   // window starts after), then the unmasked stages, then the masked rest.
-  if (st_lo < st_hi) stage_load(st_lo, (st_lo & 1) ? lds1 : lds0);
-  int st = st_lo;
+  if (st_lo < st_hi) stage_load(st_lo, stage_buf(st_lo));
   const int head_end = win >= 0 ? max(st0, (khead + kStageKeys - 1) / kStageKeys) : st0;
+  auto run_stages = [&](auto defer) __attribute__((always_inline)) {
+    int st = st_lo;
 #pragma unroll 1
-  for (; st < st_hi && st < head_end; ++st) step(std::true_type{}, st);
+    for (; st < st_hi && st < head_end; ++st) step(std::true_type{}, st, defer);
 #pragma unroll 1
-  for (; st < st_hi && stage_unmasked(st); ++st) step(std::false_type{}, st);
+    for (; st < st_hi && stage_unmasked(st); ++st) step(std::false_type{}, st, defer);
 #pragma unroll 1
-  for (; st < st_hi; ++st) step(std::true_type{}, st);
+    for (; st < st_hi; ++st) step(std::true_type{}, st, defer);
+    if constexpr (decltype(defer)::value) run_pending();
+  };
+  if constexpr (kPingPong) {
+    if (half == 1)
+      run_stages(std::true_type{});
+    else
+      run_stages(std::false_type{});
+  } else {
+    run_stages(std::false_type{});
+  }
   // Row maxima and sums of the rows this lane holds (row 4g + i of block nb).
   float m_row[kCB][4], l_row[kCB][4];
 #pragma unroll
