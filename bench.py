@@ -811,8 +811,19 @@ def bench_table(args):
     c3 = workloads.c3_decode(dev)
     c5 = workloads.c5_fp8_decode(dev)
     cpu_legs, oracle_legs = {}, {}
+    # C3's batch and context lengths at the other head shapes the reference builds the
+    # decode op with: Qwen3-Next's full attention (qwen3_next_attention.py:148-150),
+    # Whisper large's (whisper_attention.py:185-190) and a gpt-oss-like group of 8.
+    shapes = (("Qwen3-Next heads", 16, 2, 256), ("Whisper heads", 20, 20, 64),
+              ("gpt-oss-like heads", 64, 8, 64))
     for name, case, splits, nseq in (("C4", dec, 0, 256), ("C3", c3, 0, 64), ("C5", c5, 0, 1),
-                                     ("C5", c5, 16, 0), ("C5", c5, 32, 0), ("C5", c5, 64, 0)):
+                                     ("C5", c5, 16, 0), ("C5", c5, 32, 0), ("C5", c5, 64, 0),
+                                     *((n, (hq_, hk_, d_), 0, 4) for n, hq_, hk_, d_ in shapes)):
+        if isinstance(case, tuple):  # C3's lengths at another head shape
+            del out, ws
+            torch.cuda.empty_cache()
+            case = workloads.c3_decode(dev, num_heads=case[0], kv_heads=case[1],
+                                       head_dim=case[2])
         b, hq, d = case.q.shape
         hk = case.k_cache.shape[2]
         part, nparts, wsb = ops.paged_decode_plan(b, hq, hk, d, case.max_seq_len, splits)
@@ -821,7 +832,8 @@ def bench_table(args):
         if nseq:
             cpu_legs[name], oracle_legs[name] = decode_cpu(case, nseq)
         add(name, f"paged_decode {str(case.k_cache.dtype).replace('torch.', '')} B={b} Hq={hq} "
-                  f"{'balanced' if part == 0 else f'{nparts} partitions'}",
+                  + (f"Hk={hk} D={d} " if d != 128 else "")
+                  + f"{'balanced' if part == 0 else f'{nparts} partitions'}",
             lambda: ops.paged_decode(out, case.q, case.k_cache, case.v_cache, case.block_tables,
                                      case.ctx_lens, case.scale, part, nparts, ws, case.k_scale,
                                      case.v_scale), case.algorithmic_bytes(),
@@ -829,13 +841,19 @@ def bench_table(args):
             parity=lambda name=name, out=out: decode_parity(name, out, oracle_legs[name]))
     # Prefill (FlashAttnPrefill with a block table) at Qwen3-8B heads, with torch's
     # own SDPA (flash backend, dense contiguous K/V) on the same GPU beside it.
-    for label, ql, kl in PREFILL_CASES:
-        q, kc, vc, bt, cu_q, cu_k, mq, flop = prefill_case(dev, ql, kl, workloads.SEED + 11)
+    del case, out, ws
+    torch.cuda.empty_cache()
+    pf_cases = [(label, ql, kl, 32, 8, 128) for label, ql, kl in PREFILL_CASES]
+    pf_cases += [("1x2048 prompt", [2048], [2048], hq_, hk_, d_) for _, hq_, hk_, d_ in shapes[:2]]
+    for label, ql, kl, hq_, hk_, d_ in pf_cases:
+        q, kc, vc, bt, cu_q, cu_k, mq, flop = prefill_case(dev, ql, kl, workloads.SEED + 11,
+                                                           hq_, hk_, d_)
         pout = torch.empty_like(q)
         med, _ = time_call(lambda: ops.paged_prefill(pout, q, kc, vc, bt, cu_q, cu_k, mq,
-                                                     128 ** -0.5, max_seqlen_k=max(kl)),
+                                                     d_ ** -0.5, max_seqlen_k=max(kl)),
                            iters=20, warmup=3, flush=flush)
-        row = {"config": "prefill", "op": f"paged_prefill bf16 Hq=32 Hk=8 {label}",
+        heads = f"Hq={hq_} Hk={hk_}" + (f" D={d_}" if d_ != 128 else "")
+        row = {"config": "prefill", "op": f"paged_prefill bf16 {heads} {label}",
                "us_median": round(med * 1e3, 2), "flop": flop,
                "TFLOPs": round(flop / (med * 1e-3) / 1e12, 1),
                "frac_of_2.5PFLOPs": round(flop / (med * 1e-3) / 2.5e15, 4)}
@@ -894,9 +912,9 @@ PREFILL_CASES = (("1x2048 prompt", [2048], [2048]),
                  ("16x512 prompts", [512] * 16, [512] * 16))
 
 
-def prefill_case(dev, q_lens, k_lens, seed):
-    """Paged prefill inputs at Qwen3-8B heads (Hq 32, Hk 8, head 128, 256-token pages
-    from a seeded permutation), and the FLOPs of the visible (query, key) pairs."""
+def prefill_case(dev, q_lens, k_lens, seed, hq=32, hk=8, d=128):
+    """Paged prefill inputs (default Qwen3-8B heads: Hq 32, Hk 8, head 128; 256-token
+    pages from a seeded permutation), and the FLOPs of the visible (query, key) pairs."""
     import numpy as np
     import torch
 
@@ -912,12 +930,12 @@ def prefill_case(dev, q_lens, k_lens, seed):
         off += p
     cu_q = torch.tensor([0] + list(np.cumsum(q_lens)), dtype=torch.int32, device=dev)
     cu_k = torch.tensor([0] + list(np.cumsum(k_lens)), dtype=torch.int32, device=dev)
-    q = torch.randn(sum(q_lens), 32, 128, generator=g).to(torch.bfloat16).to(dev)
-    kc = torch.randn(nb, bs, 8, 128, generator=g).to(torch.bfloat16).to(dev)
-    vc = torch.randn(nb, bs, 8, 128, generator=g).to(torch.bfloat16).to(dev)
+    q = torch.randn(sum(q_lens), hq, d, generator=g).to(torch.bfloat16).to(dev)
+    kc = torch.randn(nb, bs, hk, d, generator=g).to(torch.bfloat16).to(dev)
+    vc = torch.randn(nb, bs, hk, d, generator=g).to(torch.bfloat16).to(dev)
     visible = sum(sum(max(0, min(kl, kl - ql + j + 1)) for j in range(ql))
                   for ql, kl in zip(q_lens, k_lens))
-    return q, kc, vc, bt.to(dev), cu_q, cu_k, max(q_lens), visible * 32 * 4 * 128
+    return q, kc, vc, bt.to(dev), cu_q, cu_k, max(q_lens), visible * hq * 4 * d
 
 
 def profile_prefill(reps: int = 3):

@@ -724,11 +724,28 @@ struct WaveState {
   }
 };
 
+// Registers held to what two waves per SIMD leave (256 VGPRs + AGPRs): for a
+// work-group of fewer than 8 waves the compiler's own occupancy target would
+// let them grow past it (to 272 at head size 256, one wave per SIMD), and the
+// plans count on up to 8 resident waves per CU.
+#ifndef FK_DECODE_WAVES_PER_EU
+#define FK_DECODE_WAVES_PER_EU 2
+#endif
+// Balanced schedule with fewer than 8 virtual heads (work-groups of fewer than
+// 8 waves, each streaming its own range): waves planned per CU.  Each group is
+// a separate stream through the cache, and four per CU (one wave per SIMD)
+// measured faster than eight: Hq 16 / Hk 2 / head 256 at C3's lengths 122.9 ->
+// 115.7 us, Hq 8 / Hk 1 / head 128 42.6 -> 40.4 us.
+#ifndef FK_DECODE_SMALL_WAVES
+#define FK_DECODE_SMALL_WAVES 4
+#endif
+
 // Fixed partitions: work-group = (partition p, virtual-head group, sequence b);
 // wave w owns virtual head blockIdx.y * NH + w and streams the partition.
 // Partial rows: (b * max_parts + p) * Hq + hq.
 template <int NH, int kG, int D, bool kFp8, int U, bool kStore>
-__global__ __launch_bounds__(NH * 64) void paged_decode_partition_kernel(
+__global__ __launch_bounds__(NH * 64)
+__attribute__((amdgpu_waves_per_eu(FK_DECODE_WAVES_PER_EU))) void paged_decode_partition_kernel(
     DecodeParams P, const int32_t* __restrict__ block_tables, const int32_t* __restrict__ ctx_lens,
     const void* __restrict__ slot_mapping) {
   const int p = blockIdx.x;
@@ -788,7 +805,8 @@ __device__ __forceinline__ int tiles_of(const DecodeParams& P, int ctx) {
 // (w * 2 + slot) * Hq + hq, slot 0 = the group's first segment, slot 1 = its
 // last (a group holds at most one cut sequence at each end).
 template <int NH, int kG, int D, bool kFp8, int U, bool kStore>
-__global__ __launch_bounds__(NH * 64) void paged_decode_balanced_kernel(
+__global__ __launch_bounds__(NH * 64)
+__attribute__((amdgpu_waves_per_eu(FK_DECODE_WAVES_PER_EU))) void paged_decode_balanced_kernel(
     DecodeParams P, const int32_t* __restrict__ block_tables, const int32_t* __restrict__ ctx_lens,
     const void* __restrict__ slot_mapping) {
   extern __shared__ int32_t toff[];  // [batch + 1] tile prefix sums
@@ -1141,7 +1159,8 @@ __global__ __launch_bounds__(kWaves * 64) void paged_decode_balanced_reduce_kern
 
 // Tuning knobs (compile-time): tiles per load set for bf16 pages at head sizes
 // up to 128 (at 256 a tile's loads fill as many registers as two tiles do at
-// 128, so one), and for fp8 pages.
+// 128, so one), and for fp8 pages.  At head size 64, four tiles per set
+// measured +2% on 20 kv heads and -2% on 8 (C3's lengths), so two.
 #ifndef FK_DECODE_CHUNK
 #define FK_DECODE_CHUNK 2
 #endif
@@ -1419,10 +1438,12 @@ extern "C" int fk_paged_decode_plan(int64_t batch, int num_heads, int num_kv_hea
   const int vh = virtual_heads(num_heads, num_kv_heads);
   if (num_splits == 0 && batch <= kMaxBalancedBatch) {
     // Balanced: one work-group per CU for each virtual-head group when a group
-    // fills a CU (8 waves), proportionally more for fewer virtual heads.
+    // fills a CU (8 waves); with fewer virtual heads, work-groups of nh waves
+    // up to FK_DECODE_SMALL_WAVES per CU.
     const int nh = waves_per_group(vh);
     *part_tokens = 0;
-    *max_parts = static_cast<int64_t>(num_cus()) * (kMaxWavesPerGroup / nh);
+    const int waves = nh < kMaxWavesPerGroup ? FK_DECODE_SMALL_WAVES : kMaxWavesPerGroup;
+    *max_parts = static_cast<int64_t>(num_cus()) * (waves > nh ? waves / nh : 1);
   } else {
     int64_t part;
     if (num_splits > 0) {
