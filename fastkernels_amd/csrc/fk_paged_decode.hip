@@ -1321,6 +1321,17 @@ int prepare(const char* name, Launch& L, void* out, int64_t out_row_stride, cons
   L.head_size = head_size;
   const int vh = virtual_heads(num_heads, num_kv_heads);
   L.nh = waves_per_group(vh);
+  if (!balanced) {
+    // Fixed partitions: while the grid holds fewer work-groups than CUs (few
+    // partitions of a small batch), fewer virtual heads per work-group (a
+    // power of two, as the launches take) and more work-groups.
+    while (L.nh > 1 && static_cast<int64_t>(max_parts) * batch * ((vh + L.nh - 1) / L.nh) <
+                           num_cus()) {
+      int p2 = 1;
+      while (2 * p2 < L.nh) p2 *= 2;
+      L.nh = p2;
+    }
+  }
   const unsigned hgroups = static_cast<unsigned>((vh + L.nh - 1) / L.nh);
   L.grid = balanced ? dim3(static_cast<unsigned>(max_parts), hgroups, 1)
                     : dim3(static_cast<unsigned>(max_parts), hgroups, static_cast<unsigned>(batch));
