@@ -50,10 +50,11 @@ namespace {
 #ifndef FK_PREFILL_COLS
 #define FK_PREFILL_COLS 2
 #endif
-// Two waves per SIMD at head sizes up to 128 (two 4-wave work-groups per CU;
-// each holds 32 KB of LDS for bf16 pages at 128); at 256 one column block per
-// wave still needs more than the 256 registers two waves leave, so one.
-constexpr int prefill_waves_per_simd(int D) { return D >= 256 ? 1 : 2; }
+// Two waves per SIMD (two 4-wave work-groups per CU; each holds 32 KB of LDS for
+// bf16 pages at head size 128, 64 KB at 256).  At 256 the bf16 P.V operands go
+// in two halves to fit in the 256 registers two waves leave (fp8 fits as is);
+// dense keys at 256 (the row clamping) would still spill 11 VGPRs, so one.
+constexpr int prefill_waves_per_simd(int D, bool paged) { return D >= 256 && !paged ? 1 : 2; }
 #ifndef FK_PREFILL_LAZY
 #define FK_PREFILL_LAZY 8.0f
 #endif
@@ -237,7 +238,7 @@ __device__ __forceinline__ short4_t lds_v_slice(const uint8_t* buf, int tt, int 
 // kKS = 2: the key split (8 waves; head sizes up to 128).
 template <bool kFp8, bool kPaged, int D, int kKS>
 __global__ __launch_bounds__(kKS * kPrefillWaves * 64)
-__attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D)))) void paged_prefill_kernel(
+__attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D, kPaged)))) void paged_prefill_kernel(
     PrefillParams P, const int32_t* __restrict__ block_tables,
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_k) {
   using S = Stage<kFp8, D>;
@@ -509,6 +510,62 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D)))) void paged_prefi
                      const short4_t (&p_a)[kCB],
                      const short4_t (&p_b)[kCB]) __attribute__((always_inline)) {
     asm volatile("" ::: "memory");  // V reads stay after the score work
+    if constexpr (!kFp8 && D >= 256) {
+      // bf16 at head size 256: the V slices go in two halves (read, mask, MFMAs),
+      // so that half the V operands are live at once and two waves fit on a
+      // SIMD; otherwise as below.
+      constexpr int kDS = D / 32;  // slices per half
+      uint32_t ma[2] = {~0u, ~0u}, mb[2] = {~0u, ~0u};
+      if (vmask) {
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2) {
+          const int k0 = tok0 + 4 * g + 2 * h2;
+          ma[h2] = ((ok_a && k0 < kend) ? 0x0000ffffu : 0u) | ((ok_a && k0 + 1 < kend) ? 0xffff0000u : 0u);
+          mb[h2] = ((ok_b && k0 + kTile < kend) ? 0x0000ffffu : 0u) |
+                   ((ok_b && k0 + kTile + 1 < kend) ? 0xffff0000u : 0u);
+        }
+      }
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        if (hh > 0) asm volatile("" ::: "memory");  // the second half's reads after the first's MFMAs
+        short4_t vba[kDS], vbb[kDS];
+#pragma unroll
+        for (int d = 0; d < kDS; ++d) {
+          vba[d] = lds_v_slice<D>(buf, tt, hh * kDS + d, r, g);
+          vbb[d] = lds_v_slice<D>(buf, tt + 1, hh * kDS + d, r, g);
+        }
+        if (vmask) {
+#pragma unroll
+          for (int d = 0; d < kDS; ++d) {
+            uint2 wa = __builtin_bit_cast(uint2, vba[d]), wb = __builtin_bit_cast(uint2, vbb[d]);
+            wa.x &= ma[0]; wa.y &= ma[1];
+            wb.x &= mb[0]; wb.y &= mb[1];
+            vba[d] = __builtin_bit_cast(short4_t, wa);
+            vbb[d] = __builtin_bit_cast(short4_t, wb);
+          }
+        }
+        __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+        for (int nb = 0; nb < kCB; ++nb) {
+          const bf16x8_t pab = __builtin_bit_cast(
+              bf16x8_t, make_uint4(__builtin_bit_cast(uint2, p_a[nb]).x,
+                                   __builtin_bit_cast(uint2, p_a[nb]).y,
+                                   __builtin_bit_cast(uint2, p_b[nb]).x,
+                                   __builtin_bit_cast(uint2, p_b[nb]).y));
+#pragma unroll
+          for (int d = 0; d < kDS; ++d) {
+            const uint2 va = __builtin_bit_cast(uint2, vba[d]), vb = __builtin_bit_cast(uint2, vbb[d]);
+            const bf16x8_t v8 = __builtin_bit_cast(bf16x8_t, make_uint4(va.x, va.y, vb.x, vb.y));
+            o[nb][hh * kDS + d] =
+                __builtin_amdgcn_mfma_f32_16x16x32_bf16(pab, v8, o[nb][hh * kDS + d], 0, 0, 0);
+          }
+          if (hh == 1)
+            l_acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pab, ones, l_acc[nb], 0, 0, 0);
+        }
+        __builtin_amdgcn_s_setprio(0);
+      }
+      return;
+    }
     short4_t vba[D / 16], vbb[D / 16];  // shared by the column blocks
     if constexpr (!kFp8) {
       // Slice d holds dims 16d .. 16d + 15 (lane r: dim 16d + r).
