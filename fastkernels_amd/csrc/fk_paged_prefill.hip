@@ -235,14 +235,15 @@ __device__ __forceinline__ short4_t lds_v_slice(const uint8_t* buf, int tt, int 
 // times qs = kPrefillWaves / hw blocks of kQTokens query tokens (a group larger
 // than kPrefillWaves heads spans hsplit work-groups).  All waves share the K/V
 // stages; each walks the tiles up to its own last visible key.
-// kKS = 2: the key split (8 waves; head sizes up to 128).
+// kKS = 2: the key split (8 waves; head sizes up to 128, and 256 with paged keys).
 template <bool kFp8, bool kPaged, int D, int kKS>
 __global__ __launch_bounds__(kKS * kPrefillWaves * 64)
 __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D, kPaged)))) void paged_prefill_kernel(
     PrefillParams P, const int32_t* __restrict__ block_tables,
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_k) {
   using S = Stage<kFp8, D>;
-  static_assert(kKS == 1 || (kKS == 2 && D <= 128), "key split: two halves, head size <= 128");
+  static_assert(kKS == 1 || (kKS == 2 && (D <= 128 || kPaged)),
+                "key split: two halves, head size <= 128 (256 with paged keys)");
   constexpr int kCB = col_blocks_for(D);  // 16-query column blocks per wave
   constexpr int kQT = 16 * kCB;           // query tokens per wave
   // Stage buffers (two per half), and with the key split the exchange area
@@ -250,7 +251,8 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D, kPaged)))) void pag
   constexpr int kXFloats = split_exchange_floats<D, kCB>();
   // Key split with one pair per stage: the halves run opposite phases (half 1
   // defers each pair's P.V past the next barrier), three stage buffers a half.
-  constexpr bool kPingPong = kKS > 1 && kStageTiles == 2;
+  // (At head size 256 three buffers a half would not fit in LDS: two, in phase.)
+  constexpr bool kPingPong = kKS > 1 && kStageTiles == 2 && D <= 128;
   constexpr int kBufs = kPingPong ? 3 : 2;
   constexpr int kStageAll = kKS * kBufs * S::kBytes;
   constexpr int kXBytes = kKS > 1 ? kPrefillWaves * kXFloats * 4 : 0;
@@ -903,7 +905,7 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D, kPaged)))) void pag
 template <bool FP8, bool PAGED, int D>
 void launch_prefill(bool split, const PrefillParams& P, dim3 grid, const int32_t* bt,
                     const int32_t* cu_q, const int32_t* cu_k, hipStream_t stream) {
-  if constexpr (D <= 128) {
+  if constexpr (D <= 128 || PAGED) {
     if (split) {
       hipLaunchKernelGGL((paged_prefill_kernel<FP8, PAGED, D, 2>), grid,
                          dim3(2 * kPrefillWaves * 64), 0, stream, P, bt, cu_q, cu_k);
@@ -1021,7 +1023,7 @@ int prefill_entry(const char* name, bool paged, void* out, int64_t out_row_strid
   const bool may_pair = causal && max_seqlen_k > 0 && max_seqlen_k < 2 * max_seqlen_q;
   const int64_t wgs = static_cast<int64_t>(num_kv_heads) * hsplit * batch *
                       (may_pair ? (qblocks + 1) / 2 : qblocks);
-  const bool split = head_size <= 128 && wgs < 2LL * num_cus();
+  const bool split = (head_size <= 128 || paged) && wgs < 2LL * num_cus();
   switch (head_size) {
     case 64: launch_prefill_d<64>(paged, fp8, split, P, grid, block_tables, cu_seqlens_q, cu_seqlens_k, s); break;
     case 256: launch_prefill_d<256>(paged, fp8, split, P, grid, block_tables, cu_seqlens_q, cu_seqlens_k, s); break;
