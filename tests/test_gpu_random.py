@@ -4,9 +4,11 @@ page size, bf16 / fp8 pages, window, sinks, schedule, causal / dense), each
 against the CPU oracle at the same bars (bf16 atol = rtol = 1e-2, fp8 3e-2).
 
 Sizes stay small so that the numpy oracle finishes in seconds; every case prints
-its parameters before it runs.
+its parameters before it runs.  FK_RANDOM_SCALE=k runs k times as many cases.
 """
 from __future__ import annotations
+
+import os
 
 import numpy as np
 import pytest
@@ -17,8 +19,10 @@ from fastkernels_amd import ops, workloads
 
 pytestmark = pytest.mark.gpu
 
-N_DECODE = 120
-N_PREFILL = 80
+# Case counts; FK_RANDOM_SCALE multiplies them for a wider sweep (seeds stay fixed per case).
+_SCALE = max(1, int(os.environ.get("FK_RANDOM_SCALE", "1")))
+N_DECODE = 120 * _SCALE
+N_PREFILL = 80 * _SCALE
 
 
 def _close(got, ref, tol, what):
@@ -169,7 +173,7 @@ def test_random_prefill(cuda, i):
     _close(out, ref, 3e-2 if p["fp8"] else 1e-2, f"random prefill {i} {p}")
 
 
-N_FUSED = 40
+N_FUSED = 40 * _SCALE
 
 
 @pytest.mark.parametrize("i", range(N_FUSED))
