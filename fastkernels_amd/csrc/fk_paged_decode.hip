@@ -731,11 +731,12 @@ struct WaveState {
 #ifndef FK_DECODE_WAVES_PER_EU
 #define FK_DECODE_WAVES_PER_EU 2
 #endif
-// Balanced schedule with fewer than 8 virtual heads (work-groups of fewer than
-// 8 waves, each streaming its own range): waves planned per CU.  Each group is
-// a separate stream through the cache, and four per CU (one wave per SIMD)
-// measured faster than eight: Hq 16 / Hk 2 / head 256 at C3's lengths 122.9 ->
-// 115.7 us, Hq 8 / Hk 1 / head 128 42.6 -> 40.4 us.
+// Balanced schedule with fewer than 8 virtual heads (one work-group of fewer
+// than 8 waves holds every kv head, and streams its own range): work-groups
+// per CU times the kv heads.  A group-count sweep at C3's lengths put the
+// optimum at four kv heads' worth per CU (1 kv head: 4 groups; 2: 2; 4: 1):
+// Hq 16 / Hk 2 / head 256 122.9 -> 115.7 us, Hq 8 / Hk 1 / head 128 42.6 ->
+// 40.4 us, Hq 64 / Hk 2 / head 128 94.3 -> 79.4 us.
 #ifndef FK_DECODE_SMALL_WAVES
 #define FK_DECODE_SMALL_WAVES 4
 #endif
@@ -1448,13 +1449,24 @@ extern "C" int fk_paged_decode_plan(int64_t batch, int num_heads, int num_kv_hea
   const int64_t L = max_seq_len > 0 ? max_seq_len : 1;
   const int vh = virtual_heads(num_heads, num_kv_heads);
   if (num_splits == 0 && batch <= kMaxBalancedBatch) {
-    // Balanced: one work-group per CU for each virtual-head group when a group
-    // fills a CU (8 waves); with fewer virtual heads, work-groups of nh waves
-    // up to FK_DECODE_SMALL_WAVES per CU.
+    // Balanced: one work-group per CU when one group of 8 virtual heads covers
+    // them all; with several full groups, one work-group per CU over all the
+    // groups together (a group count that does not divide evenly, or a last
+    // group with idle waves, keeps one per CU per group).  Fewer than 8
+    // virtual heads make one group of all the kv heads: FK_DECODE_SMALL_WAVES /
+    // num_kv_heads work-groups per CU (at least one).
     const int nh = waves_per_group(vh);
+    const int hgroups = (vh + nh - 1) / nh;
+    const int64_t cus = num_cus();
     *part_tokens = 0;
-    const int waves = nh < kMaxWavesPerGroup ? FK_DECODE_SMALL_WAVES : kMaxWavesPerGroup;
-    *max_parts = static_cast<int64_t>(num_cus()) * (waves > nh ? waves / nh : 1);
+    if (nh < kMaxWavesPerGroup) {
+      const int per = FK_DECODE_SMALL_WAVES / num_kv_heads;
+      *max_parts = cus * (per > 1 ? per : 1);
+    } else if (hgroups > 1 && vh % kMaxWavesPerGroup == 0 && cus % hgroups == 0) {
+      *max_parts = cus / hgroups;
+    } else {
+      *max_parts = cus;
+    }
   } else {
     int64_t part;
     if (num_splits > 0) {
