@@ -83,10 +83,19 @@ def test_plan_host_logic(lib):
     _, n64, ws64 = _native.plan(64, 32, 8, 64, 8192, 0)
     _, n256, ws256 = _native.plan(64, 32, 8, 256, 8192, 0)
     assert n64 == n256 and ws256 - ws64 >= n64 * 2 * 32 * (256 - 64) * 4
-    # groups above 16: one wave per 16 query columns, so fewer work-groups fill a CU
+    # Balanced group counts, relative to C3's (8 kv heads: one work-group per CU).
+    # Fewer than 8 virtual heads: 4 / Hk work-groups per CU, whatever the group size
+    # (a group above 16 query heads takes one wave per 16 query columns).
+    _, n_c3, _ = _native.plan(64, 32, 8, 128, 8192, 0)
     _, n_g32, _ = _native.plan(64, 64, 2, 128, 8192, 0)  # 2 kv heads x 2 column blocks
     _, n_g8, _ = _native.plan(64, 16, 2, 128, 8192, 0)   # 2 kv heads x 1 column block
-    assert n_g8 == 2 * n_g32
+    assert n_g8 == n_g32 == 2 * n_c3
+    assert _native.plan(64, 8, 1, 128, 8192, 0)[1] == 4 * n_c3
+    assert _native.plan(64, 16, 4, 128, 8192, 0)[1] == n_c3
+    # Several full groups of 8 virtual heads: one work-group per CU over all of them;
+    # a last group with idle waves keeps one per CU per group.
+    assert _native.plan(16, 32, 32, 128, 8192, 0)[1] * 4 == n_c3
+    assert _native.plan(64, 20, 20, 64, 8192, 0)[1] == n_c3
     with pytest.raises(_native.FkError, match="head_size"):
         _native.plan(64, 32, 8, 96, 8192, 0)
     with pytest.raises(_native.FkError):
