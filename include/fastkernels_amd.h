@@ -223,7 +223,7 @@ int fk_paged_decode_reduce(void* out, int64_t out_row_stride, const void* q,
  * rejected with FK_ERR_WORKSPACE (use fk_paged_decode then).  Nothing is allocated.
  * Every call on one device shares the array: calls that overlap on one device
  * (concurrent streams or host threads) race on it and must be serialised by the caller. */
-#define FK_PAGED_DECODE_NOALLOC_MAX_BYTES (32LL << 20)
+#define FK_PAGED_DECODE_NOALLOC_MAX_BYTES (64LL << 20)
 int fk_paged_decode_noalloc(void* out, int64_t out_row_stride, const void* q,
                             int64_t q_row_stride, const void* k_cache, const void* v_cache,
                             int kv_dtype, const float* k_scale, const float* v_scale,

@@ -57,7 +57,7 @@ def test_noalloc_matches_workspace_entry_point_twice(cuda, num_splits):
     print(f"noalloc: C3 then small batch, num_splits={num_splits}", flush=True)
     big = workloads.c3_decode(cuda, seed=200)
     ref_big, plan = _with_workspace(big, num_splits)
-    assert plan.workspace_bytes <= 32 << 20  # FK_PAGED_DECODE_NOALLOC_MAX_BYTES
+    assert plan.workspace_bytes <= 64 << 20  # FK_PAGED_DECODE_NOALLOC_MAX_BYTES
     got_big = _noalloc(big, num_splits)
     assert torch.equal(got_big, ref_big)
     small = workloads.c3_decode(cuda, batch=5, num_heads=16, kv_heads=4, pool_blocks=128,
