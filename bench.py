@@ -843,17 +843,28 @@ def bench_table(args):
     # own SDPA (flash backend, dense contiguous K/V) on the same GPU beside it.
     del case, out, ws
     torch.cuda.empty_cache()
-    pf_cases = [(label, ql, kl, 32, 8, 128) for label, ql, kl in PREFILL_CASES]
-    pf_cases += [("1x2048 prompt", [2048], [2048], hq_, hk_, d_) for _, hq_, hk_, d_ in shapes[:2]]
-    for label, ql, kl, hq_, hk_, d_ in pf_cases:
+    pf_cases = [(label, ql, kl, 32, 8, 128, False) for label, ql, kl in PREFILL_CASES]
+    pf_cases += [("1x2048 prompt", [2048], [2048], hq_, hk_, d_, False)
+                 for _, hq_, hk_, d_ in shapes[:2]]
+    # fp8 e4m3fn pages (per-kv-head scales), dequantised exactly in the kernel.
+    pf_cases += [(label, ql, kl, 32, 8, 128, True) for label, ql, kl in PREFILL_CASES[:2]]
+    for label, ql, kl, hq_, hk_, d_, fp8 in pf_cases:
         q, kc, vc, bt, cu_q, cu_k, mq, flop = prefill_case(dev, ql, kl, workloads.SEED + 11,
                                                            hq_, hk_, d_)
+        ks = vs = None
+        if fp8:
+            gs = torch.Generator().manual_seed(workloads.SEED + 13)
+            ks = (0.01 + 0.09 * torch.rand(hk_, generator=gs)).float().to(dev)
+            vs = (0.01 + 0.09 * torch.rand(hk_, generator=gs)).float().to(dev)
+            kc = workloads.quantize_fp8(kc.float(), ks)
+            vc = workloads.quantize_fp8(vc.float(), vs)
         pout = torch.empty_like(q)
         med, _ = time_call(lambda: ops.paged_prefill(pout, q, kc, vc, bt, cu_q, cu_k, mq,
-                                                     d_ ** -0.5, max_seqlen_k=max(kl)),
+                                                     d_ ** -0.5, ks, vs, max_seqlen_k=max(kl)),
                            iters=20, warmup=3, flush=flush)
         heads = f"Hq={hq_} Hk={hk_}" + (f" D={d_}" if d_ != 128 else "")
-        row = {"config": "prefill", "op": f"paged_prefill bf16 {heads} {label}",
+        row = {"config": "prefill",
+               "op": f"paged_prefill {'fp8' if fp8 else 'bf16'} {heads} {label}",
                "us_median": round(med * 1e3, 2), "flop": flop,
                "TFLOPs": round(flop / (med * 1e-3) / 1e12, 1),
                "frac_of_2.5PFLOPs": round(flop / (med * 1e-3) / 2.5e15, 4)}

@@ -68,6 +68,11 @@ constexpr int kPrefillWaves = 4;               // waves per work-group
 #ifndef FK_PREFILL_STAGE
 #define FK_PREFILL_STAGE 32
 #endif
+// fp8 pages: each stage converted once into bf16 LDS buffers (1), or every
+// wave dequantising the K / V bytes it reads (0).
+#ifndef FK_PREFILL_FP8_CONVERT
+#define FK_PREFILL_FP8_CONVERT 1
+#endif
 // Keys per LDS stage (a multiple of 32).  Measured on MI355X (bf16, 1x2048,
 // 4x512 over 4096, 16x512 prompts): 32 keys 102 / 220 / 89 us against 117 /
 // 244 / 99 us for 64; again with the current loop, 88 / 187 / 83 against
@@ -242,6 +247,15 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D, kPaged)))) void pag
     PrefillParams P, const int32_t* __restrict__ block_tables,
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_k) {
   using S = Stage<kFp8, D>;
+  // fp8 pages: the work-group converts each staged stage once into a bf16
+  // stage (float(x) * scale rounded to bf16, the value each wave would form),
+  // and the waves compute on bf16 tiles, instead of each wave dequantising the
+  // same K / V bytes for its own query head.  Up to head size 128: at 256 the
+  // bf16 buffers would not fit beside the fp8 ones with the key split, and the
+  // bf16 tile path needs more registers than two waves per SIMD leave.
+  constexpr bool kConv = kFp8 && FK_PREFILL_FP8_CONVERT && D <= 128;
+  constexpr bool kFp8T = kFp8 && !kConv;  // fp8 tiles in the compute path
+  using SB = Stage<kFp8T, D>;             // the layout the compute path reads
   static_assert(kKS == 1 || (kKS == 2 && (D <= 128 || kPaged)),
                 "key split: two halves, head size <= 128 (256 with paged keys)");
   constexpr int kCB = col_blocks_for(D);  // 16-query column blocks per wave
@@ -252,9 +266,10 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D, kPaged)))) void pag
   // Key split with one pair per stage: the halves run opposite phases (half 1
   // defers each pair's P.V past the next barrier), three stage buffers a half.
   // (At head size 256 three buffers a half would not fit in LDS: two, in phase.)
-  constexpr bool kPingPong = kKS > 1 && kStageTiles == 2 && D <= 128;
+  constexpr bool kPingPong = kKS > 1 && kStageTiles == 2 && D <= 128 && !kConv;
   constexpr int kBufs = kPingPong ? 3 : 2;
-  constexpr int kStageAll = kKS * kBufs * S::kBytes;
+  constexpr int kHalfBytes = kBufs * (S::kBytes + (kConv ? SB::kBytes : 0));  // a half's buffers
+  constexpr int kStageAll = kKS * kHalfBytes;
   constexpr int kXBytes = kKS > 1 ? kPrefillWaves * kXFloats * 4 : 0;
   __shared__ __align__(16) uint8_t lds_all[kStageAll > kXBytes ? kStageAll : kXBytes];
   // Grid: x = kv head (x hsplit), y = sequence, z = query block.  The block
@@ -286,10 +301,16 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D, kPaged)))) void pag
   const int wave_id = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int half = kKS > 1 ? wave_id / kPrefillWaves : 0;  // key-split half
   const int wave = wave_id & (kPrefillWaves - 1);           // role within the half
-  uint8_t* const lds_half = lds_all + half * kBufs * S::kBytes;
+  uint8_t* const lds_half = lds_all + half * kHalfBytes;
   // Stage st's buffer: two alternate; with three, stage st mod 3.
   auto stage_buf = [&](int st) {
     return lds_half + (kBufs == 2 ? (st & 1) : st % kBufs) * S::kBytes;
+  };
+  // The buffer the compute path reads stage st from: the staged one, or with
+  // kConv its bf16 conversion.
+  auto comp_buf = [&](int st) {
+    if constexpr (kConv) return lds_half + kBufs * S::kBytes + (st & 1) * SB::kBytes;
+    else return stage_buf(st);
   };
   const int lane = threadIdx.x & 63;
   const int r = lane & 15;
@@ -346,7 +367,7 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D, kPaged)))) void pag
                          static_cast<int64_t>(hq) * D;
 #pragma unroll
     for (int c = 0; c < D / 32; ++c) {
-      const int d0 = kFp8 ? (D / 4) * g + 8 * c : 32 * c + 8 * g;
+      const int d0 = kFp8T ? (D / 4) * g + 8 * c : 32 * c + 8 * g;
       const uint4 v = ok ? *reinterpret_cast<const uint4*>(qp + d0) : make_uint4(0, 0, 0, 0);
       qb[nb][c] = __builtin_bit_cast(bf16x8_t, v);
     }
@@ -401,7 +422,7 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D, kPaged)))) void pag
                          bool ok_b, short4_t (&p_a)[kCB],
                          short4_t (&p_b)[kCB]) __attribute__((always_inline)) {
     constexpr bool kMasked = decltype(masked)::value;
-    DTile<kFp8, D> ta, tb;
+    DTile<kFp8T, D> ta, tb;
     // Scores of tile a for every column block, then tile b's K is read: the two
     // K tiles are never live at once (20 fewer VGPRs in the compiler's own
     // allocation; measured 1% faster).
@@ -411,7 +432,7 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D, kPaged)))) void pag
     // 174.3 -> 168.7 us; the shorter cases unchanged).
     __builtin_amdgcn_s_setprio(1);
     {
-      lds_tile_k<kFp8, D>(buf, tt, r, g, ta);
+      lds_tile_k<kFp8T, D>(buf, tt, r, g, ta);
       uint4 ka[D / 32];
       k_chunks_d(ta, ka, ks);
 #pragma unroll
@@ -419,7 +440,7 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D, kPaged)))) void pag
     }
     asm volatile("" ::: "memory");  // tile b's K reads stay after tile a's
     {
-      lds_tile_k<kFp8, D>(buf, tt + 1, r, g, tb);
+      lds_tile_k<kFp8T, D>(buf, tt + 1, r, g, tb);
       uint4 kb[D / 32];
       k_chunks_d(tb, kb, ks);
 #pragma unroll
@@ -512,7 +533,7 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D, kPaged)))) void pag
                      const short4_t (&p_a)[kCB],
                      const short4_t (&p_b)[kCB]) __attribute__((always_inline)) {
     asm volatile("" ::: "memory");  // V reads stay after the score work
-    if constexpr (!kFp8 && D >= 256) {
+    if constexpr (!kFp8T && D >= 256) {
       // bf16 at head size 256: the V slices go in two halves (read, mask, MFMAs),
       // so that half the V operands are live at once and two waves fit on a
       // SIMD; otherwise as below.
@@ -569,7 +590,7 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D, kPaged)))) void pag
       return;
     }
     short4_t vba[D / 16], vbb[D / 16];  // shared by the column blocks
-    if constexpr (!kFp8) {
+    if constexpr (!kFp8T) {
       // Slice d holds dims 16d .. 16d + 15 (lane r: dim 16d + r).
 #pragma unroll
       for (int d = 0; d < D / 16; ++d) {
@@ -597,9 +618,9 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D, kPaged)))) void pag
       }
     } else {
       // Slice d holds dims (D/16) r + d (lane r), packed from the row loads.
-      DTile<kFp8, D> ta, tb;
-      lds_tile_v<kFp8, D>(buf, tt, r, g, ta);
-      lds_tile_v<kFp8, D>(buf, tt + 1, r, g, tb);
+      DTile<kFp8T, D> ta, tb;
+      lds_tile_v<kFp8T, D>(buf, tt, r, g, ta);
+      lds_tile_v<kFp8T, D>(buf, tt + 1, r, g, tb);
       bool keep_a[4], keep_b[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -657,9 +678,10 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D, kPaged)))) void pag
     const int64_t rb = which ? P.v_row_bytes : P.k_row_bytes;
     lane_off[i] = static_cast<uint32_t>((row & 15) * rb + head_off + 16 * q);
   }
-  // Whether every page of the stage staged last is readable (the unmasked loop's
-  // test for that stage, so it needs no page lookups of its own).
-  bool staged_ok = true;
+  // Whether every page of a stage is readable, for the last two stages staged
+  // (by stage parity): the unmasked loop's test for that stage, so it needs no
+  // page lookups of its own.
+  bool staged_ok[2] = {true, true};
   auto stage_load = [&](int st, uint8_t* buf) {
     // Wave-uniform (the buffer is the half's); readfirstlane keeps it in an SGPR
     // for M0 where the compiler cannot prove it.
@@ -673,7 +695,7 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D, kPaged)))) void pag
       row0[tt] = key_row<kPaged>(P, bt_row, k_start, st * kStageKeys + tt * kTile, ok, pc);
       all_ok = all_ok && ok;
     }
-    staged_ok = all_ok;
+    staged_ok[st & 1] = all_ok;
 #pragma unroll
     for (int i = 0; i < S::kLoads; ++i) {
       const int pos0 = 64 * (kPrefillWaves * i + wave);  // wave-uniform
@@ -748,28 +770,72 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D, kPaged)))) void pag
     pend = false;
   };
   // A stage needs no mask when this wave sees all its keys in full (below nfull)
-  // and none of its pages is masked.  Called for stage st only when st is the
-  // stage staged last (the loop below tests stage st after step(st - 1), or
-  // after the first stage_load), so its page test is staged_ok.
+  // and none of its pages is masked.  Called for stage st before step(st): the
+  // stages staged by then are st and st + 1 at most (st + 2 is staged inside
+  // step(st)), so staged_ok[st & 1] is stage st's page test.
   auto stage_unmasked = [&](int st) {
     if ((st + 1) * kStageTiles > nfull) return false;
     if (win >= 0 && st * kStageKeys < khead) return false;
-    return staged_ok;
+    return staged_ok[st & 1];
+  };
+  // kConv: stage st's fp8 rows into its bf16 buffer, the chunks spread over the
+  // threads of the half.  fp8 chunk q of a row (dims 16q .. 16q + 15) becomes
+  // bf16 chunks 2q and 2q + 1 of the row, in the bf16 stage layout.
+  auto stage_convert = [&](int st) {
+    if constexpr (kConv) {
+      constexpr int kRowChunks = kStageKeys * S::kChunks;  // fp8 chunks of K (or V)
+      constexpr int kThreads = kPrefillWaves * 64;
+      const uint8_t* fbuf = stage_buf(st);
+      uint8_t* bbuf = comp_buf(st);
+      const int tid = threadIdx.x & (kThreads - 1);
+#pragma unroll
+      for (int c0 = 0; c0 < 2 * kRowChunks; c0 += kThreads) {
+        const int c = c0 + tid;
+        const int which = c / kRowChunks;  // 0: K, 1: V
+        const int rem = c - which * kRowChunks;
+        const int row = rem / S::kChunks;
+        const int q = rem - row * S::kChunks;
+        const uint4 x = *reinterpret_cast<const uint4*>(fbuf + S::offset(which, row, q));
+        const float sc = which ? vsc : ks;
+        const uint2 a = fp8x4_to_bf16x4(x.x, sc), b = fp8x4_to_bf16x4(x.y, sc);
+        const uint2 e = fp8x4_to_bf16x4(x.z, sc), f = fp8x4_to_bf16x4(x.w, sc);
+        *reinterpret_cast<uint4*>(bbuf + SB::offset(which, row, 2 * q)) = make_uint4(a.x, a.y, b.x, b.y);
+        *reinterpret_cast<uint4*>(bbuf + SB::offset(which, row, 2 * q + 1)) =
+            make_uint4(e.x, e.y, f.x, f.y);
+      }
+    }
   };
   // One step: wait for stage st's loads (every thread's, through the barrier,
   // which also frees the buffer the next loads go to), issue stage st + 1's,
   // consume stage st.  The unmasked and masked stages run in separate loops;
   // every wave passes exactly nsteps barriers whichever loops it is in.
+  // kConv: stage st + 1's loads landed (the wait and the barrier), so it is
+  // converted, and stage st + 2 is staged into the fp8 buffer stage st held
+  // (converted in the step before); stage st is read from its bf16 buffer.
   auto step = [&](auto masked, int st, auto defer) __attribute__((always_inline)) {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if constexpr (decltype(defer)::value) run_pending();
-    if (st + 1 < st_hi) stage_load(st + 1, stage_buf(st + 1));
-    stage_compute(masked, st, stage_buf(st), defer);
+    if constexpr (kConv) {
+      if (st + 1 < st_hi) stage_convert(st + 1);
+      if (st + 2 < st_hi) stage_load(st + 2, stage_buf(st + 2));
+    } else {
+      if (st + 1 < st_hi) stage_load(st + 1, stage_buf(st + 1));
+    }
+    stage_compute(masked, st, comp_buf(st), defer);
   };
   // Stages [st0, nstages): under a window, a masked head (keys some query's
   // window starts after), then the unmasked stages, then the masked rest.
   if (st_lo < st_hi) stage_load(st_lo, stage_buf(st_lo));
+  if constexpr (kConv) {
+    // The first stage converted before the loop, the second staged; every wave
+    // of the work-group passes this barrier (with the key split the halves'
+    // ranges differ, one may be empty).
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (st_lo < st_hi) stage_convert(st_lo);
+    if (st_lo + 1 < st_hi) stage_load(st_lo + 1, stage_buf(st_lo + 1));
+  }
   const int head_end = win >= 0 ? max(st0, (khead + kStageKeys - 1) / kStageKeys) : st0;
   auto run_stages = [&](auto defer) __attribute__((always_inline)) {
     int st = st_lo;
@@ -863,7 +929,7 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D, kPaged)))) void pag
       const float f = l > 0.f ? 1.f / l : 0.f;
       uint16_t* orow = P.out + static_cast<int64_t>(q_start + jr) * P.out_row_stride +
                        static_cast<int64_t>(hq) * D;
-      if constexpr (!kFp8) {
+      if constexpr (!kFp8T) {
         // o[nb][d] holds dim 16d + r: lanes r = 0..15 write 16 adjacent dims.
 #pragma unroll
         for (int d = 0; d < D / 16; ++d)
