@@ -260,12 +260,15 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D, kPaged)))) void pag
                 "key split: two halves, head size <= 128 (256 with paged keys)");
   constexpr int kCB = col_blocks_for(D);  // 16-query column blocks per wave
   constexpr int kQT = 16 * kCB;           // query tokens per wave
-  // Stage buffers (two per half), and with the key split the exchange area
-  // that reuses them once the last stage is consumed.
+  // Stage buffers (two or three per half; with kConv a bf16 buffer beside each
+  // fp8 one), and with the key split the exchange area that reuses them once
+  // the last stage is consumed.
   constexpr int kXFloats = split_exchange_floats<D, kCB>();
   // Key split with one pair per stage: the halves run opposite phases (half 1
   // defers each pair's P.V past the next barrier), three stage buffers a half.
-  // (At head size 256 three buffers a half would not fit in LDS: two, in phase.)
+  // (At head size 256 three buffers a half would not fit in LDS, nor with the
+  // fp8 stage conversion, whose bf16 buffers come beside the fp8 ones: two, in
+  // phase.)
   constexpr bool kPingPong = kKS > 1 && kStageTiles == 2 && D <= 128 && !kConv;
   constexpr int kBufs = kPingPong ? 3 : 2;
   constexpr int kHalfBytes = kBufs * (S::kBytes + (kConv ? SB::kBytes : 0));  // a half's buffers
