@@ -250,11 +250,14 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D, kPaged)))) void pag
   // fp8 pages: the work-group converts each staged stage once into a bf16
   // stage (float(x) * scale rounded to bf16, the value each wave would form),
   // and the waves compute on bf16 tiles, instead of each wave dequantising the
-  // same K / V bytes for its own query head.  Up to head size 128: at 256 the
-  // bf16 buffers would not fit beside the fp8 ones with the key split, and the
-  // bf16 tile path needs more registers than two waves per SIMD leave.
+  // same K / V bytes for its own query head.  Up to head size 128 each fp8
+  // buffer has its bf16 one (kConv); at 256 two of those would not fit in LDS
+  // with two work-groups per CU, so one bf16 buffer serves the stages in turn
+  // (kConv1: converted after every wave is done with the stage before, a second
+  // barrier per stage).
   constexpr bool kConv = kFp8 && FK_PREFILL_FP8_CONVERT && D <= 128;
-  constexpr bool kFp8T = kFp8 && !kConv;  // fp8 tiles in the compute path
+  constexpr bool kConv1 = kFp8 && FK_PREFILL_FP8_CONVERT && D > 128;
+  constexpr bool kFp8T = kFp8 && !kConv && !kConv1;  // fp8 tiles in the compute path
   using SB = Stage<kFp8T, D>;             // the layout the compute path reads
   static_assert(kKS == 1 || (kKS == 2 && (D <= 128 || kPaged)),
                 "key split: two halves, head size <= 128 (256 with paged keys)");
@@ -271,7 +274,8 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D, kPaged)))) void pag
   // phase.)
   constexpr bool kPingPong = kKS > 1 && kStageTiles == 2 && D <= 128 && !kConv;
   constexpr int kBufs = kPingPong ? 3 : 2;
-  constexpr int kHalfBytes = kBufs * (S::kBytes + (kConv ? SB::kBytes : 0));  // a half's buffers
+  constexpr int kHalfBytes =  // a half's buffers
+      kBufs * (S::kBytes + (kConv ? SB::kBytes : 0)) + (kConv1 ? SB::kBytes : 0);
   constexpr int kStageAll = kKS * kHalfBytes;
   constexpr int kXBytes = kKS > 1 ? kPrefillWaves * kXFloats * 4 : 0;
   __shared__ __align__(16) uint8_t lds_all[kStageAll > kXBytes ? kStageAll : kXBytes];
@@ -313,6 +317,7 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D, kPaged)))) void pag
   // kConv its bf16 conversion.
   auto comp_buf = [&](int st) {
     if constexpr (kConv) return lds_half + kBufs * S::kBytes + (st & 1) * SB::kBytes;
+    else if constexpr (kConv1) return lds_half + kBufs * S::kBytes;
     else return stage_buf(st);
   };
   const int lane = threadIdx.x & 63;
@@ -785,7 +790,7 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D, kPaged)))) void pag
   // threads of the half.  fp8 chunk q of a row (dims 16q .. 16q + 15) becomes
   // bf16 chunks 2q and 2q + 1 of the row, in the bf16 stage layout.
   auto stage_convert = [&](int st) {
-    if constexpr (kConv) {
+    if constexpr (kConv || kConv1) {
       constexpr int kRowChunks = kStageKeys * S::kChunks;  // fp8 chunks of K (or V)
       constexpr int kThreads = kPrefillWaves * 64;
       const uint8_t* fbuf = stage_buf(st);
@@ -822,15 +827,20 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D, kPaged)))) void pag
     if constexpr (kConv) {
       if (st + 1 < st_hi) stage_convert(st + 1);
       if (st + 2 < st_hi) stage_load(st + 2, stage_buf(st + 2));
-    } else {
+    } else if constexpr (!kConv1) {
       if (st + 1 < st_hi) stage_load(st + 1, stage_buf(st + 1));
     }
     stage_compute(masked, st, comp_buf(st), defer);
+    if constexpr (kConv1) {
+      __syncthreads();  // every wave is done with the bf16 buffer
+      if (st + 1 < st_hi) stage_convert(st + 1);
+      if (st + 2 < st_hi) stage_load(st + 2, stage_buf(st + 2));
+    }
   };
   // Stages [st0, nstages): under a window, a masked head (keys some query's
   // window starts after), then the unmasked stages, then the masked rest.
   if (st_lo < st_hi) stage_load(st_lo, stage_buf(st_lo));
-  if constexpr (kConv) {
+  if constexpr (kConv || kConv1) {
     // The first stage converted before the loop, the second staged; every wave
     // of the work-group passes this barrier (with the key split the halves'
     // ranges differ, one may be empty).
@@ -872,6 +882,7 @@ __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D, kPaged)))) void pag
     for (int k = st_hi - st_lo; k < nsteps; ++k) {  // the shorter half's empty steps
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
+      if constexpr (kConv1) __syncthreads();
     }
     __syncthreads();  // every wave is done with the stage buffers
     // Exchange area of this wave role: O tiles, row sums, column maxima.
