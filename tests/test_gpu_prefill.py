@@ -213,6 +213,28 @@ def test_paged_prefill_qwen3_prompt_2048(cuda):
     _close(got, ref.transpose(0, 1).cpu().numpy(), 1e-2, "2048 prompt")
 
 
+@pytest.mark.parametrize("hq,hk,d", [(32, 8, 128), (16, 2, 256)])
+def test_paged_prefill_fp8_prompt_2048(cuda, hq, hk, d):
+    """One 2048-token prompt on fp8 pages (the key split, with the stages converted to
+    bf16 in LDS), Qwen3-8B and Qwen3-Next heads: against torch fp32 causal attention on
+    K / V dequantised as the reference does (float(x) * scale rounded to bf16)."""
+    _flush(f"paged prefill fp8 2048-token prompt Hq={hq} Hk={hk} D={d} vs torch fp32")
+    c = _case(cuda, [2048], [2048], hq=hq, hk=hk, bs=256, seed=78, fp8=True, d=d)
+    got = _run(c)
+    ids = c["bt"][0, :8].long()
+
+    def deq(cache, scale):
+        x = cache[ids].float().reshape(2048, hk, d) * scale.view(1, hk, 1)
+        return x.to(torch.bfloat16).float().repeat_interleave(hq // hk, dim=1).transpose(0, 1)
+
+    kf = deq(c["kc"], c["ks"]).contiguous()
+    vf = deq(c["vc"], c["vs"]).contiguous()
+    qf = c["q"].float().transpose(0, 1)
+    ref = torch.nn.functional.scaled_dot_product_attention(qf, kf, vf, is_causal=True,
+                                                           scale=d ** -0.5)
+    _close(got, ref.transpose(0, 1).cpu().numpy(), 3e-2, f"fp8 2048 prompt D={d}")
+
+
 @pytest.mark.parametrize("fp8", [False, True])
 def test_paged_prefill_deterministic(cuda, fp8):
     """The same call repeated gives bit-identical outputs (causal chunks, masked and
