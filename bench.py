@@ -57,6 +57,9 @@ def _parse():
     ap.add_argument("--profile-prefill", action="store_true",
                     help="the table's prefill cases after a cache flush, for rocprofv3")
     ap.add_argument("--seed", type=int, default=200)
+    ap.add_argument("--block-size", type=int, default=256,
+                    help="C3's page size in tokens (the pool keeps C3's 1 GiB per cache: "
+                         "4096 * 256 / block_size pages)")
     return ap.parse_args()
 
 
@@ -280,7 +283,8 @@ def bench_decode(args):
     from fastkernels_amd import ops, workloads
 
     dev = torch.device("cuda:0")
-    case = workloads.c3_decode(dev, seed=args.seed)
+    case = workloads.c3_decode(dev, seed=args.seed, block_size=args.block_size,
+                               pool_blocks=4096 * 256 // args.block_size)
     b, hq, d = case.q.shape
     hk = case.k_cache.shape[2]
     part, nparts, wsb = ops.paged_decode_plan(b, hq, hk, d, case.max_seq_len, args.num_splits)
@@ -365,7 +369,7 @@ def bench_decode(args):
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": _committed_traffic(
                 "paged_decode_balanced_kernel" if part == 0 else "paged_decode_partition_kernel",
-                part) if args.seed == 200 else None,
+                part, case.k_cache.shape[1]) if args.seed == 200 else None,
             "traffic_source": "profiles/paged_decode_c3_traffic.json (rocprofv3 FETCH_SIZE/WRITE_SIZE, copy-calibrated)",
             "avg_kernel_us": round(kavg * 1e3, 2),
             "kernel_samples": len(kern_ms),
@@ -410,15 +414,17 @@ def _graph_replay_us(call, replays: int) -> float:
     return us
 
 
-def _committed_traffic(kernel: str, part: int):
+def _committed_traffic(kernel: str, part: int, block_size: int = 256):
     """HBM bytes per launch of the dominant kernel from the committed rocprof PMC
-    summary (profiles/paged_decode_c3_traffic.json), if it covers this kernel."""
+    summary (profiles/paged_decode_c3_traffic.json), if it covers this kernel and page
+    size."""
     path = ROOT / "profiles" / "paged_decode_c3_traffic.json"
     try:
         d = json.loads(path.read_text())
     except (OSError, ValueError):
         return None
-    if d.get("workload") != "C3" or d.get("part_tokens") != part or kernel not in d.get("kernel", ""):
+    if (d.get("workload") != "C3" or d.get("part_tokens") != part
+            or kernel not in d.get("kernel", "") or d.get("block_size", 256) != block_size):
         return None
     return d.get("traffic_bytes")
 
@@ -816,14 +822,20 @@ def bench_table(args):
     # Whisper large's (whisper_attention.py:185-190) and a gpt-oss-like group of 8.
     shapes = (("Qwen3-Next heads", 16, 2, 256), ("Whisper heads", 20, 20, 64),
               ("gpt-oss-like heads", 64, 8, 64))
+    # C3 at the page sizes the reference engine picks besides 256: 16 tokens
+    # (AttnBackendConfig.auto_detect for capability major 9, infra/context.py:68-73,
+    # which PyTorch-ROCm reports for gfx950) and 64, over a pool of the same bytes.
+    pages = (("C3 16-token pages", 16), ("C3 64-token pages", 64))
     for name, case, splits, nseq in (("C4", dec, 0, 256), ("C3", c3, 0, 64), ("C5", c5, 0, 1),
                                      ("C5", c5, 16, 0), ("C5", c5, 32, 0), ("C5", c5, 64, 0),
-                                     *((n, (hq_, hk_, d_), 0, 4) for n, hq_, hk_, d_ in shapes)):
-        if isinstance(case, tuple):  # C3's lengths at another head shape
+                                     *((n, (32, 8, 128, bs_), 0, 4) for n, bs_ in pages),
+                                     *((n, (hq_, hk_, d_, 256), 0, 4) for n, hq_, hk_, d_ in shapes)):
+        if isinstance(case, tuple):  # C3's lengths at another head shape or page size
             del out, ws
             torch.cuda.empty_cache()
             case = workloads.c3_decode(dev, num_heads=case[0], kv_heads=case[1],
-                                       head_dim=case[2])
+                                       head_dim=case[2], block_size=case[3],
+                                       pool_blocks=4096 * 256 // case[3])
         b, hq, d = case.q.shape
         hk = case.k_cache.shape[2]
         part, nparts, wsb = ops.paged_decode_plan(b, hq, hk, d, case.max_seq_len, splits)
@@ -833,6 +845,7 @@ def bench_table(args):
             cpu_legs[name], oracle_legs[name] = decode_cpu(case, nseq)
         add(name, f"paged_decode {str(case.k_cache.dtype).replace('torch.', '')} B={b} Hq={hq} "
                   + (f"Hk={hk} D={d} " if d != 128 else "")
+                  + (f"block={case.k_cache.shape[1]} " if case.k_cache.shape[1] != 256 else "")
                   + f"{'balanced' if part == 0 else f'{nparts} partitions'}",
             lambda: ops.paged_decode(out, case.q, case.k_cache, case.v_cache, case.block_tables,
                                      case.ctx_lens, case.scale, part, nparts, ws, case.k_scale,

@@ -628,7 +628,7 @@ _LIB.define("paged_decode(Tensor(a!) out, Tensor q, Tensor k_cache, Tensor v_cac
 _LIB.define("store_paged_decode(Tensor(a!) out, Tensor q, Tensor key, Tensor value, "
             "Tensor(b!) k_cache, Tensor(c!) v_cache, Tensor slot_mapping, Tensor block_table, "
             "Tensor cache_seqlens, float softmax_scale, int part_tokens, int max_parts, "
-            "Tensor? workspace, Tensor? k_scale=None, Tensor? v_scale=None, "
+            "Tensor(d!)? workspace, Tensor? k_scale=None, Tensor? v_scale=None, "
             "int window_left=-1, Tensor? sinks=None) -> ()")
 _LIB.define("qk_norm_rope_store(Tensor positions, Tensor(a!) query, Tensor(b!) key, "
             "Tensor value, Tensor(c!) k_cache, Tensor(d!) v_cache, Tensor slot_mapping, "

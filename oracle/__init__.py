@@ -226,11 +226,20 @@ def gather_seq(cache: np.ndarray, block_row: np.ndarray, length: int) -> np.ndar
 
 def dequant_kv(cache: np.ndarray, scale: np.ndarray | None, q_dtype: str) -> np.ndarray:
     """fp8 per-(kv head) dequant: cast(float(x) * scale) to the query dtype
-    (_cast_kv_tile, triton_unified_attention.py:64-67).  Non-fp8 caches pass through."""
+    (_cast_kv_tile, triton_unified_attention.py:64-67).  Non-fp8 caches pass through.
+    `scale` is one value per kv head, or a single per-tensor value (the reference's
+    FP8_PER_TENSOR mode, kv_quant_mode.py:20) broadcast to every head."""
     if cache.dtype != np.uint8:
         return np.asarray(cache, np.float32)
     hk = cache.shape[2]
-    sc = np.ones(hk, np.float32) if scale is None else np.asarray(scale, np.float32).reshape(hk)
+    if scale is None:
+        sc = np.ones(hk, np.float32)
+    else:
+        sc = np.asarray(scale, np.float32).reshape(-1)
+        if sc.size == 1:
+            sc = np.full(hk, sc[0], np.float32)
+        elif sc.size != hk:
+            raise ValueError(f"dequant_kv: {sc.size} scales for {hk} kv heads")
     # The value is a function of (code, kv head) only: tabulate round(decode(c) * s_h)
     # for the 256 codes of each head, then gather (the same values, one pass).
     tables = round_to(E4M3FN_TABLE[None, :] * sc[:, None], q_dtype)  # [Hk, 256]

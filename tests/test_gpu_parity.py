@@ -328,10 +328,13 @@ def oracle_decode(case, seqs=None, window_left=-1, sinks=None):
     return out
 
 
-def test_paged_decode_c3_north_star(cuda):
-    """Full C3 launch (64 seqs, ctx U[512, 8192]); every sequence against the oracle."""
-    _flush("paged_decode C3")
-    case = workloads.c3_decode(cuda)
+@pytest.mark.parametrize("block_size", [256, 64, 16])
+def test_paged_decode_c3_north_star(cuda, block_size):
+    """Full C3 launch (64 seqs, ctx U[512, 8192]); every sequence against the oracle.
+    Also at 16-token pages (what the reference engine's AttnBackendConfig.auto_detect
+    picks on this GPU, infra/context.py:68-73) and 64, over a pool of the same bytes."""
+    _flush(f"paged_decode C3, block_size {block_size}")
+    case = workloads.c3_decode(cuda, block_size=block_size, pool_blocks=4096 * 256 // block_size)
     out = run_decode(case)
     ref = oracle_decode(case)
     got = f32(out)
@@ -699,10 +702,13 @@ def test_candidate_decode_reference_harness_inputs(cuda, kv_dtype, num_splits):
 # ---------------------------------------------------------------------------
 # Candidate classes (drop-in surface) and the C4 chain
 # ---------------------------------------------------------------------------
-def test_candidates_chain_c4(cuda):
+@pytest.fixture(scope="module")
+def c4_chain_run(cuda):
     """C4: add+RMSNorm -> rotary -> store_kvcache -> paged decode -> SiLU-and-mul through
-    the candidate classes, each against the oracle on the same inputs."""
-    _flush("chain C4")
+    the candidate classes on the full C4 inputs.  Returns the inputs, each op's input
+    snapshot and each op's output; the tests below check every output against the
+    oracle."""
+    _flush("chain C4: GPU launches")
     from fastkernels_amd.candidate.L1.flash_attn_decode import FlashAttnDecode
     from fastkernels_amd.candidate.L1.rms_norm import RMSNorm
     from fastkernels_amd.candidate.L1.rotary_emb import RotaryEmbedding
@@ -711,41 +717,73 @@ def test_candidates_chain_c4(cuda):
 
     c = workloads.c4_chain(cuda)
     t, hq, hk, d = 256, 32, 8, 128
+    res = {"c": c}
     norm = RMSNorm(4096).to(cuda)
     norm.weight.data.copy_(c.norm_weight.float())
-    h0, r0 = f32(c.hidden), f32(c.residual)
-    hn, rn = norm(c.hidden.clone(), c.residual.clone())
-    ref_h, ref_r = oracle.rms_norm(h0, f32(c.norm_weight), 1e-6, "bf16", residual=r0)
-    assert np.array_equal(f32(rn), ref_r)
-    assert_close(f32(hn), ref_h, BF16_TOL, BF16_TOL, "norm")
+    res["norm_out"] = norm(c.hidden.clone(), c.residual.clone())
 
     rope = RotaryEmbedding(d, c.max_position, c.rope_theta).to(cuda)
+    res["cos_sin"] = f32(rope.cos_sin_cache)
     qkv = c.qkv.clone()
     q, k, v = qkv[:, :hq * d], qkv[:, hq * d:(hq + hk) * d], qkv[:, (hq + hk) * d:]
-    ref_q, ref_k = oracle.rotary(c.positions.cpu().numpy(), f32(q), f32(k), d,
-                                 f32(rope.cos_sin_cache), True, "bf16")
+    res["q_in"], res["k_in"] = f32(q), f32(k)
     rope(c.positions, q, k)
-    assert_close(f32(q), ref_q, BF16_TOL, BF16_TOL, "rope q")
-    assert_close(f32(k), ref_k, BF16_TOL, BF16_TOL, "rope k")
+    res["q"], res["k"] = q, k
 
     dec = c.decode
     StoreKVCache()(k.view(t, hk, d), v.view(t, hk, d), dec.k_cache, dec.v_cache, c.slot_mapping)
-    torch.cuda.synchronize()
-    rows = c.slot_mapping.cpu()
-    kflat = dec.k_cache.view(-1, hk * d)
-    assert torch.equal(kflat[rows.to(cuda)].view(torch.int16), k.contiguous().view(torch.int16))
-
     attn = FlashAttnDecode(hq, hk, d, page_size=256)
     o = attn(q.view(t, hq, d), dec.k_cache, dec.v_cache, cache_seqlens=dec.ctx_lens,
              block_table=dec.block_tables, softmax_scale=dec.scale, causal=True,
              max_seq_len=dec.max_seq_len)
     dec.q = q.view(t, hq, d)
-    seqs = list(range(0, t, 17))
-    ref_o = oracle_decode(dec, seqs)
-    assert_close(f32(o)[seqs], ref_o[seqs], BF16_TOL, BF16_TOL, "decode")
+    res["attn"] = f32(o)
+    res["act"] = SiluAndMul()(c.gate_up)
+    torch.cuda.synchronize()
+    return res
 
-    act = SiluAndMul()(c.gate_up)
-    assert_close(f32(act), oracle.silu_and_mul(f32(c.gate_up), "bf16"), BF16_TOL, BF16_TOL, "silu")
+
+def test_candidates_chain_c4(c4_chain_run):
+    """The C4 chain's norm, rotary, store and SiLU outputs against the oracle (the
+    residual and the stored cache rows bit-exact)."""
+    _flush("chain C4: norm / rotary / store / silu")
+    res = c4_chain_run
+    c = res["c"]
+    t, hk, d = 256, 8, 128
+    hn, rn = res["norm_out"]
+    ref_h, ref_r = oracle.rms_norm(f32(c.hidden), f32(c.norm_weight), 1e-6, "bf16",
+                                   residual=f32(c.residual))
+    assert np.array_equal(f32(rn), ref_r)
+    assert_close(f32(hn), ref_h, BF16_TOL, BF16_TOL, "norm")
+
+    ref_q, ref_k = oracle.rotary(c.positions.cpu().numpy(), res["q_in"], res["k_in"], d,
+                                 res["cos_sin"], True, "bf16")
+    assert_close(f32(res["q"]), ref_q, BF16_TOL, BF16_TOL, "rope q")
+    assert_close(f32(res["k"]), ref_k, BF16_TOL, BF16_TOL, "rope k")
+
+    dec = c.decode
+    rows = c.slot_mapping
+    kflat = dec.k_cache.view(-1, hk * d)
+    assert torch.equal(kflat[rows].view(torch.int16), res["k"].contiguous().view(torch.int16))
+    vflat = dec.v_cache.view(-1, hk * d)
+    v = c.qkv[:, (32 + hk) * d:]
+    assert torch.equal(vflat[rows].view(torch.int16), v.contiguous().view(torch.int16))
+
+    assert_close(f32(res["act"]), oracle.silu_and_mul(f32(c.gate_up), "bf16"), BF16_TOL,
+                 BF16_TOL, "silu")
+
+
+@pytest.mark.parametrize("first", [0, 64, 128, 192])
+def test_candidates_chain_c4_decode(c4_chain_run, first):
+    """The C4 chain's paged decode (B = 256, ctx U[256, 4096], over the caches the
+    chain's store wrote): every sequence against the oracle, 64 per test."""
+    res = c4_chain_run
+    seqs = list(range(first, first + 64))
+    _flush(f"chain C4: decode oracle for sequences {first}..{first + 63}")
+    ref = oracle_decode(res["c"].decode, seqs)
+    got = res["attn"]
+    assert np.isfinite(got[seqs]).all()
+    assert_close(got[seqs], ref[seqs], BF16_TOL, BF16_TOL, f"C4 decode seqs {first}..")
 
 
 def test_flash_attn_decode_defaults_no_sync(cuda):

@@ -432,6 +432,13 @@ def test_fp8_dequant_matches_torch():
     ours = oracle.dequant_kv(codes, scale, "bf16")
     t = torch.from_numpy(codes).view(torch.float8_e4m3fn).float() * torch.from_numpy(scale).view(1, 1, 2, 1)
     assert np.array_equal(ours, t.bfloat16().float().numpy())
+    # One per-tensor scale (the reference's FP8_PER_TENSOR) applies to every kv head,
+    # as a 0-d or a size-1 array.
+    t1 = torch.from_numpy(codes).view(torch.float8_e4m3fn).float() * 0.05
+    for s in (np.float32(0.05), np.array([0.05], np.float32)):
+        assert np.array_equal(oracle.dequant_kv(codes, s, "bf16"), t1.bfloat16().float().numpy())
+    with pytest.raises(ValueError):
+        oracle.dequant_kv(codes, np.ones(3, np.float32), "bf16")
 
 
 # ---------------------------------------------------------------------------
