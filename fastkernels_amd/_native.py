@@ -19,6 +19,10 @@ FK_ERR_INVALID_ARG = -1
 FK_ERR_UNSUPPORTED = -2
 FK_ERR_WORKSPACE = -3
 
+# The C ABI's major version these bindings are written for (FK_VERSION_MAJOR in
+# include/fastkernels_amd.h; fk_version() = 10000 * major + 100 * minor + patch).
+ABI_MAJOR = 2
+
 FK_DTYPE_F32 = 0
 FK_DTYPE_F16 = 1
 FK_DTYPE_BF16 = 2
@@ -75,12 +79,12 @@ _SIGNATURES = {
                                       c_int64, c_int64, c_int, c_int, c_int, c_int, c_void_p]),
     "fk_paged_prefill": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_int,
                                  c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_void_p,
-                                 c_int64, c_int64, c_int64, c_int, c_int, c_int, c_int, c_int64,
-                                 c_float, c_int, c_int, c_void_p, c_void_p]),
+                                 c_int64, c_int64, c_int64, c_int, c_int, c_int, c_int, c_int,
+                                 c_int64, c_float, c_int, c_int, c_void_p, c_void_p]),
     "fk_varlen_prefill": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64,
                                   c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_int64,
-                                  c_int64, c_int, c_int, c_int, c_float, c_int, c_int, c_void_p,
-                                  c_void_p]),
+                                  c_int64, c_int, c_int, c_int, c_int, c_float, c_int, c_int,
+                                  c_void_p, c_void_p, c_int64, c_void_p]),
     "fk_store_kvcache_convert": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_int, c_void_p,
                                          c_void_p, c_int, c_void_p, c_int, c_int64, c_int64,
                                          c_int64, c_void_p]),
@@ -113,6 +117,13 @@ def lib() -> ctypes.CDLL:
             f"libfk_amd.so not found at {path}; build it with `python -m fastkernels_amd.build`"
             " (the HIP kernels are the only implementation; there is no fallback)")
     handle = ctypes.CDLL(str(path))
+    handle.fk_version.restype = c_int
+    handle.fk_version.argtypes = []
+    version = handle.fk_version()
+    if version // 10000 != ABI_MAJOR:
+        raise RuntimeError(
+            f"{path} implements C ABI version {version}, these bindings need major version "
+            f"{ABI_MAJOR}: rebuild it with `python -m fastkernels_amd.build`")
     for name, (restype, argtypes) in _SIGNATURES.items():
         fn = getattr(handle, name)
         fn.restype = restype

@@ -58,10 +58,19 @@ except ImportError:  # loaded by file path from the reference harness
 from fastkernels_amd import ops
 
 
+# Head sizes the decode kernel is built for (Whisper 64; Llama / Qwen3 128;
+# Qwen3-Next, Gemma 256).
+DECODE_HEAD_SIZES = (64, 128, 256)
+
+
 class FlashAttnDecode(nn.Module):
     def __init__(self, num_heads: int, num_kv_heads: int, head_dim: int,
                  page_size: int | None = None):
         super().__init__()
+        if head_dim not in DECODE_HEAD_SIZES:
+            # Refused here rather than at the first forward.
+            raise NotImplementedError(f"FlashAttnDecode (gfx950): head_dim {head_dim} is not "
+                                      f"built (head sizes {DECODE_HEAD_SIZES})")
         self.num_heads = num_heads
         self.num_kv_heads = num_kv_heads
         self.head_dim = head_dim

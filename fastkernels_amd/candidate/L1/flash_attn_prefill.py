@@ -20,6 +20,10 @@ logits, one per query head) as ``Attention._forward_pure`` passes them
 (attention_impl.py:401-434).  ``max_seqlen_q`` must bound every query chunk (it
 sizes the launch); no host synchronisation happens.  Returns
 ``[total_q, num_heads, head_dim]``.
+
+Head sizes (``ops.PREFILL_HEADS``): 32, 64, 72, 80, 96, 128 and 256 with bf16 keys
+(72 and 80 are Qwen3-VL's and Qwen2/2.5-VL's vision encoders, L2/vision_attention.py:
+32,39), 64, 128 and 256 with fp8 pages; the constructor refuses others.
 """
 from __future__ import annotations
 
@@ -39,6 +43,11 @@ from fastkernels_amd import ops
 class FlashAttnPrefill(nn.Module):
     def __init__(self, num_heads: int, num_kv_heads: int, head_dim: int):
         super().__init__()
+        if not ops.prefill_heads_supported(head_dim):
+            # Refused here rather than at the first forward.
+            raise NotImplementedError(
+                f"FlashAttnPrefill (gfx950): head_dim {head_dim} is not built (bf16: "
+                f"{sorted(d for d, dv in ops.PREFILL_HEADS if d == dv)}; fp8 pages: 64, 128, 256)")
         self.num_heads = num_heads
         self.num_kv_heads = num_kv_heads
         self.head_dim = head_dim

@@ -1,1018 +1,32 @@
-// Paged prefill attention (variable-length query chunks over a paged KV cache)
-// for MI355X (gfx950).
-//
-// Semantics: FlashAttnPrefill.forward with a block table
-// (fastkernels/tasks/baseline/L1/flash_attn_prefill.py:28-74: flash_attn_varlen_func
-// with cu_seqlens_q, seqused_k = cu_seqlens_k[1:] - cu_seqlens_k[:-1], causal), and
-// the reference's torch fallback Attention._prefill_torch_from_cache
-// (fastkernels/tasks/baseline/L2/attention_impl.py:640-652, _sdpa_one :606-622):
-// sequence b owns query rows [cu_q[b], cu_q[b+1]) (q_len of them) and the first
-// k_len = cu_k[b+1] - cu_k[b] tokens of its paged cache.  Query j (0-based in
-// its chunk) sits at position k_len - q_len + j and sees keys
-// [0, k_len - q_len + j] (causal, aligned to the end of the keys), or, under
-// a sliding window (flash-attn window_size = (window_left, 0)), keys
-// [k_len - q_len + j - window_left, k_len - q_len + j].  A query with no
-// visible key gets a zero row.  Attention sinks (s_aux: one logit per query
-// head) join each row's softmax denominator, as in the decode kernel.  kv head
-// = hq / (Hq / Hk); fp8 pages are dequantised per kv head as in the decode
-// kernel.
-//
-// Work decomposition: work-group = 4 waves over one kv head and one block of
-// query tokens of one sequence: the waves are the group's query heads (up to
-// 4; larger groups span several work-groups) times consecutive 32-token query
-// blocks (4 / heads of them).  A wave keeps two 16-query column blocks of one
-// head in MFMA tiles (fk_attn_tile.h: S = K Q^T per 16-key tile, online
-// softmax per query column, O += P V).  The work-group streams the keys in
-// stages of 32 through LDS (double-buffered: the next stage's global loads are
-// in flight while the current one is consumed), so the waves share each K/V
-// byte and no wave waits on a global load per tile; each wave stops at its own
-// last visible key.  In a causal chunk with few cached keys before it, a
-// work-group takes two query blocks, one near the chunk's end and one near its
-// start, so that the work-groups are even.
-//
-// Key split.  When the launch has too few work-groups to give every SIMD two
-// waves (a single prompt: 2048 tokens over 8 kv heads make 256 work-groups
-// after pairing), the work-group has 8 waves in two halves of 4: both halves
-// take the same queries, the first half streams the first half of the block's
-// key stages and the second half the rest, each through its own LDS buffers,
-// in lock step (one barrier per stage; the half with fewer stages passes empty
-// barriers).  At the end the second half leaves its (O, max, sum) in LDS and
-// the first half merges them with the log-sum-exp rule before it writes the
-// rows.  Each block's serial chain of stages halves, and every SIMD runs two
-// waves.
-#include <type_traits>
+// C entry points of the prefill attention kernel (fk_prefill_kernel.h):
+// fk_paged_prefill (FlashAttnPrefill with a block table) and fk_varlen_prefill
+// (dense keys: FlashAttnPrefill without one, and FlashAttnVarlen).  This file
+// instantiates the kernel at D = DV in {64, 128, 256} with bf16 and fp8 pages
+// and dense keys; fk_prefill_heads.hip instantiates the other head sizes.
+#include <algorithm>
 
-#include "fk_attn_tile.h"
+#include "fk_prefill_kernel.h"
 
 namespace fk {
 namespace {
 
-#ifndef FK_PREFILL_COLS
-#define FK_PREFILL_COLS 2
-#endif
-// Two waves per SIMD (two 4-wave work-groups per CU; each holds 32 KB of LDS for
-// bf16 pages at head size 128, 64 KB at 256).  At 256 the bf16 P.V operands go
-// in two halves to fit in the 256 registers two waves leave (fp8 fits as is);
-// dense keys at 256 (the row clamping) would still spill 11 VGPRs, so one.
-constexpr int prefill_waves_per_simd(int D, bool paged) { return D >= 256 && !paged ? 1 : 2; }
-#ifndef FK_PREFILL_LAZY
-#define FK_PREFILL_LAZY 8.0f
-#endif
-constexpr int kColBlocks = FK_PREFILL_COLS;    // 16-query column blocks per wave
-constexpr float kLazy = FK_PREFILL_LAZY;       // max-update threshold (log2 units)
-constexpr int kQTokens = 16 * kColBlocks;      // query tokens per wave at head size 128
-// Column blocks per wave at head size D: at 256 the O accumulators of one block
-// (16 tiles of 4 fp32 per lane) already take what two take at 128.
-constexpr int col_blocks_for(int D) { return D >= 256 ? 1 : kColBlocks; }
-constexpr int kPrefillWaves = 4;               // waves per work-group
-#ifndef FK_PREFILL_STAGE
-#define FK_PREFILL_STAGE 32
-#endif
-// fp8 pages: each stage converted once into bf16 LDS buffers (1), or every
-// wave dequantising the K / V bytes it reads (0).
-#ifndef FK_PREFILL_FP8_CONVERT
-#define FK_PREFILL_FP8_CONVERT 1
-#endif
-// Keys per LDS stage (a multiple of 32).  Measured on MI355X (bf16, 1x2048,
-// 4x512 over 4096, 16x512 prompts): 32 keys 102 / 220 / 89 us against 117 /
-// 244 / 99 us for 64; again with the current loop, 88 / 187 / 83 against
-// 98 / 208 / 91.
-constexpr int kStageKeys = FK_PREFILL_STAGE;
-constexpr int kStageTiles = kStageKeys / kTile;
-
-struct PrefillParams {
-  uint16_t* out;
-  int64_t out_row_stride;
-  const uint16_t* q;
-  int64_t q_row_stride;
-  const uint8_t* k_cache;  // paged: the caches; dense: the first key / value row
-  const uint8_t* v_cache;
-  int64_t k_row_bytes;     // bytes between key rows (paged: Hk * 128 * elem)
-  int64_t v_row_bytes;
-  const float* k_scale;
-  const float* v_scale;
-  int64_t bt_row_stride;
-  int num_kv_heads;
-  int gqa;
-  int block_size_log2;
-  int64_t num_blocks;
-  float scale_log2;
-  int causal;        // 0: every query sees all k_len keys
-  int window_left;   // causal sliding window: keys >= position - window_left (-1: none)
-  const float* sinks;  // attention sink logits [num_heads] fp32, or nullptr
-};
-
-__device__ __forceinline__ int64_t prefill_page(const PrefillParams& P,
-                                                const int32_t* __restrict__ bt_row, int tok) {
-  const int idx = tok >> P.block_size_log2;
-  if (idx >= P.bt_row_stride) return -1;
-  const int64_t page = bt_row[idx];
-  return (page >= 0 && page < P.num_blocks) ? page : -1;
-}
-
-// The last block-table entry a wave looked up (wave-uniform): a page spans
-// block_size / 32 stages, so most lookups reuse it instead of waiting for a
-// scalar load.
-struct PageCache {
-  int idx = -1;
-  int64_t page = -1;
-};
-
-// Row index of key `tok` of the sequence and whether it is readable: paged, the
-// slot through the block table (-1 pages masked; page 0 is read instead);
-// dense, row k_start + tok of the key/value tensors.
-template <bool kPaged>
-__device__ __forceinline__ int64_t key_row(const PrefillParams& P,
-                                           const int32_t* __restrict__ bt_row, int k_start,
-                                           int tok, bool& ok, PageCache& pc) {
-  if constexpr (kPaged) {
-    const int idx = tok >> P.block_size_log2;
-    if (idx != pc.idx) {
-      pc.page = prefill_page(P, bt_row, tok);
-      pc.idx = idx;
-    }
-    const int64_t page = pc.page;
-    ok = page >= 0;
-    return ((page < 0 ? 0 : page) << P.block_size_log2) + (tok & ((1 << P.block_size_log2) - 1));
-  } else {
-    ok = true;
-    return static_cast<int64_t>(k_start) + tok;
-  }
-}
-
-// LDS staging of key/value rows.  A stage is kStageKeys consecutive keys of one
-// kv head: kStageKeys K rows, then kStageKeys V rows, each kRowBytes long, with
-// the 16-byte chunks of row R stored at chunk index q ^ (R mod kChunks) so
-// that the row-parallel writes and the MFMA-layout reads (16 rows at one chunk
-// index, or one row's 16 chunks) hit distinct banks.
-template <bool kFp8, int D>
-struct Stage {
-  static constexpr int kRowBytes = kFp8 ? D : 2 * D;
-  static constexpr int kChunks = kRowBytes / 16;
-  static constexpr int kBytes = 2 * kStageKeys * kRowBytes;  // K rows + V rows
-  // Direct-to-LDS loads per thread per stage (16 bytes each).
-  static constexpr int kLoads = 2 * kStageKeys * kChunks / (kPrefillWaves * 64);
-  __device__ __forceinline__ static int offset(int which, int row, int q) {
-    return (which * kStageKeys + row) * kRowBytes + ((q ^ (row & (kChunks - 1))) << 4);
-  }
-};
-
-// 16 bytes from global memory straight into LDS (gfx950 global_load_lds_dwordx4):
-// lane l of the wave writes at byte lds_addr + 16 l.  Written as inline asm, so
-// the compiler's wait-count pass does not see it: its builtin form makes the
-// pass wait for the load before every later LDS read, including reads of the
-// other stage buffer, which would serialise the double buffer.  The kernel
-// orders it explicitly instead (s_waitcnt vmcnt(0), then a barrier, before the
-// buffer is read).  M0 carries the LDS address: an input operand bound to M0, so
-// the compiler writes it (and knows it changed) with no save and restore; the
-// s_nop is the wait state between that write and the load that reads M0.
-__device__ __forceinline__ void lds_dma16(const uint8_t* src, uint32_t lds_addr) {
-  asm volatile(
-      "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %0, off"
-      :
-      : "v"(src), "{m0}"(lds_addr)
-      : "memory");
-}
-
-// LDS byte address of a pointer into a __shared__ array.
-__device__ __forceinline__ uint32_t lds_addr_of(const uint8_t* p) {
-  return static_cast<uint32_t>(
-      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const uint8_t*)p));
-}
-
-// Floats one wave of the key split's second half leaves in LDS for its partner:
-// O (kCB x D/16 MFMA tiles of 4 floats per lane), the row sums (kCB x 4 per
-// lane) and the column maxima (kCB per lane).
-template <int D, int kCB>
-constexpr int split_exchange_floats() {
-  return kCB * (D / 16) * 64 * 4 + kCB * 64 * 4 + kCB * 64;
-}
-
-// Tile tt (rows 16 tt .. 16 tt + 15) of a staged buffer in the register layout
-// a global load of the tile would give (DTile, fk_attn_tile.h): the K rows (t.k)
-// and, for fp8 stages, the V rows (t.v), read separately so that a caller can
-// keep them apart in time.
-template <bool kFp8, int D>
-__device__ __forceinline__ void lds_tile_k(const uint8_t* buf, int tt, int r, int g,
-                                           DTile<kFp8, D>& t) {
-  using S = Stage<kFp8, D>;
-  const int kr = 16 * tt + r;
-  if constexpr (!kFp8) {
-#pragma unroll
-    for (int c = 0; c < D / 32; ++c)
-      t.k[c] = *reinterpret_cast<const uint4*>(buf + S::offset(0, kr, 4 * c + g));
-  } else {
-#pragma unroll
-    for (int c = 0; c < D / 64; ++c)
-      t.k[c] = *reinterpret_cast<const uint4*>(buf + S::offset(0, kr, (D / 64) * g + c));
-  }
-}
-// fp8 V rows 4g + i: lane r's D / 16 bytes (dims (D/16) r ..), inside one chunk.
-template <bool kFp8, int D>
-__device__ __forceinline__ void lds_tile_v(const uint8_t* buf, int tt, int r, int g,
-                                           DTile<kFp8, D>& t) {
-  static_assert(kFp8, "bf16 V rows are read with lds_v_slice");
-  using S = Stage<kFp8, D>;
-  const int byte = (D / 16) * r;
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-    ld_words(buf + S::offset(1, 16 * tt + 4 * g + i, byte >> 4) + (byte & 15), t.v[i]);
-}
-
-// P.V operand of the 16-dim slice d of tile tt (bf16 stages), read with the LDS
-// transpose load: lane (r, g) gets V[keys 16 tt + 4g .. 16 tt + 4g + 3][dim
-// 16 d + r], the B-operand layout of the 16x16x16 MFMA, with no register
-// regrouping.  ds_read_b64_tr_b16 gives lane j of each 16-lane group, as its
-// element a, element j mod 4 of the 8 bytes addressed by lane 4a + j / 4; so
-// lane 4a + q addresses row 4g + a, dims 16d + 4q .. 16d + 4q + 3.
-template <int D>
-__device__ __forceinline__ short4_t lds_v_slice(const uint8_t* buf, int tt, int d, int r, int g) {
-  using S = Stage<false, D>;
-  const int row = 16 * tt + 4 * g + (r >> 2);
-  const int q = r & 3;
-  const int off = S::offset(1, row, 2 * d + (q >> 1)) + 8 * (q & 1);
-  typedef __attribute__((address_space(3))) short4_t* lds_short4;
-  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4)(buf + off));
-}
-
-// Work-group = kPrefillWaves waves over one kv head: hw query heads of its group
-// times qs = kPrefillWaves / hw blocks of kQTokens query tokens (a group larger
-// than kPrefillWaves heads spans hsplit work-groups).  All waves share the K/V
-// stages; each walks the tiles up to its own last visible key.
-// kKS = 2: the key split (8 waves; head sizes up to 128, and 256 with paged keys).
-template <bool kFp8, bool kPaged, int D, int kKS>
-__global__ __launch_bounds__(kKS * kPrefillWaves * 64)
-__attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D, kPaged)))) void paged_prefill_kernel(
-    PrefillParams P, const int32_t* __restrict__ block_tables,
-    const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_k) {
-  using S = Stage<kFp8, D>;
-  // fp8 pages: the work-group converts each staged stage once into a bf16
-  // stage (float(x) * scale rounded to bf16, the value each wave would form),
-  // and the waves compute on bf16 tiles, instead of each wave dequantising the
-  // same K / V bytes for its own query head.  Up to head size 128 each fp8
-  // buffer has its bf16 one (kConv); at 256 two of those would not fit in LDS
-  // with two work-groups per CU, so one bf16 buffer serves the stages in turn
-  // (kConv1: converted after every wave is done with the stage before, a second
-  // barrier per stage).
-  constexpr bool kConv = kFp8 && FK_PREFILL_FP8_CONVERT && D <= 128;
-  constexpr bool kConv1 = kFp8 && FK_PREFILL_FP8_CONVERT && D > 128;
-  constexpr bool kFp8T = kFp8 && !kConv && !kConv1;  // fp8 tiles in the compute path
-  using SB = Stage<kFp8T, D>;             // the layout the compute path reads
-  static_assert(kKS == 1 || (kKS == 2 && (D <= 128 || kPaged)),
-                "key split: two halves, head size <= 128 (256 with paged keys)");
-  constexpr int kCB = col_blocks_for(D);  // 16-query column blocks per wave
-  constexpr int kQT = 16 * kCB;           // query tokens per wave
-  // Stage buffers (two or three per half; with kConv a bf16 buffer beside each
-  // fp8 one), and with the key split the exchange area that reuses them once
-  // the last stage is consumed.
-  constexpr int kXFloats = split_exchange_floats<D, kCB>();
-  // Key split with one pair per stage: the halves run opposite phases (half 1
-  // defers each pair's P.V past the next barrier), three stage buffers a half.
-  // (At head size 256 three buffers a half would not fit in LDS, nor with the
-  // fp8 stage conversion, whose bf16 buffers come beside the fp8 ones: two, in
-  // phase.)
-  constexpr bool kPingPong = kKS > 1 && kStageTiles == 2 && D <= 128 && !kConv;
-  constexpr int kBufs = kPingPong ? 3 : 2;
-  constexpr int kHalfBytes =  // a half's buffers
-      kBufs * (S::kBytes + (kConv ? SB::kBytes : 0)) + (kConv1 ? SB::kBytes : 0);
-  constexpr int kStageAll = kKS * kHalfBytes;
-  constexpr int kXBytes = kKS > 1 ? kPrefillWaves * kXFloats * 4 : 0;
-  __shared__ __align__(16) uint8_t lds_all[kStageAll > kXBytes ? kStageAll : kXBytes];
-  // Grid: x = kv head (x hsplit), y = sequence, z = query block.  The block
-  // index varies slowest, so the work-groups that have work (low z when blocks
-  // are paired) are dispatched first and spread over every CU.
-  const int b = blockIdx.y;
-  const int hw = P.gqa < kPrefillWaves ? P.gqa : kPrefillWaves;  // heads per work-group
-  const int qs = kPrefillWaves / hw;                             // query blocks per work-group
-  const int hsplit = (P.gqa + hw - 1) / hw;
-  const int h = blockIdx.x / hsplit;
-  const int head0 = (blockIdx.x - h * hsplit) * hw;
-  const int q_start = cu_q[b];
-  const int q_len = cu_q[b + 1] - q_start;
-  const int k_start = cu_k[b];
-  const int k_len = cu_k[b + 1] - k_start;
-  // Query blocks of the sequence at work-group granularity (wg_tokens queries
-  // each).  When the causal triangle dominates the sequence's work (fewer than
-  // q_len cached keys before the chunk), work-group p takes the pair of blocks
-  // nqb - 1 - p (the most keys) and p (the fewest), one after the other, so its
-  // work-groups stream about the same number of keys and no wave is left with a
-  // long tail on its own; the upper half of the grid then has nothing to do.
-  // Otherwise the blocks' key counts are close, and work-group x takes block
-  // nqb - 1 - x alone (the heaviest first), keeping twice the work-groups.
-  const int wg_tokens = qs * kQT;
-  const int nqb = (q_len + wg_tokens - 1) / wg_tokens;
-  const bool paired = P.causal && k_len - q_len < q_len;
-  const int x = static_cast<int>(blockIdx.z);
-  if (x >= (paired ? (nqb + 1) / 2 : nqb)) return;  // uniform over the work-group
-  const int wave_id = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int half = kKS > 1 ? wave_id / kPrefillWaves : 0;  // key-split half
-  const int wave = wave_id & (kPrefillWaves - 1);           // role within the half
-  uint8_t* const lds_half = lds_all + half * kHalfBytes;
-  // Stage st's buffer: two alternate; with three, stage st mod 3.
-  auto stage_buf = [&](int st) {
-    return lds_half + (kBufs == 2 ? (st & 1) : st % kBufs) * S::kBytes;
-  };
-  // The buffer the compute path reads stage st from: the staged one, or with
-  // kConv its bf16 conversion.
-  auto comp_buf = [&](int st) {
-    if constexpr (kConv) return lds_half + kBufs * S::kBytes + (st & 1) * SB::kBytes;
-    else if constexpr (kConv1) return lds_half + kBufs * S::kBytes;
-    else return stage_buf(st);
-  };
-  const int lane = threadIdx.x & 63;
-  const int r = lane & 15;
-  const int g = lane >> 4;
-  const int head = head0 + wave % hw;
-  const int hq = h * P.gqa + (head < P.gqa ? head : 0);
-  // Position of query 0; non-causal, every query sits past the last key.
-  const int offset = P.causal ? k_len - q_len : k_len;
-  const int32_t* bt_row = kPaged ? block_tables + static_cast<int64_t>(b) * P.bt_row_stride
-                                 : nullptr;
-  // Dense keys: rows past the sequence's last key would run off the tensor.
-  const int64_t row_cap = kPaged ? INT64_MAX : static_cast<int64_t>(k_start) + max(k_len, 1) - 1;
-  const float s2 = P.scale_log2;
-  // fp8 dequant scales of kv head h (1 for bf16 pages or no scale tensor): each
-  // K / V element enters the MFMAs as float(x) * scale rounded to bf16.
-  const float ks = (kFp8 && P.k_scale) ? P.k_scale[h] : 1.f;
-  const float vsc = (kFp8 && P.v_scale) ? P.v_scale[h] : 1.f;
-
-  const int win = P.window_left;
-  // Stages [st0, nstages) of 32 keys that query block qblk streams: up to its
-  // last query's last key, from its first query's window start.
-  auto block_stages = [&](int qblk, int& st0, int& nstages) {
-    const int jw0 = qblk * wg_tokens;
-    const int kend_wg = max(0, min(k_len, offset + min(jw0 + wg_tokens, q_len)));
-    const int kbeg_wg = win >= 0 ? max(0, offset + jw0 - win) : 0;
-    nstages = (kend_wg + kStageKeys - 1) / kStageKeys;
-    st0 = min(kbeg_wg / kStageKeys, nstages);
-  };
-
-  PageCache pc;
-  // One query block of the work-group, start to finish (its own K/V stages);
-  // with the key split both halves take it, each streaming half its stages.
-  auto process_block = [&](int qblk) {
-  const int jw0 = qblk * wg_tokens;  // first query of the work-group
-  const int j0 = jw0 + (wave / hw) * kQT;
-  // Waves without queries (past the chunk, or past the group) still stage.
-  const bool active = j0 < q_len && head < P.gqa && wave < qs * hw;
-  // Keys [0, kend) cover every query of this wave's block.
-  const int kend = active ? max(0, min(k_len, offset + min(j0 + kQT, q_len))) : 0;
-  // Sliding window: query j sees keys from offset + j - win.  kbeg (this wave's
-  // first query) bounds the keys from below; the work-group starts streaming at
-  // the stage holding its first query's (block_stages), and a stage at or after
-  // khead (the last query's window start) is inside every query's window.
-  const int kbeg = (win >= 0 && active) ? max(0, offset + j0 - win) : 0;
-  const int khead = (win >= 0 && active) ? offset + min(j0 + kQT, q_len) - 1 - win : 0;
-
-  // Q^T operands: column r of block nb = query j0 + 16 nb + r.
-  bf16x8_t qb[kCB][D / 32];
-#pragma unroll
-  for (int nb = 0; nb < kCB; ++nb) {
-    const int j = j0 + 16 * nb + r;
-    const bool ok = active && j < q_len;
-    const uint16_t* qp = P.q + static_cast<int64_t>(q_start + (ok ? j : 0)) * P.q_row_stride +
-                         static_cast<int64_t>(hq) * D;
-#pragma unroll
-    for (int c = 0; c < D / 32; ++c) {
-      const int d0 = kFp8T ? (D / 4) * g + 8 * c : 32 * c + 8 * g;
-      const uint4 v = ok ? *reinterpret_cast<const uint4*>(qp + d0) : make_uint4(0, 0, 0, 0);
-      qb[nb][c] = __builtin_bit_cast(bf16x8_t, v);
-    }
-  }
-  // Running max per query column (log2 units, this lane's column r), and the
-  // softmax denominators in the O layout: l_acc[nb][i] is the sum for query row
-  // 4g + i, accumulated by an MFMA of P against ones beside the P.V ones (the
-  // same bf16 P weights as the numerator), so no VALU adds and no cross-lane
-  // fetch at the end.
-  float m_run[kCB];
-  floatx4_t o[kCB][D / 16], l_acc[kCB];
-#pragma unroll
-  for (int nb = 0; nb < kCB; ++nb) {
-    m_run[nb] = kNegInf;
-    l_acc[nb] = floatx4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int d = 0; d < D / 16; ++d) o[nb][d] = floatx4_t{0.f, 0.f, 0.f, 0.f};
-  }
-  const bf16x8_t ones = __builtin_bit_cast(
-      bf16x8_t, make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u));
-
-  const int ntiles = (kend + kTile - 1) / kTile;
-  // Tiles every query of the block sees in full need no mask: keys up to
-  // offset + j0 (query j0's last key), inside [0, kend).
-  const int nfull = active ? max(0, min(kend, offset + j0 + 1)) / kTile : 0;
-  int st0, nstages;  // the block's stages
-  block_stages(qblk, st0, nstages);
-  const int tbeg = kbeg / kTile;                      // this wave's first tile
-  // This half's stages [st_lo, st_hi) and the barriers every wave passes
-  // (nsteps): the whole range, or with the key split its first or second half.
-  int st_lo = st0, st_hi = nstages, nsteps = nstages - st0;
-  if constexpr (kKS > 1) {
-    const int n0 = (nstages - st0 + 1) / 2;
-    st_lo = half == 0 ? st0 : st0 + n0;
-    st_hi = half == 0 ? st0 + n0 : nstages;
-    nsteps = n0;
-  }
-
-  // Two 16-key tiles (tiles tt, tt + 1 of `buf`, keys tok0 .. tok0 + 31):
-  // scores, one online-softmax update per query column for the 32 keys, P.V.
-  // kMasked applies the causal / length / window / page mask; unmasked pairs skip
-  // it (every score is finite there, so the running max never stays -inf).
-  // Updating the running max, the rescale test and the cross-lane row max once
-  // per 32 keys instead of per 16 halves that part of the VALU work, and the two
-  // tiles' score MFMAs form independent chains.  The V rows are read only after
-  // the scores of both column blocks are done, so K, the scores and V are never
-  // all live at once.
-  //
-  // pair_scores runs the scores and the softmax update (P into p_a / p_b) and
-  // returns whether the pair's V rows need masking; pair_pv runs P.V.
-  auto pair_scores = [&](auto masked, int tok0, const uint8_t* buf, int tt, bool ok_a,
-                         bool ok_b, short4_t (&p_a)[kCB],
-                         short4_t (&p_b)[kCB]) __attribute__((always_inline)) {
-    constexpr bool kMasked = decltype(masked)::value;
-    DTile<kFp8T, D> ta, tb;
-    // Scores of tile a for every column block, then tile b's K is read: the two
-    // K tiles are never live at once (20 fewer VGPRs in the compiler's own
-    // allocation; measured 1% faster).
-    floatx4_t sc_a[kCB], sc_b[kCB];
-    // The MFMA blocks run at raised wave priority: while one wave of a SIMD is in
-    // its softmax, the other's MFMAs issue first (4x512 chunks over 4096 keys
-    // 174.3 -> 168.7 us; the shorter cases unchanged).
-    __builtin_amdgcn_s_setprio(1);
-    {
-      lds_tile_k<kFp8T, D>(buf, tt, r, g, ta);
-      uint4 ka[D / 32];
-      k_chunks_d(ta, ka, ks);
-#pragma unroll
-      for (int nb = 0; nb < kCB; ++nb) sc_a[nb] = qk_scores_n(ka, qb[nb]);
-    }
-    asm volatile("" ::: "memory");  // tile b's K reads stay after tile a's
-    {
-      lds_tile_k<kFp8T, D>(buf, tt + 1, r, g, tb);
-      uint4 kb[D / 32];
-      k_chunks_d(tb, kb, ks);
-#pragma unroll
-      for (int nb = 0; nb < kCB; ++nb) sc_b[nb] = qk_scores_n(kb, qb[nb]);
-    }
-    __builtin_amdgcn_s_setprio(0);
-#pragma unroll
-    for (int nb = 0; nb < kCB; ++nb) {
-      const floatx4_t acc_a = sc_a[nb];
-      const floatx4_t acc_b = sc_b[nb];
-      const int j = j0 + 16 * nb + r;  // this lane's query column
-      const int last = offset + j;     // its last visible key
-      // Masked pairs: key tok0 + rel (rel = 16 * tile + 4g + e) is visible when
-      // its tile's page is readable and dl <= rel - 4g <= dh: one range test per
-      // key instead of the causal, length, chunk and window tests each.
-      // Scores in log2 units, s = s2 * (K.Q), one product each: a product is
-      // canonical, so the max below compiles to plain v_max3 with no
-      // NaN-quieting step per operand (as the raw MFMA results would need).
-      // Masked keys take -inf in the max and P = 0 after the exponent.
-      float s[8], sm[8];
-      bool ok[8];
-      int dh = 0, dl = 0;
-      if constexpr (kMasked) {
-        const int hi = j < q_len ? min(last, kend - 1) : -1;  // last visible key
-        const int lo = win >= 0 ? last - win : 0;             // first visible key
-        dh = hi - tok0 - 4 * g;
-        dl = lo - tok0 - 4 * g;
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        s[i] = acc_a[i] * s2;
-        s[4 + i] = acc_b[i] * s2;
-      }
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        if constexpr (kMasked) {
-          const int rel = (i >> 2) * kTile + (i & 3);  // compile-time
-          ok[i] = ((i >> 2) ? ok_b : ok_a) && rel <= dh && rel >= dl;
-          sm[i] = ok[i] ? s[i] : kNegInf;
-        } else {
-          ok[i] = true;
-          sm[i] = s[i];
-        }
-      }
-      // This lane's max over its 8 keys of the column.
-      const float lt = fmaxf(fmaxf(fmaxf(sm[0], sm[1]), fmaxf(sm[2], sm[3])),
-                             fmaxf(fmaxf(sm[4], sm[5]), fmaxf(sm[6], sm[7])));
-      // Lazy rescaling: the running max only moves when a score exceeds it by
-      // more than kLazy (log2 units), so P <= 2^kLazy and the O / l rescale (a
-      // cross-lane fetch per row) is rare after the first tiles.  The test
-      // needs no cross-lane max: some column's max exceeds its m_run + kLazy
-      // exactly when some lane's own max does, and the ballot spans every
-      // lane.  The column max itself is taken only in the rare branch.  The
-      // final normalisation divides by l accumulated against the same max, so
-      // the result is unchanged up to rounding.
-      if (__ballot(lt > m_run[nb] + kLazy) != 0) {
-        const float mt = pair_max(lt);
-        const float m_new = mt > m_run[nb] + kLazy ? mt : m_run[nb];
-        // 1 where the column's max stays (also -inf to -inf), 0 from -inf.
-        const float alpha = m_new == m_run[nb] ? 1.f : __builtin_amdgcn_exp2f(m_run[nb] - m_new);
-        m_run[nb] = m_new;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float a = row_value<16>(alpha, g, i);
-#pragma unroll
-          for (int d = 0; d < D / 16; ++d) o[nb][d][i] *= a;
-          l_acc[nb][i] *= a;
-        }
-      }
-      // A column with no visible key yet (masked stages only) keeps m = -inf;
-      // all its P are masked to 0.
-      const float m_use = (kMasked && m_run[nb] == kNegInf) ? 0.f : m_run[nb];
-      float pr[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        // Masked scores are -inf in sm, so their P is 2^-inf = 0.
-        pr[i] = __builtin_amdgcn_exp2f(sm[i] - m_use);
-      }
-      const float (&pa)[4] = *reinterpret_cast<const float(*)[4]>(&pr[0]);
-      const float (&pb)[4] = *reinterpret_cast<const float(*)[4]>(&pr[4]);
-      p_a[nb] = p_operand(pa);
-      p_b[nb] = p_operand(pb);
-    }
-    // Keys past the wave's keys (or on a masked page) may hold anything in V.
-    // A pair of readable tiles wholly below kend (the causal diagonal of a
-    // prompt) needs no V mask.
-    return kMasked && (!ok_a || !ok_b || tok0 + 2 * kTile > kend);
-  };
-  auto pair_pv = [&](int tok0, const uint8_t* buf, int tt, bool ok_a, bool ok_b, bool vmask,
-                     const short4_t (&p_a)[kCB],
-                     const short4_t (&p_b)[kCB]) __attribute__((always_inline)) {
-    asm volatile("" ::: "memory");  // V reads stay after the score work
-    if constexpr (!kFp8T && D >= 256) {
-      // bf16 at head size 256: the V slices go in two halves (read, mask, MFMAs),
-      // so that half the V operands are live at once and two waves fit on a
-      // SIMD; otherwise as below.
-      constexpr int kDS = D / 32;  // slices per half
-      uint32_t ma[2] = {~0u, ~0u}, mb[2] = {~0u, ~0u};
-      if (vmask) {
-#pragma unroll
-        for (int h2 = 0; h2 < 2; ++h2) {
-          const int k0 = tok0 + 4 * g + 2 * h2;
-          ma[h2] = ((ok_a && k0 < kend) ? 0x0000ffffu : 0u) | ((ok_a && k0 + 1 < kend) ? 0xffff0000u : 0u);
-          mb[h2] = ((ok_b && k0 + kTile < kend) ? 0x0000ffffu : 0u) |
-                   ((ok_b && k0 + kTile + 1 < kend) ? 0xffff0000u : 0u);
-        }
-      }
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        if (hh > 0) asm volatile("" ::: "memory");  // the second half's reads after the first's MFMAs
-        short4_t vba[kDS], vbb[kDS];
-#pragma unroll
-        for (int d = 0; d < kDS; ++d) {
-          vba[d] = lds_v_slice<D>(buf, tt, hh * kDS + d, r, g);
-          vbb[d] = lds_v_slice<D>(buf, tt + 1, hh * kDS + d, r, g);
-        }
-        if (vmask) {
-#pragma unroll
-          for (int d = 0; d < kDS; ++d) {
-            uint2 wa = __builtin_bit_cast(uint2, vba[d]), wb = __builtin_bit_cast(uint2, vbb[d]);
-            wa.x &= ma[0]; wa.y &= ma[1];
-            wb.x &= mb[0]; wb.y &= mb[1];
-            vba[d] = __builtin_bit_cast(short4_t, wa);
-            vbb[d] = __builtin_bit_cast(short4_t, wb);
-          }
-        }
-        __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-        for (int nb = 0; nb < kCB; ++nb) {
-          const bf16x8_t pab = __builtin_bit_cast(
-              bf16x8_t, make_uint4(__builtin_bit_cast(uint2, p_a[nb]).x,
-                                   __builtin_bit_cast(uint2, p_a[nb]).y,
-                                   __builtin_bit_cast(uint2, p_b[nb]).x,
-                                   __builtin_bit_cast(uint2, p_b[nb]).y));
-#pragma unroll
-          for (int d = 0; d < kDS; ++d) {
-            const uint2 va = __builtin_bit_cast(uint2, vba[d]), vb = __builtin_bit_cast(uint2, vbb[d]);
-            const bf16x8_t v8 = __builtin_bit_cast(bf16x8_t, make_uint4(va.x, va.y, vb.x, vb.y));
-            o[nb][hh * kDS + d] =
-                __builtin_amdgcn_mfma_f32_16x16x32_bf16(pab, v8, o[nb][hh * kDS + d], 0, 0, 0);
-          }
-          if (hh == 1)
-            l_acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pab, ones, l_acc[nb], 0, 0, 0);
-        }
-        __builtin_amdgcn_s_setprio(0);
-      }
-      return;
-    }
-    short4_t vba[D / 16], vbb[D / 16];  // shared by the column blocks
-    if constexpr (!kFp8T) {
-      // Slice d holds dims 16d .. 16d + 15 (lane r: dim 16d + r).
-#pragma unroll
-      for (int d = 0; d < D / 16; ++d) {
-        vba[d] = lds_v_slice<D>(buf, tt, d, r, g);
-        vbb[d] = lds_v_slice<D>(buf, tt + 1, d, r, g);
-      }
-      // Zero the masked keys' V rows so that P = 0 never meets a NaN.
-      if (vmask) {
-        uint32_t ma[2], mb[2];
-#pragma unroll
-        for (int h2 = 0; h2 < 2; ++h2) {
-          const int k0 = tok0 + 4 * g + 2 * h2;
-          ma[h2] = ((ok_a && k0 < kend) ? 0x0000ffffu : 0u) | ((ok_a && k0 + 1 < kend) ? 0xffff0000u : 0u);
-          mb[h2] = ((ok_b && k0 + kTile < kend) ? 0x0000ffffu : 0u) |
-                   ((ok_b && k0 + kTile + 1 < kend) ? 0xffff0000u : 0u);
-        }
-#pragma unroll
-        for (int d = 0; d < D / 16; ++d) {
-          uint2 wa = __builtin_bit_cast(uint2, vba[d]), wb = __builtin_bit_cast(uint2, vbb[d]);
-          wa.x &= ma[0]; wa.y &= ma[1];
-          wb.x &= mb[0]; wb.y &= mb[1];
-          vba[d] = __builtin_bit_cast(short4_t, wa);
-          vbb[d] = __builtin_bit_cast(short4_t, wb);
-        }
-      }
-    } else {
-      // Slice d holds dims (D/16) r + d (lane r), packed from the row loads.
-      DTile<kFp8T, D> ta, tb;
-      lds_tile_v<kFp8T, D>(buf, tt, r, g, ta);
-      lds_tile_v<kFp8T, D>(buf, tt + 1, r, g, tb);
-      bool keep_a[4], keep_b[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        keep_a[i] = ok_a && tok0 + 4 * g + i < kend;
-        keep_b[i] = ok_b && tok0 + kTile + 4 * g + i < kend;
-      }
-      const bool vall = !vmask;
-      v_operands_fp8(ta, vsc, vall, keep_a, vba);
-      v_operands_fp8(tb, vsc, vall, keep_b, vbb);
-    }
-    __builtin_amdgcn_s_setprio(1);
-    // P.V over the 32 keys with the 16x16x32 MFMA (the 16x16x16 one takes as
-    // long on gfx950 for half the work).  Its k index 8g + e stands for key
-    // 4g + e of tile a (e < 4) and 4g + e - 4 of tile b (e >= 4): the A operand
-    // (P) and the B operand (V) both take tile a's four keys then tile b's, so
-    // the sum runs over the same 32 keys.
-#pragma unroll
-    for (int nb = 0; nb < kCB; ++nb) {
-      const bf16x8_t pab = __builtin_bit_cast(
-          bf16x8_t, make_uint4(__builtin_bit_cast(uint2, p_a[nb]).x,
-                               __builtin_bit_cast(uint2, p_a[nb]).y,
-                               __builtin_bit_cast(uint2, p_b[nb]).x,
-                               __builtin_bit_cast(uint2, p_b[nb]).y));
-#pragma unroll
-      for (int d = 0; d < D / 16; ++d) {
-        const uint2 va = __builtin_bit_cast(uint2, vba[d]), vb = __builtin_bit_cast(uint2, vbb[d]);
-        const bf16x8_t v8 = __builtin_bit_cast(bf16x8_t, make_uint4(va.x, va.y, vb.x, vb.y));
-        o[nb][d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pab, v8, o[nb][d], 0, 0, 0);
-      }
-      l_acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pab, ones, l_acc[nb], 0, 0, 0);
-    }
-    __builtin_amdgcn_s_setprio(0);
-  };
-
-  // Staging with direct global-to-LDS loads (lds_dma16).  Load i of wave w
-  // fills stage chunk positions p = 64 (4 i + w) + lane; position p is physical
-  // chunk p mod kChunks of row p / kChunks (K rows, then V rows), so the lane
-  // reads the logical chunk that the swizzle puts there.  Rows of a masked page
-  // (-1 table entry) read page 0 and rows past a dense tensor's end re-read its
-  // last row; the consumer masks both.
-  // All lanes of load i fall in one tile of the stage (a load covers 64 chunks,
-  // 4 rows of bf16 or 8 of fp8, and the positions are 64-aligned), so its
-  // source address is a wave-uniform part (that tile's first row) plus a
-  // per-lane part that does not change from stage to stage, computed once here.
-  const int64_t head_off = static_cast<int64_t>(h) * D * (kFp8 ? 1 : 2);
-  constexpr int kStageChunks = kStageKeys * S::kChunks;  // chunks of K (or V) per stage
-  uint32_t lane_off[S::kLoads];
-#pragma unroll
-  for (int i = 0; i < S::kLoads; ++i) {
-    const int pos0 = 64 * (kPrefillWaves * i + wave);
-    const int which = pos0 / kStageChunks;
-    const int rel = pos0 + lane - which * kStageChunks;
-    const int row = rel / S::kChunks;
-    const int q = (rel - row * S::kChunks) ^ (row & (S::kChunks - 1));
-    const int64_t rb = which ? P.v_row_bytes : P.k_row_bytes;
-    lane_off[i] = static_cast<uint32_t>((row & 15) * rb + head_off + 16 * q);
-  }
-  // Whether every page of a stage is readable, for the last two stages staged
-  // (by stage parity): the unmasked loop's test for that stage, so it needs no
-  // page lookups of its own.
-  bool staged_ok[2] = {true, true};
-  auto stage_load = [&](int st, uint8_t* buf) {
-    // Wave-uniform (the buffer is the half's); readfirstlane keeps it in an SGPR
-    // for M0 where the compiler cannot prove it.
-    const uint32_t buf_addr = __builtin_amdgcn_readfirstlane(lds_addr_of(buf));
-    // First rows of the stage's tiles: page lookups once per tile, wave-uniform.
-    int64_t row0[kStageTiles];
-    bool all_ok = true;
-#pragma unroll
-    for (int tt = 0; tt < kStageTiles; ++tt) {
-      bool ok;
-      row0[tt] = key_row<kPaged>(P, bt_row, k_start, st * kStageKeys + tt * kTile, ok, pc);
-      all_ok = all_ok && ok;
-    }
-    staged_ok[st & 1] = all_ok;
-#pragma unroll
-    for (int i = 0; i < S::kLoads; ++i) {
-      const int pos0 = 64 * (kPrefillWaves * i + wave);  // wave-uniform
-      const int which = pos0 / kStageChunks;              // 0: K, 1: V
-      const int tt = ((pos0 - which * kStageChunks) / S::kChunks) >> 4;
-      int64_t first = row0[0];
-#pragma unroll
-      for (int u = 1; u < kStageTiles; ++u)
-        if (tt == u) first = row0[u];
-      const int64_t rb = which ? P.v_row_bytes : P.k_row_bytes;
-      const uint8_t* base = which ? P.v_cache : P.k_cache;
-      const uint8_t* src;
-      if (kPaged || first + 15 <= row_cap) {
-        src = base + first * rb + lane_off[i];
-      } else {
-        // Dense keys whose tile runs past the tensor's end: clamp each row.
-        const int rel = pos0 + lane - which * kStageChunks;
-        const int row = rel / S::kChunks;
-        const int q = (rel - row * S::kChunks) ^ (row & (S::kChunks - 1));
-        src = base + min(first + (row & 15), row_cap) * rb + head_off + 16 * q;
-      }
-      lds_dma16(src, buf_addr + 16 * pos0);
-    }
-  };
-  // Key split, half 1: each pair's P.V waits for the next step and runs right
-  // after its barrier, before that step's loads and scores (the pair's V stays in
-  // its stage buffer: three buffers per half, so the loads issued in step s,
-  // into buffer (s + 1) mod 3, never meet the V of stage s - 1).  The two halves
-  // then run opposite phases between barriers: while half 0's waves issue
-  // their score MFMAs half 1's run the previous softmax's P.V, and while half 0
-  // runs its softmax half 1 issues score MFMAs, instead of both waves of a SIMD
-  // contending for the same pipe at the same time.
-  short4_t pend_pa[kCB], pend_pb[kCB];  // P of the pending pair
-  bool pend = false, pend_ok_a = true, pend_ok_b = true, pend_vm = false;
-  int pend_tok0 = 0;
-  const uint8_t* pend_buf = nullptr;
-  // Consumes one stage from `buf` (this wave's tiles only, two at a time; a pair
-  // whose second tile is past the wave's keys has those keys masked), every pair
-  // with the mask or every pair without it: one variant per loop body keeps the
-  // register count where two waves fit on a SIMD.  With `defer` (half 1 of the
-  // key split, one pair per stage) the pair's P.V is left pending.
-  auto stage_compute = [&](auto masked, int st, const uint8_t* buf,
-                           auto defer) __attribute__((always_inline)) {
-    // Not unrolled: unrolling lets the compiler hoist every tile's LDS reads
-    // (32 registers each) ahead of the first pair's math, and spill.
-#pragma unroll 1
-    for (int tt = 0; tt < kStageTiles; tt += 2) {
-      const int t = st * kStageTiles + tt;
-      if (t >= ntiles) break;  // wave-uniform; the rest of the stage is past this wave's keys
-      if (t + 1 < tbeg) continue;  // wave-uniform; both tiles precede this wave's window
-      bool ok_a = true, ok_b = true;
-      if constexpr (decltype(masked)::value && kPaged) {
-        (void)key_row<kPaged>(P, bt_row, k_start, t * kTile, ok_a, pc);
-        (void)key_row<kPaged>(P, bt_row, k_start, (t + 1) * kTile, ok_b, pc);
-      }
-      if constexpr (decltype(defer)::value) {
-        pend_vm = pair_scores(masked, t * kTile, buf, tt, ok_a, ok_b, pend_pa, pend_pb);
-        pend = true;
-        pend_tok0 = t * kTile;
-        pend_buf = buf;
-        pend_ok_a = ok_a;
-        pend_ok_b = ok_b;
-      } else {
-        short4_t p_a[kCB], p_b[kCB];
-        const bool vm = pair_scores(masked, t * kTile, buf, tt, ok_a, ok_b, p_a, p_b);
-        pair_pv(t * kTile, buf, tt, ok_a, ok_b, vm, p_a, p_b);
-      }
-    }
-  };
-  auto run_pending = [&]() __attribute__((always_inline)) {
-    if (pend) pair_pv(pend_tok0, pend_buf, 0, pend_ok_a, pend_ok_b, pend_vm, pend_pa, pend_pb);
-    pend = false;
-  };
-  // A stage needs no mask when this wave sees all its keys in full (below nfull)
-  // and none of its pages is masked.  Called for stage st before step(st): the
-  // stages staged by then are st and st + 1 at most (st + 2 is staged inside
-  // step(st)), so staged_ok[st & 1] is stage st's page test.
-  auto stage_unmasked = [&](int st) {
-    if ((st + 1) * kStageTiles > nfull) return false;
-    if (win >= 0 && st * kStageKeys < khead) return false;
-    return staged_ok[st & 1];
-  };
-  // kConv: stage st's fp8 rows into its bf16 buffer, the chunks spread over the
-  // threads of the half.  fp8 chunk q of a row (dims 16q .. 16q + 15) becomes
-  // bf16 chunks 2q and 2q + 1 of the row, in the bf16 stage layout.
-  auto stage_convert = [&](int st) {
-    if constexpr (kConv || kConv1) {
-      constexpr int kRowChunks = kStageKeys * S::kChunks;  // fp8 chunks of K (or V)
-      constexpr int kThreads = kPrefillWaves * 64;
-      const uint8_t* fbuf = stage_buf(st);
-      uint8_t* bbuf = comp_buf(st);
-      const int tid = threadIdx.x & (kThreads - 1);
-#pragma unroll
-      for (int c0 = 0; c0 < 2 * kRowChunks; c0 += kThreads) {
-        const int c = c0 + tid;
-        const int which = c / kRowChunks;  // 0: K, 1: V
-        const int rem = c - which * kRowChunks;
-        const int row = rem / S::kChunks;
-        const int q = rem - row * S::kChunks;
-        const uint4 x = *reinterpret_cast<const uint4*>(fbuf + S::offset(which, row, q));
-        const float sc = which ? vsc : ks;
-        const uint2 a = fp8x4_to_bf16x4(x.x, sc), b = fp8x4_to_bf16x4(x.y, sc);
-        const uint2 e = fp8x4_to_bf16x4(x.z, sc), f = fp8x4_to_bf16x4(x.w, sc);
-        *reinterpret_cast<uint4*>(bbuf + SB::offset(which, row, 2 * q)) = make_uint4(a.x, a.y, b.x, b.y);
-        *reinterpret_cast<uint4*>(bbuf + SB::offset(which, row, 2 * q + 1)) =
-            make_uint4(e.x, e.y, f.x, f.y);
-      }
-    }
-  };
-  // One step: wait for stage st's loads (every thread's, through the barrier,
-  // which also frees the buffer the next loads go to), issue stage st + 1's,
-  // consume stage st.  The unmasked and masked stages run in separate loops;
-  // every wave passes exactly nsteps barriers whichever loops it is in.
-  // kConv: stage st + 1's loads landed (the wait and the barrier), so it is
-  // converted, and stage st + 2 is staged into the fp8 buffer stage st held
-  // (converted in the step before); stage st is read from its bf16 buffer.
-  auto step = [&](auto masked, int st, auto defer) __attribute__((always_inline)) {
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if constexpr (decltype(defer)::value) run_pending();
-    if constexpr (kConv) {
-      if (st + 1 < st_hi) stage_convert(st + 1);
-      if (st + 2 < st_hi) stage_load(st + 2, stage_buf(st + 2));
-    } else if constexpr (!kConv1) {
-      if (st + 1 < st_hi) stage_load(st + 1, stage_buf(st + 1));
-    }
-    stage_compute(masked, st, comp_buf(st), defer);
-    if constexpr (kConv1) {
-      __syncthreads();  // every wave is done with the bf16 buffer
-      if (st + 1 < st_hi) stage_convert(st + 1);
-      if (st + 2 < st_hi) stage_load(st + 2, stage_buf(st + 2));
-    }
-  };
-  // Stages [st0, nstages): under a window, a masked head (keys some query's
-  // window starts after), then the unmasked stages, then the masked rest.
-  if (st_lo < st_hi) stage_load(st_lo, stage_buf(st_lo));
-  if constexpr (kConv || kConv1) {
-    // The first stage converted before the loop, the second staged; every wave
-    // of the work-group passes this barrier (with the key split the halves'
-    // ranges differ, one may be empty).
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (st_lo < st_hi) stage_convert(st_lo);
-    if (st_lo + 1 < st_hi) stage_load(st_lo + 1, stage_buf(st_lo + 1));
-  }
-  const int head_end = win >= 0 ? max(st0, (khead + kStageKeys - 1) / kStageKeys) : st0;
-  auto run_stages = [&](auto defer) __attribute__((always_inline)) {
-    int st = st_lo;
-#pragma unroll 1
-    for (; st < st_hi && st < head_end; ++st) step(std::true_type{}, st, defer);
-#pragma unroll 1
-    for (; st < st_hi && stage_unmasked(st); ++st) step(std::false_type{}, st, defer);
-#pragma unroll 1
-    for (; st < st_hi; ++st) step(std::true_type{}, st, defer);
-    if constexpr (decltype(defer)::value) run_pending();
-  };
-  if constexpr (kPingPong) {
-    if (half == 1)
-      run_stages(std::true_type{});
-    else
-      run_stages(std::false_type{});
-  } else {
-    run_stages(std::false_type{});
-  }
-  // Row maxima and sums of the rows this lane holds (row 4g + i of block nb).
-  float m_row[kCB][4], l_row[kCB][4];
-#pragma unroll
-  for (int nb = 0; nb < kCB; ++nb)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      m_row[nb][i] = row_value<16>(m_run[nb], g, i);
-      l_row[nb][i] = l_acc[nb][i];
-    }
-  if constexpr (kKS > 1) {
-#pragma unroll 1
-    for (int k = st_hi - st_lo; k < nsteps; ++k) {  // the shorter half's empty steps
-      __builtin_amdgcn_s_waitcnt(0);
-      __syncthreads();
-      if constexpr (kConv1) __syncthreads();
-    }
-    __syncthreads();  // every wave is done with the stage buffers
-    // Exchange area of this wave role: O tiles, row sums, column maxima.
-    float* const xo = reinterpret_cast<float*>(lds_all) + wave * kXFloats;
-    float* const xl = xo + kCB * (D / 16) * 64 * 4;
-    float* const xm = xl + kCB * 64 * 4;
-    if (half == 1 && active) {
-#pragma unroll
-      for (int nb = 0; nb < kCB; ++nb) {
-#pragma unroll
-        for (int d = 0; d < D / 16; ++d)
-          *reinterpret_cast<floatx4_t*>(xo + ((nb * (D / 16) + d) * 64 + lane) * 4) = o[nb][d];
-        *reinterpret_cast<floatx4_t*>(xl + (nb * 64 + lane) * 4) = l_acc[nb];
-        xm[nb * 64 + lane] = m_run[nb];
-      }
-    }
-    __syncthreads();
-    if (half == 1) return;  // from process_block: the first half writes the rows
-    if (active) {
-      // Log-sum-exp merge of the two halves, row by row (reduce_segments'
-      // rule): M = max(m_a, m_b), O = O_a 2^(m_a - M) + O_b 2^(m_b - M), and
-      // the same for the sums; a half that saw no key (max -inf) weighs 0.
-#pragma unroll
-      for (int nb = 0; nb < kCB; ++nb) {
-        const float mb_col = xm[nb * 64 + lane];
-        const floatx4_t lb = *reinterpret_cast<const floatx4_t*>(xl + (nb * 64 + lane) * 4);
-        float wa[4], wb[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float ma = m_row[nb][i];
-          const float mb = row_value<16>(mb_col, g, i);
-          const float mx = fmaxf(ma, mb);
-          wa[i] = ma == kNegInf ? 0.f : __builtin_amdgcn_exp2f(ma - mx);
-          wb[i] = mb == kNegInf ? 0.f : __builtin_amdgcn_exp2f(mb - mx);
-          m_row[nb][i] = mx;
-          l_row[nb][i] = l_row[nb][i] * wa[i] + lb[i] * wb[i];
-        }
-#pragma unroll
-        for (int d = 0; d < D / 16; ++d) {
-          const floatx4_t ob =
-              *reinterpret_cast<const floatx4_t*>(xo + ((nb * (D / 16) + d) * 64 + lane) * 4);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) o[nb][d][i] = o[nb][d][i] * wa[i] + ob[i] * wb[i];
-        }
-      }
-    }
-  }
-  if (!active) return;  // from process_block: this wave has no queries here
-
-#pragma unroll
-  for (int nb = 0; nb < kCB; ++nb) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int jr = j0 + 16 * nb + 4 * g + i;  // query row this lane holds
-      float l = l_row[nb][i];
-      if (P.sinks) l = with_sink(l, m_row[nb][i], P.sinks[hq] * kLog2e);
-      if (jr >= q_len) continue;
-      const float f = l > 0.f ? 1.f / l : 0.f;
-      uint16_t* orow = P.out + static_cast<int64_t>(q_start + jr) * P.out_row_stride +
-                       static_cast<int64_t>(hq) * D;
-      if constexpr (!kFp8T) {
-        // o[nb][d] holds dim 16d + r: lanes r = 0..15 write 16 adjacent dims.
-#pragma unroll
-        for (int d = 0; d < D / 16; ++d)
-          orow[16 * d + r] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(o[nb][d][i] * f));
-      } else {
-        // o[nb][d] holds dim (D/16) r + d: D/16 adjacent dims per lane.
-        uint32_t w[D / 32];
-#pragma unroll
-        for (int d = 0; d < D / 32; ++d) {
-          const bf16x2_t pk = {static_cast<__bf16>(o[nb][2 * d][i] * f),
-                               static_cast<__bf16>(o[nb][2 * d + 1][i] * f)};
-          w[d] = __builtin_bit_cast(uint32_t, pk);
-        }
-        uint16_t* dst = orow + (D / 16) * r;
-        if constexpr (D == 64) {
-          *reinterpret_cast<uint2*>(dst) = make_uint2(w[0], w[1]);
-        } else {
-#pragma unroll
-          for (int q = 0; q < D / 128; ++q)
-            *reinterpret_cast<uint4*>(dst + 8 * q) =
-                make_uint4(w[4 * q], w[4 * q + 1], w[4 * q + 2], w[4 * q + 3]);
-        }
-      }
-    }
-  }
-  };
-  const int heavy = nqb - 1 - x;
-  // A loop rather than two calls: one copy of the block code (registers).
-#pragma unroll 1
-  for (int k = 0; k < 2; ++k) {
-    if (k == 1) {
-      if (!paired || x == heavy) break;  // unpaired, or the middle block of an odd count
-      __syncthreads();                   // every wave is done with the last stage buffer
-    }
-    process_block(k == 0 ? heavy : x);
-  }
-}
-
-template <bool FP8, bool PAGED, int D>
-void launch_prefill(bool split, const PrefillParams& P, dim3 grid, const int32_t* bt,
-                    const int32_t* cu_q, const int32_t* cu_k, hipStream_t stream) {
-  if constexpr (D <= 128 || PAGED) {
-    if (split) {
-      hipLaunchKernelGGL((paged_prefill_kernel<FP8, PAGED, D, 2>), grid,
-                         dim3(2 * kPrefillWaves * 64), 0, stream, P, bt, cu_q, cu_k);
-      return;
-    }
-  }
-  hipLaunchKernelGGL((paged_prefill_kernel<FP8, PAGED, D, 1>), grid, dim3(kPrefillWaves * 64), 0,
-                     stream, P, bt, cu_q, cu_k);
+// (query / key, value) head sizes the library is built for.
+bool prefill_heads_supported(int d, int dv, bool fp8_pages) {
+  if (fp8_pages) return d == dv && (d == 64 || d == 128 || d == 256);
+  if (d == dv)
+    return d == 32 || d == 64 || d == 72 || d == 80 || d == 96 || d == 128 || d == 256;
+  return d == 192 && dv == 128;
 }
 
 template <int D>
 void launch_prefill_d(bool paged, bool fp8, bool split, const PrefillParams& P, dim3 grid,
                       const int32_t* bt, const int32_t* cu_q, const int32_t* cu_k,
                       hipStream_t stream) {
-  if (!paged)
-    launch_prefill<false, false, D>(split, P, grid, nullptr, cu_q, cu_k, stream);
-  else if (fp8)
-    launch_prefill<true, true, D>(split, P, grid, bt, cu_q, cu_k, stream);
+  if (paged && fp8)
+    launch_prefill<true, true, D, D>(split, P, grid, bt, cu_q, cu_k, stream);
   else
-    launch_prefill<false, true, D>(split, P, grid, bt, cu_q, cu_k, stream);
+    launch_prefill_bf16<D, D>(paged, split, P, grid, bt, cu_q, cu_k, stream);
 }
-
-}  // namespace
-}  // namespace fk
-
-namespace fk {
-namespace {
 
 int prefill_entry(const char* name, bool paged, void* out, int64_t out_row_stride, const void* q,
                   int64_t q_row_stride, const void* k, int64_t k_row_bytes, const void* v,
@@ -1020,8 +34,9 @@ int prefill_entry(const char* name, bool paged, void* out, int64_t out_row_strid
                   const int32_t* block_tables, int64_t bt_row_stride,
                   const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int64_t batch,
                   int64_t max_seqlen_q, int64_t max_seqlen_k, int num_heads, int num_kv_heads,
-                  int head_size, int block_size, int64_t num_blocks, float scale, int causal,
-                  int window_left, const float* sinks, void* stream) {
+                  int head_size, int head_size_v, int block_size, int64_t num_blocks,
+                  float scale, int causal, int window_left, const float* sinks, float* lse,
+                  int64_t lse_row_stride, void* stream) {
   FK_REQUIRE(batch >= 0 && batch <= 65535, "%s: batch %lld out of range [0, 65535]", name,
              (long long)batch);
   FK_REQUIRE(window_left >= -1, "%s: window_left %d must be -1 (no window) or >= 0", name,
@@ -1035,9 +50,11 @@ int prefill_entry(const char* name, bool paged, void* out, int64_t out_row_strid
   FK_REQUIRE(num_heads > 0 && num_kv_heads > 0 && num_heads % num_kv_heads == 0,
              "%s: num_heads %d must be a positive multiple of num_kv_heads %d", name, num_heads,
              num_kv_heads);
-  if (head_size != 64 && head_size != 128 && head_size != 256)
-    return set_error(FK_ERR_UNSUPPORTED, "%s: head_size %d unsupported (64, 128 or 256)", name,
-                     head_size);
+  if (!prefill_heads_supported(head_size, head_size_v, kv_dtype == FK_DTYPE_FP8_E4M3FN && paged))
+    return set_error(FK_ERR_UNSUPPORTED,
+                     "%s: head sizes (query/key %d, value %d) unsupported: equal sizes 32, 64, 72, "
+                     "80, 96, 128 or 256, or 192 / 128 (fp8 pages: 64, 128 or 256)",
+                     name, head_size, head_size_v);
   FK_REQUIRE(num_kv_heads <= 32767, "%s: too many kv heads", name);
   if (paged) {
     FK_REQUIRE(block_size >= kTile && (block_size & (block_size - 1)) == 0,
@@ -1046,12 +63,14 @@ int prefill_entry(const char* name, bool paged, void* out, int64_t out_row_strid
                "%s: kv dtype %d unsupported (bf16 or fp8 e4m3fn)", name, kv_dtype);
   }
   FK_REQUIRE(q_row_stride >= static_cast<int64_t>(num_heads) * head_size &&
-                 out_row_stride >= static_cast<int64_t>(num_heads) * head_size,
+                 out_row_stride >= static_cast<int64_t>(num_heads) * head_size_v,
              "%s: row stride shorter than num_heads * head_size", name);
   const int64_t elem = kv_dtype == FK_DTYPE_FP8_E4M3FN ? 1 : 2;
   FK_REQUIRE(k_row_bytes >= num_kv_heads * head_size * elem &&
-                 v_row_bytes >= num_kv_heads * head_size * elem,
-             "%s: key/value rows shorter than num_kv_heads * head_size", name);
+                 v_row_bytes >= num_kv_heads * head_size_v * elem,
+             "%s: key/value rows shorter than num_kv_heads * head size", name);
+  FK_REQUIRE(!lse || lse_row_stride >= 0, "%s: lse row stride must be >= 0", name);
+  FK_REQUIRE(!lse || !paged, "%s: the log-sum-exp output is built for dense keys only", name);
   if (batch == 0 || max_seqlen_q == 0) return FK_OK;
   FK_REQUIRE(out && q && k && v && cu_seqlens_q && cu_seqlens_k && (!paged || block_tables),
              "%s: null pointer", name);
@@ -1063,7 +82,7 @@ int prefill_entry(const char* name, bool paged, void* out, int64_t out_row_strid
   const int gqa = num_heads / num_kv_heads;
   const int hw = gqa < kPrefillWaves ? gqa : kPrefillWaves;  // query heads per work-group
   const int64_t wg_tokens =
-      static_cast<int64_t>(kPrefillWaves / hw) * 16 * col_blocks_for(head_size);
+      static_cast<int64_t>(kPrefillWaves / hw) * 16 * col_blocks_for(head_size, head_size_v);
   const int64_t qblocks = (max_seqlen_q + wg_tokens - 1) / wg_tokens;
   PrefillParams P;
   P.out = static_cast<uint16_t*>(out);
@@ -1087,6 +106,8 @@ int prefill_entry(const char* name, bool paged, void* out, int64_t out_row_strid
   P.causal = causal ? 1 : 0;
   P.window_left = window_left;
   P.sinks = sinks;
+  P.lse = lse;
+  P.lse_row_stride = lse_row_stride;
   const int hsplit = (gqa + hw - 1) / hw;
   FK_REQUIRE(qblocks <= 65535, "%s: max_seqlen_q %lld needs more than 65535 query blocks", name,
              (long long)max_seqlen_q);
@@ -1103,11 +124,18 @@ int prefill_entry(const char* name, bool paged, void* out, int64_t out_row_strid
   const bool may_pair = causal && max_seqlen_k > 0 && max_seqlen_k < 2 * max_seqlen_q;
   const int64_t wgs = static_cast<int64_t>(num_kv_heads) * hsplit * batch *
                       (may_pair ? (qblocks + 1) / 2 : qblocks);
-  const bool split = (head_size <= 128 || paged) && wgs < 2LL * num_cus();
-  switch (head_size) {
-    case 64: launch_prefill_d<64>(paged, fp8, split, P, grid, block_tables, cu_seqlens_q, cu_seqlens_k, s); break;
-    case 256: launch_prefill_d<256>(paged, fp8, split, P, grid, block_tables, cu_seqlens_q, cu_seqlens_k, s); break;
-    default: launch_prefill_d<128>(paged, fp8, split, P, grid, block_tables, cu_seqlens_q, cu_seqlens_k, s); break;
+  const bool split = (std::max(head_size, head_size_v) <= 192 || paged) &&
+                     wgs < 2LL * num_cus();
+  if (head_size == head_size_v && (head_size == 64 || head_size == 128 || head_size == 256)) {
+    switch (head_size) {
+      case 64: launch_prefill_d<64>(paged, fp8, split, P, grid, block_tables, cu_seqlens_q, cu_seqlens_k, s); break;
+      case 256: launch_prefill_d<256>(paged, fp8, split, P, grid, block_tables, cu_seqlens_q, cu_seqlens_k, s); break;
+      default: launch_prefill_d<128>(paged, fp8, split, P, grid, block_tables, cu_seqlens_q, cu_seqlens_k, s); break;
+    }
+  } else if (!launch_prefill_extra(head_size, head_size_v, paged, split, P, grid, block_tables,
+                                   cu_seqlens_q, cu_seqlens_k, s)) {
+    return set_error(FK_ERR_UNSUPPORTED, "%s: head sizes %d / %d not built", name, head_size,
+                     head_size_v);
   }
   return check_launch(name);
 }
@@ -1121,16 +149,18 @@ extern "C" int fk_paged_prefill(void* out, int64_t out_row_stride, const void* q
                                 const int32_t* block_tables, int64_t bt_row_stride,
                                 const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
                                 int64_t batch, int64_t max_seqlen_q, int64_t max_seqlen_k,
-                                int num_heads, int num_kv_heads, int head_size, int block_size,
-                                int64_t num_blocks, float scale, int causal, int window_left,
-                                const float* sinks, void* stream) {
-  const int64_t row = static_cast<int64_t>(num_kv_heads) * head_size *
-                      (kv_dtype == FK_DTYPE_FP8_E4M3FN ? 1 : 2);
+                                int num_heads, int num_kv_heads, int head_size, int head_size_v,
+                                int block_size, int64_t num_blocks, float scale, int causal,
+                                int window_left, const float* sinks, void* stream) {
+  const int64_t elem = kv_dtype == FK_DTYPE_FP8_E4M3FN ? 1 : 2;
+  const int64_t k_row = static_cast<int64_t>(num_kv_heads) * head_size * elem;
+  const int64_t v_row = static_cast<int64_t>(num_kv_heads) * head_size_v * elem;
   return fk::prefill_entry("fk_paged_prefill", true, out, out_row_stride, q, q_row_stride,
-                           k_cache, row, v_cache, row, kv_dtype, k_scale, v_scale, block_tables,
-                           bt_row_stride, cu_seqlens_q, cu_seqlens_k, batch, max_seqlen_q,
-                           max_seqlen_k, num_heads, num_kv_heads, head_size, block_size,
-                           num_blocks, scale, causal, window_left, sinks, stream);
+                           k_cache, k_row, v_cache, v_row, kv_dtype, k_scale, v_scale,
+                           block_tables, bt_row_stride, cu_seqlens_q, cu_seqlens_k, batch,
+                           max_seqlen_q, max_seqlen_k, num_heads, num_kv_heads, head_size,
+                           head_size_v, block_size, num_blocks, scale, causal, window_left,
+                           sinks, nullptr, 0, stream);
 }
 
 extern "C" int fk_varlen_prefill(void* out, int64_t out_row_stride, const void* q,
@@ -1138,12 +168,13 @@ extern "C" int fk_varlen_prefill(void* out, int64_t out_row_stride, const void* 
                                  const void* value, int64_t value_row_stride,
                                  const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
                                  int64_t batch, int64_t max_seqlen_q, int64_t max_seqlen_k,
-                                 int num_heads, int num_kv_heads, int head_size, float scale,
-                                 int causal, int window_left, const float* sinks,
-                                 void* stream) {
+                                 int num_heads, int num_kv_heads, int head_size, int head_size_v,
+                                 float scale, int causal, int window_left, const float* sinks,
+                                 float* lse, int64_t lse_row_stride, void* stream) {
   return fk::prefill_entry("fk_varlen_prefill", false, out, out_row_stride, q, q_row_stride, key,
                            key_row_stride * 2, value, value_row_stride * 2, FK_DTYPE_BF16,
                            nullptr, nullptr, nullptr, 0, cu_seqlens_q, cu_seqlens_k, batch,
-                           max_seqlen_q, max_seqlen_k, num_heads, num_kv_heads, head_size, 16, 0,
-                           scale, causal, window_left, sinks, stream);
+                           max_seqlen_q, max_seqlen_k, num_heads, num_kv_heads, head_size,
+                           head_size_v, 16, 0, scale, causal, window_left, sinks, lse,
+                           lse_row_stride, stream);
 }

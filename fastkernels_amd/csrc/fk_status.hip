@@ -47,6 +47,8 @@ int num_cus() {
 
 }  // namespace fk
 
-extern "C" int fk_version(void) { return 100; }  // 0.1.0
+// 2.0.0: fk_paged_prefill / fk_varlen_prefill gained head_size_v, lse and
+// lse_row_stride (1.x had max_seqlen_k added in the middle of both signatures).
+extern "C" int fk_version(void) { return FK_VERSION_MAJOR * 10000; }
 
 extern "C" const char* fk_last_error(void) { return fk::g_last_error; }

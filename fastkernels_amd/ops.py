@@ -444,17 +444,42 @@ def _check_prefill_extras(q, causal, window_left, sinks):
         _same_device(q, sinks)
 
 
-def _check_prefill(out, q, cu_seqlens_q, cu_seqlens_k):
+# (query / key, value) head sizes the prefill kernel is built for (fp8 pages: the
+# equal sizes 64, 128 and 256).
+PREFILL_HEADS = {(32, 32), (64, 64), (72, 72), (80, 80), (96, 96), (128, 128), (256, 256),
+                 (192, 128)}
+PREFILL_FP8_HEADS = {(64, 64), (128, 128), (256, 256)}
+
+
+def prefill_heads_supported(head_size: int, head_size_v: int | None = None,
+                            fp8: bool = False) -> bool:
+    """Whether the prefill kernel runs at these query / key and value head sizes."""
+    pair = (int(head_size), int(head_size if head_size_v is None else head_size_v))
+    return pair in (PREFILL_FP8_HEADS if fp8 else PREFILL_HEADS)
+
+
+def _check_prefill(out, q, cu_seqlens_q, cu_seqlens_k, dv=None):
+    dv = q.shape[2] if dv is None else dv
     if q.dim() != 3 or q.dtype != torch.bfloat16 or q.stride(2) != 1 or q.stride(1) != q.shape[2]:
         raise ValueError("prefill: q must be bf16 [tokens, Hq, D] with contiguous heads")
-    if out.shape != q.shape or out.dtype != q.dtype or out.stride(2) != 1 or \
-            out.stride(1) != q.shape[2]:
-        raise ValueError("prefill: out must be bf16 [tokens, Hq, D] with contiguous heads")
+    if tuple(out.shape) != (q.shape[0], q.shape[1], dv) or out.dtype != q.dtype or \
+            out.stride(2) != 1 or out.stride(1) != dv:
+        raise ValueError("prefill: out must be bf16 [tokens, Hq, Dv] with contiguous heads")
     for t, nm in ((cu_seqlens_q, "cu_seqlens_q"), (cu_seqlens_k, "cu_seqlens_k")):
         if t.dtype != torch.int32 or t.dim() != 1 or not t.is_contiguous():
             raise TypeError(f"prefill: {nm} must be contiguous int32 [batch + 1]")
     if cu_seqlens_k.numel() < cu_seqlens_q.numel():
         raise ValueError("prefill: cu_seqlens_k shorter than cu_seqlens_q")
+
+
+def _check_lse(lse, q, what):
+    if lse is None:
+        return
+    if lse.dtype != torch.float32 or lse.dim() != 2 or lse.shape[0] != q.shape[1] or \
+            lse.shape[1] < q.shape[0] or lse.stride(1) != 1:
+        raise ValueError(f"{what}: lse must be float32 [num_heads, >= total_q] with "
+                         "contiguous rows")
+    _same_device(q, lse)
 
 
 def paged_prefill(out: torch.Tensor, q: torch.Tensor, k_cache: torch.Tensor,
@@ -463,16 +488,23 @@ def paged_prefill(out: torch.Tensor, q: torch.Tensor, k_cache: torch.Tensor,
                   k_scale: torch.Tensor | None = None, v_scale: torch.Tensor | None = None,
                   causal: bool = True, window_left: int = -1,
                   sinks: torch.Tensor | None = None, max_seqlen_k: int = 0) -> None:
-    """Causal prefill over paged K/V into ``out`` ([tokens, Hq, D] bf16): sequence b's
+    """Causal prefill over paged K/V into ``out`` ([tokens, Hq, Dv] bf16): sequence b's
     queries q[cu_q[b]:cu_q[b+1]] attend to its first cu_k[b+1]-cu_k[b] cached tokens,
     aligned to their end (flash_attn_varlen_func with block_table, seqused_k).
     window_left >= 0: each query sees its last window_left + 1 positions; sinks
     (float32 [Hq]) join each row's softmax denominator.  max_seqlen_k bounds every
-    sequence's key count (0: unknown); it only chooses the launch shape."""
-    _check_prefill(out, q, cu_seqlens_q, cu_seqlens_k)
+    sequence's key count (0: unknown); it only chooses the launch shape.  The value
+    cache may have its own head size Dv (``PREFILL_HEADS``)."""
+    dv = v_cache.shape[3] if v_cache.dim() == 4 else q.shape[2]
+    _check_prefill(out, q, cu_seqlens_q, cu_seqlens_k, dv)
     _check_prefill_extras(q, causal, window_left, sinks)
-    if k_cache.dim() != 4 or v_cache.shape != k_cache.shape or k_cache.shape[3] != q.shape[2]:
-        raise ValueError("paged_prefill: caches must be [num_blocks, block_size, Hk, D]")
+    if k_cache.dim() != 4 or v_cache.dim() != 4 or v_cache.shape[:3] != k_cache.shape[:3] or \
+            k_cache.shape[3] != q.shape[2]:
+        raise ValueError("paged_prefill: caches must be [num_blocks, block_size, Hk, D] "
+                         "(the value cache's head size may differ)")
+    if not prefill_heads_supported(q.shape[2], dv, k_cache.dtype == _FP8):
+        raise NotImplementedError(f"paged_prefill: head sizes {q.shape[2]} / {dv} are not "
+                                  "built (see ops.PREFILL_HEADS)")
     if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
         raise ValueError("paged_prefill: caches must be contiguous")
     if k_cache.dtype != v_cache.dtype or k_cache.dtype not in (torch.bfloat16, _FP8):
@@ -496,21 +528,33 @@ def paged_prefill(out: torch.Tensor, q: torch.Tensor, k_cache: torch.Tensor,
                  _native.FK_DTYPE_FP8_E4M3FN if k_cache.dtype == _FP8 else _native.FK_DTYPE_BF16,
                  _ptr(k_scale), _ptr(v_scale), _ptr(block_table), block_table.stride(0),
                  _ptr(cu_seqlens_q), _ptr(cu_seqlens_k), batch, int(max_seqlen_q),
-                 int(max_seqlen_k), q.shape[1], hk, q.shape[2], bs, nb, float(softmax_scale),
-                 int(bool(causal)), int(window_left), _ptr(sinks), _stream(q))
+                 int(max_seqlen_k), q.shape[1], hk, q.shape[2], dv, bs, nb,
+                 float(softmax_scale), int(bool(causal)), int(window_left), _ptr(sinks),
+                 _stream(q))
 
 
 def varlen_prefill(out: torch.Tensor, q: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
                    cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor, max_seqlen_q: int,
                    softmax_scale: float, causal: bool = True, window_left: int = -1,
-                   sinks: torch.Tensor | None = None, max_seqlen_k: int = 0) -> None:
-    """Causal prefill over dense keys: key/value [total_k, Hk, D] bf16 (rows may be strided
-    views), sequence b's keys being rows cu_k[b]..cu_k[b+1].  window_left, sinks and
-    max_seqlen_k as in :func:`paged_prefill`."""
-    _check_prefill(out, q, cu_seqlens_q, cu_seqlens_k)
+                   sinks: torch.Tensor | None = None, max_seqlen_k: int = 0,
+                   lse: torch.Tensor | None = None) -> None:
+    """Causal prefill over dense keys: key [total_k, Hk, D] / value [total_k, Hk, Dv] bf16
+    (rows may be strided views), sequence b's keys being rows cu_k[b]..cu_k[b+1].
+    window_left, sinks, max_seqlen_k and head sizes as in :func:`paged_prefill`.  lse
+    (float32 [Hq, >= total_q], rows contiguous) receives each row's softmax log-sum-exp,
+    -inf without visible keys (FlashAttnVarlen's return_softmax_lse,
+    flash_attn_varlen.py:21-47)."""
+    dv = value.shape[2] if value.dim() == 3 else q.shape[2]
+    _check_prefill(out, q, cu_seqlens_q, cu_seqlens_k, dv)
     _check_prefill_extras(q, causal, window_left, sinks)
-    if key.dim() != 3 or value.shape != key.shape or key.shape[2] != q.shape[2]:
-        raise ValueError("varlen_prefill: key/value must be [total_k, Hk, D]")
+    _check_lse(lse, q, "varlen_prefill")
+    if key.dim() != 3 or value.dim() != 3 or value.shape[:2] != key.shape[:2] or \
+            key.shape[2] != q.shape[2]:
+        raise ValueError("varlen_prefill: key must be [total_k, Hk, D] and value "
+                         "[total_k, Hk, Dv]")
+    if not prefill_heads_supported(q.shape[2], dv):
+        raise NotImplementedError(f"varlen_prefill: head sizes {q.shape[2]} / {dv} are not "
+                                  "built (see ops.PREFILL_HEADS)")
     for t, nm in ((key, "key"), (value, "value")):
         if t.dtype != torch.bfloat16 or t.stride(2) != 1 or (t.shape[1] > 1 and
                                                              t.stride(1) != t.shape[2]):
@@ -522,8 +566,9 @@ def varlen_prefill(out: torch.Tensor, q: torch.Tensor, key: torch.Tensor, value:
     _native.call("fk_varlen_prefill", _ptr(out), out.stride(0), _ptr(q), q.stride(0), _ptr(key),
                  key.stride(0), _ptr(value), value.stride(0), _ptr(cu_seqlens_q),
                  _ptr(cu_seqlens_k), batch, int(max_seqlen_q), int(max_seqlen_k), q.shape[1],
-                 key.shape[1], q.shape[2], float(softmax_scale), int(bool(causal)),
-                 int(window_left), _ptr(sinks), _stream(q))
+                 key.shape[1], q.shape[2], dv, float(softmax_scale), int(bool(causal)),
+                 int(window_left), _ptr(sinks), _ptr(lse), 0 if lse is None else lse.stride(0),
+                 _stream(q))
 
 
 def paged_decode_phases(out, q, k_cache, v_cache, block_table, cache_seqlens, softmax_scale,
@@ -641,7 +686,7 @@ _LIB.define("paged_prefill(Tensor(a!) out, Tensor q, Tensor k_cache, Tensor v_ca
 _LIB.define("varlen_prefill(Tensor(a!) out, Tensor q, Tensor key, Tensor value, "
             "Tensor cu_seqlens_q, Tensor cu_seqlens_k, int max_seqlen_q, float softmax_scale, "
             "bool causal=True, int window_left=-1, Tensor? sinks=None, "
-            "int max_seqlen_k=0) -> ()")
+            "int max_seqlen_k=0, Tensor(b!)? lse=None) -> ()")
 _LIB.define("silu_and_mul(Tensor! result, Tensor input) -> ()")
 _LIB.define("merge_attn_states(Tensor(a!) output, Tensor prefix_output, Tensor prefix_lse, "
             "Tensor suffix_output, Tensor suffix_lse, Tensor(b!)? output_lse) -> ()")

@@ -73,7 +73,10 @@ extern "C" {
 #define FK_DTYPE_BF16 2
 #define FK_DTYPE_FP8_E4M3FN 3 /* OCP float8 e4m3fn (torch.float8_e4m3fn) */
 
-/* Library version as 10000*major + 100*minor + patch. */
+/* Library version as 10000*major + 100*minor + patch.  The major version changes
+ * whenever an existing entry point's signature changes; a caller built against this
+ * header checks fk_version() / 10000 == FK_VERSION_MAJOR before binding. */
+#define FK_VERSION_MAJOR 2
 int fk_version(void);
 
 /* Message describing the last failing call on this thread ("" if none). */
@@ -263,31 +266,44 @@ int fk_store_kvcache_convert(const void* key, int64_t key_row_stride, const void
  * query tokens, 128 for GQA group 1).  max_seqlen_k (flash_attn_varlen_func's
  * max_seqlen_k): a bound on every sequence's key count, or 0 if unknown; it only
  * chooses the launch shape (with few query blocks, each block's keys are split over
- * two halves of a work-group and merged).  head_size 64, 128 or 256; num_heads any
- * multiple of num_kv_heads; kv dtype bf16 or fp8 e4m3fn (with k_scale / v_scale as in
- * fk_paged_decode).  No workspace; nothing is allocated. */
+ * two halves of a work-group and merged).  num_heads any multiple of num_kv_heads.
+ * Head sizes: head_size (query / key) and head_size_v (value; out rows are
+ * [rows, Hq*head_size_v], the v cache [num_blocks, block_size, Hk, head_size_v]):
+ * equal sizes 32, 64, 72, 80, 96, 128 or 256, or 192 / 128 (MLA); others give
+ * FK_ERR_UNSUPPORTED.  kv dtype bf16, or fp8 e4m3fn at equal sizes 64, 128, 256 (with
+ * k_scale / v_scale as in fk_paged_decode).
+ * No workspace; nothing is allocated.
+ * Changed in version 20000: head_size_v added. */
 int fk_paged_prefill(void* out, int64_t out_row_stride, const void* q, int64_t q_row_stride,
                      const void* k_cache, const void* v_cache, int kv_dtype, const float* k_scale,
                      const float* v_scale, const int32_t* block_tables, int64_t bt_row_stride,
                      const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int64_t batch,
                      int64_t max_seqlen_q, int64_t max_seqlen_k, int num_heads,
-                     int num_kv_heads, int head_size, int block_size, int64_t num_blocks,
-                     float scale, int causal, int window_left, const float* sinks,
-                     void* stream);
+                     int num_kv_heads, int head_size, int head_size_v, int block_size,
+                     int64_t num_blocks, float scale, int causal, int window_left,
+                     const float* sinks, void* stream);
 
 /* The same attention over dense keys: FlashAttnPrefill.forward without a block table
  * (flash_attn_prefill.py:65-74; Attention._prefill_torch_from_tensors,
  * attention_impl.py:624-638).  key / value: [total_k, Hk*head_size] bf16 rows (strides in
  * elements; views of the qkv buffer allowed); sequence b's keys are rows
- * [cu_seqlens_k[b], cu_seqlens_k[b+1]).  max_seqlen_k, window_left and sinks as
- * fk_paged_prefill. */
+ * [cu_seqlens_k[b], cu_seqlens_k[b+1]); value rows are [total_k, Hk*head_size_v].
+ * Also FlashAttnVarlen.forward (flash_attn_varlen.py:21-47), including MLA's query /
+ * key 192 with value 128 and return_softmax_lse:
+ * lse: NULL, or device fp32 [num_heads, lse_row_stride] receiving each row's softmax
+ * log-sum-exp at [hq, cu_seqlens_q[b] + j]: ln(sum over visible keys of
+ * e^(scale q.k)) (summed in fp32), plus e^sink when sinks are given, -inf for a row
+ * with no visible key (flash-attn writes +inf there; fk_merge_attn_states reads
+ * both as an empty row).  max_seqlen_k, window_left, sinks and head sizes as
+ * fk_paged_prefill.
+ * Changed in version 20000: head_size_v, lse and lse_row_stride added. */
 int fk_varlen_prefill(void* out, int64_t out_row_stride, const void* q, int64_t q_row_stride,
                       const void* key, int64_t key_row_stride, const void* value,
                       int64_t value_row_stride, const int32_t* cu_seqlens_q,
                       const int32_t* cu_seqlens_k, int64_t batch, int64_t max_seqlen_q,
                       int64_t max_seqlen_k, int num_heads, int num_kv_heads, int head_size,
-                      float scale, int causal, int window_left, const float* sinks,
-                      void* stream);
+                      int head_size_v, float scale, int causal, int window_left,
+                      const float* sinks, float* lse, int64_t lse_row_stride, void* stream);
 
 /* Per-head q/k RMSNorm (optional) + rotary embedding + store_kvcache in one launch:
  * the attention block between the qkv projection and the decode

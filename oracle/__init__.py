@@ -314,11 +314,16 @@ def paged_decode(q: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray,
 
 
 def _prefill_one(qq: np.ndarray, ks: np.ndarray, vs: np.ndarray, scale: float,
-                 causal: bool, window_left: int = -1, sinks: np.ndarray | None = None) -> np.ndarray:
-    """_sdpa_one (attention_impl.py:606-622) in float64: qq [q_len, hq, d], ks/vs
-    [k_len, hk, d]; key_offset = k_len - q_len when causal, else all keys visible.
-    window_left >= 0 (causal): query j also drops keys before pos_j - window_left
-    (triton_unified_attention.py:577-590); sinks as in attend_one."""
+                 causal: bool, window_left: int = -1, sinks: np.ndarray | None = None,
+                 return_lse: bool = False):
+    """_sdpa_one (attention_impl.py:606-622) in float64: qq [q_len, hq, d], ks [k_len,
+    hk, d], vs [k_len, hk, dv] (dv may differ from d, as in MLA prefill); key_offset =
+    k_len - q_len when causal, else all keys visible.  window_left >= 0 (causal): query
+    j also drops keys before pos_j - window_left (triton_unified_attention.py:577-590);
+    sinks as in attend_one.  return_lse: also the rows' log-sum-exp [hq, q_len],
+    ln(sum over visible keys of e^(scale q.k)) plus e^sink with sinks (the denominator
+    the output is divided by), -inf for a row with no visible key
+    (flash_attn_varlen_func's return_softmax_lse, flash_attn_varlen.py:33-46)."""
     q_len, hq, _ = qq.shape
     k_len, hk, _ = ks.shape
     grp = hq // hk
@@ -340,22 +345,37 @@ def _prefill_one(qq: np.ndarray, ks: np.ndarray, vs: np.ndarray, scale: float,
         l = np.where(l > 0, l + np.exp(np.asarray(sinks, np.float64).reshape(hq, 1, 1)
                                        - np.where(has, m, 0.0)), l)
     p = np.where(l > 0, e / np.where(l > 0, l, 1.0), 0.0)
-    return np.einsum("hjt,thd->jhd", p, vh)
+    out = np.einsum("hjt,thd->jhd", p, vh)
+    if not return_lse:
+        return out
+    with np.errstate(divide="ignore"):
+        lse = np.where(l > 0, np.where(has, m, 0.0) + np.log(np.where(l > 0, l, 1.0)), -np.inf)
+    return out, lse[..., 0]
 
 
 def varlen_prefill(q: np.ndarray, key: np.ndarray, value: np.ndarray, cu_seqlens_q: np.ndarray,
                    cu_seqlens_k: np.ndarray, scale: float, causal: bool = True,
-                   window_left: int = -1, sinks: np.ndarray | None = None) -> np.ndarray:
+                   window_left: int = -1, sinks: np.ndarray | None = None,
+                   return_lse: bool = False):
     """_prefill_torch_from_tensors (attention_impl.py:624-638): dense keys, sequence i's
-    being rows cu_k[i]..cu_k[i+1] of key/value [total_k, hk, d]."""
-    out = np.zeros(q.shape, np.float64)
+    being rows cu_k[i]..cu_k[i+1] of key [total_k, hk, d] / value [total_k, hk, dv];
+    the output is [total_q, hq, dv].  return_lse: also (out, lse [hq, total_q]), lse as
+    in _prefill_one (FlashAttnVarlen's return_softmax_lse, flash_attn_varlen.py:33-46);
+    rows of a sequence with no queries are not touched (-inf)."""
+    total_q, hq, _ = q.shape
+    out = np.zeros((total_q, hq, value.shape[-1]), np.float64)
+    lse = np.full((hq, total_q), -np.inf)
     for i in range(len(cu_seqlens_q) - 1):
         qs, qe = int(cu_seqlens_q[i]), int(cu_seqlens_q[i + 1])
         ks, ke = int(cu_seqlens_k[i]), int(cu_seqlens_k[i + 1])
         if qe > qs:
-            out[qs:qe] = _prefill_one(q[qs:qe], key[ks:ke], value[ks:ke], scale, causal,
-                                      window_left, sinks)
-    return out
+            r = _prefill_one(q[qs:qe], key[ks:ke], value[ks:ke], scale, causal, window_left,
+                             sinks, return_lse)
+            if return_lse:
+                out[qs:qe], lse[:, qs:qe] = r
+            else:
+                out[qs:qe] = r
+    return (out, lse) if return_lse else out
 
 
 def paged_prefill(q: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray,
@@ -363,13 +383,16 @@ def paged_prefill(q: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray,
                   scale: float, k_scale: np.ndarray | None = None,
                   v_scale: np.ndarray | None = None, q_dtype: str = "bf16",
                   causal: bool = True, window_left: int = -1,
-                  sinks: np.ndarray | None = None) -> np.ndarray:
+                  sinks: np.ndarray | None = None, return_lse: bool = False):
     """_prefill_torch_from_cache + _sdpa_one (attention_impl.py:606-622, 640-652), the
     torch restatement of FlashAttnPrefill with a block table (flash_attn_prefill.py:28-74):
     sequence i's queries q[cu_q[i]:cu_q[i+1]] attend to the first k_len = cu_k[i+1]-cu_k[i]
     cached tokens, query j seeing keys [0, k_len - q_len + j] (key_offset = k_len - q_len).
-    A query with no visible key gives a zero row.  float64 throughout."""
-    out = np.zeros(q.shape, np.float64)
+    A query with no visible key gives a zero row.  float64 throughout.  The value cache
+    may have its own head size (the output takes it); return_lse as varlen_prefill."""
+    total_q, hq, _ = q.shape
+    out = np.zeros((total_q, hq, v_cache.shape[-1]), np.float64)
+    lse = np.full((hq, total_q), -np.inf)
     fp8 = k_cache.dtype == np.uint8
     for i in range(len(cu_seqlens_q) - 1):
         qs, qe = int(cu_seqlens_q[i]), int(cu_seqlens_q[i + 1])
@@ -381,8 +404,12 @@ def paged_prefill(q: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray,
         if fp8:
             ks = dequant_kv(ks[None], k_scale, q_dtype)[0]
             vs = dequant_kv(vs[None], v_scale, q_dtype)[0]
-        out[qs:qe] = _prefill_one(q[qs:qe], ks, vs, scale, causal, window_left, sinks)
-    return out
+        r = _prefill_one(q[qs:qe], ks, vs, scale, causal, window_left, sinks, return_lse)
+        if return_lse:
+            out[qs:qe], lse[:, qs:qe] = r
+        else:
+            out[qs:qe] = r
+    return (out, lse) if return_lse else out
 
 
 def attend_partials(q: np.ndarray, k_seq: np.ndarray, v_seq: np.ndarray, scale: float,

@@ -57,7 +57,38 @@ def test_library_exports_every_header_symbol(lib):
 
 
 def test_version_and_clean_error(lib):
-    assert lib.fk_version() == 100
+    from fastkernels_amd import _native
+
+    # Major version 2: fk_paged_prefill / fk_varlen_prefill took head_size_v, lse and
+    # lse_row_stride; the bindings refuse a library of another major version.
+    assert lib.fk_version() // 10000 == _native.ABI_MAJOR == 2
+    text = HEADER.read_text()
+    assert re.search(r"#define FK_VERSION_MAJOR 2\b", text)
+
+
+def test_prefill_head_sizes_and_lse_arguments(lib):
+    """fk_varlen_prefill refuses head-size pairs that are not built (before any launch)
+    and names them; the Python layer's table agrees with the C library's."""
+    from fastkernels_amd import _native as N
+    from fastkernels_amd import ops
+
+    fake = ctypes.c_void_p(0x100000)
+    cu = ctypes.c_void_p(0x200000)
+
+    def varlen(d, dv, lse_stride=0):
+        return lib.fk_varlen_prefill(fake, 8 * dv, fake, 8 * d, fake, 2 * d, fake, 2 * dv,
+                                     cu, cu, 1, 16, 16, 8, 2, d, dv, 0.1, 1, -1, None,
+                                     fake if lse_stride else None, lse_stride, None)
+
+    for d, dv in ((48, 48), (128, 64), (192, 192), (512, 512), (80, 72)):
+        assert not ops.prefill_heads_supported(d, dv)
+        assert varlen(d, dv) == N.FK_ERR_UNSUPPORTED, (d, dv)
+        assert "head sizes" in _last_error(lib)
+    for d, dv in ((80, 80), (192, 128), (72, 72), (32, 32), (96, 96)):
+        assert ops.prefill_heads_supported(d, dv)
+    assert not ops.prefill_heads_supported(80, 80, fp8=True)
+    assert ops.prefill_heads_supported(128, 128, fp8=True)
+    assert varlen(128, 128, lse_stride=-1) == N.FK_ERR_INVALID_ARG
 
 
 def _last_error(lib) -> str:

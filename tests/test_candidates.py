@@ -72,6 +72,36 @@ def test_candidate_class_and_signatures(stem):
     assert fwd == fwd_params
 
 
+def test_attention_candidates_refuse_unbuilt_head_sizes_at_construction():
+    """A head size the kernels are not built for is refused by the constructor, not at
+    the first forward: decode runs at 64 / 128 / 256; prefill also at 32, 72, 80 and 96
+    (Qwen-VL vision encoders: 1280 / 16 = 80, L2/vision_attention.py:32,39)."""
+    dec = load_by_path("flash_attn_decode").FlashAttnDecode
+    pre = load_by_path("flash_attn_prefill").FlashAttnPrefill
+    for d in (64, 128, 256):
+        dec(8, 2, d)
+    for d in (80, 96, 192, 512):
+        with pytest.raises(NotImplementedError, match="head_dim"):
+            dec(8, 2, d)
+    for d in (32, 64, 72, 80, 96, 128, 256):
+        assert pre(16, 16, d).head_dim == d
+    for d in (48, 192, 512):
+        with pytest.raises(NotImplementedError, match="head_dim"):
+            pre(8, 2, d)
+
+
+def test_flash_attn_varlen_refuses_unbuilt_head_sizes():
+    """FlashAttnVarlen takes no head size at construction: an unbuilt (query / key,
+    value) pair is refused at forward, before anything runs (CPU tensors here)."""
+    cls = load_by_path("flash_attn_varlen").FlashAttnVarlen
+    cu = torch.tensor([0, 4], dtype=torch.int32)
+    for d, dv in ((48, 48), (128, 64), (192, 192)):
+        q = torch.zeros(4, 2, d, dtype=torch.bfloat16)
+        v = torch.zeros(4, 2, dv, dtype=torch.bfloat16)
+        with pytest.raises(NotImplementedError, match="head sizes"):
+            cls()(q, q, v, cu, cu, 4, 4, 0.1, True, True)
+
+
 def test_merge_attn_states_function_signature():
     """merge_attn_states.py:32-41: the module-level function keeps the reference's arguments."""
     fn = load_by_path("merge_attn_states").merge_attn_states

@@ -176,8 +176,8 @@ def test_varlen_prefill_dense_strided(cuda):
 ])
 def test_flash_attn_varlen_candidate(cuda, causal, hq, hk, d, q_lens, k_lens):
     """FlashAttnVarlen (flash_attn_varlen.py:21-47): dense varlen attention through the
-    candidate class, against oracle.varlen_prefill; return_softmax_lse and unequal
-    head sizes raise."""
+    candidate class, against oracle.varlen_prefill, with and without
+    return_softmax_lse (the LSE against the oracle's within 1e-5)."""
     from fastkernels_amd.candidate.L1.flash_attn_varlen import FlashAttnVarlen
     _flush(f"FlashAttnVarlen causal={causal} hq={hq} hk={hk} d={d}")
     g = torch.Generator().manual_seed(83 + d)
@@ -193,8 +193,16 @@ def test_flash_attn_varlen_candidate(cuda, causal, hq, hk, d, q_lens, k_lens):
                                 v.float().cpu().numpy(), cu_q.cpu().numpy(), cu_k.cpu().numpy(),
                                 d ** -0.5, causal=causal)
     _close(out, ref, 1e-2, f"FlashAttnVarlen causal={causal} d={d}")
-    with pytest.raises(NotImplementedError):
-        m(q, k, v, cu_q, cu_k, max(q_lens), max(k_lens), d ** -0.5, return_softmax_lse=True)
+    out2, lse = m(q, k, v, cu_q, cu_k, max(q_lens), max(k_lens), d ** -0.5, causal=causal,
+                  return_softmax_lse=True)
+    torch.cuda.synchronize()
+    _, ref_lse = oracle.varlen_prefill(q.float().cpu().numpy(), k.float().cpu().numpy(),
+                                       v.float().cpu().numpy(), cu_q.cpu().numpy(),
+                                       cu_k.cpu().numpy(), d ** -0.5, causal=causal,
+                                       return_lse=True)
+    assert torch.equal(out2, out)
+    assert lse.shape == (hq, sum(q_lens)) and lse.dtype == torch.float32
+    np.testing.assert_allclose(lse.cpu().numpy(), ref_lse, rtol=1e-5, atol=1e-5)
 
 
 def test_paged_prefill_qwen3_prompt_2048(cuda):

@@ -592,6 +592,103 @@ def test_varlen_prefill_planted_cu_seqlens_swap_is_caught():
     assert not np.allclose(good, swapped, atol=1e-3)
 
 
+def _masked_scores64(q, key, cu_q, cu_k, i, scale, causal):
+    """Scores [hq, q_len, k_len] of sequence i in float64 with -inf where masked
+    (end-aligned causal or all keys), by torch's matmul."""
+    qs, qe, ks, ke = int(cu_q[i]), int(cu_q[i + 1]), int(cu_k[i]), int(cu_k[i + 1])
+    ql, kl = qe - qs, ke - ks
+    hq, hk = q.shape[1], key.shape[1]
+    k = torch.from_numpy(key[ks:ke]).double().repeat_interleave(hq // hk, 1).transpose(0, 1)
+    qq = torch.from_numpy(q[qs:qe]).double().transpose(0, 1)
+    sc = torch.matmul(qq, k.transpose(1, 2)) * scale
+    if causal:
+        mask = torch.arange(kl)[None, :] <= (kl - ql + torch.arange(ql))[:, None]
+        sc = sc.masked_fill(~mask, float("-inf"))
+    return sc
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_varlen_prefill_lse_vs_torch_logsumexp(causal):
+    """return_lse: lse[h, cu_q[i] + j] equals torch.logsumexp (float64) of query j's
+    visible scaled scores; a chunk longer than its keys (causal) has rows with no visible
+    key, whose lse is -inf (and whose output row is zero)."""
+    q, key, value, cu_q, cu_k = _varlen_case(seed=41, q_lens=(5, 1, 9, 6), k_lens=(5, 17, 30, 4))
+    scale = 0.3
+    out, lse = oracle.varlen_prefill(q, key, value, cu_q, cu_k, scale, causal=causal,
+                                     return_lse=True)
+    assert lse.shape == (q.shape[1], q.shape[0])
+    np.testing.assert_array_equal(out, oracle.varlen_prefill(q, key, value, cu_q, cu_k, scale,
+                                                             causal=causal))
+    for i in range(len(cu_q) - 1):
+        qs, qe = int(cu_q[i]), int(cu_q[i + 1])
+        ref = torch.logsumexp(_masked_scores64(q, key, cu_q, cu_k, i, scale, causal), dim=-1)
+        np.testing.assert_allclose(lse[:, qs:qe], ref.numpy(), rtol=1e-12, atol=1e-12)
+    if causal:  # sequence 3: 6 queries over 4 keys, its first two see nothing
+        assert np.isneginf(lse[:, int(cu_q[3]):int(cu_q[3]) + 2]).all()
+        assert (out[int(cu_q[3]):int(cu_q[3]) + 2] == 0).all()
+    # Planted mistakes a kernel could make are caught: the log in base 2, or the
+    # unscaled scores.
+    fin = np.isfinite(lse)
+    ln2 = np.where(fin, lse / np.log(2.0), 0.0)
+    assert not np.allclose(ln2[fin], lse[fin], atol=1e-3)
+    bad = oracle.varlen_prefill(q, key, value, cu_q, cu_k, 1.0, causal=causal, return_lse=True)[1]
+    assert not np.allclose(bad[fin], lse[fin], atol=1e-3)
+
+
+def test_varlen_prefill_lse_merge_of_key_halves_is_whole():
+    """Attention over a key set split in two (non-causal, the MLA context-chunk form),
+    each half returning (out, lse), merged by merge_attn_states, equals attention over
+    the whole set, and the merged lse equals the whole lse."""
+    q, key, value, cu_q, cu_k = _varlen_case(seed=42, q_lens=(7, 3), k_lens=(20, 11))
+    scale = 0.25
+    whole, whole_lse = oracle.varlen_prefill(q, key, value, cu_q, cu_k, scale, causal=False,
+                                             return_lse=True)
+    halves = []
+    for part in (0, 1):
+        ks, vs, cuk = [], [], [0]
+        for i in range(len(cu_k) - 1):
+            a, b = int(cu_k[i]), int(cu_k[i + 1])
+            mid = (a + b) // 2
+            lo, hi = (a, mid) if part == 0 else (mid, b)
+            ks.append(key[lo:hi])
+            vs.append(value[lo:hi])
+            cuk.append(cuk[-1] + hi - lo)
+        halves.append(oracle.varlen_prefill(q, np.concatenate(ks), np.concatenate(vs), cu_q,
+                                            np.array(cuk, np.int32), scale, causal=False,
+                                            return_lse=True))
+    (o0, l0), (o1, l1) = halves
+    merged, merged_lse = oracle.merge_attn_states(o0, l0.astype(np.float32), o1,
+                                                  l1.astype(np.float32), "f32")
+    np.testing.assert_allclose(merged, whole, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(merged_lse, whole_lse, rtol=1e-6, atol=1e-6)
+
+
+def test_varlen_prefill_value_head_size_differs_vs_torch_sdpa():
+    """MLA prefill shapes: query / key head 24 and value head 16 (192 / 128 scaled down):
+    against float64 torch SDPA, which takes a value of its own head size."""
+    rng = np.random.default_rng(43)
+    q_lens, k_lens, hq, hk, d, dv = (4, 9), (4, 13), 4, 4, 24, 16
+    cu_q = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
+    cu_k = np.concatenate([[0], np.cumsum(k_lens)]).astype(np.int32)
+    q = rng.standard_normal((int(cu_q[-1]), hq, d)).astype(np.float32)
+    key = rng.standard_normal((int(cu_k[-1]), hk, d)).astype(np.float32)
+    value = rng.standard_normal((int(cu_k[-1]), hk, dv)).astype(np.float32)
+    for causal in (True, False):
+        out = oracle.varlen_prefill(q, key, value, cu_q, cu_k, 0.2, causal=causal)
+        assert out.shape == (q.shape[0], hq, dv)
+        for i in range(2):
+            qs, qe, ks, ke = int(cu_q[i]), int(cu_q[i + 1]), int(cu_k[i]), int(cu_k[i + 1])
+            ql, kl = qe - qs, ke - ks
+            qq = torch.from_numpy(q[qs:qe]).double().transpose(0, 1)
+            k = torch.from_numpy(key[ks:ke]).double().transpose(0, 1)
+            v = torch.from_numpy(value[ks:ke]).double().transpose(0, 1)
+            mask = (torch.arange(kl)[None, :] <= (kl - ql + torch.arange(ql))[:, None]
+                    if causal else None)
+            ref = F.scaled_dot_product_attention(qq, k, v, attn_mask=mask, scale=0.2)
+            np.testing.assert_allclose(out[qs:qe], ref.transpose(0, 1).numpy(), rtol=1e-10,
+                                       atol=1e-12)
+
+
 # ---------------------------------------------------------------------------
 # the reference's torch decode path (the CPU baseline leg), oracle/torch_path.py
 # ---------------------------------------------------------------------------
