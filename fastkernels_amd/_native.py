@@ -90,7 +90,7 @@ _SIGNATURES = {
                                          c_int64, c_void_p]),
     "fk_merge_attn_states": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p,
                                      c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int, c_int,
-                                     c_int64, c_int, c_void_p]),
+                                     c_int64, c_int, c_int, c_void_p, c_void_p]),
 }
 
 EXPORTED = tuple(_SIGNATURES)

@@ -82,6 +82,28 @@ struct F32 {
   __device__ __forceinline__ static float round(float f) { return f; }
 };
 
+// fp32 -> OCP e4m3fn code: round to nearest even, |x| >= 448 saturates to
+// +-448, NaN stays NaN (0x7F with the sign), subnormals below 2^-6.
+__device__ __forceinline__ uint8_t f32_to_e4m3fn_sat(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  const float a = __builtin_fabsf(x);
+  if (a != a) return static_cast<uint8_t>(sign | 0x7Fu);
+  if (a >= 448.f) return static_cast<uint8_t>(sign | 0x7Eu);
+  if (a < 0.015625f) {  // 2^-6: subnormal grid of 2^-9 (exact scaling)
+    const uint32_t m = static_cast<uint32_t>(__builtin_rintf(a * 512.f));  // 0..8; 8 = 2^-6
+    return static_cast<uint8_t>(sign | m);
+  }
+  const int e = static_cast<int>((u >> 23) & 0xFFu) - 127;  // -6 .. 8
+  const uint32_t mant = u & 0x7FFFFFu;
+  uint32_t r = mant >> 20;
+  const uint32_t rem = mant & 0xFFFFFu;
+  r += (rem > 0x80000u || (rem == 0x80000u && (r & 1u))) ? 1u : 0u;
+  uint32_t code = (static_cast<uint32_t>(e + 7) << 3) + r;  // r == 8 carries into the exponent
+  if (code > 0x7Eu) code = 0x7Eu;
+  return static_cast<uint8_t>(sign | code);
+}
+
 // 16-byte vector of storage elements.
 template <typename T>
 struct Vec16 {

@@ -622,19 +622,32 @@ def silu_and_mul(out: torch.Tensor, x: torch.Tensor) -> None:
 def merge_attn_states(output: torch.Tensor, prefix_output: torch.Tensor, prefix_lse: torch.Tensor,
                       suffix_output: torch.Tensor, suffix_lse: torch.Tensor,
                       output_lse: torch.Tensor | None = None,
-                      prefill_tokens_with_context: int | None = None) -> None:
+                      prefill_tokens_with_context: int | None = None,
+                      output_scale: torch.Tensor | None = None) -> None:
     """LSE merge of two partial attention results into ``output`` (and ``output_lse``).
 
     output / prefix_output / suffix_output: [T, H, D] (D contiguous; prefix and suffix
-    share strides); *_lse: float32 [H, T], natural log."""
+    share strides); *_lse: float32 [H, T], natural log.  An ``output`` of
+    float8_e4m3fn takes ``output_scale`` (float32, one element): every output value
+    becomes e4m3fn(clamp(v / output_scale, -448, 448)) (merge_attn_states.cu's
+    USE_FP8_OUTPUT form)."""
     if prefix_output.stride(1) != suffix_output.stride(1) or \
             prefix_output.stride(0) != suffix_output.stride(0):
         raise ValueError("merge_attn_states: prefix_output and suffix_output must share strides")
     if output.dim() != 3 or prefix_output.shape != output.shape or suffix_output.shape != output.shape:
         raise ValueError("merge_attn_states: outputs must be [tokens, heads, head_size]")
-    if output.dtype != prefix_output.dtype or suffix_output.dtype != output.dtype:
-        raise TypeError("merge_attn_states: fp8 output (output_scale) is not supported; "
-                        "output, prefix and suffix must share a dtype")
+    if suffix_output.dtype != prefix_output.dtype:
+        raise TypeError("merge_attn_states: prefix and suffix must share a dtype")
+    fp8_out = output.dtype == _FP8
+    if fp8_out:
+        if output_scale is None:
+            raise ValueError(f"merge_attn_states: output_scale is required when output is "
+                             f"{output.dtype}")
+        if output_scale.dtype != torch.float32 or output_scale.numel() != 1:
+            raise ValueError("merge_attn_states: output_scale must be one float32 value")
+        _same_device(output, output_scale)
+    elif output.dtype != prefix_output.dtype:
+        raise TypeError("merge_attn_states: output must be the inputs' dtype or float8_e4m3fn")
     t, h, d = output.shape
     for x in (output, prefix_output, suffix_output):
         if x.stride(2) != 1:
@@ -646,11 +659,13 @@ def merge_attn_states(output: torch.Tensor, prefix_output: torch.Tensor, prefix_
     _same_device(output, prefix_output, suffix_output, prefix_lse, suffix_lse)
     if t == 0 or h == 0:
         return
+    in_tag = _tag(prefix_output, "merge_attn_states")
     _native.call("fk_merge_attn_states", _ptr(output), output.stride(0), output.stride(1),
                  _ptr(output_lse), _ptr(prefix_output), _ptr(prefix_lse), _ptr(suffix_output),
                  _ptr(suffix_lse), prefix_output.stride(0), prefix_output.stride(1), t, h, d,
                  -1 if prefill_tokens_with_context is None else int(prefill_tokens_with_context),
-                 _tag(output, "merge_attn_states"), _stream(output))
+                 in_tag, _native.FK_DTYPE_FP8_E4M3FN if fp8_out else in_tag,
+                 _ptr(output_scale if fp8_out else None), _stream(output))
 
 
 # ---------------------------------------------------------------------------
@@ -689,7 +704,8 @@ _LIB.define("varlen_prefill(Tensor(a!) out, Tensor q, Tensor key, Tensor value, 
             "int max_seqlen_k=0, Tensor(b!)? lse=None) -> ()")
 _LIB.define("silu_and_mul(Tensor! result, Tensor input) -> ()")
 _LIB.define("merge_attn_states(Tensor(a!) output, Tensor prefix_output, Tensor prefix_lse, "
-            "Tensor suffix_output, Tensor suffix_lse, Tensor(b!)? output_lse) -> ()")
+            "Tensor suffix_output, Tensor suffix_lse, Tensor(b!)? output_lse, "
+            "int? prefill_tokens_with_context=None, Tensor? output_scale=None) -> ()")
 
 _IMPLS = {
     "rmsnorm": lambda result, input, weight, eps: rms_norm(result, input, weight, eps),

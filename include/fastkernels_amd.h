@@ -361,13 +361,20 @@ int fk_store_paged_decode(void* out, int64_t out_row_stride, const void* q, int6
  * (prefix and suffix share theirs); lse tensors: fp32 [heads, tokens] contiguous.
  * Tokens >= prefill_tokens_with_context (a negative value = all tokens) copy the
  * suffix and its lse.  dtype: F32, F16 or BF16 (computed in fp32).
+ * out_dtype: dtype, or FP8_E4M3FN for an fp8 output (output_scale: device fp32
+ * scalar): every output value, merged or copied, becomes
+ * e4m3fn(clamp(v * (1 / *output_scale), -448, 448)) (round to nearest even; the
+ * clamp takes NaN to 448), as merge_attn_states.cu:2436-2571 with USE_FP8_OUTPUT;
+ * out strides are then in bytes.
  * Replaces merge_attn_states / MergeAttnStates.forward
- * (fastkernels/tasks/baseline/L1/merge_attn_states.py:30-122). */
+ * (fastkernels/tasks/baseline/L1/merge_attn_states.py:30-122).
+ * Changed in version 20000: out_dtype and output_scale added. */
 int fk_merge_attn_states(void* out, int64_t out_token_stride, int64_t out_head_stride,
                          float* out_lse, const void* prefix, const float* prefix_lse,
                          const void* suffix, const float* suffix_lse, int64_t in_token_stride,
                          int64_t in_head_stride, int64_t tokens, int heads, int head_size,
-                         int64_t prefill_tokens_with_context, int dtype, void* stream);
+                         int64_t prefill_tokens_with_context, int dtype, int out_dtype,
+                         const float* output_scale, void* stream);
 
 /* SiLU-and-mul: out[r, j] = cast(cast(silu(x[r, j])) * x[r, d + j]) for j < d.
  * x: [rows, 2d] rows `x_row_stride` elements apart; out: [rows, d] rows

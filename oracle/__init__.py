@@ -457,8 +457,14 @@ def merge_partials(parts) -> np.ndarray:
 
 def merge_attn_states(prefix: np.ndarray, prefix_lse: np.ndarray, suffix: np.ndarray,
                       suffix_lse: np.ndarray, dtype: str,
-                      prefill_tokens_with_context: int | None = None):
+                      prefill_tokens_with_context: int | None = None,
+                      output_scale: float | None = None):
     """(out [T, H, D], out_lse [H, T]) of the two-partition LSE merge.
+
+    output_scale (the fp8 output, USE_FP8_OUTPUT, cu:2436-2571): out holds e4m3fn codes
+    (uint8) of every output value v -- the fp32 merge, not rounded to ``dtype``, or the
+    copied prefix / suffix value -- as e4m3fn(fmax(-448, fmin(v * inv, 448))) with
+    inv = 1 / output_scale in fp32 (so a NaN becomes 448, the IEEE fmin/fmax rule).
 
     Tokens t < P (P = prefill_tokens_with_context, default T): infinite lse read as
     -inf (cu:2476-2477); M = max(p, s); if M = -inf the prefix rows and -inf are
@@ -484,9 +490,16 @@ def merge_attn_states(prefix: np.ndarray, prefix_lse: np.ndarray, suffix: np.nda
     e = np.where(empty, 1.0, ep + es)
     merged = prefix[:n].astype(np.float64) * (ep / e)[..., None] + \
         suffix[:n].astype(np.float64) * (es / e)[..., None]
-    merged = round_to(merged.astype(np.float32), dtype)
+    merged = merged.astype(np.float32)
+    if output_scale is None:
+        merged = round_to(merged, dtype)
     out[:n] = np.where(empty[..., None], prefix[:n], merged)
     out_lse[:, :n] = np.where(empty, -np.inf, np.log(e) + mz).T.astype(np.float32)
+    if output_scale is not None:
+        inv = np.float32(1.0) / np.float32(output_scale)
+        x = out.astype(np.float32) * inv
+        x = np.where(np.isnan(x), np.float32(E4M3FN_MAX), np.clip(x, -E4M3FN_MAX, E4M3FN_MAX))
+        return fp8_e4m3fn_encode(x.astype(np.float32)), out_lse
     return out, out_lse
 
 

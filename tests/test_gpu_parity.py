@@ -907,6 +907,64 @@ def test_merge_attn_states_candidate(cuda):
     _check_merge(out, out_lse, po, pl, so, sl, torch.bfloat16)
 
 
+@pytest.mark.parametrize("dtype,t,h,d,prefill", [
+    (torch.bfloat16, 300, 16, 128, None),  # vector path, 16 lanes a head
+    (torch.bfloat16, 64, 8, 512, 40),      # 64 lanes a head; a suffix-only tail
+    (torch.float16, 33, 4, 72, None),      # 9 vectors a head
+    (torch.float32, 50, 4, 128, 20),
+    (torch.bfloat16, 20, 3, 100, None),    # head 100: the scalar path
+])
+def test_merge_attn_states_fp8_output(cuda, dtype, t, h, d, prefill):
+    """fp8 e4m3fn output (output_scale; merge_attn_states.cu's USE_FP8_OUTPUT form): the
+    copied rows (both sides empty, tokens past prefill_tokens_with_context) equal the
+    oracle's codes bit for bit; every merged value is the oracle's code or a neighbour
+    (the fp32 merge rounds once more in fp8), 99% of them exactly; the lse is as with
+    a bf16 output.  Values beyond +-448 saturate."""
+    _flush(f"merge_attn_states fp8 output {dtype} {t}x{h}x{d} prefill={prefill}")
+    po, pl, so, sl = _merge_inputs(t, h, d, dtype, cuda, seed=31 + d)
+    po, so = po * 100, so * 100  # some values past 448 * scale
+    scale = torch.tensor([0.5], dtype=torch.float32, device=cuda)
+    out = torch.empty(t, h, d, dtype=torch.float8_e4m3fn, device=cuda)
+    out_lse = torch.empty_like(pl)
+    ops.merge_attn_states(out, po, pl, so, sl, out_lse, prefill, scale)
+    torch.cuda.synchronize()
+    codes, ref_lse = oracle.merge_attn_states(f32(po), f32(pl), f32(so), f32(sl), _DT[dtype],
+                                              prefill, output_scale=0.5)
+    got = out.view(torch.uint8).cpu().numpy()
+    both = (torch.isinf(pl) & torch.isinf(sl)).cpu().numpy().T  # [t, h]
+    n = t if prefill is None else prefill
+    copied = np.zeros((t, h), bool)
+    copied[:n] = both[:n]
+    copied[n:] = True
+    assert np.array_equal(got[copied], codes[copied]), "copied rows"
+    dg, dr = oracle.fp8_e4m3fn_decode(got[~copied]), oracle.fp8_e4m3fn_decode(codes[~copied])
+    step = np.maximum(np.abs(dr) * 2.0 ** -3, 2.0 ** -9)
+    assert (np.abs(dg - dr) <= step).all(), "merged values more than one e4m3fn step apart"
+    assert (got[~copied] == codes[~copied]).mean() > 0.99
+    assert (np.abs(oracle.fp8_e4m3fn_decode(got)) == 448.0).any()  # saturation exercised
+    fin = np.isfinite(ref_lse)
+    assert np.array_equal(np.isneginf(f32(out_lse)), np.isneginf(ref_lse))
+    assert_close(f32(out_lse)[fin], ref_lse[fin], 1e-5, 1e-5, what="merge lse")
+
+
+def test_merge_attn_states_candidate_fp8_output(cuda):
+    """The candidate function with output_scale (the reference's keyword) into an fp8
+    output; a missing scale is refused."""
+    from fastkernels_amd.candidate.L1.merge_attn_states import merge_attn_states
+    t, h, d = 16, 8, 128
+    po, pl, so, sl = _merge_inputs(t, h, d, torch.bfloat16, cuda, seed=19)
+    out = torch.empty(t, h, d, dtype=torch.float8_e4m3fn, device=cuda)
+    merge_attn_states(out, po, pl, so, sl, output_scale=torch.tensor([0.125], device=cuda))
+    torch.cuda.synchronize()
+    codes, _ = oracle.merge_attn_states(f32(po), f32(pl), f32(so), f32(sl), "bf16",
+                                        output_scale=0.125)
+    dg = oracle.fp8_e4m3fn_decode(out.view(torch.uint8).cpu().numpy())
+    dr = oracle.fp8_e4m3fn_decode(codes)
+    assert (np.abs(dg - dr) <= np.maximum(np.abs(dr) * 2.0 ** -3, 2.0 ** -9)).all()
+    with pytest.raises(ValueError, match="output_scale"):
+        merge_attn_states(out, po, pl, so, sl)
+
+
 # ---------------------------------------------------------------------------
 # store_kvcache with a dtype conversion (bf16/fp16/fp32 key -> fp8 / bf16 cache)
 # ---------------------------------------------------------------------------

@@ -830,6 +830,37 @@ def test_merge_attn_states_special_cases():
     assert np.array_equal(b[mask], oracle.round_to(f[mask], "bf16"))
 
 
+def test_merge_attn_states_fp8_output():
+    """The fp8 output (output_scale): copied rows are torch's own e4m3fn cast of
+    value / scale (exact); merged rows are within one e4m3fn step of the fp32 merge /
+    scale; values beyond +-448 saturate and NaN becomes 448 (fmin/fmax clamp); a
+    planted mistake (multiplying by the scale instead of dividing) is caught."""
+    (po, pl), (so, sl), _ = _halves(seed=13, t=6, h=2)
+    pl, sl = pl.astype(np.float32), sl.astype(np.float32)
+    po = (po * 40).astype(np.float32)
+    so = (so * 40).astype(np.float32)
+    so[5, 0, 0] = np.nan
+    so[5, 0, 1] = 1e6
+    scale = 0.25
+    codes, lse = oracle.merge_attn_states(po, pl, so, sl, "bf16", prefill_tokens_with_context=5,
+                                          output_scale=scale)
+    assert codes.dtype == np.uint8
+    f32, f_lse = oracle.merge_attn_states(po, pl, so, sl, "f32", prefill_tokens_with_context=5)
+    np.testing.assert_array_equal(lse, f_lse)
+    dec = oracle.fp8_e4m3fn_decode(codes)
+    # copied suffix rows (token 5): torch's cast of the clamped value / scale
+    x = torch.from_numpy(so[5] * np.float32(1 / scale)).clamp(-448, 448)
+    want = torch.nan_to_num(x, nan=448.0).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(codes[5], want)
+    assert dec[5, 0, 0] == 448.0 and dec[5, 0, 1] == 448.0
+    # merged rows: within one e4m3fn step (2^-3 relative, 2^-9 absolute below 2^-6)
+    ref = np.clip(f32[:5] / scale, -448, 448)
+    step = np.maximum(np.abs(ref) * 2.0 ** -3, 2.0 ** -9)
+    assert (np.abs(dec[:5] - ref) <= step).all()
+    wrong = oracle.fp8_e4m3fn_decode(oracle.fp8_e4m3fn_encode(np.clip(f32[:5] * scale, -448, 448)))
+    assert not (np.abs(wrong - ref) <= step).all(), "planted mistake (scale multiplied) not caught"
+
+
 # ---------------------------------------------------------------------------
 # SiLU-and-mul
 # ---------------------------------------------------------------------------
