@@ -338,6 +338,7 @@ def bench_decode(args):
     graph_us = _graph_replay_us(lambda: ops.paged_decode(
         out, case.q, case.k_cache, case.v_cache, case.block_tables, case.ctx_lens, case.scale,
         part, nparts, ws), replays=max(20, args.steps))
+    step_calls, step_us = _graph_step_us(case, part, nparts, ws, args.seed)
     result = {
         "metric": METRIC,
         "value": round(total_bytes / (ms_per_step * 1e-3) / 1e9, 2),
@@ -384,6 +385,13 @@ def bench_decode(args):
         "graph_replay": {"us_per_call": round(graph_us, 2),
                          "GBs": round(total_bytes / (graph_us * 1e-6) / 1e9, 1),
                          "frac": round(total_bytes / (graph_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)},
+        # The engine captures a whole decode step -- every layer's attention -- in one
+        # graph (engine.py:5386-5428): Qwen3-8B's 36 layers' decode calls, each on its
+        # own q / out and on one of four cache sets in turn (so no call finds its
+        # predecessor's pages in the MALL), replayed; µs per call = replay / 36.
+        "graph_step": {"calls": step_calls, "us_per_call": round(step_us, 2),
+                       "GBs": round(total_bytes / (step_us * 1e-6) / 1e9, 1),
+                       "frac": round(total_bytes / (step_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)},
     }
     return result, case, out
 
@@ -412,6 +420,61 @@ def _graph_replay_us(call, replays: int) -> float:
     us = (time.perf_counter() - t0) * 1e6 / replays
     del graph
     return us
+
+
+def _graph_step_us(case, part: int, nparts: int, ws, seed: int, layers: int = 36,
+                   cache_sets: int = 4, replays: int = 10) -> tuple[int, float]:
+    """µs per decode call when `layers` calls (a decode step of Qwen3-8B's 36 layers) are
+    captured in one HIP graph and replayed: each call has its own q and out, and the
+    calls cycle over `cache_sets` K/V cache pairs of C3's shape (the first is C3's own;
+    the others hold other seeded values), with C3's block tables and lengths.  One
+    workspace serves the calls, which run one after another on the stream."""
+    import torch
+
+    from fastkernels_amd import ops
+
+    dev = case.q.device
+    caches = [(case.k_cache, case.v_cache)]
+    for i in range(1, cache_sets):
+        g = torch.Generator(device=dev)
+        g.manual_seed(seed + 1000 + i)
+        kc = torch.randn(case.k_cache.shape, generator=g, device=dev,
+                         dtype=torch.float32).to(torch.bfloat16)
+        vc = torch.randn(case.k_cache.shape, generator=g, device=dev,
+                         dtype=torch.float32).to(torch.bfloat16)
+        caches.append((kc, vc))
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed + 2000)
+    qs = [torch.randn(case.q.shape, generator=g, device=dev).to(torch.bfloat16)
+          for _ in range(layers)]
+    outs = [torch.empty_like(case.q) for _ in range(layers)]
+
+    def step():
+        for i in range(layers):
+            kc, vc = caches[i % cache_sets]
+            ops.paged_decode(outs[i], qs[i], kc, vc, case.block_tables, case.ctx_lens,
+                             case.scale, part, nparts, ws)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for _ in range(2):
+        graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(replays):
+        graph.replay()
+    torch.cuda.synchronize()
+    us = (time.perf_counter() - t0) * 1e6 / (replays * layers)
+    del graph, caches, qs, outs
+    torch.cuda.empty_cache()
+    return layers, us
 
 
 def _committed_traffic(kernel: str, part: int, block_size: int = 256):

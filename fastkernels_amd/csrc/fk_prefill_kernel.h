@@ -120,6 +120,7 @@ constexpr int kPrefillWaves = 4;               // waves per work-group
 #ifndef FK_PREFILL_STAGE
 #define FK_PREFILL_STAGE 32
 #endif
+
 // fp8 pages: each stage converted once into bf16 LDS buffers (1), or every
 // wave dequantising the K / V bytes it reads (0).
 #ifndef FK_PREFILL_FP8_CONVERT
