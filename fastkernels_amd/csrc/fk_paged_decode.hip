@@ -120,6 +120,10 @@ struct DecodeParams {
   int64_t new_k_stride;  // bytes between the rows of new_k
   int64_t new_v_stride;
   int slot_is_i64;
+  // Fixed partitions: waves per virtual head (1 or 2).  With 2, each takes half
+  // of the partition's tiles and the second leaves its state in LDS for the
+  // first to merge (launches that would otherwise leave one wave per SIMD).
+  int split;
 };
 
 // The query heads one wave handles: kv head kvh, query heads qbase .. qbase +
@@ -336,14 +340,16 @@ struct WaveState {
   // at the context end writes b's new row before it fetches the last tile.
   // idle: a wave past the last virtual head; it loads nothing and only keeps
   // the work-group's barrier count.
+  // lockstep false: no lock-step barriers (the waves of the work-group stream
+  // ranges of different lengths).
   __device__ __forceinline__ void run(const DecodeParams& P, const int32_t* __restrict__ bt,
                                       const void* __restrict__ sm, int b, const VHead& vh,
                                       int tok_begin, int tok_end, int ctx, int key_lo, int r,
-                                      int g, bool idle) {
+                                      int g, bool idle, bool lockstep = true) {
     constexpr int kSyncChunks = kFp8 ? FK_DECODE_SYNC_CHUNKS_FP8 : FK_DECODE_SYNC_CHUNKS;
     constexpr bool kSync = kSyncChunks > 0 && !kLds;
     if (idle) {
-      if constexpr (kSync) {
+      if (kSync && lockstep) {
         const int n = (tok_end - tok_begin + kTile - 1) / kTile;
 #pragma unroll 1
         for (int t0 = 0, c = 0; t0 < n; t0 += U, ++c)
@@ -573,7 +579,7 @@ struct WaveState {
         // Lock step (no wait for memory: gfx950's barrier does not drain the
         // loads in flight).
         if constexpr (kSync) {
-          if (c % kSyncChunks == 0) __builtin_amdgcn_s_barrier();
+          if (lockstep && c % kSyncChunks == 0) __builtin_amdgcn_s_barrier();
         }
         if constexpr (kStore) {
           if (t_store >= t0 && t_store < t0 + U && new_slot >= 0)
@@ -744,17 +750,28 @@ struct WaveState {
 // Fixed partitions: work-group = (partition p, virtual-head group, sequence b);
 // wave w owns virtual head blockIdx.y * NH + w and streams the partition.
 // Partial rows: (b * max_parts + p) * Hq + hq.
+// With P.split = 2 the work-group has 2 NH waves: wave w + NH takes the second
+// half of the partition's tiles for the same virtual head, leaves (O, max, sum)
+// in LDS (dynamic, split_state_floats per virtual head) and wave w merges it
+// with the log-sum-exp rule before writing.  A launch whose fixed partitions
+// give one wave per SIMD (C5's 16 partitions: 8 sequences x 16 partitions x 8
+// kv heads = 1024 waves) then runs two.
+template <int D>
+constexpr int split_state_floats() { return (D / 16) * 4 * 64 + 2 * 64; }
 template <int NH, int kG, int D, bool kFp8, int U, bool kStore>
-__global__ __launch_bounds__(NH * 64)
+__global__ __launch_bounds__(NH < 8 ? 2 * NH * 64 : NH * 64)
 __attribute__((amdgpu_waves_per_eu(FK_DECODE_WAVES_PER_EU))) void paged_decode_partition_kernel(
     DecodeParams P, const int32_t* __restrict__ block_tables, const int32_t* __restrict__ ctx_lens,
     const void* __restrict__ slot_mapping) {
+  extern __shared__ __align__(16) float split_x[];  // P.split == 2: the second waves' states
   const int p = blockIdx.x;
   const int b = blockIdx.z;
   const int ctx = ctx_lens[b];
   const int tok_begin = p * P.part_tokens;
   // Wave index made provably uniform so that page lookups are scalar loads.
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wave_id = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wave = wave_id & (NH - 1);  // the virtual-head slot
+  const int sub = wave_id / NH;         // which half of the partition (P.split == 2)
   const int v = blockIdx.y * NH + wave;
   // Waves past the last virtual head only keep the work-group's barrier count.
   const bool idle = v >= P.num_kv_heads * P.col_blocks;  // uniform over the wave
@@ -776,8 +793,48 @@ __attribute__((amdgpu_waves_per_eu(FK_DECODE_WAVES_PER_EU))) void paged_decode_p
     WS st;
     __shared__ __align__(16) uint8_t ring[WS::kLds ? NH * 2 * kStageBytes : 16];
     st.ring = ring + wave * 2 * kStageBytes;
-    st.run(P, block_tables, slot_mapping, b, vh, max(tok_begin, lo & ~(kTile - 1)), tok_end, ctx,
-           lo, r, g, idle);
+    const int seg_begin = max(tok_begin, lo & ~(kTile - 1));
+    if (P.split == 1) {
+      st.run(P, block_tables, slot_mapping, b, vh, seg_begin, tok_end, ctx, lo, r, g, idle);
+    } else {
+      // Halves of the partition's tiles (the first takes the odd one); the
+      // waves stream different lengths, so no lock-step barriers.
+      const int n = max(0, (tok_end - seg_begin + kTile - 1) / kTile);
+      const int mid = min(tok_end, seg_begin + ((n + 1) / 2) * kTile);
+      st.run(P, block_tables, slot_mapping, b, vh, sub == 0 ? seg_begin : mid,
+             sub == 0 ? mid : tok_end, ctx, lo, r, g, idle, false);
+      constexpr int kSl = D / 16;
+      float* const x = split_x + wave * split_state_floats<D>();
+      if (sub == 1 && !idle) {
+#pragma unroll
+        for (int d = 0; d < kSl; ++d)
+          *reinterpret_cast<floatx4_t*>(x + (d * 64 + lane) * 4) = st.o[d];
+        x[kSl * 256 + lane] = st.m_run;
+        x[kSl * 256 + 64 + lane] = st.l_run;
+      }
+      __syncthreads();
+      if (sub == 1) return;
+      if (!idle) {
+        // reduce_segments' rule per query column (m, l in column layout; O rows
+        // 4g + i take their column's weights): M = max, w = 2^(m - M), 0 for an
+        // empty half.
+        const float mb = x[kSl * 256 + lane];
+        const float lb = x[kSl * 256 + 64 + lane];
+        const float ma = st.m_run;
+        const float mx = fmaxf(ma, mb);
+        const float wa = ma == kNegInf ? 0.f : __builtin_amdgcn_exp2f(ma - mx);
+        const float wb = mb == kNegInf ? 0.f : __builtin_amdgcn_exp2f(mb - mx);
+        st.m_run = mx;
+        st.l_run = st.l_run * wa + lb * wb;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float fa = row_value<kG>(wa, g, i), fb = row_value<kG>(wb, g, i);
+#pragma unroll
+          for (int d = 0; d < kSl; ++d)
+            st.o[d][i] = st.o[d][i] * fa + x[(d * 64 + lane) * 4 + i] * fb;
+        }
+      }
+    }
     if (idle) return;
     if (nparts == 1) {
       st.write_final(P, b, vh, r, g);
@@ -788,7 +845,7 @@ __attribute__((amdgpu_waves_per_eu(FK_DECODE_WAVES_PER_EU))) void paged_decode_p
   }
   // No partition streams position ctx - 1 (no context): partition 0 writes b's
   // row.
-  if (kStore && p == 0 && ctx <= 0 && vh.first && !idle) {
+  if (kStore && p == 0 && ctx <= 0 && vh.first && !idle && sub == 0) {
     const int64_t os = valid_slot(P, slot_mapping, b);
     if (os >= 0) store_new_row<kFp8, D>(P, b, vh.kvh, os, lane);
   }
@@ -1246,6 +1303,7 @@ struct Launch {
   int nh;
   int head_size;
   dim3 grid;
+  size_t part_lds = 0;  // fixed partitions split over two waves: the merge area
 };
 
 int prepare(const char* name, Launch& L, void* out, int64_t out_row_stride, const void* q,
@@ -1333,6 +1391,14 @@ int prepare(const char* name, Launch& L, void* out, int64_t out_row_stride, cons
       L.nh = p2;
     }
   }
+  // Fixed partitions that would run one wave per SIMD (or fewer) split each
+  // partition over two waves of the work-group.
+  P.split = 1;
+  if (!balanced && L.nh <= 4 &&
+      static_cast<int64_t>(max_parts) * batch * vh < 2LL * 4 * num_cus()) {
+    P.split = 2;
+    L.part_lds = static_cast<size_t>(L.nh) * (head_size / 16 * 4 * 64 + 2 * 64) * sizeof(float);
+  }
   const unsigned hgroups = static_cast<unsigned>((vh + L.nh - 1) / L.nh);
   L.grid = balanced ? dim3(static_cast<unsigned>(max_parts), hgroups, 1)
                     : dim3(static_cast<unsigned>(max_parts), hgroups, static_cast<unsigned>(batch));
@@ -1349,8 +1415,8 @@ void launch_main_st(const Launch& L, hipStream_t stream) {
                        L.slot_mapping);
   } else {
     hipLaunchKernelGGL((paged_decode_partition_kernel<NH, G, D, FP8, U, ST>), L.grid,
-                       dim3(NH * 64), 0, stream, L.P, L.P.block_tables, L.P.ctx_lens,
-                       L.slot_mapping);
+                       dim3(NH * L.P.split * 64), L.part_lds, stream, L.P, L.P.block_tables,
+                       L.P.ctx_lens, L.slot_mapping);
   }
 }
 
