@@ -338,7 +338,7 @@ def bench_decode(args):
     graph_us = _graph_replay_us(lambda: ops.paged_decode(
         out, case.q, case.k_cache, case.v_cache, case.block_tables, case.ctx_lens, case.scale,
         part, nparts, ws), replays=max(20, args.steps))
-    step_calls, step_us = _graph_step_us(case, part, nparts, ws, args.seed)
+    step_calls, step_us, step_eager_us = _graph_step_us(case, part, nparts, ws, args.seed)
     result = {
         "metric": METRIC,
         "value": round(total_bytes / (ms_per_step * 1e-3) / 1e9, 2),
@@ -388,10 +388,15 @@ def bench_decode(args):
         # The engine captures a whole decode step -- every layer's attention -- in one
         # graph (engine.py:5386-5428): Qwen3-8B's 36 layers' decode calls, each on its
         # own q / out and on one of four cache sets in turn (so no call finds its
-        # predecessor's pages in the MALL), replayed; µs per call = replay / 36.
+        # predecessor's pages in the MALL), replayed; µs per call = replay / 36
+        # (median of 10 replays).  `eager_us_per_call`: the same 36 calls launched
+        # eagerly, timed in alternation with the replays.
         "graph_step": {"calls": step_calls, "us_per_call": round(step_us, 2),
                        "GBs": round(total_bytes / (step_us * 1e-6) / 1e9, 1),
-                       "frac": round(total_bytes / (step_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)},
+                       "frac": round(total_bytes / (step_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                       "eager_us_per_call": round(step_eager_us, 2),
+                       "eager_frac": round(total_bytes / (step_eager_us * 1e-6) / 1e9
+                                           / HBM_PEAK_GBS, 4)},
     }
     return result, case, out
 
@@ -423,12 +428,13 @@ def _graph_replay_us(call, replays: int) -> float:
 
 
 def _graph_step_us(case, part: int, nparts: int, ws, seed: int, layers: int = 36,
-                   cache_sets: int = 4, replays: int = 10) -> tuple[int, float]:
+                   cache_sets: int = 4, replays: int = 10) -> tuple[int, float, float]:
     """µs per decode call when `layers` calls (a decode step of Qwen3-8B's 36 layers) are
     captured in one HIP graph and replayed: each call has its own q and out, and the
     calls cycle over `cache_sets` K/V cache pairs of C3's shape (the first is C3's own;
     the others hold other seeded values), with C3's block tables and lengths.  One
-    workspace serves the calls, which run one after another on the stream."""
+    workspace serves the calls, which run one after another on the stream.  Returns
+    (calls, graph µs per call, eager µs per call)."""
     import torch
 
     from fastkernels_amd import ops
@@ -467,14 +473,23 @@ def _graph_step_us(case, part: int, nparts: int, ws, seed: int, layers: int = 36
     for _ in range(2):
         graph.replay()
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
+    # The replays alternate with the same 36 calls launched eagerly, so that the
+    # two figures see the same clocks (a sustained load runs a few percent slower
+    # than the first second after idle; measuring one after the other would put
+    # that difference between them).
+    g_us, e_us = [], []
     for _ in range(replays):
+        t0 = time.perf_counter()
         graph.replay()
-    torch.cuda.synchronize()
-    us = (time.perf_counter() - t0) * 1e6 / (replays * layers)
+        torch.cuda.synchronize()
+        g_us.append((time.perf_counter() - t0) * 1e6 / layers)
+        t0 = time.perf_counter()
+        step()
+        torch.cuda.synchronize()
+        e_us.append((time.perf_counter() - t0) * 1e6 / layers)
     del graph, caches, qs, outs
     torch.cuda.empty_cache()
-    return layers, us
+    return layers, statistics.median(g_us), statistics.median(e_us)
 
 
 def _committed_traffic(kernel: str, part: int, block_size: int = 256):
@@ -915,10 +930,41 @@ def bench_table(args):
                                      case.v_scale), case.algorithmic_bytes(),
             cpu_legs[name] if nseq else None, iters=30,
             parity=lambda name=name, out=out: decode_parity(name, out, oracle_legs[name]))
-    # Prefill (FlashAttnPrefill with a block table) at Qwen3-8B heads, with torch's
-    # own SDPA (flash backend, dense contiguous K/V) on the same GPU beside it.
     del case, out, ws
     torch.cuda.empty_cache()
+    # C3 at 256-, 16- and 64-token pages timed in alternation: six rounds of 10 calls
+    # of each (every call after the flush), so that the page sizes see the same
+    # clocks; the rows above time each once, minutes apart.
+    ilv_cases = {bs_: workloads.c3_decode(dev, block_size=bs_, pool_blocks=4096 * 256 // bs_)
+                 for bs_ in (256, 16, 64)}
+    ilv_fns, ilv_keep, ilv_us = {}, [], {bs_: [] for bs_ in ilv_cases}
+    for bs_, cs in ilv_cases.items():
+        b_, hq_, d_ = cs.q.shape
+        part_, np_, wsb_ = ops.paged_decode_plan(b_, hq_, cs.k_cache.shape[2], d_, cs.max_seq_len, 0)
+        ws_ = torch.zeros(max(1, wsb_), dtype=torch.uint8, device=dev)
+        out_ = torch.empty_like(cs.q)
+        ilv_keep.append((ws_, out_))
+        ilv_fns[bs_] = (lambda cs=cs, out_=out_, ws_=ws_, part_=part_, np_=np_: ops.paged_decode(
+            out_, cs.q, cs.k_cache, cs.v_cache, cs.block_tables, cs.ctx_lens, cs.scale, part_,
+            np_, ws_))
+    for _ in range(6):
+        for bs_, fn_ in ilv_fns.items():
+            ilv_us[bs_].append(time_call(fn_, iters=10, warmup=2, flush=flush)[0] * 1e3)
+    ilv_row = {"config": "C3 page sizes", "op": "paged_decode bfloat16 B=64 Hq=32 at 256-, 16- "
+               "and 64-token pages, timed in alternation (6 rounds x 10 calls each)",
+               "us_median": {}, "frac_of_8TBs": {}, "ratio_to_256": {}}
+    for bs_, us_ in ilv_us.items():
+        med_ = statistics.median(us_)
+        nb_ = ilv_cases[bs_].algorithmic_bytes()
+        ilv_row["us_median"][str(bs_)] = round(med_, 2)
+        ilv_row["frac_of_8TBs"][str(bs_)] = round(nb_ / (med_ * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
+        ilv_row["ratio_to_256"][str(bs_)] = round(med_ / statistics.median(ilv_us[256]), 4)
+    rows.append(ilv_row)
+    print(json.dumps(ilv_row), file=sys.stderr, flush=True)
+    del ilv_cases, ilv_fns, ilv_keep
+    torch.cuda.empty_cache()
+    # Prefill (FlashAttnPrefill with a block table) at Qwen3-8B heads, with torch's
+    # own SDPA (flash backend, dense contiguous K/V) on the same GPU beside it.
     pf_cases = [(label, ql, kl, 32, 8, 128, False) for label, ql, kl in PREFILL_CASES]
     pf_cases += [("1x2048 prompt", [2048], [2048], hq_, hk_, d_, False)
                  for _, hq_, hk_, d_ in shapes[:2]]

@@ -51,18 +51,21 @@ def _hipcc() -> str:
     return found
 
 
-def _compile(src: Path, obj_dir: Path = OBJ_DIR, defines: tuple = ()) -> Path:
+def _compile(src: Path, obj_dir: Path = OBJ_DIR, defines: tuple = (), cflags: tuple = ()) -> Path:
     obj = obj_dir / (src.stem + ".o")
-    cmd = [_hipcc(), *HIP_FLAGS, *(f"-D{d}" for d in defines), "-c", str(src), "-o", str(obj)]
+    cmd = [_hipcc(), *HIP_FLAGS, *cflags, *(f"-D{d}" for d in defines), "-c", str(src), "-o",
+           str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{proc.stderr}")
     return obj
 
 
-def build(verbose: bool = True, defines: tuple = (), out_dir: Path | None = None) -> Path:
+def build(verbose: bool = True, defines: tuple = (), out_dir: Path | None = None,
+          cflags: tuple = ()) -> Path:
     """Compile every csrc/*.hip for gfx950 and link libfk_amd.so; return its path.
-    With out_dir, objects and library go there (a variant build with `defines`)."""
+    With out_dir, objects and library go there (a variant build with `defines`
+    and extra compiler flags `cflags`)."""
     obj_dir = OBJ_DIR if out_dir is None else Path(out_dir) / "_obj"
     lib_path = LIB_PATH if out_dir is None else Path(out_dir) / "libfk_amd.so"
     obj_dir.mkdir(parents=True, exist_ok=True)
@@ -72,7 +75,8 @@ def build(verbose: bool = True, defines: tuple = (), out_dir: Path | None = None
         raise RuntimeError(f"no HIP sources under {CSRC}")
     workers = min(len(sources), os.cpu_count() or 4, 8)
     with cf.ThreadPoolExecutor(max_workers=workers) as ex:
-        objs = list(ex.map(lambda src: _compile(src, obj_dir, tuple(defines)), sources))
+        objs = list(ex.map(lambda src: _compile(src, obj_dir, tuple(defines), tuple(cflags)),
+                           sources))
     tmp = lib_path.with_suffix(".so.tmp")
     cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
@@ -88,8 +92,9 @@ def build(verbose: bool = True, defines: tuple = (), out_dir: Path | None = None
 if __name__ == "__main__":
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--define", action="append", default=[], help="preprocessor macro (repeatable)")
+    ap.add_argument("--cflag", action="append", default=[], help="extra hipcc flag (repeatable)")
     ap.add_argument("--out", type=Path, default=None, help="output directory of a variant build")
     a = ap.parse_args()
-    if a.define and a.out is None:
-        ap.error("--define needs --out (the in-tree library is always the default build)")
-    build(defines=tuple(a.define), out_dir=a.out)
+    if (a.define or a.cflag) and a.out is None:
+        ap.error("--define / --cflag need --out (the in-tree library is always the default build)")
+    build(defines=tuple(a.define), out_dir=a.out, cflags=tuple(a.cflag))
