@@ -121,6 +121,13 @@ constexpr int kPrefillWaves = 4;               // waves per work-group
 #define FK_PREFILL_STAGE 32
 #endif
 
+// bf16 V slices of a pair read right after its score MFMAs, so that their LDS
+// latency passes under the softmax (1), or after the softmax (0).  Applies at
+// value head sizes 128 .. 255 (below, the earlier reads measured slower).
+#ifndef FK_PREFILL_VEARLY
+#define FK_PREFILL_VEARLY 1
+#endif
+
 // fp8 pages: each stage converted once into bf16 LDS buffers (1), or every
 // wave dequantising the K / V bytes it reads (0).
 #ifndef FK_PREFILL_FP8_CONVERT
@@ -500,9 +507,14 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
   //
   // pair_scores runs the scores and the softmax update (P into p_a / p_b) and
   // returns whether the pair's V rows need masking; pair_pv runs P.V.
+  // Same box, A/B in alternating processes, two rounds (µs): 1x2048 60.3 / 59.6 ->
+  // 59.6 / 59.0, 4x512 over 4096 161.9 / 160.2 -> 155.9 / 156.3, 16x512 75.6 / 76.1 ->
+  // 74.2 / 74.5; at head size 64 (Whisper heads, 4x512 over 4096) 124.9 -> 128.1.
+  constexpr bool kVEarly = FK_PREFILL_VEARLY && !kFp8T && kDVP >= 128 && kDVP < 256;
+  short4_t vpre_a[kVS], vpre_b[kVS];  // kVEarly: the pair's V slices, read with its scores
   auto pair_scores = [&](auto masked, int tok0, const uint8_t* buf, int tt, bool ok_a,
-                         bool ok_b, short4_t (&p_a)[kCB],
-                         short4_t (&p_b)[kCB]) __attribute__((always_inline)) {
+                         bool ok_b, short4_t (&p_a)[kCB], short4_t (&p_b)[kCB],
+                         auto early) __attribute__((always_inline)) {
     constexpr bool kMasked = decltype(masked)::value;
     DTile<kFp8T, D> ta, tb;
     // Scores of tile a for every column block, then tile b's K is read: the two
@@ -535,6 +547,14 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
       }
 #pragma unroll
       for (int nb = 0; nb < kCB; ++nb) sc_b[nb] = qk_scores_n(kb, qb[nb]);
+    }
+    if constexpr (kVEarly && decltype(early)::value) {
+      asm volatile("" ::: "memory");  // after tile b's K reads
+#pragma unroll
+      for (int d = 0; d < kVS; ++d) {
+        vpre_a[d] = lds_v_slice<D, DV>(buf, tt, d, r, g);
+        vpre_b[d] = lds_v_slice<D, DV>(buf, tt + 1, d, r, g);
+      }
     }
     __builtin_amdgcn_s_setprio(0);
 #pragma unroll
@@ -623,8 +643,8 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
     return kMasked && (!ok_a || !ok_b || tok0 + 2 * kTile > kend);
   };
   auto pair_pv = [&](int tok0, const uint8_t* buf, int tt, bool ok_a, bool ok_b, bool vmask,
-                     const short4_t (&p_a)[kCB],
-                     const short4_t (&p_b)[kCB]) __attribute__((always_inline)) {
+                     const short4_t (&p_a)[kCB], const short4_t (&p_b)[kCB],
+                     auto early) __attribute__((always_inline)) {
     asm volatile("" ::: "memory");  // V reads stay after the score work
     if constexpr (!kFp8T && kDVP >= 256) {
       // bf16 at head size 256: the V slices go in two halves (read, mask, MFMAs),
@@ -687,8 +707,13 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
       // Slice d holds dims 16d .. 16d + 15 (lane r: dim 16d + r).
 #pragma unroll
       for (int d = 0; d < kVS; ++d) {
-        vba[d] = lds_v_slice<D, DV>(buf, tt, d, r, g);
-        vbb[d] = lds_v_slice<D, DV>(buf, tt + 1, d, r, g);
+        if constexpr (kVEarly && decltype(early)::value) {
+          vba[d] = vpre_a[d];
+          vbb[d] = vpre_b[d];
+        } else {
+          vba[d] = lds_v_slice<D, DV>(buf, tt, d, r, g);
+          vbb[d] = lds_v_slice<D, DV>(buf, tt + 1, d, r, g);
+        }
       }
       // Zero the masked keys' V rows so that P = 0 never meets a NaN.
       if (vmask) {
@@ -866,7 +891,8 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
         (void)key_row<kPaged>(P, bt_row, k_start, (t + 1) * kTile, ok_b, pc);
       }
       if constexpr (decltype(defer)::value) {
-        pend_vm = pair_scores(masked, t * kTile, buf, tt, ok_a, ok_b, pend_pa, pend_pb);
+        pend_vm = pair_scores(masked, t * kTile, buf, tt, ok_a, ok_b, pend_pa, pend_pb,
+                              std::false_type{});
         pend = true;
         pend_tok0 = t * kTile;
         pend_buf = buf;
@@ -874,13 +900,16 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
         pend_ok_b = ok_b;
       } else {
         short4_t p_a[kCB], p_b[kCB];
-        const bool vm = pair_scores(masked, t * kTile, buf, tt, ok_a, ok_b, p_a, p_b);
-        pair_pv(t * kTile, buf, tt, ok_a, ok_b, vm, p_a, p_b);
+        const bool vm =
+            pair_scores(masked, t * kTile, buf, tt, ok_a, ok_b, p_a, p_b, std::true_type{});
+        pair_pv(t * kTile, buf, tt, ok_a, ok_b, vm, p_a, p_b, std::true_type{});
       }
     }
   };
   auto run_pending = [&]() __attribute__((always_inline)) {
-    if (pend) pair_pv(pend_tok0, pend_buf, 0, pend_ok_a, pend_ok_b, pend_vm, pend_pa, pend_pb);
+    if (pend)
+      pair_pv(pend_tok0, pend_buf, 0, pend_ok_a, pend_ok_b, pend_vm, pend_pa, pend_pb,
+              std::false_type{});
     pend = false;
   };
   // A stage needs no mask when this wave sees all its keys in full (below nfull)
