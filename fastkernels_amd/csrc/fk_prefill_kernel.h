@@ -107,6 +107,13 @@ constexpr int prefill_waves_per_simd(int D, bool paged) { return D > 192 && !pag
 #endif
 constexpr int kColBlocks = FK_PREFILL_COLS;    // 16-query column blocks per wave
 constexpr float kLazy = FK_PREFILL_LAZY;       // max-update threshold (log2 units)
+#ifndef FK_PREFILL_FMA_EXP
+#define FK_PREFILL_FMA_EXP 1
+#endif
+// The softmax's exponent argument s2 (K.Q) - m in one FMA per key (the lazy test
+// on its lane max); 0: the scaled score, then the subtraction.
+constexpr bool kFmaExp = FK_PREFILL_FMA_EXP;
+constexpr float kFar = -1.0e30f;  // the max the exponent subtracts before a column's first key
 constexpr int kQTokens = 16 * kColBlocks;      // query tokens per wave at head size 128
 // Column blocks per wave at head sizes (D, DV): at 256 the O accumulators of one
 // block (16 tiles of 4 fp32 per lane) already take what two take at 128; above
@@ -463,6 +470,10 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
   // same bf16 P weights as the numerator), so no VALU adds and no cross-lane
   // fetch at the end.
   float m_run[kCB];
+  // kFmaExp: the max the exponent subtracts, m_run once it is finite and kFar
+  // before (so that the first visible score of a column exceeds it by more than
+  // kLazy and takes the rescale branch, which sets m_run).
+  float m_ref[kCB];
   floatx4_t o[kCB][kVS], l_acc[kCB];
   // kLse: this lane's fp32 share of its query column's sum (keys 4g .. 4g + 3 of
   // every tile), against m_run.
@@ -470,6 +481,7 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
 #pragma unroll
   for (int nb = 0; nb < kCB; ++nb) {
     m_run[nb] = kNegInf;
+    m_ref[nb] = kFar;
     l32[nb] = 0.f;
     l_acc[nb] = floatx4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -566,8 +578,8 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
       // Masked pairs: key tok0 + rel (rel = 16 * tile + 4g + e) is visible when
       // its tile's page is readable and dl <= rel - 4g <= dh: one range test per
       // key instead of the causal, length, chunk and window tests each.
-      // Scores in log2 units, s = s2 * (K.Q), one product each: a product is
-      // canonical, so the max below compiles to plain v_max3 with no
+      // Scores in log2 units, s2 * (K.Q), formed by an FMA or a product: either
+      // result is canonical, so the max below compiles to plain v_max3 with no
       // NaN-quieting step per operand (as the raw MFMA results would need).
       // Masked keys take -inf in the max and P = 0 after the exponent.
       float s[8], sm[8];
@@ -580,21 +592,64 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
         dl = lo - tok0 - 4 * g;
       }
 #pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if constexpr (kMasked) {
+          const int rel = (i >> 2) * kTile + (i & 3);  // compile-time
+          ok[i] = ((i >> 2) ? ok_b : ok_a) && rel <= dh && rel >= dl;
+        } else {
+          ok[i] = true;
+        }
+      }
+      float pr[8];
+      if constexpr (kFmaExp) {
+        // The exponent's argument in one FMA per key, s2 (K.Q) - m_ref, whose
+        // lane max is the lazy test (an FMA result is canonical: plain v_max3).
+        // The scaled score itself is formed only in the rare rescale branch.
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          s[i] = __builtin_fmaf(acc_a[i], s2, -m_ref[nb]);
+          s[4 + i] = __builtin_fmaf(acc_b[i], s2, -m_ref[nb]);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) sm[i] = ok[i] ? s[i] : kNegInf;
+        const float lt = fmaxf(fmaxf(fmaxf(sm[0], sm[1]), fmaxf(sm[2], sm[3])),
+                               fmaxf(fmaxf(sm[4], sm[5]), fmaxf(sm[6], sm[7])));
+        if (__ballot(lt > kLazy) != 0) {
+          // A visible key's argument is finite, a masked one's -inf: the masks
+          // need not stay live through the loop body.
+          auto acc_of = [&](int i) { return i < 4 ? acc_a[i] : acc_b[i - 4]; };
+          float ls = kNegInf;  // this lane's max of the scaled visible scores
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+            ls = fmaxf(ls, (kMasked && sm[i] == kNegInf) ? kNegInf : acc_of(i) * s2);
+          const float mt = pair_max(ls);
+          const float m_new = mt > m_run[nb] + kLazy ? mt : m_run[nb];
+          const float alpha = m_new == m_run[nb] ? 1.f : __builtin_amdgcn_exp2f(m_run[nb] - m_new);
+          m_run[nb] = m_new;
+          m_ref[nb] = m_new == kNegInf ? kFar : m_new;
+          if constexpr (kLse) l32[nb] *= alpha;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float a = row_value<16>(alpha, g, i);
+#pragma unroll
+            for (int d = 0; d < kVS; ++d) o[nb][d][i] *= a;
+            l_acc[nb][i] *= a;
+          }
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+            sm[i] = (kMasked && sm[i] == kNegInf) ? kNegInf
+                                                  : __builtin_fmaf(acc_of(i), s2, -m_ref[nb]);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) pr[i] = __builtin_amdgcn_exp2f(sm[i]);
+      } else {
+#pragma unroll
       for (int i = 0; i < 4; ++i) {
         s[i] = acc_a[i] * s2;
         s[4 + i] = acc_b[i] * s2;
       }
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        if constexpr (kMasked) {
-          const int rel = (i >> 2) * kTile + (i & 3);  // compile-time
-          ok[i] = ((i >> 2) ? ok_b : ok_a) && rel <= dh && rel >= dl;
-          sm[i] = ok[i] ? s[i] : kNegInf;
-        } else {
-          ok[i] = true;
-          sm[i] = s[i];
-        }
-      }
+      for (int i = 0; i < 8; ++i) sm[i] = ok[i] ? s[i] : kNegInf;
       // This lane's max over its 8 keys of the column.
       const float lt = fmaxf(fmaxf(fmaxf(sm[0], sm[1]), fmaxf(sm[2], sm[3])),
                              fmaxf(fmaxf(sm[4], sm[5]), fmaxf(sm[6], sm[7])));
@@ -624,11 +679,11 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
       // A column with no visible key yet (masked stages only) keeps m = -inf;
       // all its P are masked to 0.
       const float m_use = (kMasked && m_run[nb] == kNegInf) ? 0.f : m_run[nb];
-      float pr[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         // Masked scores are -inf in sm, so their P is 2^-inf = 0.
         pr[i] = __builtin_amdgcn_exp2f(sm[i] - m_use);
+      }
       }
       const float (&pa)[4] = *reinterpret_cast<const float(*)[4]>(&pr[0]);
       const float (&pb)[4] = *reinterpret_cast<const float(*)[4]>(&pr[4]);
