@@ -85,6 +85,18 @@ _SIGNATURES = {
                                   c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_int64,
                                   c_int64, c_int, c_int, c_int, c_int, c_float, c_int, c_int,
                                   c_void_p, c_void_p, c_int64, c_void_p]),
+    "fk_prefill_split_plan": (c_int, [c_int, c_int, c_int64, c_int64, c_int64, c_int64, c_int,
+                                      c_int, c_int, c_int, c_int, ctypes.POINTER(c_int64)]),
+    "fk_paged_prefill_ws": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p,
+                                    c_int, c_void_p, c_void_p, c_void_p, c_int64, c_void_p,
+                                    c_void_p, c_int64, c_int64, c_int64, c_int, c_int, c_int,
+                                    c_int, c_int, c_int64, c_float, c_int, c_int, c_void_p,
+                                    c_int64, c_void_p, c_int64, c_void_p]),
+    "fk_varlen_prefill_ws": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64,
+                                     c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_int64,
+                                     c_int64, c_int, c_int, c_int, c_int, c_float, c_int, c_int,
+                                     c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_int64,
+                                     c_void_p]),
     "fk_store_kvcache_convert": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_int, c_void_p,
                                          c_void_p, c_int, c_void_p, c_int, c_int64, c_int64,
                                          c_int64, c_void_p]),
@@ -141,6 +153,19 @@ def check(fn: str, code: int) -> None:
 def call(fn: str, *args) -> None:
     """Call entry point ``fn`` and raise FkError on a non-zero status."""
     check(fn, getattr(lib(), fn)(*args))
+
+
+def prefill_split_bytes(paged: bool, kv_dtype: int, batch: int, total_q: int, max_seqlen_q: int,
+                        max_seqlen_k: int, num_heads: int, num_kv_heads: int, head_size: int,
+                        head_size_v: int, causal: bool) -> int:
+    """fk_prefill_split_plan: the workspace bytes of the prefill's work-group key split
+    (0: the launch does not split)."""
+    ws = c_int64(0)
+    check("fk_prefill_split_plan",
+          lib().fk_prefill_split_plan(int(paged), kv_dtype, batch, total_q, max_seqlen_q,
+                                      max_seqlen_k, num_heads, num_kv_heads, head_size,
+                                      head_size_v, int(bool(causal)), ctypes.byref(ws)))
+    return ws.value
 
 
 def plan(batch: int, num_heads: int, num_kv_heads: int, head_size: int, max_seq_len: int,

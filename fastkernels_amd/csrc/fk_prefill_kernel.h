@@ -84,7 +84,20 @@ struct PrefillParams {
   const float* sinks;  // attention sink logits [num_heads] fp32, or nullptr
   float* lse;          // log-sum-exp [num_heads, lse_row_stride] fp32, or nullptr
   int64_t lse_row_stride;
+  // Work-group key split: each query block's key stages are divided over xs
+  // work-groups (1: none), which leave their partial states in `part` for
+  // prefill_merge_kernel: O [xs][part_rows][num_heads][DV] fp32, then per row
+  // [xs][part_rows][num_heads][4] fp32 (running max in log2 units, the sum the
+  // output divides by, the fp32 sum of the log-sum-exp output, unused).
+  int xs;
+  float* part;
+  int64_t part_rows;  // rows of q (at least cu_seqlens_q[batch])
+  int num_heads;
 };
+
+// Floats of the partial state per (part, row, head) besides O.
+constexpr int kPartMl = 4;
+constexpr int kMaxKeyParts = 8;  // work-group key split: parts per query block at most
 
 // Launches the kernel for the head sizes fk_prefill_heads.hip instantiates
 // (besides D = DV in {64, 128, 256}); false when (D, DV) is not among them.
@@ -362,9 +375,10 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
   constexpr int kStageAll = kKS * kHalfBytes;
   constexpr int kXBytes = kKS > 1 ? kPrefillWaves * kXFloats * 4 : 0;
   __shared__ __align__(16) uint8_t lds_all[kStageAll > kXBytes ? kStageAll : kXBytes];
-  // Grid: x = kv head (x hsplit), y = sequence, z = query block.  The block
-  // index varies slowest, so the work-groups that have work (low z when blocks
-  // are paired) are dispatched first and spread over every CU.
+  // Grid: x = kv head (x hsplit), y = sequence, z = query block (x P.xs key
+  // parts, the part fastest).  The block index varies slowest, so the
+  // work-groups that have work (low z when blocks are paired) are dispatched
+  // first and spread over every CU.
   const int b = blockIdx.y;
   const int hw = P.gqa < kPrefillWaves ? P.gqa : kPrefillWaves;  // heads per work-group
   const int qs = kPrefillWaves / hw;                             // query blocks per work-group
@@ -386,7 +400,9 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
   const int wg_tokens = qs * kQT;
   const int nqb = (q_len + wg_tokens - 1) / wg_tokens;
   const bool paired = P.causal && k_len - q_len < q_len;
-  const int x = static_cast<int>(blockIdx.z);
+  const int xs = P.xs;
+  const int x = static_cast<int>(blockIdx.z) / xs;
+  const int xpart = static_cast<int>(blockIdx.z) - x * xs;  // this work-group's key part
   if (x >= (paired ? (nqb + 1) / 2 : nqb)) return;  // uniform over the work-group
   const int wave_id = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int half = kKS > 1 ? wave_id / kPrefillWaves : 0;  // key-split half
@@ -498,13 +514,16 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
   block_stages(qblk, st0, nstages);
   const int tbeg = kbeg / kTile;                      // this wave's first tile
   // This half's stages [st_lo, st_hi) and the barriers every wave passes
-  // (nsteps): the whole range, or with the key split its first or second half.
+  // (nsteps): the whole range, or with the key split (within the work-group,
+  // over work-groups, or both) its part of them: part xpart * kKS + half of
+  // xs * kKS equal parts (a part past the end is empty).
   int st_lo = st0, st_hi = nstages, nsteps = nstages - st0;
-  if constexpr (kKS > 1) {
-    const int n0 = (nstages - st0 + 1) / 2;
-    st_lo = half == 0 ? st0 : st0 + n0;
-    st_hi = half == 0 ? st0 + n0 : nstages;
-    nsteps = n0;
+  if (kKS * xs > 1) {
+    const int n0 = (nstages - st0 + kKS * xs - 1) / (kKS * xs);
+    const int part = xpart * kKS + half;
+    st_lo = min(st0 + part * n0, nstages);
+    st_hi = min(st0 + (part + 1) * n0, nstages);
+    nsteps = kKS > 1 ? n0 : st_hi - st_lo;
   }
 
   // Two 16-key tiles (tiles tt, tt + 1 of `buf`, keys tok0 .. tok0 + 31):
@@ -1137,6 +1156,42 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
     }
   }
   if (!active) return;  // from process_block: this wave has no queries here
+
+  // Work-group key split: this part's state (O before the division, the row's
+  // max and sum) for prefill_merge_kernel, which applies the sink and writes the
+  // rows and the log-sum-exp.  Every part writes every row of its block, also
+  // one that saw no key (max -inf, sum 0).
+  if (xs > 1) {
+    const int64_t prow0 = static_cast<int64_t>(xpart) * P.part_rows + q_start;
+#pragma unroll
+    for (int nb = 0; nb < kCB; ++nb) {
+      if constexpr (kLse) {  // column layout: lanes of row group 0 hold column r's sum
+        const int jc = j0 + 16 * nb + r;
+        if (g == 0 && jc < q_len)
+          P.part[static_cast<int64_t>(xs) * P.part_rows * P.num_heads * DV +
+                 ((prow0 + jc) * P.num_heads + hq) * kPartMl + 2] = l32[nb];
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int jr = j0 + 16 * nb + 4 * g + i;
+        if (jr >= q_len) continue;
+        const int64_t rh = (prow0 + jr) * P.num_heads + hq;
+        float* const po = P.part + rh * DV;
+#pragma unroll
+        for (int d = 0; d < kVS; ++d) {
+          const int dim = kFp8T ? (D / 16) * r + d : 16 * d + r;
+          if (kFp8T ? dim < DV : (16 * d + 16 <= DV || dim < DV)) po[dim] = o[nb][d][i];
+        }
+        if (r == 0) {
+          float* const pm =
+              P.part + static_cast<int64_t>(xs) * P.part_rows * P.num_heads * DV + rh * kPartMl;
+          pm[0] = m_row[nb][i];
+          pm[1] = l_row[nb][i];
+        }
+      }
+    }
+    return;
+  }
 
   // kLse: lse = ln(sum e^(scale q.k)) = (m + log2 l) ln 2 per query column, the
   // sink included; -inf for a row with no visible key.  Lanes of row group 0

@@ -49,6 +49,7 @@ int num_cus() {
 
 // 2.0.0: fk_paged_prefill / fk_varlen_prefill gained head_size_v, lse and
 // lse_row_stride (1.x had max_seqlen_k added in the middle of both signatures).
-extern "C" int fk_version(void) { return FK_VERSION_MAJOR * 10000; }
+// 2.1.0: fk_prefill_split_plan, fk_paged_prefill_ws and fk_varlen_prefill_ws added.
+extern "C" int fk_version(void) { return FK_VERSION_MAJOR * 10000 + FK_VERSION_MINOR * 100; }
 
 extern "C" const char* fk_last_error(void) { return fk::g_last_error; }

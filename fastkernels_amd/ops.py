@@ -482,6 +482,22 @@ def _check_lse(lse, q, what):
     _same_device(q, lse)
 
 
+# Work-group key split of the prefill: False launches without it (the library's
+# plain launch, for A/B timing and the tests that compare the two).
+PREFILL_SPLIT = True
+
+
+def _split_workspace(q, paged, kv_dtype, batch, max_seqlen_q, max_seqlen_k, hk, dv, causal):
+    """The workspace of the prefill's work-group key split (fk_prefill_split_plan), from
+    torch's allocator on q's stream, or None when the launch does not split."""
+    if not PREFILL_SPLIT:
+        return None
+    nbytes = _native.prefill_split_bytes(paged, kv_dtype, batch, q.shape[0], int(max_seqlen_q),
+                                         int(max_seqlen_k), q.shape[1], hk, q.shape[2], dv,
+                                         causal)
+    return torch.empty(nbytes, dtype=torch.uint8, device=q.device) if nbytes > 0 else None
+
+
 def paged_prefill(out: torch.Tensor, q: torch.Tensor, k_cache: torch.Tensor,
                   v_cache: torch.Tensor, block_table: torch.Tensor, cu_seqlens_q: torch.Tensor,
                   cu_seqlens_k: torch.Tensor, max_seqlen_q: int, softmax_scale: float,
@@ -523,14 +539,15 @@ def paged_prefill(out: torch.Tensor, q: torch.Tensor, k_cache: torch.Tensor,
     if batch <= 0 or q.shape[0] == 0:
         return
     nb, bs = k_cache.shape[:2]
-    _native.call("fk_paged_prefill", _ptr(out), out.stride(0), _ptr(q), q.stride(0),
-                 _ptr(k_cache), _ptr(v_cache),
-                 _native.FK_DTYPE_FP8_E4M3FN if k_cache.dtype == _FP8 else _native.FK_DTYPE_BF16,
+    kv_dtype = _native.FK_DTYPE_FP8_E4M3FN if k_cache.dtype == _FP8 else _native.FK_DTYPE_BF16
+    ws = _split_workspace(q, True, kv_dtype, batch, max_seqlen_q, max_seqlen_k, hk, dv, causal)
+    _native.call("fk_paged_prefill_ws", _ptr(out), out.stride(0), _ptr(q), q.stride(0),
+                 _ptr(k_cache), _ptr(v_cache), kv_dtype,
                  _ptr(k_scale), _ptr(v_scale), _ptr(block_table), block_table.stride(0),
                  _ptr(cu_seqlens_q), _ptr(cu_seqlens_k), batch, int(max_seqlen_q),
                  int(max_seqlen_k), q.shape[1], hk, q.shape[2], dv, bs, nb,
                  float(softmax_scale), int(bool(causal)), int(window_left), _ptr(sinks),
-                 _stream(q))
+                 q.shape[0], _ptr(ws), 0 if ws is None else ws.numel(), _stream(q))
 
 
 def varlen_prefill(out: torch.Tensor, q: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
@@ -563,12 +580,14 @@ def varlen_prefill(out: torch.Tensor, q: torch.Tensor, key: torch.Tensor, value:
     batch = cu_seqlens_q.numel() - 1
     if batch <= 0 or q.shape[0] == 0:
         return
-    _native.call("fk_varlen_prefill", _ptr(out), out.stride(0), _ptr(q), q.stride(0), _ptr(key),
-                 key.stride(0), _ptr(value), value.stride(0), _ptr(cu_seqlens_q),
+    ws = _split_workspace(q, False, _native.FK_DTYPE_BF16, batch, max_seqlen_q, max_seqlen_k,
+                          key.shape[1], dv, causal)
+    _native.call("fk_varlen_prefill_ws", _ptr(out), out.stride(0), _ptr(q), q.stride(0),
+                 _ptr(key), key.stride(0), _ptr(value), value.stride(0), _ptr(cu_seqlens_q),
                  _ptr(cu_seqlens_k), batch, int(max_seqlen_q), int(max_seqlen_k), q.shape[1],
                  key.shape[1], q.shape[2], dv, float(softmax_scale), int(bool(causal)),
                  int(window_left), _ptr(sinks), _ptr(lse), 0 if lse is None else lse.stride(0),
-                 _stream(q))
+                 q.shape[0], _ptr(ws), 0 if ws is None else ws.numel(), _stream(q))
 
 
 def paged_decode_phases(out, q, k_cache, v_cache, block_table, cache_seqlens, softmax_scale,

@@ -77,6 +77,7 @@ extern "C" {
  * whenever an existing entry point's signature changes; a caller built against this
  * header checks fk_version() / 10000 == FK_VERSION_MAJOR before binding. */
 #define FK_VERSION_MAJOR 2
+#define FK_VERSION_MINOR 1 /* 2.1: fk_prefill_split_plan, fk_paged_prefill_ws, fk_varlen_prefill_ws */
 int fk_version(void);
 
 /* Message describing the last failing call on this thread ("" if none). */
@@ -304,6 +305,49 @@ int fk_varlen_prefill(void* out, int64_t out_row_stride, const void* q, int64_t 
                       int64_t max_seqlen_k, int num_heads, int num_kv_heads, int head_size,
                       int head_size_v, float scale, int causal, int window_left,
                       const float* sinks, float* lse, int64_t lse_row_stride, void* stream);
+
+/* Work-group key split of the prefill launches (no counterpart in the reference's
+ * interface: FlashAttnPrefill / FlashAttnVarlen call flash-attn, whose own split-KV
+ * path plays this part).  When a launch would leave CUs without a work-group (one
+ * prompt over a few kv heads, or a short chunk over a long cache), each query block's
+ * keys are divided over up to 8 work-groups, which leave their partial (O, max, sum)
+ * in a caller-owned workspace, and a second kernel merges them with the log-sum-exp
+ * rule and writes the rows (and the log-sum-exp).
+ * fk_prefill_split_plan: *workspace_bytes = the workspace fk_paged_prefill_ws /
+ * fk_varlen_prefill_ws need for these sizes (paged: 1 for the paged entry point,
+ * kv_dtype its cache dtype; total_q = rows of q and out, >= cu_seqlens_q[batch]);
+ * 0 when the launch does not split (any workspace, or NULL, then gives the plain
+ * launch).  The decision uses these host-side bounds only. */
+int fk_prefill_split_plan(int paged, int kv_dtype, int64_t batch, int64_t total_q,
+                          int64_t max_seqlen_q, int64_t max_seqlen_k, int num_heads,
+                          int num_kv_heads, int head_size, int head_size_v, int causal,
+                          int64_t* workspace_bytes);
+
+/* fk_paged_prefill / fk_varlen_prefill with the work-group key split's workspace:
+ * workspace NULL runs exactly the entry point without _ws; otherwise
+ * workspace_bytes must be at least fk_prefill_split_plan's figure for the same
+ * arguments (else FK_ERR_WORKSPACE) and the workspace 16-byte aligned.  Its contents
+ * need no initialisation and are scratch after the call; calls that share a
+ * workspace must be ordered (the same stream).  Results match the entry point
+ * without _ws to rounding (the parts' O is merged in fp32). */
+int fk_paged_prefill_ws(void* out, int64_t out_row_stride, const void* q, int64_t q_row_stride,
+                        const void* k_cache, const void* v_cache, int kv_dtype,
+                        const float* k_scale, const float* v_scale, const int32_t* block_tables,
+                        int64_t bt_row_stride, const int32_t* cu_seqlens_q,
+                        const int32_t* cu_seqlens_k, int64_t batch, int64_t max_seqlen_q,
+                        int64_t max_seqlen_k, int num_heads, int num_kv_heads, int head_size,
+                        int head_size_v, int block_size, int64_t num_blocks, float scale,
+                        int causal, int window_left, const float* sinks, int64_t total_q,
+                        void* workspace, int64_t workspace_bytes, void* stream);
+int fk_varlen_prefill_ws(void* out, int64_t out_row_stride, const void* q, int64_t q_row_stride,
+                         const void* key, int64_t key_row_stride, const void* value,
+                         int64_t value_row_stride, const int32_t* cu_seqlens_q,
+                         const int32_t* cu_seqlens_k, int64_t batch, int64_t max_seqlen_q,
+                         int64_t max_seqlen_k, int num_heads, int num_kv_heads, int head_size,
+                         int head_size_v, float scale, int causal, int window_left,
+                         const float* sinks, float* lse, int64_t lse_row_stride,
+                         int64_t total_q, void* workspace, int64_t workspace_bytes,
+                         void* stream);
 
 /* Per-head q/k RMSNorm (optional) + rotary embedding + store_kvcache in one launch:
  * the attention block between the qkv projection and the decode
