@@ -972,7 +972,12 @@ def bench_table(args):
                  for _, hq_, hk_, d_ in shapes[:2]]
     # fp8 e4m3fn pages (per-kv-head scales), dequantised exactly in the kernel.
     pf_cases += [(label, ql, kl, 32, 8, 128, True) for label, ql, kl in PREFILL_CASES[:2]]
-    for label, ql, kl, hq_, hk_, d_, fp8 in pf_cases:
+    pf_cases = [c_ + (True,) for c_ in pf_cases]
+    # One chunk over a long cache (128 work-groups): the work-group key split spreads
+    # each block's keys over several work-groups; the launch without it beside it.
+    pf_cases += [("1x512 chunk over 8192", [512], [8192], 32, 8, 128, False, sp_)
+                 for sp_ in (True, False)]
+    for label, ql, kl, hq_, hk_, d_, fp8, split_ in pf_cases:
         q, kc, vc, bt, cu_q, cu_k, mq, flop = prefill_case(dev, ql, kl, workloads.SEED + 11,
                                                            hq_, hk_, d_)
         ks = vs = None
@@ -983,12 +988,18 @@ def bench_table(args):
             kc = workloads.quantize_fp8(kc.float(), ks)
             vc = workloads.quantize_fp8(vc.float(), vs)
         pout = torch.empty_like(q)
-        med, _ = time_call(lambda: ops.paged_prefill(pout, q, kc, vc, bt, cu_q, cu_k, mq,
-                                                     d_ ** -0.5, ks, vs, max_seqlen_k=max(kl)),
-                           iters=20, warmup=3, flush=flush)
+        ops.PREFILL_SPLIT = split_
+        try:
+            med, _ = time_call(lambda: ops.paged_prefill(pout, q, kc, vc, bt, cu_q, cu_k, mq,
+                                                         d_ ** -0.5, ks, vs,
+                                                         max_seqlen_k=max(kl)),
+                               iters=20, warmup=3, flush=flush)
+        finally:
+            ops.PREFILL_SPLIT = True
         heads = f"Hq={hq_} Hk={hk_}" + (f" D={d_}" if d_ != 128 else "")
         row = {"config": "prefill",
-               "op": f"paged_prefill {'fp8' if fp8 else 'bf16'} {heads} {label}",
+               "op": f"paged_prefill {'fp8' if fp8 else 'bf16'} {heads} {label}" +
+                     ("" if split_ else " (without the work-group key split)"),
                "us_median": round(med * 1e3, 2), "flop": flop,
                "TFLOPs": round(flop / (med * 1e-3) / 1e12, 1),
                "frac_of_2.5PFLOPs": round(flop / (med * 1e-3) / 2.5e15, 4)}
