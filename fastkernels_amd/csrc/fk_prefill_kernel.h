@@ -514,16 +514,32 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
   block_stages(qblk, st0, nstages);
   const int tbeg = kbeg / kTile;                      // this wave's first tile
   // This half's stages [st_lo, st_hi) and the barriers every wave passes
-  // (nsteps): the whole range, or with the key split (within the work-group,
-  // over work-groups, or both) its part of them: part xpart * kKS + half of
-  // xs * kKS equal parts (a part past the end is empty).
+  // (nsteps): the whole range, or with the key split its part of it.  Over
+  // work-groups, part xpart of xs equal parts (a part past the end is empty);
+  // within the work-group, the first or second half of that.  With the
+  // deferred P.V of the ping-pong the second half ends about one stage after
+  // the first (head size 128, per-wave clock stamps: 1.1 us), so the first half
+  // takes the extra stage of an even count and the second half's tail runs
+  // under the first's last stage.
   int st_lo = st0, st_hi = nstages, nsteps = nstages - st0;
   if (kKS * xs > 1) {
-    const int n0 = (nstages - st0 + kKS * xs - 1) / (kKS * xs);
-    const int part = xpart * kKS + half;
-    st_lo = min(st0 + part * n0, nstages);
-    st_hi = min(st0 + (part + 1) * n0, nstages);
-    nsteps = kKS > 1 ? n0 : st_hi - st_lo;
+    int wlo = st0, whi = nstages;  // this work-group's part
+    if (xs > 1) {
+      const int n1 = (nstages - st0 + xs - 1) / xs;
+      wlo = min(st0 + xpart * n1, nstages);
+      whi = min(wlo + n1, nstages);
+    }
+    st_lo = wlo;
+    st_hi = whi;
+    nsteps = whi - wlo;
+    if constexpr (kKS > 1) {
+      const int m = whi - wlo;
+      // the first half's stages (at head size 64 the second half measured no lag)
+      const int h0 = (kPingPong && kDQ > 64) ? min(m, (m + 2) / 2) : (m + 1) / 2;
+      st_lo = half == 0 ? wlo : wlo + h0;
+      st_hi = half == 0 ? wlo + h0 : whi;
+      nsteps = h0;
+    }
   }
 
   // Two 16-key tiles (tiles tt, tt + 1 of `buf`, keys tok0 .. tok0 + 31):
