@@ -245,6 +245,14 @@ __device__ __forceinline__ void lds_dma16(const uint8_t* src, uint32_t lds_addr)
       : "memory");
 }
 
+// Value of `x` held by lane 4g + i (g = this lane's row group, lanes 16g ..
+// 16g + 15), for the O row 4g + i this lane accumulates: one cross-lane read
+// (ds_bpermute) rather than four readlanes and a select chain, which the
+// compiler turns into branches.
+__device__ __forceinline__ float row_from(float x, int g, int i) {
+  return __int_as_float(__builtin_amdgcn_ds_bpermute((4 * g + i) * 4, __float_as_int(x)));
+}
+
 // LDS byte address of a pointer into a __shared__ array.
 __device__ __forceinline__ uint32_t lds_addr_of(const uint8_t* p) {
   return static_cast<uint32_t>(
@@ -665,7 +673,7 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
           if constexpr (kLse) l32[nb] *= alpha;
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const float a = row_value<16>(alpha, g, i);
+            const float a = row_from(alpha, g, i);
 #pragma unroll
             for (int d = 0; d < kVS; ++d) o[nb][d][i] *= a;
             l_acc[nb][i] *= a;
@@ -705,7 +713,7 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
         if constexpr (kLse) l32[nb] *= alpha;  // column layout, like alpha
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float a = row_value<16>(alpha, g, i);
+          const float a = row_from(alpha, g, i);
 #pragma unroll
           for (int d = 0; d < kVS; ++d) o[nb][d][i] *= a;
           l_acc[nb][i] *= a;
@@ -1105,7 +1113,7 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
   for (int nb = 0; nb < kCB; ++nb)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      m_row[nb][i] = row_value<16>(m_run[nb], g, i);
+      m_row[nb][i] = row_from(m_run[nb], g, i);
       l_row[nb][i] = l_acc[nb][i];
     }
   if constexpr (kKS > 1) {
@@ -1154,7 +1162,7 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const float ma = m_row[nb][i];
-          const float mb = row_value<16>(mb_col, g, i);
+          const float mb = row_from(mb_col, g, i);
           const float mx = fmaxf(ma, mb);
           wa[i] = ma == kNegInf ? 0.f : __builtin_amdgcn_exp2f(ma - mx);
           wb[i] = mb == kNegInf ? 0.f : __builtin_amdgcn_exp2f(mb - mx);
