@@ -221,6 +221,12 @@ int prefill_entry(const char* name, bool paged, void* out, int64_t out_row_strid
   FK_REQUIRE(k_row_bytes >= num_kv_heads * head_size * elem &&
                  v_row_bytes >= num_kv_heads * head_size_v * elem,
              "%s: key/value rows shorter than num_kv_heads * head size", name);
+  // The kernel addresses a page's rows (a dense tile's 16 rows) by 32-bit offsets
+  // from the page's (tile's) first row.
+  FK_REQUIRE((paged ? static_cast<int64_t>(block_size) : int64_t(kTile)) *
+                     (k_row_bytes > v_row_bytes ? k_row_bytes : v_row_bytes) <=
+                 (int64_t(1) << 32) - 1,
+             "%s: a page of key/value rows must span fewer than 2^32 bytes", name);
   FK_REQUIRE(!lse || lse_row_stride >= 0, "%s: lse row stride must be >= 0", name);
   FK_REQUIRE(!lse || !paged, "%s: the log-sum-exp output is built for dense keys only", name);
   if (batch == 0 || max_seqlen_q == 0) return FK_OK;

@@ -56,6 +56,7 @@
 // waves.
 #pragma once
 
+#include <climits>
 #include <type_traits>
 
 #include "fk_attn_tile.h"
@@ -168,33 +169,44 @@ __device__ __forceinline__ int64_t prefill_page(const PrefillParams& P,
   return (page >= 0 && page < P.num_blocks) ? page : -1;
 }
 
-// The last block-table entry a wave looked up (wave-uniform): a page spans
+// The last block-table entry a wave looked up (wave-uniform), with the K and V
+// rows of its page's first slot (the kv head's row of the caches): a page spans
 // block_size / 32 stages, so most lookups reuse it instead of waiting for a
-// scalar load.
+// scalar load, and a tile's source address is that row plus a 32-bit offset.
 struct PageCache {
   int idx = -1;
-  int64_t page = -1;
+  int64_t page = -1;             // the block-table entry (-1: masked; page 0 is read)
+  const uint8_t* kb = nullptr;   // K row of the page's slot 0, kv head h
+  const uint8_t* vb = nullptr;   // V row of the page's slot 0, kv head h
 };
 
-// Row index of key `tok` of the sequence and whether it is readable: paged, the
-// slot through the block table (-1 pages masked; page 0 is read instead);
-// dense, row k_start + tok of the key/value tensors.
+// Paged keys: the page of key `tok` into pc (a scalar load only when the page
+// changes).
+__device__ __forceinline__ void page_lookup(const PrefillParams& P,
+                                            const int32_t* __restrict__ bt_row, int tok,
+                                            const uint8_t* kh, const uint8_t* vh, PageCache& pc) {
+  const int idx = tok >> P.block_size_log2;
+  if (idx != pc.idx) {
+    const int64_t page = prefill_page(P, bt_row, tok);
+    const int64_t slot0 = (page < 0 ? 0 : page) << P.block_size_log2;
+    pc.idx = idx;
+    pc.page = page;
+    pc.kb = kh + slot0 * P.k_row_bytes;
+    pc.vb = vh + slot0 * P.v_row_bytes;
+  }
+}
+
+// Whether key `tok` of the sequence is readable: paged, its page's block-table
+// entry is not -1; dense keys always are.
 template <bool kPaged>
-__device__ __forceinline__ int64_t key_row(const PrefillParams& P,
-                                           const int32_t* __restrict__ bt_row, int k_start,
-                                           int tok, bool& ok, PageCache& pc) {
+__device__ __forceinline__ bool key_ok(const PrefillParams& P, const int32_t* __restrict__ bt_row,
+                                       int tok, const uint8_t* kh, const uint8_t* vh,
+                                       PageCache& pc) {
   if constexpr (kPaged) {
-    const int idx = tok >> P.block_size_log2;
-    if (idx != pc.idx) {
-      pc.page = prefill_page(P, bt_row, tok);
-      pc.idx = idx;
-    }
-    const int64_t page = pc.page;
-    ok = page >= 0;
-    return ((page < 0 ? 0 : page) << P.block_size_log2) + (tok & ((1 << P.block_size_log2) - 1));
+    page_lookup(P, bt_row, tok, kh, vh, pc);
+    return pc.page >= 0;
   } else {
-    ok = true;
-    return static_cast<int64_t>(k_start) + tok;
+    return true;
   }
 }
 
@@ -242,6 +254,18 @@ __device__ __forceinline__ void lds_dma16(const uint8_t* src, uint32_t lds_addr)
       "global_load_lds_dwordx4 %0, off"
       :
       : "v"(src), "{m0}"(lds_addr)
+      : "memory");
+}
+// The same load with a wave-uniform 64-bit base in SGPRs and a per-lane 32-bit
+// byte offset (the load's saddr form): lane l reads base + off.  A tile's base
+// changes from stage to stage and the lanes' offsets do not, so a stage's
+// loads take no 64-bit address arithmetic per lane.
+__device__ __forceinline__ void lds_dma16_s(const uint8_t* base, uint32_t off, uint32_t lds_addr) {
+  asm volatile(
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, %1"
+      :
+      : "v"(off), "s"(base), "{m0}"(lds_addr)
       : "memory");
 }
 
@@ -422,6 +446,12 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
   };
   // The buffer the compute path reads stage st from: the staged one, or with
   // kConv its bf16 conversion.
+  // The LDS byte address of stage st's buffer, as an integer (M0 of the
+  // direct-to-LDS loads; no generic-pointer conversion per stage).
+  const uint32_t lds_half_addr = __builtin_amdgcn_readfirstlane(lds_addr_of(lds_half));
+  auto stage_addr = [&](int st) -> uint32_t {
+    return lds_half_addr + (kBufs == 2 ? (st & 1) : st % kBufs) * S::kBytes;
+  };
   auto comp_buf = [&](int st) {
     if constexpr (kConv) return lds_half + kBufs * S::kBytes + (st & 1) * SB::kBytes;
     else if constexpr (kConv1) return lds_half + kBufs * S::kBytes;
@@ -886,6 +916,9 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
   constexpr int64_t kElt = kFp8 ? 1 : 2;
   const int64_t k_head_off = static_cast<int64_t>(h) * D * kElt;
   const int64_t v_head_off = static_cast<int64_t>(h) * DV * kElt;
+  // Row 0 of the caches (paged) or of the tensors (dense) at kv head h.
+  const uint8_t* const kh = P.k_cache + k_head_off;
+  const uint8_t* const vh = P.v_cache + v_head_off;
   // Slot -> (K or V, row, logical chunk) of load i for this lane.
   auto slot_of = [&](int i, int& which, int& row, int& q) {
     const int pos = 64 * (kPrefillWaves * i + wave) + lane;
@@ -899,6 +932,7 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
       q = (rel - row * S::kKChunks) ^ (row & S::kKMask);
     }
   };
+  // The lane's byte offset from its tile's first row, for load i.
   uint32_t lane_off[S::kLoads];
   // Whether the lane's slot of load i holds data (not row padding).
   bool lane_ld[S::kLoads];
@@ -907,53 +941,65 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
     int which, row, q;
     slot_of(i, which, row, q);
     const int64_t rb = which ? P.v_row_bytes : P.k_row_bytes;
-    lane_off[i] = static_cast<uint32_t>((row & 15) * rb + (which ? v_head_off : k_head_off) +
-                                        16 * q);
+    lane_off[i] = static_cast<uint32_t>((row & 15) * rb + 16 * q);
     lane_ld[i] = q < (which ? S::kVReal : S::kKReal);
   }
-  // Whether every page of a stage is readable, for the last two stages staged
-  // (by stage parity): the unmasked loop's test for that stage, so it needs no
-  // page lookups of its own.
-  bool staged_ok[2] = {true, true};
-  auto stage_load = [&](int st, uint8_t* buf) {
-    // Wave-uniform (the buffer is the half's); readfirstlane keeps it in an SGPR
-    // for M0 where the compiler cannot prove it.
-    const uint32_t buf_addr = __builtin_amdgcn_readfirstlane(lds_addr_of(buf));
-    // First rows of the stage's tiles: page lookups once per tile, wave-uniform.
-    int64_t row0[kStageTiles];
+  // The first stage staged with a masked page (a -1 block-table entry), or
+  // INT_MAX: the unmasked loop stops before it, so that it needs no page lookups
+  // of its own.  Stages are staged in increasing order and before they are
+  // consumed, so every stage below it that has been staged is readable.
+  int ok_until = INT_MAX;
+  const uint32_t slot_mask = (1u << P.block_size_log2) - 1;
+  auto stage_load = [&](int st) {
+    const uint32_t buf_addr = stage_addr(st);  // wave-uniform (the buffer is the half's)
+    // First K and V rows of the stage's tiles, wave-uniform: paged, the cached
+    // page's slot-0 rows plus the slot's 32-bit offset in the page (the host
+    // bounds a page's bytes below 2^32); dense, row k_start + token.
+    const uint8_t* kt[kStageTiles];
+    const uint8_t* vt[kStageTiles];
+    int64_t row0[kStageTiles];  // dense keys: the tiles' first rows
     bool all_ok = true;
 #pragma unroll
     for (int tt = 0; tt < kStageTiles; ++tt) {
-      bool ok;
-      row0[tt] = key_row<kPaged>(P, bt_row, k_start, st * kStageKeys + tt * kTile, ok, pc);
-      all_ok = all_ok && ok;
+      const int tok = st * kStageKeys + tt * kTile;
+      if constexpr (kPaged) {
+        page_lookup(P, bt_row, tok, kh, vh, pc);  // the cached page unless it changes
+        all_ok = all_ok && pc.page >= 0;
+        const uint32_t slot = static_cast<uint32_t>(tok) & slot_mask;
+        kt[tt] = pc.kb + slot * static_cast<uint32_t>(P.k_row_bytes);
+        vt[tt] = pc.vb + slot * static_cast<uint32_t>(P.v_row_bytes);
+        row0[tt] = 0;
+      } else {
+        row0[tt] = static_cast<int64_t>(k_start) + tok;
+        kt[tt] = kh + row0[tt] * P.k_row_bytes;
+        vt[tt] = vh + row0[tt] * P.v_row_bytes;
+      }
     }
-    staged_ok[st & 1] = all_ok;
+    if (!all_ok) ok_until = min(ok_until, st);
 #pragma unroll
     for (int i = 0; i < S::kLoads; ++i) {
       const int pos0 = 64 * (kPrefillWaves * i + wave);  // wave-uniform
       const int which = pos0 >= S::kNK;                   // 0: K, 1: V
       const int tt = which ? ((pos0 - S::kNK) / S::kVChunks) >> 4 : (pos0 / S::kKChunks) >> 4;
+      const uint8_t* base = which ? vt[0] : kt[0];
       int64_t first = row0[0];
 #pragma unroll
       for (int u = 1; u < kStageTiles; ++u)
-        if (tt == u) first = row0[u];
-      const int64_t rb = which ? P.v_row_bytes : P.k_row_bytes;
-      const uint8_t* base = which ? P.v_cache : P.k_cache;
-      const uint8_t* src;
+        if (tt == u) {
+          base = which ? vt[u] : kt[u];
+          first = row0[u];
+        }
       if (kPaged || first + 15 <= row_cap) {
-        src = base + first * rb + lane_off[i];
+        // (padded rows: the padding chunks are not loaded)
+        if ((S::kKReal == S::kKChunks && S::kVReal == S::kVChunks) || lane_ld[i])
+          lds_dma16_s(base, lane_off[i], buf_addr + 16 * pos0);
       } else {
         // Dense keys whose tile runs past the tensor's end: clamp each row.
         int wh, row, q;
         slot_of(i, wh, row, q);
-        src = base + min(first + (row & 15), row_cap) * rb + (which ? v_head_off : k_head_off) +
-              16 * q;
-      }
-      if constexpr (S::kKReal == S::kKChunks && S::kVReal == S::kVChunks) {
-        lds_dma16(src, buf_addr + 16 * pos0);
-      } else if (lane_ld[i]) {  // padded rows: the padding chunks are not loaded
-        lds_dma16(src, buf_addr + 16 * pos0);
+        const int64_t rb = which ? P.v_row_bytes : P.k_row_bytes;
+        const uint8_t* src = (which ? vh : kh) + min(first + (row & 15), row_cap) * rb + 16 * q;
+        if (lane_ld[i]) lds_dma16(src, buf_addr + 16 * pos0);
       }
     }
   };
@@ -985,8 +1031,8 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
       if (t + 1 < tbeg) continue;  // wave-uniform; both tiles precede this wave's window
       bool ok_a = true, ok_b = true;
       if constexpr (decltype(masked)::value && kPaged) {
-        (void)key_row<kPaged>(P, bt_row, k_start, t * kTile, ok_a, pc);
-        (void)key_row<kPaged>(P, bt_row, k_start, (t + 1) * kTile, ok_b, pc);
+        ok_a = key_ok<kPaged>(P, bt_row, t * kTile, kh, vh, pc);
+        ok_b = key_ok<kPaged>(P, bt_row, (t + 1) * kTile, kh, vh, pc);
       }
       if constexpr (decltype(defer)::value) {
         pend_vm = pair_scores(masked, t * kTile, buf, tt, ok_a, ok_b, pend_pa, pend_pb,
@@ -1010,15 +1056,12 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
               std::false_type{});
     pend = false;
   };
-  // A stage needs no mask when this wave sees all its keys in full (below nfull)
-  // and none of its pages is masked.  Called for stage st before step(st): the
-  // stages staged by then are st and st + 1 at most (st + 2 is staged inside
-  // step(st)), so staged_ok[st & 1] is stage st's page test.
-  auto stage_unmasked = [&](int st) {
-    if ((st + 1) * kStageTiles > nfull) return false;
-    if (win >= 0 && st * kStageKeys < khead) return false;
-    return staged_ok[st & 1];
-  };
+  // A stage needs no mask when this wave sees all its keys in full (its tiles
+  // below nfull: stages below un_full) and none of its pages is masked (below
+  // ok_until; stage st is staged before step(st) tests it); under a window it
+  // also starts at or after khead, which every stage after the masked head does.
+  const int un_full = nfull / kStageTiles;
+  auto stage_unmasked = [&](int st) { return st < min(un_full, ok_until); };
   // kConv: stage st's fp8 rows into its bf16 buffer, the chunks spread over the
   // threads of the half.  fp8 chunk q of a row (dims 16q .. 16q + 15) becomes
   // bf16 chunks 2q and 2q + 1 of the row, in the bf16 stage layout.
@@ -1060,20 +1103,20 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
     if constexpr (decltype(defer)::value) run_pending();
     if constexpr (kConv) {
       if (st + 1 < st_hi) stage_convert(st + 1);
-      if (st + 2 < st_hi) stage_load(st + 2, stage_buf(st + 2));
+      if (st + 2 < st_hi) stage_load(st + 2);
     } else if constexpr (!kConv1) {
-      if (st + 1 < st_hi) stage_load(st + 1, stage_buf(st + 1));
+      if (st + 1 < st_hi) stage_load(st + 1);
     }
     stage_compute(masked, st, comp_buf(st), defer);
     if constexpr (kConv1) {
       __syncthreads();  // every wave is done with the bf16 buffer
       if (st + 1 < st_hi) stage_convert(st + 1);
-      if (st + 2 < st_hi) stage_load(st + 2, stage_buf(st + 2));
+      if (st + 2 < st_hi) stage_load(st + 2);
     }
   };
   // Stages [st0, nstages): under a window, a masked head (keys some query's
   // window starts after), then the unmasked stages, then the masked rest.
-  if (st_lo < st_hi) stage_load(st_lo, stage_buf(st_lo));
+  if (st_lo < st_hi) stage_load(st_lo);
   if constexpr (kConv || kConv1) {
     // The first stage converted before the loop, the second staged; every wave
     // of the work-group passes this barrier (with the key split the halves'
@@ -1081,7 +1124,7 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (st_lo < st_hi) stage_convert(st_lo);
-    if (st_lo + 1 < st_hi) stage_load(st_lo + 1, stage_buf(st_lo + 1));
+    if (st_lo + 1 < st_hi) stage_load(st_lo + 1);
   }
   const int head_end = win >= 0 ? max(st0, (khead + kStageKeys - 1) / kStageKeys) : st0;
   auto run_stages = [&](auto defer) __attribute__((always_inline)) {
