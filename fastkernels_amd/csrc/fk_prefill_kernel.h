@@ -149,6 +149,12 @@ constexpr int kPrefillWaves = 4;               // waves per work-group
 #define FK_PREFILL_VEARLY 1
 #endif
 
+// Tile a's K chunks of an unmasked stage read right after the barrier, before
+// the staging loads (1, head sizes 64 and 256), or with the pair's scores (0).
+#ifndef FK_PREFILL_KEARLY
+#define FK_PREFILL_KEARLY 1
+#endif
+
 // fp8 pages: each stage converted once into bf16 LDS buffers (1), or every
 // wave dequantising the K / V bytes it reads (0).
 #ifndef FK_PREFILL_FP8_CONVERT
@@ -597,6 +603,17 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
   // 74.2 / 74.5; at head size 64 (Whisper heads, 4x512 over 4096) 124.9 -> 128.1.
   constexpr bool kVEarly = FK_PREFILL_VEARLY && !kFp8T && kDVP >= 128 && kDVP < 256;
   short4_t vpre_a[kVS], vpre_b[kVS];  // kVEarly: the pair's V slices, read with its scores
+  // kKEarly: tile a's K chunks of an unmasked stage, read right after the barrier,
+  // before the stage's staging loads are issued, so that the scalar work of the
+  // staging covers their LDS latency.  Same box, A/B in alternating processes, two
+  // rounds (us): head 64 (Whisper heads) 4x512 over 4096 127.9 / 128.2 -> 121.2 /
+  // 120.6, 1x2048 48.8 / 48.9 -> 47.7 / 47.4; head 256 (Qwen3-Next heads) 1x2048
+  // 70.1 / 70.0 -> 68.7 / 68.4; at head 128 level to 1% slower (16x512 73.2 / 72.5
+  // -> 74.0 / 73.0), so not there, nor at the sizes not measured.
+  constexpr bool kKEarly =
+      FK_PREFILL_KEARLY && !kFp8T && kStageTiles == 2 && (kDQ == 64 || kDQ == 256);
+  uint4 kpre[kQC];
+  bool kpre_ok = false;  // wave-uniform: kpre holds this pair's tile a
   auto pair_scores = [&](auto masked, int tok0, const uint8_t* buf, int tt, bool ok_a,
                          bool ok_b, short4_t (&p_a)[kCB], short4_t (&p_b)[kCB],
                          auto early) __attribute__((always_inline)) {
@@ -616,7 +633,12 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
         lds_tile_k<kFp8T, D>(buf, tt, r, g, ta);
         k_chunks_d(ta, ka, ks);
       } else {
-        lds_k_chunks<D, DV>(buf, tt, r, g, ka);
+        if (kKEarly && kpre_ok) {
+#pragma unroll
+          for (int c = 0; c < kQC; ++c) ka[c] = kpre[c];
+        } else {
+          lds_k_chunks<D, DV>(buf, tt, r, g, ka);
+        }
       }
 #pragma unroll
       for (int nb = 0; nb < kCB; ++nb) sc_a[nb] = qk_scores_n(ka, qb[nb]);
@@ -1101,6 +1123,10 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if constexpr (decltype(defer)::value) run_pending();
+    if constexpr (kKEarly && !decltype(masked)::value && !decltype(defer)::value) {
+      lds_k_chunks<D, DV>(comp_buf(st), 0, r, g, kpre);
+      kpre_ok = true;
+    }
     if constexpr (kConv) {
       if (st + 1 < st_hi) stage_convert(st + 1);
       if (st + 2 < st_hi) stage_load(st + 2);
@@ -1108,6 +1134,7 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
       if (st + 1 < st_hi) stage_load(st + 1);
     }
     stage_compute(masked, st, comp_buf(st), defer);
+    kpre_ok = false;
     if constexpr (kConv1) {
       __syncthreads();  // every wave is done with the bf16 buffer
       if (st + 1 < st_hi) stage_convert(st + 1);
