@@ -358,6 +358,30 @@ __device__ __forceinline__ short4_t lds_v_slice(const uint8_t* buf, int tt, int 
   typedef __attribute__((address_space(3))) short4_t* lds_short4;
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4)(buf + off));
 }
+// Slice d of tiles tt and tt + 1 (va, vb).  At value head 64 (the swizzle repeats
+// every 16 rows there) tile tt + 1's address is tile tt's plus a constant, which
+// the read takes as its immediate offset: one address per slice instead of two.
+// Same box, A/B in alternating processes, two rounds (us), with the ones operand
+// kept in registers in both: Whisper heads 4x512 over 4096 118.7 / 119.0 ->
+// 114.0 / 114.1; at value head 128 (also one address per slice) 4x512 over 4096
+// 145.7 / 147.1 -> 149.2 / 152.6, so there each tile has its own addresses.
+template <int D, int DV>
+__device__ __forceinline__ void lds_v_slice2(const uint8_t* buf, int tt, int d, int r, int g,
+                                             short4_t& va, short4_t& vb) {
+  using S = Stage<false, D, DV>;
+  if constexpr (S::kVMask < 16 && v_extent(DV) <= 64) {
+    const int row = 16 * tt + 4 * g + (r >> 2);
+    const int q = r & 3;
+    const int off = S::offset(1, row, 2 * d + (q >> 1)) + 8 * (q & 1);
+    typedef __attribute__((address_space(3))) short4_t* lds_short4;
+    const uint8_t* p = buf + off;
+    va = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4)p);
+    vb = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4)(p + 16 * S::kVChunks * 16));
+  } else {
+    va = lds_v_slice<D, DV>(buf, tt, d, r, g);
+    vb = lds_v_slice<D, DV>(buf, tt + 1, d, r, g);
+  }
+}
 
 // Work-group = kPrefillWaves waves over one kv head: hw query heads of its group
 // times qs = kPrefillWaves / hw blocks of kQTokens query tokens (a group larger
@@ -547,8 +571,13 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
 #pragma unroll
     for (int d = 0; d < kVS; ++d) o[nb][d] = floatx4_t{0.f, 0.f, 0.f, 0.f};
   }
-  const bf16x8_t ones = __builtin_bit_cast(
-      bf16x8_t, make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u));
+  // (Passed through an empty asm so that it stays in four VGPRs: as a constant the
+  // compiler rebuilt it with five moves in every stage.  Same box, A/B in
+  // alternating processes, two rounds, us: 4x512 over 4096 148.4 / 151.2 ->
+  // 145.7 / 147.1, Qwen3-Next heads 1x2048 68.4 / 68.7 -> 67.4 / 67.5.)
+  uint4 ones_w = make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u);
+  asm volatile("" : "+v"(ones_w.x), "+v"(ones_w.y), "+v"(ones_w.z), "+v"(ones_w.w));
+  const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, ones_w);
 
   const int ntiles = (kend + kTile - 1) / kTile;
   // Tiles every query of the block sees in full need no mask: keys up to
@@ -659,8 +688,7 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
       asm volatile("" ::: "memory");  // after tile b's K reads
 #pragma unroll
       for (int d = 0; d < kVS; ++d) {
-        vpre_a[d] = lds_v_slice<D, DV>(buf, tt, d, r, g);
-        vpre_b[d] = lds_v_slice<D, DV>(buf, tt + 1, d, r, g);
+        lds_v_slice2<D, DV>(buf, tt, d, r, g, vpre_a[d], vpre_b[d]);
       }
     }
     __builtin_amdgcn_s_setprio(0);
@@ -817,8 +845,7 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
         short4_t vba[kDS], vbb[kDS];
 #pragma unroll
         for (int d = 0; d < kDS; ++d) {
-          vba[d] = lds_v_slice<D, DV>(buf, tt, hh * kDS + d, r, g);
-          vbb[d] = lds_v_slice<D, DV>(buf, tt + 1, hh * kDS + d, r, g);
+          lds_v_slice2<D, DV>(buf, tt, hh * kDS + d, r, g, vba[d], vbb[d]);
         }
         if (vmask) {
 #pragma unroll
@@ -861,8 +888,7 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
           vba[d] = vpre_a[d];
           vbb[d] = vpre_b[d];
         } else {
-          vba[d] = lds_v_slice<D, DV>(buf, tt, d, r, g);
-          vbb[d] = lds_v_slice<D, DV>(buf, tt + 1, d, r, g);
+          lds_v_slice2<D, DV>(buf, tt, d, r, g, vba[d], vbb[d]);
         }
       }
       // Zero the masked keys' V rows so that P = 0 never meets a NaN.
