@@ -467,3 +467,61 @@ def test_paged_prefill_key_split_window_and_sinks(cuda, window_left):
     _close(_run(c, window_left=window_left, sinks=sinks), ref, 1e-2, "key split")
     _close(_run(dict(c, max_q=20000), window_left=window_left, sinks=sinks), ref, 1e-2,
            "single pass")
+
+
+def _masked_page_reference(c, holes):
+    """float64 attention with the kernel's rule for a -1 block-table entry inside a
+    sequence's pages: its keys are masked (not read), causal positions unchanged;
+    a query with no visible key gives a zero row.  holes: (sequence, page index)."""
+    q = c["q"].double().cpu()
+    kc, vc = c["kc"].double().cpu(), c["vc"].double().cpu()
+    bt = c["bt"].cpu().clone()
+    for b, p in holes:
+        bt[b, p] = -1
+    cu_q, cu_k = c["cu_q"].cpu().tolist(), c["cu_k"].cpu().tolist()
+    bs, hk = kc.shape[1], kc.shape[2]
+    hq = q.shape[1]
+    out = torch.zeros(q.shape, dtype=torch.float64)
+    for i in range(len(cu_q) - 1):
+        q_len, k_len = cu_q[i + 1] - cu_q[i], cu_k[i + 1] - cu_k[i]
+        if q_len == 0:
+            continue
+        pages = bt[i, :(k_len + bs - 1) // bs]
+        ok_page = pages >= 0
+        ks = kc[pages.clamp(min=0).long()].reshape(-1, hk, kc.shape[-1])[:k_len]
+        vs = vc[pages.clamp(min=0).long()].reshape(-1, hk, vc.shape[-1])[:k_len]
+        key_ok = ok_page.repeat_interleave(bs)[:k_len]
+        pos = torch.arange(k_len - q_len, k_len)
+        vis = (torch.arange(k_len)[None, :] <= pos[:, None]) & key_ok[None, :]
+        qi = q[cu_q[i]:cu_q[i + 1]]
+        kk = ks.repeat_interleave(hq // hk, dim=1)
+        vv = vs.repeat_interleave(hq // hk, dim=1)
+        s = torch.einsum("qhd,khd->hqk", qi, kk) * c["scale"]
+        s = s.masked_fill(~vis[None], float("-inf"))
+        p = torch.softmax(s, dim=-1).nan_to_num(0.0)
+        out[cu_q[i]:cu_q[i + 1]] = torch.einsum("hqk,khd->qhd", p, vv)
+    return out.numpy(), bt
+
+
+@pytest.mark.parametrize("label,q_lens,k_lens,bs,holes", [
+    # a chunk over a longer cache: the hole lies in the stages every query sees in full
+    ("chunk, 16-token pages", [300], [700], 16, [(0, 5), (0, 30)]),
+    # a 2048-token prompt: paired blocks with the key split; 256-token pages
+    ("prompt 2048, 256-token pages", [2048], [2048], 256, [(0, 2)]),
+    # four chunks with holes at different places, 64-token pages
+    ("4 chunks, 64-token pages", [128] * 4, [1024] * 4, 64, [(0, 1), (1, 7), (2, 15), (3, 0)]),
+    # one chunk over a long cache: the work-group key split's parts
+    ("chunk over 8192, key-split parts", [512], [8192], 256, [(0, 10), (0, 29)]),
+])
+def test_paged_prefill_masked_pages(cuda, label, q_lens, k_lens, bs, holes):
+    """A -1 block-table entry inside a sequence's pages masks that page's keys (the
+    kernel reads page 0 in its place and discards it).  The reference leaves such a
+    table undefined (its torch path indexes block -1), so the check is against the
+    kernel's own rule, restated in float64 torch."""
+    _flush(f"masked pages: {label}")
+    c = _case(cuda, q_lens, k_lens, bs=bs, seed=91)
+    ref, bt = _masked_page_reference(c, holes)
+    c["bt"] = bt.to(cuda)
+    got = _run(c)
+    _close(got, ref, 1e-2, f"masked pages, {label}")
+    assert torch.equal(_run(c), got), f"masked pages, {label}: repeat"
