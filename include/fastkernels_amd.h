@@ -272,7 +272,10 @@ int fk_store_kvcache_convert(const void* key, int64_t key_row_stride, const void
  * [rows, Hq*head_size_v], the v cache [num_blocks, block_size, Hk, head_size_v]):
  * equal sizes 32, 64, 72, 80, 96, 128 or 256, or 192 / 128 (MLA); others give
  * FK_ERR_UNSUPPORTED.  kv dtype bf16, or fp8 e4m3fn at equal sizes 64, 128, 256 (with
- * k_scale / v_scale as in fk_paged_decode).
+ * k_scale / v_scale as in fk_paged_decode).  A page of key / value rows
+ * (block_size * Hk * head size elements) must span fewer than 2^32 bytes (the kernel
+ * addresses a page's rows by 32-bit offsets; else FK_ERR_INVALID_ARG).  A -1 (or
+ * out-of-range) block-table entry inside a sequence's pages masks that page's keys.
  * No workspace; nothing is allocated.
  * Changed in version 20000: head_size_v added. */
 int fk_paged_prefill(void* out, int64_t out_row_stride, const void* q, int64_t q_row_stride,

@@ -91,6 +91,27 @@ def test_prefill_head_sizes_and_lse_arguments(lib):
     assert varlen(128, 128, lse_stride=-1) == N.FK_ERR_INVALID_ARG
 
 
+def test_prefill_page_bytes_bound(lib):
+    """fk_paged_prefill addresses a page's rows by 32-bit offsets from its first row, so
+    it refuses pages of 2^32 bytes or more (before any launch); one byte less per page
+    passes that check."""
+    from fastkernels_amd import _native as N
+
+    fake = ctypes.c_void_p(0x100000)
+    cu = ctypes.c_void_p(0x200000)
+
+    def paged(block_size, hk, d):
+        return lib.fk_paged_prefill(fake, 32 * d, fake, 32 * d, fake, fake, N.FK_DTYPE_BF16,
+                                    None, None, fake, 4, cu, cu, 1, 0, 0, 32, hk, d, d,
+                                    block_size, 1, 0.1, 1, -1, None, None)
+
+    # 2^22 slots of 8 heads x 128 bf16 (2 KiB rows): 2^33 bytes per page
+    assert paged(1 << 22, 8, 128) == N.FK_ERR_INVALID_ARG
+    assert "2^32" in _last_error(lib)
+    # 2^20 slots of 2 KiB rows: 2^31 bytes; max_seqlen_q 0 then returns before launching
+    assert paged(1 << 20, 8, 128) == N.FK_OK
+
+
 def _last_error(lib) -> str:
     return lib.fk_last_error().decode()
 
