@@ -155,6 +155,10 @@ constexpr int kPrefillWaves = 4;               // waves per work-group
 #define FK_PREFILL_KEARLY 1
 #endif
 
+#ifndef FK_PREFILL_ALT_ORDER
+#define FK_PREFILL_ALT_ORDER 1
+#endif
+
 // fp8 pages: each stage converted once into bf16 LDS buffers (1), or every
 // wave dequantising the K / V bytes it reads (0).
 #ifndef FK_PREFILL_FP8_CONVERT
@@ -1369,14 +1373,18 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
   }
   };
   const int heavy = nqb - 1 - x;
-  // A loop rather than two calls: one copy of the block code (registers).
+  // A loop rather than two calls: one copy of the block code (registers).  With
+  // FK_PREFILL_ALT_ORDER, odd work-groups of a paired launch take their light block
+  // first, so that the two work-groups a CU holds (the same work each) reach their
+  // block change at different times instead of stalling together.
+  const bool light_first = FK_PREFILL_ALT_ORDER && kKS == 1 && paired && (x & 1);
 #pragma unroll 1
   for (int k = 0; k < 2; ++k) {
     if (k == 1) {
       if (!paired || x == heavy) break;  // unpaired, or the middle block of an odd count
       __syncthreads();                   // every wave is done with the last stage buffer
     }
-    process_block(k == 0 ? heavy : x);
+    process_block((k == 0) != light_first ? heavy : x);
   }
 }
 
