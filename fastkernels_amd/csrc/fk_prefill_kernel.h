@@ -155,6 +155,9 @@ constexpr int kPrefillWaves = 4;               // waves per work-group
 #define FK_PREFILL_KEARLY 1
 #endif
 
+#ifndef FK_PREFILL_SPLIT_PAIR
+#define FK_PREFILL_SPLIT_PAIR 1
+#endif
 #ifndef FK_PREFILL_ALT_ORDER
 #define FK_PREFILL_ALT_ORDER 1
 #endif
@@ -436,6 +439,14 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
   constexpr bool kPingPong =
       kKS > 1 && kStageTiles == 2 && 6 * S::kBytes <= 120 * 1024 && !kConv && !kConv1;
   constexpr int kBufs = kPingPong ? 3 : 2;
+  // Causal pairs under the key split: the halves take the blocks as described at
+  // the block loop (FK_PREFILL_SPLIT_PAIR; bf16 stages, where no barrier precedes a
+  // block's first step; head size 128: same box, A/B in alternating processes, two
+  // rounds, us: 1x2048 61.2 / 60.9 -> 60.0 / 59.6, 1x1024 37.9 / 37.9 -> 36.7 / 36.9,
+  // but Whisper heads (64) 1x2048 45.2 / 45.4 -> 47.3 / 47.0 and Qwen3-Next heads
+  // (256) 66.6 / 66.2 -> 68.4 / 67.1).
+  constexpr bool kSplitPair = FK_PREFILL_SPLIT_PAIR && kKS > 1 && !kConv && !kConv1 &&
+                              kDQ == 128 && kDVP == 128;
   constexpr int kHalfBytes =  // a half's buffers
       kBufs * (S::kBytes + (kConv ? SB::kBytes : 0)) + (kConv1 ? SB::kBytes : 0);
   constexpr int kStageAll = kKS * kHalfBytes;
@@ -475,8 +486,12 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
   const int wave = wave_id & (kPrefillWaves - 1);           // role within the half
   uint8_t* const lds_half = lds_all + half * kHalfBytes;
   // Stage st's buffer: two alternate; with three, stage st mod 3.
+  // buf_rot: added to the stage index when picking its buffer (a block that starts
+  // right after another in the same half, split pairs below, takes the buffer the
+  // previous block's next stage would have used).
+  int buf_rot = 0;
   auto stage_buf = [&](int st) {
-    return lds_half + (kBufs == 2 ? (st & 1) : st % kBufs) * S::kBytes;
+    return lds_half + (kBufs == 2 ? ((st + buf_rot) & 1) : (st + buf_rot) % kBufs) * S::kBytes;
   };
   // The buffer the compute path reads stage st from: the staged one, or with
   // kConv its bf16 conversion.
@@ -484,7 +499,8 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
   // direct-to-LDS loads; no generic-pointer conversion per stage).
   const uint32_t lds_half_addr = __builtin_amdgcn_readfirstlane(lds_addr_of(lds_half));
   auto stage_addr = [&](int st) -> uint32_t {
-    return lds_half_addr + (kBufs == 2 ? (st & 1) : st % kBufs) * S::kBytes;
+    return lds_half_addr +
+           (kBufs == 2 ? ((st + buf_rot) & 1) : (st + buf_rot) % kBufs) * S::kBytes;
   };
   auto comp_buf = [&](int st) {
     if constexpr (kConv) return lds_half + kBufs * S::kBytes + (st & 1) * SB::kBytes;
@@ -519,10 +535,48 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
     st0 = min(kbeg_wg / kStageKeys, nstages);
   };
 
+  // This work-group's stages [wlo, whi) of query block qblk (st0: the block's
+  // first stage): all of them, or with the work-group key split part xpart of xs
+  // equal parts (a part past the end is empty).
+  auto wg_range = [&](int qblk, int& st0, int& wlo, int& whi) {
+    int nstages;
+    block_stages(qblk, st0, nstages);
+    wlo = st0;
+    whi = nstages;
+    if (xs > 1) {
+      const int n1 = (nstages - st0 + xs - 1) / xs;
+      wlo = min(st0 + xpart * n1, nstages);
+      whi = min(wlo + n1, nstages);
+    }
+  };
+  // This half's stages [st_lo, st_hi) of block qblk and the barriers every wave
+  // passes (nsteps): the work-group's range, or with the key split the first or
+  // second half of it.  With the deferred P.V of the ping-pong the second half
+  // ends about one stage after the first (head size 128, per-wave clock stamps:
+  // 1.1 us), so the first half takes the extra stage of an even count and the
+  // second half's tail runs under the first's last stage.
+  auto stage_range = [&](int qblk, int& st0, int& st_lo, int& st_hi, int& nsteps) {
+    int wlo, whi;
+    wg_range(qblk, st0, wlo, whi);
+    st_lo = wlo;
+    st_hi = whi;
+    nsteps = whi - wlo;
+    if constexpr (kKS > 1) {
+      const int m = whi - wlo;
+      // the first half's stages (at head size 64 the second half measured no lag)
+      const int h0 = (kPingPong && kDQ > 64) ? min(m, (m + 2) / 2) : (m + 1) / 2;
+      st_lo = half == 0 ? wlo : wlo + h0;
+      st_hi = half == 0 ? wlo + h0 : whi;
+      nsteps = h0;
+    }
+  };
+
   PageCache pc;
-  // One query block of the work-group, start to finish (its own K/V stages);
-  // with the key split both halves take it, each streaming half its stages.
-  auto process_block = [&](int qblk) {
+  // One query block of the work-group, start to finish: this half streams stages
+  // [st_lo, st_hi) of it (st0: the block's first stage) and every wave passes
+  // nsteps step barriers; with the key split the halves then merge (unless solo:
+  // a block this half streams whole, which writes its own rows).
+  auto process_block = [&](int qblk, int st0, int st_lo, int st_hi, int nsteps, bool solo) {
   const int jw0 = qblk * wg_tokens;  // first query of the work-group
   const int j0 = jw0 + (wave / hw) * kQT;
   // Waves without queries (past the chunk, or past the group) still stage.
@@ -587,37 +641,7 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
   // Tiles every query of the block sees in full need no mask: keys up to
   // offset + j0 (query j0's last key), inside [0, kend).
   const int nfull = active ? max(0, min(kend, offset + j0 + 1)) / kTile : 0;
-  int st0, nstages;  // the block's stages
-  block_stages(qblk, st0, nstages);
-  const int tbeg = kbeg / kTile;                      // this wave's first tile
-  // This half's stages [st_lo, st_hi) and the barriers every wave passes
-  // (nsteps): the whole range, or with the key split its part of it.  Over
-  // work-groups, part xpart of xs equal parts (a part past the end is empty);
-  // within the work-group, the first or second half of that.  With the
-  // deferred P.V of the ping-pong the second half ends about one stage after
-  // the first (head size 128, per-wave clock stamps: 1.1 us), so the first half
-  // takes the extra stage of an even count and the second half's tail runs
-  // under the first's last stage.
-  int st_lo = st0, st_hi = nstages, nsteps = nstages - st0;
-  if (kKS * xs > 1) {
-    int wlo = st0, whi = nstages;  // this work-group's part
-    if (xs > 1) {
-      const int n1 = (nstages - st0 + xs - 1) / xs;
-      wlo = min(st0 + xpart * n1, nstages);
-      whi = min(wlo + n1, nstages);
-    }
-    st_lo = wlo;
-    st_hi = whi;
-    nsteps = whi - wlo;
-    if constexpr (kKS > 1) {
-      const int m = whi - wlo;
-      // the first half's stages (at head size 64 the second half measured no lag)
-      const int h0 = (kPingPong && kDQ > 64) ? min(m, (m + 2) / 2) : (m + 1) / 2;
-      st_lo = half == 0 ? wlo : wlo + h0;
-      st_hi = half == 0 ? wlo + h0 : whi;
-      nsteps = h0;
-    }
-  }
+  const int tbeg = kbeg / kTile;  // this wave's first tile
 
   // Two 16-key tiles (tiles tt, tt + 1 of `buf`, keys tok0 .. tok0 + 31):
   // scores, one online-softmax update per query column for the 32 keys, P.V.
@@ -1216,7 +1240,7 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
       m_row[nb][i] = row_from(m_run[nb], g, i);
       l_row[nb][i] = l_acc[nb][i];
     }
-  if constexpr (kKS > 1) {
+  if (kKS > 1 && !solo) {
 #pragma unroll 1
     for (int k = st_hi - st_lo; k < nsteps; ++k) {  // the shorter half's empty steps
       __builtin_amdgcn_s_waitcnt(0);
@@ -1373,6 +1397,32 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
   }
   };
   const int heavy = nqb - 1 - x;
+  // Key split over a causal pair (kSplitPair): the first half streams the head of
+  // the heavy block; the second half streams the whole light block and writes its
+  // rows (no merge), then the heavy block's tail; the halves then merge the heavy
+  // block.  Each half passes T step barriers (the shorter pads with empty steps)
+  // and the merge's two barriers.  The second half's heavy stages start in the
+  // buffer the light block's next stage would have used: every wave of the half
+  // is past the light block's last barrier by then, and that buffer held a stage
+  // at least two steps old.
+  if (kSplitPair && paired && x != heavy) {
+    int s0l, lol, hil, s0h, loh, hih;
+    wg_range(x, s0l, lol, hil);
+    wg_range(heavy, s0h, loh, hih);
+    const int nl = hil - lol, nh = hih - loh;
+    const int a0 = (kPingPong && kDQ > 64) ? (nh + nl + 2) / 2 : (nh + nl + 1) / 2;
+    const int a = min(nh, a0);          // the heavy block's stages of the first half
+    const int T = max(a, nl + nh - a);  // step barriers per half
+    if (half == 0) {
+      process_block(heavy, s0h, loh, loh + a, T, false);
+    } else {
+      process_block(x, s0l, lol, hil, nl, true);
+      const int kb = kBufs;
+      buf_rot = ((hil - (loh + a)) % kb + kb) % kb;
+      process_block(heavy, s0h, loh + a, hih, T - nl, false);
+    }
+    return;
+  }
   // A loop rather than two calls: one copy of the block code (registers).  With
   // FK_PREFILL_ALT_ORDER, odd work-groups of a paired launch take their light block
   // first, so that the two work-groups a CU holds (the same work each) reach their
@@ -1384,7 +1434,10 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
       if (!paired || x == heavy) break;  // unpaired, or the middle block of an odd count
       __syncthreads();                   // every wave is done with the last stage buffer
     }
-    process_block((k == 0) != light_first ? heavy : x);
+    const int qblk = (k == 0) != light_first ? heavy : x;
+    int st0, st_lo, st_hi, nsteps;
+    stage_range(qblk, st0, st_lo, st_hi, nsteps);
+    process_block(qblk, st0, st_lo, st_hi, nsteps, false);
   }
 }
 
