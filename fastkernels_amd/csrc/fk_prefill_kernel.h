@@ -1405,39 +1405,60 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
   // buffer the light block's next stage would have used: every wave of the half
   // is past the light block's last barrier by then, and that buffer held a stage
   // at least two steps old.
-  if (kSplitPair && paired && x != heavy) {
-    int s0l, lol, hil, s0h, loh, hih;
+  const bool split_pair = kSplitPair && paired && x != heavy;
+  int s0l = 0, lol = 0, hil = 0, s0h = 0, loh = 0, hih = 0, sp_a = 0, sp_t = 0;
+  if (split_pair) {
     wg_range(x, s0l, lol, hil);
     wg_range(heavy, s0h, loh, hih);
     const int nl = hil - lol, nh = hih - loh;
     const int a0 = (kPingPong && kDQ > 64) ? (nh + nl + 2) / 2 : (nh + nl + 1) / 2;
-    const int a = min(nh, a0);          // the heavy block's stages of the first half
-    const int T = max(a, nl + nh - a);  // step barriers per half
-    if (half == 0) {
-      process_block(heavy, s0h, loh, loh + a, T, false);
-    } else {
-      process_block(x, s0l, lol, hil, nl, true);
-      const int kb = kBufs;
-      buf_rot = ((hil - (loh + a)) % kb + kb) % kb;
-      process_block(heavy, s0h, loh + a, hih, T - nl, false);
-    }
-    return;
+    sp_a = min(nh, a0);                   // the heavy block's stages of the first half
+    sp_t = max(sp_a, nl + nh - sp_a);     // step barriers per half
   }
-  // A loop rather than two calls: one copy of the block code (registers).  With
-  // FK_PREFILL_ALT_ORDER, odd work-groups of a paired launch take their light block
-  // first, so that the two work-groups a CU holds (the same work each) reach their
-  // block change at different times instead of stalling together.
+  // Odd work-groups of a paired launch (4-wave work-groups) take their light block
+  // first (FK_PREFILL_ALT_ORDER), so that the two work-groups a CU holds (the same
+  // work each) reach their block change at different times instead of stalling
+  // together.
   const bool light_first = FK_PREFILL_ALT_ORDER && kKS == 1 && paired && (x & 1);
+  if constexpr (kSplitPair) {
+    // The blocks this half takes, in order: one loop and one call site, so that
+    // the block code is emitted once (an instance per call site tripled the
+    // kernel's code, 37 -> 140 KB).
+    const int nseg = split_pair ? (half == 0 ? 1 : 2) : ((paired && x != heavy) ? 2 : 1);
 #pragma unroll 1
-  for (int k = 0; k < 2; ++k) {
-    if (k == 1) {
-      if (!paired || x == heavy) break;  // unpaired, or the middle block of an odd count
-      __syncthreads();                   // every wave is done with the last stage buffer
+    for (int k = 0; k < nseg; ++k) {
+      int qblk, st0, st_lo, st_hi, nsteps;
+      bool solo = false;
+      if (split_pair) {
+        if (half == 0) {
+          qblk = heavy, st0 = s0h, st_lo = loh, st_hi = loh + sp_a, nsteps = sp_t;
+        } else if (k == 0) {
+          qblk = x, st0 = s0l, st_lo = lol, st_hi = hil, nsteps = hil - lol, solo = true;
+        } else {
+          qblk = heavy, st0 = s0h, st_lo = loh + sp_a, st_hi = hih,
+          nsteps = sp_t - (hil - lol);
+          buf_rot = ((hil - st_lo) % kBufs + kBufs) % kBufs;
+        }
+      } else {
+        if (k == 1) __syncthreads();  // every wave is done with the last stage buffer
+        qblk = k == 0 ? heavy : x;
+        stage_range(qblk, st0, st_lo, st_hi, nsteps);
+      }
+      process_block(qblk, st0, st_lo, st_hi, nsteps, solo);
     }
-    const int qblk = (k == 0) != light_first ? heavy : x;
-    int st0, st_lo, st_hi, nsteps;
-    stage_range(qblk, st0, st_lo, st_hi, nsteps);
-    process_block(qblk, st0, st_lo, st_hi, nsteps, false);
+  } else {
+    // A loop rather than two calls: one copy of the block code (registers).
+#pragma unroll 1
+    for (int k = 0; k < 2; ++k) {
+      if (k == 1) {
+        if (!paired || x == heavy) break;  // unpaired, or the middle block of an odd count
+        __syncthreads();                   // every wave is done with the last stage buffer
+      }
+      const int qblk = (k == 0) != light_first ? heavy : x;
+      int st0, st_lo, st_hi, nsteps;
+      stage_range(qblk, st0, st_lo, st_hi, nsteps);
+      process_block(qblk, st0, st_lo, st_hi, nsteps, false);
+    }
   }
 }
 
