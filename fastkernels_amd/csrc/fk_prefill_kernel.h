@@ -441,12 +441,13 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
   constexpr int kBufs = kPingPong ? 3 : 2;
   // Causal pairs under the key split: the halves take the blocks as described at
   // the block loop (FK_PREFILL_SPLIT_PAIR; bf16 stages, where no barrier precedes a
-  // block's first step; head size 128: same box, A/B in alternating processes, two
-  // rounds, us: 1x2048 61.2 / 60.9 -> 60.0 / 59.6, 1x1024 37.9 / 37.9 -> 36.7 / 36.9,
-  // but Whisper heads (64) 1x2048 45.2 / 45.4 -> 47.3 / 47.0 and Qwen3-Next heads
-  // (256) 66.6 / 66.2 -> 68.4 / 67.1).
-  constexpr bool kSplitPair = FK_PREFILL_SPLIT_PAIR && kKS > 1 && !kConv && !kConv1 &&
-                              kDQ == 128 && kDVP == 128;
+  // block's first step; query / key heads of 128 and up).  Same box, A/B in
+  // alternating processes, two rounds, us: head 128 1x2048 61.2 / 60.9 -> 60.0 /
+  // 59.6, 1x1024 37.9 / 37.9 -> 36.7 / 36.9; head 256 (Qwen3-Next heads) 1x2048
+  // 67.4 / 67.4 -> 65.8 / 66.5; head 64 (Whisper heads) 1x2048 45.1 / 45.1 -> 46.7 /
+  // 46.5, so not there.
+  constexpr bool kSplitPair =
+      FK_PREFILL_SPLIT_PAIR && kKS > 1 && !kConv && !kConv1 && kDQ >= 128;
   constexpr int kHalfBytes =  // a half's buffers
       kBufs * (S::kBytes + (kConv ? SB::kBytes : 0)) + (kConv1 ? SB::kBytes : 0);
   constexpr int kStageAll = kKS * kHalfBytes;
