@@ -51,6 +51,12 @@ PAGED_CASES = [
     ("fp8 pages", [256], [4096], {"hq": 8, "hk": 2, "bs": 64, "fp8": True}),
     ("head 256", [128, 7], [4096, 900], {"hq": 16, "hk": 2, "d": 256, "bs": 64}),
     ("GQA 8, head 64", [200], [3000], {"hq": 16, "hk": 2, "d": 64, "bs": 256}),
+    # causal pairs at heads 128 and 256: the halves take the pair's blocks apart
+    # (light block whole in the second half), each work-group on its part of both
+    ("prompt 1024, GQA 4 head 128 (paired blocks)", [1024], [1024],
+     {"hq": 8, "hk": 2, "bs": 64}),
+    ("prompt 2048, head 256 (paired blocks)", [2048], [2048],
+     {"hq": 8, "hk": 1, "d": 256, "bs": 64}),
 ]
 
 
