@@ -155,9 +155,14 @@ constexpr int kPrefillWaves = 4;               // waves per work-group
 #define FK_PREFILL_KEARLY 1
 #endif
 
+// Causal pairs under the key split at heads of 128 and up: the second half streams
+// the light block whole and the heavy block's tail (1), or both halves split both
+// blocks (0).
 #ifndef FK_PREFILL_SPLIT_PAIR
 #define FK_PREFILL_SPLIT_PAIR 1
 #endif
+// Causal pairs in 4-wave work-groups: odd work-groups take their light block first
+// (1), or every work-group its heavy block first (0).
 #ifndef FK_PREFILL_ALT_ORDER
 #define FK_PREFILL_ALT_ORDER 1
 #endif
@@ -494,8 +499,6 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
   auto stage_buf = [&](int st) {
     return lds_half + (kBufs == 2 ? ((st + buf_rot) & 1) : (st + buf_rot) % kBufs) * S::kBytes;
   };
-  // The buffer the compute path reads stage st from: the staged one, or with
-  // kConv its bf16 conversion.
   // The LDS byte address of stage st's buffer, as an integer (M0 of the
   // direct-to-LDS loads; no generic-pointer conversion per stage).
   const uint32_t lds_half_addr = __builtin_amdgcn_readfirstlane(lds_addr_of(lds_half));
@@ -503,6 +506,8 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
     return lds_half_addr +
            (kBufs == 2 ? ((st + buf_rot) & 1) : (st + buf_rot) % kBufs) * S::kBytes;
   };
+  // The buffer the compute path reads stage st from: the staged one, or with
+  // kConv its bf16 conversion.
   auto comp_buf = [&](int st) {
     if constexpr (kConv) return lds_half + kBufs * S::kBytes + (st & 1) * SB::kBytes;
     else if constexpr (kConv1) return lds_half + kBufs * S::kBytes;
