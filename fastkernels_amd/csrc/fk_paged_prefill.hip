@@ -35,6 +35,7 @@ struct PrefillShape {
   int hsplit;       // work-groups per kv head (head groups of up to 4)
   int ks;           // key parts within a work-group (1 or 2)
   int xs;           // key parts over work-groups (1: none), with a workspace
+  int ks_plain;     // ks of the same call without a workspace (xs = 1)
 };
 
 PrefillShape prefill_shape(bool paged, bool fp8, int64_t batch, int64_t max_seqlen_q,
@@ -55,6 +56,7 @@ PrefillShape prefill_shape(bool paged, bool fp8, int64_t batch, int64_t max_seql
   const int64_t wgs = static_cast<int64_t>(num_kv_heads) * sh.hsplit * batch *
                       (may_pair ? (sh.qblocks + 1) / 2 : sh.qblocks);
   sh.ks = ((std::max(head_size, head_size_v) <= 192 || paged) && wgs < 2LL * num_cus()) ? 2 : 1;
+  sh.ks_plain = sh.ks;
   // Work-group key split when even that leaves CUs without a work-group (one
   // work-group per CU at this size): each block's keys in xs parts over xs
   // work-groups, merged by prefill_merge_kernel.  xs minimises an estimate of
@@ -67,6 +69,27 @@ PrefillShape prefill_shape(bool paged, bool fp8, int64_t batch, int64_t max_seql
   // launch.  Short blocks (prompts) keep one part: their per-block costs stay.
   sh.xs = 1;
   const int64_t ncu = num_cus();
+  // Paged bf16 at head sizes up to 64: a paired launch with fewer work-groups
+  // than CUs runs faster as 4-wave work-groups, two per CU, each block's keys
+  // in xs parts over work-groups, than as one key-split work-group per pair on
+  // fewer CUs than the chip has: xs fills at least 7/8 of the two-per-CU slots,
+  // and a part keeps at least 16 stages of 32 keys.  Measured on MI355X
+  // (Whisper large's heads, Hq = Hk = 20): a 2048-token prompt, 160 pairs ->
+  // 480 work-groups, 45.6 -> 40.3 us; a 1536-token prompt at 4 parts 33.6 ->
+  // 33.1 us, so shorter parts are not taken; at head size 128 a 1024-token
+  // prompt at 2-4 parts was 2-19% slower, so the rule stops at 64.
+  if (paged && !fp8 && std::max(head_size, head_size_v) <= 64 && may_pair && wgs > 0 &&
+      wgs < ncu) {
+    const int64_t xs = std::min<int64_t>(kMaxKeyParts, 2 * ncu / wgs);
+    const double stages = static_cast<double>(std::max(max_seqlen_k, max_seqlen_q) + wg_tokens) /
+                          kStageKeys;  // a pair's stages
+    if (xs >= 2 && 8 * wgs * xs >= 7 * 2 * ncu && stages >= 16.0 * xs &&
+        sh.qblocks * xs <= 65535) {
+      sh.ks = 1;
+      sh.xs = static_cast<int>(xs);
+      return sh;
+    }
+  }
   if (wgs > 0 && wgs < ncu) {
     constexpr double kStageUs = 1.2, kBlockUs = 6.0, kMergeUs = 3.0;
     constexpr double kMergeBytesPerUs = 2.5e6;
@@ -242,6 +265,7 @@ int prefill_entry(const char* name, bool paged, void* out, int64_t out_row_strid
                                   num_kv_heads, head_size, head_size_v, causal);
   if (workspace == nullptr) {
     sh.xs = 1;  // no workspace: the launch without the work-group key split
+    sh.ks = sh.ks_plain;
   } else {
     FK_REQUIRE(total_q >= 0, "%s: total_q %lld must be >= 0", name, (long long)total_q);
     const int64_t need = prefill_ws_bytes(sh, total_q, num_heads, head_size_v);

@@ -57,6 +57,9 @@ PAGED_CASES = [
      {"hq": 8, "hk": 2, "bs": 64}),
     ("prompt 2048, head 256 (paired blocks)", [2048], [2048],
      {"hq": 8, "hk": 1, "d": 256, "bs": 64}),
+    # head 64, 160 pairs: 4-wave work-groups, two per CU, three key parts each
+    ("prompt 2048, MHA head 64, 20 heads (4-wave work-groups)", [2048], [2048],
+     {"hq": 20, "hk": 20, "d": 64, "bs": 256}),
 ]
 
 
