@@ -57,9 +57,42 @@ PrefillShape prefill_shape(bool paged, bool fp8, int64_t batch, int64_t max_seql
                       (may_pair ? (sh.qblocks + 1) / 2 : sh.qblocks);
   sh.ks = ((std::max(head_size, head_size_v) <= 192 || paged) && wgs < 2LL * num_cus()) ? 2 : 1;
   sh.ks_plain = sh.ks;
-  // Work-group key split when even that leaves CUs without a work-group (one
-  // work-group per CU at this size): each block's keys in xs parts over xs
-  // work-groups, merged by prefill_merge_kernel.  xs minimises an estimate of
+  sh.xs = 1;
+  const int64_t ncu = num_cus();
+  // Paged keys where the key split would run (fewer 4-wave work-groups than two
+  // per CU): 4-wave work-groups, two per CU, with each block's keys in xs parts
+  // over work-groups, instead of one 8-wave key-split work-group per block, for
+  // chunks over cached keys (blocks not paired) and, at head sizes up to 64 with
+  // bf16 pages, for causal pairs.  xs = floor(2 CUs / work-groups) when that is
+  // at least 2 and fills 7/8 of the two-per-CU slots, else the ceiling (at most
+  // kMaxKeyParts), and only while a part keeps at least 20 stages of 32 keys.
+  // Measured on MI355X (whole call, µs, key split -> this): Qwen3-8B heads
+  // (32 / 8 / 128) 1x512 over 8192 100.2 -> 81.8, 2x512 over 4096 92.4 -> 82.1,
+  // 3x512 over 4096 159.6 -> 133.4, fp8 pages 1x512 over 8192 115.1 -> 105.4;
+  // Qwen3-Next heads (16 / 2 / 256) 1x512 over 8192 117.7 -> 104.3; Whisper
+  // heads (20 / 20 / 64) 4x512 over 4096 111.3 -> 73.5, prompts 1x2048 45.6 ->
+  // 40.3, 2x2048 79.9 -> 60.0, 1x4096 130.0 -> 89.7.  Causal pairs at head 128
+  // and 256 stay on the key split with split pairs (1x2048: 58.9 -> 68.3 and
+  // 65.7 -> 73.8 this way), and so do shorter parts (Whisper heads 1x1536 at 4
+  // parts of 13 stages: 33.6 -> 33.1; 2x1024 at 3 parts of 12: 31.6 -> 33.2).
+  if (paged && sh.ks == 2 && wgs > 0 &&
+      (!may_pair || (!fp8 && std::max(head_size, head_size_v) <= 64))) {
+    const int64_t slots = 2 * ncu;
+    int64_t xs = slots / wgs;
+    if (xs < 2 || 8 * wgs * xs < 7 * slots) xs = (slots + wgs - 1) / wgs;
+    xs = std::min<int64_t>(xs, kMaxKeyParts);
+    const double stages = static_cast<double>(std::max(max_seqlen_k, max_seqlen_q) +
+                                              (may_pair ? wg_tokens : 0)) /
+                          kStageKeys;  // the heaviest work-group's stages (a pair's)
+    if (xs >= 2 && stages >= 20.0 * xs && sh.qblocks * xs <= 65535) {
+      sh.ks = 1;
+      sh.xs = static_cast<int>(xs);
+      return sh;
+    }
+  }
+  // Otherwise, work-group key split when even the key split leaves CUs without
+  // a work-group (one work-group per CU at this size): each block's keys in xs
+  // parts over xs work-groups, merged by prefill_merge_kernel.  xs minimises an estimate of
   // the call's time (µs; constants measured on MI355X): the heaviest work-group
   // streams S stages of 32 keys (all of max_seqlen_k; a causal pair of blocks
   // about max_seqlen_k plus one block) at kStageUs per stage and key-split half,
@@ -67,29 +100,6 @@ PrefillShape prefill_shape(bool paged, bool fp8, int64_t batch, int64_t max_seql
   // the work-groups run ceil(wgs * xs / CUs) rounds; the parts' states are
   // written and read back at kMergeBytesPerUs, plus kMergeUs for the merge's
   // launch.  Short blocks (prompts) keep one part: their per-block costs stay.
-  sh.xs = 1;
-  const int64_t ncu = num_cus();
-  // Paged bf16 at head sizes up to 64: a paired launch with fewer work-groups
-  // than CUs runs faster as 4-wave work-groups, two per CU, each block's keys
-  // in xs parts over work-groups, than as one key-split work-group per pair on
-  // fewer CUs than the chip has: xs fills at least 7/8 of the two-per-CU slots,
-  // and a part keeps at least 16 stages of 32 keys.  Measured on MI355X
-  // (Whisper large's heads, Hq = Hk = 20): a 2048-token prompt, 160 pairs ->
-  // 480 work-groups, 45.6 -> 40.3 us; a 1536-token prompt at 4 parts 33.6 ->
-  // 33.1 us, so shorter parts are not taken; at head size 128 a 1024-token
-  // prompt at 2-4 parts was 2-19% slower, so the rule stops at 64.
-  if (paged && !fp8 && std::max(head_size, head_size_v) <= 64 && may_pair && wgs > 0 &&
-      wgs < ncu) {
-    const int64_t xs = std::min<int64_t>(kMaxKeyParts, 2 * ncu / wgs);
-    const double stages = static_cast<double>(std::max(max_seqlen_k, max_seqlen_q) + wg_tokens) /
-                          kStageKeys;  // a pair's stages
-    if (xs >= 2 && 8 * wgs * xs >= 7 * 2 * ncu && stages >= 16.0 * xs &&
-        sh.qblocks * xs <= 65535) {
-      sh.ks = 1;
-      sh.xs = static_cast<int>(xs);
-      return sh;
-    }
-  }
   if (wgs > 0 && wgs < ncu) {
     constexpr double kStageUs = 1.2, kBlockUs = 6.0, kMergeUs = 3.0;
     constexpr double kMergeBytesPerUs = 2.5e6;

@@ -57,9 +57,21 @@ PAGED_CASES = [
      {"hq": 8, "hk": 2, "bs": 64}),
     ("prompt 2048, head 256 (paired blocks)", [2048], [2048],
      {"hq": 8, "hk": 1, "d": 256, "bs": 64}),
-    # head 64, 160 pairs: 4-wave work-groups, two per CU, three key parts each
+    # 4-wave work-groups, two per CU, each block's keys in parts over work-groups
+    # (in place of the 8-wave key split): chunks over cached keys at every head
+    # size and page type, causal pairs at head 64
     ("prompt 2048, MHA head 64, 20 heads (4-wave work-groups)", [2048], [2048],
      {"hq": 20, "hk": 20, "d": 64, "bs": 256}),
+    ("prompts 2x2048, MHA head 64, 10 heads (4-wave work-groups)", [2048, 2048], [2048, 2048],
+     {"hq": 10, "hk": 10, "d": 64, "bs": 256}),
+    ("chunk 512 over 8192, GQA 4 (4-wave work-groups)", [512], [8192],
+     {"hq": 8, "hk": 2, "bs": 256}),
+    ("fp8 pages, chunk 512 over 8192 (4-wave work-groups)", [512], [8192],
+     {"hq": 8, "hk": 2, "bs": 64, "fp8": True}),
+    ("head 256, chunk 512 over 8192 (4-wave work-groups)", [512], [8192],
+     {"hq": 4, "hk": 1, "d": 256, "bs": 64}),
+    ("chunks of a batch over long caches (4-wave work-groups)", [1, 300, 512],
+     [8192, 5000, 4096], {"hq": 8, "hk": 2, "bs": 16}),
 ]
 
 
