@@ -66,15 +66,17 @@ PrefillShape prefill_shape(bool paged, bool fp8, int64_t batch, int64_t max_seql
   // bf16 pages, for causal pairs.  xs = floor(2 CUs / work-groups) when that is
   // at least 2 and fills 7/8 of the two-per-CU slots, else the ceiling (at most
   // kMaxKeyParts), and only while a part keeps at least 20 stages of 32 keys.
-  // Measured on MI355X (whole call, µs, key split -> this): Qwen3-8B heads
-  // (32 / 8 / 128) 1x512 over 8192 100.2 -> 81.8, 2x512 over 4096 92.4 -> 82.1,
-  // 3x512 over 4096 159.6 -> 133.4, fp8 pages 1x512 over 8192 115.1 -> 105.4;
-  // Qwen3-Next heads (16 / 2 / 256) 1x512 over 8192 117.7 -> 104.3; Whisper
-  // heads (20 / 20 / 64) 4x512 over 4096 111.3 -> 73.5, prompts 1x2048 45.6 ->
-  // 40.3, 2x2048 79.9 -> 60.0, 1x4096 130.0 -> 89.7.  Causal pairs at head 128
-  // and 256 stay on the key split with split pairs (1x2048: 58.9 -> 68.3 and
-  // 65.7 -> 73.8 this way), and so do shorter parts (Whisper heads 1x1536 at 4
-  // parts of 13 stages: 33.6 -> 33.1; 2x1024 at 3 parts of 12: 31.6 -> 33.2).
+  // Measured on MI355X (whole call, µs, key split -> this; same box, A/B in
+  // alternating processes, two rounds averaged): Qwen3-8B heads (32 / 8 / 128)
+  // 1x512 over 8192 102.9 -> 91.2, 2x512 over 4096 92.8 -> 86.5, 3x512 over 4096
+  // 160.2 -> 145.9, fp8 pages 1x512 over 8192 114.7 -> 109.8; Qwen3-Next heads
+  // (16 / 2 / 256) 1x512 over 8192 116.0 -> 106.4, 2x512 over 4096 109.4 ->
+  // 103.5; Whisper heads (20 / 20 / 64) 4x512 over 4096 112.9 -> 80.4, 2x512
+  // over 4096 57.2 -> 47.8, 1x512 over 8192 54.9 -> 48.5, prompts 1x2048 45.2 ->
+  // 40.8, 2x2048 80.5 -> 61.7, 1x4096 132.0 -> 93.7.  In single probes, causal
+  // pairs at head 128 and 256 were slower this way (1x2048: 58.9 -> 68.3 and
+  // 65.7 -> 73.8; they keep the key split with split pairs), and so were short
+  // parts (Whisper heads 2x1024 at 3 parts of 12 stages: 31.6 -> 33.2).
   if (paged && sh.ks == 2 && wgs > 0 &&
       (!may_pair || (!fp8 && std::max(head_size, head_size_v) <= 64))) {
     const int64_t slots = 2 * ncu;
@@ -92,8 +94,8 @@ PrefillShape prefill_shape(bool paged, bool fp8, int64_t batch, int64_t max_seql
   }
   // Otherwise, work-group key split when even the key split leaves CUs without
   // a work-group (one work-group per CU at this size): each block's keys in xs
-  // parts over xs work-groups, merged by prefill_merge_kernel.  xs minimises an estimate of
-  // the call's time (µs; constants measured on MI355X): the heaviest work-group
+  // parts over xs work-groups, merged by prefill_merge_kernel.  xs minimises an
+  // estimate of the call's time (µs; constants measured on MI355X): the heaviest work-group
   // streams S stages of 32 keys (all of max_seqlen_k; a causal pair of blocks
   // about max_seqlen_k plus one block) at kStageUs per stage and key-split half,
   // plus kBlockUs per block (its queries, the first stage's latency, the rows);
