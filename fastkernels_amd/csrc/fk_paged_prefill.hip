@@ -102,6 +102,8 @@ PrefillShape prefill_shape(bool paged, bool fp8, int64_t batch, int64_t max_seql
   // the work-groups run ceil(wgs * xs / CUs) rounds; the parts' states are
   // written and read back at kMergeBytesPerUs, plus kMergeUs for the merge's
   // launch.  Short blocks (prompts) keep one part: their per-block costs stay.
+  // (The constants were fitted with the parts' O in fp32; the estimate keeps
+  // those bytes, so that its choices stay the measured ones.)
   if (wgs > 0 && wgs < ncu) {
     constexpr double kStageUs = 1.2, kBlockUs = 6.0, kMergeUs = 3.0;
     constexpr double kMergeBytesPerUs = 2.5e6;
@@ -128,8 +130,9 @@ PrefillShape prefill_shape(bool paged, bool fp8, int64_t batch, int64_t max_seql
 // Bytes of the work-group key split's partial states (0 without the split).
 int64_t prefill_ws_bytes(const PrefillShape& sh, int64_t total_q, int num_heads, int head_size_v) {
   if (sh.xs <= 1) return 0;
-  const int64_t floats = static_cast<int64_t>(sh.xs) * total_q * num_heads * (head_size_v + kPartMl);
-  return (floats * 4 + 255) / 256 * 256;
+  const int64_t bytes = part_ml_offset(sh.xs, total_q, num_heads, head_size_v) +
+                        static_cast<int64_t>(sh.xs) * total_q * num_heads * kPartMl * 4;
+  return (bytes + 255) / 256 * 256;
 }
 
 // The merge of a work-group key split: per (row, head), the parts' states
@@ -141,7 +144,7 @@ int64_t prefill_ws_bytes(const PrefillShape& sh, int64_t total_q, int num_heads,
 struct PrefillMergeParams {
   uint16_t* out;
   int64_t out_row_stride;
-  const float* part;
+  const void* part;
   int64_t part_rows;
   int xs;
   int num_heads;
@@ -163,16 +166,17 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillMergeParams M
   const int64_t row = rh / M.num_heads;
   const int hq = static_cast<int>(rh - row * M.num_heads);
   const int64_t plane = M.part_rows * M.num_heads;  // (row, head) records per part
-  const float* const ml = M.part + M.xs * plane * M.dv;
-  // Every part's record and O slice are loaded before any is used.
-  float4 rec[kMaxKeyParts], oa[kMaxKeyParts], ob[kMaxKeyParts];
+  const float* const ml = reinterpret_cast<const float*>(
+      static_cast<const uint8_t*>(M.part) + part_ml_offset(M.xs, M.part_rows, M.num_heads, M.dv));
+  const uint16_t* const po = static_cast<const uint16_t*>(M.part);
+  // Every part's record and O slice (8 bf16) are loaded before any is used.
+  float4 rec[kMaxKeyParts];
+  uint4 ov[kMaxKeyParts];
 #pragma unroll
   for (int p = 0; p < kMaxKeyParts; ++p) {
     if (p < M.xs) {
       rec[p] = *reinterpret_cast<const float4*>(ml + (p * plane + rh) * kPartMl);
-      const float* const o = M.part + (p * plane + rh) * M.dv + 8 * c8;
-      oa[p] = *reinterpret_cast<const float4*>(o);
-      ob[p] = *reinterpret_cast<const float4*>(o + 4);
+      ov[p] = *reinterpret_cast<const uint4*>(po + (p * plane + rh) * M.dv + 8 * c8);
     }
   }
   float mx = kNegInf;
@@ -186,14 +190,12 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillMergeParams M
       const float w = rec[p].x == kNegInf ? 0.f : __builtin_amdgcn_exp2f(rec[p].x - mx);
       l += w * rec[p].y;
       l32 += w * rec[p].z;
-      acc[0] += w * oa[p].x;
-      acc[1] += w * oa[p].y;
-      acc[2] += w * oa[p].z;
-      acc[3] += w * oa[p].w;
-      acc[4] += w * ob[p].x;
-      acc[5] += w * ob[p].y;
-      acc[6] += w * ob[p].z;
-      acc[7] += w * ob[p].w;
+      const uint32_t ow[4] = {ov[p].x, ov[p].y, ov[p].z, ov[p].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {  // dims 2i (low half) and 2i + 1 (high half)
+        acc[2 * i] += w * __builtin_bit_cast(float, ow[i] << 16);
+        acc[2 * i + 1] += w * __builtin_bit_cast(float, ow[i] & 0xffff0000u);
+      }
     }
   }
   const float sink2 = M.sinks ? M.sinks[hq] * kLog2e : kNegInf;
@@ -312,7 +314,7 @@ int prefill_entry(const char* name, bool paged, void* out, int64_t out_row_strid
   P.lse = lse;
   P.lse_row_stride = lse_row_stride;
   P.xs = sh.xs;
-  P.part = static_cast<float*>(workspace);
+  P.part = workspace;
   P.part_rows = total_q;
   P.num_heads = num_heads;
   FK_REQUIRE(qblocks <= 65535, "%s: max_seqlen_q %lld needs more than 65535 query blocks", name,

@@ -87,17 +87,24 @@ struct PrefillParams {
   int64_t lse_row_stride;
   // Work-group key split: each query block's key stages are divided over xs
   // work-groups (1: none), which leave their partial states in `part` for
-  // prefill_merge_kernel: O [xs][part_rows][num_heads][DV] fp32, then per row
-  // [xs][part_rows][num_heads][4] fp32 (running max in log2 units, the sum the
-  // output divides by, the fp32 sum of the log-sum-exp output, unused).
+  // prefill_merge_kernel: O [xs][part_rows][num_heads][DV] bf16 (before the
+  // division by the sum, rounded once), then from byte 2 xs part_rows num_heads
+  // DV (a multiple of 16: DV is a multiple of 8) [xs][part_rows][num_heads][4]
+  // fp32 (running max in log2 units, the sum the output divides by, the fp32 sum
+  // of the log-sum-exp output, unused).
   int xs;
-  float* part;
+  void* part;
   int64_t part_rows;  // rows of q (at least cu_seqlens_q[batch])
   int num_heads;
 };
 
 // Floats of the partial state per (part, row, head) besides O.
 constexpr int kPartMl = 4;
+// The fp32 records of the key parts' states, after their bf16 O.
+__host__ __device__ inline int64_t part_ml_offset(int xs, int64_t part_rows, int num_heads,
+                                                  int dv) {
+  return static_cast<int64_t>(xs) * part_rows * num_heads * dv * 2;
+}
 constexpr int kMaxKeyParts = 8;  // work-group key split: parts per query block at most
 
 // Launches the kernel for the head sizes fk_prefill_heads.hip instantiates
@@ -1317,28 +1324,30 @@ paged_prefill_kernel(PrefillParams P, const int32_t* __restrict__ block_tables,
   // one that saw no key (max -inf, sum 0).
   if (xs > 1) {
     const int64_t prow0 = static_cast<int64_t>(xpart) * P.part_rows + q_start;
+    uint16_t* const part_o = static_cast<uint16_t*>(P.part);
+    float* const part_ml = reinterpret_cast<float*>(
+        static_cast<uint8_t*>(P.part) + part_ml_offset(xs, P.part_rows, P.num_heads, DV));
 #pragma unroll
     for (int nb = 0; nb < kCB; ++nb) {
       if constexpr (kLse) {  // column layout: lanes of row group 0 hold column r's sum
         const int jc = j0 + 16 * nb + r;
         if (g == 0 && jc < q_len)
-          P.part[static_cast<int64_t>(xs) * P.part_rows * P.num_heads * DV +
-                 ((prow0 + jc) * P.num_heads + hq) * kPartMl + 2] = l32[nb];
+          part_ml[((prow0 + jc) * P.num_heads + hq) * kPartMl + 2] = l32[nb];
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int jr = j0 + 16 * nb + 4 * g + i;
         if (jr >= q_len) continue;
         const int64_t rh = (prow0 + jr) * P.num_heads + hq;
-        float* const po = P.part + rh * DV;
+        uint16_t* const po = part_o + rh * DV;
 #pragma unroll
         for (int d = 0; d < kVS; ++d) {
           const int dim = kFp8T ? (D / 16) * r + d : 16 * d + r;
-          if (kFp8T ? dim < DV : (16 * d + 16 <= DV || dim < DV)) po[dim] = o[nb][d][i];
+          if (kFp8T ? dim < DV : (16 * d + 16 <= DV || dim < DV))
+            po[dim] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(o[nb][d][i]));
         }
         if (r == 0) {
-          float* const pm =
-              P.part + static_cast<int64_t>(xs) * P.part_rows * P.num_heads * DV + rh * kPartMl;
+          float* const pm = part_ml + rh * kPartMl;
           pm[0] = m_row[nb][i];
           pm[1] = l_row[nb][i];
         }

@@ -332,7 +332,8 @@ int fk_prefill_split_plan(int paged, int kv_dtype, int64_t batch, int64_t total_
  * arguments (else FK_ERR_WORKSPACE) and the workspace 16-byte aligned.  Its contents
  * need no initialisation and are scratch after the call; calls that share a
  * workspace must be ordered (the same stream).  Results match the entry point
- * without _ws to rounding (the parts' O is merged in fp32). */
+ * without _ws to rounding (each part's O is kept in bf16 before the division by its
+ * sum, its max and sums in fp32, and merged in fp32). */
 int fk_paged_prefill_ws(void* out, int64_t out_row_stride, const void* q, int64_t q_row_stride,
                         const void* k_cache, const void* v_cache, int kv_dtype,
                         const float* k_scale, const float* v_scale, const int32_t* block_tables,

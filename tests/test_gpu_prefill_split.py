@@ -174,14 +174,14 @@ def test_paged_prefill_ws_entry_point_contract(cuda):
 
 
 def test_prefill_split_plan_sizes():
-    """The plan's workspace: parts x rows x heads x (value head size + 4) fp32, rounded
-    up to 256 bytes; zero for launches that fill the GPU and for empty calls."""
+    """The plan's workspace: parts x rows x heads x (value head size bf16 + 4 fp32),
+    rounded up to 256 bytes; zero for launches that fill the GPU and for empty calls."""
     b = _native.prefill_split_bytes
     # a single 2048-token prompt over Qwen3-8B heads fills every CU: no split
     assert b(True, _native.FK_DTYPE_BF16, 1, 2048, 2048, 2048, 32, 8, 128, 128, True) == 0
     assert b(True, _native.FK_DTYPE_BF16, 1, 0, 0, 0, 32, 8, 128, 128, True) == 0
     nbytes = b(True, _native.FK_DTYPE_BF16, 1, 512, 512, 8192, 32, 8, 128, 128, True)
-    rec = 512 * 32 * (128 + 4) * 4
+    rec = 512 * 32 * (128 * 2 + 4 * 4)
     assert nbytes > 0 and nbytes % 256 == 0 and nbytes % rec < 256
     parts = nbytes // rec
     assert 2 <= parts <= 8
