@@ -59,13 +59,15 @@ PrefillShape prefill_shape(bool paged, bool fp8, int64_t batch, int64_t max_seql
   sh.ks_plain = sh.ks;
   sh.xs = 1;
   const int64_t ncu = num_cus();
-  // Paged keys where the key split would run (fewer 4-wave work-groups than two
-  // per CU): 4-wave work-groups, two per CU, with each block's keys in xs parts
-  // over work-groups, instead of one 8-wave key-split work-group per block, for
+  // Where the key split would run (fewer 4-wave work-groups than two per CU):
+  // 4-wave work-groups, two per CU, with each block's keys in xs parts over
+  // work-groups, instead of one 8-wave key-split work-group per block, for
   // chunks over cached keys (blocks not paired) and, at head sizes up to 64 with
   // bf16 pages, for causal pairs.  xs = floor(2 CUs / work-groups) when that is
   // at least 2 and fills 7/8 of the two-per-CU slots, else the ceiling (at most
-  // kMaxKeyParts), and only while a part keeps at least 20 stages of 32 keys.
+  // kMaxKeyParts), and only while a part keeps at least 20 stages of 32 keys (40
+  // above head size 64: a dense 2048-token non-causal prompt at 16 / 16 / 80
+  // heads, 2 parts of 32 stages, went 48.8 -> 52.9).
   // Measured on MI355X (whole call, µs, key split -> this; same box, A/B in
   // alternating processes, two rounds averaged): Qwen3-8B heads (32 / 8 / 128)
   // 1x512 over 8192 102.9 -> 91.2, 2x512 over 4096 92.8 -> 86.5, 3x512 over 4096
@@ -73,11 +75,13 @@ PrefillShape prefill_shape(bool paged, bool fp8, int64_t batch, int64_t max_seql
   // (16 / 2 / 256) 1x512 over 8192 116.0 -> 106.4, 2x512 over 4096 109.4 ->
   // 103.5; Whisper heads (20 / 20 / 64) 4x512 over 4096 112.9 -> 80.4, 2x512
   // over 4096 57.2 -> 47.8, 1x512 over 8192 54.9 -> 48.5, prompts 1x2048 45.2 ->
-  // 40.8, 2x2048 80.5 -> 61.7, 1x4096 132.0 -> 93.7.  In single probes, causal
+  // 40.8, 2x2048 80.5 -> 61.7, 1x4096 132.0 -> 93.7; dense keys, 1x512 over 8192
+  // at Qwen3-8B heads 98.6 -> 90.1 and at MLA's (16 / 16 / 192 / 128, not
+  // causal) 92.7 -> 81.2, 2x512 over 4096 93.7 -> 89.4.  In single probes, causal
   // pairs at head 128 and 256 were slower this way (1x2048: 58.9 -> 68.3 and
   // 65.7 -> 73.8; they keep the key split with split pairs), and so were short
   // parts (Whisper heads 2x1024 at 3 parts of 12 stages: 31.6 -> 33.2).
-  if (paged && sh.ks == 2 && wgs > 0 &&
+  if (sh.ks == 2 && wgs > 0 &&
       (!may_pair || (!fp8 && std::max(head_size, head_size_v) <= 64))) {
     const int64_t slots = 2 * ncu;
     int64_t xs = slots / wgs;
@@ -86,7 +90,8 @@ PrefillShape prefill_shape(bool paged, bool fp8, int64_t batch, int64_t max_seql
     const double stages = static_cast<double>(std::max(max_seqlen_k, max_seqlen_q) +
                                               (may_pair ? wg_tokens : 0)) /
                           kStageKeys;  // the heaviest work-group's stages (a pair's)
-    if (xs >= 2 && stages >= 20.0 * xs && sh.qblocks * xs <= 65535) {
+    const double min_stages = std::max(head_size, head_size_v) <= 64 ? 20.0 : 40.0;
+    if (xs >= 2 && stages >= min_stages * xs && sh.qblocks * xs <= 65535) {
       sh.ks = 1;
       sh.xs = static_cast<int>(xs);
       return sh;

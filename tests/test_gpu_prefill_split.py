@@ -64,11 +64,11 @@ PAGED_CASES = [
      {"hq": 20, "hk": 20, "d": 64, "bs": 256}),
     ("prompts 2x2048, MHA head 64, 10 heads (4-wave work-groups)", [2048, 2048], [2048, 2048],
      {"hq": 10, "hk": 10, "d": 64, "bs": 256}),
-    ("chunk 512 over 8192, GQA 4 (4-wave work-groups)", [512], [8192],
-     {"hq": 8, "hk": 2, "bs": 256}),
-    ("fp8 pages, chunk 512 over 8192 (4-wave work-groups)", [512], [8192],
-     {"hq": 8, "hk": 2, "bs": 64, "fp8": True}),
-    ("head 256, chunk 512 over 8192 (4-wave work-groups)", [512], [8192],
+    ("chunks of 512 over 4000-8192 keys, GQA 4 (4-wave work-groups)", [512, 512, 300, 512],
+     [8192, 6000, 8192, 4000], {"hq": 8, "hk": 2, "bs": 256}),
+    ("fp8 pages, chunks over long caches (4-wave work-groups)", [512, 512, 300, 512],
+     [8192, 6000, 8192, 4000], {"hq": 8, "hk": 2, "bs": 64, "fp8": True}),
+    ("head 256, chunks of 512 over 8192 (4-wave work-groups)", [512] * 4, [8192] * 4,
      {"hq": 4, "hk": 1, "d": 256, "bs": 64}),
     ("chunks of a batch over long caches (4-wave work-groups)", [1, 300, 512],
      [8192, 5000, 4096], {"hq": 8, "hk": 2, "bs": 16}),
@@ -132,6 +132,32 @@ def test_varlen_prefill_workgroup_key_split_lse(cuda, hq, hk, d, dv, causal):
     H._close(out2, ref_o, 1e-2, "output without the split")
     H._lse_close(lse2, ref_l, "lse without the split")
     out3, lse3 = H._run_dense(q, k, v, cu_q, cu_k, 600, scale, causal, lse=True, max_k=2000)
+    assert torch.equal(out3, out) and torch.equal(lse3, lse), "repeat differs"
+
+
+@pytest.mark.parametrize("hq,hk,d,dv,causal,nseq", [(8, 2, 128, 128, True, 4),
+                                                    (2, 2, 192, 128, False, 8),
+                                                    (4, 4, 80, 80, False, 8)])
+def test_varlen_prefill_key_parts_long_keys(cuda, hq, hk, d, dv, causal, nseq):
+    """Dense keys, 512-query chunks over 8192 keys (128 blocks): 4-wave work-groups with
+    each block's keys in parts over work-groups (in place of the 8-wave key split), with
+    the log-sum-exp output."""
+    _flush(f"varlen key parts over 8192 keys {hq}/{hk}/{d}/{dv} causal={causal} x{nseq}")
+    q_lens, k_lens = [512] * nseq, [8192] * nseq
+    q, k, v, cu_q, cu_k = H._dense(cuda, q_lens, k_lens, hq, hk, d, dv, seed=470 + d)
+    nbytes = _native.prefill_split_bytes(False, _native.FK_DTYPE_BF16, nseq, q.shape[0], 512,
+                                         8192, hq, hk, d, dv, causal)
+    assert nbytes > 0
+    scale = d ** -0.5
+    ref_o, ref_l = H._oracle_dense(q, k, v, cu_q, cu_k, scale, causal, lse=True)
+    out, lse = H._run_dense(q, k, v, cu_q, cu_k, 512, scale, causal, lse=True, max_k=8192)
+    H._close(out, ref_o, 1e-2, "key parts output")
+    H._lse_close(lse, ref_l, "key parts lse")
+    out2, lse2 = _plain(lambda: H._run_dense(q, k, v, cu_q, cu_k, 512, scale, causal, lse=True,
+                                             max_k=8192))
+    H._close(out2, ref_o, 1e-2, "output without the parts")
+    H._lse_close(lse2, ref_l, "lse without the parts")
+    out3, lse3 = H._run_dense(q, k, v, cu_q, cu_k, 512, scale, causal, lse=True, max_k=8192)
     assert torch.equal(out3, out) and torch.equal(lse3, lse), "repeat differs"
 
 
