@@ -88,12 +88,19 @@ def test_paged_prefill_workgroup_key_split(cuda, label, q_lens, k_lens, kw):
     assert torch.equal(P._run(c), got), f"{label}: repeat differs"
 
 
+# (q_lens, k_lens): the key split with parts, and (128 blocks over long caches) 4-wave
+# work-groups with parts
+_WINDOW_SHAPES = [([300, 9], [3000, 2500]), ([512, 300, 9, 512], [8192, 6000, 2500, 8192])]
+
+
+@pytest.mark.parametrize("shape", [0, 1])
 @pytest.mark.parametrize("window_left", [0, 100, 1000])
-def test_paged_prefill_workgroup_key_split_window_and_sinks(cuda, window_left):
+def test_paged_prefill_workgroup_key_split_window_and_sinks(cuda, window_left, shape):
     """A sliding window (parts whose stages all precede a query's window) and sinks,
     which join the sum once, in the merge."""
-    _flush(f"prefill work-group key split window={window_left}")
-    c = P._case(cuda, [300, 9], [3000, 2500], hq=8, hk=2, bs=16, seed=410 + window_left)
+    _flush(f"prefill work-group key split window={window_left} shape={shape}")
+    q_lens, k_lens = _WINDOW_SHAPES[shape]
+    c = P._case(cuda, q_lens, k_lens, hq=8, hk=2, bs=16, seed=410 + window_left + shape)
     assert _paged_ws_bytes(c) > 0
     g = torch.Generator().manual_seed(411)
     sinks = (2 * torch.randn(8, generator=g)).float().to(cuda)
