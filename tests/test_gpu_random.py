@@ -115,10 +115,42 @@ def _prefill_params(i):
                 window=window, fp8=fp8, sinks=sinks, dense=dense, seed=4000 + i)
 
 
+def _prefill_params_long(i):
+    """Chunks over long caches (the launches that split each block's keys over
+    work-groups, with the key split or with 4-wave work-groups), heads kept few so that
+    the oracle stays within seconds."""
+    rng = np.random.default_rng(5000 + i)
+    d = int(rng.choice([64, 128]))
+    hk, group = [(2, 1), (2, 2), (2, 4), (4, 1), (4, 2), (4, 4), (8, 1), (8, 2)][
+        int(rng.integers(0, 8))]
+    bs = int(rng.choice([16, 64, 256]))
+    n = int(rng.integers(1, 4))
+    q_lens = [int(rng.integers(200, 513)) for _ in range(n)]
+    k_lens = [int(rng.integers(2048, 8193)) for _ in range(n)]
+    causal = bool(rng.random() < 0.8)
+    window = int(rng.choice([-1, -1, -1, -1, 300, 2000])) if causal else -1
+    fp8 = bool(rng.random() < 0.3)
+    sinks = bool(rng.random() < 0.3)
+    dense = bool(rng.random() < 0.25) and not fp8
+    return dict(d=d, hk=hk, hq=hk * group, bs=bs, q_lens=q_lens, k_lens=k_lens, causal=causal,
+                window=window, fp8=fp8, sinks=sinks, dense=dense, seed=6000 + i)
+
+
+N_PREFILL_LONG = 16 * _SCALE
+
+
 @pytest.mark.parametrize("i", range(N_PREFILL))
 def test_random_prefill(cuda, i):
-    p = _prefill_params(i)
-    print(f"random prefill {i}: {p}", flush=True)
+    _random_prefill(cuda, f"random prefill {i}", _prefill_params(i))
+
+
+@pytest.mark.parametrize("i", range(N_PREFILL_LONG))
+def test_random_prefill_long_caches(cuda, i):
+    _random_prefill(cuda, f"random prefill over a long cache {i}", _prefill_params_long(i))
+
+
+def _random_prefill(cuda, i, p):
+    print(f"{i}: {p}", flush=True)
     g = torch.Generator().manual_seed(p["seed"])
     hq, hk, d, bs = p["hq"], p["hk"], p["d"], p["bs"]
     q_lens, k_lens = p["q_lens"], p["k_lens"]
@@ -139,7 +171,7 @@ def test_random_prefill(cuda, i):
                                     cu_q.numpy(), cu_k.numpy(), scale, causal=p["causal"],
                                     window_left=p["window"],
                                     sinks=None if sinks is None else sinks.numpy())
-        _close(out, ref, 1e-2, f"random prefill {i} {p}")
+        _close(out, ref, 1e-2, f"{i} {p}")
         return
     pages = [(kl + bs - 1) // bs for kl in k_lens]
     nb = sum(pages) + 2
@@ -170,7 +202,7 @@ def test_random_prefill(cuda, i):
                                None if vs is None else vs.numpy(), causal=p["causal"],
                                window_left=p["window"],
                                sinks=None if sinks is None else sinks.numpy())
-    _close(out, ref, 3e-2 if p["fp8"] else 1e-2, f"random prefill {i} {p}")
+    _close(out, ref, 3e-2 if p["fp8"] else 1e-2, f"{i} {p}")
 
 
 N_FUSED = 40 * _SCALE
